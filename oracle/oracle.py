@@ -1,0 +1,213 @@
+"""ctypes front end of the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use
+this module, and only as the checker.  The product never imports it.
+
+The oracle itself is oracle/refcpu.c, a plain-C restatement of the
+reference's CPU path; see that file for the per-function citations.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librefcpu.so")
+
+ARCH = {"nanochat": 0, "llama2": 1}
+GRAD = {"compat": 0, "true": 1}
+
+
+class OrcCfg(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("hidden", C.c_int32), ("heads", C.c_int32),
+                ("layers", C.c_int32), ("vocab", C.c_int32), ("seq", C.c_int32),
+                ("arch", C.c_int32), ("grad_mode", C.c_int32), ("rope_theta", C.c_double)]
+
+
+class OrcAdam(C.Structure):
+    _fields_ = [(n, C.c_float) for n in (
+        "lr", "beta1", "beta2", "eps", "weight_decay", "grad_clip", "embed_lr_mult",
+        "scalar_lr_mult", "lambda_lr_mult", "lambda_beta1", "lambda_beta2")]
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        fp = C.POINTER(C.c_float)
+        u16 = C.POINTER(C.c_uint16)
+        L.orc_param_count.restype = C.c_size_t
+        L.orc_param_count.argtypes = [C.POINTER(OrcCfg)]
+        L.orc_param_segments.restype = C.c_int
+        L.orc_param_segments.argtypes = [C.POINTER(OrcCfg), C.POINTER(C.c_int64),
+                                         C.POINTER(C.c_int64), C.c_int]
+        L.orc_forward_loss.restype = C.c_float
+        L.orc_forward_loss.argtypes = [C.POINTER(OrcCfg), fp, u16, u16, C.c_int, fp, fp]
+        L.orc_grads.restype = C.c_float
+        L.orc_grads.argtypes = [C.POINTER(OrcCfg), fp, u16, u16, C.c_int, C.c_float, fp]
+        L.orc_adam_update.restype = None
+        L.orc_adam_update.argtypes = [C.POINTER(OrcCfg), fp, fp, fp, fp, C.c_int, C.POINTER(OrcAdam)]
+        L.orc_set_threads.argtypes = [C.c_int]
+        L.orc_set_parallel_linear.argtypes = [C.c_int]
+        L.orc_linear_cf.argtypes = [fp, fp, fp, C.c_int, C.c_int, C.c_int]
+        L.orc_rmsnorm_noweight_cf.argtypes = [fp, fp, C.c_int, C.c_int]
+        L.orc_rmsnorm_cf.argtypes = [fp, fp, fp, C.c_int, C.c_int]
+        L.orc_causal_attention_cf.argtypes = [fp, fp, fp, fp, C.c_int, C.c_int, C.c_int]
+        L.orc_build_rope.argtypes = [fp, fp, C.c_int, C.c_int, C.c_double]
+        L.orc_apply_rope_cf.argtypes = [fp, C.c_int, C.c_int, C.c_int, fp, fp]
+        L.orc_qknorm_cf.argtypes = [fp, fp, C.c_int, C.c_int, C.c_int]
+        L.orc_cross_entropy.restype = C.c_float
+        L.orc_cross_entropy.argtypes = [fp, fp, u16, C.c_int, C.c_int]
+        L.orc_softcap.argtypes = [fp, C.c_size_t]
+        L.orc_drand48_seed.restype = C.c_uint64
+        L.orc_drand48_seed.argtypes = [C.c_int64]
+        L.orc_drand48_next.restype = C.c_double
+        L.orc_drand48_next.argtypes = [C.POINTER(C.c_uint64)]
+        ncpu = os.cpu_count() or 1
+        L.orc_set_threads(min(ncpu, 64))
+        L.orc_set_parallel_linear(1)
+        _lib = L
+    return _lib
+
+
+def set_threads(n: int, parallel_linear: bool = True):
+    lib().orc_set_threads(int(n))
+    lib().orc_set_parallel_linear(1 if parallel_linear else 0)
+
+
+def _f(a):
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _u16(a):
+    assert a.dtype == np.uint16 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.POINTER(C.c_uint16))
+
+
+def cfg_struct(cfg) -> OrcCfg:
+    """cfg: any object with dim/hidden/heads/layers/vocab/seq/arch/grad_mode/rope_theta."""
+    return OrcCfg(cfg.dim, cfg.hidden, cfg.heads, cfg.layers, cfg.vocab, cfg.seq,
+                  ARCH[cfg.arch], GRAD[cfg.grad_mode], float(cfg.rope_theta))
+
+
+def param_count(cfg) -> int:
+    return int(lib().orc_param_count(C.byref(cfg_struct(cfg))))
+
+
+def param_segments(cfg):
+    c = cfg_struct(cfg)
+    n = lib().orc_param_segments(C.byref(c), None, None, 0)
+    off = (C.c_int64 * n)()
+    sz = (C.c_int64 * n)()
+    lib().orc_param_segments(C.byref(c), off, sz, n)
+    return [(int(off[i]), int(sz[i])) for i in range(n)]
+
+
+def forward_loss(cfg, params, tokens, targets, want_logits=False):
+    """tokens/targets: uint16 [nseq, seq]. Returns (mean, per_seq, logits|None);
+    logits are [nseq, V, seq] vocab-major, as EvalLogits returns them."""
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint16).reshape(-1, cfg.seq)
+    targets = np.ascontiguousarray(targets, dtype=np.uint16).reshape(-1, cfg.seq)
+    n = tokens.shape[0]
+    per = np.zeros(n, np.float32)
+    lg = np.zeros((n, cfg.vocab, cfg.seq), np.float32) if want_logits else None
+    m = lib().orc_forward_loss(C.byref(cfg_struct(cfg)), _f(params), _u16(tokens), _u16(targets), n,
+                               _f(lg) if lg is not None else None, _f(per))
+    return float(m), per, lg
+
+
+def grads(cfg, params, tokens, targets, loss_scale=256.0):
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint16).reshape(-1, cfg.seq)
+    targets = np.ascontiguousarray(targets, dtype=np.uint16).reshape(-1, cfg.seq)
+    g = np.zeros(param_count(cfg), np.float32)
+    loss = lib().orc_grads(C.byref(cfg_struct(cfg)), _f(params), _u16(tokens), _u16(targets),
+                           tokens.shape[0], float(loss_scale), _f(g))
+    return float(loss), g
+
+
+def adam_update(cfg, params, g, m, v, step, hp: dict):
+    h = OrcAdam(**{k: float(hp[k]) for k in (
+        "lr", "beta1", "beta2", "eps", "weight_decay", "grad_clip", "embed_lr_mult",
+        "scalar_lr_mult", "lambda_lr_mult", "lambda_beta1", "lambda_beta2")})
+    lib().orc_adam_update(C.byref(cfg_struct(cfg)), _f(params), _f(g), _f(m), _f(v), int(step), C.byref(h))
+
+
+# --- single ops (channel-first, reference signatures) ---------------------
+def linear_cf(w, x):
+    oc, ic = w.shape
+    seq = x.shape[1]
+    out = np.zeros((oc, seq), np.float32)
+    lib().orc_linear_cf(_f(out), _f(w), _f(x), oc, ic, seq)
+    return out
+
+
+def rmsnorm_noweight_cf(x):
+    out = np.zeros_like(x)
+    lib().orc_rmsnorm_noweight_cf(_f(out), _f(x), x.shape[0], x.shape[1])
+    return out
+
+
+def rmsnorm_cf(x, w):
+    out = np.zeros_like(x)
+    lib().orc_rmsnorm_cf(_f(out), _f(x), _f(w), x.shape[0], x.shape[1])
+    return out
+
+
+def causal_attention_cf(q, k, v, heads):
+    out = np.zeros_like(q)
+    dim, seq = q.shape
+    lib().orc_causal_attention_cf(_f(out), _f(q), _f(k), _f(v), heads, dim // heads, seq)
+    return out
+
+
+def rope_tables(seq, head_dim, theta):
+    c = np.zeros((seq, head_dim // 2), np.float32)
+    s = np.zeros((seq, head_dim // 2), np.float32)
+    lib().orc_build_rope(_f(c), _f(s), seq, head_dim, float(theta))
+    return c, s
+
+
+def apply_rope_cf(x, heads, cos_t, sin_t):
+    x = np.ascontiguousarray(x.copy())
+    dim, seq = x.shape
+    lib().orc_apply_rope_cf(_f(x), heads, dim // heads, seq, _f(cos_t), _f(sin_t))
+    return x
+
+
+def qknorm_cf(q, k, heads):
+    q = np.ascontiguousarray(q.copy())
+    k = np.ascontiguousarray(k.copy())
+    lib().orc_qknorm_cf(_f(q), _f(k), q.shape[0], heads, q.shape[1])
+    return q, k
+
+
+def cross_entropy(logits, targets):
+    v, s = logits.shape
+    dl = np.zeros_like(logits)
+    t = np.ascontiguousarray(targets, dtype=np.uint16)
+    loss = lib().orc_cross_entropy(_f(dl), _f(np.ascontiguousarray(logits)), _u16(t), v, s)
+    return float(loss), dl
+
+
+def softcap(x):
+    x = np.ascontiguousarray(x.copy(), dtype=np.float32)
+    lib().orc_softcap(_f(x), x.size)
+    return x
+
+
+def drand48_stream(seed, n):
+    st = C.c_uint64(lib().orc_drand48_seed(int(seed)))
+    return np.array([lib().orc_drand48_next(C.byref(st)) for _ in range(n)])

@@ -1,0 +1,100 @@
+/*
+ * refcpu.h -- CPU oracle for the ane transformer path (TEST INFRASTRUCTURE).
+ *
+ * This is a plain-C restatement of the reference's non-darwin ("CPU path")
+ * model math, used ONLY as the checker by tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg.  The product (libane_hip.so) never links,
+ * loads or calls it.
+ *
+ * Layout follows the reference: activations channel-first [C, seq] per
+ * sequence, weights row-major [out, in], logits vocab-major [V, seq].
+ *
+ * Parameters travel as ONE flat fp32 vector in the canonical order below
+ * (the same order the product's C-ABI uses):
+ *   arch NANOCHAT (reference-exact, ane/engine.go:954-1038):
+ *     per layer l: Wq[D*D] Wk[D*D] Wv[D*D] Wo[D*D] W1[H*D] W2[D*H]
+ *                  (+ VEEmbed[V*D] VEGate[NH*12] when l is a VE layer)
+ *     then Embed[V*D] ResidLambdas[L] X0Lambdas[L] SmearGate[D*D]
+ *          SmearLambda[1] BackoutLambda[1]
+ *     (order of ane/engine.go:811-840 writeModelGrad)
+ *   arch LLAMA2 (built from the reference primitives):
+ *     per layer l: Wq Wk Wv Wo W1[H*D] W2[D*H] W3[H*D] g_att[D] g_ffn[D]
+ *     then Embed[V*D] g_final[D]
+ */
+#ifndef REFCPU_H
+#define REFCPU_H
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ORC_ARCH_NANOCHAT = 0, ORC_ARCH_LLAMA2 = 1 };
+enum { ORC_GRAD_COMPAT = 0, ORC_GRAD_TRUE = 1 };
+
+typedef struct {
+  int32_t dim, hidden, heads, layers, vocab, seq;
+  int32_t arch;       /* ORC_ARCH_* */
+  int32_t grad_mode;  /* ORC_GRAD_*: compat reproduces the reference backward */
+  double rope_theta;  /* 100000 (nanochat, ane/train_util.go:196) / 10000 */
+} orc_cfg;
+
+typedef struct {
+  float lr, beta1, beta2, eps, weight_decay, grad_clip;
+  float embed_lr_mult, scalar_lr_mult, lambda_lr_mult;
+  float lambda_beta1, lambda_beta2;
+} orc_adam;
+
+/* threading knob: n worker threads for parallelFor-style loops (>=1). */
+void orc_set_threads(int n);
+/* when nonzero, linearCF-style GEMMs are split over output rows too
+ * (bit-identical results; the reference runs them serially). */
+void orc_set_parallel_linear(int on);
+
+size_t orc_param_count(const orc_cfg *c);
+/* fills offsets/sizes of the n-th canonical segment; returns #segments */
+int orc_param_segments(const orc_cfg *c, int64_t *offsets, int64_t *sizes, int max);
+int orc_is_ve_layer(const orc_cfg *c, int l);
+
+/* Forward + loss over nseq independent sequences.
+ * tokens/targets: [nseq][seq] uint16.  logits (optional, may be NULL):
+ * [nseq][V][seq] vocab-major after softcap (nanochat).  loss_per_seq
+ * (optional): mean CE per sequence.  Returns the mean over sequences. */
+float orc_forward_loss(const orc_cfg *c, const float *params,
+                       const uint16_t *tokens, const uint16_t *targets,
+                       int nseq, float *logits, float *loss_per_seq);
+
+/* Forward + backward over nseq sequences.  grads (size orc_param_count)
+ * receives the mean over sequences of each sequence's gradient, after the
+ * loss-scale round trip and before clipping (ane/train_full.go:822-945).
+ * Returns the mean loss. */
+float orc_grads(const orc_cfg *c, const float *params,
+                const uint16_t *tokens, const uint16_t *targets, int nseq,
+                float loss_scale, float *grads);
+
+/* Global-norm clip + AdamW update with the reference's parameter groups
+ * (ane/train_full.go:167-196, 1088-1150; ane/engine.go:646-682).
+ * step is the 1-based Adam step t. grads are modified by clipping. */
+void orc_adam_update(const orc_cfg *c, float *params, float *grads, float *m,
+                     float *v, int step, const orc_adam *h);
+
+/* --- single ops at the reference's signatures (channel-first) --------- */
+void orc_linear_cf(float *out, const float *w, const float *in, int out_ch, int in_ch, int seq);
+void orc_rmsnorm_noweight_cf(float *out, const float *x, int dim, int seq);
+void orc_rmsnorm_cf(float *out, const float *x, const float *w, int dim, int seq);
+void orc_causal_attention_cf(float *out, const float *q, const float *k, const float *v,
+                             int heads, int head_dim, int seq);
+void orc_build_rope(float *cos_t, float *sin_t, int seq, int head_dim, double theta);
+void orc_apply_rope_cf(float *x, int heads, int head_dim, int seq, const float *cos_t,
+                       const float *sin_t);
+void orc_qknorm_cf(float *q, float *k, int dim, int heads, int seq);
+float orc_cross_entropy(float *dlogits, const float *logits, const uint16_t *targets, int v, int s);
+void orc_softcap(float *x, size_t n);
+uint64_t orc_drand48_seed(int64_t seed);
+double orc_drand48_next(uint64_t *state);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
