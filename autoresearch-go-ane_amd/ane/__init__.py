@@ -7,3 +7,4 @@ through libane_hip.so (no CPU fallback: a missing library raises).
 """
 from .config import (Config, stories110m, tiny, is_ve_layer, param_layout, param_count,  # noqa: F401
                      views, init_params, make_tokens, VE_GATE_CHANNELS)
+from .engine import Options, Open, Engine, EngineError  # noqa: F401

@@ -1,0 +1,196 @@
+"""Host-side mirror of the reference's ``ane.Engine`` over libane_hip.so.
+
+Names, argument meaning and error wording follow ane/engine.go:
+``Open(Options)`` (ane/engine.go:184), ``Engine.EvalLogits`` (:449),
+``Engine.Step`` (:381), ``Flush`` (:484), ``LR``/``SetLR`` (:358,366),
+``State``/``LoadState`` (:498,506), ``Close`` (:567).  Errors raise
+``EngineError`` carrying the library's message ("storiesane <op>: ...")
+where the Go API returns ``error``.
+
+Additions of this engine (no reference counterpart): ``Options.Config``
+(model shape; the reference hard-codes stories110M), ``Options.Params``
+(flat fp32 weights in the canonical layout, in place of a model file),
+``Options.MaxBatch`` (sequences per device call), ``EvalLoss`` /
+``EvalLossWindows`` (batched forward + loss), and ``Profile*``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+from .config import Config, param_count
+
+
+class EngineError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+@dataclasses.dataclass
+class Options:
+    """ane/engine.go:14-40 (zero values take the defaults of Open)."""
+    ModelPath: str = ""
+    Tokens: Optional[np.ndarray] = None
+    Seq: int = 0
+    AccumSteps: int = 0
+    LR: float = 0.0
+    Seed: int = 0
+    AdamBeta1: float = 0.0
+    AdamBeta2: float = 0.0
+    AdamEps: float = 0.0
+    WeightDecay: float = 0.0
+    GradClip: float = 0.0
+    LossScale: float = 0.0
+    CPUClassifierHead: bool = False
+    GradTaskLimit: int = 0
+    UseANE: bool = False
+    HybridBackward: bool = False
+    EmbedLRMult: float = 0.0
+    ScalarLRMult: float = 0.0
+    LambdaLRMult: float = 0.0
+    LambdaBeta1: float = 0.0
+    LambdaBeta2: float = 0.0
+    # additions of this engine
+    Config: Optional[Config] = None
+    Params: Optional[np.ndarray] = None
+    MaxBatch: int = 1
+    Device: int = 0
+
+
+def _check(lib, eng, rc):
+    if rc != _lib.ANE_OK:
+        msg = lib.ane_last_error(eng)
+        raise EngineError(rc, msg.decode() if msg else f"storiesane: error {rc}")
+
+
+def _f32(a):
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _u16(a):
+    return a.ctypes.data_as(C.POINTER(C.c_uint16))
+
+
+def Open(opts: Options) -> "Engine":
+    """ane/engine.go:184-355.  Weights come from ``opts.Params``."""
+    lib = _lib.load()
+    if opts.Params is None and not opts.ModelPath:
+        raise EngineError(_lib.ANE_ERR_ARG, "storiesane open: model path is empty")
+    if opts.Params is None:
+        raise EngineError(_lib.ANE_ERR_ARG, f"storiesane open: load model: {opts.ModelPath}: "
+                                            "model files are not supported by this engine; pass Params")
+    cfg = opts.Config or Config()
+    if opts.Seq and opts.Seq != cfg.seq:
+        cfg = dataclasses.replace(cfg, seq=opts.Seq)
+    tokens = None
+    if opts.Tokens is not None and len(opts.Tokens) > 0:
+        tokens = np.ascontiguousarray(opts.Tokens, dtype=np.uint16)
+        if len(tokens) < cfg.seq + 1:
+            raise EngineError(_lib.ANE_ERR_ARG, f"storiesane open: not enough tokens for seq={cfg.seq}")
+    o = _lib.Options(opts.AccumSteps, opts.LR, opts.Seed, opts.AdamBeta1, opts.AdamBeta2, opts.AdamEps,
+                     opts.WeightDecay, opts.GradClip, opts.LossScale, opts.EmbedLRMult, opts.ScalarLRMult,
+                     opts.LambdaLRMult, opts.LambdaBeta1, opts.LambdaBeta2, max(1, opts.MaxBatch), opts.Device)
+    mc = _lib.model_cfg(cfg)
+    h = C.c_void_p()
+    rc = lib.ane_open(C.byref(mc), C.byref(o), C.byref(h))
+    if rc != _lib.ANE_OK:
+        msg = lib.ane_last_error(h) if h.value else b"storiesane open: failed"
+        if h.value:
+            lib.ane_destroy(h)
+        raise EngineError(rc, msg.decode())
+    eng = Engine(lib, h, cfg, o)
+    try:
+        eng.SetParams(opts.Params)
+        if tokens is not None:
+            _check(lib, h, lib.ane_set_tokens(h, _u16(tokens), len(tokens)))
+            eng._ntokens = len(tokens)
+    except Exception:
+        eng.Destroy()
+        raise
+    return eng
+
+
+class Engine:
+    def __init__(self, lib, handle, cfg: Config, opts):
+        self._lib = lib
+        self._h = handle
+        self.cfg = cfg
+        self.max_batch = opts.max_batch
+        self._ntokens = 0
+
+    # -- weights ---------------------------------------------------------
+    def SetParams(self, flat: np.ndarray):
+        flat = np.ascontiguousarray(flat, dtype=np.float32).reshape(-1)
+        if flat.size != param_count(self.cfg):
+            raise EngineError(_lib.ANE_ERR_ARG, f"storiesane set params: len={flat.size} "
+                                                f"want={param_count(self.cfg)}")
+        _check(self._lib, self._h, self._lib.ane_set_params(self._h, _f32(flat), flat.size))
+
+    def Params(self) -> np.ndarray:
+        out = np.empty(param_count(self.cfg), np.float32)
+        _check(self._lib, self._h, self._lib.ane_get_params(self._h, _f32(out), out.size))
+        return out
+
+    # -- forward ---------------------------------------------------------
+    def EvalLogits(self, tokens) -> np.ndarray:
+        """ane/engine.go:449-462: a fresh [vocab*seq] vocab-major fp32 slice."""
+        tok = np.ascontiguousarray(tokens, dtype=np.uint16).reshape(-1)
+        out = np.empty(self.cfg.vocab * self.cfg.seq, np.float32)
+        _check(self._lib, self._h, self._lib.ane_eval_logits(self._h, _u16(tok), tok.size, _f32(out)))
+        return out
+
+    def EvalLoss(self, tokens, targets):
+        """Batched forward + loss.  tokens/targets [nseq, seq] -> (mean, per_seq)."""
+        tok = np.ascontiguousarray(tokens, dtype=np.uint16).reshape(-1, self.cfg.seq)
+        tgt = np.ascontiguousarray(targets, dtype=np.uint16).reshape(-1, self.cfg.seq)
+        if tok.shape != tgt.shape:
+            raise EngineError(_lib.ANE_ERR_ARG, "storiesane eval loss: tokens/targets shape mismatch")
+        n = tok.shape[0]
+        per = np.zeros(n, np.float32)
+        mean = C.c_float()
+        _check(self._lib, self._h, self._lib.ane_eval_loss(self._h, _u16(tok), _u16(tgt), n, _f32(per),
+                                                           C.byref(mean)))
+        return float(mean.value), per
+
+    def EvalLossWindows(self, positions):
+        pos = np.ascontiguousarray(positions, dtype=np.uint64).reshape(-1)
+        per = np.zeros(pos.size, np.float32)
+        mean = C.c_float()
+        _check(self._lib, self._h, self._lib.ane_eval_loss_windows(
+            self._h, pos.ctypes.data_as(C.POINTER(C.c_uint64)), pos.size, _f32(per), C.byref(mean)))
+        return float(mean.value), per
+
+    # -- diagnostics -----------------------------------------------------
+    def ProfileEnable(self, on: bool = True):
+        _check(self._lib, self._h, self._lib.ane_profile_enable(self._h, 1 if on else 0))
+
+    def ProfileRead(self, reset: bool = True) -> dict:
+        arr = (_lib.ProfEntry * 8)()
+        _check(self._lib, self._h, self._lib.ane_profile_read(self._h, arr, 8, 1 if reset else 0))
+        return {name: dict(launches=int(arr[i].launches), ms=float(arr[i].ms), flops=float(arr[i].flops),
+                           bytes=float(arr[i].bytes)) for i, name in enumerate(_lib.PROF_CLASSES)}
+
+    def Sync(self):
+        _check(self._lib, self._h, self._lib.ane_sync(self._h))
+
+    # -- lifecycle -------------------------------------------------------
+    def Close(self):
+        """ane/engine.go:567: frees device memory; later calls fail with 'engine is closed'."""
+        if self._h:
+            self._lib.ane_close(self._h)
+
+    def Destroy(self):
+        if self._h:
+            self._lib.ane_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.Destroy()
+        except Exception:
+            pass

@@ -1,0 +1,247 @@
+// Fused causal attention forward, head_dim 64 (reference: causalAttentionCF,
+// ane/common.go:61-89, with RoPE ane/train_util.go:204-224 and QK-norm
+// ane/common.go:199-227 applied in-kernel; value embeddings
+// ane/train_full.go:1035-1059 added while V is staged).
+//
+// One workgroup per (sequence, head, group of q-block pairs).  The whole
+// sequence's K (after RoPE / QK-norm) and V^T are staged once in LDS; each
+// wave then owns two 32-row q-blocks (i, nqb-1-i) so every wave walks the
+// same number of causal key blocks.  Scores are computed transposed,
+// S^T = K Q^T, which leaves each lane holding 16 keys of ONE query: the
+// online-softmax statistics are per lane (plus one xor-32 exchange), and
+// the probabilities are already in the B-operand layout of O^T = V^T P^T,
+// so P never leaves registers.
+//
+// The reference fills masked scores with -65504 and takes exp in float64,
+// which yields exactly 0 for every masked key; skipping masked keys is the
+// same function.
+#include "attention.h"
+
+namespace ane {
+
+namespace {
+
+constexpr int HD = 64;
+
+template <int SMAX>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) half_t Ks[SMAX * HD];
+  constexpr int VST = SMAX + 4;  // V^T row stride (halves): 2-way-free b64 reads
+  __shared__ __attribute__((aligned(16))) half_t Vt[HD * VST];
+
+  const int S = a.S, NH = a.NH, D = NH * HD, D3 = 3 * D;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int nthr = blockDim.x, tid = threadIdx.x;
+  const size_t tok0 = (size_t)b * S;
+  const half_t* base = a.qkv + tok0 * D3;
+
+  // ---- stage K: RoPE (+ QK-norm), swizzled rows of 64 halves ----------------
+  for (int c = tid; c < S * 8; c += nthr) {
+    const int j = c >> 3, ch = c & 7;
+    half8 raw = ld_h8(base + (size_t)j * D3 + D + h * HD + ch * 8);
+    float f[8];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const int i = ch * 4 + p;
+      const float cs = a.rope_cos[j * 32 + i], sn = a.rope_sin[j * 32 + i];
+      const float e = (float)raw[2 * p], o = (float)raw[2 * p + 1];
+      f[2 * p] = e * cs - o * sn;
+      f[2 * p + 1] = o * cs + e * sn;
+    }
+    if (a.qknorm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int p = 0; p < 8; p++) ss += f[p] * f[p];
+      ss += __shfl_xor(ss, 1, 64);
+      ss += __shfl_xor(ss, 2, 64);
+      ss += __shfl_xor(ss, 4, 64);
+      const float sc = 1.2f / sqrtf(ss * (1.0f / HD) + 1e-5f);
+#pragma unroll
+      for (int p = 0; p < 8; p++) f[p] *= sc;
+    }
+    half8 w;
+#pragma unroll
+    for (int p = 0; p < 8; p++) w[p] = (half_t)f[p];
+    st_h8(Ks + j * HD + swz(j, ch) * 8, w);
+  }
+
+  // ---- stage V^T (8 keys x 8 dims per thread), value embeddings added --------
+  for (int blk = tid; blk < S; blk += nthr) {
+    const int nkc = S / 8;
+    const int kc = blk % nkc, dc = blk / nkc;
+    float v[8][8];
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      const int j = kc * 8 + jj;
+      half8 raw = ld_h8(base + (size_t)j * D3 + 2 * D + h * HD + dc * 8);
+#pragma unroll
+      for (int i = 0; i < 8; i++) v[jj][i] = (float)raw[i];
+      if (a.ve_x) {
+        const float* xr = a.ve_x + (tok0 + j) * D;
+        float gp = 0.f;
+#pragma unroll
+        for (int c2 = 0; c2 < 12; c2++) gp += a.ve_gate[h * 12 + c2] * xr[c2];
+        const float gate = 3.0f / (1.0f + __expf(-gp));
+        const int tk = a.tokens[tok0 + j];
+        if (tk < a.vocab) {
+          const float* er = a.ve_embed + (size_t)tk * D + h * HD + dc * 8;
+#pragma unroll
+          for (int i = 0; i < 8; i++) v[jj][i] += gate * er[i];
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      half4 lo, hi;
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) {
+        lo[jj] = (half_t)v[jj][i];
+        hi[jj] = (half_t)v[jj + 4][i];
+      }
+      half_t* dst = Vt + (dc * 8 + i) * VST + kc * 8;
+      *reinterpret_cast<half4*>(dst) = lo;
+      *reinterpret_cast<half4*>(dst + 4) = hi;
+    }
+  }
+  __syncthreads();
+
+  // ---- per wave: q-block pair ------------------------------------------------
+  const int lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;
+  const int nqb = S / 32, npairs = nqb / 2;
+  const int pair = blockIdx.x * nw + wave;
+  if (pair >= npairs) return;
+  const int g = lane >> 5, ql = lane & 31;
+  const float l2e = 1.4426950408889634f;
+  const float sl2 = a.scale * l2e;
+
+  for (int which = 0; which < 2; which++) {
+    const int qb = which == 0 ? pair : nqb - 1 - pair;
+    const int q = qb * 32 + ql;
+    // Q fragment (B operand of S^T = K Q^T): dims s*16 + 8g + [0..7]
+    float qf[4][8];
+    const half_t* qrow = base + (size_t)q * D3 + h * HD;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const int d0 = s * 16 + g * 8;
+      half8 raw = ld_h8(qrow + d0);
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const int i = d0 / 2 + p;
+        const float cs = a.rope_cos[q * 32 + i], sn = a.rope_sin[q * 32 + i];
+        const float e = (float)raw[2 * p], o = (float)raw[2 * p + 1];
+        qf[s][2 * p] = e * cs - o * sn;
+        qf[s][2 * p + 1] = o * cs + e * sn;
+      }
+    }
+    if (a.qknorm) {
+      float ss = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (int p = 0; p < 8; p++) ss += qf[s][p] * qf[s][p];
+      ss += __shfl_xor(ss, 32, 64);
+      const float sc = 1.2f / sqrtf(ss * (1.0f / HD) + 1e-5f);
+#pragma unroll
+      for (int s = 0; s < 4; s++)
+#pragma unroll
+        for (int p = 0; p < 8; p++) qf[s][p] *= sc;
+    }
+    half8 qfrag[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++)
+#pragma unroll
+      for (int p = 0; p < 8; p++) qfrag[s][p] = (half_t)qf[s][p];
+
+    floatx16 o0, o1;
+#pragma unroll
+    for (int r = 0; r < 16; r++) { o0[r] = 0.f; o1[r] = 0.f; }
+    float m = -INFINITY, lsum = 0.f;
+
+    for (int kb = 0; kb <= qb; kb++) {
+      floatx16 sacc;
+#pragma unroll
+      for (int r = 0; r < 16; r++) sacc[r] = 0.f;
+      const int krow = kb * 32 + ql;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        half8 kf = ld_h8(Ks + krow * HD + swz(krow, s * 2 + g) * 8);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qfrag[s], sacc, 0, 0, 0);
+      }
+      // sacc[r]: key kb*32 + 8*(r/4) + 4g + r%4, query q (scores * log2 e)
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        float sv = sacc[r] * sl2;
+        if (kb == qb && (8 * (r >> 2) + 4 * g + (r & 3)) > ql) sv = -INFINITY;
+        sacc[r] = sv;
+        mloc = fmaxf(mloc, sv);
+      }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float mnew = fmaxf(m, mloc);
+      const float alpha = exp2f(m - mnew);
+      float ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        float p = exp2f(sacc[r] - mnew);
+        sacc[r] = p;
+        ps += p;
+      }
+      lsum = lsum * alpha + ps;
+#pragma unroll
+      for (int r = 0; r < 16; r++) { o0[r] *= alpha; o1[r] *= alpha; }
+      m = mnew;
+#pragma unroll
+      for (int jh = 0; jh < 2; jh++) {
+        half8 pf;
+#pragma unroll
+        for (int u = 0; u < 8; u++) pf[u] = (half_t)sacc[8 * jh + u];
+        const int k0 = kb * 32 + 16 * jh + 4 * g;
+        half8 v0, v1;
+        {
+          const half_t* r0 = Vt + ql * VST + k0;
+          const half_t* r1 = Vt + (32 + ql) * VST + k0;
+          half4 a0 = *reinterpret_cast<const half4*>(r0), a1 = *reinterpret_cast<const half4*>(r0 + 8);
+          half4 b0 = *reinterpret_cast<const half4*>(r1), b1 = *reinterpret_cast<const half4*>(r1 + 8);
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            v0[u] = a0[u]; v0[u + 4] = a1[u];
+            v1[u] = b0[u]; v1[u + 4] = b1[u];
+          }
+        }
+        o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, pf, o0, 0, 0, 0);
+        o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, pf, o1, 0, 0, 0);
+      }
+    }
+    lsum += __shfl_xor(lsum, 32, 64);
+    const float inv = 1.0f / lsum;
+    half_t* orow = a.out + (tok0 + q) * D + h * HD;
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+      half4 w0, w1;
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        w0[u] = (half_t)(o0[4 * rr + u] * inv);
+        w1[u] = (half_t)(o1[4 * rr + u] * inv);
+      }
+      *reinterpret_cast<half4*>(orow + 8 * rr + 4 * g) = w0;
+      *reinterpret_cast<half4*>(orow + 32 + 8 * rr + 4 * g) = w1;
+    }
+    if (a.lse && g == 0) a.lse[(tok0 + q) * NH + h] = (m + log2f(lsum)) / l2e;
+  }
+}
+
+}  // namespace
+
+hipError_t attention_fwd(const AttnArgs& a, hipStream_t stream) {
+  if (a.S <= 0 || a.S % 64 != 0 || a.S > 512 || a.NH <= 0 || a.nseq <= 0) return hipErrorInvalidValue;
+  const int npairs = a.S / 64;
+  const int nw = npairs < 4 ? npairs : 4;
+  dim3 grid((npairs + nw - 1) / nw, a.NH, a.nseq);
+  if (a.S <= 256)
+    hipLaunchKernelGGL(attn_fwd_kernel<256>, grid, dim3(64 * nw), 0, stream, a);
+  else
+    hipLaunchKernelGGL(attn_fwd_kernel<512>, grid, dim3(64 * nw), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace ane

@@ -1,0 +1,722 @@
+// Engine: device state and the C-ABI entry points of libane_hip.so.
+//
+// This replaces the reference's accelerator objects (layerForward /
+// offload / refreshANERuntimeForWeights: ane/layer_darwin.go,
+// ane/offload_darwin.go, ane/runtime.go) with one device-resident model:
+// fp32 master weights and their fp16 GEMM shadows live in HBM, activations
+// never round-trip to the host between layers, and every stage runs on the
+// engine's single HIP stream in order (which also removes the reference's
+// eval-vs-refresh race, ane/engine.go:449 vs ane/runtime.go:74).
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/ane_hip.h"
+#include "attention.h"
+#include "engine_internal.h"
+#include "gemm.h"
+#include "rowops.h"
+
+using namespace ane;
+
+// ---------------------------------------------------------------------------
+// canonical parameter layout (one flat fp32 vector)
+// ---------------------------------------------------------------------------
+static constexpr int kVEGateCh = 12;  // ane/stories/weights.go:28
+
+static bool cfg_is_ve_layer(const ane_model_cfg& c, int l) {
+  // ane/stories/weights.go:22: value embeddings on layers with the parity of the last layer
+  return c.arch == ANE_ARCH_NANOCHAT && (l % 2) == ((c.layers - 1) % 2);
+}
+
+void build_param_map(const ane_model_cfg& c, ParamMap* m) {
+  const int64_t D = c.dim, H = c.hidden, V = c.vocab, NH = c.heads;
+  int64_t off = 0;
+  m->L.assign(c.layers, LayerOff());
+  for (int l = 0; l < c.layers; l++) {
+    LayerOff& o = m->L[l];
+    o.wq = off; off += D * D;
+    o.wk = off; off += D * D;
+    o.wv = off; off += D * D;
+    o.wo = off; off += D * D;
+    o.w1 = off; off += H * D;
+    o.w2 = off; off += D * H;
+    if (c.arch == ANE_ARCH_LLAMA2) {
+      o.w3 = off; off += H * D;
+      o.g_att = off; off += D;
+      o.g_ffn = off; off += D;
+    } else if (cfg_is_ve_layer(c, l)) {
+      o.ve_embed = off; off += V * D;
+      o.ve_gate = off; off += NH * kVEGateCh;
+    }
+  }
+  m->embed = off; off += V * D;
+  if (c.arch == ANE_ARCH_LLAMA2) {
+    m->g_final = off; off += D;
+  } else {
+    m->resid = off; off += c.layers;
+    m->x0l = off; off += c.layers;
+    m->smear_gate = off; off += D * D;
+    m->smear_lambda = off; off += 1;
+    m->backout_lambda = off; off += 1;
+  }
+  m->total = off;
+}
+
+static void param_segments(const ane_model_cfg& c, std::vector<std::pair<int64_t, int64_t>>* segs) {
+  ParamMap m;
+  build_param_map(c, &m);
+  const int64_t D = c.dim, H = c.hidden, V = c.vocab, NH = c.heads;
+  segs->clear();
+  for (int l = 0; l < c.layers; l++) {
+    const LayerOff& o = m.L[l];
+    segs->push_back({o.wq, D * D});
+    segs->push_back({o.wk, D * D});
+    segs->push_back({o.wv, D * D});
+    segs->push_back({o.wo, D * D});
+    segs->push_back({o.w1, H * D});
+    segs->push_back({o.w2, D * H});
+    if (c.arch == ANE_ARCH_LLAMA2) {
+      segs->push_back({o.w3, H * D});
+      segs->push_back({o.g_att, D});
+      segs->push_back({o.g_ffn, D});
+    } else if (o.ve_embed >= 0) {
+      segs->push_back({o.ve_embed, V * D});
+      segs->push_back({o.ve_gate, NH * kVEGateCh});
+    }
+  }
+  segs->push_back({m.embed, V * D});
+  if (c.arch == ANE_ARCH_LLAMA2) {
+    segs->push_back({m.g_final, D});
+  } else {
+    segs->push_back({m.resid, c.layers});
+    segs->push_back({m.x0l, c.layers});
+    segs->push_back({m.smear_gate, D * D});
+    segs->push_back({m.smear_lambda, 1});
+    segs->push_back({m.backout_lambda, 1});
+  }
+}
+
+// ---------------------------------------------------------------------------
+// errors
+// ---------------------------------------------------------------------------
+int eng_fail(ane_engine* e, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (e) e->err = buf;
+  return code;
+}
+
+#define HIPCHK(op, expr)                                                                             \
+  do {                                                                                               \
+    hipError_t _h = (expr);                                                                          \
+    if (_h != hipSuccess) return eng_fail(e, ANE_ERR_HIP, "storiesane %s: %s: %s", op, #expr,        \
+                                          hipGetErrorString(_h));                                    \
+  } while (0)
+
+#define CLOSED_CHECK(op) \
+  do { \
+    if (!e) return ANE_ERR_CLOSED; \
+    if (e->closed) return eng_fail(e, ANE_ERR_CLOSED, "storiesane %s: engine is closed", op); \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// profiling (HIP events bracketing tracked launches)
+// ---------------------------------------------------------------------------
+void prof_begin(ane_engine* e, int cls) {
+  if (!e->prof_on) return;
+  if (e->prof_next >= e->prof_events.size()) {
+    ProfEvent pe;
+    (void)hipEventCreate(&pe.a);
+    (void)hipEventCreate(&pe.b);
+    e->prof_events.push_back(pe);
+  }
+  ProfEvent& pe = e->prof_events[e->prof_next];
+  pe.cls = cls;
+  (void)hipEventRecord(pe.a, e->stream);
+}
+void prof_end(ane_engine* e, double flops, double bytes) {
+  if (!e->prof_on) return;
+  ProfEvent& pe = e->prof_events[e->prof_next];
+  pe.flops = flops;
+  pe.bytes = bytes;
+  (void)hipEventRecord(pe.b, e->stream);
+  e->prof_next++;
+}
+
+hipError_t eng_gemm(ane_engine* e, int cls, const half_t* A, int lda, bool at, const half_t* B, int ldb, bool bt,
+                    int M, int N, int K, int epi, const EpiParams& p, int bm, int bn) {
+  GemmArgs g;
+  g.A = A; g.B = B; g.lda = lda; g.ldb = ldb; g.M = M; g.N = N; g.K = K; g.a_t = at; g.b_t = bt;
+  prof_begin(e, cls);
+  hipError_t r = gemm_run(g, epi, p, e->stream, bm, bn);
+  prof_end(e, 2.0 * M * N * K, 2.0 * ((double)M * K + (double)N * K));
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// allocation
+// ---------------------------------------------------------------------------
+template <class T>
+static hipError_t dalloc(ane_engine* e, T** p, size_t n) {
+  void* q = nullptr;
+  hipError_t r = hipMalloc(&q, n * sizeof(T) > 0 ? n * sizeof(T) : 16);
+  if (r == hipSuccess) {
+    e->allocs.push_back(q);
+    *p = (T*)q;
+  }
+  return r;
+}
+
+static void free_all(ane_engine* e) {
+  if (e->dev_set) (void)hipSetDevice(e->device);
+  if (e->stream) (void)hipStreamSynchronize(e->stream);
+  for (void* p : e->allocs) (void)hipFree(p);
+  e->allocs.clear();
+  for (ProfEvent& pe : e->prof_events) {
+    (void)hipEventDestroy(pe.a);
+    (void)hipEventDestroy(pe.b);
+  }
+  e->prof_events.clear();
+  if (e->stream) (void)hipStreamDestroy(e->stream);
+  e->stream = nullptr;
+}
+
+static int validate_cfg(ane_engine* e, const ane_model_cfg& c) {
+  if (c.arch != ANE_ARCH_NANOCHAT && c.arch != ANE_ARCH_LLAMA2)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane open: unknown arch %d", c.arch);
+  if (c.heads <= 0 || c.dim != 64 * c.heads)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane open: dim=%d must be 64*heads (heads=%d)", c.dim, c.heads);
+  if (c.dim % 64 || c.hidden <= 0 || c.hidden % 64 || c.vocab <= 0 || c.vocab % 64 || c.layers <= 0)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane open: dim/hidden/vocab must be positive multiples of 64");
+  if (c.seq <= 0 || c.seq % 64 || c.seq > 512)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane open: seq=%d must be a multiple of 64 and <= 512", c.seq);
+  if (c.arch == ANE_ARCH_NANOCHAT && c.layers < 2)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane open: nanochat needs >= 2 layers (backout)");
+  return ANE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// lifecycle
+// ---------------------------------------------------------------------------
+extern "C" int64_t ane_param_count(const ane_model_cfg* cfg) {
+  if (!cfg) return -1;
+  ParamMap m;
+  build_param_map(*cfg, &m);
+  return m.total;
+}
+
+extern "C" int ane_param_layout(const ane_model_cfg* cfg, int64_t* offsets, int64_t* sizes, int max) {
+  if (!cfg) return ANE_ERR_ARG;
+  std::vector<std::pair<int64_t, int64_t>> segs;
+  param_segments(*cfg, &segs);
+  for (int i = 0; i < (int)segs.size() && i < max; i++) {
+    if (offsets) offsets[i] = segs[i].first;
+    if (sizes) sizes[i] = segs[i].second;
+  }
+  return (int)segs.size();
+}
+
+extern "C" const char* ane_last_error(const ane_engine* e) { return e ? e->err.c_str() : "storiesane: null engine"; }
+
+static void apply_option_defaults(ane_options* o) {
+  // ane/engine.go:185-240
+  if (o->lr <= 0) o->lr = 3e-4f;
+  if (o->accum_steps <= 0) o->accum_steps = 1;
+  if (o->seed == 0) o->seed = 42;
+  if (o->adam_beta1 <= 0) o->adam_beta1 = 0.9f;
+  if (o->adam_beta2 <= 0) o->adam_beta2 = 0.999f;
+  if (o->adam_eps <= 0) o->adam_eps = 1e-8f;
+  if (o->grad_clip < 0) o->grad_clip = 0;
+  if (o->loss_scale <= 0) o->loss_scale = 256;
+  if (o->embed_lr_mult <= 0) o->embed_lr_mult = 1.0f;
+  if (o->scalar_lr_mult <= 0) o->scalar_lr_mult = 1.0f;
+  if (o->lambda_lr_mult <= 0) o->lambda_lr_mult = 0.01f;
+  if (o->lambda_beta1 <= 0) o->lambda_beta1 = o->adam_beta1;
+  if (o->lambda_beta2 <= 0) o->lambda_beta2 = o->adam_beta2;
+  if (o->max_batch <= 0) o->max_batch = 1;
+}
+
+static int open_impl(ane_engine* e) {
+  const char* op = "open";
+  const ane_model_cfg& c = e->cfg;
+  const int D = c.dim, H = c.hidden, V = c.vocab, S = c.seq, NH = c.heads, L = c.layers;
+  const size_t T = (size_t)e->opt.max_batch * S;
+  HIPCHK(op, hipSetDevice(e->device));
+  e->dev_set = true;
+  HIPCHK(op, hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking));
+  build_param_map(c, &e->pm);
+  const size_t P = (size_t)e->pm.total;
+  HIPCHK(op, dalloc(e, &e->P, P));
+  HIPCHK(op, hipMemsetAsync(e->P, 0, P * sizeof(float), e->stream));
+
+  // fp16 shadows
+  size_t nsh = 0;
+  const bool llama = c.arch == ANE_ARCH_LLAMA2;
+  const size_t per_layer = (size_t)3 * D * D + (size_t)D * D + (size_t)(llama ? 2 : 1) * H * D + (size_t)D * H;
+  nsh = per_layer * L + (size_t)V * D + (llama ? 0 : (size_t)D * D);
+  HIPCHK(op, dalloc(e, &e->shadow, nsh));
+  e->ls.assign(L, LayerShadow());
+  half_t* q = e->shadow;
+  for (int l = 0; l < L; l++) {
+    LayerShadow& s = e->ls[l];
+    s.wqkv = q; q += (size_t)3 * D * D;
+    s.wo = q; q += (size_t)D * D;
+    s.w13 = q; q += (size_t)(llama ? 2 : 1) * H * D;
+    s.w2 = q; q += (size_t)D * H;
+  }
+  e->embed_h = q; q += (size_t)V * D;
+  if (!llama) { e->smear_h = q; q += (size_t)D * D; }
+
+  // RoPE tables: buildRoPETables (ane/train_util.go:183-202), theta as configured
+  {
+    const int half = 32;
+    std::vector<float> cs((size_t)S * half), sn((size_t)S * half);
+    for (int pos = 0; pos < S; pos++)
+      for (int i = 0; i < half; i++) {
+        double freq = (double)pos / pow(c.rope_theta, (double)(2 * i) / 64.0);
+        cs[(size_t)pos * half + i] = (float)cos(freq);
+        sn[(size_t)pos * half + i] = (float)sin(freq);
+      }
+    HIPCHK(op, dalloc(e, &e->rope_cos, cs.size()));
+    HIPCHK(op, dalloc(e, &e->rope_sin, sn.size()));
+    HIPCHK(op, hipMemcpy(e->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    HIPCHK(op, hipMemcpy(e->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  }
+
+  // activations
+  HIPCHK(op, dalloc(e, &e->tok, T));
+  HIPCHK(op, dalloc(e, &e->tgt, T));
+  HIPCHK(op, dalloc(e, &e->pos_d, (size_t)e->opt.max_batch));
+  HIPCHK(op, dalloc(e, &e->x, T * D));
+  if (!llama) {
+    HIPCHK(op, dalloc(e, &e->x0, T * D));
+    HIPCHK(op, dalloc(e, &e->xpre, T * D));
+    HIPCHK(op, dalloc(e, &e->xmid, T * D));
+  }
+  HIPCHK(op, dalloc(e, &e->xh, T * D));
+  HIPCHK(op, dalloc(e, &e->qkv, T * 3 * D));
+  HIPCHK(op, dalloc(e, &e->att, T * D));
+  HIPCHK(op, dalloc(e, &e->gate, T * H));
+  e->ce_bm = (V % 256 == 0) ? 256 : ((V % 128 == 0) ? 128 : 64);
+  e->ce_np = 2 * V / e->ce_bm;
+  HIPCHK(op, dalloc(e, &e->partial, (size_t)e->ce_np * T));
+  HIPCHK(op, dalloc(e, &e->tgt_logit, T));
+  HIPCHK(op, dalloc(e, &e->lse, T));
+  HIPCHK(op, dalloc(e, &e->loss_seq, (size_t)e->opt.max_batch));
+  HIPCHK(op, dalloc(e, &e->logits, (size_t)V * S));
+  (void)NH;
+  HIPCHK(op, hipStreamSynchronize(e->stream));
+  return ANE_OK;
+}
+
+extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_engine** out) {
+  if (!out || !cfg) return ANE_ERR_ARG;
+  *out = nullptr;
+  ane_engine* e = new ane_engine();
+  e->cfg = *cfg;
+  if (e->cfg.rope_theta <= 0) e->cfg.rope_theta = e->cfg.arch == ANE_ARCH_LLAMA2 ? 10000.0 : 100000.0;
+  if (opts) e->opt = *opts;
+  apply_option_defaults(&e->opt);
+  e->device = e->opt.device;
+  e->lr = e->opt.lr;
+  int rc = validate_cfg(e, e->cfg);
+  if (rc == ANE_OK) rc = open_impl(e);
+  if (rc != ANE_OK) {
+    free_all(e);
+    e->closed = true;
+  } else {
+    e->rng = drand48_seed(e->opt.seed);
+  }
+  *out = e;
+  return rc;
+}
+
+extern "C" void ane_close(ane_engine* e) {
+  if (!e || e->closed) return;
+  free_all(e);
+  e->closed = true;
+}
+
+extern "C" void ane_destroy(ane_engine* e) {
+  if (!e) return;
+  ane_close(e);
+  delete e;
+}
+
+extern "C" int ane_sync(ane_engine* e) {
+  CLOSED_CHECK("sync");
+  HIPCHK("sync", hipStreamSynchronize(e->stream));
+  return ANE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// weights
+// ---------------------------------------------------------------------------
+int refresh_shadows(ane_engine* e) {
+  const char* op = "refresh weights";
+  const ane_model_cfg& c = e->cfg;
+  const int D = c.dim, H = c.hidden, V = c.vocab;
+  const bool llama = c.arch == ANE_ARCH_LLAMA2;
+  for (int l = 0; l < c.layers; l++) {
+    const LayerOff& o = e->pm.L[l];
+    LayerShadow& s = e->ls[l];
+    HIPCHK(op, f32_to_f16(s.wqkv, e->P + o.wq, (size_t)3 * D * D, e->stream));  // Wq|Wk|Wv are adjacent
+    HIPCHK(op, f32_to_f16(s.wo, e->P + o.wo, (size_t)D * D, e->stream));
+    if (llama)
+      HIPCHK(op, interleave_w13(s.w13, e->P + o.w1, e->P + o.w3, H, D, e->stream));
+    else
+      HIPCHK(op, f32_to_f16(s.w13, e->P + o.w1, (size_t)H * D, e->stream));
+    HIPCHK(op, f32_to_f16(s.w2, e->P + o.w2, (size_t)D * H, e->stream));
+  }
+  HIPCHK(op, f32_to_f16(e->embed_h, e->P + e->pm.embed, (size_t)V * D, e->stream));
+  if (!llama) HIPCHK(op, f32_to_f16(e->smear_h, e->P + e->pm.smear_gate, (size_t)D * D, e->stream));
+  return ANE_OK;
+}
+
+extern "C" int ane_set_params(ane_engine* e, const float* params, int64_t n) {
+  CLOSED_CHECK("set params");
+  if (!params || n != e->pm.total)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane set params: len=%lld want=%lld", (long long)n,
+                    (long long)e->pm.total);
+  HIPCHK("set params", hipMemcpyAsync(e->P, params, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
+  int rc = refresh_shadows(e);
+  if (rc) return rc;
+  HIPCHK("set params", hipStreamSynchronize(e->stream));
+  return ANE_OK;
+}
+
+extern "C" int ane_get_params(ane_engine* e, float* params, int64_t n) {
+  CLOSED_CHECK("get params");
+  if (!params || n != e->pm.total)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane get params: len=%lld want=%lld", (long long)n,
+                    (long long)e->pm.total);
+  HIPCHK("get params", hipMemcpyAsync(params, e->P, (size_t)n * 4, hipMemcpyDeviceToHost, e->stream));
+  HIPCHK("get params", hipStreamSynchronize(e->stream));
+  return ANE_OK;
+}
+
+extern "C" int ane_set_tokens(ane_engine* e, const uint16_t* tokens, int64_t n) {
+  CLOSED_CHECK("set tokens");
+  if (n > 0 && n < (int64_t)e->cfg.seq + 1)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane open: not enough tokens for seq=%d", e->cfg.seq);
+  if (e->data) {
+    HIPCHK("set tokens", hipStreamSynchronize(e->stream));
+    HIPCHK("set tokens", hipFree(e->data));
+    for (auto it = e->allocs.begin(); it != e->allocs.end(); ++it)
+      if (*it == (void*)e->data) { e->allocs.erase(it); break; }
+    e->data = nullptr;
+    e->ndata = 0;
+  }
+  if (n <= 0) return ANE_OK;
+  HIPCHK("set tokens", dalloc(e, &e->data, (size_t)n));
+  HIPCHK("set tokens", hipMemcpy(e->data, tokens, (size_t)n * 2, hipMemcpyHostToDevice));
+  e->ndata = n;
+  return ANE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+// One pass of the layer stack over T = nseq * seq tokens already in e->tok.
+// Leaves fp16 final-normed hidden states in e->xh.  Mirrors
+// forwardTrainingCPU (ane/train_full.go:383-453) and evalLogitsCPUInto
+// (ane/engine.go:954-1038) for nanochat; llama2 uses gain RMSNorm, SwiGLU,
+// plain residuals and no QK-norm / VE / smear / backout.
+int forward_body(ane_engine* e, int nseq) {
+  const char* op = "forward";
+  const ane_model_cfg& c = e->cfg;
+  const int D = c.dim, H = c.hidden, V = c.vocab, S = c.seq, NH = c.heads, L = c.layers;
+  const int T = nseq * S;
+  const bool llama = c.arch == ANE_ARCH_LLAMA2;
+  const float* P = e->P;
+  hipStream_t st = e->stream;
+
+  if (llama) {
+    prof_begin(e, 7);
+    HIPCHK(op, embed_lookup(e->x, P + e->pm.embed, e->tok, T, D, V, st));
+    prof_end(e, 0, (double)T * D * 8);
+  } else {
+    prof_begin(e, 7);
+    HIPCHK(op, embed_norm(e->xpre, e->x0, e->xh, P + e->pm.embed, e->tok, T, D, V, st));
+    prof_end(e, 0, (double)T * D * 14);
+    // smear (ane/common.go:324-339): x = x0 + lambda * sigmoid(SmearGate x0)[t] * x0[t-1]
+    EpiParams p;
+    p.C = e->x; p.ldc = D; p.X0 = e->x0; p.alpha_ptr = P + e->pm.smear_lambda; p.seq = S;
+    HIPCHK(op, eng_gemm(e, 7, e->xh, D, false, e->smear_h, D, false, T, D, D, EPI_SMEAR, p));
+  }
+  for (int l = 0; l < L; l++) {
+    const LayerOff& o = e->pm.L[l];
+    const LayerShadow& s = e->ls[l];
+    prof_begin(e, 6);
+    HIPCHK(op, rmsnorm_f16(e->xh, e->x, nullptr, nullptr, llama ? P + o.g_att : nullptr, T, D, st));
+    prof_end(e, 0, (double)T * D * 6);
+    {
+      EpiParams p;
+      p.C = e->qkv; p.ldc = 3 * D;
+      HIPCHK(op, eng_gemm(e, 0, e->xh, D, false, s.wqkv, D, false, T, 3 * D, D, EPI_STORE_H, p));
+    }
+    {
+      AttnArgs a;
+      memset(&a, 0, sizeof a);
+      a.qkv = e->qkv; a.out = e->att; a.lse = nullptr;
+      a.rope_cos = e->rope_cos; a.rope_sin = e->rope_sin;
+      a.nseq = nseq; a.S = S; a.NH = NH;
+      a.qknorm = llama ? 0 : 1;
+      a.scale = 0.125f;
+      if (o.ve_embed >= 0) {
+        a.ve_x = e->x; a.ve_gate = P + o.ve_gate; a.ve_embed = P + o.ve_embed; a.tokens = e->tok; a.vocab = V;
+      }
+      prof_begin(e, 5);
+      HIPCHK(op, attention_fwd(a, st));
+      // causal FLOPs: QK^T and PV over the lower triangle
+      prof_end(e, 4.0 * 64 * NH * (double)nseq * ((double)S * (S + 1) / 2), (double)T * D * 2 * 4);
+    }
+    {
+      EpiParams p;
+      p.C = e->x; p.ldc = D; p.R = e->x;
+      if (!llama) { p.alpha_ptr = P + e->pm.resid + l; p.X0 = e->x0; p.beta_ptr = P + e->pm.x0l + l; }
+      HIPCHK(op, eng_gemm(e, 1, e->att, D, false, s.wo, D, false, T, D, D, EPI_RESID, p));
+    }
+    prof_begin(e, 6);
+    HIPCHK(op, rmsnorm_f16(e->xh, e->x, nullptr, nullptr, llama ? P + o.g_ffn : nullptr, T, D, st));
+    prof_end(e, 0, (double)T * D * 6);
+    {
+      EpiParams p;
+      p.C = e->gate; p.ldc = H;
+      if (llama)
+        HIPCHK(op, eng_gemm(e, 2, e->xh, D, false, s.w13, D, false, T, 2 * H, D, EPI_SWIGLU, p));
+      else
+        HIPCHK(op, eng_gemm(e, 2, e->xh, D, false, s.w13, D, false, T, H, D, EPI_RELU2, p));
+    }
+    {
+      EpiParams p;
+      p.C = e->x; p.ldc = D; p.R = e->x;
+      if (!llama) {
+        p.alpha_ptr = P + e->pm.resid + l; p.X0 = e->x0; p.beta_ptr = P + e->pm.x0l + l;
+        if (l == L / 2 - 1) p.C2 = e->xmid;  // backout snapshot (ane/train_full.go:447-449)
+      }
+      HIPCHK(op, eng_gemm(e, 3, e->gate, H, false, s.w2, H, false, T, D, H, EPI_RESID, p));
+    }
+  }
+  // final norm (backout first for nanochat, ane/common.go:385-389)
+  prof_begin(e, 6);
+  if (llama)
+    HIPCHK(op, rmsnorm_f16(e->xh, e->x, nullptr, nullptr, P + e->pm.g_final, T, D, st));
+  else
+    HIPCHK(op, rmsnorm_f16(e->xh, e->x, e->xmid, P + e->pm.backout_lambda, nullptr, T, D, st));
+  prof_end(e, 0, (double)T * D * (llama ? 6 : 10));
+  return ANE_OK;
+}
+
+// classifier + softcap + cross-entropy partials, then the per-sequence mean
+int head_loss(ane_engine* e, int nseq, float* colscale, float dscale) {
+  const char* op = "final head";
+  const ane_model_cfg& c = e->cfg;
+  const int D = c.dim, V = c.vocab, S = c.seq;
+  const int T = nseq * S;
+  EpiParams p;
+  p.targets = e->tgt; p.partial = e->partial; p.tgt_logit = e->tgt_logit;
+  p.softcap = c.arch == ANE_ARCH_NANOCHAT; p.cap = 15.f; p.vocab = V;
+  HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_CE, p, e->ce_bm, 0));
+  prof_begin(e, 7);
+  HIPCHK(op, ce_reduce(e->loss_seq, e->lse, colscale, dscale, e->partial, e->ce_np, e->tgt_logit, e->tgt, V, nseq,
+                       S, e->stream));
+  prof_end(e, 0, (double)e->ce_np * T * 8);
+  return ANE_OK;
+}
+
+static int finish_loss(ane_engine* e, int nseq, float* loss_per_seq, float* mean_loss) {
+  const char* op = "eval loss";
+  std::vector<float> ls(nseq);
+  HIPCHK(op, hipMemcpyAsync(ls.data(), e->loss_seq, (size_t)nseq * 4, hipMemcpyDeviceToHost, e->stream));
+  HIPCHK(op, hipStreamSynchronize(e->stream));
+  double tot = 0;
+  for (int b = 0; b < nseq; b++) {
+    tot += ls[b];
+    if (loss_per_seq) loss_per_seq[b] = ls[b];
+  }
+  if (mean_loss) *mean_loss = nseq > 0 ? (float)(tot / nseq) : 0.f;
+  return ANE_OK;
+}
+
+extern "C" int ane_eval_loss(ane_engine* e, const uint16_t* tokens, const uint16_t* targets, int32_t nseq,
+                             float* loss_per_seq, float* mean_loss) {
+  CLOSED_CHECK("eval loss");
+  if (nseq <= 0 || nseq > e->opt.max_batch || !tokens || !targets)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane eval loss: nseq=%d must be in [1, %d]", nseq, e->opt.max_batch);
+  const size_t T = (size_t)nseq * e->cfg.seq;
+  HIPCHK("eval loss", hipMemcpyAsync(e->tok, tokens, T * 2, hipMemcpyHostToDevice, e->stream));
+  HIPCHK("eval loss", hipMemcpyAsync(e->tgt, targets, T * 2, hipMemcpyHostToDevice, e->stream));
+  int rc = forward_body(e, nseq);
+  if (!rc) rc = head_loss(e, nseq, nullptr, 0.f);
+  if (!rc) rc = finish_loss(e, nseq, loss_per_seq, mean_loss);
+  return rc;
+}
+
+int load_windows(ane_engine* e, const uint64_t* positions, int nseq) {
+  const char* op = "eval loss";
+  if (!e->data) return eng_fail(e, ANE_ERR_STATE, "storiesane step: not enough tokens");
+  const uint64_t S = (uint64_t)e->cfg.seq;
+  for (int b = 0; b < nseq; b++)
+    if (positions[b] + S + 1 > (uint64_t)e->ndata)
+      return eng_fail(e, ANE_ERR_ARG, "storiesane eval loss: window %d at %llu exceeds %lld tokens", b,
+                      (unsigned long long)positions[b], (long long)e->ndata);
+  HIPCHK(op, hipMemcpyAsync(e->pos_d, positions, (size_t)nseq * 8, hipMemcpyHostToDevice, e->stream));
+  HIPCHK(op, gather_windows(e->tok, e->tgt, e->data, e->pos_d, nseq, e->cfg.seq, e->stream));
+  return ANE_OK;
+}
+
+extern "C" int ane_eval_loss_windows(ane_engine* e, const uint64_t* positions, int32_t nseq, float* loss_per_seq,
+                                     float* mean_loss) {
+  CLOSED_CHECK("eval loss");
+  if (nseq <= 0 || nseq > e->opt.max_batch || !positions)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane eval loss: nseq=%d must be in [1, %d]", nseq, e->opt.max_batch);
+  int rc = load_windows(e, positions, nseq);
+  if (!rc) rc = forward_body(e, nseq);
+  if (!rc) rc = head_loss(e, nseq, nullptr, 0.f);
+  if (!rc) rc = finish_loss(e, nseq, loss_per_seq, mean_loss);
+  return rc;
+}
+
+extern "C" int ane_eval_logits(ane_engine* e, const uint16_t* tokens, int64_t ntok, float* logits) {
+  CLOSED_CHECK("eval logits");
+  if (ntok != e->cfg.seq || !tokens)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane eval logits: token len=%lld want=%d", (long long)ntok, e->cfg.seq);
+  if (!logits) return eng_fail(e, ANE_ERR_ARG, "storiesane eval logits: null output");
+  const char* op = "eval logits";
+  const ane_model_cfg& c = e->cfg;
+  const int D = c.dim, V = c.vocab, S = c.seq;
+  HIPCHK(op, hipMemcpyAsync(e->tok, tokens, (size_t)S * 2, hipMemcpyHostToDevice, e->stream));
+  int rc = forward_body(e, 1);
+  if (rc) return rc;
+  EpiParams p;
+  p.C = e->logits; p.ldc = S; p.softcap = c.arch == ANE_ARCH_NANOCHAT; p.cap = 15.f;
+  HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, S, D, EPI_LOGITS, p));
+  HIPCHK(op, hipMemcpyAsync(logits, e->logits, (size_t)V * S * 4, hipMemcpyDeviceToHost, e->stream));
+  HIPCHK(op, hipStreamSynchronize(e->stream));
+  return ANE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// profiling API
+// ---------------------------------------------------------------------------
+extern "C" int ane_profile_enable(ane_engine* e, int on) {
+  CLOSED_CHECK("profile");
+  e->prof_on = on != 0;
+  return ANE_OK;
+}
+
+extern "C" int ane_profile_read(ane_engine* e, ane_prof_entry* out, int max, int reset) {
+  CLOSED_CHECK("profile");
+  HIPCHK("profile", hipStreamSynchronize(e->stream));
+  for (size_t i = 0; i < e->prof_next; i++) {
+    ProfEvent& pe = e->prof_events[i];
+    float ms = 0.f;
+    HIPCHK("profile", hipEventElapsedTime(&ms, pe.a, pe.b));
+    ane_prof_entry& a = e->prof_acc[pe.cls];
+    a.launches++;
+    a.ms += ms;
+    a.flops += pe.flops;
+    a.bytes += pe.bytes;
+  }
+  e->prof_next = 0;
+  for (int i = 0; i < max && i < ANE_PROF_CLASSES; i++) out[i] = e->prof_acc[i];
+  if (reset)
+    for (int i = 0; i < ANE_PROF_CLASSES; i++) e->prof_acc[i] = ane_prof_entry{0, 0, 0, 0};
+  return ANE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// kernel-level diagnostics (unit tests of single kernels; no engine)
+// ---------------------------------------------------------------------------
+static std::string g_debug_err;
+
+static int debug_fail(const char* what, hipError_t h) {
+  g_debug_err = std::string("storiesane debug: ") + what + ": " + hipGetErrorString(h);
+  return ANE_ERR_HIP;
+}
+
+#define DBGCHK(expr)                                  \
+  do {                                                \
+    hipError_t _h = (expr);                           \
+    if (_h != hipSuccess) { rc = debug_fail(#expr, _h); goto done; } \
+  } while (0)
+
+extern "C" const char* ane_debug_last_error(void) { return g_debug_err.c_str(); }
+
+extern "C" int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_t* A, const uint16_t* B,
+                              void* C, int bm, int bn) {
+  if (epi != EPI_STORE_F && epi != EPI_STORE_H) {
+    g_debug_err = "storiesane debug: epilogue must be STORE_F or STORE_H";
+    return ANE_ERR_ARG;
+  }
+  int rc = ANE_OK;
+  void *dA = nullptr, *dB = nullptr, *dC = nullptr;
+  const size_t esz = epi == EPI_STORE_F ? 4 : 2;
+  GemmArgs g;
+  EpiParams p;
+  DBGCHK(hipMalloc(&dA, (size_t)M * K * 2));
+  DBGCHK(hipMalloc(&dB, (size_t)N * K * 2));
+  DBGCHK(hipMalloc(&dC, (size_t)M * N * esz));
+  DBGCHK(hipMemcpy(dA, A, (size_t)M * K * 2, hipMemcpyHostToDevice));
+  DBGCHK(hipMemcpy(dB, B, (size_t)N * K * 2, hipMemcpyHostToDevice));
+  g.A = (const half_t*)dA; g.B = (const half_t*)dB;
+  g.lda = a_t ? M : K; g.ldb = b_t ? N : K;
+  g.M = M; g.N = N; g.K = K; g.a_t = a_t != 0; g.b_t = b_t != 0;
+  p.C = dC; p.ldc = N;
+  DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn));
+  DBGCHK(hipDeviceSynchronize());
+  DBGCHK(hipMemcpy(C, dC, (size_t)M * N * esz, hipMemcpyDeviceToHost));
+done:
+  if (dA) (void)hipFree(dA);
+  if (dB) (void)hipFree(dB);
+  if (dC) (void)hipFree(dC);
+  return rc;
+}
+
+extern "C" int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, const uint16_t* qkv,
+                                   uint16_t* out, float* lse) {
+  int rc = ANE_OK;
+  const int D = 64 * NH;
+  const size_t T = (size_t)nseq * S;
+  void *dq = nullptr, *dout = nullptr, *dc = nullptr, *ds = nullptr, *dl = nullptr;
+  std::vector<float> cs((size_t)S * 32), sn((size_t)S * 32);
+  AttnArgs a;
+  memset(&a, 0, sizeof a);
+  for (int pos = 0; pos < S; pos++)
+    for (int i = 0; i < 32; i++) {
+      double f = (double)pos / pow(theta, (double)(2 * i) / 64.0);
+      cs[(size_t)pos * 32 + i] = (float)cos(f);
+      sn[(size_t)pos * 32 + i] = (float)sin(f);
+    }
+  DBGCHK(hipMalloc(&dq, T * 3 * D * 2));
+  DBGCHK(hipMalloc(&dout, T * D * 2));
+  DBGCHK(hipMalloc(&dc, cs.size() * 4));
+  DBGCHK(hipMalloc(&ds, sn.size() * 4));
+  DBGCHK(hipMalloc(&dl, T * NH * 4));
+  DBGCHK(hipMemcpy(dq, qkv, T * 3 * D * 2, hipMemcpyHostToDevice));
+  DBGCHK(hipMemcpy(dc, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  DBGCHK(hipMemcpy(ds, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  a.qkv = (const half_t*)dq; a.out = (half_t*)dout; a.lse = (float*)dl;
+  a.rope_cos = (const float*)dc; a.rope_sin = (const float*)ds;
+  a.nseq = nseq; a.S = S; a.NH = NH; a.qknorm = qknorm; a.scale = 0.125f;
+  DBGCHK(attention_fwd(a, nullptr));
+  DBGCHK(hipDeviceSynchronize());
+  DBGCHK(hipMemcpy(out, dout, T * D * 2, hipMemcpyDeviceToHost));
+  if (lse) DBGCHK(hipMemcpy(lse, dl, T * NH * 4, hipMemcpyDeviceToHost));
+done:
+  if (dq) (void)hipFree(dq);
+  if (dout) (void)hipFree(dout);
+  if (dc) (void)hipFree(dc);
+  if (ds) (void)hipFree(ds);
+  if (dl) (void)hipFree(dl);
+  return rc;
+}

@@ -1,0 +1,105 @@
+// Engine state shared by the host-side translation units of libane_hip.
+#pragma once
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/ane_hip.h"
+#include "gemm.h"
+
+struct LayerOff {
+  int64_t wq = -1, wk = -1, wv = -1, wo = -1, w1 = -1, w2 = -1, w3 = -1, g_att = -1, g_ffn = -1, ve_embed = -1,
+          ve_gate = -1;
+};
+struct ParamMap {
+  std::vector<LayerOff> L;
+  int64_t embed = -1, resid = -1, x0l = -1, smear_gate = -1, smear_lambda = -1, backout_lambda = -1,
+          g_final = -1, total = 0;
+};
+void build_param_map(const ane_model_cfg& c, ParamMap* m);
+
+struct LayerShadow {
+  ane::half_t* wqkv = nullptr;  // [3D, D]: Wq | Wk | Wv
+  ane::half_t* wo = nullptr;    // [D, D]
+  ane::half_t* w13 = nullptr;   // llama2: [2H, D] W1/W3 interleaved by 32 rows; nanochat: W1 [H, D]
+  ane::half_t* w2 = nullptr;    // [D, H]
+};
+
+struct ProfEvent {
+  hipEvent_t a = nullptr, b = nullptr;
+  int cls = 0;
+  double flops = 0, bytes = 0;
+};
+
+// drand48 (ane/engine.go:177-181, 873-880)
+inline uint64_t drand48_seed(int64_t seed) { return (((uint64_t)seed & 0xffffffffULL) << 16) | 0x330EULL; }
+inline double drand48_next(uint64_t* st) {
+  *st = (0x5DEECE66DULL * *st + 0xBULL) & ((1ULL << 48) - 1);
+  return (double)*st / (double)(1ULL << 48);
+}
+
+struct ane_engine {
+  ane_model_cfg cfg{};
+  ane_options opt{};
+  int device = 0;
+  bool dev_set = false;
+  bool closed = false;
+  std::string err;
+  hipStream_t stream = nullptr;
+  std::vector<void*> allocs;
+  ParamMap pm;
+
+  // weights
+  float* P = nullptr;  // fp32 masters, canonical layout
+  ane::half_t* shadow = nullptr;
+  std::vector<LayerShadow> ls;
+  ane::half_t* embed_h = nullptr;  // [V, D]
+  ane::half_t* smear_h = nullptr;  // [D, D]
+  float* rope_cos = nullptr;
+  float* rope_sin = nullptr;
+
+  // token stream (Options.Tokens) and per-call windows
+  uint16_t* data = nullptr;
+  int64_t ndata = 0;
+  uint16_t* tok = nullptr;
+  uint16_t* tgt = nullptr;
+  uint64_t* pos_d = nullptr;
+
+  // activations ([T, C] token-major)
+  float* x = nullptr;
+  float* x0 = nullptr;
+  float* xpre = nullptr;
+  float* xmid = nullptr;
+  ane::half_t* xh = nullptr;
+  ane::half_t* qkv = nullptr;
+  ane::half_t* att = nullptr;
+  ane::half_t* gate = nullptr;
+  int ce_bm = 256, ce_np = 0;
+  float2* partial = nullptr;
+  float* tgt_logit = nullptr;
+  float* lse = nullptr;
+  float* loss_seq = nullptr;
+  float* logits = nullptr;  // [V, S]
+
+  // host-side engine state (ane/engine.go:76-175)
+  ane_state state{};
+  uint64_t rng = 0;
+  float lr = 0.f;
+
+  // profiling
+  bool prof_on = false;
+  std::vector<ProfEvent> prof_events;
+  size_t prof_next = 0;
+  ane_prof_entry prof_acc[ANE_PROF_CLASSES] = {};
+};
+
+int eng_fail(ane_engine* e, int code, const char* fmt, ...);
+void prof_begin(ane_engine* e, int cls);
+void prof_end(ane_engine* e, double flops, double bytes);
+hipError_t eng_gemm(ane_engine* e, int cls, const ane::half_t* A, int lda, bool at, const ane::half_t* B, int ldb,
+                    bool bt, int M, int N, int K, int epi, const ane::EpiParams& p, int bm = 0, int bn = 0);
+int refresh_shadows(ane_engine* e);
+int forward_body(ane_engine* e, int nseq);
+int head_loss(ane_engine* e, int nseq, float* colscale, float dscale);
+int load_windows(ane_engine* e, const uint64_t* positions, int nseq);

@@ -1,0 +1,72 @@
+// MFMA GEMM for gfx950: C[m, n] = sum_k A(m, k) * B(n, k), fp16 in, fp32 acc.
+//
+// Operand storage (ld = leading dimension, in elements):
+//   A(m, k) = a_t ? A[k * lda + m] : A[m * lda + k]
+//   B(n, k) = b_t ? B[k * ldb + n] : B[n * ldb + k]
+// The non-transposed form is the natural one for "activation x weight^T"
+// with token-major activations [T, in] and row-major weights [out, in]
+// (the reference's linearCF, ane/common.go:91-105).  Transposed operands
+// (dX = dY * W and dW = dY^T * X of the backward) are transposed while
+// being staged into LDS, so every MFMA reads K-contiguous fragments.
+//
+// M, N must be multiples of the chosen block tile (64/128/256) and K a
+// multiple of 64; gemm_run() checks this on the host and refuses
+// anything else with hipErrorInvalidValue.
+#pragma once
+#include "hip_common.h"
+
+namespace ane {
+
+enum Epi : int {
+  EPI_STORE_H = 0,   // C (fp16) = scale * acc
+  EPI_STORE_F = 1,   // C (fp32) = scale * acc  (+= when accumulate)
+  EPI_LOGITS = 2,    // C (fp32) = softcap ? cap * tanh(acc / cap) : acc
+  EPI_RESID = 3,     // C (fp32) = alpha * R + acc + beta * X0; C2 (fp32, optional) = same
+  EPI_SWIGLU = 4,    // C (fp16) = silu(h1) * h3 over 32-column interleaved W1|W3; C2 (fp16) = h1|h3
+  EPI_RELU2 = 5,     // C (fp16) = max(acc, 0)^2; C2 (fp16, optional) = acc
+  EPI_SMEAR = 6,     // C (fp32) = X0 + [t % seq != 0] * alpha * sigmoid(acc) * X0[t-1]; C2 (fp32) = sigmoid(acc)
+  EPI_CE = 7,        // rows = vocab, cols = tokens: per-column partial (max, sumexp) + target logit
+  EPI_DLOGITS = 8,   // rows = vocab, cols = tokens: C (fp16) = dlogit (see kernel)
+  EPI_STORE_W13 = 9, // C (fp32) rows of an interleaved W1|W3 gradient scattered to two outputs
+};
+
+struct GemmArgs {
+  const half_t* A;
+  const half_t* B;
+  int lda, ldb;
+  int M, N, K;
+  bool a_t, b_t;
+};
+
+struct EpiParams {
+  void* C = nullptr;
+  int ldc = 0;
+  void* C2 = nullptr;
+  int ldc2 = 0;
+  const float* R = nullptr;   // residual input (EPI_RESID), ld = ldc
+  const float* X0 = nullptr;  // x0 (EPI_RESID / EPI_SMEAR), ld = ldc
+  float alpha = 1.f, beta = 0.f, scale = 1.f;
+  const float* alpha_ptr = nullptr;   // when set, alpha = *alpha_ptr (device scalar)
+  const float* beta_ptr = nullptr;    // when set, beta = *beta_ptr
+  int accumulate = 0;
+  int seq = 0;
+  // classifier epilogues
+  const uint16_t* targets = nullptr;  // [N] target id per token column
+  float2* partial = nullptr;          // [2 * M / BM][N] (max, sumexp)
+  float* tgt_logit = nullptr;         // [N]
+  const float* lse = nullptr;         // [N] log-sum-exp (EPI_DLOGITS)
+  const float* colscale = nullptr;    // [N] dlogit scale per token (EPI_DLOGITS)
+  int softcap = 0;
+  float cap = 15.f;
+  int vocab = 0;                      // rows >= vocab are padding (ignored)
+  float* C3 = nullptr;                // second fp32 output (EPI_STORE_W13: W3 grad)
+};
+
+// Launches one GEMM on `stream`.  bm/bn force a block tile (0 = heuristic).
+hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t stream,
+                    int bm = 0, int bn = 0);
+
+// Tile the heuristic would pick (for reporting).
+void gemm_pick_tile(int M, int N, int K, int epi, int* bm, int* bn);
+
+}  // namespace ane

@@ -1,0 +1,430 @@
+// MFMA GEMM kernels (gfx950, v_mfma_f32_32x32x16_f16) with fused epilogues.
+//
+// Block = 256 threads = 4 waves in a 2x2 grid; block tile BM x BN, k-tile 64.
+// Each wave owns a (BM/2) x (BN/2) sub-tile made of 32x32 MFMA tiles, so a
+// 256x256 block keeps 256 fp32 accumulators per lane (AGPRs) and reads
+// 8 fragments of 16 B from LDS per 16 MFMAs.  The k-loop double-buffers LDS:
+// the next k-tile is fetched from HBM into registers while the current one
+// is consumed, then written to the other LDS stage; one barrier per k-tile.
+//
+// MFMA 32x32 accumulator layout (CDNA3/CDNA4): lane l, register r holds
+// row 8*(r/4) + 4*(l/32) + (r%4), column l%32.  Operand fragments: lane l
+// supplies row l%32 of A (column l%32 of B) and 8 k-values; A and B use the
+// same k-slot assignment, so the kernel's choice k = 16*s + 8*(l/32) + j
+// only permutes the reduction order.
+#include "gemm.h"
+
+namespace ane {
+
+namespace {
+
+constexpr int BK = 64;
+
+// ---- K-major operand: rows of 64 contiguous k -------------------------------
+template <int R>
+__device__ __forceinline__ void load_kmajor(half8 (&v)[R / 32], const half_t* base, int ld, int row0,
+                                            int k0, int tid) {
+#pragma unroll
+  for (int i = 0; i < R / 32; i++) {
+    int c = tid + 256 * i;
+    int row = c >> 3, ch = c & 7;
+    v[i] = ld_h8(base + (size_t)(row0 + row) * ld + k0 + ch * 8);
+  }
+}
+template <int R>
+__device__ __forceinline__ void store_kmajor(half_t* tile, const half8 (&v)[R / 32], int tid) {
+#pragma unroll
+  for (int i = 0; i < R / 32; i++) {
+    int c = tid + 256 * i;
+    int row = c >> 3, ch = c & 7;
+    st_h8(tile + row * BK + swz(row, ch) * 8, v[i]);
+  }
+}
+
+// ---- transposed operand: element (r, k) at k * ld + r ------------------------
+// R/8 row-chunks x 8 k-chunks = R blocks of 8x8; thread tid < R owns one.
+template <int R>
+__device__ __forceinline__ void load_tmajor(half8 (&v)[8], const half_t* base, int ld, int row0, int k0,
+                                            int tid) {
+  if (tid < R) {
+    int rc = tid % (R / 8), kc = tid / (R / 8);
+#pragma unroll
+    for (int j = 0; j < 8; j++) v[j] = ld_h8(base + (size_t)(k0 + kc * 8 + j) * ld + row0 + rc * 8);
+  }
+}
+template <int R>
+__device__ __forceinline__ void store_tmajor(half_t* tile, const half8 (&v)[8], int tid) {
+  if (tid < R) {
+    int rc = tid % (R / 8), kc = tid / (R / 8);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      half8 w;
+#pragma unroll
+      for (int j = 0; j < 8; j++) w[j] = v[j][i];
+      int row = rc * 8 + i;
+      st_h8(tile + row * BK + swz(row, kc) * 8, w);
+    }
+  }
+}
+
+template <int R, bool T>
+struct Stage;
+template <int R>
+struct Stage<R, false> {
+  half8 v[R / 32];
+  __device__ __forceinline__ void load(const half_t* b, int ld, int r0, int k0, int tid) {
+    load_kmajor<R>(v, b, ld, r0, k0, tid);
+  }
+  __device__ __forceinline__ void store(half_t* tile, int tid) const { store_kmajor<R>(tile, v, tid); }
+};
+template <int R>
+struct Stage<R, true> {
+  half8 v[8];
+  __device__ __forceinline__ void load(const half_t* b, int ld, int r0, int k0, int tid) {
+    load_tmajor<R>(v, b, ld, r0, k0, tid);
+  }
+  __device__ __forceinline__ void store(half_t* tile, int tid) const { store_tmajor<R>(tile, v, tid); }
+};
+
+__device__ __forceinline__ float softcap_f(float v, float cap) { return cap * tanhf(v / cap); }
+
+template <int BM, int BN, bool AT, bool BT, int EPI>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
+  constexpr int TM = BM / 64, TN = BN / 64;
+  constexpr int STAGE = (BM + BN) * BK;
+  __shared__ __attribute__((aligned(16))) half_t lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // block -> tile: spread consecutive tiles of one XCD over a contiguous
+  // range (hardware deals block i to XCD i % 8), then walk groups of 8
+  // M-tiles so neighbouring blocks share A rows and B columns in L2.
+  const int nbm = g.M / BM, nbn = g.N / BN, nb = nbm * nbn;
+  int bid = blockIdx.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  constexpr int GROUP = 8;
+  const int group_size = GROUP * nbn;
+  const int first_m = (bid / group_size) * GROUP;
+  const int gm = min(nbm - first_m, GROUP);
+  const int bm = first_m + (bid % group_size) % gm;
+  const int bn = (bid % group_size) / gm;
+  const int m0 = bm * BM, n0 = bn * BN;
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  Stage<BM, AT> sa;
+  Stage<BN, BT> sb;
+  const int nk = g.K / BK;
+  sa.load(g.A, g.lda, m0, 0, tid);
+  sb.load(g.B, g.ldb, n0, 0, tid);
+  sa.store(lds, tid);
+  sb.store(lds + BM * BK, tid);
+  __syncthreads();
+
+  const int frow = lane & 31, fch = lane >> 5;
+  for (int kt = 0; kt < nk; kt++) {
+    const half_t* cur = lds + (kt & 1) * STAGE;
+    if (kt + 1 < nk) {
+      sa.load(g.A, g.lda, m0, (kt + 1) * BK, tid);
+      sb.load(g.B, g.ldb, n0, (kt + 1) * BK, tid);
+    }
+#pragma unroll
+    for (int s = 0; s < BK / 16; s++) {
+      half8 a[TM], b[TN];
+      const int ch = s * 2 + fch;
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        int row = wm * (BM / 2) + i * 32 + frow;
+        a[i] = ld_h8(cur + row * BK + swz(row, ch) * 8);
+      }
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        int row = wn * (BN / 2) + j * 32 + frow;
+        b[j] = ld_h8(cur + BM * BK + row * BK + swz(row, ch) * 8);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) {
+      half_t* nxt = lds + ((kt + 1) & 1) * STAGE;
+      sa.store(nxt, tid);
+      sb.store(nxt + BM * BK, tid);
+    }
+    __syncthreads();
+  }
+
+  // ---------------------------------------------------------------- epilogue
+  const int rbase = m0 + wm * (BM / 2) + 4 * (lane >> 5);
+  const int cbase = n0 + wn * (BN / 2) + (lane & 31);
+#define ROW(i, r) (rbase + (i) * 32 + 8 * ((r) >> 2) + ((r) & 3))
+#define COL(j) (cbase + (j) * 32)
+
+  if constexpr (EPI == EPI_STORE_H) {
+    half_t* C = (half_t*)e.C;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) C[(size_t)ROW(i, r) * e.ldc + COL(j)] = (half_t)(acc[i][j][r] * e.scale);
+  } else if constexpr (EPI == EPI_STORE_F) {
+    float* C = (float*)e.C;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          size_t idx = (size_t)ROW(i, r) * e.ldc + COL(j);
+          float v = acc[i][j][r] * e.scale;
+          C[idx] = e.accumulate ? C[idx] + v : v;
+        }
+  } else if constexpr (EPI == EPI_STORE_W13) {
+    // rows are 32-row blocks alternating W1 / W3 (block b even -> W1 row
+    // (b/2)*32 + r%32, odd -> W3); C = W1 grad, C3 = W3 grad, both [H, ldc]
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          int f = ROW(i, r);
+          int b = f >> 5;
+          float* dst = (b & 1) ? e.C3 : (float*)e.C;
+          size_t idx = (size_t)((b >> 1) * 32 + (f & 31)) * e.ldc + COL(j);
+          float v = acc[i][j][r] * e.scale;
+          dst[idx] = e.accumulate ? dst[idx] + v : v;
+        }
+  } else if constexpr (EPI == EPI_LOGITS) {
+    float* C = (float*)e.C;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          float v = acc[i][j][r];
+          if (e.softcap) v = softcap_f(v, e.cap);
+          C[(size_t)ROW(i, r) * e.ldc + COL(j)] = v;
+        }
+  } else if constexpr (EPI == EPI_RESID) {
+    float* C = (float*)e.C;
+    float* C2 = (float*)e.C2;
+    const float alpha = e.alpha_ptr ? *e.alpha_ptr : e.alpha;
+    const float beta = e.beta_ptr ? *e.beta_ptr : e.beta;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          size_t idx = (size_t)ROW(i, r) * e.ldc + COL(j);
+          float v = alpha * e.R[idx] + acc[i][j][r];
+          if (e.X0) v += beta * e.X0[idx];
+          C[idx] = v;
+          if (C2) C2[idx] = v;
+        }
+  } else if constexpr (EPI == EPI_SWIGLU) {
+    static_assert(TN % 2 == 0, "SwiGLU epilogue pairs 32-column tiles");
+    half_t* C = (half_t*)e.C;
+    half_t* C2 = (half_t*)e.C2;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j += 2) {
+        const int b = (COL(j) - (lane & 31)) >> 5;  // even 32-column block of W1
+        const int hcol = (b >> 1) * 32 + (lane & 31);
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          float h1 = acc[i][j][r], h3 = acc[i][j + 1][r];
+          float sg = 1.0f / (1.0f + __expf(-h1));
+          size_t row = (size_t)ROW(i, r);
+          C[row * e.ldc + hcol] = (half_t)(h1 * sg * h3);
+          if (C2) {
+            C2[row * e.ldc2 + COL(j)] = (half_t)h1;
+            C2[row * e.ldc2 + COL(j + 1)] = (half_t)h3;
+          }
+        }
+      }
+  } else if constexpr (EPI == EPI_RELU2) {
+    half_t* C = (half_t*)e.C;
+    half_t* C2 = (half_t*)e.C2;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          float h = acc[i][j][r];
+          size_t row = (size_t)ROW(i, r);
+          float rl = h > 0.f ? h : 0.f;
+          C[row * e.ldc + COL(j)] = (half_t)(rl * rl);
+          if (C2) C2[row * e.ldc2 + COL(j)] = (half_t)h;
+        }
+  } else if constexpr (EPI == EPI_SMEAR) {
+    float* C = (float*)e.C;
+    float* C2 = (float*)e.C2;
+    const float alpha = e.alpha_ptr ? *e.alpha_ptr : e.alpha;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          int t = ROW(i, r);
+          size_t idx = (size_t)t * e.ldc + COL(j);
+          float ga = 1.0f / (1.0f + __expf(-acc[i][j][r]));
+          float v = e.X0[idx];
+          if (t % e.seq != 0) v += alpha * ga * e.X0[idx - e.ldc];
+          C[idx] = v;
+          if (C2) C2[idx] = ga;
+        }
+  } else if constexpr (EPI == EPI_CE) {
+    // rows = vocab ids, columns = tokens.  Each wave reduces its BM/2 rows
+    // of every column to (max, sum exp(v - max)); lanes l and l^32 hold the
+    // two row halves of one column.
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int n = COL(j);
+      const int tg = e.targets[n];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          float v = acc[i][j][r];
+          if (e.softcap) v = softcap_f(v, e.cap);
+          acc[i][j][r] = v;
+          if (ROW(i, r) < e.vocab) mx = fmaxf(mx, v);
+          if (ROW(i, r) == tg) e.tgt_logit[n] = v;
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      float s = 0.f;
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          if (ROW(i, r) < e.vocab) s += __expf(acc[i][j][r] - mx);
+      s += __shfl_xor(s, 32, 64);
+      if (lane < 32) e.partial[(size_t)(bm * 2 + wm) * g.N + n] = make_float2(mx, s);
+    }
+  } else if constexpr (EPI == EPI_DLOGITS) {
+    // d = (softmax - onehot) * colscale[n], times (1 - tanh^2) under softcap
+    half_t* C = (half_t*)e.C;
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int n = COL(j);
+      const int tg = e.targets[n];
+      const float lse = e.lse[n], cs = e.colscale[n];
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int m = ROW(i, r);
+          float v = acc[i][j][r], dsc = 1.f;
+          if (e.softcap) {
+            float th = tanhf(v / e.cap);
+            v = e.cap * th;
+            dsc = 1.f - th * th;
+          }
+          float d = __expf(v - lse) - (m == tg ? 1.f : 0.f);
+          d = (m < e.vocab) ? d * cs * dsc : 0.f;
+          C[(size_t)m * e.ldc + n] = (half_t)d;
+        }
+    }
+  }
+#undef ROW
+#undef COL
+}
+
+template <bool AT, bool BT, int EPI, int BM, int BN>
+hipError_t launch_tile(const GemmArgs& g, const EpiParams& e, hipStream_t s) {
+  dim3 grid((g.M / BM) * (g.N / BN));
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, AT, BT, EPI>), grid, dim3(256), 0, s, g, e);
+  return hipGetLastError();
+}
+
+template <bool AT, bool BT, int EPI>
+hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, int bn) {
+  const int key = bm * 1000 + bn;
+  switch (key) {
+    case 256256: return launch_tile<AT, BT, EPI, 256, 256>(g, e, s);
+    case 256128: return launch_tile<AT, BT, EPI, 256, 128>(g, e, s);
+    case 128256: return launch_tile<AT, BT, EPI, 128, 256>(g, e, s);
+    case 128128: return launch_tile<AT, BT, EPI, 128, 128>(g, e, s);
+    case 64128: return launch_tile<AT, BT, EPI, 64, 128>(g, e, s);
+    default: break;
+  }
+  if constexpr (EPI != EPI_SWIGLU) {
+    switch (key) {
+      case 128064: return launch_tile<AT, BT, EPI, 128, 64>(g, e, s);
+      case 64064: return launch_tile<AT, BT, EPI, 64, 64>(g, e, s);
+      default: break;
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+void gemm_pick_tile(int M, int N, int K, int epi, int* pbm, int* pbn) {
+  // Candidate tiles with a relative per-FLOP efficiency (bigger wave tiles
+  // reuse each LDS fragment more).  Score = waves of blocks over the 256
+  // CUs times the cost of one block.
+  static const int cand[][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}, {64, 128}, {128, 64}, {64, 64}};
+  static const float eff[] = {1.0f, 0.92f, 0.92f, 0.80f, 0.62f, 0.62f, 0.45f};
+  const int ncu = 256;
+  float best = 1e30f;
+  int bbm = 0, bbn = 0;
+  for (int c = 0; c < 7; c++) {
+    int bm = cand[c][0], bn = cand[c][1];
+    if (M % bm || N % bn) continue;
+    if (epi == EPI_SWIGLU && bn < 128) continue;
+    long blocks = (long)(M / bm) * (N / bn);
+    long rounds = (blocks + ncu - 1) / ncu;
+    float cost = (float)rounds * (float)bm * (float)bn / eff[c];
+    if (cost < best * 0.999f) { best = cost; bbm = bm; bbn = bn; }
+  }
+  *pbm = bbm;
+  *pbn = bbn;
+  (void)K;
+}
+
+hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t s, int bm, int bn) {
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0) return hipErrorInvalidValue;
+  if (bm == 0 || bn == 0) gemm_pick_tile(g.M, g.N, g.K, epi, &bm, &bn);
+  if (bm == 0 || (g.M % bm) || (g.N % bn)) return hipErrorInvalidValue;
+  const int lay = (g.a_t ? 2 : 0) | (g.b_t ? 1 : 0);
+#define CASE(L, AT, BT, E) \
+  if (lay == L && epi == E) return launch<AT, BT, E>(g, e, s, bm, bn);
+  // forward (activation x weight^T)
+  CASE(0, false, false, EPI_STORE_H)
+  CASE(0, false, false, EPI_STORE_F)
+  CASE(0, false, false, EPI_LOGITS)
+  CASE(0, false, false, EPI_RESID)
+  CASE(0, false, false, EPI_SWIGLU)
+  CASE(0, false, false, EPI_RELU2)
+  CASE(0, false, false, EPI_SMEAR)
+  CASE(0, false, false, EPI_CE)
+  CASE(0, false, false, EPI_DLOGITS)
+  // backward dX = dY * W  (B transposed)
+  CASE(1, false, true, EPI_STORE_H)
+  CASE(1, false, true, EPI_STORE_F)
+  // backward dW = dY^T * X (both transposed)
+  CASE(3, true, true, EPI_STORE_F)
+  CASE(3, true, true, EPI_STORE_W13)
+#undef CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ane

@@ -1,0 +1,59 @@
+// Shared device helpers for the gfx950 kernels of libane_hip.
+//
+// Conventions used by every kernel in this library:
+//  * activations are token-major [T, C] (T = sequences * seq), so the
+//    channel dimension is contiguous and feeds MFMA operands directly;
+//  * GEMM operands are fp16 with fp32 accumulation; the residual stream,
+//    norm statistics and softmax statistics stay fp32;
+//  * waves are 64 lanes (CDNA4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ane {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// 16-byte chunk swizzle for LDS tiles stored as rows of 64 halves (8 chunks
+// of 16 B).  Rows r..r+7 read at one logical chunk land on 8 distinct
+// chunk slots, and so do rows r, r+8, ..., r+56 (the transposed-staging
+// write pattern), so both patterns are free of bank conflicts.
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return chunk ^ ((row ^ (row >> 3)) & 7);
+}
+
+__device__ __forceinline__ half8 ld_h8(const half_t* p) {
+  return *reinterpret_cast<const half8*>(p);
+}
+__device__ __forceinline__ void st_h8(half_t* p, half8 v) {
+  *reinterpret_cast<half8*>(p) = v;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+}  // namespace ane

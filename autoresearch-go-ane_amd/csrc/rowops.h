@@ -1,0 +1,38 @@
+// Row-wise (per token) and elementwise kernels: embedding, RMSNorm,
+// cross-entropy reduction, window gather, weight shadow conversion.
+#pragma once
+#include "hip_common.h"
+
+namespace ane {
+
+// x[t, :] = embed[tok_t, :] (zero row for tok_t >= vocab)      ane/stories/cpu.go:41-72
+hipError_t embed_lookup(float* x, const float* embed, const uint16_t* tok, int T, int D, int V,
+                        hipStream_t s);
+
+// nanochat entry: xpre = embed[tok]; x0 = xpre / rms(xpre) (fp32 scale);
+// xh = fp16(x0)                      ane/train_full.go:386-390, ane/common.go:157-174
+hipError_t embed_norm(float* xpre, float* x0, half_t* xh, const float* embed, const uint16_t* tok, int T,
+                      int D, int V, hipStream_t s);
+
+// out = fp16((x - *lam * xsub) / rms(x - lam * xsub) * gain); xsub, gain optional.
+// Gain-free form: rmsNormNoWeightCF (ane/common.go:157-174); gain form:
+// stories.RMSNorm (ane/stories/cpu.go:97-111); backout: ane/common.go:385-389.
+hipError_t rmsnorm_f16(half_t* out, const float* x, const float* xsub, const float* lam, const float* gain,
+                       int T, int D, hipStream_t s);
+
+// tok[b*S + t] = data[pos[b] + t]; tgt[b*S + t] = data[pos[b] + t + 1]   ane/engine.go:403-404
+hipError_t gather_windows(uint16_t* tok, uint16_t* tgt, const uint16_t* data, const uint64_t* pos, int nseq,
+                          int S, hipStream_t s);
+
+// Merges the classifier's per-block (max, sumexp) partials into per-token
+// log-sum-exp and the per-sequence mean cross-entropy over valid targets
+// (stories.CrossEntropyLoss, ane/stories/cpu.go:212-292).  colscale (optional)
+// receives dscale / valid_b for valid tokens and 0 otherwise.
+hipError_t ce_reduce(float* loss_seq, float* lse, float* colscale, float dscale, const float2* partial, int np,
+                     const float* tgt_logit, const uint16_t* tgt, int V, int nseq, int S, hipStream_t s);
+
+hipError_t f32_to_f16(half_t* dst, const float* src, size_t n, hipStream_t s);
+// dst [2H, D] with 32-row blocks alternating W1 / W3 rows
+hipError_t interleave_w13(half_t* dst, const float* w1, const float* w3, int H, int D, hipStream_t s);
+
+}  // namespace ane

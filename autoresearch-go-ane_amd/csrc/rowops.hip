@@ -1,0 +1,196 @@
+// Row-wise and elementwise kernels (HBM-bound).  One wave per token row:
+// lanes stride the channel dimension, so every load and store is
+// coalesced across the wave.
+#include "rowops.h"
+
+namespace ane {
+
+namespace {
+
+constexpr int ROWS_PER_BLOCK = 4;  // 4 waves
+
+__global__ __launch_bounds__(256) void embed_kernel(float* x, const float* E, const uint16_t* tok, int T, int D,
+                                                    int V) {
+  const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const int tk = tok[t];
+  float* xr = x + (size_t)t * D;
+  const float* er = E + (size_t)tk * D;
+  for (int i = lane; i < D; i += 64) xr[i] = tk < V ? er[i] : 0.f;
+}
+
+__global__ __launch_bounds__(256) void embed_norm_kernel(float* xpre, float* x0, half_t* xh, const float* E,
+                                                         const uint16_t* tok, int T, int D, int V) {
+  const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const int tk = tok[t];
+  const float* er = E + (size_t)tk * D;
+  float ss = 0.f;
+  for (int i = lane; i < D; i += 64) {
+    float v = tk < V ? er[i] : 0.f;
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  const float sc = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+  for (int i = lane; i < D; i += 64) {
+    float v = tk < V ? er[i] : 0.f;
+    size_t idx = (size_t)t * D + i;
+    xpre[idx] = v;
+    float y = v * sc;
+    x0[idx] = y;
+    xh[idx] = (half_t)y;
+  }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(half_t* out, const float* x, const float* xsub,
+                                                      const float* lamp, const float* gain, int T, int D) {
+  const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const float lam = xsub ? *lamp : 0.f;
+  const float* xr = x + (size_t)t * D;
+  const float* sr = xsub ? xsub + (size_t)t * D : nullptr;
+  float ss = 0.f;
+  for (int i = lane; i < D; i += 64) {
+    float v = xr[i];
+    if (sr) v -= lam * sr[i];
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  const float sc = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+  half_t* orow = out + (size_t)t * D;
+  for (int i = lane; i < D; i += 64) {
+    float v = xr[i];
+    if (sr) v -= lam * sr[i];
+    v *= sc;
+    if (gain) v *= gain[i];
+    orow[i] = (half_t)v;
+  }
+}
+
+__global__ void gather_kernel(uint16_t* tok, uint16_t* tgt, const uint16_t* data, const uint64_t* pos, int nseq,
+                              int S) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nseq * S) return;
+  const int b = i / S, t = i % S;
+  const uint64_t p = pos[b] + (uint64_t)t;
+  tok[i] = data[p];
+  tgt[i] = data[p + 1];
+}
+
+__global__ __launch_bounds__(256) void ce_reduce_kernel(float* loss_seq, float* lse_out, float* colscale,
+                                                        float dscale, const float2* partial, int np,
+                                                        const float* tgt_logit, const uint16_t* tgt, int V, int S,
+                                                        int T) {
+  const int b = blockIdx.x;
+  __shared__ float red_l[256];
+  __shared__ int red_v[256];
+  float lsum = 0.f;
+  int nvalid = 0;
+  for (int t = threadIdx.x; t < S; t += blockDim.x) {
+    const int n = b * S + t;
+    float mx = -INFINITY;
+    for (int p = 0; p < np; p++) mx = fmaxf(mx, partial[(size_t)p * T + n].x);
+    float sum = 0.f;
+    for (int p = 0; p < np; p++) {
+      float2 v = partial[(size_t)p * T + n];
+      sum += v.y * __expf(v.x - mx);
+    }
+    const float lse = mx + __logf(sum);
+    if (lse_out) lse_out[n] = lse;
+    if (tgt[n] < V) {
+      const float logp = tgt_logit[n] - lse;
+      const float floor_ = -23.025850929940457f;  // log(1e-10)
+      lsum += -(logp > floor_ ? logp : floor_);
+      nvalid++;
+    }
+  }
+  red_l[threadIdx.x] = lsum;
+  red_v[threadIdx.x] = nvalid;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      red_l[threadIdx.x] += red_l[threadIdx.x + o];
+      red_v[threadIdx.x] += red_v[threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  const int valid = red_v[0];
+  if (threadIdx.x == 0) loss_seq[b] = valid > 0 ? red_l[0] / (float)valid : 0.f;
+  if (colscale) {
+    const float cs = valid > 0 ? dscale / (float)valid : 0.f;
+    for (int t = threadIdx.x; t < S; t += blockDim.x) {
+      const int n = b * S + t;
+      colscale[n] = tgt[n] < V ? cs : 0.f;
+    }
+  }
+}
+
+__global__ void f32_to_f16_kernel(half_t* dst, const float* src, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) dst[i] = (half_t)src[i];
+}
+
+__global__ void interleave_w13_kernel(half_t* dst, const float* w1, const float* w3, int H, int D) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t n = (size_t)2 * H * D, stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    const int f = (int)(i / D), c = (int)(i % D);
+    const int blk = f >> 5;
+    const int row = (blk >> 1) * 32 + (f & 31);
+    const float* src = (blk & 1) ? w3 : w1;
+    dst[i] = (half_t)src[(size_t)row * D + c];
+  }
+}
+
+inline int rows_grid(int T) { return (T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK; }
+inline int flat_grid(size_t n) {
+  size_t g = (n + 255) / 256;
+  return (int)(g > 65536 ? 65536 : (g == 0 ? 1 : g));
+}
+
+}  // namespace
+
+hipError_t embed_lookup(float* x, const float* E, const uint16_t* tok, int T, int D, int V, hipStream_t s) {
+  hipLaunchKernelGGL(embed_kernel, dim3(rows_grid(T)), dim3(256), 0, s, x, E, tok, T, D, V);
+  return hipGetLastError();
+}
+
+hipError_t embed_norm(float* xpre, float* x0, half_t* xh, const float* E, const uint16_t* tok, int T, int D,
+                      int V, hipStream_t s) {
+  hipLaunchKernelGGL(embed_norm_kernel, dim3(rows_grid(T)), dim3(256), 0, s, xpre, x0, xh, E, tok, T, D, V);
+  return hipGetLastError();
+}
+
+hipError_t rmsnorm_f16(half_t* out, const float* x, const float* xsub, const float* lam, const float* gain, int T,
+                       int D, hipStream_t s) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows_grid(T)), dim3(256), 0, s, out, x, xsub, lam, gain, T, D);
+  return hipGetLastError();
+}
+
+hipError_t gather_windows(uint16_t* tok, uint16_t* tgt, const uint16_t* data, const uint64_t* pos, int nseq, int S,
+                          hipStream_t s) {
+  const int n = nseq * S;
+  hipLaunchKernelGGL(gather_kernel, dim3((n + 255) / 256), dim3(256), 0, s, tok, tgt, data, pos, nseq, S);
+  return hipGetLastError();
+}
+
+hipError_t ce_reduce(float* loss_seq, float* lse, float* colscale, float dscale, const float2* partial, int np,
+                     const float* tgt_logit, const uint16_t* tgt, int V, int nseq, int S, hipStream_t s) {
+  hipLaunchKernelGGL(ce_reduce_kernel, dim3(nseq), dim3(256), 0, s, loss_seq, lse, colscale, dscale, partial, np,
+                     tgt_logit, tgt, V, S, nseq * S);
+  return hipGetLastError();
+}
+
+hipError_t f32_to_f16(half_t* dst, const float* src, size_t n, hipStream_t s) {
+  hipLaunchKernelGGL(f32_to_f16_kernel, dim3(flat_grid(n)), dim3(256), 0, s, dst, src, n);
+  return hipGetLastError();
+}
+
+hipError_t interleave_w13(half_t* dst, const float* w1, const float* w3, int H, int D, hipStream_t s) {
+  hipLaunchKernelGGL(interleave_w13_kernel, dim3(flat_grid((size_t)2 * H * D)), dim3(256), 0, s, dst, w1, w3, H,
+                     D);
+  return hipGetLastError();
+}
+
+}  // namespace ane

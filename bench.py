@@ -1,0 +1,120 @@
+"""Benchmark: stories110M forward + loss at B32 x 256 on one MI355X.
+
+One "step" = one batched forward + mean cross-entropy over 32 sequences of
+256 tokens (8192 tokens), the workload of BASELINE configs[1]: Llama2-style
+stories110M (SwiGLU, gain RMSNorm, RoPE 1e4), weights N(0, 0.02) from seed 0,
+token ids uniform in [0, 32000) from seed 2, fp16 weights/activations with
+fp32 accumulation.  The token windows are resident in HBM before timing
+starts (Options.Tokens + per-call window positions).
+
+Prints ONE JSON line.  Besides the throughput it carries:
+  roofline      the dominant kernel's achieved TFLOP/s (algorithmic FLOPs per
+                launch / mean launch time from HIP events recorded on the
+                engine's stream during the timed steps) against the MI355X
+                dense fp16 MFMA peak;
+  cpu_baseline  the reference's CPU path (the C oracle, with the reference's
+                threading: serial linearCF, parallel norms / classifier / CE)
+                timed on a bounded sample of the same workload on this host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "autoresearch-go-ane_amd"), os.path.join(ROOT, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+METRIC = "fwd+loss tokens/s (stories110M, B32x256, fp16) + MFMA util %; decode tok/s"
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def cpu_baseline(cfg, params, tok, tgt, threads):
+    """Times the oracle (reference CPU-path semantics) on one sequence."""
+    import oracle
+    oracle.set_threads(threads, parallel_linear=False)
+    t0 = time.perf_counter()
+    oracle.forward_loss(cfg, params, tok[:1], tgt[:1])
+    dt = time.perf_counter() - t0
+    return {"value": round(cfg.seq / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"1 of the 32 sequences ({cfg.seq} tokens), {dt:.1f} s; oracle/refcpu.c with the "
+                      "reference's threading (serial linearCF, parallelFor over tokens/vocab elsewhere)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--arch", default="llama2", choices=["llama2", "nanochat"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-profile", action="store_true", help="time without per-launch HIP events")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the forward shards "
+              "by sequence with no exchange, so N GPUs would each run this same single-GPU workload.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import ane
+    cfg = ane.stories110m(args.arch)
+    B, S = args.batch, cfg.seq
+    params = ane.init_params(cfg, seed=0, std=0.02)
+    tok, tgt = ane.make_tokens(cfg, B, seed=2)
+    # resident token stream: window b = stream[b*(S+1) : b*(S+1)+S+1]
+    stream = np.concatenate([np.concatenate([tok[b], tgt[b][-1:]]) for b in range(B)]).astype(np.uint16)
+    pos = np.arange(B, dtype=np.uint64) * np.uint64(S + 1)
+    eng = ane.Open(ane.Options(Config=cfg, Params=params, MaxBatch=B, Tokens=stream))
+
+    for _ in range(args.warmup):
+        eng.EvalLossWindows(pos)
+    eng.Sync()
+    if not args.no_profile:
+        eng.ProfileEnable(True)
+        eng.ProfileRead(reset=True)
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        loss, _ = eng.EvalLossWindows(pos)
+    eng.Sync()
+    dt = time.perf_counter() - t0
+    ms = dt / args.steps * 1e3
+    tps = B * S * args.steps / dt
+
+    out = {"metric": METRIC, "value": round(tps, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": "fp16",
+           "data": "synthetic: token ids uniform [0,32000) seed 2; random-init N(0,0.02) weights seed 0",
+           "config": {"workload": f"stories110M-{args.arch} forward+loss, batch {B} x seq {S} (BASELINE configs[1])",
+                      "arch": args.arch, "batch": B, "seq": S, "tokens_per_step": B * S},
+           "loss": round(loss, 6)}
+    if not args.no_profile:
+        prof = eng.ProfileRead(reset=True)
+        gemm_cls = ["qkv_gemm", "wo_gemm", "ffn_up_gemm", "ffn_down_gemm", "classifier_gemm"]
+        dom = max(prof, key=lambda k: prof[k]["ms"])
+        d = prof[dom]
+        avg_ms = d["ms"] / max(1, d["launches"])
+        per_launch = d["flops"] / max(1, d["launches"])
+        achieved = per_launch / (avg_ms * 1e-3) / 1e12
+        out["roofline"] = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
+                           "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                           "traffic": None, "avg_launch_ms": round(avg_ms, 5), "flops_per_launch": per_launch}
+        g_ms = sum(prof[k]["ms"] for k in gemm_cls)
+        g_fl = sum(prof[k]["flops"] for k in gemm_cls)
+        out["mfma_util_projection_gemms"] = round(g_fl / (g_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)
+        out["kernel_ms_per_step"] = {k: round(v["ms"] / args.steps, 4) for k, v in prof.items()}
+    eng.Destroy()
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        out["cpu_baseline"] = cpu_baseline(cfg, params, tok, tgt, threads)
+        out["gpu_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

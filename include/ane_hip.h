@@ -1,0 +1,183 @@
+/*
+ * ane_hip.h -- C-ABI of libane_hip.so, the MI355X (gfx950) engine for the
+ * reference's `ane` transformer compute path (tmc/autoresearch-go-ane).
+ *
+ * Every entry point takes plain pointers and sizes.  Host buffers are
+ * caller-owned and only read or written for the duration of the call;
+ * device memory is owned by the engine from ane_open() to ane_close().
+ * One engine = one HIP device + one HIP stream; an engine is not
+ * thread-safe (the reference's Engine is not goroutine-safe either).
+ *
+ * Return value of every int entry point: ANE_OK (0) or a negative ANE_ERR_*
+ * code; ane_last_error() then holds a message in the reference's wording
+ * ("storiesane <op>: ...").  There is no silent fallback: a HIP failure is
+ * returned, never replaced by a CPU computation.
+ *
+ * Layouts at the boundary follow the reference:
+ *   - parameters: one flat fp32 vector in the canonical order of
+ *     ane_param_layout() (nanochat: the order of writeModelGrad,
+ *     ane/engine.go:811-840);
+ *   - logits: vocab-major [vocab, seq] per sequence, as EvalLogits returns
+ *     them (ane/engine.go:449-462, ane/stories/cpu.go:303-327);
+ *   - tokens: uint16 ids.
+ */
+#ifndef ANE_HIP_H
+#define ANE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  ANE_OK = 0,
+  ANE_ERR_CLOSED = -1,  /* "storiesane <op>: engine is closed" */
+  ANE_ERR_ARG = -2,     /* bad length / size / configuration */
+  ANE_ERR_HIP = -3,     /* a HIP runtime call or kernel launch failed */
+  ANE_ERR_NOMEM = -4,   /* device allocation failed */
+  ANE_ERR_STATE = -5    /* call not valid in the engine's current state */
+};
+
+enum { ANE_ARCH_NANOCHAT = 0, ANE_ARCH_LLAMA2 = 1 };
+enum { ANE_GRAD_COMPAT = 0, ANE_GRAD_TRUE = 1 };
+
+/* Model shape.  The reference fixes these as package constants
+ * (ane/stories/config.go:3-18: Dim 768, Hidden 2048, Heads 12, Layers 12,
+ * Vocab 32000, SeqDefault 256) and RoPE theta 1e5 (ane/train_util.go:196).
+ * arch NANOCHAT is the reference's CPU-path model; LLAMA2 is the SwiGLU /
+ * gain-RMSNorm variant of the benchmark configs.  Constraints of the
+ * kernels: dim == 64 * heads, dim, hidden, vocab multiples of 64, seq a
+ * multiple of 64 and <= 512. */
+typedef struct ane_model_cfg {
+  int32_t dim, hidden, heads, layers, vocab, seq;
+  int32_t arch;      /* ANE_ARCH_* */
+  int32_t grad_mode; /* ANE_GRAD_*: COMPAT reproduces the reference backward */
+  double rope_theta; /* 0 selects the arch default (1e5 nanochat, 1e4 llama2) */
+} ane_model_cfg;
+
+/* Options (ane/engine.go:14-40).  Zero fields take the reference defaults
+ * applied in Open (ane/engine.go:185-240).  ModelPath / UseANE /
+ * HybridBackward / CPUClassifierHead / GradTaskLimit have no meaning here:
+ * weights arrive through ane_set_params, the device path is the only path.
+ * max_batch sizes the device activation buffers (sequences per call). */
+typedef struct ane_options {
+  int32_t accum_steps;
+  float lr;
+  int64_t seed;
+  float adam_beta1, adam_beta2, adam_eps, weight_decay, grad_clip, loss_scale;
+  float embed_lr_mult, scalar_lr_mult, lambda_lr_mult;
+  float lambda_beta1, lambda_beta2;
+  int32_t max_batch;
+  int32_t device;
+} ane_options;
+
+/* State (ane/engine.go:43-52). */
+typedef struct ane_state {
+  uint64_t token_pos;
+  float last_loss;
+  double cum_train_ms, cum_wall_ms;
+  uint32_t cum_steps, cum_batches, adam_t, pending_steps;
+} ane_state;
+
+/* StepResult (ane/engine.go:55-69); durations in nanoseconds.  The ANE /
+ * compile fields keep their names; on this engine "ane_eval_ns" is the
+ * device time of the forward and backward kernels (HIP events). */
+typedef struct ane_step_result {
+  float loss;
+  int64_t step_ns, compile_ns, startup_compile_ns, ane_eval_ns, cpu_work_ns, weight_refresh_ns,
+      final_head_ns, embed_grad_ns, rms_dw_ns, dw_gemm_ns, dw_wait_ns, adam_ns;
+} ane_step_result;
+
+typedef struct ane_engine ane_engine;
+
+/* ---- lifecycle ---------------------------------------------------------- */
+
+/* Open (ane/engine.go:184-355): allocates device buffers for max_batch
+ * sequences, zero-initialised weights and optimizer state. */
+int ane_open(const ane_model_cfg *cfg, const ane_options *opts, ane_engine **out);
+/* Close (ane/engine.go:567-644): frees all device memory; later calls
+ * return ANE_ERR_CLOSED.  The handle itself stays valid until
+ * ane_destroy(). */
+void ane_close(ane_engine *e);
+void ane_destroy(ane_engine *e);
+const char *ane_last_error(const ane_engine *e);
+
+/* Number of fp32 parameters, and the canonical segments (offset, size) in
+ * order; returns the segment count (writes at most max entries). */
+int64_t ane_param_count(const ane_model_cfg *cfg);
+int ane_param_layout(const ane_model_cfg *cfg, int64_t *offsets, int64_t *sizes, int max);
+
+/* Weight load / read-back: the device replacement of LoadPretrained /
+ * LoadCheckpoint's weight copy (ane/stories/weights.go:73-153) and of the
+ * per-update weight re-staging (refreshANERuntimeForWeights,
+ * ane/runtime.go:25-69): fp32 masters live in HBM and the fp16 GEMM
+ * shadows are rebuilt on the device. */
+int ane_set_params(ane_engine *e, const float *params, int64_t n);
+int ane_get_params(ane_engine *e, float *params, int64_t n);
+
+/* Options.Tokens (ane/engine.go:17): the token stream the window sampler
+ * draws from, copied once into HBM. */
+int ane_set_tokens(ane_engine *e, const uint16_t *tokens, int64_t n);
+
+/* ---- forward ------------------------------------------------------------ */
+
+/* EvalLogits (ane/engine.go:449-462): one sequence of exactly seq tokens;
+ * writes vocab*seq fp32 logits, vocab-major (after the 15*tanh softcap
+ * for nanochat). */
+int ane_eval_logits(ane_engine *e, const uint16_t *tokens, int64_t ntok, float *logits);
+
+/* Batched forward + mean cross-entropy over nseq sequences (the loss of
+ * runFinalHead / stories.CrossEntropyLoss, ane/train_full.go:480-508,
+ * ane/stories/cpu.go:212-292, without the backward).  tokens/targets:
+ * [nseq][seq] host arrays; targets >= vocab are excluded.  loss_per_seq
+ * (optional): mean CE of each sequence; *mean_loss: mean over sequences. */
+int ane_eval_loss(ane_engine *e, const uint16_t *tokens, const uint16_t *targets, int32_t nseq,
+                  float *loss_per_seq, float *mean_loss);
+
+/* Same, over windows of the resident token stream: sequence b is
+ * tokens[pos[b] : pos[b]+seq], targets shifted by one (the window rule of
+ * Step, ane/engine.go:395-405).  Inputs never leave HBM. */
+int ane_eval_loss_windows(ane_engine *e, const uint64_t *positions, int32_t nseq, float *loss_per_seq,
+                          float *mean_loss);
+
+/* ---- diagnostics -------------------------------------------------------- */
+
+/* Per-kernel-class device timing with HIP events on the engine's stream.
+ * When enabled, every launch of the classes below is bracketed by events;
+ * ane_profile_read() synchronises and returns, per class, the launch
+ * count, summed milliseconds, and the algorithmic FLOPs and HBM bytes of
+ * those launches.  Classes: 0 qkv-gemm, 1 wo-gemm, 2 ffn-up-gemm,
+ * 3 ffn-down-gemm, 4 classifier-gemm, 5 attention, 6 rmsnorm, 7 other. */
+enum { ANE_PROF_CLASSES = 8 };
+typedef struct ane_prof_entry {
+  int64_t launches;
+  double ms;
+  double flops;
+  double bytes;
+} ane_prof_entry;
+int ane_profile_enable(ane_engine *e, int on);
+int ane_profile_read(ane_engine *e, ane_prof_entry *out, int max, int reset);
+
+/* Blocks until all queued device work of the engine has finished. */
+int ane_sync(ane_engine *e);
+
+/* Single-kernel entry points for unit tests (no counterpart in the
+ * reference; they run one kernel on device 0 from host buffers).
+ * ane_debug_gemm: C = A(m,k) B(n,k)^T with A stored [K, M] when a_t else
+ * [M, K], B stored [K, N] when b_t else [N, K] (fp16 bit patterns); C is
+ * [M, N] fp32 (epi 1) or fp16 (epi 0); bm/bn force a block tile (0 = auto).
+ * ane_debug_attention: causal attention over qkv [nseq*S, 3*64*NH] (fp16,
+ * q|k|v per row, pre-RoPE) -> out [nseq*S, 64*NH] fp16 and lse [nseq*S, NH].
+ * Messages: ane_debug_last_error(). */
+int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_t *A, const uint16_t *B,
+                   void *C, int bm, int bn);
+int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, const uint16_t *qkv, uint16_t *out,
+                        float *lse);
+const char *ane_debug_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,66 @@
+"""C-ABI checks that run without a GPU: the library loads, exports every
+entry point include/ane_hip.h declares, and its host-side layout functions
+agree with the Python mirror and the oracle.  No device call is made."""
+import ctypes
+import os
+import re
+
+import numpy as np
+
+import ane
+from ane import _lib
+import oracle
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    names = []
+    inc = os.path.join(ROOT, "include")
+    for fn in sorted(os.listdir(inc)):
+        if not fn.endswith(".h"):
+            continue
+        src = open(os.path.join(inc, fn)).read()
+        src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+        names += re.findall(r"^[A-Za-z_][\w \*]*?\b(ane_\w+)\s*\(", src, flags=re.M)
+    return sorted(set(names))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    for must in ("ane_open", "ane_close", "ane_eval_logits", "ane_eval_loss", "ane_set_params"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    # and the Python binding covers each of them
+    assert sorted(_lib.SIGNATURES) == declared_functions()
+    _lib.load()
+
+
+def test_param_layout_matches_python_and_oracle():
+    lib = _lib.load()
+    for arch in ("llama2", "nanochat"):
+        for cfg in (ane.tiny(arch), ane.stories110m(arch), ane.tiny(arch, layers=3)):
+            mc = _lib.model_cfg(cfg)
+            n = lib.ane_param_count(ctypes.byref(mc))
+            assert n == ane.param_count(cfg) == oracle.param_count(cfg)
+            nseg = lib.ane_param_layout(ctypes.byref(mc), None, None, 0)
+            off = (ctypes.c_int64 * nseg)()
+            sz = (ctypes.c_int64 * nseg)()
+            lib.ane_param_layout(ctypes.byref(mc), off, sz, nseg)
+            got = [(off[i], sz[i]) for i in range(nseg)]
+            assert got == oracle.param_segments(cfg)
+            assert got == [(o, int(np.prod(s))) for _, o, s in ane.param_layout(cfg)]
+
+
+def test_open_requires_weights():
+    try:
+        ane.Open(ane.Options())
+    except ane.EngineError as e:
+        assert str(e) == "storiesane open: model path is empty"
+    else:
+        raise AssertionError("Open without weights must fail")

@@ -1,0 +1,110 @@
+"""Single-kernel parity on the GPU (through the C-ABI debug entry points).
+
+GEMM: every operand layout and block tile against a float64 matmul of the
+same fp16-rounded operands (fp32 accumulation: ~1e-6 relative).
+Attention: the fused causal kernel (RoPE, optional QK-norm) against a
+float64 numpy restatement of causalAttentionCF (ane/common.go:61-89) with
+RoPE (ane/train_util.go:204-224) and QK-norm (ane/common.go:199-227).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from ane import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def _u16(a):
+    return a.ctypes.data_as(C.POINTER(C.c_uint16))
+
+
+def run_gemm(A, B, a_t, b_t, bm=0, bn=0, out_f16=False):
+    """A: (M,K) logical, B: (N,K) logical, both float16 arrays."""
+    lib = _lib.load()
+    M, K = A.shape
+    N = B.shape[0]
+    As = np.ascontiguousarray(A.T if a_t else A).view(np.uint16)
+    Bs = np.ascontiguousarray(B.T if b_t else B).view(np.uint16)
+    out = np.zeros((M, N), np.float16 if out_f16 else np.float32)
+    rc = lib.ane_debug_gemm(int(a_t), int(b_t), 0 if out_f16 else 1, M, N, K, _u16(As), _u16(Bs),
+                            out.ctypes.data_as(C.c_void_p), bm, bn)
+    assert rc == 0, lib.ane_debug_last_error()
+    return out
+
+
+TILES = [(256, 256), (256, 128), (128, 256), (128, 128), (64, 128), (128, 64), (64, 64)]
+
+
+@pytest.mark.parametrize("a_t,b_t", [(False, False), (False, True), (True, True)])
+@pytest.mark.parametrize("bm,bn", TILES)
+def test_gemm_layouts_and_tiles(a_t, b_t, bm, bn):
+    r = np.random.default_rng(bm * 7 + bn + 3 * a_t + b_t)
+    M, N, K = 512, 256, 320
+    A = r.standard_normal((M, K)).astype(np.float16)
+    B = r.standard_normal((N, K)).astype(np.float16)
+    got = run_gemm(A, B, a_t, b_t, bm, bn)
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-4)
+
+
+def test_gemm_real_shapes_auto_tile():
+    r = np.random.default_rng(5)
+    for (M, N, K) in [(1024, 2304, 768), (512, 768, 2048), (1024, 4096, 768)]:
+        A = (r.standard_normal((M, K)) * 0.5).astype(np.float16)
+        B = (r.standard_normal((N, K)) * 0.02).astype(np.float16)
+        got = run_gemm(A, B, False, False)
+        ref = A.astype(np.float64) @ B.astype(np.float64).T
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+    got16 = run_gemm(A, B, False, False, out_f16=True)
+    np.testing.assert_allclose(got16.astype(np.float64), ref, rtol=2e-3, atol=1e-3)
+
+
+def attn_ref(qkv, nseq, S, NH, qknorm, theta):
+    x = qkv.astype(np.float64).reshape(nseq, S, 3, NH, 64)
+    q, k, v = x[:, :, 0], x[:, :, 1], x[:, :, 2]
+    ang = np.arange(S)[:, None] / theta ** (2 * np.arange(32)[None, :] / 64)
+    c, s = np.cos(ang)[None, :, None, :], np.sin(ang)[None, :, None, :]
+
+    def rope(z):
+        e, o = z[..., 0::2], z[..., 1::2]
+        out = np.empty_like(z)
+        out[..., 0::2] = e * c - o * s
+        out[..., 1::2] = o * c + e * s
+        return out
+
+    q, k = rope(q), rope(k)
+    if qknorm:
+        q = 1.2 * q / np.sqrt((q * q).mean(-1, keepdims=True) + 1e-5)
+        k = 1.2 * k / np.sqrt((k * k).mean(-1, keepdims=True) + 1e-5)
+    sc = np.einsum("bshd,bthd->bhst", q, k) / 8.0
+    sc = np.where(np.tril(np.ones((S, S), bool))[None, None], sc, -np.inf)
+    mx = sc.max(-1, keepdims=True)
+    p = np.exp(sc - mx)
+    lse = (mx[..., 0] + np.log(p.sum(-1)))
+    p /= p.sum(-1, keepdims=True)
+    out = np.einsum("bhst,bthd->bshd", p, v).reshape(nseq * S, NH * 64)
+    return out, lse.transpose(0, 2, 1).reshape(nseq * S, NH)
+
+
+@pytest.mark.parametrize("S,NH,nseq,qknorm", [(256, 12, 2, True), (256, 4, 3, False), (64, 2, 1, True),
+                                             (128, 3, 2, False), (512, 2, 1, True)])
+def test_attention_matches_f64(S, NH, nseq, qknorm):
+    lib = _lib.load()
+    r = np.random.default_rng(S + NH + nseq)
+    D = 64 * NH
+    qkv = r.standard_normal((nseq * S, 3 * D)).astype(np.float16)
+    out = np.zeros((nseq * S, D), np.float16)
+    lse = np.zeros((nseq * S, NH), np.float32)
+    theta = 100000.0 if qknorm else 10000.0
+    rc = lib.ane_debug_attention(nseq, S, NH, int(qknorm), theta, _u16(qkv.view(np.uint16)),
+                                 _u16(out.view(np.uint16)), lse.ctypes.data_as(C.POINTER(C.c_float)))
+    assert rc == 0, lib.ane_debug_last_error()
+    ref, ref_lse = attn_ref(qkv, nseq, S, NH, qknorm, theta)
+    tol = 2e-2 if qknorm else 6e-3
+    np.testing.assert_allclose(out.astype(np.float64), ref, atol=tol)
+    np.testing.assert_allclose(lse, ref_lse, atol=tol * 2)
+    # row 0 of every sequence attends only to itself: out = v[0]
+    v0 = qkv.reshape(nseq, S, 3, D)[:, 0, 2].astype(np.float64)
+    np.testing.assert_allclose(out.reshape(nseq, S, D)[:, 0].astype(np.float64), v0, atol=2e-3)
