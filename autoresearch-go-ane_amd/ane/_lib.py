@@ -81,6 +81,7 @@ SIGNATURES = {
                                  C.c_int, C.c_int]),
     "ane_debug_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, _u16, _u16, _fp]),
     "ane_debug_last_error": (C.c_char_p, []),
+    "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 9 + [_fp]),
 }
 
 _lib = None

@@ -305,11 +305,13 @@ static int open_impl(ane_engine* e) {
   HIPCHK(op, dalloc(e, &e->qkv, T * 3 * D));
   HIPCHK(op, dalloc(e, &e->att, T * D));
   HIPCHK(op, dalloc(e, &e->gate, T * H));
-  e->ce_bm = (V % 256 == 0) ? 256 : ((V % 128 == 0) ? 128 : 64);
-  e->ce_np = 2 * V / e->ce_bm;
+  // classifier block rows: one (max, sumexp) partial per block row and token
+  e->ce_bm = (V % 128 == 0) ? 128 : 64;
+  e->ce_np = V / e->ce_bm;
   HIPCHK(op, dalloc(e, &e->partial, (size_t)e->ce_np * T));
   HIPCHK(op, dalloc(e, &e->tgt_logit, T));
   HIPCHK(op, dalloc(e, &e->lse, T));
+  HIPCHK(op, dalloc(e, &e->tok_loss, T));
   HIPCHK(op, dalloc(e, &e->loss_seq, (size_t)e->opt.max_batch));
   HIPCHK(op, dalloc(e, &e->logits, (size_t)V * S));
   (void)NH;
@@ -527,7 +529,7 @@ int head_loss(ane_engine* e, int nseq, float* colscale, float dscale) {
   p.softcap = c.arch == ANE_ARCH_NANOCHAT; p.cap = 15.f; p.vocab = V;
   HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_CE, p, e->ce_bm, 0));
   prof_begin(e, 7);
-  HIPCHK(op, ce_reduce(e->loss_seq, e->lse, colscale, dscale, e->partial, e->ce_np, e->tgt_logit, e->tgt, V, nseq,
+  HIPCHK(op, ce_reduce(e->loss_seq, e->lse, e->tok_loss, colscale, dscale, e->partial, e->ce_np, e->tgt_logit, e->tgt, V, nseq,
                        S, e->stream));
   prof_end(e, 0, (double)e->ce_np * T * 8);
   return ANE_OK;
@@ -676,6 +678,48 @@ extern "C" int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, co
   DBGCHK(hipDeviceSynchronize());
   DBGCHK(hipMemcpy(C, dC, (size_t)M * N * esz, hipMemcpyDeviceToHost));
 done:
+  if (dA) (void)hipFree(dA);
+  if (dB) (void)hipFree(dB);
+  if (dC) (void)hipFree(dC);
+  return rc;
+}
+
+// Times `iters` launches of one GEMM (device-resident operands filled with
+// small values) with HIP events; *avg_ms receives the mean launch time.
+extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int iters,
+                                    float* avg_ms) {
+  if (epi != EPI_STORE_F && epi != EPI_STORE_H) {
+    g_debug_err = "storiesane debug: epilogue must be STORE_F or STORE_H";
+    return ANE_ERR_ARG;
+  }
+  int rc = ANE_OK;
+  void *dA = nullptr, *dB = nullptr, *dC = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  GemmArgs g;
+  EpiParams p;
+  float ms = 0.f;
+  DBGCHK(hipMalloc(&dA, (size_t)M * K * 2));
+  DBGCHK(hipMalloc(&dB, (size_t)N * K * 2));
+  DBGCHK(hipMalloc(&dC, (size_t)M * N * (epi == EPI_STORE_F ? 4 : 2)));
+  DBGCHK(hipMemset(dA, 0x11, (size_t)M * K * 2));
+  DBGCHK(hipMemset(dB, 0x11, (size_t)N * K * 2));
+  DBGCHK(hipEventCreate(&e0));
+  DBGCHK(hipEventCreate(&e1));
+  g.A = (const half_t*)dA; g.B = (const half_t*)dB;
+  g.lda = a_t ? M : K; g.ldb = b_t ? N : K;
+  g.M = M; g.N = N; g.K = K; g.a_t = a_t != 0; g.b_t = b_t != 0;
+  p.C = dC; p.ldc = N;
+  DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn));
+  DBGCHK(hipDeviceSynchronize());
+  DBGCHK(hipEventRecord(e0, nullptr));
+  for (int i = 0; i < iters; i++) DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn));
+  DBGCHK(hipEventRecord(e1, nullptr));
+  DBGCHK(hipEventSynchronize(e1));
+  DBGCHK(hipEventElapsedTime(&ms, e0, e1));
+  *avg_ms = ms / (float)(iters > 0 ? iters : 1);
+done:
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
   if (dA) (void)hipFree(dA);
   if (dB) (void)hipFree(dB);
   if (dC) (void)hipFree(dC);

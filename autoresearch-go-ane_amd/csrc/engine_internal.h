@@ -79,6 +79,7 @@ struct ane_engine {
   float2* partial = nullptr;
   float* tgt_logit = nullptr;
   float* lse = nullptr;
+  float* tok_loss = nullptr;
   float* loss_seq = nullptr;
   float* logits = nullptr;  // [V, S]
 

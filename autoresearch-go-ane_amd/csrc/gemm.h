@@ -52,7 +52,7 @@ struct EpiParams {
   int seq = 0;
   // classifier epilogues
   const uint16_t* targets = nullptr;  // [N] target id per token column
-  float2* partial = nullptr;          // [2 * M / BM][N] (max, sumexp)
+  float2* partial = nullptr;          // [M / BM][N] (max, sumexp) per block row
   float* tgt_logit = nullptr;         // [N]
   const float* lse = nullptr;         // [N] log-sum-exp (EPI_DLOGITS)
   const float* colscale = nullptr;    // [N] dlogit scale per token (EPI_DLOGITS)
@@ -66,7 +66,8 @@ struct EpiParams {
 hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t stream,
                     int bm = 0, int bn = 0);
 
-// Tile the heuristic would pick (for reporting).
+// Tile the heuristic picks; nonzero *bm / *bn on entry are kept as
+// constraints (set both to 0 for a free choice).  0 = no tile fits.
 void gemm_pick_tile(int M, int N, int K, int epi, int* bm, int* bn);
 
 }  // namespace ane

@@ -67,24 +67,46 @@ __device__ __forceinline__ void store_tmajor(half_t* tile, const half8 (&v)[8], 
   }
 }
 
+// ---- K-major operand, direct HBM -> LDS (global_load_lds_dwordx4) ----------
+// One wave instruction fills 1 KB of LDS = 8 swizzled rows; lane l lands at
+// slot l (row l/8, physical chunk l%8), so it fetches the logical chunk that
+// the swizzle maps to that slot (the XOR swizzle is its own inverse).
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+template <int R>
+__device__ __forceinline__ void load_direct(half_t* tile, const half_t* base, int ld, int row0, int k0, int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+  for (int it = 0; it < R / 32; it++) {
+    const int gi = wave + 4 * it;
+    const int r = gi * 8 + (lane >> 3);
+    const int lc = swz(r, lane & 7);
+    const half_t* gp = base + (size_t)(row0 + r) * ld + k0 + lc * 8;
+    __builtin_amdgcn_global_load_lds((const void*)gp, (lds_ptr_t)(tile + gi * 8 * BK), 16, 0, 0);
+  }
+}
+
+// Stage<R, transposed>: issue() starts the HBM reads of one k-tile, commit()
+// makes them LDS-resident (register path) -- the direct path has nothing to
+// commit; its completion is awaited by wait_tile() before the barrier.
 template <int R, bool T>
 struct Stage;
 template <int R>
 struct Stage<R, false> {
-  half8 v[R / 32];
-  __device__ __forceinline__ void load(const half_t* b, int ld, int r0, int k0, int tid) {
-    load_kmajor<R>(v, b, ld, r0, k0, tid);
+  __device__ __forceinline__ void issue(const half_t* b, int ld, int r0, int k0, half_t* tile, int tid) {
+    load_direct<R>(tile, b, ld, r0, k0, tid);
   }
-  __device__ __forceinline__ void store(half_t* tile, int tid) const { store_kmajor<R>(tile, v, tid); }
+  __device__ __forceinline__ void commit(half_t*, int) const {}
 };
 template <int R>
 struct Stage<R, true> {
   half8 v[8];
-  __device__ __forceinline__ void load(const half_t* b, int ld, int r0, int k0, int tid) {
+  __device__ __forceinline__ void issue(const half_t* b, int ld, int r0, int k0, half_t*, int tid) {
     load_tmajor<R>(v, b, ld, r0, k0, tid);
   }
-  __device__ __forceinline__ void store(half_t* tile, int tid) const { store_tmajor<R>(tile, v, tid); }
+  __device__ __forceinline__ void commit(half_t* tile, int tid) const { store_tmajor<R>(tile, v, tid); }
 };
+
+__device__ __forceinline__ void wait_tile() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ float softcap_f(float v, float cap) { return cap * tanhf(v / cap); }
 
@@ -122,44 +144,54 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
   Stage<BM, AT> sa;
   Stage<BN, BT> sb;
   const int nk = g.K / BK;
-  sa.load(g.A, g.lda, m0, 0, tid);
-  sb.load(g.B, g.ldb, n0, 0, tid);
-  sa.store(lds, tid);
-  sb.store(lds + BM * BK, tid);
+  sa.issue(g.A, g.lda, m0, 0, lds, tid);
+  sb.issue(g.B, g.ldb, n0, 0, lds + BM * BK, tid);
+  sa.commit(lds, tid);
+  sb.commit(lds + BM * BK, tid);
+  wait_tile();
   __syncthreads();
 
   const int frow = lane & 31, fch = lane >> 5;
+  int arow[TM], brow[TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++) arow[i] = wm * (BM / 2) + i * 32 + frow;
+#pragma unroll
+  for (int j = 0; j < TN; j++) brow[j] = wn * (BN / 2) + j * 32 + frow;
+
   for (int kt = 0; kt < nk; kt++) {
     const half_t* cur = lds + (kt & 1) * STAGE;
+    half_t* nxt = lds + ((kt + 1) & 1) * STAGE;
     if (kt + 1 < nk) {
-      sa.load(g.A, g.lda, m0, (kt + 1) * BK, tid);
-      sb.load(g.B, g.ldb, n0, (kt + 1) * BK, tid);
+      sa.issue(g.A, g.lda, m0, (kt + 1) * BK, nxt, tid);
+      sb.issue(g.B, g.ldb, n0, (kt + 1) * BK, nxt + BM * BK, tid);
     }
+    // fragments double-buffered across the four 16-wide k-substeps
+    half8 a[2][TM], b[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++) a[0][i] = ld_h8(cur + arow[i] * BK + swz(arow[i], fch) * 8);
+#pragma unroll
+    for (int j = 0; j < TN; j++) b[0][j] = ld_h8(cur + BM * BK + brow[j] * BK + swz(brow[j], fch) * 8);
 #pragma unroll
     for (int s = 0; s < BK / 16; s++) {
-      half8 a[TM], b[TN];
-      const int ch = s * 2 + fch;
+      const int c = s & 1;
+      if (s + 1 < BK / 16) {
+        const int ch = (s + 1) * 2 + fch;
 #pragma unroll
-      for (int i = 0; i < TM; i++) {
-        int row = wm * (BM / 2) + i * 32 + frow;
-        a[i] = ld_h8(cur + row * BK + swz(row, ch) * 8);
-      }
+        for (int i = 0; i < TM; i++) a[c ^ 1][i] = ld_h8(cur + arow[i] * BK + swz(arow[i], ch) * 8);
 #pragma unroll
-      for (int j = 0; j < TN; j++) {
-        int row = wn * (BN / 2) + j * 32 + frow;
-        b[j] = ld_h8(cur + BM * BK + row * BK + swz(row, ch) * 8);
+        for (int j = 0; j < TN; j++) b[c ^ 1][j] = ld_h8(cur + BM * BK + brow[j] * BK + swz(brow[j], ch) * 8);
       }
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
     }
     if (kt + 1 < nk) {
-      half_t* nxt = lds + ((kt + 1) & 1) * STAGE;
-      sa.store(nxt, tid);
-      sb.store(nxt + BM * BK, tid);
+      sa.commit(nxt, tid);
+      sb.commit(nxt + BM * BK, tid);
     }
+    wait_tile();
     __syncthreads();
   }
 
@@ -178,17 +210,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
 #pragma unroll
         for (int r = 0; r < 16; r++) C[(size_t)ROW(i, r) * e.ldc + COL(j)] = (half_t)(acc[i][j][r] * e.scale);
   } else if constexpr (EPI == EPI_STORE_F) {
+    // Loads of a tile's 16 old values are issued before any of its stores:
+    // C may alias nothing else, but the compiler cannot know that, and a
+    // load-use-store chain per element would serialise on memory latency.
     float* C = (float*)e.C;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int j = 0; j < TN; j++)
+      for (int j = 0; j < TN; j++) {
+        const size_t base = (size_t)(rbase + i * 32) * e.ldc + COL(j);
+        float old[16];
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          size_t idx = (size_t)ROW(i, r) * e.ldc + COL(j);
-          float v = acc[i][j][r] * e.scale;
-          C[idx] = e.accumulate ? C[idx] + v : v;
-        }
+        for (int r = 0; r < 16; r++)
+          old[r] = e.accumulate ? C[base + (size_t)(8 * (r >> 2) + (r & 3)) * e.ldc] : 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) C[base + (size_t)(8 * (r >> 2) + (r & 3)) * e.ldc] = old[r] + acc[i][j][r] * e.scale;
+      }
   } else if constexpr (EPI == EPI_STORE_W13) {
     // rows are 32-row blocks alternating W1 / W3 (block b even -> W1 row
     // (b/2)*32 + r%32, odd -> W3); C = W1 grad, C3 = W3 grad, both [H, ldc]
@@ -222,18 +259,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
     float* C2 = (float*)e.C2;
     const float alpha = e.alpha_ptr ? *e.alpha_ptr : e.alpha;
     const float beta = e.beta_ptr ? *e.beta_ptr : e.beta;
+    const bool has_x0 = e.X0 != nullptr;
+    // R usually IS C (in-place residual); all 16 reads of a tile precede its
+    // writes, and each element is read and written by the same lane only.
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int j = 0; j < TN; j++)
+      for (int j = 0; j < TN; j++) {
+        const size_t base = (size_t)(rbase + i * 32) * e.ldc + COL(j);
+        float rv[16], xv[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) rv[r] = e.R[base + (size_t)(8 * (r >> 2) + (r & 3)) * e.ldc];
+#pragma unroll
+        for (int r = 0; r < 16; r++) xv[r] = has_x0 ? e.X0[base + (size_t)(8 * (r >> 2) + (r & 3)) * e.ldc] : 0.f;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          size_t idx = (size_t)ROW(i, r) * e.ldc + COL(j);
-          float v = alpha * e.R[idx] + acc[i][j][r];
-          if (e.X0) v += beta * e.X0[idx];
+          const size_t idx = base + (size_t)(8 * (r >> 2) + (r & 3)) * e.ldc;
+          const float v = alpha * rv[r] + acc[i][j][r] + beta * xv[r];
           C[idx] = v;
           if (C2) C2[idx] = v;
         }
+      }
   } else if constexpr (EPI == EPI_SWIGLU) {
     static_assert(TN % 2 == 0, "SwiGLU epilogue pairs 32-column tiles");
     half_t* C = (half_t*)e.C;
@@ -278,26 +324,36 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int j = 0; j < TN; j++)
+      for (int j = 0; j < TN; j++) {
+        float cur[16], prev[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          int t = ROW(i, r);
-          size_t idx = (size_t)t * e.ldc + COL(j);
-          float ga = 1.0f / (1.0f + __expf(-acc[i][j][r]));
-          float v = e.X0[idx];
-          if (t % e.seq != 0) v += alpha * ga * e.X0[idx - e.ldc];
-          C[idx] = v;
+          const int t = ROW(i, r);
+          const size_t idx = (size_t)t * e.ldc + COL(j);
+          cur[r] = e.X0[idx];
+          prev[r] = (t % e.seq != 0) ? e.X0[idx - e.ldc] : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const size_t idx = (size_t)ROW(i, r) * e.ldc + COL(j);
+          const float ga = 1.0f / (1.0f + __expf(-acc[i][j][r]));
+          C[idx] = cur[r] + alpha * ga * prev[r];
           if (C2) C2[idx] = ga;
         }
+      }
   } else if constexpr (EPI == EPI_CE) {
-    // rows = vocab ids, columns = tokens.  Each wave reduces its BM/2 rows
-    // of every column to (max, sum exp(v - max)); lanes l and l^32 hold the
-    // two row halves of one column.
+    // rows = vocab ids (M == vocab), columns = tokens.  Each wave reduces
+    // its BM/2 rows of every column to (max, sum exp(v - max)); lanes l and
+    // l^32 hold the two row halves of one column; the two waves sharing a
+    // column range merge through LDS into one partial per block row.
+    float2* red = reinterpret_cast<float2*>(lds);  // [2][BN], main loop done
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-      const int n = COL(j);
+      const int nl = wn * (BN / 2) + j * 32 + (lane & 31);
+      const int n = n0 + nl;
       const int tg = e.targets[n];
-      float mx = -INFINITY;
+      float mx = -INFINITY, tv = 0.f;
+      bool hit = false;
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -305,18 +361,33 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
           float v = acc[i][j][r];
           if (e.softcap) v = softcap_f(v, e.cap);
           acc[i][j][r] = v;
-          if (ROW(i, r) < e.vocab) mx = fmaxf(mx, v);
-          if (ROW(i, r) == tg) e.tgt_logit[n] = v;
+          mx = fmaxf(mx, v);
+          const bool h = ROW(i, r) == tg;
+          tv = h ? v : tv;
+          hit = hit || h;
         }
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int r = 0; r < 16; r++)
-          if (ROW(i, r) < e.vocab) s += __expf(acc[i][j][r] - mx);
+        for (int r = 0; r < 16; r++) s += __expf(acc[i][j][r] - mx);
       s += __shfl_xor(s, 32, 64);
-      if (lane < 32) e.partial[(size_t)(bm * 2 + wm) * g.N + n] = make_float2(mx, s);
+      if (hit) e.tgt_logit[n] = tv;  // exactly one lane of the grid holds (tg, n)
+      if (lane < 32) red[wm * BN + nl] = make_float2(mx, s);
+    }
+    __syncthreads();
+    if (wm == 0) {
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int nl = wn * (BN / 2) + j * 32 + (lane & 31);
+        if (lane < 32) {
+          const float2 p0 = red[nl], p1 = red[BN + nl];
+          const float M = fmaxf(p0.x, p1.x);
+          e.partial[(size_t)bm * g.N + n0 + nl] =
+              make_float2(M, p0.y * __expf(p0.x - M) + p1.y * __expf(p1.x - M));
+        }
+      }
     }
   } else if constexpr (EPI == EPI_DLOGITS) {
     // d = (softmax - onehot) * colscale[n], times (1 - tanh^2) under softcap
@@ -368,6 +439,7 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
   if constexpr (EPI != EPI_SWIGLU) {
     switch (key) {
       case 128064: return launch_tile<AT, BT, EPI, 128, 64>(g, e, s);
+      case 256064: return launch_tile<AT, BT, EPI, 256, 64>(g, e, s);
       case 64064: return launch_tile<AT, BT, EPI, 64, 64>(g, e, s);
       default: break;
     }
@@ -378,32 +450,49 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
 }  // namespace
 
 void gemm_pick_tile(int M, int N, int K, int epi, int* pbm, int* pbn) {
-  // Candidate tiles with a relative per-FLOP efficiency (bigger wave tiles
-  // reuse each LDS fragment more).  Score = waves of blocks over the 256
-  // CUs times the cost of one block.
-  static const int cand[][2] = {{256, 256}, {256, 128}, {128, 256}, {128, 128}, {64, 128}, {128, 64}, {64, 64}};
-  static const float eff[] = {1.0f, 0.92f, 0.92f, 0.80f, 0.62f, 0.62f, 0.45f};
-  const int ncu = 256;
-  float best = 1e30f;
-  int bbm = 0, bbn = 0;
-  for (int c = 0; c < 7; c++) {
-    int bm = cand[c][0], bn = cand[c][1];
+  // Preference order with a minimum block count each: a tile is taken only
+  // if it yields enough blocks to keep the 256 CUs (and 2-3 resident blocks
+  // per CU for the smaller tiles) busy.  Thresholds come from a sweep of
+  // the stories110M shapes on MI355X (M = 8192 tokens): 128x128 wins at
+  // N >= 2048, 128x64 at N = 768 with K <= 2048, 64x64 for narrow outputs
+  // with long K.  A nonzero *pbm / *pbn on entry is a constraint the chosen
+  // tile keeps (callers size buffers by it).
+  static const int cand[][3] = {{256, 256, 4096}, {128, 128, 1024}, {128, 64, 600}, {64, 128, 600},
+                                {256, 128, 600},  {128, 256, 600},  {256, 64, 600}, {64, 64, 0}};
+  constexpr int NCAND = 8;
+  const int want_bm = *pbm, want_bn = *pbn;
+  int fbm = 0, fbn = 0;
+  for (int c = 0; c < NCAND; c++) {
+    const int bm = cand[c][0], bn = cand[c][1];
+    if ((want_bm && bm != want_bm) || (want_bn && bn != want_bn)) continue;
     if (M % bm || N % bn) continue;
     if (epi == EPI_SWIGLU && bn < 128) continue;
-    long blocks = (long)(M / bm) * (N / bn);
-    long rounds = (blocks + ncu - 1) / ncu;
-    float cost = (float)rounds * (float)bm * (float)bn / eff[c];
-    if (cost < best * 0.999f) { best = cost; bbm = bm; bbn = bn; }
+    const long blocks = (long)(M / bm) * (N / bn);
+    if (!fbm) { fbm = bm; fbn = bn; }  // first that fits, if none is big enough
+    if (blocks >= cand[c][2]) {
+      *pbm = bm;
+      *pbn = bn;
+      return;
+    }
   }
-  *pbm = bbm;
-  *pbn = bbn;
+  // nothing reaches its threshold: the smallest-tile choice that fits
+  for (int c = NCAND - 1; c >= 0; c--) {
+    const int bm = cand[c][0], bn = cand[c][1];
+    if ((want_bm && bm != want_bm) || (want_bn && bn != want_bn)) continue;
+    if (M % bm || N % bn || (epi == EPI_SWIGLU && bn < 128)) continue;
+    fbm = bm;
+    fbn = bn;
+    break;
+  }
+  *pbm = fbm;
+  *pbn = fbn;
   (void)K;
 }
 
 hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t s, int bm, int bn) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0) return hipErrorInvalidValue;
   if (bm == 0 || bn == 0) gemm_pick_tile(g.M, g.N, g.K, epi, &bm, &bn);
-  if (bm == 0 || (g.M % bm) || (g.N % bn)) return hipErrorInvalidValue;
+  if (bm == 0 || bn == 0 || (g.M % bm) || (g.N % bn)) return hipErrorInvalidValue;
   const int lay = (g.a_t ? 2 : 0) | (g.b_t ? 1 : 0);
 #define CASE(L, AT, BT, E) \
   if (lay == L && epi == E) return launch<AT, BT, E>(g, e, s, bm, bn);

@@ -28,8 +28,10 @@ hipError_t gather_windows(uint16_t* tok, uint16_t* tgt, const uint16_t* data, co
 // log-sum-exp and the per-sequence mean cross-entropy over valid targets
 // (stories.CrossEntropyLoss, ane/stories/cpu.go:212-292).  colscale (optional)
 // receives dscale / valid_b for valid tokens and 0 otherwise.
-hipError_t ce_reduce(float* loss_seq, float* lse, float* colscale, float dscale, const float2* partial, int np,
-                     const float* tgt_logit, const uint16_t* tgt, int V, int nseq, int S, hipStream_t s);
+// lse and tok_loss ([T] each) are required scratch/outputs.
+hipError_t ce_reduce(float* loss_seq, float* lse, float* tok_loss, float* colscale, float dscale,
+                     const float2* partial, int np, const float* tgt_logit, const uint16_t* tgt, int V, int nseq, int S,
+                     hipStream_t s);
 
 hipError_t f32_to_f16(half_t* dst, const float* src, size_t n, hipStream_t s);
 // dst [2H, D] with 32-row blocks alternating W1 / W3 rows

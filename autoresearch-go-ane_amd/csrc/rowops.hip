@@ -47,23 +47,43 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(half_t* out, const float* 
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (t >= T) return;
   const float lam = xsub ? *lamp : 0.f;
-  const float* xr = x + (size_t)t * D;
-  const float* sr = xsub ? xsub + (size_t)t * D : nullptr;
+  // D is a multiple of 64: each lane owns float4 groups i = 4*lane + 256*k,
+  // held in registers between the reduction and the store (D <= 1024).
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * D);
+  const float4* sr = xsub ? reinterpret_cast<const float4*>(xsub + (size_t)t * D) : nullptr;
+  const int nv = D / 4;
+  float4 v[4];
   float ss = 0.f;
-  for (int i = lane; i < D; i += 64) {
-    float v = xr[i];
-    if (sr) v -= lam * sr[i];
-    ss += v * v;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int i = lane + 64 * k;
+    if (i < nv) {
+      float4 a = xr[i];
+      if (sr) {
+        const float4 b = sr[i];
+        a.x -= lam * b.x; a.y -= lam * b.y; a.z -= lam * b.z; a.w -= lam * b.w;
+      }
+      v[k] = a;
+      ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
   }
   ss = wave_sum(ss);
   const float sc = 1.0f / sqrtf(ss / (float)D + 1e-5f);
-  half_t* orow = out + (size_t)t * D;
-  for (int i = lane; i < D; i += 64) {
-    float v = xr[i];
-    if (sr) v -= lam * sr[i];
-    v *= sc;
-    if (gain) v *= gain[i];
-    orow[i] = (half_t)v;
+  half4* orow = reinterpret_cast<half4*>(out + (size_t)t * D);
+  const float4* g4 = reinterpret_cast<const float4*>(gain);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int i = lane + 64 * k;
+    if (i < nv) {
+      float4 a = v[k];
+      float4 gg = gain ? g4[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+      half4 h;
+      h[0] = (half_t)(a.x * sc * gg.x);
+      h[1] = (half_t)(a.y * sc * gg.y);
+      h[2] = (half_t)(a.z * sc * gg.z);
+      h[3] = (half_t)(a.w * sc * gg.w);
+      orow[i] = h;
+    }
   }
 }
 
@@ -77,10 +97,43 @@ __global__ void gather_kernel(uint16_t* tok, uint16_t* tgt, const uint16_t* data
   tgt[i] = data[p + 1];
 }
 
-__global__ __launch_bounds__(256) void ce_reduce_kernel(float* loss_seq, float* lse_out, float* colscale,
-                                                        float dscale, const float2* partial, int np,
-                                                        const float* tgt_logit, const uint16_t* tgt, int V, int S,
-                                                        int T) {
+// Per token: merge the partials with a running (max, sum) pair; 4 lanes
+// split the partials of one token and combine with two xor-shuffles.
+__global__ __launch_bounds__(256) void ce_token_kernel(float* lse_out, float* tok_loss, const float2* partial,
+                                                       int np, const float* tgt_logit, const uint16_t* tgt, int V,
+                                                       int T) {
+  const int n = blockIdx.x * 64 + (threadIdx.x >> 2), q = threadIdx.x & 3;
+  float mx = -INFINITY, sum = 0.f;
+  if (n < T) {
+    for (int p = q; p < np; p += 4) {
+      const float2 v = partial[(size_t)p * T + n];
+      const float m2 = fmaxf(mx, v.x);
+      sum = sum * __expf(mx - m2) + v.y * __expf(v.x - m2);
+      mx = m2;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 4; o <<= 1) {
+    const float om = __shfl_xor(mx, o, 64), os = __shfl_xor(sum, o, 64);
+    const float m2 = fmaxf(mx, om);
+    sum = (mx == -INFINITY ? 0.f : sum * __expf(mx - m2)) + (om == -INFINITY ? 0.f : os * __expf(om - m2));
+    mx = m2;
+  }
+  if (n < T && q == 0) {
+    const float lse = mx + __logf(sum);
+    lse_out[n] = lse;
+    float l = 0.f;
+    if (tgt[n] < V) {
+      const float logp = tgt_logit[n] - lse;
+      const float floor_ = -23.025850929940457f;  // log(1e-10): p clamped at 1e-10
+      l = -(logp > floor_ ? logp : floor_);
+    }
+    tok_loss[n] = l;
+  }
+}
+
+__global__ __launch_bounds__(256) void ce_reduce_kernel(float* loss_seq, float* colscale, float dscale,
+                                                        const float* tok_loss, const uint16_t* tgt, int V, int S) {
   const int b = blockIdx.x;
   __shared__ float red_l[256];
   __shared__ int red_v[256];
@@ -88,19 +141,8 @@ __global__ __launch_bounds__(256) void ce_reduce_kernel(float* loss_seq, float* 
   int nvalid = 0;
   for (int t = threadIdx.x; t < S; t += blockDim.x) {
     const int n = b * S + t;
-    float mx = -INFINITY;
-    for (int p = 0; p < np; p++) mx = fmaxf(mx, partial[(size_t)p * T + n].x);
-    float sum = 0.f;
-    for (int p = 0; p < np; p++) {
-      float2 v = partial[(size_t)p * T + n];
-      sum += v.y * __expf(v.x - mx);
-    }
-    const float lse = mx + __logf(sum);
-    if (lse_out) lse_out[n] = lse;
     if (tgt[n] < V) {
-      const float logp = tgt_logit[n] - lse;
-      const float floor_ = -23.025850929940457f;  // log(1e-10)
-      lsum += -(logp > floor_ ? logp : floor_);
+      lsum += tok_loss[n];
       nvalid++;
     }
   }
@@ -175,10 +217,13 @@ hipError_t gather_windows(uint16_t* tok, uint16_t* tgt, const uint16_t* data, co
   return hipGetLastError();
 }
 
-hipError_t ce_reduce(float* loss_seq, float* lse, float* colscale, float dscale, const float2* partial, int np,
-                     const float* tgt_logit, const uint16_t* tgt, int V, int nseq, int S, hipStream_t s) {
-  hipLaunchKernelGGL(ce_reduce_kernel, dim3(nseq), dim3(256), 0, s, loss_seq, lse, colscale, dscale, partial, np,
-                     tgt_logit, tgt, V, S, nseq * S);
+hipError_t ce_reduce(float* loss_seq, float* lse, float* tok_loss, float* colscale, float dscale,
+                     const float2* partial, int np, const float* tgt_logit, const uint16_t* tgt, int V, int nseq, int S,
+                     hipStream_t s) {
+  const int T = nseq * S;
+  hipLaunchKernelGGL(ce_token_kernel, dim3((T + 63) / 64), dim3(256), 0, s, lse, tok_loss, partial, np, tgt_logit,
+                     tgt, V, T);
+  hipLaunchKernelGGL(ce_reduce_kernel, dim3(nseq), dim3(256), 0, s, loss_seq, colscale, dscale, tok_loss, tgt, V, S);
   return hipGetLastError();
 }
 

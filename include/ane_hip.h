@@ -175,6 +175,9 @@ int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_
                    void *C, int bm, int bn);
 int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, const uint16_t *qkv, uint16_t *out,
                         float *lse);
+/* Mean time of `iters` launches of one GEMM on device-resident operands. */
+int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int iters,
+                         float *avg_ms);
 const char *ane_debug_last_error(void);
 
 #ifdef __cplusplus

@@ -34,7 +34,7 @@ def run_gemm(A, B, a_t, b_t, bm=0, bn=0, out_f16=False):
     return out
 
 
-TILES = [(256, 256), (256, 128), (128, 256), (128, 128), (64, 128), (128, 64), (64, 64)]
+TILES = [(256, 256), (256, 128), (128, 256), (128, 128), (64, 128), (128, 64), (256, 64), (64, 64)]
 
 
 @pytest.mark.parametrize("a_t,b_t", [(False, False), (False, True), (True, True)])
