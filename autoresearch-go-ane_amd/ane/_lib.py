@@ -74,12 +74,23 @@ SIGNATURES = {
     "ane_eval_logits": (C.c_int, [_eng, _u16, C.c_int64, _fp]),
     "ane_eval_loss": (C.c_int, [_eng, _u16, _u16, C.c_int32, _fp, _fp]),
     "ane_eval_loss_windows": (C.c_int, [_eng, _u64, C.c_int32, _fp, _fp]),
+    "ane_step": (C.c_int, [_eng, C.POINTER(StepResult)]),
+    "ane_train_batch": (C.c_int, [_eng, C.c_int32, C.POINTER(StepResult)]),
+    "ane_flush": (C.c_int, [_eng, C.POINTER(C.c_int64)]),
+    "ane_lr": (C.c_float, [_eng]),
+    "ane_set_lr": (C.c_int, [_eng, C.c_float]),
+    "ane_get_state": (C.c_int, [_eng, C.POINTER(State)]),
+    "ane_load_state": (C.c_int, [_eng, C.POINTER(State)]),
+    "ane_grads": (C.c_int, [_eng, _u16, _u16, C.c_int32, _fp, _fp]),
+    "ane_set_grads": (C.c_int, [_eng, _fp, C.c_int64, C.c_uint32]),
+    "ane_get_opt_state": (C.c_int, [_eng, _fp, _fp, C.c_int64]),
     "ane_profile_enable": (C.c_int, [_eng, C.c_int]),
     "ane_profile_read": (C.c_int, [_eng, C.POINTER(ProfEntry), C.c_int, C.c_int]),
     "ane_sync": (C.c_int, [_eng]),
     "ane_debug_gemm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _u16, _u16, C.c_void_p,
                                  C.c_int, C.c_int]),
-    "ane_debug_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, _u16, _u16, _fp]),
+    "ane_debug_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, C.c_float, C.c_int, _u16,
+                                      _u16, _fp]),
     "ane_debug_last_error": (C.c_char_p, []),
     "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 9 + [_fp]),
 }

@@ -165,6 +165,60 @@ class Engine:
             self._h, pos.ctypes.data_as(C.POINTER(C.c_uint64)), pos.size, _f32(per), C.byref(mean)))
         return float(mean.value), per
 
+    # -- training --------------------------------------------------------
+    def Step(self) -> "_lib.StepResult":
+        """ane/engine.go:381-442: one drand48-sampled window, AdamW every AccumSteps."""
+        r = _lib.StepResult()
+        _check(self._lib, self._h, self._lib.ane_step(self._h, C.byref(r)))
+        return r
+
+    def TrainBatch(self, nseq: int) -> "_lib.StepResult":
+        """nseq consecutive Steps fused into one batched forward/backward."""
+        r = _lib.StepResult()
+        _check(self._lib, self._h, self._lib.ane_train_batch(self._h, int(nseq), C.byref(r)))
+        return r
+
+    def Flush(self) -> int:
+        """ane/engine.go:484-496; returns nanoseconds."""
+        ns = C.c_int64()
+        _check(self._lib, self._h, self._lib.ane_flush(self._h, C.byref(ns)))
+        return int(ns.value)
+
+    def LR(self) -> float:
+        return float(self._lib.ane_lr(self._h)) if self._h else 0.0
+
+    def SetLR(self, lr: float):
+        _check(self._lib, self._h, self._lib.ane_set_lr(self._h, float(lr)))
+
+    def State(self) -> "_lib.State":
+        s = _lib.State()
+        self._lib.ane_get_state(self._h, C.byref(s))
+        return s
+
+    def LoadState(self, s: "_lib.State"):
+        _check(self._lib, self._h, self._lib.ane_load_state(self._h, C.byref(s)))
+
+    def Grads(self, tokens, targets):
+        """Gradient of the mean loss over explicit sequences (flushed scale)."""
+        tok = np.ascontiguousarray(tokens, dtype=np.uint16).reshape(-1, self.cfg.seq)
+        tgt = np.ascontiguousarray(targets, dtype=np.uint16).reshape(-1, self.cfg.seq)
+        g = np.zeros(param_count(self.cfg), np.float32)
+        mean = C.c_float()
+        _check(self._lib, self._h, self._lib.ane_grads(self._h, _u16(tok), _u16(tgt), tok.shape[0], _f32(g),
+                                                       C.byref(mean)))
+        return float(mean.value), g
+
+    def SetGrads(self, grads: np.ndarray, pending: int):
+        g = np.ascontiguousarray(grads, dtype=np.float32).reshape(-1)
+        _check(self._lib, self._h, self._lib.ane_set_grads(self._h, _f32(g), g.size, int(pending)))
+
+    def OptState(self):
+        n = param_count(self.cfg)
+        m = np.zeros(n, np.float32)
+        v = np.zeros(n, np.float32)
+        _check(self._lib, self._h, self._lib.ane_get_opt_state(self._h, _f32(m), _f32(v), n))
+        return m, v
+
     # -- diagnostics -----------------------------------------------------
     def ProfileEnable(self, on: bool = True):
         _check(self._lib, self._h, self._lib.ane_profile_enable(self._h, 1 if on else 0))

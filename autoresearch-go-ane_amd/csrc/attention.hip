@@ -23,9 +23,14 @@ namespace {
 
 constexpr int HD = 64;
 
-template <int SMAX>
+// HILO: scores from split operands q = q_hi + q_lo, k = k_hi + k_lo (each
+// fp16), s = q_hi.k_hi + q_lo.k_hi + q_hi.k_lo, i.e. ~fp32 accuracy.  Used
+// where the scores are large enough for fp16 rounding of q and k to matter
+// (the reference's scale-1 recompute, ane/train_full.go:268-269).
+template <int SMAX, bool HILO>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) half_t Ks[SMAX * HD];
+  __shared__ __attribute__((aligned(16))) half_t Ks_lo[HILO ? SMAX * HD : 8];
   constexpr int VST = SMAX + 4;  // V^T row stride (halves): 2-way-free b64 reads
   __shared__ __attribute__((aligned(16))) half_t Vt[HD * VST];
 
@@ -59,10 +64,16 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int p = 0; p < 8; p++) f[p] *= sc;
     }
-    half8 w;
+    half8 w, wl;
 #pragma unroll
-    for (int p = 0; p < 8; p++) w[p] = (half_t)f[p];
+    for (int p = 0; p < 8; p++) {
+      w[p] = (half_t)f[p];
+      wl[p] = (half_t)(f[p] - (float)w[p]);
+    }
     st_h8(Ks + j * HD + swz(j, ch) * 8, w);
+    if constexpr (HILO) st_h8(Ks_lo + j * HD + swz(j, ch) * 8, wl);
+    if (a.qkvt && blockIdx.x == 0) st_h8(a.qkvt + (tok0 + j) * D3 + D + h * HD + ch * 8, w);
+    if (a.qkvt_lo && blockIdx.x == 0) st_h8(a.qkvt_lo + (tok0 + j) * 2 * D + D + h * HD + ch * 8, wl);
   }
 
   // ---- stage V^T (8 keys x 8 dims per thread), value embeddings added --------
@@ -101,6 +112,15 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       half_t* dst = Vt + (dc * 8 + i) * VST + kc * 8;
       *reinterpret_cast<half4*>(dst) = lo;
       *reinterpret_cast<half4*>(dst + 4) = hi;
+    }
+    if (a.qkvt && blockIdx.x == 0) {
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++) {
+        half8 w;
+#pragma unroll
+        for (int i = 0; i < 8; i++) w[i] = (half_t)v[jj][i];
+        st_h8(a.qkvt + (tok0 + kc * 8 + jj) * D3 + 2 * D + h * HD + dc * 8, w);
+      }
     }
   }
   __syncthreads();
@@ -146,11 +166,22 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
         for (int p = 0; p < 8; p++) qf[s][p] *= sc;
     }
-    half8 qfrag[4];
+    half8 qfrag[4], qlo[4];
 #pragma unroll
     for (int s = 0; s < 4; s++)
 #pragma unroll
-      for (int p = 0; p < 8; p++) qfrag[s][p] = (half_t)qf[s][p];
+      for (int p = 0; p < 8; p++) {
+        qfrag[s][p] = (half_t)qf[s][p];
+        qlo[s][p] = (half_t)(qf[s][p] - (float)qfrag[s][p]);
+      }
+    if (a.qkvt) {
+#pragma unroll
+      for (int s = 0; s < 4; s++) st_h8(a.qkvt + (tok0 + q) * D3 + h * HD + s * 16 + g * 8, qfrag[s]);
+    }
+    if (a.qkvt_lo) {
+#pragma unroll
+      for (int s = 0; s < 4; s++) st_h8(a.qkvt_lo + (tok0 + q) * 2 * D + h * HD + s * 16 + g * 8, qlo[s]);
+    }
 
     floatx16 o0, o1;
 #pragma unroll
@@ -164,8 +195,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       const int krow = kb * 32 + ql;
 #pragma unroll
       for (int s = 0; s < 4; s++) {
-        half8 kf = ld_h8(Ks + krow * HD + swz(krow, s * 2 + g) * 8);
+        const int off = krow * HD + swz(krow, s * 2 + g) * 8;
+        half8 kf = ld_h8(Ks + off);
         sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qfrag[s], sacc, 0, 0, 0);
+        if constexpr (HILO) {
+          sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ld_h8(Ks_lo + off), qfrag[s], sacc, 0, 0, 0);
+          sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qlo[s], sacc, 0, 0, 0);
+        }
       }
       // sacc[r]: key kb*32 + 8*(r/4) + 4g + r%4, query q (scores * log2 e)
       float mloc = -INFINITY;
@@ -237,10 +273,13 @@ hipError_t attention_fwd(const AttnArgs& a, hipStream_t stream) {
   const int npairs = a.S / 64;
   const int nw = npairs < 4 ? npairs : 4;
   dim3 grid((npairs + nw - 1) / nw, a.NH, a.nseq);
-  if (a.S <= 256)
-    hipLaunchKernelGGL(attn_fwd_kernel<256>, grid, dim3(64 * nw), 0, stream, a);
+  if (a.hilo && a.S > 256) return hipErrorInvalidValue;
+  if (a.hilo)
+    hipLaunchKernelGGL((attn_fwd_kernel<256, true>), grid, dim3(64 * nw), 0, stream, a);
+  else if (a.S <= 256)
+    hipLaunchKernelGGL((attn_fwd_kernel<256, false>), grid, dim3(64 * nw), 0, stream, a);
   else
-    hipLaunchKernelGGL(attn_fwd_kernel<512>, grid, dim3(64 * nw), 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<512, false>), grid, dim3(64 * nw), 0, stream, a);
   return hipGetLastError();
 }
 

@@ -11,6 +11,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <time.h>
 
 #include <string>
 #include <vector>
@@ -20,6 +21,7 @@
 #include "engine_internal.h"
 #include "gemm.h"
 #include "rowops.h"
+#include "train_ops.h"
 
 using namespace ane;
 
@@ -114,18 +116,6 @@ int eng_fail(ane_engine* e, int code, const char* fmt, ...) {
   return code;
 }
 
-#define HIPCHK(op, expr)                                                                             \
-  do {                                                                                               \
-    hipError_t _h = (expr);                                                                          \
-    if (_h != hipSuccess) return eng_fail(e, ANE_ERR_HIP, "storiesane %s: %s: %s", op, #expr,        \
-                                          hipGetErrorString(_h));                                    \
-  } while (0)
-
-#define CLOSED_CHECK(op) \
-  do { \
-    if (!e) return ANE_ERR_CLOSED; \
-    if (e->closed) return eng_fail(e, ANE_ERR_CLOSED, "storiesane %s: engine is closed", op); \
-  } while (0)
 
 // ---------------------------------------------------------------------------
 // profiling (HIP events bracketing tracked launches)
@@ -164,17 +154,6 @@ hipError_t eng_gemm(ane_engine* e, int cls, const half_t* A, int lda, bool at, c
 // ---------------------------------------------------------------------------
 // allocation
 // ---------------------------------------------------------------------------
-template <class T>
-static hipError_t dalloc(ane_engine* e, T** p, size_t n) {
-  void* q = nullptr;
-  hipError_t r = hipMalloc(&q, n * sizeof(T) > 0 ? n * sizeof(T) : 16);
-  if (r == hipSuccess) {
-    e->allocs.push_back(q);
-    *p = (T*)q;
-  }
-  return r;
-}
-
 static void free_all(ane_engine* e) {
   if (e->dev_set) (void)hipSetDevice(e->device);
   if (e->stream) (void)hipStreamSynchronize(e->stream);
@@ -185,6 +164,13 @@ static void free_all(ane_engine* e) {
     (void)hipEventDestroy(pe.b);
   }
   e->prof_events.clear();
+  for (hipEvent_t& ev : e->step_ev)
+    if (ev) {
+      (void)hipEventDestroy(ev);
+      ev = nullptr;
+    }
+  e->train_ready = false;
+  e->tr = TrainBufs();
   if (e->stream) (void)hipStreamDestroy(e->stream);
   e->stream = nullptr;
 }
@@ -336,6 +322,9 @@ extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_e
     e->closed = true;
   } else {
     e->rng = drand48_seed(e->opt.seed);
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    e->start_s = (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
   }
   *out = e;
   return rc;
@@ -432,7 +421,10 @@ extern "C" int ane_set_tokens(ane_engine* e, const uint16_t* tokens, int64_t n) 
 // forwardTrainingCPU (ane/train_full.go:383-453) and evalLogitsCPUInto
 // (ane/engine.go:954-1038) for nanochat; llama2 uses gain RMSNorm, SwiGLU,
 // plain residuals and no QK-norm / VE / smear / backout.
-int forward_body(ane_engine* e, int nseq) {
+// In training mode (train != 0, buffers of ensure_train) every layer keeps
+// its activations: the residual GEMMs write out-of-place into the next
+// layer's input buffer, so nothing is copied.
+int forward_body(ane_engine* e, int nseq, int train) {
   const char* op = "forward";
   const ane_model_cfg& c = e->cfg;
   const int D = c.dim, H = c.hidden, V = c.vocab, S = c.seq, NH = c.heads, L = c.layers;
@@ -440,41 +432,52 @@ int forward_body(ane_engine* e, int nseq) {
   const bool llama = c.arch == ANE_ARCH_LLAMA2;
   const float* P = e->P;
   hipStream_t st = e->stream;
+  TrainBufs& tb = e->tr;
 
+  float* x_first = train ? tb.L[0].xin : e->x;
   if (llama) {
     prof_begin(e, 7);
-    HIPCHK(op, embed_lookup(e->x, P + e->pm.embed, e->tok, T, D, V, st));
+    HIPCHK(op, embed_lookup(x_first, P + e->pm.embed, e->tok, T, D, V, st));
     prof_end(e, 0, (double)T * D * 8);
   } else {
+    half_t* x0h = train ? tb.x0h : e->xh;
     prof_begin(e, 7);
-    HIPCHK(op, embed_norm(e->xpre, e->x0, e->xh, P + e->pm.embed, e->tok, T, D, V, st));
+    HIPCHK(op, embed_norm(e->xpre, e->x0, x0h, P + e->pm.embed, e->tok, T, D, V, st));
     prof_end(e, 0, (double)T * D * 14);
     // smear (ane/common.go:324-339): x = x0 + lambda * sigmoid(SmearGate x0)[t] * x0[t-1]
     EpiParams p;
-    p.C = e->x; p.ldc = D; p.X0 = e->x0; p.alpha_ptr = P + e->pm.smear_lambda; p.seq = S;
-    HIPCHK(op, eng_gemm(e, 7, e->xh, D, false, e->smear_h, D, false, T, D, D, EPI_SMEAR, p));
+    p.C = x_first; p.ldc = D; p.X0 = e->x0; p.alpha_ptr = P + e->pm.smear_lambda; p.seq = S;
+    if (train) p.C2 = tb.sg_act;
+    HIPCHK(op, eng_gemm(e, 7, x0h, D, false, e->smear_h, D, false, T, D, D, EPI_SMEAR, p));
   }
   for (int l = 0; l < L; l++) {
     const LayerOff& o = e->pm.L[l];
     const LayerShadow& s = e->ls[l];
+    LayerActs A;
+    if (train) {
+      A = tb.L[l];
+    } else {
+      A.xin = e->x; A.x2 = e->x; A.xn = e->xh; A.xn2 = e->xh; A.qkv = e->qkv; A.att = e->att; A.gate = e->gate;
+    }
+    float* xout = train ? (l + 1 < L ? tb.L[l + 1].xin : tb.xlast) : e->x;
     prof_begin(e, 6);
-    HIPCHK(op, rmsnorm_f16(e->xh, e->x, nullptr, nullptr, llama ? P + o.g_att : nullptr, T, D, st));
+    HIPCHK(op, rmsnorm_f16(A.xn, A.xin, nullptr, nullptr, llama ? P + o.g_att : nullptr, T, D, st));
     prof_end(e, 0, (double)T * D * 6);
     {
       EpiParams p;
-      p.C = e->qkv; p.ldc = 3 * D;
-      HIPCHK(op, eng_gemm(e, 0, e->xh, D, false, s.wqkv, D, false, T, 3 * D, D, EPI_STORE_H, p));
+      p.C = A.qkv; p.ldc = 3 * D;
+      HIPCHK(op, eng_gemm(e, 0, A.xn, D, false, s.wqkv, D, false, T, 3 * D, D, EPI_STORE_H, p));
     }
     {
       AttnArgs a;
       memset(&a, 0, sizeof a);
-      a.qkv = e->qkv; a.out = e->att; a.lse = nullptr;
+      a.qkv = A.qkv; a.out = A.att; a.lse = A.lse; a.qkvt = A.qkvt; a.qkvt_lo = A.qk_lo;
       a.rope_cos = e->rope_cos; a.rope_sin = e->rope_sin;
       a.nseq = nseq; a.S = S; a.NH = NH;
       a.qknorm = llama ? 0 : 1;
       a.scale = 0.125f;
       if (o.ve_embed >= 0) {
-        a.ve_x = e->x; a.ve_gate = P + o.ve_gate; a.ve_embed = P + o.ve_embed; a.tokens = e->tok; a.vocab = V;
+        a.ve_x = A.xin; a.ve_gate = P + o.ve_gate; a.ve_embed = P + o.ve_embed; a.tokens = e->tok; a.vocab = V;
       }
       prof_begin(e, 5);
       HIPCHK(op, attention_fwd(a, st));
@@ -483,37 +486,44 @@ int forward_body(ane_engine* e, int nseq) {
     }
     {
       EpiParams p;
-      p.C = e->x; p.ldc = D; p.R = e->x;
+      p.C = A.x2; p.ldc = D; p.R = A.xin;
       if (!llama) { p.alpha_ptr = P + e->pm.resid + l; p.X0 = e->x0; p.beta_ptr = P + e->pm.x0l + l; }
-      HIPCHK(op, eng_gemm(e, 1, e->att, D, false, s.wo, D, false, T, D, D, EPI_RESID, p));
+      HIPCHK(op, eng_gemm(e, 1, A.att, D, false, s.wo, D, false, T, D, D, EPI_RESID, p));
     }
     prof_begin(e, 6);
-    HIPCHK(op, rmsnorm_f16(e->xh, e->x, nullptr, nullptr, llama ? P + o.g_ffn : nullptr, T, D, st));
+    HIPCHK(op, rmsnorm_f16(A.xn2, A.x2, nullptr, nullptr, llama ? P + o.g_ffn : nullptr, T, D, st));
     prof_end(e, 0, (double)T * D * 6);
     {
       EpiParams p;
-      p.C = e->gate; p.ldc = H;
+      p.C = A.gate; p.ldc = H;
+      p.C2 = A.h13; p.ldc2 = llama ? 2 * H : H;
       if (llama)
-        HIPCHK(op, eng_gemm(e, 2, e->xh, D, false, s.w13, D, false, T, 2 * H, D, EPI_SWIGLU, p));
+        HIPCHK(op, eng_gemm(e, 2, A.xn2, D, false, s.w13, D, false, T, 2 * H, D, EPI_SWIGLU, p));
       else
-        HIPCHK(op, eng_gemm(e, 2, e->xh, D, false, s.w13, D, false, T, H, D, EPI_RELU2, p));
+        HIPCHK(op, eng_gemm(e, 2, A.xn2, D, false, s.w13, D, false, T, H, D, EPI_RELU2, p));
     }
     {
       EpiParams p;
-      p.C = e->x; p.ldc = D; p.R = e->x;
+      p.C = xout; p.ldc = D; p.R = A.x2;
       if (!llama) {
         p.alpha_ptr = P + e->pm.resid + l; p.X0 = e->x0; p.beta_ptr = P + e->pm.x0l + l;
         if (l == L / 2 - 1) p.C2 = e->xmid;  // backout snapshot (ane/train_full.go:447-449)
       }
-      HIPCHK(op, eng_gemm(e, 3, e->gate, H, false, s.w2, H, false, T, D, H, EPI_RESID, p));
+      HIPCHK(op, eng_gemm(e, 3, A.gate, H, false, s.w2, H, false, T, D, H, EPI_RESID, p));
     }
   }
   // final norm (backout first for nanochat, ane/common.go:385-389)
+  float* xl = train ? tb.xlast : e->x;
   prof_begin(e, 6);
-  if (llama)
-    HIPCHK(op, rmsnorm_f16(e->xh, e->x, nullptr, nullptr, P + e->pm.g_final, T, D, st));
-  else
-    HIPCHK(op, rmsnorm_f16(e->xh, e->x, e->xmid, P + e->pm.backout_lambda, nullptr, T, D, st));
+  if (llama) {
+    HIPCHK(op, rmsnorm_f16(e->xh, xl, nullptr, nullptr, P + e->pm.g_final, T, D, st));
+  } else if (train) {
+    // keep the post-backout state for the final norm's backward
+    HIPCHK(op, backout_fwd(tb.xfinal, xl, e->xmid, P + e->pm.backout_lambda, (size_t)T * D, st));
+    HIPCHK(op, rmsnorm_f16(e->xh, tb.xfinal, nullptr, nullptr, nullptr, T, D, st));
+  } else {
+    HIPCHK(op, rmsnorm_f16(e->xh, xl, e->xmid, P + e->pm.backout_lambda, nullptr, T, D, st));
+  }
   prof_end(e, 0, (double)T * D * (llama ? 6 : 10));
   return ANE_OK;
 }
@@ -557,7 +567,7 @@ extern "C" int ane_eval_loss(ane_engine* e, const uint16_t* tokens, const uint16
   const size_t T = (size_t)nseq * e->cfg.seq;
   HIPCHK("eval loss", hipMemcpyAsync(e->tok, tokens, T * 2, hipMemcpyHostToDevice, e->stream));
   HIPCHK("eval loss", hipMemcpyAsync(e->tgt, targets, T * 2, hipMemcpyHostToDevice, e->stream));
-  int rc = forward_body(e, nseq);
+  int rc = forward_body(e, nseq, 0);
   if (!rc) rc = head_loss(e, nseq, nullptr, 0.f);
   if (!rc) rc = finish_loss(e, nseq, loss_per_seq, mean_loss);
   return rc;
@@ -582,7 +592,7 @@ extern "C" int ane_eval_loss_windows(ane_engine* e, const uint64_t* positions, i
   if (nseq <= 0 || nseq > e->opt.max_batch || !positions)
     return eng_fail(e, ANE_ERR_ARG, "storiesane eval loss: nseq=%d must be in [1, %d]", nseq, e->opt.max_batch);
   int rc = load_windows(e, positions, nseq);
-  if (!rc) rc = forward_body(e, nseq);
+  if (!rc) rc = forward_body(e, nseq, 0);
   if (!rc) rc = head_loss(e, nseq, nullptr, 0.f);
   if (!rc) rc = finish_loss(e, nseq, loss_per_seq, mean_loss);
   return rc;
@@ -597,7 +607,7 @@ extern "C" int ane_eval_logits(ane_engine* e, const uint16_t* tokens, int64_t nt
   const ane_model_cfg& c = e->cfg;
   const int D = c.dim, V = c.vocab, S = c.seq;
   HIPCHK(op, hipMemcpyAsync(e->tok, tokens, (size_t)S * 2, hipMemcpyHostToDevice, e->stream));
-  int rc = forward_body(e, 1);
+  int rc = forward_body(e, 1, 0);
   if (rc) return rc;
   EpiParams p;
   p.C = e->logits; p.ldc = S; p.softcap = c.arch == ANE_ARCH_NANOCHAT; p.cap = 15.f;
@@ -726,8 +736,8 @@ done:
   return rc;
 }
 
-extern "C" int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, const uint16_t* qkv,
-                                   uint16_t* out, float* lse) {
+extern "C" int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float scale, int hilo,
+                                   const uint16_t* qkv, uint16_t* out, float* lse) {
   int rc = ANE_OK;
   const int D = 64 * NH;
   const size_t T = (size_t)nseq * S;
@@ -751,7 +761,7 @@ extern "C" int ane_debug_attention(int nseq, int S, int NH, int qknorm, double t
   DBGCHK(hipMemcpy(ds, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
   a.qkv = (const half_t*)dq; a.out = (half_t*)dout; a.lse = (float*)dl;
   a.rope_cos = (const float*)dc; a.rope_sin = (const float*)ds;
-  a.nseq = nseq; a.S = S; a.NH = NH; a.qknorm = qknorm; a.scale = 0.125f;
+  a.nseq = nseq; a.S = S; a.NH = NH; a.qknorm = qknorm; a.scale = scale; a.hilo = hilo;
   DBGCHK(attention_fwd(a, nullptr));
   DBGCHK(hipDeviceSynchronize());
   DBGCHK(hipMemcpy(out, dout, T * D * 2, hipMemcpyDeviceToHost));

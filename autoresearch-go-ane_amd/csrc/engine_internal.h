@@ -26,6 +26,55 @@ struct LayerShadow {
   ane::half_t* w2 = nullptr;    // [D, H]
 };
 
+// activations one layer keeps for its backward ([T, C] token-major)
+struct LayerActs {
+  float* xin = nullptr;         // layer input (fp32 residual stream)
+  ane::half_t* xn = nullptr;    // RMSNorm(xin), QKV GEMM operand
+  ane::half_t* qkv = nullptr;   // [T, 3D] projections (pre-RoPE)
+  ane::half_t* qkvt = nullptr;  // [T, 3D] q, k after RoPE / QK-norm, v after VE
+  ane::half_t* qk_lo = nullptr; // [T, 2D] fp16 residuals of those q, k (reference-compat backward)
+  ane::half_t* att = nullptr;   // attention output
+  float* lse = nullptr;         // [T, NH]
+  float* x2 = nullptr;          // residual after attention
+  ane::half_t* xn2 = nullptr;   // RMSNorm(x2)
+  ane::half_t* h13 = nullptr;   // FFN pre-activations ([T, 2H] interleaved W1|W3, or [T, H])
+  ane::half_t* gate = nullptr;  // FFN activation, W2 operand
+};
+
+struct TrainBufs {
+  std::vector<LayerActs> L;
+  float* xlast = nullptr;   // output of the last layer
+  float* xfinal = nullptr;  // nanochat: after backout
+  float* sg_act = nullptr;  // nanochat: smear gate sigmoid
+  ane::half_t* x0h = nullptr;
+  // gradients and optimizer state (canonical layout)
+  float* G = nullptr;
+  float* M = nullptr;
+  float* Vv = nullptr;
+  // backward scratch
+  float* dcur = nullptr;
+  ane::half_t* dcur_h = nullptr;
+  float* dx2 = nullptr;
+  ane::half_t* dx2_h = nullptr;
+  float* dxn = nullptr;
+  ane::half_t* dh13 = nullptr;
+  ane::half_t* datt = nullptr;
+  ane::half_t* dqkv = nullptr;
+  float* delta = nullptr;
+  ane::half_t* att1 = nullptr;  // compat: scale-1 attention output
+  float* lse1 = nullptr;
+  ane::half_t* dl = nullptr;    // [V, T] dlogits
+  float* colscale = nullptr;
+  float* gx0 = nullptr;
+  float* ginj = nullptr;
+  float* ve_dx = nullptr;
+  ane::half_t* dgp = nullptr;
+  float* dgain_part = nullptr;
+  double* dot_part = nullptr;
+  double* sumsq = nullptr;
+  double* sumsq_part = nullptr;
+};
+
 struct ProfEvent {
   hipEvent_t a = nullptr, b = nullptr;
   int cls = 0;
@@ -87,6 +136,11 @@ struct ane_engine {
   ane_state state{};
   uint64_t rng = 0;
   float lr = 0.f;
+  bool train_ready = false;
+  TrainBufs tr;
+  double start_s = 0.0;  // wall clock at open (CumWallMS)
+  hipEvent_t step_ev[4] = {nullptr, nullptr, nullptr, nullptr};  // step start, head start/end, adam start
+  bool flushed = false;
 
   // profiling
   bool prof_on = false;
@@ -96,11 +150,34 @@ struct ane_engine {
 };
 
 int eng_fail(ane_engine* e, int code, const char* fmt, ...);
+
+#define HIPCHK(op, expr)                                                                             \
+  do {                                                                                               \
+    hipError_t _h = (expr);                                                                          \
+    if (_h != hipSuccess) return eng_fail(e, ANE_ERR_HIP, "storiesane %s: %s: %s", op, #expr,        \
+                                          hipGetErrorString(_h));                                    \
+  } while (0)
+
+#define CLOSED_CHECK(op)                                                                          \
+  do {                                                                                            \
+    if (!e) return ANE_ERR_CLOSED;                                                                \
+    if (e->closed) return eng_fail(e, ANE_ERR_CLOSED, "storiesane %s: engine is closed", op);     \
+  } while (0)
 void prof_begin(ane_engine* e, int cls);
 void prof_end(ane_engine* e, double flops, double bytes);
 hipError_t eng_gemm(ane_engine* e, int cls, const ane::half_t* A, int lda, bool at, const ane::half_t* B, int ldb,
                     bool bt, int M, int N, int K, int epi, const ane::EpiParams& p, int bm = 0, int bn = 0);
 int refresh_shadows(ane_engine* e);
-int forward_body(ane_engine* e, int nseq);
+int forward_body(ane_engine* e, int nseq, int train);
+template <class T>
+hipError_t dalloc(ane_engine* e, T** p, size_t n) {
+  void* q = nullptr;
+  hipError_t r = hipMalloc(&q, n * sizeof(T) > 0 ? n * sizeof(T) : 16);
+  if (r == hipSuccess) {
+    e->allocs.push_back(q);
+    *p = (T*)q;
+  }
+  return r;
+}
 int head_loss(ane_engine* e, int nseq, float* colscale, float dscale);
 int load_windows(ane_engine* e, const uint64_t* positions, int nseq);

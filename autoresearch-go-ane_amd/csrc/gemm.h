@@ -28,6 +28,8 @@ enum Epi : int {
   EPI_CE = 7,        // rows = vocab, cols = tokens: per-column partial (max, sumexp) + target logit
   EPI_DLOGITS = 8,   // rows = vocab, cols = tokens: C (fp16) = dlogit (see kernel)
   EPI_STORE_W13 = 9, // C (fp32) rows of an interleaved W1|W3 gradient scattered to two outputs
+  EPI_SWIGLU_BWD = 10, // acc = dgate [T, H]; C2 (fp16) = h1|h3 interleaved -> C (fp16) = dh1|dh3 interleaved
+  EPI_RELU2_BWD = 11,  // acc = dgate [T, H]; C2 (fp16) = h1 -> C (fp16) = dgate * 2 * max(h1, 0)
 };
 
 struct GemmArgs {

@@ -317,6 +317,51 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
           C[row * e.ldc + COL(j)] = (half_t)(rl * rl);
           if (C2) C2[row * e.ldc2 + COL(j)] = (half_t)h;
         }
+  } else if constexpr (EPI == EPI_SWIGLU_BWD) {
+    // columns are hidden units h; W1|W3 rows are interleaved by 32, so the
+    // pre-activations of h sit at (h/32)*64 + h%32 (h1) and +32 (h3).
+    // SwiGLU derivative as the llama2 variant's CPU restatement computes it.
+    half_t* C = (half_t*)e.C;
+    const half_t* H13 = (const half_t*)e.C2;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        const int h = COL(j);
+        const int c1 = (h >> 5) * 64 + (h & 31);
+        float h1v[16], h3v[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const size_t row = (size_t)ROW(i, r) * e.ldc2;
+          h1v[r] = (float)H13[row + c1];
+          h3v[r] = (float)H13[row + c1 + 32];
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float dg = acc[i][j][r];
+          const float sg = 1.0f / (1.0f + __expf(-h1v[r]));
+          const size_t row = (size_t)ROW(i, r) * e.ldc;
+          C[row + c1] = (half_t)(dg * h3v[r] * (sg + h1v[r] * sg * (1.f - sg)));
+          C[row + c1 + 32] = (half_t)(dg * h1v[r] * sg);
+        }
+      }
+  } else if constexpr (EPI == EPI_RELU2_BWD) {
+    // reluSquaredBackwardSimple (ane/accel_stub.go:21-29): dh = dgate * 2 * relu(h)
+    half_t* C = (half_t*)e.C;
+    const half_t* H1 = (const half_t*)e.C2;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        float hv[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) hv[r] = (float)H1[(size_t)ROW(i, r) * e.ldc2 + COL(j)];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float rl = hv[r] > 0.f ? hv[r] : 0.f;
+          C[(size_t)ROW(i, r) * e.ldc + COL(j)] = (half_t)(acc[i][j][r] * 2.f * rl);
+        }
+      }
   } else if constexpr (EPI == EPI_SMEAR) {
     float* C = (float*)e.C;
     float* C2 = (float*)e.C2;
@@ -509,6 +554,8 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
   // backward dX = dY * W  (B transposed)
   CASE(1, false, true, EPI_STORE_H)
   CASE(1, false, true, EPI_STORE_F)
+  CASE(1, false, true, EPI_SWIGLU_BWD)
+  CASE(1, false, true, EPI_RELU2_BWD)
   // backward dW = dY^T * X (both transposed)
   CASE(3, true, true, EPI_STORE_F)
   CASE(3, true, true, EPI_STORE_W13)

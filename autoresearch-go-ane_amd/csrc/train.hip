@@ -1,0 +1,571 @@
+// Training: backward pass, gradient accumulation, clipping and AdamW, and
+// the Step / Flush / SetLR / State entry points of the C-ABI.
+//
+// Follows the reference's CPU path (backwardAndAccumulate / backwardAndApply,
+// ane/train_full.go:691-967; runFinalHead, :480-558; flushPending,
+// ane/engine.go:646-682) on the device:
+//  * the loss seed is dlogits = (softmax - onehot) * lossScale / valid per
+//    sequence (times the softcap derivative for nanochat), so every
+//    activation gradient carries the loss scale, as in the reference;
+//  * weight gradients are summed over all sequences of a call by the dW
+//    GEMMs (reduction over T = nseq * seq) and accumulate into one fp32
+//    gradient vector in the canonical parameter layout;
+//  * a flush scales by 1 / (pending * lossScale), clips the global L2 norm of
+//    the layer + embedding gradients, and applies AdamW with the reference's
+//    parameter groups, then rebuilds the fp16 weight shadows.
+// dlogits are stored fp16 times kDlScale (so probabilities ~1e-5 stay
+// normal fp16 numbers); the two GEMMs that consume them divide it out.
+#include <math.h>
+#include <string.h>
+#include <time.h>
+
+#include <vector>
+
+#include "attention.h"
+#include "engine_internal.h"
+#include "gemm.h"
+#include "rowops.h"
+#include "train_ops.h"
+
+using namespace ane;
+
+namespace {
+
+constexpr float kDlScale = 64.f;
+
+double now_s() {
+  timespec ts;
+  clock_gettime(CLOCK_MONOTONIC, &ts);
+  return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+int ensure_train(ane_engine* e, const char* op) {
+  if (e->train_ready) return ANE_OK;
+  const ane_model_cfg& c = e->cfg;
+  const bool llama = c.arch == ANE_ARCH_LLAMA2;
+  const size_t D = c.dim, H = c.hidden, V = c.vocab, NH = c.heads;
+  const size_t T = (size_t)e->opt.max_batch * c.seq;
+  const size_t KH = llama ? 2 * H : H;
+  if (c.seq > 256)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane %s: training supports seq <= 256 (got %d)", op, c.seq);
+  TrainBufs& tb = e->tr;
+  tb.L.assign(c.layers, LayerActs());
+  for (int l = 0; l < c.layers; l++) {
+    LayerActs& A = tb.L[l];
+    HIPCHK(op, dalloc(e, &A.xin, T * D));
+    HIPCHK(op, dalloc(e, &A.xn, T * D));
+    HIPCHK(op, dalloc(e, &A.qkv, T * 3 * D));
+    HIPCHK(op, dalloc(e, &A.qkvt, T * 3 * D));
+    if (!llama && c.grad_mode == ANE_GRAD_COMPAT) HIPCHK(op, dalloc(e, &A.qk_lo, T * 2 * D));
+    HIPCHK(op, dalloc(e, &A.att, T * D));
+    HIPCHK(op, dalloc(e, &A.lse, T * NH));
+    HIPCHK(op, dalloc(e, &A.x2, T * D));
+    HIPCHK(op, dalloc(e, &A.xn2, T * D));
+    HIPCHK(op, dalloc(e, &A.h13, T * KH));
+    HIPCHK(op, dalloc(e, &A.gate, T * H));
+  }
+  HIPCHK(op, dalloc(e, &tb.xlast, T * D));
+  if (!llama) {
+    HIPCHK(op, dalloc(e, &tb.xfinal, T * D));
+    HIPCHK(op, dalloc(e, &tb.sg_act, T * D));
+    HIPCHK(op, dalloc(e, &tb.x0h, T * D));
+    HIPCHK(op, dalloc(e, &tb.gx0, T * D));
+    HIPCHK(op, dalloc(e, &tb.ginj, T * D));
+    HIPCHK(op, dalloc(e, &tb.ve_dx, T * 12));
+    HIPCHK(op, dalloc(e, &tb.dgp, T * D));
+    HIPCHK(op, dalloc(e, &tb.att1, T * D));
+    HIPCHK(op, dalloc(e, &tb.lse1, T * NH));
+  }
+  const size_t P = (size_t)e->pm.total;
+  HIPCHK(op, dalloc(e, &tb.G, P));
+  HIPCHK(op, dalloc(e, &tb.M, P));
+  HIPCHK(op, dalloc(e, &tb.Vv, P));
+  HIPCHK(op, fill_f32(tb.G, P, 0.f, e->stream));
+  HIPCHK(op, fill_f32(tb.M, P, 0.f, e->stream));
+  HIPCHK(op, fill_f32(tb.Vv, P, 0.f, e->stream));
+  HIPCHK(op, dalloc(e, &tb.dcur, T * D));
+  HIPCHK(op, dalloc(e, &tb.dcur_h, T * D));
+  HIPCHK(op, dalloc(e, &tb.dx2, T * D));
+  HIPCHK(op, dalloc(e, &tb.dx2_h, T * D));
+  HIPCHK(op, dalloc(e, &tb.dxn, T * D));
+  HIPCHK(op, dalloc(e, &tb.dh13, T * KH));
+  HIPCHK(op, dalloc(e, &tb.datt, T * D));
+  HIPCHK(op, dalloc(e, &tb.dqkv, T * 3 * D));
+  HIPCHK(op, dalloc(e, &tb.delta, T * NH));
+  HIPCHK(op, dalloc(e, &tb.dl, V * T));
+  HIPCHK(op, dalloc(e, &tb.colscale, T));
+  const size_t nblk = (size_t)norm_bwd_blocks((int)T);
+  HIPCHK(op, dalloc(e, &tb.dgain_part, nblk * D));
+  HIPCHK(op, dalloc(e, &tb.dot_part, (nblk > 256 ? nblk : 256) * 2));
+  HIPCHK(op, dalloc(e, &tb.sumsq, 1));
+  HIPCHK(op, dalloc(e, &tb.sumsq_part, 256));
+  for (int i = 0; i < 4; i++) HIPCHK(op, hipEventCreate(&e->step_ev[i]));
+  e->train_ready = true;
+  return ANE_OK;
+}
+
+// Forward + backward of the nseq sequences in e->tok / e->tgt; ADDS the
+// loss-scaled gradient sum to tr.G and leaves per-sequence losses in
+// e->loss_seq.
+int backward_pass(ane_engine* e, int nseq) {
+  const char* op = "step";
+  const ane_model_cfg& c = e->cfg;
+  const bool llama = c.arch == ANE_ARCH_LLAMA2;
+  const bool compat = !llama && c.grad_mode == ANE_GRAD_COMPAT;
+  const int D = c.dim, H = c.hidden, V = c.vocab, S = c.seq, NH = c.heads, L = c.layers;
+  const int T = nseq * S, KH = llama ? 2 * H : H;
+  const int nblk = norm_bwd_blocks(T);
+  TrainBufs& tb = e->tr;
+  const float* P = e->P;
+  float* G = tb.G;
+  hipStream_t st = e->stream;
+  const ParamMap& pm = e->pm;
+
+  int rc = forward_body(e, nseq, 1);
+  if (rc) return rc;
+
+  // ---- final head (runFinalHead, ane/train_full.go:480-558) ----------------
+  (void)hipEventRecord(e->step_ev[1], st);
+  rc = head_loss(e, nseq, tb.colscale, e->opt.loss_scale * kDlScale);
+  if (rc) return rc;
+  {
+    EpiParams p;
+    p.C = tb.dl; p.ldc = T; p.targets = e->tgt; p.lse = e->lse; p.colscale = tb.colscale;
+    p.softcap = !llama; p.cap = 15.f; p.vocab = V;
+    HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_DLOGITS, p));
+  }
+  {  // dy = Embed^T dlogits (MatMulEmbedTScale, ane/stories/cpu.go:333-360)
+    EpiParams p;
+    p.C = tb.dxn; p.ldc = D; p.scale = 1.f / kDlScale;
+    HIPCHK(op, eng_gemm(e, 7, tb.dl, T, true, e->embed_h, D, true, T, D, V, EPI_STORE_F, p));
+  }
+  {  // classifier part of the embedding gradient (MatMulGradEmbedScale, ane/stories/cpu.go:366-385)
+    EpiParams p;
+    p.C = G + pm.embed; p.ldc = D; p.scale = 1.f / kDlScale; p.accumulate = 1;
+    HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, e->xh, D, true, V, D, T, EPI_STORE_F, p));
+  }
+  {  // final RMSNorm backward (+ backout backward for nanochat)
+    NormBwdArgs a;
+    a.dy = tb.dxn; a.T = T; a.D = D; a.out = tb.dcur; a.out_h = tb.dcur_h;
+    if (llama) {
+      a.x = tb.xlast; a.gain = P + pm.g_final; a.dgain_part = tb.dgain_part;
+    } else {
+      a.x = tb.xfinal;
+    }
+    HIPCHK(op, norm_bwd(a, st));
+    if (llama) {
+      HIPCHK(op, reduce_partials_add(G + pm.g_final, tb.dgain_part, nblk, D, st));
+    } else {
+      HIPCHK(op, backout_bwd(tb.ginj, tb.dot_part, tb.dcur, e->xmid, P + pm.backout_lambda, T, D, st));
+      HIPCHK(op, reduce_dots_add(G + pm.backout_lambda, nullptr, tb.dot_part, 256, -1.f, st));
+      HIPCHK(op, fill_f32(tb.gx0, (size_t)T * D, 0.f, st));
+    }
+  }
+  (void)hipEventRecord(e->step_ev[2], st);
+
+  // ---- layers, last to first ------------------------------------------------
+  for (int l = L - 1; l >= 0; l--) {
+    const LayerOff& o = pm.L[l];
+    const LayerShadow& s = e->ls[l];
+    const LayerActs& A = tb.L[l];
+    const float* rl_p = llama ? nullptr : P + pm.resid + l;
+    const float* xl_p = llama ? nullptr : P + pm.x0l + l;
+    // FFN (backwardFFNCPU, ane/train_full.go:592-601)
+    {
+      EpiParams p;
+      p.C = tb.dh13; p.ldc = KH; p.C2 = A.h13; p.ldc2 = KH;
+      HIPCHK(op, eng_gemm(e, 3, tb.dcur_h, D, false, s.w2, H, true, T, H, D, llama ? EPI_SWIGLU_BWD : EPI_RELU2_BWD,
+                          p));
+    }
+    {
+      EpiParams p;
+      p.C = tb.dxn; p.ldc = D;
+      HIPCHK(op, eng_gemm(e, 2, tb.dh13, KH, false, s.w13, D, true, T, D, KH, EPI_STORE_F, p));
+    }
+    {  // dW2 += dOut gate^T
+      EpiParams p;
+      p.C = G + o.w2; p.ldc = H; p.accumulate = 1;
+      HIPCHK(op, eng_gemm(e, 3, tb.dcur_h, D, true, A.gate, H, true, D, H, T, EPI_STORE_F, p));
+    }
+    {  // dW1 (| dW3) += dh x2Norm^T
+      EpiParams p;
+      p.C = G + o.w1; p.ldc = D; p.accumulate = 1;
+      if (llama) {
+        p.C3 = G + o.w3;
+        HIPCHK(op, eng_gemm(e, 2, tb.dh13, KH, true, A.xn2, D, true, KH, D, T, EPI_STORE_W13, p));
+      } else {
+        HIPCHK(op, eng_gemm(e, 2, tb.dh13, KH, true, A.xn2, D, true, KH, D, T, EPI_STORE_F, p));
+      }
+    }
+    {  // dx2 = rl * dOut + RMSNorm-backward(dxn2; x2)
+      NormBwdArgs a;
+      a.dy = tb.dxn; a.x = A.x2; a.T = T; a.D = D; a.addend = tb.dcur; a.alpha_p = rl_p;
+      a.out = tb.dx2; a.out_h = tb.dx2_h;
+      if (llama) {
+        a.gain = P + o.g_ffn; a.dgain_part = tb.dgain_part;
+      } else {
+        a.lam_x = A.x2; a.lam_x0 = e->x0; a.lam_part = tb.dot_part; a.gx0 = tb.gx0; a.xl_p = xl_p;
+      }
+      HIPCHK(op, norm_bwd(a, st));
+      if (llama)
+        HIPCHK(op, reduce_partials_add(G + o.g_ffn, tb.dgain_part, nblk, D, st));
+      else
+        HIPCHK(op, reduce_dots_add(G + pm.resid + l, G + pm.x0l + l, tb.dot_part, nblk, 1.f, st));
+    }
+    // attention (backwardAttentionCPU, ane/train_full.go:644-675)
+    {
+      EpiParams p;
+      p.C = tb.datt; p.ldc = D;
+      HIPCHK(op, eng_gemm(e, 1, tb.dx2_h, D, false, s.wo, D, true, T, D, D, EPI_STORE_H, p));
+    }
+    {
+      EpiParams p;
+      p.C = G + o.wo; p.ldc = D; p.accumulate = 1;
+      HIPCHK(op, eng_gemm(e, 1, tb.dx2_h, D, true, A.att, D, true, D, D, T, EPI_STORE_F, p));
+    }
+    {
+      AttnBwdArgs b;
+      memset(&b, 0, sizeof b);
+      b.qkv = A.qkv; b.qkvt = A.qkvt; b.dout = tb.datt; b.delta = tb.delta; b.dqkv = tb.dqkv;
+      b.rope_cos = e->rope_cos; b.rope_sin = e->rope_sin; b.nseq = nseq; b.S = S; b.NH = NH;
+      b.qknorm = llama ? 0 : 1;
+      if (compat) {
+        // the reference's backward recomputes the probabilities with scale
+        // 1.0 (ane/train_full.go:268-269): its O and lse come from a scale-1 forward
+        AttnArgs f;
+        memset(&f, 0, sizeof f);
+        f.qkv = A.qkv; f.out = tb.att1; f.lse = tb.lse1; f.rope_cos = e->rope_cos; f.rope_sin = e->rope_sin;
+        f.nseq = nseq; f.S = S; f.NH = NH; f.qknorm = 1; f.scale = 1.0f;
+        // scale-1 scores reach |q.k| ~ 1.44 * 64: fp16 rounding of q and k
+        // would move them by ~0.05, so both passes use split operands
+        f.hilo = 1;
+        if (o.ve_embed >= 0) {
+          f.ve_x = A.xin; f.ve_gate = P + o.ve_gate; f.ve_embed = P + o.ve_embed; f.tokens = e->tok; f.vocab = V;
+        }
+        prof_begin(e, 5);
+        HIPCHK(op, attention_fwd(f, st));
+        prof_end(e, 0, 0);
+        b.o = tb.att1; b.lse = tb.lse1; b.scale_p = 1.f; b.scale_ds = 1.f; b.qk_coef2 = 1.2f * 1.2f; b.rope_bwd = 0;
+        b.qkvt_lo = A.qk_lo; b.hilo = 1;
+      } else {
+        b.o = A.att; b.lse = A.lse; b.scale_p = 0.125f; b.scale_ds = 0.125f; b.qk_coef2 = 1.2f; b.rope_bwd = 1;
+      }
+      prof_begin(e, 5);
+      HIPCHK(op, attention_bwd(b, st));
+      prof_end(e, 2.5 * 4.0 * 64 * NH * (double)nseq * ((double)S * (S + 1) / 2), 0);
+    }
+    if (o.ve_embed >= 0)
+      HIPCHK(op, ve_bwd(G + o.ve_embed, G + o.ve_gate, tb.ve_dx, tb.dqkv + 2 * D, 3 * D, A.xin, P + o.ve_embed,
+                        P + o.ve_gate, e->tok, T, D, NH, V, st));
+    {
+      EpiParams p;
+      p.C = tb.dxn; p.ldc = D;
+      HIPCHK(op, eng_gemm(e, 0, tb.dqkv, 3 * D, false, s.wqkv, D, true, T, D, 3 * D, EPI_STORE_F, p));
+    }
+    {  // dWq | dWk | dWv += dqkv xNorm^T
+      EpiParams p;
+      p.C = G + o.wq; p.ldc = D; p.accumulate = 1;
+      HIPCHK(op, eng_gemm(e, 0, tb.dqkv, 3 * D, true, A.xn, D, true, 3 * D, D, T, EPI_STORE_F, p));
+    }
+    {  // dPrev = rl * dx2 + RMSNorm-backward(dxn; x) (+ VE gate grads, + backout injection)
+      NormBwdArgs a;
+      a.dy = tb.dxn; a.x = A.xin; a.T = T; a.D = D; a.addend = tb.dx2; a.alpha_p = rl_p;
+      a.out = tb.dcur; a.out_h = tb.dcur_h;
+      if (llama) {
+        a.gain = P + o.g_att; a.dgain_part = tb.dgain_part;
+      } else {
+        a.lam_x = A.xin; a.lam_x0 = e->x0; a.lam_part = tb.dot_part; a.gx0 = tb.gx0; a.xl_p = xl_p;
+        if (o.ve_embed >= 0) a.ve_dx = tb.ve_dx;
+        if (l == L / 2) a.addend2 = tb.ginj;  // ane/train_full.go:784-787
+      }
+      HIPCHK(op, norm_bwd(a, st));
+      if (llama)
+        HIPCHK(op, reduce_partials_add(G + o.g_att, tb.dgain_part, nblk, D, st));
+      else
+        HIPCHK(op, reduce_dots_add(G + pm.resid + l, G + pm.x0l + l, tb.dot_part, nblk, 1.f, st));
+    }
+  }
+
+  // ---- embedding side ---------------------------------------------------------
+  if (!llama) {
+    // compat: the x0 gradient joins before the smear backward
+    // (ane/train_full.go:790-798); exact: after it (x0 is pre-smear)
+    if (compat) HIPCHK(op, axpy_inplace(tb.dcur, tb.gx0, nullptr, (size_t)T * D, st));
+    HIPCHK(op, smear_bwd_prep(tb.dgp, tb.dx2, tb.dot_part, tb.dcur, tb.sg_act, e->x0, P + pm.smear_lambda, T, D, S,
+                              st));
+    HIPCHK(op, reduce_dots_add(G + pm.smear_lambda, nullptr, tb.dot_part, 256, 1.f, st));
+    {
+      EpiParams p;
+      p.C = G + pm.smear_gate; p.ldc = D; p.accumulate = 1;
+      HIPCHK(op, eng_gemm(e, 7, tb.dgp, D, true, tb.x0h, D, true, D, D, T, EPI_STORE_F, p));
+    }
+    {
+      EpiParams p;
+      p.C = tb.dx2; p.ldc = D; p.accumulate = 1;
+      HIPCHK(op, eng_gemm(e, 7, tb.dgp, D, false, e->smear_h, D, true, T, D, D, EPI_STORE_F, p));
+    }
+    if (!compat) HIPCHK(op, axpy_inplace(tb.dx2, tb.gx0, nullptr, (size_t)T * D, st));
+    NormBwdArgs a;  // embedding RMSNorm backward (ane/train_full.go:921-925)
+    a.dy = tb.dx2; a.x = e->xpre; a.T = T; a.D = D; a.out = tb.dcur;
+    HIPCHK(op, norm_bwd(a, st));
+  }
+  HIPCHK(op, embed_bwd(G + pm.embed, tb.dcur, e->tok, T, D, V, st));
+  return ANE_OK;
+}
+
+void bias_inv(int t, float b1, float b2, float* i1, float* i2) {
+  // adamBiasCorrectionInv (ane/train_full.go:1107-1111)
+  const float bc1 = (float)(1.0 - pow((double)b1, (double)t));
+  const float bc2 = (float)(1.0 - pow((double)b2, (double)t));
+  *i1 = 1.f / bc1;
+  *i2 = 1.f / bc2;
+}
+
+void add_seg(AdamArgs& a, int64_t off, int64_t len, float lr, float wd, float b1, float b2, float i1, float i2,
+             int clip) {
+  AdamSeg& s = a.seg[a.nseg++];
+  s.off = off; s.len = len; s.lr = lr; s.wd = wd; s.b1 = b1; s.b2 = b2; s.i1 = i1; s.i2 = i2; s.clip = clip;
+  s.pad = 0;
+}
+
+// flushPending (ane/engine.go:646-682)
+int flush_pending(ane_engine* e) {
+  const char* op = "flush";
+  if (!e->train_ready || e->state.pending_steps == 0) return ANE_OK;
+  const ane_model_cfg& c = e->cfg;
+  const bool llama = c.arch == ANE_ARCH_LLAMA2;
+  const int64_t D = c.dim, H = c.hidden, V = c.vocab, NH = c.heads, L = c.layers;
+  const ParamMap& pm = e->pm;
+  TrainBufs& tb = e->tr;
+  const ane_options& O = e->opt;
+  hipStream_t st = e->stream;
+
+  float gscale = (float)(1.0 / (double)e->state.pending_steps);
+  gscale /= O.loss_scale;
+  HIPCHK(op, sumsq(tb.sumsq, tb.sumsq_part, tb.G, (size_t)(pm.embed + V * D), st));
+  e->state.adam_t++;
+  const int t = (int)e->state.adam_t;
+  float i1, i2, l1, l2;
+  bias_inv(t, O.adam_beta1, O.adam_beta2, &i1, &i2);
+  bias_inv(t, O.lambda_beta1, O.lambda_beta2, &l1, &l2);
+  const float lr = e->lr, embed_lr = e->lr * O.embed_lr_mult, scalar_lr = e->lr * O.scalar_lr_mult;
+  const float lambda_lr = e->lr * O.scalar_lr_mult * O.lambda_lr_mult;
+  const float b1 = O.adam_beta1, b2 = O.adam_beta2, wd = O.weight_decay;
+  AdamArgs a;
+  memset(&a, 0, sizeof a);
+  a.w = e->P; a.g = tb.G; a.m = tb.M; a.v = tb.Vv; a.sumsq = tb.sumsq;
+  a.gscale = gscale; a.clip = O.grad_clip; a.eps = O.adam_eps;
+  // applyLayerAdam (ane/train_full.go:1088-1100): matrices with lr + wd; gains
+  // and VE gate with the scalar lr, VE table with the embedding lr, no wd
+  for (int l = 0; l < L; l++) {
+    const LayerOff& o = pm.L[l];
+    add_seg(a, o.wq, o.w2 + D * H - o.wq, lr, wd, b1, b2, i1, i2, 1);
+    if (llama) {
+      add_seg(a, o.w3, H * D, lr, wd, b1, b2, i1, i2, 1);
+      add_seg(a, o.g_att, 2 * D, scalar_lr, 0.f, b1, b2, i1, i2, 1);
+    } else if (o.ve_embed >= 0) {
+      add_seg(a, o.ve_embed, V * D, embed_lr, 0.f, b1, b2, i1, i2, 1);
+      add_seg(a, o.ve_gate, NH * 12, scalar_lr, 0.f, b1, b2, i1, i2, 1);
+    }
+  }
+  // model-level groups (ane/engine.go:659-673)
+  add_seg(a, pm.embed, V * D, embed_lr, 0.f, b1, b2, i1, i2, 1);
+  if (llama) {
+    add_seg(a, pm.g_final, D, scalar_lr, 0.f, b1, b2, i1, i2, 0);
+  } else {
+    add_seg(a, pm.smear_gate, D * D, lr, wd, b1, b2, i1, i2, 0);
+    add_seg(a, pm.smear_lambda, 2, scalar_lr, 0.f, b1, b2, i1, i2, 0);
+    add_seg(a, pm.resid, 2 * L, lambda_lr, 0.f, O.lambda_beta1, O.lambda_beta2, l1, l2, 0);
+  }
+  if (a.nseg > kMaxAdamSegs) return eng_fail(e, ANE_ERR_ARG, "storiesane flush: too many parameter groups");
+  (void)hipEventRecord(e->step_ev[3], st);
+  HIPCHK(op, adam_update(a, st));
+  int rc = refresh_shadows(e);
+  if (rc) return rc;
+  HIPCHK(op, fill_f32(tb.G, (size_t)pm.total, 0.f, st));
+  e->state.pending_steps = 0;
+  e->state.cum_batches++;
+  e->flushed = true;
+  return ANE_OK;
+}
+
+int read_losses(ane_engine* e, int nseq, float* per, double* mean) {
+  const char* op = "step";
+  std::vector<float> ls(nseq);
+  HIPCHK(op, hipMemcpyAsync(ls.data(), e->loss_seq, (size_t)nseq * 4, hipMemcpyDeviceToHost, e->stream));
+  HIPCHK(op, hipStreamSynchronize(e->stream));
+  double tot = 0;
+  for (int b = 0; b < nseq; b++) {
+    tot += ls[b];
+    if (per) per[b] = ls[b];
+  }
+  *mean = nseq > 0 ? tot / nseq : 0.0;
+  return ANE_OK;
+}
+
+// nseq windows drawn from the drand48 stream, one fused forward/backward,
+// pending += nseq, flush when pending >= AccumSteps: the same update as
+// nseq consecutive reference Steps (ane/engine.go:381-442).
+int train_windows(ane_engine* e, int nseq, ane_step_result* res) {
+  const char* op = "step";
+  const double t0 = now_s();
+  if (!e->data || e->ndata < (int64_t)e->cfg.seq + 1) return eng_fail(e, ANE_ERR_STATE, "storiesane step: not enough tokens");
+  if (nseq <= 0 || nseq > e->opt.max_batch)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane step: nseq=%d must be in [1, %d]", nseq, e->opt.max_batch);
+  int rc = ensure_train(e, op);
+  if (rc) return rc;
+  const uint64_t S = (uint64_t)e->cfg.seq;
+  const uint64_t limit = (uint64_t)e->ndata - S - 1;
+  std::vector<uint64_t> pos(nseq);
+  for (int b = 0; b < nseq; b++) {
+    uint64_t p = 0;
+    if (limit > 0) {
+      p = (uint64_t)(drand48_next(&e->rng) * (double)limit);
+      if (p >= limit) p = limit - 1;
+    }
+    pos[b] = p;
+    e->state.token_pos = p + S;
+  }
+  rc = load_windows(e, pos.data(), nseq);
+  if (rc) return rc;
+  e->flushed = false;
+  (void)hipEventRecord(e->step_ev[0], e->stream);
+  rc = backward_pass(e, nseq);
+  if (rc) return rc;
+  e->state.pending_steps += (uint32_t)nseq;
+  if ((int)e->state.pending_steps >= e->opt.accum_steps) {
+    rc = flush_pending(e);
+    if (rc) return rc;
+  }
+  double mean = 0;
+  rc = read_losses(e, nseq, nullptr, &mean);
+  if (rc) return rc;
+  const double dt = now_s() - t0;
+  e->state.last_loss = (float)mean;
+  e->state.cum_steps += (uint32_t)nseq;
+  e->state.cum_train_ms += dt * 1e3;
+  e->state.cum_wall_ms = (now_s() - e->start_s) * 1e3;
+  if (res) {
+    memset(res, 0, sizeof *res);
+    res->loss = (float)mean;
+    res->step_ns = (int64_t)(dt * 1e9);
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, e->step_ev[0], e->step_ev[e->flushed ? 3 : 2]) == hipSuccess)
+      res->ane_eval_ns = (int64_t)((double)ms * 1e6);
+    if (hipEventElapsedTime(&ms, e->step_ev[1], e->step_ev[2]) == hipSuccess)
+      res->final_head_ns = (int64_t)((double)ms * 1e6);
+    if (e->flushed) {
+      (void)hipEventRecord(e->step_ev[1], e->stream);  // reuse: end of Adam + refresh
+      (void)hipEventSynchronize(e->step_ev[1]);
+      if (hipEventElapsedTime(&ms, e->step_ev[3], e->step_ev[1]) == hipSuccess)
+        res->adam_ns = (int64_t)((double)ms * 1e6);
+    }
+    res->cpu_work_ns = res->step_ns - res->ane_eval_ns - res->adam_ns;
+    if (res->cpu_work_ns < 0) res->cpu_work_ns = 0;
+  }
+  return ANE_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C-ABI
+// ---------------------------------------------------------------------------
+extern "C" int ane_step(ane_engine* e, ane_step_result* res) {
+  CLOSED_CHECK("step");
+  return train_windows(e, 1, res);
+}
+
+extern "C" int ane_train_batch(ane_engine* e, int32_t nseq, ane_step_result* res) {
+  CLOSED_CHECK("step");
+  return train_windows(e, nseq, res);
+}
+
+extern "C" int ane_flush(ane_engine* e, int64_t* ns) {
+  CLOSED_CHECK("flush");
+  const double t0 = now_s();
+  int rc = flush_pending(e);
+  if (rc) return rc;
+  HIPCHK("flush", hipStreamSynchronize(e->stream));
+  if (ns) *ns = (int64_t)((now_s() - t0) * 1e9);
+  return ANE_OK;
+}
+
+extern "C" int ane_grads(ane_engine* e, const uint16_t* tokens, const uint16_t* targets, int32_t nseq, float* grads,
+                         float* mean_loss) {
+  CLOSED_CHECK("grads");
+  const char* op = "grads";
+  if (nseq <= 0 || nseq > e->opt.max_batch || !tokens || !targets || !grads)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane grads: nseq=%d must be in [1, %d]", nseq, e->opt.max_batch);
+  int rc = ensure_train(e, op);
+  if (rc) return rc;
+  if (e->state.pending_steps)
+    return eng_fail(e, ANE_ERR_STATE, "storiesane grads: %u accumulated steps pending; Flush first",
+                    e->state.pending_steps);
+  const size_t T = (size_t)nseq * e->cfg.seq, P = (size_t)e->pm.total;
+  HIPCHK(op, hipMemcpyAsync(e->tok, tokens, T * 2, hipMemcpyHostToDevice, e->stream));
+  HIPCHK(op, hipMemcpyAsync(e->tgt, targets, T * 2, hipMemcpyHostToDevice, e->stream));
+  HIPCHK(op, fill_f32(e->tr.G, P, 0.f, e->stream));
+  rc = backward_pass(e, nseq);
+  if (rc) return rc;
+  HIPCHK(op, hipMemcpyAsync(grads, e->tr.G, P * 4, hipMemcpyDeviceToHost, e->stream));
+  HIPCHK(op, fill_f32(e->tr.G, P, 0.f, e->stream));
+  double mean = 0;
+  rc = read_losses(e, nseq, nullptr, &mean);
+  if (rc) return rc;
+  // the reference's flush scale: 1 / n, then / lossScale (ane/engine.go:650-654)
+  float sc = (float)(1.0 / (double)nseq);
+  sc /= e->opt.loss_scale;
+  for (size_t i = 0; i < P; i++) grads[i] *= sc;
+  if (mean_loss) *mean_loss = (float)mean;
+  return ANE_OK;
+}
+
+extern "C" int ane_set_grads(ane_engine* e, const float* grads, int64_t n, uint32_t pending) {
+  CLOSED_CHECK("set grads");
+  const char* op = "set grads";
+  if (!grads || n != e->pm.total)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane set grads: len=%lld want=%lld", (long long)n, (long long)e->pm.total);
+  int rc = ensure_train(e, op);
+  if (rc) return rc;
+  HIPCHK(op, hipMemcpyAsync(e->tr.G, grads, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
+  HIPCHK(op, hipStreamSynchronize(e->stream));
+  e->state.pending_steps = pending;
+  return ANE_OK;
+}
+
+extern "C" int ane_get_opt_state(ane_engine* e, float* m, float* v, int64_t n) {
+  CLOSED_CHECK("optimizer state");
+  const char* op = "optimizer state";
+  if (n != e->pm.total)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane optimizer state: len=%lld want=%lld", (long long)n,
+                    (long long)e->pm.total);
+  int rc = ensure_train(e, op);
+  if (rc) return rc;
+  if (m) HIPCHK(op, hipMemcpyAsync(m, e->tr.M, (size_t)n * 4, hipMemcpyDeviceToHost, e->stream));
+  if (v) HIPCHK(op, hipMemcpyAsync(v, e->tr.Vv, (size_t)n * 4, hipMemcpyDeviceToHost, e->stream));
+  HIPCHK(op, hipStreamSynchronize(e->stream));
+  return ANE_OK;
+}
+
+extern "C" float ane_lr(const ane_engine* e) { return (e && !e->closed) ? e->lr : 0.f; }
+
+extern "C" int ane_set_lr(ane_engine* e, float lr) {
+  CLOSED_CHECK("set lr");
+  if (!(lr > 0.f)) return eng_fail(e, ANE_ERR_ARG, "storiesane set lr: lr must be > 0");
+  e->lr = lr;
+  return ANE_OK;
+}
+
+extern "C" int ane_get_state(ane_engine* e, ane_state* out) {
+  if (!e || !out) return ANE_ERR_ARG;
+  *out = e->closed ? ane_state{} : e->state;
+  return ANE_OK;
+}
+
+extern "C" int ane_load_state(ane_engine* e, const ane_state* s) {
+  CLOSED_CHECK("load state");
+  if (!s) return eng_fail(e, ANE_ERR_ARG, "storiesane load state: null state");
+  e->state = *s;
+  return ANE_OK;
+}

@@ -1,0 +1,96 @@
+// Row-wise and elementwise kernels of the backward pass and the optimizer.
+#pragma once
+#include "hip_common.h"
+
+namespace ane {
+
+constexpr int kNormBwdRows = 16;  // rows per block of norm_bwd (4 waves x 4 rows)
+
+// out = alpha * addend + addend2 + RMSNorm-backward(dy; x, gain) (+ ve_dx on
+// channels 0..11), fp32 and optionally fp16.  Gain-free form:
+// rmsNormNoWeightBackwardCF (ane/common.go:176-197); gain form:
+// stories.RMSNormBackward (ane/stories/cpu.go:191-210, gain on both terms
+// as there).  Per block of kNormBwdRows rows it also writes partials of
+// dgain (sum dy*x*rrms) and of the two lambda dots (addend.lam_x,
+// addend.lam_x0, in double), and accumulates gx0 += xl * addend.
+struct NormBwdArgs {
+  const float* dy = nullptr;
+  const float* x = nullptr;
+  const float* gain = nullptr;
+  float* dgain_part = nullptr;      // [nblocks][D]
+  const float* addend = nullptr;
+  const float* alpha_p = nullptr;   // device scalar (else alpha)
+  float alpha = 1.f;
+  const float* addend2 = nullptr;
+  const float* ve_dx = nullptr;     // [T][12]
+  float* out = nullptr;
+  half_t* out_h = nullptr;
+  const float* lam_x = nullptr;
+  const float* lam_x0 = nullptr;
+  double* lam_part = nullptr;       // [nblocks][2]
+  float* gx0 = nullptr;
+  const float* xl_p = nullptr;
+  int T = 0, D = 0;
+};
+hipError_t norm_bwd(const NormBwdArgs& a, hipStream_t s);
+inline int norm_bwd_blocks(int T) { return (T + kNormBwdRows - 1) / kNormBwdRows; }
+
+// dst[i] += sum over blocks of part[b][i]  (i < n)
+hipError_t reduce_partials_add(float* dst, const float* part, int nblocks, int n, hipStream_t s);
+// dst[k] += (float)(sign * sum over blocks of part[b][k])  for k < 2 (lambda grads)
+hipError_t reduce_dots_add(float* dst0, float* dst1, const double* part, int nblocks, float sign, hipStream_t s);
+
+// backoutBackwardCF (ane/common.go:393-403): part[b] = partial sum of d * xmid
+// (double), ginj = -lambda * d
+hipError_t backout_bwd(float* ginj, double* part, const float* d, const float* xmid, const float* lam_p, int T,
+                       int D, hipStream_t s);
+
+// backoutForwardCF (ane/common.go:385-389), out of place: out = x - lambda * xmid
+hipError_t backout_fwd(float* out, const float* x, const float* xmid, const float* lam_p, size_t n, hipStream_t s);
+
+// y += x (n floats); with out_h, also writes fp16(y)
+hipError_t axpy_inplace(float* y, const float* x, half_t* out_h, size_t n, hipStream_t s);
+
+// smearBackwardCF first half (ane/common.go:343-382):
+// dgp = dy*lam*s*g*(1-g) (fp16), dout2[t] = dy[t] + dy[t+1]*lam*g[t+1]
+// (same sequence), part = partial sums of dy*g*s (double); s = x0[t-1].
+hipError_t smear_bwd_prep(half_t* dgp, float* dout2, double* part, const float* dy, const float* gact,
+                          const float* x0, const float* lam_p, int T, int D, int seq, hipStream_t s);
+
+// stories.EmbedBackward (ane/stories/cpu.go:74-95): G[tok_t, :] += dx[t, :]
+hipError_t embed_bwd(float* gembed, const float* dx, const uint16_t* tok, int T, int D, int V, hipStream_t s);
+
+// veBackwardCF (ane/train_full.go:1062-1086) for one VE layer.
+hipError_t ve_bwd(float* gve_embed, float* gve_gate, float* ve_dx, const half_t* dv, int ldv, const float* x,
+                  const float* ve_embed, const float* ve_gate, const uint16_t* tok, int T, int D, int NH, int V,
+                  hipStream_t s);
+
+hipError_t fill_f32(float* p, size_t n, float v, hipStream_t s);
+
+// sum of squares of g[0, n) in double -> *out (two passes through part[256])
+hipError_t sumsq(double* out, double* part, const float* g, size_t n, hipStream_t s);
+
+// AdamW over parameter segments (adamUpdateCFWithInv, ane/train_full.go:1113-1150):
+// g' = g * gscale * (clip segment ? clip factor : 1), clip factor =
+// clip / ||g * gscale||_(clip segments) when that norm exceeds clip
+// (clipLayerGradients, ane/train_full.go:167-196).
+struct AdamSeg {
+  int64_t off, len;
+  float lr, wd, b1, b2, i1, i2;
+  int clip;
+  int pad;
+};
+constexpr int kMaxAdamSegs = 64;
+struct AdamArgs {
+  float* w;
+  const float* g;
+  float* m;
+  float* v;
+  const double* sumsq;  // device: sum of squares of the raw clip-segment grads
+  float gscale, clip, eps;
+  int nseg;
+  AdamSeg seg[kMaxAdamSegs];
+};
+hipError_t adam_update(const AdamArgs& a, hipStream_t s);
+
+}  // namespace ane

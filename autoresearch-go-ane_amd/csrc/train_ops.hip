@@ -1,0 +1,397 @@
+// Backward-pass row kernels and the on-device optimizer (HBM-bound).
+// Rows are token-major [T, D]; one wave per row, float4 per lane.
+#include "train_ops.h"
+
+namespace ane {
+
+namespace {
+
+constexpr int kMaxVec = 4;  // D <= 1024: float4 groups per lane
+
+__global__ __launch_bounds__(256) void norm_bwd_kernel(NormBwdArgs a) {
+  __shared__ float gsh[4][1024];
+  __shared__ double lsh[4][2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int D = a.D, nv = D / 4;
+  const float alpha = a.alpha_p ? *a.alpha_p : a.alpha;
+  const float xl = a.xl_p ? *a.xl_p : 0.f;
+  float4 dg[kMaxVec];
+#pragma unroll
+  for (int k = 0; k < kMaxVec; k++) dg[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+  double la = 0.0, lb = 0.0;
+  for (int rr = 0; rr < kNormBwdRows / 4; rr++) {
+    const int t = blockIdx.x * kNormBwdRows + wave * (kNormBwdRows / 4) + rr;
+    if (t >= a.T) break;
+    const size_t ro = (size_t)t * D;
+    float4 dy[kMaxVec], xv[kMaxVec], gv[kMaxVec];
+    float ss = 0.f, dot = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxVec; k++) {
+      const int i = lane + 64 * k;
+      if (i < nv) {
+        dy[k] = reinterpret_cast<const float4*>(a.dy + ro)[i];
+        xv[k] = reinterpret_cast<const float4*>(a.x + ro)[i];
+        gv[k] = a.gain ? reinterpret_cast<const float4*>(a.gain)[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+        ss += xv[k].x * xv[k].x + xv[k].y * xv[k].y + xv[k].z * xv[k].z + xv[k].w * xv[k].w;
+        dot += dy[k].x * xv[k].x * gv[k].x + dy[k].y * xv[k].y * gv[k].y + dy[k].z * xv[k].z * gv[k].z +
+               dy[k].w * xv[k].w * gv[k].w;
+      }
+    }
+    ss = wave_sum(ss);
+    dot = wave_sum(dot);
+    const float rrms = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+    const float c = dot * rrms * rrms / (float)D;  // both forms: dx = (dy - x*c) * rrms * gain
+    float pa = 0.f, pb = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxVec; k++) {
+      const int i = lane + 64 * k;
+      if (i >= nv) continue;
+      float o[4] = {(dy[k].x - xv[k].x * c) * rrms * gv[k].x, (dy[k].y - xv[k].y * c) * rrms * gv[k].y,
+                    (dy[k].z - xv[k].z * c) * rrms * gv[k].z, (dy[k].w - xv[k].w * c) * rrms * gv[k].w};
+      if (a.dgain_part) {
+        dg[k].x += dy[k].x * xv[k].x * rrms;
+        dg[k].y += dy[k].y * xv[k].y * rrms;
+        dg[k].z += dy[k].z * xv[k].z * rrms;
+        dg[k].w += dy[k].w * xv[k].w * rrms;
+      }
+      if (a.addend) {
+        const float4 ad = reinterpret_cast<const float4*>(a.addend + ro)[i];
+        const float av[4] = {ad.x, ad.y, ad.z, ad.w};
+#pragma unroll
+        for (int u = 0; u < 4; u++) o[u] += alpha * av[u];
+        if (a.lam_x) {
+          const float4 lx = reinterpret_cast<const float4*>(a.lam_x + ro)[i];
+          pa += av[0] * lx.x + av[1] * lx.y + av[2] * lx.z + av[3] * lx.w;
+        }
+        if (a.lam_x0) {
+          const float4 lx = reinterpret_cast<const float4*>(a.lam_x0 + ro)[i];
+          pb += av[0] * lx.x + av[1] * lx.y + av[2] * lx.z + av[3] * lx.w;
+        }
+        if (a.gx0) {
+          float4* gp = reinterpret_cast<float4*>(a.gx0 + ro) + i;
+          float4 gg = *gp;
+          gg.x += xl * av[0]; gg.y += xl * av[1]; gg.z += xl * av[2]; gg.w += xl * av[3];
+          *gp = gg;
+        }
+      }
+      if (a.addend2) {
+        const float4 ad = reinterpret_cast<const float4*>(a.addend2 + ro)[i];
+        o[0] += ad.x; o[1] += ad.y; o[2] += ad.z; o[3] += ad.w;
+      }
+      if (a.ve_dx && i < 3) {  // channels 0..11 = float4 groups 0..2
+#pragma unroll
+        for (int u = 0; u < 4; u++) o[u] += a.ve_dx[(size_t)t * 12 + 4 * i + u];
+      }
+      reinterpret_cast<float4*>(a.out + ro)[i] = make_float4(o[0], o[1], o[2], o[3]);
+      if (a.out_h) {
+        half4 hv;
+#pragma unroll
+        for (int u = 0; u < 4; u++) hv[u] = (half_t)o[u];
+        reinterpret_cast<half4*>(a.out_h + ro)[i] = hv;
+      }
+    }
+    la += (double)pa;
+    lb += (double)pb;
+  }
+  if (a.dgain_part) {
+#pragma unroll
+    for (int k = 0; k < kMaxVec; k++) {
+      const int i = lane + 64 * k;
+      if (i < nv) {
+        gsh[wave][4 * i] = dg[k].x; gsh[wave][4 * i + 1] = dg[k].y;
+        gsh[wave][4 * i + 2] = dg[k].z; gsh[wave][4 * i + 3] = dg[k].w;
+      }
+    }
+  }
+  if (a.lam_part) {
+    la = wave_sum_d(la);
+    lb = wave_sum_d(lb);
+    if (lane == 0) { lsh[wave][0] = la; lsh[wave][1] = lb; }
+  }
+  __syncthreads();
+  if (a.dgain_part)
+    for (int i = threadIdx.x; i < D; i += 256)
+      a.dgain_part[(size_t)blockIdx.x * D + i] = gsh[0][i] + gsh[1][i] + gsh[2][i] + gsh[3][i];
+  if (a.lam_part && threadIdx.x < 2)
+    a.lam_part[blockIdx.x * 2 + threadIdx.x] =
+        lsh[0][threadIdx.x] + lsh[1][threadIdx.x] + lsh[2][threadIdx.x] + lsh[3][threadIdx.x];
+}
+
+__global__ void reduce_partials_kernel(float* dst, const float* part, int nblocks, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float s = 0.f;
+  for (int b = 0; b < nblocks; b++) s += part[(size_t)b * n + i];
+  dst[i] += s;
+}
+
+__global__ __launch_bounds__(256) void reduce_dots_kernel(float* d0, float* d1, const double* part, int nblocks,
+                                                          float sign) {
+  __shared__ double sh[2][256];
+  double s0 = 0.0, s1 = 0.0;
+  for (int b = threadIdx.x; b < nblocks; b += 256) {
+    s0 += part[2 * b];
+    s1 += part[2 * b + 1];
+  }
+  sh[0][threadIdx.x] = s0;
+  sh[1][threadIdx.x] = s1;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) {
+      sh[0][threadIdx.x] += sh[0][threadIdx.x + o];
+      sh[1][threadIdx.x] += sh[1][threadIdx.x + o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    if (d0) *d0 += (float)(sign * sh[0][0]);
+    if (d1) *d1 += (float)(sign * sh[1][0]);
+  }
+}
+
+__global__ __launch_bounds__(256) void backout_bwd_kernel(float* ginj, double* part, const float* d, const float* xm,
+                                                          const float* lam_p, size_t n) {
+  __shared__ double sh[256];
+  const float lam = *lam_p;
+  double acc = 0.0;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    acc += (double)(d[i] * xm[i]);
+    ginj[i] = -lam * d[i];
+  }
+  sh[threadIdx.x] = acc;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) { part[2 * blockIdx.x] = sh[0]; part[2 * blockIdx.x + 1] = 0.0; }
+}
+
+__global__ void backout_fwd_kernel(float* out, const float* x, const float* xm, const float* lam_p, size_t n) {
+  const float lam = *lam_p;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+    out[i] = x[i] - lam * xm[i];
+}
+
+__global__ void axpy_kernel(float* y, const float* x, half_t* yh, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    const float v = y[i] + x[i];
+    y[i] = v;
+    if (yh) yh[i] = (half_t)v;
+  }
+}
+
+__global__ __launch_bounds__(256) void smear_bwd_kernel(half_t* dgp, float* dout2, double* part, const float* dy,
+                                                        const float* gact, const float* x0, const float* lam_p, int T,
+                                                        int D, int seq) {
+  __shared__ double sh[256];
+  const float lam = *lam_p;
+  const size_t n = (size_t)T * D;
+  double acc = 0.0;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const int t = (int)(i / D);
+    const bool first = (t % seq) == 0, last = (t % seq) == seq - 1;
+    const float g = gact[i], y = dy[i];
+    const float s = first ? 0.f : x0[i - D];
+    acc += (double)(y * g * s);
+    dgp[i] = (half_t)(y * lam * s * g * (1.f - g));
+    float o = y;
+    if (!last) o += dy[i + D] * lam * gact[i + D];
+    dout2[i] = o;
+  }
+  sh[threadIdx.x] = acc;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) { part[2 * blockIdx.x] = sh[0]; part[2 * blockIdx.x + 1] = 0.0; }
+}
+
+__global__ __launch_bounds__(256) void embed_bwd_kernel(float* G, const float* dx, const uint16_t* tok, int T, int D,
+                                                        int V) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const int tk = tok[t];
+  if (tk >= V) return;
+  float* gr = G + (size_t)tk * D;
+  const float* xr = dx + (size_t)t * D;
+  for (int i = lane; i < D; i += 64) atomicAdd(gr + i, xr[i]);
+}
+
+// one wave per token; lane = dim within a head, loop over heads
+__global__ __launch_bounds__(256) void ve_bwd_kernel(float* gemb, float* ggate, float* ve_dx, const half_t* dv,
+                                                     int ldv, const float* x, const float* emb, const float* vg,
+                                                     const uint16_t* tok, int T, int D, int NH, int V) {
+  __shared__ float gsh[4][16 * 12];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + wave;
+  for (int i = lane; i < NH * 12; i += 64) gsh[wave][i] = 0.f;
+  if (t < T) {
+    const int tk = tok[t];
+    const float* xr = x + (size_t)t * D;
+    float xc[12];
+#pragma unroll
+    for (int c = 0; c < 12; c++) xc[c] = xr[c];
+    float dxc[12];
+#pragma unroll
+    for (int c = 0; c < 12; c++) dxc[c] = 0.f;
+    for (int h = 0; h < NH; h++) {
+      float gp = 0.f;
+#pragma unroll
+      for (int c = 0; c < 12; c++) gp += vg[h * 12 + c] * xc[c];
+      const float act = (float)(1.0 / (1.0 + exp(-(double)gp)));
+      const float gate = 3.0f * act;
+      const float dvd = (float)dv[(size_t)t * ldv + h * 64 + lane];
+      const float ev = tk < V ? emb[(size_t)tk * D + h * 64 + lane] : 0.f;
+      if (tk < V) atomicAdd(gemb + (size_t)tk * D + h * 64 + lane, dvd * gate);
+      const float dg = wave_sum(dvd * ev);
+      const float dgp = dg * 3.0f * act * (1.f - act);
+      if (lane < 12) gsh[wave][h * 12 + lane] = dgp * xc[lane];
+#pragma unroll
+      for (int c = 0; c < 12; c++) dxc[c] += dgp * vg[h * 12 + c];
+    }
+    if (lane < 12) ve_dx[(size_t)t * 12 + lane] = dxc[lane];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < NH * 12; i += 256)
+    atomicAdd(ggate + i, gsh[0][i] + gsh[1][i] + gsh[2][i] + gsh[3][i]);
+}
+
+__global__ void fill_kernel(float* p, size_t n, float v) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+__global__ __launch_bounds__(256) void sumsq_kernel(double* part, const float* g, size_t n) {
+  __shared__ double sh[256];
+  double acc = 0.0;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const double f = g[i];
+    acc += f * f;
+  }
+  sh[threadIdx.x] = acc;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = sh[0];
+}
+
+__global__ __launch_bounds__(256) void sumsq_final_kernel(double* out, const double* part, int n) {
+  __shared__ double sh[256];
+  double acc = 0.0;
+  for (int i = threadIdx.x; i < n; i += 256) acc += part[i];
+  sh[threadIdx.x] = acc;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (threadIdx.x < o) sh[threadIdx.x] += sh[threadIdx.x + o];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out = sh[0];
+}
+
+__global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
+  const AdamSeg& sg = a.seg[blockIdx.y];
+  float cf = 1.f;
+  if (sg.clip && a.clip > 0.f) {
+    const double n2 = *a.sumsq * (double)a.gscale * (double)a.gscale;
+    if (n2 > 0.0) {
+      const float norm = (float)sqrt(n2);
+      if (norm > a.clip) cf = a.clip / norm;
+    }
+  }
+  const float gs = a.gscale;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < sg.len; i += (int64_t)gridDim.x * 256) {
+    const int64_t k = sg.off + i;
+    float g = a.g[k] * gs;
+    g *= cf;
+    const float m = sg.b1 * a.m[k] + (1.f - sg.b1) * g;
+    const float v = sg.b2 * a.v[k] + (1.f - sg.b2) * g * g;
+    a.m[k] = m;
+    a.v[k] = v;
+    const float mh = m * sg.i1, vh = v * sg.i2;
+    float upd = mh / (sqrtf(vh) + a.eps);
+    if (sg.wd != 0.f) upd += sg.wd * a.w[k];
+    a.w[k] -= sg.lr * upd;
+  }
+}
+
+inline int flat_grid(size_t n, int cap = 4096) {
+  size_t g = (n + 255) / 256;
+  return (int)(g > (size_t)cap ? cap : (g == 0 ? 1 : g));
+}
+
+}  // namespace
+
+hipError_t norm_bwd(const NormBwdArgs& a, hipStream_t s) {
+  if (a.D % 64 || a.D > 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(norm_bwd_kernel, dim3(norm_bwd_blocks(a.T)), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t reduce_partials_add(float* dst, const float* part, int nblocks, int n, hipStream_t s) {
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((n + 255) / 256), dim3(256), 0, s, dst, part, nblocks, n);
+  return hipGetLastError();
+}
+
+hipError_t reduce_dots_add(float* d0, float* d1, const double* part, int nblocks, float sign, hipStream_t s) {
+  hipLaunchKernelGGL(reduce_dots_kernel, dim3(1), dim3(256), 0, s, d0, d1, part, nblocks, sign);
+  return hipGetLastError();
+}
+
+hipError_t backout_bwd(float* ginj, double* part, const float* d, const float* xmid, const float* lam_p, int T, int D,
+                       hipStream_t s) {
+  hipLaunchKernelGGL(backout_bwd_kernel, dim3(256), dim3(256), 0, s, ginj, part, d, xmid, lam_p, (size_t)T * D);
+  return hipGetLastError();
+}
+
+hipError_t backout_fwd(float* out, const float* x, const float* xm, const float* lam_p, size_t n, hipStream_t s) {
+  hipLaunchKernelGGL(backout_fwd_kernel, dim3(flat_grid(n)), dim3(256), 0, s, out, x, xm, lam_p, n);
+  return hipGetLastError();
+}
+
+hipError_t axpy_inplace(float* y, const float* x, half_t* yh, size_t n, hipStream_t s) {
+  hipLaunchKernelGGL(axpy_kernel, dim3(flat_grid(n)), dim3(256), 0, s, y, x, yh, n);
+  return hipGetLastError();
+}
+
+hipError_t smear_bwd_prep(half_t* dgp, float* dout2, double* part, const float* dy, const float* gact,
+                          const float* x0, const float* lam_p, int T, int D, int seq, hipStream_t s) {
+  hipLaunchKernelGGL(smear_bwd_kernel, dim3(256), dim3(256), 0, s, dgp, dout2, part, dy, gact, x0, lam_p, T, D, seq);
+  return hipGetLastError();
+}
+
+hipError_t embed_bwd(float* G, const float* dx, const uint16_t* tok, int T, int D, int V, hipStream_t s) {
+  hipLaunchKernelGGL(embed_bwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, G, dx, tok, T, D, V);
+  return hipGetLastError();
+}
+
+hipError_t ve_bwd(float* gemb, float* ggate, float* ve_dx, const half_t* dv, int ldv, const float* x, const float* emb,
+                  const float* vg, const uint16_t* tok, int T, int D, int NH, int V, hipStream_t s) {
+  if (NH > 16) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(ve_bwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, gemb, ggate, ve_dx, dv, ldv, x, emb, vg, tok,
+                     T, D, NH, V);
+  return hipGetLastError();
+}
+
+hipError_t fill_f32(float* p, size_t n, float v, hipStream_t s) {
+  hipLaunchKernelGGL(fill_kernel, dim3(flat_grid(n)), dim3(256), 0, s, p, n, v);
+  return hipGetLastError();
+}
+
+hipError_t sumsq(double* out, double* part, const float* g, size_t n, hipStream_t s) {
+  hipLaunchKernelGGL(sumsq_kernel, dim3(256), dim3(256), 0, s, part, g, n);
+  hipLaunchKernelGGL(sumsq_final_kernel, dim3(1), dim3(256), 0, s, out, part, 256);
+  return hipGetLastError();
+}
+
+hipError_t adam_update(const AdamArgs& a, hipStream_t s) {
+  if (a.nseg <= 0 || a.nseg > kMaxAdamSegs) return hipErrorInvalidValue;
+  int64_t mx = 1;
+  for (int i = 0; i < a.nseg; i++) mx = a.seg[i].len > mx ? a.seg[i].len : mx;
+  hipLaunchKernelGGL(adam_kernel, dim3(flat_grid((size_t)mx, 2048), a.nseg), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+}  // namespace ane

@@ -142,6 +142,45 @@ int ane_eval_loss(ane_engine *e, const uint16_t *tokens, const uint16_t *targets
 int ane_eval_loss_windows(ane_engine *e, const uint64_t *positions, int32_t nseq, float *loss_per_seq,
                           float *mean_loss);
 
+/* ---- training ------------------------------------------------------------ */
+
+/* Step (ane/engine.go:381-442): draws one window from the resident token
+ * stream with the drand48 sampler (seeded from Options.Seed, ane/engine.go:
+ * 395-405, 873-880), runs forward + backward, accumulates the loss-scaled
+ * gradients, and applies clipping + AdamW once AccumSteps windows are
+ * pending (flushPending, ane/engine.go:646-682).  Errors: ANE_ERR_STATE with
+ * "storiesane step: not enough tokens" when no stream is set.  Training
+ * kernels support seq <= 256. */
+int ane_step(ane_engine *e, ane_step_result *res);
+/* nseq consecutive Steps fused into one batched forward/backward (same
+ * windows, same update; no reference counterpart: the reference runs one
+ * sequence per call).  res->loss is the mean over the nseq windows. */
+int ane_train_batch(ane_engine *e, int32_t nseq, ane_step_result *res);
+/* Flush (ane/engine.go:484-496): applies pending accumulated gradients;
+ * *ns receives the wall time. */
+int ane_flush(ane_engine *e, int64_t *ns);
+/* LR / SetLR (ane/engine.go:358-376); SetLR rejects lr <= 0 with
+ * "storiesane set lr: lr must be > 0". */
+float ane_lr(const ane_engine *e);
+int ane_set_lr(ane_engine *e, float lr);
+/* State / LoadState (ane/engine.go:498-513). */
+int ane_get_state(ane_engine *e, ane_state *out);
+int ane_load_state(ane_engine *e, const ane_state *s);
+
+/* Gradient of the mean loss over nseq explicit sequences (the flushed
+ * gradient the reference's Adam would see for these windows: loss-scaled
+ * sum divided by nseq * lossScale, before clipping).  Leaves weights and
+ * optimizer state untouched; fails with ANE_ERR_STATE while steps are
+ * pending.  No reference counterpart (parity / diagnostics). */
+int ane_grads(ane_engine *e, const uint16_t *tokens, const uint16_t *targets, int32_t nseq, float *grads,
+              float *mean_loss);
+/* Replaces the accumulated (loss-scaled) gradient sum and the pending step
+ * count, e.g. to apply an externally computed gradient with ane_flush().
+ * No reference counterpart (optimizer parity tests). */
+int ane_set_grads(ane_engine *e, const float *grads, int64_t n, uint32_t pending);
+/* Reads the AdamW moments (OptimState, ane/stories/cpu.go:294-301). */
+int ane_get_opt_state(ane_engine *e, float *m, float *v, int64_t n);
+
 /* ---- diagnostics -------------------------------------------------------- */
 
 /* Per-kernel-class device timing with HIP events on the engine's stream.
@@ -169,12 +208,13 @@ int ane_sync(ane_engine *e);
  * [M, K], B stored [K, N] when b_t else [N, K] (fp16 bit patterns); C is
  * [M, N] fp32 (epi 1) or fp16 (epi 0); bm/bn force a block tile (0 = auto).
  * ane_debug_attention: causal attention over qkv [nseq*S, 3*64*NH] (fp16,
- * q|k|v per row, pre-RoPE) -> out [nseq*S, 64*NH] fp16 and lse [nseq*S, NH].
+ * q|k|v per row, pre-RoPE) with score scale `scale` (hilo: split-operand
+ * scores) -> out [nseq*S, 64*NH] fp16 and lse [nseq*S, NH].
  * Messages: ane_debug_last_error(). */
 int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_t *A, const uint16_t *B,
                    void *C, int bm, int bn);
-int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, const uint16_t *qkv, uint16_t *out,
-                        float *lse);
+int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float scale, int hilo,
+                        const uint16_t *qkv, uint16_t *out, float *lse);
 /* Mean time of `iters` launches of one GEMM on device-resident operands. */
 int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int iters,
                          float *avg_ms);

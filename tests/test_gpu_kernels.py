@@ -61,7 +61,7 @@ def test_gemm_real_shapes_auto_tile():
     np.testing.assert_allclose(got16.astype(np.float64), ref, rtol=2e-3, atol=1e-3)
 
 
-def attn_ref(qkv, nseq, S, NH, qknorm, theta):
+def attn_ref(qkv, nseq, S, NH, qknorm, theta, scale=0.125):
     x = qkv.astype(np.float64).reshape(nseq, S, 3, NH, 64)
     q, k, v = x[:, :, 0], x[:, :, 1], x[:, :, 2]
     ang = np.arange(S)[:, None] / theta ** (2 * np.arange(32)[None, :] / 64)
@@ -78,7 +78,7 @@ def attn_ref(qkv, nseq, S, NH, qknorm, theta):
     if qknorm:
         q = 1.2 * q / np.sqrt((q * q).mean(-1, keepdims=True) + 1e-5)
         k = 1.2 * k / np.sqrt((k * k).mean(-1, keepdims=True) + 1e-5)
-    sc = np.einsum("bshd,bthd->bhst", q, k) / 8.0
+    sc = np.einsum("bshd,bthd->bhst", q, k) * scale
     sc = np.where(np.tril(np.ones((S, S), bool))[None, None], sc, -np.inf)
     mx = sc.max(-1, keepdims=True)
     p = np.exp(sc - mx)
@@ -98,7 +98,7 @@ def test_attention_matches_f64(S, NH, nseq, qknorm):
     out = np.zeros((nseq * S, D), np.float16)
     lse = np.zeros((nseq * S, NH), np.float32)
     theta = 100000.0 if qknorm else 10000.0
-    rc = lib.ane_debug_attention(nseq, S, NH, int(qknorm), theta, _u16(qkv.view(np.uint16)),
+    rc = lib.ane_debug_attention(nseq, S, NH, int(qknorm), theta, 0.125, 0, _u16(qkv.view(np.uint16)),
                                  _u16(out.view(np.uint16)), lse.ctypes.data_as(C.POINTER(C.c_float)))
     assert rc == 0, lib.ane_debug_last_error()
     ref, ref_lse = attn_ref(qkv, nseq, S, NH, qknorm, theta)
@@ -108,3 +108,25 @@ def test_attention_matches_f64(S, NH, nseq, qknorm):
     # row 0 of every sequence attends only to itself: out = v[0]
     v0 = qkv.reshape(nseq, S, 3, D)[:, 0, 2].astype(np.float64)
     np.testing.assert_allclose(out.reshape(nseq, S, D)[:, 0].astype(np.float64), v0, atol=2e-3)
+
+
+def test_attention_split_scores_at_scale_1():
+    """The scale-1 recompute (the reference's backward probabilities) with
+    QK-norm: split hi+lo operands bring the log-sum-exp to ~fp32 accuracy,
+    plain fp16 operands do not."""
+    lib = _lib.load()
+    nseq, S, NH = 2, 256, 4
+    D = 64 * NH
+    qkv = np.random.default_rng(77).standard_normal((nseq * S, 3 * D)).astype(np.float16)
+    ref, ref_lse = attn_ref(qkv, nseq, S, NH, True, 100000.0, scale=1.0)
+    errs = {}
+    for hilo in (0, 1):
+        out = np.zeros((nseq * S, D), np.float16)
+        lse = np.zeros((nseq * S, NH), np.float32)
+        rc = lib.ane_debug_attention(nseq, S, NH, 1, 100000.0, 1.0, hilo, _u16(qkv.view(np.uint16)),
+                                     _u16(out.view(np.uint16)), lse.ctypes.data_as(C.POINTER(C.c_float)))
+        assert rc == 0, lib.ane_debug_last_error()
+        errs[hilo] = (np.abs(lse - ref_lse).max(), np.abs(out.astype(np.float64) - ref).max())
+    print("scale-1 (lse err, out err): fp16", errs[0], "split", errs[1])
+    assert errs[1][0] < 1e-3 and errs[1][1] < 4e-3
+    assert errs[1][0] < errs[0][0] / 5

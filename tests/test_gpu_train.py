@@ -1,0 +1,186 @@
+"""Backward + optimizer parity of the device engine against the CPU oracle.
+
+Weight gradients are compared per parameter tensor at relative L2 error
+<= 1e-2 (the contract's tolerance; fp16 activations and weights, fp32
+accumulation).  nanochat is checked in both gradient modes: `compat`
+reproduces the reference's backward (scale-1 attention recompute, no RoPE
+backward, 1.2^2 QK-norm coefficient, x0 gradient before smear), `true` is the
+exact gradient.  Scalar parameters (lambdas) are single sums over the whole
+activation tensor; they are held to 5e-2.
+"""
+import numpy as np
+import pytest
+
+import ane
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-2
+SCALAR_TOL = 5e-2
+HP = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=1.0, embed_lr_mult=2.0,
+          scalar_lr_mult=0.5, lambda_lr_mult=0.01, lambda_beta1=0.96, lambda_beta2=0.97)
+
+
+def open_engine(cfg, params, max_batch=1, tokens=None, **kw):
+    return ane.Open(ane.Options(Config=cfg, Params=params, MaxBatch=max_batch, Tokens=tokens, **kw))
+
+
+def seg_errors(cfg, g, ref):
+    out = {}
+    for name, off, shape in ane.param_layout(cfg):
+        n = int(np.prod(shape))
+        a, b = g[off:off + n].astype(np.float64), ref[off:off + n].astype(np.float64)
+        out[name] = np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30)
+    return out
+
+
+def check_grads(cfg, g, ref):
+    errs = seg_errors(cfg, g, ref)
+    worst = sorted(errs.items(), key=lambda kv: -kv[1])[:5]
+    print(f"{cfg.arch}/{cfg.grad_mode}: worst rel L2 {[(k, f'{v:.2e}') for k, v in worst]}")
+    for name, err in errs.items():
+        tol = SCALAR_TOL if name.split(".")[-1] in ("resid_lambdas", "x0_lambdas", "smear_lambda",
+                                                     "backout_lambda", "ve_gate") else REL_TOL
+        assert err <= tol, (name, err)
+
+
+@pytest.mark.parametrize("arch,mode", [("llama2", "true"), ("nanochat", "compat"), ("nanochat", "true")])
+def test_tiny_grads_match_oracle(arch, mode):
+    cfg = ane.tiny(arch, layers=4, grad_mode=mode)
+    p = ane.init_params(cfg, seed=21, std=0.08)
+    tok, tgt = ane.make_tokens(cfg, 3, seed=22)
+    loss_ref, g_ref = oracle.grads(cfg, p, tok, tgt)
+    eng = open_engine(cfg, p, max_batch=3)
+    loss, g = eng.Grads(tok, tgt)
+    eng.Destroy()
+    assert abs(loss - loss_ref) <= 1e-3
+    check_grads(cfg, g, g_ref)
+
+
+@pytest.mark.parametrize("arch,mode", [("llama2", "true"), ("nanochat", "compat")])
+def test_full_size_grads_match_oracle(arch, mode):
+    """BASELINE config 3 shape per sequence (stories110M, seq 256)."""
+    cfg = ane.stories110m(arch, grad_mode=mode)
+    p = ane.init_params(cfg, seed=0)
+    tok, tgt = ane.make_tokens(cfg, 1, seed=3)
+    loss_ref, g_ref = oracle.grads(cfg, p, tok, tgt)
+    eng = open_engine(cfg, p, max_batch=1)
+    loss, g = eng.Grads(tok, tgt)
+    eng.Destroy()
+    assert abs(loss - loss_ref) <= 1e-3
+    check_grads(cfg, g, g_ref)
+
+
+@pytest.mark.parametrize("arch", ["llama2", "nanochat"])
+def test_flush_matches_oracle_adam(arch):
+    """Clip + AdamW with the reference's parameter groups, two flushes."""
+    cfg = ane.tiny(arch, layers=2)
+    n = ane.param_count(cfg)
+    r = np.random.default_rng(30)
+    p = ane.init_params(cfg, seed=31, std=0.08)
+    eng = open_engine(cfg, p, AccumSteps=2, LR=HP["lr"], AdamBeta1=HP["beta1"], AdamBeta2=HP["beta2"],
+                      AdamEps=HP["eps"], WeightDecay=HP["weight_decay"], GradClip=HP["grad_clip"],
+                      EmbedLRMult=HP["embed_lr_mult"], ScalarLRMult=HP["scalar_lr_mult"],
+                      LambdaLRMult=HP["lambda_lr_mult"], LambdaBeta1=HP["lambda_beta1"],
+                      LambdaBeta2=HP["lambda_beta2"])
+    w_ref = p.copy()
+    m_ref = np.zeros(n, np.float32)
+    v_ref = np.zeros(n, np.float32)
+    for step in (1, 2):
+        raw = (r.standard_normal(n) * 3.0).astype(np.float32)   # loss-scaled sum over 2 pending steps
+        eng.SetGrads(raw, pending=2)
+        eng.Flush()
+        g = raw * np.float32(1.0 / 2.0) / np.float32(256.0)
+        oracle.adam_update(cfg, w_ref, g, m_ref, v_ref, step, HP)
+        st = eng.State()
+        assert st.adam_t == step and st.pending_steps == 0 and st.cum_batches == step
+    w = eng.Params()
+    m, v = eng.OptState()
+    eng.Destroy()
+    np.testing.assert_allclose(m, m_ref, rtol=1e-5, atol=1e-9)
+    np.testing.assert_allclose(v, v_ref, rtol=1e-5, atol=1e-12)
+    np.testing.assert_allclose(w, w_ref, rtol=1e-5, atol=1e-7)
+
+
+def drand48_positions(seed, n, limit):
+    st = oracle.lib().orc_drand48_seed(seed)
+    import ctypes
+    s = ctypes.c_uint64(st)
+    out = []
+    for _ in range(n):
+        f = oracle.lib().orc_drand48_next(ctypes.byref(s))
+        p = int(f * limit)
+        out.append(min(p, limit - 1))
+    return out
+
+
+def test_steps_follow_reference_sampler_and_batch_equivalence():
+    """Step draws windows with the reference's drand48 rule; TrainBatch(k)
+    equals k Steps; AccumSteps accumulation flushes once per k windows."""
+    cfg = ane.tiny("llama2", layers=2)
+    p = ane.init_params(cfg, seed=40, std=0.08)
+    stream = np.random.default_rng(41).integers(0, cfg.vocab, 3000).astype(np.uint16)
+    kw = dict(AccumSteps=4, Seed=7, LR=1e-3, AdamBeta2=0.95, GradClip=1.0)
+    a = open_engine(cfg, p, max_batch=4, tokens=stream, **kw)
+    b = open_engine(cfg, p, max_batch=4, tokens=stream, **kw)
+    limit = len(stream) - cfg.seq - 1
+    pos = drand48_positions(7, 8, limit)
+    for i in range(4):
+        a.Step()
+        assert a.State().token_pos == pos[i] + cfg.seq
+    sa = a.State()
+    assert sa.cum_steps == 4 and sa.adam_t == 1 and sa.pending_steps == 0 and sa.cum_batches == 1
+    b.TrainBatch(4)
+    sb = b.State()
+    assert sb.token_pos == sa.token_pos and sb.adam_t == 1 and sb.cum_steps == 4
+    np.testing.assert_allclose(a.Params(), b.Params(), rtol=1e-4, atol=2e-6)
+    # the update itself equals oracle grads of those windows + AdamW
+    tok = np.stack([stream[q:q + cfg.seq] for q in pos[:4]])
+    tgt = np.stack([stream[q + 1:q + 1 + cfg.seq] for q in pos[:4]])
+    _, g = oracle.grads(cfg, p, tok, tgt)
+    w_ref = p.copy()
+    n = ane.param_count(cfg)
+    hp = dict(HP, lr=1e-3, beta2=0.95, weight_decay=0.0, grad_clip=1.0, embed_lr_mult=1.0, scalar_lr_mult=1.0,
+              lambda_lr_mult=0.01, lambda_beta1=0.9, lambda_beta2=0.95)
+    oracle.adam_update(cfg, w_ref, g, np.zeros(n, np.float32), np.zeros(n, np.float32), 1, hp)
+    # Adam's first step is lr * g / (|g| + eps) ~ lr * sign(g): coordinates
+    # whose gradient is at rounding level may flip, so the check is on sign
+    # agreement weighted by the oracle's gradient magnitude.
+    dw_ref = w_ref - p
+    dw = b.Params() - p
+    agree = np.sign(dw) == np.sign(dw_ref)
+    wagree = np.abs(g[agree]).sum() / np.abs(g).sum()
+    print(f"update sign agreement {agree.mean():.4f}, |g|-weighted {wagree:.6f}")
+    assert wagree >= 0.999 and agree.mean() >= 0.95
+    a.Destroy()
+    b.Destroy()
+
+
+def test_training_reduces_loss():
+    cfg = ane.tiny("nanochat", layers=2)
+    p = ane.init_params(cfg, seed=50, std=0.05)
+    stream = np.tile(np.random.default_rng(51).integers(0, cfg.vocab, 200).astype(np.uint16), 5)
+    eng = open_engine(cfg, p, max_batch=4, tokens=stream, AccumSteps=4, LR=3e-3, AdamBeta2=0.95)
+    first = eng.TrainBatch(4).loss
+    for _ in range(25):
+        last = eng.TrainBatch(4).loss
+    eng.Destroy()
+    print(f"loss {first:.3f} -> {last:.3f}")
+    assert last < first - 0.5
+
+
+def test_training_error_behaviour():
+    cfg = ane.tiny("llama2", layers=2)
+    p = ane.init_params(cfg, seed=60)
+    eng = open_engine(cfg, p)
+    with pytest.raises(ane.EngineError, match="storiesane step: not enough tokens"):
+        eng.Step()
+    with pytest.raises(ane.EngineError, match="storiesane set lr: lr must be > 0"):
+        eng.SetLR(0.0)
+    eng.SetLR(1e-3)
+    assert abs(eng.LR() - 1e-3) < 1e-9
+    eng.Close()
+    with pytest.raises(ane.EngineError, match="storiesane step: engine is closed"):
+        eng.Step()
+    eng.Destroy()
