@@ -88,11 +88,11 @@ SIGNATURES = {
     "ane_profile_read": (C.c_int, [_eng, C.POINTER(ProfEntry), C.c_int, C.c_int]),
     "ane_sync": (C.c_int, [_eng]),
     "ane_debug_gemm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _u16, _u16, C.c_void_p,
-                                 C.c_int, C.c_int]),
+                                 C.c_int, C.c_int, C.c_int, C.c_int]),
     "ane_debug_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, C.c_float, C.c_int, _u16,
                                       _u16, _fp]),
     "ane_debug_last_error": (C.c_char_p, []),
-    "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 9 + [_fp]),
+    "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 11 + [_fp]),
 }
 
 _lib = None

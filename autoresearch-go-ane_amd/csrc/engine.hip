@@ -537,11 +537,16 @@ int head_loss(ane_engine* e, int nseq, float* colscale, float dscale) {
   EpiParams p;
   p.targets = e->tgt; p.partial = e->partial; p.tgt_logit = e->tgt_logit;
   p.softcap = c.arch == ANE_ARCH_NANOCHAT; p.cap = 15.f; p.vocab = V;
-  HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_CE, p, e->ce_bm, 0));
+  // block rows: 256 (8-wave 256x256 tiles) once that still gives >= 512
+  // blocks, else the open-time size; the partial buffer holds V / ce_bm rows
+  int bm = e->ce_bm, bn = 0;
+  if (V % 256 == 0 && T % 256 == 0 && (long)(V / 256) * (T / 256) >= 512) bm = bn = 256;
+  const int np = V / bm;
+  HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_CE, p, bm, bn));
   prof_begin(e, 7);
-  HIPCHK(op, ce_reduce(e->loss_seq, e->lse, e->tok_loss, colscale, dscale, e->partial, e->ce_np, e->tgt_logit, e->tgt, V, nseq,
+  HIPCHK(op, ce_reduce(e->loss_seq, e->lse, e->tok_loss, colscale, dscale, e->partial, np, e->tgt_logit, e->tgt, V, nseq,
                        S, e->stream));
-  prof_end(e, 0, (double)e->ce_np * T * 8);
+  prof_end(e, 0, (double)np * T * 8);
   return ANE_OK;
 }
 
@@ -665,7 +670,7 @@ static int debug_fail(const char* what, hipError_t h) {
 extern "C" const char* ane_debug_last_error(void) { return g_debug_err.c_str(); }
 
 extern "C" int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_t* A, const uint16_t* B,
-                              void* C, int bm, int bn) {
+                              void* C, int bm, int bn, int nw, int ns) {
   if (epi != EPI_STORE_F && epi != EPI_STORE_H) {
     g_debug_err = "storiesane debug: epilogue must be STORE_F or STORE_H";
     return ANE_ERR_ARG;
@@ -684,7 +689,7 @@ extern "C" int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, co
   g.lda = a_t ? M : K; g.ldb = b_t ? N : K;
   g.M = M; g.N = N; g.K = K; g.a_t = a_t != 0; g.b_t = b_t != 0;
   p.C = dC; p.ldc = N;
-  DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn));
+  DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn, nw, ns));
   DBGCHK(hipDeviceSynchronize());
   DBGCHK(hipMemcpy(C, dC, (size_t)M * N * esz, hipMemcpyDeviceToHost));
 done:
@@ -694,10 +699,19 @@ done:
   return rc;
 }
 
+__global__ void debug_fill_kernel(half_t* p, size_t n, uint32_t seed) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+    uint32_t x = (uint32_t)i * 2654435761u ^ seed;
+    x ^= x >> 15; x *= 2246822519u; x ^= x >> 13;
+    p[i] = (half_t)(((float)(x & 0xffff) / 65536.0f - 0.5f));
+  }
+}
+
 // Times `iters` launches of one GEMM (device-resident operands filled with
-// small values) with HIP events; *avg_ms receives the mean launch time.
-extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int iters,
-                                    float* avg_ms) {
+// pseudo-random values in [-0.5, 0.5)) with HIP events; *avg_ms receives
+// the mean launch time.
+extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw,
+                                    int ns, int iters, float* avg_ms) {
   if (epi != EPI_STORE_F && epi != EPI_STORE_H) {
     g_debug_err = "storiesane debug: epilogue must be STORE_F or STORE_H";
     return ANE_ERR_ARG;
@@ -711,18 +725,19 @@ extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int
   DBGCHK(hipMalloc(&dA, (size_t)M * K * 2));
   DBGCHK(hipMalloc(&dB, (size_t)N * K * 2));
   DBGCHK(hipMalloc(&dC, (size_t)M * N * (epi == EPI_STORE_F ? 4 : 2)));
-  DBGCHK(hipMemset(dA, 0x11, (size_t)M * K * 2));
-  DBGCHK(hipMemset(dB, 0x11, (size_t)N * K * 2));
+  hipLaunchKernelGGL(debug_fill_kernel, dim3(1024), dim3(256), 0, nullptr, (half_t*)dA, (size_t)M * K, 1u);
+  hipLaunchKernelGGL(debug_fill_kernel, dim3(1024), dim3(256), 0, nullptr, (half_t*)dB, (size_t)N * K, 2u);
+  DBGCHK(hipGetLastError());
   DBGCHK(hipEventCreate(&e0));
   DBGCHK(hipEventCreate(&e1));
   g.A = (const half_t*)dA; g.B = (const half_t*)dB;
   g.lda = a_t ? M : K; g.ldb = b_t ? N : K;
   g.M = M; g.N = N; g.K = K; g.a_t = a_t != 0; g.b_t = b_t != 0;
   p.C = dC; p.ldc = N;
-  DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn));
+  DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn, nw, ns));
   DBGCHK(hipDeviceSynchronize());
   DBGCHK(hipEventRecord(e0, nullptr));
-  for (int i = 0; i < iters; i++) DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn));
+  for (int i = 0; i < iters; i++) DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn, nw, ns));
   DBGCHK(hipEventRecord(e1, nullptr));
   DBGCHK(hipEventSynchronize(e1));
   DBGCHK(hipEventElapsedTime(&ms, e0, e1));

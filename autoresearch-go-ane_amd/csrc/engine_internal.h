@@ -124,7 +124,7 @@ struct ane_engine {
   ane::half_t* qkv = nullptr;
   ane::half_t* att = nullptr;
   ane::half_t* gate = nullptr;
-  int ce_bm = 256, ce_np = 0;
+  int ce_bm = 256, ce_np = 0;  // smallest classifier block row and the partial rows it needs
   float2* partial = nullptr;
   float* tgt_logit = nullptr;
   float* lse = nullptr;

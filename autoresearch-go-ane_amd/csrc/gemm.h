@@ -64,9 +64,12 @@ struct EpiParams {
   float* C3 = nullptr;                // second fp32 output (EPI_STORE_W13: W3 grad)
 };
 
-// Launches one GEMM on `stream`.  bm/bn force a block tile (0 = heuristic).
+// Launches one GEMM on `stream`.  bm/bn force a block tile (0 = heuristic);
+// nw = waves per block: 4 (default) or 8 (256x256 tiles only).
+// ns = LDS pipeline stages: 2 (default) or 3 (K-major operands, 4 waves,
+// tiles 256x128, 128x128, 64x128, 128x64, 64x64).
 hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t stream,
-                    int bm = 0, int bn = 0);
+                    int bm = 0, int bn = 0, int nw = 0, int ns = 0);
 
 // Tile the heuristic picks; nonzero *bm / *bn on entry are kept as
 // constraints (set both to 0 for a free choice).  0 = no tile fits.

@@ -72,12 +72,13 @@ __device__ __forceinline__ void store_tmajor(half_t* tile, const half8 (&v)[8], 
 // slot l (row l/8, physical chunk l%8), so it fetches the logical chunk that
 // the swizzle maps to that slot (the XOR swizzle is its own inverse).
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
-template <int R>
+template <int R, int NW>
 __device__ __forceinline__ void load_direct(half_t* tile, const half_t* base, int ld, int row0, int k0, int tid) {
+  static_assert(R % (8 * NW) == 0, "each wave fills whole 8-row groups");
   const int lane = tid & 63, wave = tid >> 6;
 #pragma unroll
-  for (int it = 0; it < R / 32; it++) {
-    const int gi = wave + 4 * it;
+  for (int it = 0; it < R / (8 * NW); it++) {
+    const int gi = wave + NW * it;
     const int r = gi * 8 + (lane >> 3);
     const int lc = swz(r, lane & 7);
     const half_t* gp = base + (size_t)(row0 + r) * ld + k0 + lc * 8;
@@ -85,20 +86,21 @@ __device__ __forceinline__ void load_direct(half_t* tile, const half_t* base, in
   }
 }
 
-// Stage<R, transposed>: issue() starts the HBM reads of one k-tile, commit()
-// makes them LDS-resident (register path) -- the direct path has nothing to
-// commit; its completion is awaited by wait_tile() before the barrier.
-template <int R, bool T>
+// Stage<R, transposed, waves>: issue() starts the HBM reads of one k-tile,
+// commit() makes them LDS-resident (register path) -- the direct path has
+// nothing to commit; its completion is awaited by wait_tile() before the
+// barrier.
+template <int R, bool T, int NW>
 struct Stage;
-template <int R>
-struct Stage<R, false> {
+template <int R, int NW>
+struct Stage<R, false, NW> {
   __device__ __forceinline__ void issue(const half_t* b, int ld, int r0, int k0, half_t* tile, int tid) {
-    load_direct<R>(tile, b, ld, r0, k0, tid);
+    load_direct<R, NW>(tile, b, ld, r0, k0, tid);
   }
   __device__ __forceinline__ void commit(half_t*, int) const {}
 };
-template <int R>
-struct Stage<R, true> {
+template <int R, int NW>
+struct Stage<R, true, NW> {
   half8 v[8];
   __device__ __forceinline__ void issue(const half_t* b, int ld, int r0, int k0, half_t*, int tid) {
     load_tmajor<R>(v, b, ld, r0, k0, tid);
@@ -108,16 +110,39 @@ struct Stage<R, true> {
 
 __device__ __forceinline__ void wait_tile() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// s_waitcnt vmcnt(N) with the other counters left alone (gfx9 encoding:
+// vmcnt in bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8]).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without the release fence of __syncthreads(): for LDS
+// written by global_load_lds that fence makes the compiler drain vmcnt to 0,
+// which would also wait for the loads meant to stay in flight.  The caller
+// has waited for the loads it needs; LDS reads/writes are drained here.
+__device__ __forceinline__ void barrier_keep_loads() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float softcap_f(float v, float cap) { return cap * tanhf(v / cap); }
 
-template <int BM, int BN, bool AT, bool BT, int EPI>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
-  constexpr int TM = BM / 64, TN = BN / 64;
+// NW = 4: waves 2 x 2, one wave per SIMD.  NW = 8: waves 2 x 4, two waves
+// per SIMD, so one wave's barrier wait and LDS reads overlap the other's
+// MFMAs (wave tile (BM/2) x (BN/4)).  NS = LDS stages: with NS = 3 the
+// HBM->LDS loads run two k-tiles ahead of the MFMAs (K-major operands only).
+template <int BM, int BN, bool AT, bool BT, int EPI, int NW, int NS>
+__global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) {
+  constexpr int WN = NW / 2;                 // waves along N (2 along M)
+  constexpr int WTM = BM / 2, WTN = BN / WN; // wave tile
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TN >= 1 && TM >= 1, "wave tile must hold 32x32 MFMA tiles");
+  static_assert(NS == 2 || (NS == 3 && !AT && !BT), "3 stages need direct loads on both operands");
   constexpr int STAGE = (BM + BN) * BK;
-  __shared__ __attribute__((aligned(16))) half_t lds[2 * STAGE];
+  constexpr int LPT = (BM + BN) / (8 * NW);  // direct-load instructions per wave per k-tile
+  __shared__ __attribute__((aligned(16))) half_t lds[NS * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
 
   // block -> tile: spread consecutive tiles of one XCD over a contiguous
   // range (hardware deals block i to XCD i % 8), then walk groups of 8
@@ -141,29 +166,43 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-  Stage<BM, AT> sa;
-  Stage<BN, BT> sb;
+  Stage<BM, AT, NW> sa;
+  Stage<BN, BT, NW> sb;
   const int nk = g.K / BK;
-  sa.issue(g.A, g.lda, m0, 0, lds, tid);
-  sb.issue(g.B, g.ldb, n0, 0, lds + BM * BK, tid);
+#pragma unroll
+  for (int p = 0; p < NS - 1; p++) {
+    if (p < nk) {
+      sa.issue(g.A, g.lda, m0, p * BK, lds + p * STAGE, tid);
+      sb.issue(g.B, g.ldb, n0, p * BK, lds + p * STAGE + BM * BK, tid);
+    }
+  }
   sa.commit(lds, tid);
   sb.commit(lds + BM * BK, tid);
-  wait_tile();
-  __syncthreads();
+  if constexpr (NS == 3) {
+    if (nk > 1)
+      wait_vm<LPT>();  // tile 0 landed, tile 1 may still fly
+    else
+      wait_tile();
+    barrier_keep_loads();
+  } else {
+    wait_tile();
+    __syncthreads();
+  }
 
   const int frow = lane & 31, fch = lane >> 5;
   int arow[TM], brow[TN];
 #pragma unroll
-  for (int i = 0; i < TM; i++) arow[i] = wm * (BM / 2) + i * 32 + frow;
+  for (int i = 0; i < TM; i++) arow[i] = wm * WTM + i * 32 + frow;
 #pragma unroll
-  for (int j = 0; j < TN; j++) brow[j] = wn * (BN / 2) + j * 32 + frow;
+  for (int j = 0; j < TN; j++) brow[j] = wn * WTN + j * 32 + frow;
 
   for (int kt = 0; kt < nk; kt++) {
-    const half_t* cur = lds + (kt & 1) * STAGE;
-    half_t* nxt = lds + ((kt + 1) & 1) * STAGE;
-    if (kt + 1 < nk) {
-      sa.issue(g.A, g.lda, m0, (kt + 1) * BK, nxt, tid);
-      sb.issue(g.B, g.ldb, n0, (kt + 1) * BK, nxt + BM * BK, tid);
+    const half_t* cur = lds + (kt % NS) * STAGE;
+    half_t* nxt = lds + ((kt + 1) % NS) * STAGE;             // register-path target (NS == 2)
+    half_t* far = lds + ((kt + NS - 1) % NS) * STAGE;        // direct-load target
+    if (kt + NS - 1 < nk) {
+      sa.issue(g.A, g.lda, m0, (kt + NS - 1) * BK, far, tid);
+      sb.issue(g.B, g.ldb, n0, (kt + NS - 1) * BK, far + BM * BK, tid);
     }
     // fragments double-buffered across the four 16-wide k-substeps
     half8 a[2][TM], b[2][TN];
@@ -191,13 +230,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
       sa.commit(nxt, tid);
       sb.commit(nxt + BM * BK, tid);
     }
-    wait_tile();
-    __syncthreads();
+    // tile kt+1 must have landed; with 3 stages tile kt+2 may stay in flight
+    if constexpr (NS == 3) {
+      if (kt + 2 < nk)
+        wait_vm<LPT>();
+      else
+        wait_tile();
+      barrier_keep_loads();
+    } else {
+      wait_tile();
+      __syncthreads();
+    }
   }
 
   // ---------------------------------------------------------------- epilogue
-  const int rbase = m0 + wm * (BM / 2) + 4 * (lane >> 5);
-  const int cbase = n0 + wn * (BN / 2) + (lane & 31);
+  const int rbase = m0 + wm * WTM + 4 * (lane >> 5);
+  const int cbase = n0 + wn * WTN + (lane & 31);
 #define ROW(i, r) (rbase + (i) * 32 + 8 * ((r) >> 2) + ((r) & 3))
 #define COL(j) (cbase + (j) * 32)
 
@@ -394,7 +442,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
     float2* red = reinterpret_cast<float2*>(lds);  // [2][BN], main loop done
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-      const int nl = wn * (BN / 2) + j * 32 + (lane & 31);
+      const int nl = wn * WTN + j * 32 + (lane & 31);
       const int n = n0 + nl;
       const int tg = e.targets[n];
       float mx = -INFINITY, tv = 0.f;
@@ -425,7 +473,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
     if (wm == 0) {
 #pragma unroll
       for (int j = 0; j < TN; j++) {
-        const int nl = wn * (BN / 2) + j * 32 + (lane & 31);
+        const int nl = wn * WTN + j * 32 + (lane & 31);
         if (lane < 32) {
           const float2 p0 = red[nl], p1 = red[BN + nl];
           const float M = fmaxf(p0.x, p1.x);
@@ -463,16 +511,35 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g, EpiParams e) {
 #undef COL
 }
 
-template <bool AT, bool BT, int EPI, int BM, int BN>
+template <bool AT, bool BT, int EPI, int BM, int BN, int NW = 4, int NS = 2>
 hipError_t launch_tile(const GemmArgs& g, const EpiParams& e, hipStream_t s) {
   dim3 grid((g.M / BM) * (g.N / BN));
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, AT, BT, EPI>), grid, dim3(256), 0, s, g, e);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, AT, BT, EPI, NW, NS>), grid, dim3(64 * NW), 0, s, g, e);
   return hipGetLastError();
 }
 
 template <bool AT, bool BT, int EPI>
-hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, int bn) {
+hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, int bn, int nw, int ns) {
   const int key = bm * 1000 + bn;
+  if (nw == 8) return launch_tile<AT, BT, EPI, 256, 256, 8>(g, e, s);  // caller checked the tile
+  if constexpr (!AT && !BT) {
+    if (ns == 3) {  // caller checked the tile
+      switch (key) {
+        case 256128: return launch_tile<AT, BT, EPI, 256, 128, 4, 3>(g, e, s);
+        case 128128: return launch_tile<AT, BT, EPI, 128, 128, 4, 3>(g, e, s);
+        case 64128: return launch_tile<AT, BT, EPI, 64, 128, 4, 3>(g, e, s);
+        default: break;
+      }
+      if constexpr (EPI != EPI_SWIGLU) {
+        switch (key) {
+          case 128064: return launch_tile<AT, BT, EPI, 128, 64, 4, 3>(g, e, s);
+          case 64064: return launch_tile<AT, BT, EPI, 64, 64, 4, 3>(g, e, s);
+          default: break;
+        }
+      }
+      return hipErrorInvalidValue;
+    }
+  }
   switch (key) {
     case 256256: return launch_tile<AT, BT, EPI, 256, 256>(g, e, s);
     case 256128: return launch_tile<AT, BT, EPI, 256, 128>(g, e, s);
@@ -498,11 +565,13 @@ void gemm_pick_tile(int M, int N, int K, int epi, int* pbm, int* pbn) {
   // Preference order with a minimum block count each: a tile is taken only
   // if it yields enough blocks to keep the 256 CUs (and 2-3 resident blocks
   // per CU for the smaller tiles) busy.  Thresholds come from a sweep of
-  // the stories110M shapes on MI355X (M = 8192 tokens): 128x128 wins at
-  // N >= 2048, 128x64 at N = 768 with K <= 2048, 64x64 for narrow outputs
-  // with long K.  A nonzero *pbm / *pbn on entry is a constraint the chosen
-  // tile keeps (callers size buffers by it).
-  static const int cand[][3] = {{256, 256, 4096}, {128, 128, 1024}, {128, 64, 600}, {64, 128, 600},
+  // the stories110M shapes on MI355X (M = 8192 tokens, random operands):
+  // 256x256 with 8 waves wins from 512 blocks (W1|W3: 925 vs 817 TFLOP/s
+  // for 128x128; classifier 885 vs 801), 128x128 at N >= 2048, 128x64 at
+  // N = 768 with K <= 2048, 64x64 for narrow outputs with long K.  A nonzero
+  // *pbm / *pbn on entry is a constraint the chosen tile keeps (callers
+  // size buffers by it).
+  static const int cand[][3] = {{256, 256, 512}, {128, 128, 1024}, {128, 64, 600}, {64, 128, 600},
                                 {256, 128, 600},  {128, 256, 600},  {256, 64, 600}, {64, 64, 0}};
   constexpr int NCAND = 8;
   const int want_bm = *pbm, want_bn = *pbn;
@@ -534,13 +603,22 @@ void gemm_pick_tile(int M, int N, int K, int epi, int* pbm, int* pbn) {
   (void)K;
 }
 
-hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t s, int bm, int bn) {
+hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t s, int bm, int bn, int nw,
+                    int ns) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0) return hipErrorInvalidValue;
   if (bm == 0 || bn == 0) gemm_pick_tile(g.M, g.N, g.K, epi, &bm, &bn);
   if (bm == 0 || bn == 0 || (g.M % bm) || (g.N % bn)) return hipErrorInvalidValue;
+  // 256x256 tiles run with 8 waves unless 4 are asked for (measured faster on every shape)
+  if (nw == 0) nw = (bm == 256 && bn == 256) ? 8 : 4;
+  if (nw != 4 && !(nw == 8 && bm == 256 && bn == 256)) return hipErrorInvalidValue;
+  if (ns == 0) ns = 2;
+  // three LDS stages: both operands K-major, 4 waves, tiles whose 3 stages fit the 160 KB LDS
+  if (ns != 2 && !(ns == 3 && nw == 4 && !g.a_t && !g.b_t && (bm + bn) <= 384 && !(bm == 256 && bn == 64) &&
+                   !(bm == 128 && bn == 256)))
+    return hipErrorInvalidValue;
   const int lay = (g.a_t ? 2 : 0) | (g.b_t ? 1 : 0);
 #define CASE(L, AT, BT, E) \
-  if (lay == L && epi == E) return launch<AT, BT, E>(g, e, s, bm, bn);
+  if (lay == L && epi == E) return launch<AT, BT, E>(g, e, s, bm, bn, nw, ns);
   // forward (activation x weight^T)
   CASE(0, false, false, EPI_STORE_H)
   CASE(0, false, false, EPI_STORE_F)

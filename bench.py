@@ -46,6 +46,34 @@ def cpu_baseline(cfg, params, tok, tgt, threads):
                       "reference's threading (serial linearCF, parallelFor over tokens/vocab elsewhere)"}
 
 
+def train_bench(ane, arch, steps, batch=16):
+    """full training step (forward + backward + AdamW,
+    lr 3e-4, betas 0.9/0.95, eps 1e-8, wd 0.1) at batch 16 x 256, windows
+    drawn by the reference's drand48 sampler from a token stream of seed 3.
+    One call = 16 windows = one optimizer step (AccumSteps 16)."""
+    cfg = ane.stories110m(arch)
+    params = ane.init_params(cfg, seed=0, std=0.02)
+    stream = np.random.default_rng(3).integers(0, cfg.vocab, 64 * (cfg.seq + 1)).astype(np.uint16)
+    eng = ane.Open(ane.Options(Config=cfg, Params=params, MaxBatch=batch, Tokens=stream, AccumSteps=batch,
+                               LR=3e-4, AdamBeta1=0.9, AdamBeta2=0.95, AdamEps=1e-8, WeightDecay=0.1))
+    for _ in range(2):
+        eng.TrainBatch(batch)
+    eng.Sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        r = eng.TrainBatch(batch)
+    eng.Sync()
+    dt = time.perf_counter() - t0
+    st = eng.State()
+    eng.Destroy()
+    ms = dt / steps * 1e3
+    return {"value": round(batch * cfg.seq * steps / dt, 1), "unit": "tokens/s", "ms_per_step": round(ms, 3),
+            "batch": batch, "seq": cfg.seq, "optimizer_steps": int(st.adam_t), "last_loss": round(r.loss, 5),
+            "adam_ms": round(r.adam_ns / 1e6, 3), "final_head_ms": round(r.final_head_ns / 1e6, 3),
+            "tflops_alg": round((673_643_520 if arch == "llama2" else 563_936_256) * batch * cfg.seq / (ms * 1e-3)
+                                / 1e12, 1)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -55,6 +83,8 @@ def main():
     ap.add_argument("--arch", default="llama2", choices=["llama2", "nanochat"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-profile", action="store_true", help="time without per-launch HIP events")
+    ap.add_argument("--no-train", action="store_true", help="skip the B16 training-step leg")
+    ap.add_argument("--train-steps", type=int, default=5)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the forward shards "
@@ -109,6 +139,8 @@ def main():
         out["mfma_util_projection_gemms"] = round(g_fl / (g_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)
         out["kernel_ms_per_step"] = {k: round(v["ms"] / args.steps, 4) for k, v in prof.items()}
     eng.Destroy()
+    if not args.no_train:
+        out["train_step_b16"] = train_bench(ane, args.arch, args.train_steps)
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(cfg, params, tok, tgt, threads)

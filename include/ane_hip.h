@@ -206,18 +206,21 @@ int ane_sync(ane_engine *e);
  * reference; they run one kernel on device 0 from host buffers).
  * ane_debug_gemm: C = A(m,k) B(n,k)^T with A stored [K, M] when a_t else
  * [M, K], B stored [K, N] when b_t else [N, K] (fp16 bit patterns); C is
- * [M, N] fp32 (epi 1) or fp16 (epi 0); bm/bn force a block tile (0 = auto).
+ * [M, N] fp32 (epi 1) or fp16 (epi 0); bm/bn force a block tile (0 = auto);
+ * nw: waves per block, 0 = default (4), 8 = two waves per SIMD (256x256);
+ * ns: LDS pipeline stages, 0 = default (2), 3 (K-major operands only).
  * ane_debug_attention: causal attention over qkv [nseq*S, 3*64*NH] (fp16,
  * q|k|v per row, pre-RoPE) with score scale `scale` (hilo: split-operand
  * scores) -> out [nseq*S, 64*NH] fp16 and lse [nseq*S, NH].
  * Messages: ane_debug_last_error(). */
 int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_t *A, const uint16_t *B,
-                   void *C, int bm, int bn);
+                   void *C, int bm, int bn, int nw, int ns);
 int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float scale, int hilo,
                         const uint16_t *qkv, uint16_t *out, float *lse);
-/* Mean time of `iters` launches of one GEMM on device-resident operands. */
-int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int iters,
-                         float *avg_ms);
+/* Mean time of `iters` launches of one GEMM on device-resident operands
+ * (arguments as ane_debug_gemm). */
+int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw, int ns,
+                         int iters, float *avg_ms);
 const char *ane_debug_last_error(void);
 
 #ifdef __cplusplus

@@ -20,7 +20,7 @@ def _u16(a):
     return a.ctypes.data_as(C.POINTER(C.c_uint16))
 
 
-def run_gemm(A, B, a_t, b_t, bm=0, bn=0, out_f16=False):
+def run_gemm(A, B, a_t, b_t, bm=0, bn=0, out_f16=False, nw=0, ns=0):
     """A: (M,K) logical, B: (N,K) logical, both float16 arrays."""
     lib = _lib.load()
     M, K = A.shape
@@ -29,24 +29,50 @@ def run_gemm(A, B, a_t, b_t, bm=0, bn=0, out_f16=False):
     Bs = np.ascontiguousarray(B.T if b_t else B).view(np.uint16)
     out = np.zeros((M, N), np.float16 if out_f16 else np.float32)
     rc = lib.ane_debug_gemm(int(a_t), int(b_t), 0 if out_f16 else 1, M, N, K, _u16(As), _u16(Bs),
-                            out.ctypes.data_as(C.c_void_p), bm, bn)
+                            out.ctypes.data_as(C.c_void_p), bm, bn, nw, ns)
     assert rc == 0, lib.ane_debug_last_error()
     return out
 
 
-TILES = [(256, 256), (256, 128), (128, 256), (128, 128), (64, 128), (128, 64), (256, 64), (64, 64)]
+TILES = [(256, 256, 4), (256, 256, 8), (256, 128, 4), (128, 256, 4), (128, 128, 4), (64, 128, 4),
+         (128, 64, 4), (256, 64, 4), (64, 64, 4)]
+TILES_3STAGE = [(256, 128), (128, 128), (64, 128), (128, 64), (64, 64)]
 
 
 @pytest.mark.parametrize("a_t,b_t", [(False, False), (False, True), (True, True)])
-@pytest.mark.parametrize("bm,bn", TILES)
-def test_gemm_layouts_and_tiles(a_t, b_t, bm, bn):
-    r = np.random.default_rng(bm * 7 + bn + 3 * a_t + b_t)
+@pytest.mark.parametrize("bm,bn,nw", TILES)
+def test_gemm_layouts_and_tiles(a_t, b_t, bm, bn, nw):
+    r = np.random.default_rng(bm * 7 + bn + 3 * a_t + b_t + nw)
     M, N, K = 512, 256, 320
     A = r.standard_normal((M, K)).astype(np.float16)
     B = r.standard_normal((N, K)).astype(np.float16)
-    got = run_gemm(A, B, a_t, b_t, bm, bn)
+    got = run_gemm(A, B, a_t, b_t, bm, bn, nw=nw)
     ref = A.astype(np.float64) @ B.astype(np.float64).T
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-4)
+
+
+@pytest.mark.parametrize("bm,bn", TILES_3STAGE)
+@pytest.mark.parametrize("K", [64, 128, 192, 640])
+def test_gemm_three_stage_pipeline(bm, bn, K):
+    """3-stage LDS pipeline: every k-tile count from 1 (prologue only) up."""
+    r = np.random.default_rng(bm + bn + K)
+    M, N = 512, 256
+    A = r.standard_normal((M, K)).astype(np.float16)
+    B = r.standard_normal((N, K)).astype(np.float16)
+    got = run_gemm(A, B, False, False, bm, bn, ns=3)
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-4)
+
+
+def test_gemm_three_stage_rejects_unsupported():
+    lib = _lib.load()
+    A = np.zeros((256, 64), np.float16)
+    B = np.zeros((256, 64), np.float16)
+    out = np.zeros((256, 256), np.float32)
+    for (bm, bn, nw, at) in [(256, 256, 4, 0), (128, 128, 4, 1), (256, 256, 8, 0)]:
+        rc = lib.ane_debug_gemm(at, 0, 1, 256, 256, 64, _u16(A.view(np.uint16)), _u16(B.view(np.uint16)),
+                                out.ctypes.data_as(C.c_void_p), bm, bn, nw, 3)
+        assert rc != 0
 
 
 def test_gemm_real_shapes_auto_tile():
