@@ -5,6 +5,7 @@
 meaning and error behaviour of ane/engine.go; everything computes on the GPU
 through libane_hip.so (no CPU fallback: a missing library raises).
 """
-from .config import (Config, stories110m, tiny, is_ve_layer, param_layout, param_count,  # noqa: F401
+from .config import (Config, stories110m, tiny, decode_gqa, tiny_decode, is_ve_layer, param_layout, param_count,  # noqa: F401
                      views, init_params, make_tokens, VE_GATE_CHANNELS)
 from .engine import Options, Open, Engine, EngineError  # noqa: F401
+from .decode import Decoder  # noqa: F401

@@ -52,6 +52,12 @@ class StepResult(C.Structure):
         "final_head_ns", "embed_grad_ns", "rms_dw_ns", "dw_gemm_ns", "dw_wait_ns", "adam_ns")]
 
 
+class DecodeCfg(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("hidden", C.c_int32), ("heads", C.c_int32), ("kv_heads", C.c_int32),
+                ("layers", C.c_int32), ("vocab", C.c_int32), ("max_batch", C.c_int32), ("max_ctx", C.c_int32),
+                ("rope_theta", C.c_double), ("device", C.c_int32)]
+
+
 class ProfEntry(C.Structure):
     _fields_ = [("launches", C.c_int64), ("ms", C.c_double), ("flops", C.c_double), ("bytes", C.c_double)]
 
@@ -93,6 +99,16 @@ SIGNATURES = {
                                       _u16, _fp]),
     "ane_debug_last_error": (C.c_char_p, []),
     "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 11 + [_fp]),
+    "ane_decode_open": (C.c_int, [C.POINTER(DecodeCfg), C.POINTER(C.c_void_p)]),
+    "ane_decode_destroy": (None, [_eng]),
+    "ane_decode_last_error": (C.c_char_p, [_eng]),
+    "ane_decode_param_count": (C.c_int64, [C.POINTER(DecodeCfg)]),
+    "ane_decode_set_params": (C.c_int, [_eng, _fp, C.c_int64]),
+    "ane_decode_prefill": (C.c_int, [_eng, _u16, C.c_int32, C.c_int32, _u16, _fp]),
+    "ane_decode_step": (C.c_int, [_eng, _u16, _u16, _fp]),
+    "ane_decode_generate": (C.c_int, [_eng, C.c_int32, _u16]),
+    "ane_decode_position": (C.c_int32, [_eng]),
+    "ane_decode_last_ms": (C.c_double, [_eng]),
 }
 
 _lib = None

@@ -36,6 +36,7 @@ class Config:
     arch: str = "llama2"          # "llama2" | "nanochat"
     grad_mode: str = "compat"     # nanochat backward: "compat" (reference) | "true"
     rope_theta: float = 0.0       # 0 -> arch default
+    kv_heads: int = 0             # key/value heads (llama2 only; 0 -> heads, i.e. no grouping)
 
     def __post_init__(self):
         if self.arch not in ("llama2", "nanochat"):
@@ -44,6 +45,10 @@ class Config:
             raise ValueError(f"unknown grad_mode {self.grad_mode!r}")
         if not self.rope_theta:
             self.rope_theta = 10000.0 if self.arch == "llama2" else 100000.0
+        if not self.kv_heads:
+            self.kv_heads = self.heads
+        if self.heads % self.kv_heads or (self.arch != "llama2" and self.kv_heads != self.heads):
+            raise ValueError(f"kv_heads={self.kv_heads} must divide heads={self.heads} (llama2 only)")
 
     @property
     def head_dim(self) -> int:
@@ -61,6 +66,22 @@ def tiny(arch: str = "llama2", **kw) -> Config:
     return Config(**base)
 
 
+def decode_gqa(**kw) -> Config:
+    """The decode benchmark's model: 12 layers, dim 768, 12 query / 4 key-value
+    heads of 64, vocab 32000, SwiGLU hidden 2048, tied classifier, RoPE 1e4
+    (Llama2 blocks with grouped-query attention; no reference counterpart)."""
+    base = dict(dim=768, hidden=2048, heads=12, kv_heads=4, layers=12, vocab=32000, seq=1024, arch="llama2")
+    base.update(kw)
+    return Config(**base)
+
+
+def tiny_decode(**kw) -> Config:
+    """A small grouped-query model (4 query heads over 2 key-value heads)."""
+    base = dict(dim=256, hidden=512, heads=4, kv_heads=2, layers=2, vocab=1024, seq=128, arch="llama2")
+    base.update(kw)
+    return Config(**base)
+
+
 def is_ve_layer(cfg: Config, l: int) -> bool:
     """ane/stories/weights.go:22 (nanochat only)."""
     return cfg.arch == "nanochat" and (l % 2) == ((cfg.layers - 1) % 2)
@@ -69,6 +90,7 @@ def is_ve_layer(cfg: Config, l: int) -> bool:
 def param_layout(cfg: Config):
     """Ordered list of (name, offset, shape) for the flat parameter vector."""
     D, H, V, NH, L = cfg.dim, cfg.hidden, cfg.vocab, cfg.heads, cfg.layers
+    KVD = cfg.kv_heads * cfg.head_dim
     out = []
     off = 0
 
@@ -80,8 +102,8 @@ def param_layout(cfg: Config):
 
     for l in range(L):
         seg(f"layers.{l}.wq", (D, D))
-        seg(f"layers.{l}.wk", (D, D))
-        seg(f"layers.{l}.wv", (D, D))
+        seg(f"layers.{l}.wk", (KVD, D))
+        seg(f"layers.{l}.wv", (KVD, D))
         seg(f"layers.{l}.wo", (D, D))
         seg(f"layers.{l}.w1", (H, D))
         seg(f"layers.{l}.w2", (D, H))

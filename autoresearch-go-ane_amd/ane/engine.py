@@ -85,6 +85,9 @@ def Open(opts: Options) -> "Engine":
         raise EngineError(_lib.ANE_ERR_ARG, f"storiesane open: load model: {opts.ModelPath}: "
                                             "model files are not supported by this engine; pass Params")
     cfg = opts.Config or Config()
+    if cfg.kv_heads != cfg.heads:
+        raise EngineError(_lib.ANE_ERR_ARG, "storiesane open: grouped-query attention (kv_heads != heads) "
+                                            "is served by ane.decode.Decoder only")
     if opts.Seq and opts.Seq != cfg.seq:
         cfg = dataclasses.replace(cfg, seq=opts.Seq)
     tokens = None

@@ -1,0 +1,625 @@
+// Decode kernels (see decode.h).  Decode steps are HBM- and latency-bound:
+// the weights stream once per step through 64-row MFMA "skinny" GEMMs
+// split over K, and the attention reads each sequence's K/V cache once,
+// shared by the query heads of a key/value group.
+#include <math.h>
+
+#include "decode.h"
+
+namespace ane {
+
+namespace {
+
+constexpr float kL2E = 1.4426950408889634f;
+
+// ---- skinny GEMM ------------------------------------------------------------
+// One wave per (32 weight rows, K range).  MFMA 32x32x16 with rows = tokens
+// (two tiles: tokens 0-31, 32-63) and columns = weight rows.  Lane l owns
+// token / weight row l%32 and, for k-step s of a 64-wide window, the eight
+// k-values 32*(l/32) + 8*s + [0, 8): A and B use the same k-slot map, so
+// each lane reads 64 contiguous bytes of its weight row per window and the
+// two lane halves cover the row's 128-byte line.
+template <int EPI>
+__global__ __launch_bounds__(64) void skinny_kernel(SkinnyArgs a) {
+  const int lane = threadIdx.x;
+  const int cg = blockIdx.x;
+  const int KR = a.K / a.splits, k0 = blockIdx.y * KR;
+  const int row = lane & 31, h = lane >> 5;
+  const half_t* wp = a.W + (size_t)(cg * 32 + row) * a.ldw + k0 + 32 * h;
+  const half_t* xp0 = a.X + (size_t)row * a.ldx + k0 + 32 * h;
+  const half_t* xp1 = xp0 + (size_t)32 * a.ldx;
+  floatx16 c0, c1;
+#pragma unroll
+  for (int r = 0; r < 16; r++) { c0[r] = 0.f; c1[r] = 0.f; }
+#pragma unroll 2
+  for (int k = 0; k < KR; k += 64) {
+    half8 w[4], p[4], q[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      w[s] = ld_h8(wp + k + 8 * s);
+      p[s] = ld_h8(xp0 + k + 8 * s);
+      q[s] = ld_h8(xp1 + k + 8 * s);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(p[s], w[s], c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(q[s], w[s], c1, 0, 0, 0);
+    }
+  }
+  // c[r]: token 8*(r/4) + 4*h + r%4 (+32 for c1), column cg*32 + row
+  const int col = cg * 32 + row;
+  if constexpr (EPI == 0) {
+    float* out = a.partial + (size_t)blockIdx.y * kDecRows * a.N + col;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int t = 8 * (r >> 2) + 4 * h + (r & 3);
+      out[(size_t)t * a.N] = c0[r];
+      out[(size_t)(t + 32) * a.N] = c1[r];
+    }
+  } else {
+    const bool valid = col < a.nvalid;
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int t = 8 * (r >> 2) + 4 * h + (r & 3) + 32 * half;
+        const float v0 = half ? c1[r] : c0[r];
+        if (a.logits && valid) a.logits[(size_t)t * a.N + col] = v0;
+        float v = valid ? v0 : -INFINITY;
+        int idx = col;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) {
+          const float ov = __shfl_xor(v, o, 64);
+          const int oi = __shfl_xor(idx, o, 64);
+          if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+        }
+        if (row == 0) a.amax[(size_t)cg * kDecRows + t] = make_float2(v, __int_as_float(idx));
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(uint16_t* tok_out, uint16_t* hist, const int* step,
+                                                     const float2* amax, int ngroups, int nb) {
+  const int b = blockIdx.x, tid = threadIdx.x;
+  float v = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int g = tid; g < ngroups; g += 256) {
+    const float2 p = amax[(size_t)g * kDecRows + b];
+    const int pi = __float_as_int(p.y);
+    if (p.x > v || (p.x == v && pi < idx)) { v = p.x; idx = pi; }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ov = __shfl_xor(v, o, 64);
+    const int oi = __shfl_xor(idx, o, 64);
+    if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
+  }
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  if ((tid & 63) == 0) { sv[tid >> 6] = v; si[tid >> 6] = idx; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 4; w++)
+      if (sv[w] > v || (sv[w] == v && si[w] < idx)) { v = sv[w]; idx = si[w]; }
+    tok_out[b] = (uint16_t)idx;
+    if (hist) hist[(size_t)(*step) * nb + b] = (uint16_t)idx;
+  }
+}
+
+__global__ void advance_kernel(int* ctr) {
+  if (threadIdx.x == 0) {
+    ctr[0] += 1;
+    ctr[1] += 1;
+  }
+}
+
+__global__ void set_ctr_kernel(int* ctr, int pos, int step) {
+  if (threadIdx.x == 0) {
+    ctr[0] = pos;
+    ctr[1] = step;
+  }
+}
+
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+  v = wave_sum(v);
+  const int tid = threadIdx.x;
+  __syncthreads();  // red may still be read by a previous call
+  if ((tid & 63) == 0) red[tid >> 6] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// one block of 256 per row, D <= 1024
+__global__ __launch_bounds__(256) void embed_norm_kernel(float* x, half_t* xn, const float* embed,
+                                                         const uint16_t* tok, const float* g, int D, int V) {
+  __shared__ float red[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int tk = tok[b];
+  float v[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int c = tid + 256 * i;
+    v[i] = (c < D && tk < V) ? embed[(size_t)tk * D + c] : 0.f;
+    ss += v[i] * v[i];
+  }
+  ss = block_sum_256(ss, red);
+  const float rr = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int c = tid + 256 * i;
+    if (c < D) {
+      x[(size_t)b * D + c] = v[i];
+      xn[(size_t)b * D + c] = (half_t)(v[i] * rr * g[c]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void resid_norm_kernel(float* x, half_t* xn, const float* partial, int splits,
+                                                         const float* g, int D) {
+  __shared__ float red[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  float v[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int c = tid + 256 * i;
+    v[i] = 0.f;
+    if (c < D) {
+      float s = x[(size_t)b * D + c];
+      if (partial)
+        for (int k = 0; k < splits; k++) s += partial[((size_t)k * kDecRows + b) * D + c];
+      v[i] = s;
+    }
+    ss += v[i] * v[i];
+  }
+  ss = block_sum_256(ss, red);
+  const float rr = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int c = tid + 256 * i;
+    if (c < D) {
+      x[(size_t)b * D + c] = v[i];
+      xn[(size_t)b * D + c] = (half_t)(v[i] * rr * g[c]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void swiglu_kernel(half_t* gate, const float* partial, int splits, int H) {
+  const int b = blockIdx.x, j = blockIdx.y * 256 + threadIdx.x;
+  if (j >= H) return;
+  const int N = 2 * H;
+  const int c1 = (j >> 5) * 64 + (j & 31);
+  float h1 = 0.f, h3 = 0.f;
+  for (int k = 0; k < splits; k++) {
+    const float* pr = partial + ((size_t)k * kDecRows + b) * N;
+    h1 += pr[c1];
+    h3 += pr[c1 + 32];
+  }
+  gate[(size_t)b * H + j] = (half_t)(h1 / (1.0f + __expf(-h1)) * h3);
+}
+
+__global__ __launch_bounds__(256) void qkv_finish_kernel(DecQkvArgs a) {
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int D = a.NH * 64, KVD = a.NKV * 64, N1 = D + 2 * KVD;
+  const int pos = a.ctr[0];
+  for (int c2 = tid; c2 < N1 / 2; c2 += 256) {
+    const int col = 2 * c2;
+    float e = 0.f, o = 0.f;
+    for (int k = 0; k < a.splits; k++) {
+      const float* pr = a.partial + ((size_t)k * kDecRows + b) * N1 + col;
+      e += pr[0];
+      o += pr[1];
+    }
+    if (col < D + KVD) {  // RoPE on interleaved pairs
+      const int i = (col & 63) >> 1;
+      const float cs = a.rope_cos[pos * 32 + i], sn = a.rope_sin[pos * 32 + i];
+      const float re = e * cs - o * sn, ro = o * cs + e * sn;
+      e = re;
+      o = ro;
+    }
+    half2v w;
+    w[0] = (half_t)e;
+    w[1] = (half_t)o;
+    if (col < D) {
+      *reinterpret_cast<half2v*>(a.q + (size_t)b * D + col) = w;
+    } else {
+      const bool isk = col < D + KVD;
+      const int c = col - (isk ? D : D + KVD);
+      const int kvh = c >> 6, d = c & 63;
+      half_t* dst = (isk ? a.kc : a.vc) + (((size_t)b * a.NKV + kvh) * a.max_ctx + pos) * 64 + d;
+      *reinterpret_cast<half2v*>(dst) = w;
+    }
+  }
+}
+
+// ---- decode attention ---------------------------------------------------------
+// Block (b, kv head, chunk): 8 lanes per key (16 B each), 32 keys per pass;
+// scores of the G query heads of the group in LDS; per-head max / sum by
+// one wave each; P.V with the same lane map, reduced over keys by shuffles
+// and across waves through LDS.
+constexpr int kGMax = 4;
+__global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
+  const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = a.NH / a.NKV, D = a.NH * 64;
+  const int ctx = a.ctr[0] + 1;
+  const int c0 = sp * kDecChunk;
+  if (c0 >= ctx) return;  // uniform over the block, before any barrier
+  const int n = min(kDecChunk, ctx - c0);
+  __shared__ float qs[kGMax][64];
+  __shared__ float sc[kGMax][kDecChunk];
+  __shared__ float red[4][kGMax][64];
+  __shared__ float stat[kGMax][2];
+  const float sl2 = a.scale * kL2E;
+  if (tid < G * 64) qs[tid >> 6][tid & 63] = (float)a.q[(size_t)b * D + (kvh * G) * 64 + tid] * sl2;
+  __syncthreads();
+  const size_t cache0 = ((size_t)b * a.NKV + kvh) * a.max_ctx;
+  const half_t* Kb = a.kc + (cache0 + c0) * 64;
+  const half_t* Vb = a.vc + (cache0 + c0) * 64;
+  const int kl = tid >> 3, d8 = tid & 7;
+  for (int j = kl; j < kDecChunk; j += 32) {
+    const bool ok = j < n;
+    half8 k8;
+    if (ok) k8 = ld_h8(Kb + (size_t)j * 64 + d8 * 8);
+    else
+#pragma unroll
+      for (int i = 0; i < 8; i++) k8[i] = (half_t)0.f;
+#pragma unroll
+    for (int h = 0; h < kGMax; h++) {
+      if (h < G) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) s += qs[h][d8 * 8 + i] * (float)k8[i];
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        s += __shfl_xor(s, 4, 64);
+        if (ok && d8 == 0) sc[h][j] = s;
+      }
+    }
+  }
+  __syncthreads();
+  if (wave < G) {
+    float m = -INFINITY;
+    for (int j = lane; j < n; j += 64) m = fmaxf(m, sc[wave][j]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int j = lane; j < n; j += 64) {
+      const float p = exp2f(sc[wave][j] - m);
+      sc[wave][j] = p;
+      l += p;
+    }
+    l = wave_sum(l);
+    if (lane == 0) { stat[wave][0] = m; stat[wave][1] = l; }
+  }
+  __syncthreads();
+  float acc[kGMax][8];
+#pragma unroll
+  for (int h = 0; h < kGMax; h++)
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
+  for (int j = kl; j < n; j += 32) {
+    const half8 v8 = ld_h8(Vb + (size_t)j * 64 + d8 * 8);
+#pragma unroll
+    for (int h = 0; h < kGMax; h++) {
+      if (h < G) {
+        const float p = sc[h][j];
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[h][i] += p * (float)v8[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < kGMax; h++)
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      float v = acc[h][i];
+      v += __shfl_xor(v, 8, 64);
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      acc[h][i] = v;
+    }
+  if (lane < 8) {
+#pragma unroll
+    for (int h = 0; h < kGMax; h++)
+      if (h < G)
+#pragma unroll
+        for (int i = 0; i < 8; i++) red[wave][h][lane * 8 + i] = acc[h][i];
+  }
+  __syncthreads();
+  if (tid < G * 64) {
+    const int h = tid >> 6, d = tid & 63;
+    const float o = red[0][h][d] + red[1][h][d] + red[2][h][d] + red[3][h][d];
+    float* out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nsplit + sp) * 66;
+    out[d] = o;
+    if (d == 0) { out[64] = stat[h][0]; out[65] = stat[h][1]; }
+  }
+}
+
+__global__ __launch_bounds__(64) void dec_combine_kernel(DecAttnArgs a) {
+  const int b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const int ctx = a.ctr[0] + 1;
+  const int ns = (ctx + kDecChunk - 1) / kDecChunk;
+  const float* p = a.part + ((size_t)b * a.NH + h) * a.nsplit * 66;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; s++) M = fmaxf(M, p[s * 66 + 64]);
+  float num = 0.f, den = 0.f;
+  for (int s = 0; s < ns; s++) {
+    const float w = exp2f(p[s * 66 + 64] - M);
+    num += w * p[s * 66 + d];
+    den += w * p[s * 66 + 65];
+  }
+  a.att[(size_t)b * a.NH * 64 + h * 64 + d] = (half_t)(num / den);
+}
+
+// ---- prefill ------------------------------------------------------------------
+__global__ __launch_bounds__(128) void kv_write_kernel(half_t* qkv, half_t* kc, half_t* vc, const float* rc,
+                                                       const float* rs, int seq0, int S, int NH, int NKV,
+                                                       int max_ctx) {
+  const int t = blockIdx.x;  // token row of the chunk
+  const int sl = t / S, pos = t % S, b = seq0 + sl;
+  const int D = NH * 64, KVD = NKV * 64, N1 = D + 2 * KVD;
+  half_t* row = qkv + (size_t)t * N1;
+  for (int c2 = threadIdx.x; c2 < N1 / 2; c2 += blockDim.x) {
+    const int col = 2 * c2;
+    half2v w = *reinterpret_cast<const half2v*>(row + col);
+    if (col < D + KVD) {
+      const int i = (col & 63) >> 1;
+      const float cs = rc[pos * 32 + i], sn = rs[pos * 32 + i];
+      const float e = (float)w[0], o = (float)w[1];
+      w[0] = (half_t)(e * cs - o * sn);
+      w[1] = (half_t)(o * cs + e * sn);
+    }
+    if (col < D) {
+      *reinterpret_cast<half2v*>(row + col) = w;
+    } else {
+      const bool isk = col < D + KVD;
+      const int c = col - (isk ? D : D + KVD);
+      const int kvh = c >> 6, d = c & 63;
+      half_t* dst = (isk ? kc : vc) + (((size_t)b * NKV + kvh) * max_ctx + pos) * 64 + d;
+      *reinterpret_cast<half2v*>(dst) = w;
+    }
+  }
+}
+
+// Block = 4 waves x 32 queries of one (sequence, query head); keys and V^T
+// staged through LDS in chunks of KC; scores transposed (S^T = K Q^T) so
+// each lane keeps 16 keys of one query and P feeds O^T = V^T P^T from
+// registers (the layout of the training forward kernel).
+constexpr int KC = 128;
+constexpr int VSTP = KC + 4;
+__global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
+  __shared__ __attribute__((aligned(16))) half_t Ks[KC * 64];
+  __shared__ __attribute__((aligned(16))) half_t Vt[64 * VSTP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int qt = blockIdx.x, h = blockIdx.y, sl = blockIdx.z;
+  const int S = a.S, G = a.NH / a.NKV, kvh = h / G, b = a.seq0 + sl;
+  const int qb = qt * 4 + wave;
+  const bool active = qb * 32 < S;
+  const int kend = min(S, (qt + 1) * 128);
+  const int g = lane >> 5, ql = lane & 31;
+  const int q = qb * 32 + ql;
+  const size_t cache0 = ((size_t)b * a.NKV + kvh) * a.max_ctx;
+
+  half8 qfrag[4];
+  if (active) {
+    const half_t* qrow = a.qkv + ((size_t)sl * S + q) * a.ldq + h * 64;
+#pragma unroll
+    for (int s = 0; s < 4; s++) qfrag[s] = ld_h8(qrow + s * 16 + g * 8);
+  }
+  floatx16 o0, o1;
+#pragma unroll
+  for (int r = 0; r < 16; r++) { o0[r] = 0.f; o1[r] = 0.f; }
+  float m = -INFINITY, lsum = 0.f;
+  const float sl2 = a.scale * kL2E;
+
+  for (int c0 = 0; c0 < kend; c0 += KC) {
+    __syncthreads();  // previous chunk fully consumed
+    for (int c = tid; c < KC * 8; c += 256) {
+      const int j = c >> 3, ch = c & 7;
+      half8 v;
+      if (c0 + j < S) v = ld_h8(a.kc + (cache0 + c0 + j) * 64 + ch * 8);
+      else
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (half_t)0.f;
+      st_h8(Ks + j * 64 + swz(j, ch) * 8, v);
+    }
+    if (tid < KC) {  // 8 keys x 8 dims per thread
+      const int kc8 = tid % (KC / 8), dc = tid / (KC / 8);
+      half8 v[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++) {
+        const int j = c0 + kc8 * 8 + jj;
+        if (j < S) v[jj] = ld_h8(a.vc + (cache0 + j) * 64 + dc * 8);
+        else
+#pragma unroll
+          for (int i = 0; i < 8; i++) v[jj][i] = (half_t)0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        half4 lo, hi;
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+          lo[jj] = v[jj][i];
+          hi[jj] = v[jj + 4][i];
+        }
+        half_t* dst = Vt + (dc * 8 + i) * VSTP + kc8 * 8;
+        *reinterpret_cast<half4*>(dst) = lo;
+        *reinterpret_cast<half4*>(dst + 4) = hi;
+      }
+    }
+    __syncthreads();
+    if (!active) continue;
+    for (int kbl = 0; kbl < KC / 32; kbl++) {
+      const int kb = c0 / 32 + kbl;
+      if (kb > qb) break;
+      floatx16 sacc;
+#pragma unroll
+      for (int r = 0; r < 16; r++) sacc[r] = 0.f;
+      const int krow = kbl * 32 + ql;
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const half8 kf = ld_h8(Ks + krow * 64 + swz(krow, s * 2 + g) * 8);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qfrag[s], sacc, 0, 0, 0);
+      }
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        float sv = sacc[r] * sl2;
+        if (kb == qb && (8 * (r >> 2) + 4 * g + (r & 3)) > ql) sv = -INFINITY;
+        sacc[r] = sv;
+        mloc = fmaxf(mloc, sv);
+      }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+      const float mnew = fmaxf(m, mloc);
+      const float alpha = exp2f(m - mnew);
+      float ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const float p = exp2f(sacc[r] - mnew);
+        sacc[r] = p;
+        ps += p;
+      }
+      lsum = lsum * alpha + ps;
+#pragma unroll
+      for (int r = 0; r < 16; r++) { o0[r] *= alpha; o1[r] *= alpha; }
+      m = mnew;
+#pragma unroll
+      for (int jh = 0; jh < 2; jh++) {
+        half8 pf;
+#pragma unroll
+        for (int u = 0; u < 8; u++) pf[u] = (half_t)sacc[8 * jh + u];
+        const int k0 = kbl * 32 + 16 * jh + 4 * g;
+        const half_t* r0 = Vt + ql * VSTP + k0;
+        const half_t* r1 = Vt + (32 + ql) * VSTP + k0;
+        const half4 a0 = *reinterpret_cast<const half4*>(r0), a1 = *reinterpret_cast<const half4*>(r0 + 8);
+        const half4 b0 = *reinterpret_cast<const half4*>(r1), b1 = *reinterpret_cast<const half4*>(r1 + 8);
+        half8 v0, v1;
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          v0[u] = a0[u]; v0[u + 4] = a1[u];
+          v1[u] = b0[u]; v1[u + 4] = b1[u];
+        }
+        o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, pf, o0, 0, 0, 0);
+        o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, pf, o1, 0, 0, 0);
+      }
+    }
+  }
+  if (!active) return;
+  lsum += __shfl_xor(lsum, 32, 64);
+  const float inv = 1.0f / lsum;
+  half_t* orow = a.out + ((size_t)sl * S + q) * (a.NH * 64) + h * 64;
+#pragma unroll
+  for (int rr = 0; rr < 4; rr++) {
+    half4 w0, w1;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      w0[u] = (half_t)(o0[4 * rr + u] * inv);
+      w1[u] = (half_t)(o1[4 * rr + u] * inv);
+    }
+    *reinterpret_cast<half4*>(orow + 8 * rr + 4 * g) = w0;
+    *reinterpret_cast<half4*>(orow + 32 + 8 * rr + 4 * g) = w1;
+  }
+}
+
+__global__ __launch_bounds__(256) void gather_last_kernel(float* dst, const float* src, int S, int D) {
+  const int i = blockIdx.x;
+  const float* s = src + ((size_t)i * S + S - 1) * D;
+  for (int c = threadIdx.x; c < D; c += 256) dst[(size_t)i * D + c] = s[c];
+}
+
+}  // namespace
+
+int skinny_splits(int N, int K) {
+  const int groups = N / 32, nk = K / 64;
+  int best = 1;
+  for (int s = 1; s <= nk; s++) {
+    if (nk % s) continue;
+    best = s;
+    if (groups * s >= 256) break;
+  }
+  return best;
+}
+
+hipError_t skinny_gemm(const SkinnyArgs& a, int epi, hipStream_t s) {
+  if (a.N <= 0 || a.N % 32 || a.K <= 0 || a.splits <= 0 || a.K % (64 * a.splits)) return hipErrorInvalidValue;
+  if (epi == 1 && a.splits != 1) return hipErrorInvalidValue;
+  dim3 grid(a.N / 32, a.splits);
+  if (epi == 0)
+    hipLaunchKernelGGL(skinny_kernel<0>, grid, dim3(64), 0, s, a);
+  else
+    hipLaunchKernelGGL(skinny_kernel<1>, grid, dim3(64), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t argmax_reduce(uint16_t* tok_out, uint16_t* hist, const int* step, const float2* amax, int ngroups,
+                         int nb, hipStream_t s) {
+  hipLaunchKernelGGL(argmax_kernel, dim3(nb), dim3(256), 0, s, tok_out, hist, step, amax, ngroups, nb);
+  return hipGetLastError();
+}
+
+hipError_t dec_advance(int* ctr, hipStream_t s) {
+  hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, s, ctr);
+  return hipGetLastError();
+}
+
+hipError_t dec_set_ctr(int* ctr, int pos, int step, hipStream_t s) {
+  hipLaunchKernelGGL(set_ctr_kernel, dim3(1), dim3(64), 0, s, ctr, pos, step);
+  return hipGetLastError();
+}
+
+hipError_t dec_embed_norm(float* x, half_t* xn, const float* embed, const uint16_t* tok, const float* g, int nb,
+                          int D, int V, hipStream_t s) {
+  if (D > 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(embed_norm_kernel, dim3(nb), dim3(256), 0, s, x, xn, embed, tok, g, D, V);
+  return hipGetLastError();
+}
+
+hipError_t dec_resid_norm(float* x, half_t* xn, const float* partial, int splits, const float* g, int nb, int D,
+                          hipStream_t s) {
+  if (D > 1024) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(resid_norm_kernel, dim3(nb), dim3(256), 0, s, x, xn, partial, splits, g, D);
+  return hipGetLastError();
+}
+
+hipError_t dec_swiglu(half_t* gate, const float* partial, int splits, int nb, int H, hipStream_t s) {
+  hipLaunchKernelGGL(swiglu_kernel, dim3(nb, (H + 255) / 256), dim3(256), 0, s, gate, partial, splits, H);
+  return hipGetLastError();
+}
+
+hipError_t dec_qkv_finish(const DecQkvArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(qkv_finish_kernel, dim3(a.nb), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t dec_attention(const DecAttnArgs& a, hipStream_t s) {
+  const int G = a.NH / a.NKV;
+  if (a.NH % a.NKV || G > kGMax) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(dec_attn_kernel, dim3(a.nb, a.NKV, a.nsplit), dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(dec_combine_kernel, dim3(a.nb, a.NH), dim3(64), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t prefill_kv_write(half_t* qkv, half_t* kc, half_t* vc, const float* rope_cos, const float* rope_sin,
+                            int seq0, int nseq, int S, int NH, int NKV, int max_ctx, hipStream_t s) {
+  hipLaunchKernelGGL(kv_write_kernel, dim3(nseq * S), dim3(128), 0, s, qkv, kc, vc, rope_cos, rope_sin, seq0, S,
+                     NH, NKV, max_ctx);
+  return hipGetLastError();
+}
+
+hipError_t prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
+  if (a.S <= 0 || a.S % 32 || a.S > a.max_ctx || a.NH % a.NKV) return hipErrorInvalidValue;
+  dim3 grid((a.S + 127) / 128, a.NH, a.nseq);
+  hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t gather_last_rows(float* dst, const float* src, int nseq, int S, int D, hipStream_t s) {
+  hipLaunchKernelGGL(gather_last_kernel, dim3(nseq), dim3(256), 0, s, dst, src, S, D);
+  return hipGetLastError();
+}
+
+}  // namespace ane

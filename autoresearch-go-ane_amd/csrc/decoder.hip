@@ -1,0 +1,485 @@
+// ane_decoder: greedy KV-cache decoding with grouped-query attention (the
+// C-ABI declared in include/ane_hip.h).  No counterpart in the reference;
+// see decode.h for the model and the kernels.
+//
+// Device layout (one HIP device, one stream):
+//   P        fp32 parameters (flat LLAMA2 order, Wk/Wv of kv_heads*64 rows)
+//   wqkv     fp16 [L][D + 2*KVD][D]   Wq | Wk | Wv rows
+//   wo       fp16 [L][D][D]
+//   w13      fp16 [L][2H][D]          W1 / W3 interleaved by 32 rows
+//   w2       fp16 [L][D][H]
+//   embed_h  fp16 [V][D]              tied classifier
+//   kc, vc   fp16 [L][max_batch][kv_heads][max_ctx][64]
+//   decode rows (64 each): x fp32 [64][D], xn/q/att fp16 [64][D],
+//   gate fp16 [64][H], split-K partials, attention partials, argmax partials
+//   prefill chunk (<= 8192 tokens): px fp32, pxn/pqkv/patt/pgate fp16
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <cmath>
+#include <string>
+#include <vector>
+
+#include "../../include/ane_hip.h"
+#include "decode.h"
+#include "gemm.h"
+#include "rowops.h"
+
+using namespace ane;
+
+namespace {
+
+struct DecLayerOff {
+  int64_t wq, wk, wv, wo, w1, w2, w3, g_att, g_ffn;
+};
+
+int64_t dec_layout(const ane_decode_cfg& c, std::vector<DecLayerOff>* L, int64_t* embed, int64_t* g_final) {
+  const int64_t D = c.dim, H = c.hidden, KVD = (int64_t)c.kv_heads * 64;
+  int64_t off = 0;
+  for (int l = 0; l < c.layers; l++) {
+    DecLayerOff o;
+    o.wq = off; off += D * D;
+    o.wk = off; off += KVD * D;
+    o.wv = off; off += KVD * D;
+    o.wo = off; off += D * D;
+    o.w1 = off; off += H * D;
+    o.w2 = off; off += D * H;
+    o.w3 = off; off += H * D;
+    o.g_att = off; off += D;
+    o.g_ffn = off; off += D;
+    if (L) L->push_back(o);
+  }
+  if (embed) *embed = off;
+  off += (int64_t)c.vocab * D;
+  if (g_final) *g_final = off;
+  off += D;
+  return off;
+}
+
+constexpr int kPrefillTokens = 8192;
+
+}  // namespace
+
+struct ane_decoder {
+  ane_decode_cfg cfg{};
+  int D = 0, H = 0, NH = 0, NKV = 0, KVD = 0, N1 = 0, L = 0, V = 0, B = 0, C = 0;
+  std::string err;
+  hipStream_t stream = nullptr;
+  std::vector<void*> allocs;
+  std::vector<DecLayerOff> off;
+  int64_t off_embed = 0, off_gfinal = 0, nparams = 0;
+  bool params_set = false;
+  float* P = nullptr;
+  half_t *wqkv = nullptr, *wo = nullptr, *w13 = nullptr, *w2 = nullptr, *embed_h = nullptr;
+  half_t *kc = nullptr, *vc = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  float* x = nullptr;
+  half_t *xn = nullptr, *q = nullptr, *att = nullptr, *gate = nullptr;
+  float* part = nullptr;
+  float* apart = nullptr;
+  int nsplit = 0;
+  float2* amax = nullptr;
+  float* logits_d = nullptr;
+  uint16_t *tok_d = nullptr, *hist_d = nullptr, *prefix_d = nullptr;
+  int* ctr_d = nullptr;
+  int TC = 0;
+  float* px = nullptr;
+  half_t *pxn = nullptr, *pqkv = nullptr, *patt = nullptr, *pgate = nullptr;
+  int s_qkv = 1, s_wo = 1, s_w13 = 1, s_w2 = 1;
+  int nseq = 0, pos = 0;  // active batch, filled positions
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t gexec = nullptr;
+  int graph_nseq = 0;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  double last_ms = 0.0;
+};
+
+namespace {
+
+int dfail(ane_decoder* d, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (d) d->err = buf;
+  return code;
+}
+
+#define DCHK(op, expr)                                                                                   \
+  do {                                                                                                   \
+    hipError_t _h = (expr);                                                                              \
+    if (_h != hipSuccess)                                                                                \
+      return dfail(d, ANE_ERR_HIP, "storiesane decode %s: %s: %s", op, #expr, hipGetErrorString(_h));    \
+  } while (0)
+
+template <typename T>
+hipError_t dalloc(ane_decoder* d, T** p, size_t n) {
+  void* q = nullptr;
+  hipError_t e = hipMalloc(&q, n * sizeof(T) > 0 ? n * sizeof(T) : 16);
+  if (e != hipSuccess) return e;
+  d->allocs.push_back(q);
+  *p = (T*)q;
+  return hipSuccess;
+}
+
+void free_all(ane_decoder* d) {
+  (void)hipSetDevice(d->cfg.device);
+  if (d->stream) (void)hipStreamSynchronize(d->stream);
+  if (d->gexec) (void)hipGraphExecDestroy(d->gexec);
+  if (d->graph) (void)hipGraphDestroy(d->graph);
+  d->gexec = nullptr;
+  d->graph = nullptr;
+  for (void* p : d->allocs) (void)hipFree(p);
+  d->allocs.clear();
+  if (d->ev0) (void)hipEventDestroy(d->ev0);
+  if (d->ev1) (void)hipEventDestroy(d->ev1);
+  d->ev0 = d->ev1 = nullptr;
+  if (d->stream) (void)hipStreamDestroy(d->stream);
+  d->stream = nullptr;
+}
+
+int validate(const ane_decode_cfg& c, std::string* why) {
+  char buf[256];
+  buf[0] = 0;
+  if (c.heads <= 0 || c.kv_heads <= 0 || c.dim != 64 * c.heads)
+    snprintf(buf, sizeof buf, "dim=%d must be 64 * heads (heads=%d)", c.dim, c.heads);
+  else if (c.heads % c.kv_heads || c.heads / c.kv_heads > 4)
+    snprintf(buf, sizeof buf, "heads=%d must be 1..4 times kv_heads=%d", c.heads, c.kv_heads);
+  else if (c.dim > 1024)
+    snprintf(buf, sizeof buf, "dim=%d exceeds 1024", c.dim);
+  else if (c.hidden <= 0 || c.hidden % 64)
+    snprintf(buf, sizeof buf, "hidden=%d must be a positive multiple of 64", c.hidden);
+  else if (c.vocab <= 0 || c.vocab % 32 || c.vocab > 65536)
+    snprintf(buf, sizeof buf, "vocab=%d must be a multiple of 32 up to 65536", c.vocab);
+  else if (c.layers <= 0)
+    snprintf(buf, sizeof buf, "layers=%d", c.layers);
+  else if (c.max_batch < 1 || c.max_batch > kDecRows)
+    snprintf(buf, sizeof buf, "max_batch=%d must be 1..%d", c.max_batch, kDecRows);
+  else if (c.max_ctx < 64 || c.max_ctx > 65536)
+    snprintf(buf, sizeof buf, "max_ctx=%d must be 64..65536", c.max_ctx);
+  if (buf[0]) {
+    *why = buf;
+    return ANE_ERR_ARG;
+  }
+  return ANE_OK;
+}
+
+int open_impl(ane_decoder* d) {
+  const char* op = "open";
+  const ane_decode_cfg& c = d->cfg;
+  d->D = c.dim; d->H = c.hidden; d->NH = c.heads; d->NKV = c.kv_heads; d->KVD = c.kv_heads * 64;
+  d->N1 = d->D + 2 * d->KVD; d->L = c.layers; d->V = c.vocab; d->B = c.max_batch; d->C = c.max_ctx;
+  const int D = d->D, H = d->H, N1 = d->N1, L = d->L, V = d->V, B = d->B, C = d->C;
+  d->nparams = dec_layout(c, &d->off, &d->off_embed, &d->off_gfinal);
+  DCHK(op, hipSetDevice(c.device));
+  DCHK(op, hipStreamCreateWithFlags(&d->stream, hipStreamNonBlocking));
+  DCHK(op, hipEventCreate(&d->ev0));
+  DCHK(op, hipEventCreate(&d->ev1));
+  DCHK(op, dalloc(d, &d->P, (size_t)d->nparams));
+  DCHK(op, dalloc(d, &d->wqkv, (size_t)L * N1 * D));
+  DCHK(op, dalloc(d, &d->wo, (size_t)L * D * D));
+  DCHK(op, dalloc(d, &d->w13, (size_t)L * 2 * H * D));
+  DCHK(op, dalloc(d, &d->w2, (size_t)L * D * H));
+  DCHK(op, dalloc(d, &d->embed_h, (size_t)V * D));
+  const size_t cache = (size_t)L * B * d->NKV * C * 64;
+  DCHK(op, dalloc(d, &d->kc, cache));
+  DCHK(op, dalloc(d, &d->vc, cache));
+  // RoPE tables (buildRoPETables, ane/train_util.go:183-202: f64 angle, fp32 cos/sin)
+  {
+    std::vector<float> cs((size_t)C * 32), sn((size_t)C * 32);
+    for (int p = 0; p < C; p++)
+      for (int i = 0; i < 32; i++) {
+        const double f = (double)p / std::pow(c.rope_theta, (double)(2 * i) / 64.0);
+        cs[(size_t)p * 32 + i] = (float)std::cos(f);
+        sn[(size_t)p * 32 + i] = (float)std::sin(f);
+      }
+    DCHK(op, dalloc(d, &d->rope_cos, cs.size()));
+    DCHK(op, dalloc(d, &d->rope_sin, sn.size()));
+    DCHK(op, hipMemcpy(d->rope_cos, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+    DCHK(op, hipMemcpy(d->rope_sin, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  }
+  const int R = kDecRows;
+  DCHK(op, dalloc(d, &d->x, (size_t)R * D));
+  DCHK(op, dalloc(d, &d->xn, (size_t)R * D));
+  DCHK(op, dalloc(d, &d->q, (size_t)R * D));
+  DCHK(op, dalloc(d, &d->att, (size_t)R * D));
+  DCHK(op, dalloc(d, &d->gate, (size_t)R * H));
+  d->s_qkv = skinny_splits(N1, D);
+  d->s_wo = skinny_splits(D, D);
+  d->s_w13 = skinny_splits(2 * H, D);
+  d->s_w2 = skinny_splits(D, H);
+  size_t pmax = (size_t)d->s_qkv * N1;
+  pmax = std::max(pmax, (size_t)d->s_wo * D);
+  pmax = std::max(pmax, (size_t)d->s_w13 * 2 * H);
+  pmax = std::max(pmax, (size_t)d->s_w2 * D);
+  DCHK(op, dalloc(d, &d->part, pmax * R));
+  d->nsplit = (C + kDecChunk - 1) / kDecChunk;
+  DCHK(op, dalloc(d, &d->apart, (size_t)B * d->NH * d->nsplit * 66));
+  DCHK(op, dalloc(d, &d->amax, (size_t)(V / 32) * R));
+  DCHK(op, dalloc(d, &d->logits_d, (size_t)R * V));
+  DCHK(op, dalloc(d, &d->tok_d, (size_t)R));
+  DCHK(op, dalloc(d, &d->hist_d, (size_t)C * R));
+  DCHK(op, dalloc(d, &d->prefix_d, (size_t)B * C));
+  DCHK(op, dalloc(d, &d->ctr_d, 2));
+  d->TC = std::max(kPrefillTokens, (C + 63) / 64 * 64);
+  DCHK(op, dalloc(d, &d->px, (size_t)d->TC * D));
+  DCHK(op, dalloc(d, &d->pxn, (size_t)d->TC * D));
+  DCHK(op, dalloc(d, &d->pqkv, (size_t)d->TC * N1));
+  DCHK(op, dalloc(d, &d->patt, (size_t)d->TC * D));
+  DCHK(op, dalloc(d, &d->pgate, (size_t)d->TC * H));
+  // rows beyond the active batch feed the 64-row GEMMs: keep them finite
+  DCHK(op, hipMemset(d->xn, 0, (size_t)R * D * 2));
+  DCHK(op, hipMemset(d->att, 0, (size_t)R * D * 2));
+  DCHK(op, hipMemset(d->gate, 0, (size_t)R * H * 2));
+  DCHK(op, hipMemset(d->x, 0, (size_t)R * D * 4));
+  DCHK(op, hipMemset(d->q, 0, (size_t)R * D * 2));
+  DCHK(op, hipMemset(d->tok_d, 0, (size_t)R * 2));
+  DCHK(op, hipMemset(d->ctr_d, 0, 8));
+  DCHK(op, hipDeviceSynchronize());
+  return ANE_OK;
+}
+
+hipError_t gemm(ane_decoder* d, const half_t* A, const half_t* Bw, int M, int N, int K, int epi, const EpiParams& p) {
+  GemmArgs g;
+  g.A = A; g.B = Bw; g.lda = K; g.ldb = K; g.M = M; g.N = N; g.K = K; g.a_t = false; g.b_t = false;
+  return gemm_run(g, epi, p, d->stream);
+}
+
+// One decode step for the active batch; every position/step index is read
+// from ctr_d on the device, so the same launches replay as a graph.
+int enqueue_step(ane_decoder* d, float* logits, uint16_t* hist) {
+  const char* op = "step";
+  const int D = d->D, H = d->H, N1 = d->N1, nb = d->nseq;
+  const hipStream_t st = d->stream;
+  DCHK(op, dec_embed_norm(d->x, d->xn, d->P + d->off_embed, d->tok_d, d->P + d->off[0].g_att, nb, D, d->V, st));
+  for (int l = 0; l < d->L; l++) {
+    const DecLayerOff& o = d->off[l];
+    half_t* kcl = d->kc + (size_t)l * d->B * d->NKV * d->C * 64;
+    half_t* vcl = d->vc + (size_t)l * d->B * d->NKV * d->C * 64;
+    SkinnyArgs s;
+    memset(&s, 0, sizeof s);
+    s.X = d->xn; s.ldx = D; s.W = d->wqkv + (size_t)l * N1 * D; s.ldw = D; s.N = N1; s.K = D;
+    s.splits = d->s_qkv; s.partial = d->part;
+    DCHK(op, skinny_gemm(s, 0, st));
+    DecQkvArgs qa;
+    qa.partial = d->part; qa.splits = d->s_qkv; qa.ctr = d->ctr_d; qa.rope_cos = d->rope_cos;
+    qa.rope_sin = d->rope_sin; qa.q = d->q; qa.kc = kcl; qa.vc = vcl; qa.nb = nb; qa.NH = d->NH;
+    qa.NKV = d->NKV; qa.max_ctx = d->C;
+    DCHK(op, dec_qkv_finish(qa, st));
+    DecAttnArgs aa;
+    aa.q = d->q; aa.kc = kcl; aa.vc = vcl; aa.ctr = d->ctr_d; aa.part = d->apart; aa.att = d->att; aa.nb = nb;
+    aa.NH = d->NH; aa.NKV = d->NKV; aa.max_ctx = d->C; aa.nsplit = d->nsplit; aa.scale = 0.125f;
+    DCHK(op, dec_attention(aa, st));
+    s.X = d->att; s.ldx = D; s.W = d->wo + (size_t)l * D * D; s.ldw = D; s.N = D; s.K = D; s.splits = d->s_wo;
+    DCHK(op, skinny_gemm(s, 0, st));
+    DCHK(op, dec_resid_norm(d->x, d->xn, d->part, d->s_wo, d->P + o.g_ffn, nb, D, st));
+    s.X = d->xn; s.ldx = D; s.W = d->w13 + (size_t)l * 2 * H * D; s.ldw = D; s.N = 2 * H; s.K = D;
+    s.splits = d->s_w13;
+    DCHK(op, skinny_gemm(s, 0, st));
+    DCHK(op, dec_swiglu(d->gate, d->part, d->s_w13, nb, H, st));
+    s.X = d->gate; s.ldx = H; s.W = d->w2 + (size_t)l * D * H; s.ldw = H; s.N = D; s.K = H; s.splits = d->s_w2;
+    DCHK(op, skinny_gemm(s, 0, st));
+    const float* gnext = l + 1 < d->L ? d->P + d->off[l + 1].g_att : d->P + d->off_gfinal;
+    DCHK(op, dec_resid_norm(d->x, d->xn, d->part, d->s_w2, gnext, nb, D, st));
+  }
+  SkinnyArgs s;
+  memset(&s, 0, sizeof s);
+  s.X = d->xn; s.ldx = D; s.W = d->embed_h; s.ldw = D; s.N = d->V; s.K = D; s.splits = 1; s.amax = d->amax;
+  s.logits = logits; s.nvalid = d->V;
+  DCHK(op, skinny_gemm(s, 1, st));
+  DCHK(op, argmax_reduce(d->tok_d, hist, d->ctr_d + 1, d->amax, d->V / 32, nb, st));
+  DCHK(op, dec_advance(d->ctr_d, st));
+  return ANE_OK;
+}
+
+int copy_out(ane_decoder* d, uint16_t* next_tok, float* logits) {
+  const char* op = "copy out";
+  if (next_tok) DCHK(op, hipMemcpyAsync(next_tok, d->tok_d, (size_t)d->nseq * 2, hipMemcpyDeviceToHost, d->stream));
+  if (logits)
+    DCHK(op, hipMemcpyAsync(logits, d->logits_d, (size_t)d->nseq * d->V * 4, hipMemcpyDeviceToHost, d->stream));
+  DCHK(op, hipStreamSynchronize(d->stream));
+  return ANE_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t ane_decode_param_count(const ane_decode_cfg* cfg) {
+  if (!cfg) return -1;
+  return dec_layout(*cfg, nullptr, nullptr, nullptr);
+}
+
+extern "C" int ane_decode_open(const ane_decode_cfg* cfg, ane_decoder** out) {
+  if (!out) return ANE_ERR_ARG;
+  *out = nullptr;
+  ane_decoder* d = new ane_decoder();
+  *out = d;
+  if (!cfg) return dfail(d, ANE_ERR_ARG, "storiesane decode open: no config");
+  d->cfg = *cfg;
+  std::string why;
+  if (validate(*cfg, &why) != ANE_OK) return dfail(d, ANE_ERR_ARG, "storiesane decode open: %s", why.c_str());
+  int rc = open_impl(d);
+  if (rc != ANE_OK) free_all(d);
+  return rc;
+}
+
+extern "C" void ane_decode_destroy(ane_decoder* d) {
+  if (!d) return;
+  free_all(d);
+  delete d;
+}
+
+extern "C" const char* ane_decode_last_error(ane_decoder* d) { return d ? d->err.c_str() : "no decoder"; }
+
+extern "C" int ane_decode_set_params(ane_decoder* d, const float* params, int64_t n) {
+  const char* op = "set params";
+  if (!d || !d->stream) return ANE_ERR_STATE;
+  if (!params || n != d->nparams)
+    return dfail(d, ANE_ERR_ARG, "storiesane decode set params: len=%lld want=%lld", (long long)n,
+                 (long long)d->nparams);
+  const int D = d->D, H = d->H, KVD = d->KVD, N1 = d->N1;
+  const hipStream_t st = d->stream;
+  DCHK(op, hipSetDevice(d->cfg.device));
+  DCHK(op, hipMemcpyAsync(d->P, params, (size_t)n * 4, hipMemcpyHostToDevice, st));
+  for (int l = 0; l < d->L; l++) {
+    const DecLayerOff& o = d->off[l];
+    half_t* q = d->wqkv + (size_t)l * N1 * D;
+    DCHK(op, f32_to_f16(q, d->P + o.wq, (size_t)D * D, st));
+    DCHK(op, f32_to_f16(q + (size_t)D * D, d->P + o.wk, (size_t)KVD * D, st));
+    DCHK(op, f32_to_f16(q + (size_t)(D + KVD) * D, d->P + o.wv, (size_t)KVD * D, st));
+    DCHK(op, f32_to_f16(d->wo + (size_t)l * D * D, d->P + o.wo, (size_t)D * D, st));
+    DCHK(op, interleave_w13(d->w13 + (size_t)l * 2 * H * D, d->P + o.w1, d->P + o.w3, H, D, st));
+    DCHK(op, f32_to_f16(d->w2 + (size_t)l * D * H, d->P + o.w2, (size_t)D * H, st));
+  }
+  DCHK(op, f32_to_f16(d->embed_h, d->P + d->off_embed, (size_t)d->V * D, st));
+  DCHK(op, hipStreamSynchronize(st));
+  d->params_set = true;
+  return ANE_OK;
+}
+
+extern "C" int ane_decode_prefill(ane_decoder* d, const uint16_t* prefix, int32_t nseq, int32_t plen,
+                                  uint16_t* next_tok, float* logits) {
+  const char* op = "prefill";
+  if (!d || !d->stream) return ANE_ERR_STATE;
+  if (!d->params_set) return dfail(d, ANE_ERR_STATE, "storiesane decode prefill: parameters not set");
+  if (!prefix || nseq < 1 || nseq > d->B)
+    return dfail(d, ANE_ERR_ARG, "storiesane decode prefill: nseq=%d want 1..%d", nseq, d->B);
+  if (plen < 64 || plen % 64 || plen >= d->C)
+    return dfail(d, ANE_ERR_ARG, "storiesane decode prefill: plen=%d must be a multiple of 64 below max_ctx=%d",
+                 plen, d->C);
+  const int D = d->D, H = d->H, N1 = d->N1;
+  const hipStream_t st = d->stream;
+  DCHK(op, hipSetDevice(d->cfg.device));
+  DCHK(op, hipMemcpyAsync(d->prefix_d, prefix, (size_t)nseq * plen * 2, hipMemcpyHostToDevice, st));
+  const int per = std::max(1, d->TC / plen);
+  for (int s0 = 0; s0 < nseq; s0 += per) {
+    const int n = std::min(per, nseq - s0), T = n * plen;
+    DCHK(op, embed_lookup(d->px, d->P + d->off_embed, d->prefix_d + (size_t)s0 * plen, T, D, d->V, st));
+    for (int l = 0; l < d->L; l++) {
+      const DecLayerOff& o = d->off[l];
+      half_t* kcl = d->kc + (size_t)l * d->B * d->NKV * d->C * 64;
+      half_t* vcl = d->vc + (size_t)l * d->B * d->NKV * d->C * 64;
+      DCHK(op, rmsnorm_f16(d->pxn, d->px, nullptr, nullptr, d->P + o.g_att, T, D, st));
+      {
+        EpiParams p;
+        p.C = d->pqkv; p.ldc = N1;
+        DCHK(op, gemm(d, d->pxn, d->wqkv + (size_t)l * N1 * D, T, N1, D, EPI_STORE_H, p));
+      }
+      DCHK(op, prefill_kv_write(d->pqkv, kcl, vcl, d->rope_cos, d->rope_sin, s0, n, plen, d->NH, d->NKV, d->C, st));
+      {
+        PrefillAttnArgs a;
+        a.qkv = d->pqkv; a.ldq = N1; a.kc = kcl; a.vc = vcl; a.out = d->patt; a.seq0 = s0; a.nseq = n; a.S = plen;
+        a.NH = d->NH; a.NKV = d->NKV; a.max_ctx = d->C; a.scale = 0.125f;
+        DCHK(op, prefill_attention(a, st));
+      }
+      {
+        EpiParams p;
+        p.C = d->px; p.ldc = D; p.R = d->px;
+        DCHK(op, gemm(d, d->patt, d->wo + (size_t)l * D * D, T, D, D, EPI_RESID, p));
+      }
+      DCHK(op, rmsnorm_f16(d->pxn, d->px, nullptr, nullptr, d->P + o.g_ffn, T, D, st));
+      {
+        EpiParams p;
+        p.C = d->pgate; p.ldc = H;
+        DCHK(op, gemm(d, d->pxn, d->w13 + (size_t)l * 2 * H * D, T, 2 * H, D, EPI_SWIGLU, p));
+      }
+      {
+        EpiParams p;
+        p.C = d->px; p.ldc = D; p.R = d->px;
+        DCHK(op, gemm(d, d->pgate, d->w2 + (size_t)l * D * H, T, D, H, EPI_RESID, p));
+      }
+    }
+    DCHK(op, gather_last_rows(d->x + (size_t)s0 * D, d->px, n, plen, D, st));
+  }
+  d->nseq = nseq;
+  DCHK(op, dec_resid_norm(d->x, d->xn, nullptr, 0, d->P + d->off_gfinal, nseq, D, st));
+  SkinnyArgs s;
+  memset(&s, 0, sizeof s);
+  s.X = d->xn; s.ldx = D; s.W = d->embed_h; s.ldw = D; s.N = d->V; s.K = D; s.splits = 1; s.amax = d->amax;
+  s.logits = logits ? d->logits_d : nullptr; s.nvalid = d->V;
+  DCHK(op, skinny_gemm(s, 1, st));
+  DCHK(op, argmax_reduce(d->tok_d, nullptr, nullptr, d->amax, d->V / 32, nseq, st));
+  DCHK(op, dec_set_ctr(d->ctr_d, plen, 0, st));
+  d->pos = plen;
+  return copy_out(d, next_tok, logits);
+}
+
+extern "C" int ane_decode_step(ane_decoder* d, const uint16_t* in_tok, uint16_t* next_tok, float* logits) {
+  const char* op = "step";
+  if (!d || !d->stream) return ANE_ERR_STATE;
+  if (d->nseq == 0) return dfail(d, ANE_ERR_STATE, "storiesane decode step: no prefill");
+  if (d->pos >= d->C) return dfail(d, ANE_ERR_ARG, "storiesane decode step: cache full (max_ctx=%d)", d->C);
+  DCHK(op, hipSetDevice(d->cfg.device));
+  if (in_tok) DCHK(op, hipMemcpyAsync(d->tok_d, in_tok, (size_t)d->nseq * 2, hipMemcpyHostToDevice, d->stream));
+  int rc = enqueue_step(d, logits ? d->logits_d : nullptr, nullptr);
+  if (rc != ANE_OK) return rc;
+  d->pos++;
+  return copy_out(d, next_tok, logits);
+}
+
+extern "C" int ane_decode_generate(ane_decoder* d, int32_t nsteps, uint16_t* out_tok) {
+  const char* op = "generate";
+  if (!d || !d->stream) return ANE_ERR_STATE;
+  if (d->nseq == 0) return dfail(d, ANE_ERR_STATE, "storiesane decode generate: no prefill");
+  if (nsteps < 0 || d->pos + nsteps > d->C)
+    return dfail(d, ANE_ERR_ARG, "storiesane decode generate: %d steps from position %d exceed max_ctx=%d", nsteps,
+                 d->pos, d->C);
+  if (nsteps == 0) return ANE_OK;
+  const hipStream_t st = d->stream;
+  DCHK(op, hipSetDevice(d->cfg.device));
+  if (!d->gexec || d->graph_nseq != d->nseq) {
+    if (d->gexec) (void)hipGraphExecDestroy(d->gexec);
+    if (d->graph) (void)hipGraphDestroy(d->graph);
+    d->gexec = nullptr;
+    d->graph = nullptr;
+    DCHK(op, hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue_step(d, nullptr, d->hist_d);
+    hipGraph_t g = nullptr;
+    hipError_t ce = hipStreamEndCapture(st, &g);
+    if (rc != ANE_OK) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    DCHK(op, ce);
+    d->graph = g;
+    DCHK(op, hipGraphInstantiate(&d->gexec, g, nullptr, nullptr, 0));
+    d->graph_nseq = d->nseq;
+  }
+  DCHK(op, dec_set_ctr(d->ctr_d, d->pos, 0, st));  // history rows count from 0 for this call
+  DCHK(op, hipEventRecord(d->ev0, st));
+  for (int i = 0; i < nsteps; i++) DCHK(op, hipGraphLaunch(d->gexec, st));
+  DCHK(op, hipEventRecord(d->ev1, st));
+  if (out_tok)
+    DCHK(op, hipMemcpyAsync(out_tok, d->hist_d, (size_t)nsteps * d->nseq * 2, hipMemcpyDeviceToHost, st));
+  DCHK(op, hipStreamSynchronize(st));
+  float ms = 0.f;
+  DCHK(op, hipEventElapsedTime(&ms, d->ev0, d->ev1));
+  d->last_ms = ms;
+  d->pos += nsteps;
+  return ANE_OK;
+}
+
+extern "C" int32_t ane_decode_position(ane_decoder* d) { return d ? d->pos : -1; }
+
+extern "C" double ane_decode_last_ms(ane_decoder* d) { return d ? d->last_ms : 0.0; }

@@ -74,6 +74,44 @@ def train_bench(ane, arch, steps, batch=16):
                                 / 1e12, 1)}
 
 
+def decode_bytes_per_step(cfg, batch, ctx):
+    """Algorithmic HBM bytes of one decode step with `ctx` keys per sequence:
+    fp16 weights once, K and V of every cached position, the new K/V rows,
+    fp16 logits."""
+    D, H, V, L, KVD = cfg.dim, cfg.hidden, cfg.vocab, cfg.layers, cfg.kv_heads * cfg.head_dim
+    weights = 2 * (L * (D * (D + 2 * KVD) + D * D + 3 * D * H) + V * D)
+    kv_row = L * 2 * KVD * 2  # bytes of one position's K and V over all layers
+    return weights + batch * kv_row * ctx + batch * kv_row + batch * V * 2
+
+
+def decode_bench(ane, steps, batch=64, plen=1024):
+    """GQA decode (12 layers, dim 768, 12 query / 4 kv
+    heads, vocab 32000, SwiGLU 2048, weights N(0, 0.02) seed 4), 64
+    sequences prefilled with 1024 uniform ids, then `steps` greedy steps
+    on the device (replayed HIP graph)."""
+    cfg = ane.decode_gqa()
+    params = ane.init_params(cfg, seed=4, std=0.02)
+    prefix = np.random.default_rng(4).integers(0, cfg.vocab, (batch, plen)).astype(np.uint16)
+    dec = ane.Decoder(cfg, params, max_batch=batch, max_ctx=plen + steps)
+    dec.Prefill(prefix)
+    dec.Generate(4)  # capture + warm-up
+    t0 = time.perf_counter()
+    dec.Prefill(prefix)
+    prefill_s = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    toks = dec.Generate(steps)
+    wall = time.perf_counter() - t0
+    ms = dec.LastMs()
+    dec.Close()
+    alg = sum(decode_bytes_per_step(cfg, batch, plen + 1 + s) for s in range(steps))
+    gbs = alg / (ms * 1e-3) / 1e9
+    return {"value": round(batch * steps / (ms * 1e-3), 1), "unit": "tokens/s", "batch": batch, "prefix": plen,
+            "steps": steps, "ms_per_step": round(ms / steps, 4), "wall_ms": round(wall * 1e3, 2),
+            "hbm_gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "alg_bytes": alg,
+            "prefill_ms": round(prefill_s * 1e3, 2), "prefill_tok_s": round(batch * plen / prefill_s, 1),
+            "tokens_head": toks[0, :8].tolist()}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -85,6 +123,8 @@ def main():
     ap.add_argument("--no-profile", action="store_true", help="time without per-launch HIP events")
     ap.add_argument("--no-train", action="store_true", help="skip the B16 training-step leg")
     ap.add_argument("--train-steps", type=int, default=5)
+    ap.add_argument("--no-decode", action="store_true", help="skip the GQA decode leg")
+    ap.add_argument("--decode-steps", type=int, default=128)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the forward shards "
@@ -105,9 +145,6 @@ def main():
     for _ in range(args.warmup):
         eng.EvalLossWindows(pos)
     eng.Sync()
-    if not args.no_profile:
-        eng.ProfileEnable(True)
-        eng.ProfileRead(reset=True)
     t0 = time.perf_counter()
     for _ in range(args.steps):
         loss, _ = eng.EvalLossWindows(pos)
@@ -124,7 +161,15 @@ def main():
                       "arch": args.arch, "batch": B, "seq": S, "tokens_per_step": B * S},
            "loss": round(loss, 6)}
     if not args.no_profile:
+        # a second pass of the same steps with HIP events around every launch
+        # (the timed pass above runs without them)
+        eng.ProfileEnable(True)
+        eng.ProfileRead(reset=True)
+        for _ in range(args.steps):
+            eng.EvalLossWindows(pos)
+        eng.Sync()
         prof = eng.ProfileRead(reset=True)
+        eng.ProfileEnable(False)
         gemm_cls = ["qkv_gemm", "wo_gemm", "ffn_up_gemm", "ffn_down_gemm", "classifier_gemm"]
         dom = max(prof, key=lambda k: prof[k]["ms"])
         d = prof[dom]
@@ -141,6 +186,8 @@ def main():
     eng.Destroy()
     if not args.no_train:
         out["train_step_b16"] = train_bench(ane, args.arch, args.train_steps)
+    if not args.no_decode:
+        out["decode"] = decode_bench(ane, args.decode_steps)
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(cfg, params, tok, tgt, threads)

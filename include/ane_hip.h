@@ -223,6 +223,48 @@ int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm,
                          int iters, float *avg_ms);
 const char *ane_debug_last_error(void);
 
+/* ---- greedy KV-cache decoder (grouped-query attention) --------------------
+ * No counterpart in the reference, which evaluates whole windows only
+ * (ane/engine.go:954-1038).  Serves the decode benchmark's Llama2-style
+ * model built from the reference's primitives: gain RMSNorm
+ * (ane/stories/cpu.go:97-111), RoPE (ane/train_util.go:183-224), causal
+ * softmax attention (ane/common.go:61-89) with kv_heads key/value heads
+ * shared by heads/kv_heads query heads each, SwiGLU, tied classifier
+ * (ane/stories/cpu.go:303-327), greedy = first index of the maximum logit.
+ * Parameters: the flat LLAMA2 order of ane_param_layout() with Wk, Wv of
+ * kv_heads*64 rows.  The fp16 KV cache holds max_ctx positions for each of
+ * max_batch (<= 64) sequences. */
+typedef struct {
+  int32_t dim, hidden, heads, kv_heads, layers, vocab;
+  int32_t max_batch; /* sequences decoded together, 1..64 */
+  int32_t max_ctx;   /* cache positions per sequence: prefix + decode steps */
+  double rope_theta;
+  int32_t device;
+} ane_decode_cfg;
+
+typedef struct ane_decoder ane_decoder;
+
+int ane_decode_open(const ane_decode_cfg *cfg, ane_decoder **out);
+void ane_decode_destroy(ane_decoder *d);
+const char *ane_decode_last_error(ane_decoder *d);
+int64_t ane_decode_param_count(const ane_decode_cfg *cfg);
+int ane_decode_set_params(ane_decoder *d, const float *params, int64_t n);
+/* Runs the prefix [nseq][plen] (plen % 64 == 0, plen < max_ctx) into the
+ * cache and returns the greedy token after it (next_tok [nseq]) and,
+ * optionally, the fp32 logits of the last prefix position [nseq][vocab]. */
+int ane_decode_prefill(ane_decoder *d, const uint16_t *prefix, int32_t nseq, int32_t plen, uint16_t *next_tok,
+                       float *logits);
+/* One decode step: feeds in_tok [nseq] (NULL: the previous greedy tokens)
+ * at the next position; returns the greedy tokens and optional logits. */
+int ane_decode_step(ane_decoder *d, const uint16_t *in_tok, uint16_t *next_tok, float *logits);
+/* nsteps greedy steps without host round trips (replayed HIP graph of one
+ * step); out_tok [nsteps][nseq] receives the tokens each step produced. */
+int ane_decode_generate(ane_decoder *d, int32_t nsteps, uint16_t *out_tok);
+/* current cache length (positions filled) of the active batch */
+int32_t ane_decode_position(ane_decoder *d);
+/* device time of the last ane_decode_generate call (ms, HIP events) */
+double ane_decode_last_ms(ane_decoder *d);
+
 #ifdef __cplusplus
 }
 #endif

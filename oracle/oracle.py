@@ -27,6 +27,11 @@ class OrcCfg(C.Structure):
                 ("arch", C.c_int32), ("grad_mode", C.c_int32), ("rope_theta", C.c_double)]
 
 
+class OrcDecCfg(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("hidden", C.c_int32), ("heads", C.c_int32), ("kv_heads", C.c_int32),
+                ("layers", C.c_int32), ("vocab", C.c_int32), ("rope_theta", C.c_double)]
+
+
 class OrcAdam(C.Structure):
     _fields_ = [(n, C.c_float) for n in (
         "lr", "beta1", "beta2", "eps", "weight_decay", "grad_clip", "embed_lr_mult",
@@ -75,6 +80,10 @@ def lib():
         L.orc_drand48_seed.argtypes = [C.c_int64]
         L.orc_drand48_next.restype = C.c_double
         L.orc_drand48_next.argtypes = [C.POINTER(C.c_uint64)]
+        L.orc_dec_param_count.restype = C.c_size_t
+        L.orc_dec_param_count.argtypes = [C.POINTER(OrcDecCfg)]
+        L.orc_decode.restype = None
+        L.orc_decode.argtypes = [C.POINTER(OrcDecCfg), fp, u16, C.c_int, C.c_int, u16, C.c_int, C.c_int, u16, fp]
         ncpu = os.cpu_count() or 1
         L.orc_set_threads(min(ncpu, 64))
         L.orc_set_parallel_linear(1)
@@ -206,6 +215,32 @@ def softcap(x):
     x = np.ascontiguousarray(x.copy(), dtype=np.float32)
     lib().orc_softcap(_f(x), x.size)
     return x
+
+
+def dec_cfg_struct(cfg) -> OrcDecCfg:
+    return OrcDecCfg(cfg.dim, cfg.hidden, cfg.heads, cfg.kv_heads, cfg.layers, cfg.vocab, float(cfg.rope_theta))
+
+
+def dec_param_count(cfg) -> int:
+    return int(lib().orc_dec_param_count(C.byref(dec_cfg_struct(cfg))))
+
+
+def decode(cfg, params, prefix, nsteps, forced=None, want_logits=False, threads=None):
+    """Greedy KV-cache decoding (oracle/refdecode.c).  prefix: uint16
+    [nseq, plen].  Returns (tokens [nseq, nsteps+1], logits [nseq, nsteps+1, V]
+    or None); tokens[:, 0] follows the prefix, tokens[:, i+1] decode step i,
+    whose input is forced[:, i] if given, else tokens[:, i]."""
+    prefix = np.ascontiguousarray(prefix, dtype=np.uint16)
+    nseq, plen = prefix.shape
+    if forced is not None:
+        forced = np.ascontiguousarray(forced, dtype=np.uint16).reshape(nseq, nsteps)
+    toks = np.zeros((nseq, nsteps + 1), np.uint16)
+    lg = np.zeros((nseq, nsteps + 1, cfg.vocab), np.float32) if want_logits else None
+    th = threads or min(nseq, os.cpu_count() or 1)
+    lib().orc_decode(C.byref(dec_cfg_struct(cfg)), _f(params), _u16(prefix), nseq, plen,
+                     _u16(forced) if forced is not None else None, int(nsteps), int(th), _u16(toks),
+                     _f(lg) if lg is not None else None)
+    return toks, lg
 
 
 def drand48_stream(seed, n):

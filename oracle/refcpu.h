@@ -94,6 +94,24 @@ void orc_softcap(float *x, size_t n);
 uint64_t orc_drand48_seed(int64_t seed);
 double orc_drand48_next(uint64_t *state);
 
+/* --- greedy KV-cache decoding (refdecode.c) ----------------------------
+ * Llama2-style model with grouped-query attention: kv_heads key/value
+ * heads, each shared by heads/kv_heads query heads. */
+typedef struct {
+  int32_t dim, hidden, heads, kv_heads, layers, vocab;
+  double rope_theta;
+} orc_dec_cfg;
+
+size_t orc_dec_param_count(const orc_dec_cfg *c);
+
+/* prefix: [nseq][plen] ids.  Step i (0-based) feeds forced[b][i] when
+ * forced is non-NULL ([nseq][nsteps]), else the previous greedy token, at
+ * position plen + i.  tokens_out: [nseq][nsteps+1], entry 0 = argmax of the
+ * logits at position plen-1, entry i+1 = argmax after step i.  logits_out
+ * (optional): [nseq][nsteps+1][vocab].  Sequences run on `threads` threads. */
+void orc_decode(const orc_dec_cfg *c, const float *params, const uint16_t *prefix, int nseq, int plen,
+                const uint16_t *forced, int nsteps, int threads, uint16_t *tokens_out, float *logits_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,151 @@
+"""Greedy KV-cache decoding on the GPU against the CPU decode oracle
+(oracle/refdecode.c, pinned in tests/test_oracle_decode.py).
+
+Logits are compared at max-abs <= 2e-2 (fp16 weights, activations and KV
+cache; fp32 accumulation), the contract's logit tolerance.  Greedy choices
+are checked the way a tolerance allows: the token the GPU picks must have an
+oracle logit within 2e-2 of the oracle's maximum (an exact tie-break between
+logits closer than the tolerance is not a parity statement).
+"""
+import numpy as np
+import pytest
+
+import ane
+import oracle
+from ane import _lib
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def _setup(cfg, nseq, plen, seed, std=0.05):
+    p = ane.init_params(cfg, seed=seed, std=std)
+    r = np.random.default_rng(seed + 1)
+    prefix = r.integers(0, cfg.vocab, (nseq, plen)).astype(np.uint16)
+    return p, prefix
+
+
+def _check_choice(gpu_tok, ref_logits):
+    top = ref_logits.max(-1)
+    picked = np.take_along_axis(ref_logits, gpu_tok[..., None].astype(np.int64), -1)[..., 0]
+    assert np.all(picked >= top - TOL), (picked - top).min()
+
+
+def test_prefill_and_forced_steps_match_oracle():
+    cfg = ane.tiny_decode()
+    nseq, plen, nsteps = 3, 128, 6
+    p, prefix = _setup(cfg, nseq, plen, 11)
+    forced = np.random.default_rng(12).integers(0, cfg.vocab, (nseq, nsteps)).astype(np.uint16)
+    ref_tok, ref_lg = oracle.decode(cfg, p, prefix, nsteps, forced=forced, want_logits=True)
+    dec = ane.Decoder(cfg, p, max_batch=4, max_ctx=256)
+    try:
+        t0, lg0 = dec.Prefill(prefix, want_logits=True)
+        errs = [np.abs(lg0 - ref_lg[:, 0]).max()]
+        _check_choice(t0, ref_lg[:, 0])
+        np.testing.assert_array_equal(t0, lg0.argmax(-1))
+        for i in range(nsteps):
+            ti, lgi = dec.Step(forced[:, i], want_logits=True)
+            errs.append(np.abs(lgi - ref_lg[:, i + 1]).max())
+            _check_choice(ti, ref_lg[:, i + 1])
+        assert dec.Position() == plen + nsteps
+    finally:
+        dec.Close()
+    print("decode logits max-abs err per step", [f"{e:.2e}" for e in errs])
+    assert max(errs) <= TOL
+
+
+def test_long_prefix_multi_chunk_attention():
+    """1024-token prefix: prefill attention streams 8 key chunks, decode
+    attention merges 5 context splits (max_ctx 1152)."""
+    cfg = ane.tiny_decode(layers=1)
+    nseq, plen, nsteps = 2, 1024, 3
+    p, prefix = _setup(cfg, nseq, plen, 21)
+    forced = np.random.default_rng(22).integers(0, cfg.vocab, (nseq, nsteps)).astype(np.uint16)
+    ref_tok, ref_lg = oracle.decode(cfg, p, prefix, nsteps, forced=forced, want_logits=True)
+    dec = ane.Decoder(cfg, p, max_batch=2, max_ctx=1152)
+    try:
+        _, lg0 = dec.Prefill(prefix, want_logits=True)
+        errs = [np.abs(lg0 - ref_lg[:, 0]).max()]
+        for i in range(nsteps):
+            _, lgi = dec.Step(forced[:, i], want_logits=True)
+            errs.append(np.abs(lgi - ref_lg[:, i + 1]).max())
+    finally:
+        dec.Close()
+    print("long-prefix logits max-abs err", [f"{e:.2e}" for e in errs])
+    assert max(errs) <= TOL
+
+
+def test_generate_graph_equals_eager_steps_and_oracle_choices():
+    cfg = ane.tiny_decode()
+    nseq, plen, nsteps = 4, 64, 12
+    p, prefix = _setup(cfg, nseq, plen, 31, std=0.08)
+    dec = ane.Decoder(cfg, p, max_batch=8, max_ctx=128)
+    try:
+        t0, _ = dec.Prefill(prefix)
+        gen = dec.Generate(nsteps)
+        assert gen.shape == (nseq, nsteps)
+        assert dec.Position() == plen + nsteps
+        dec.Prefill(prefix)
+        eager = np.stack([dec.Step()[0] for _ in range(nsteps)], 1)
+        # a second Generate call replays the same graph from the new position
+        more = dec.Generate(3)
+    finally:
+        dec.Close()
+    np.testing.assert_array_equal(gen, eager)
+    assert more.shape == (nseq, 3)
+    # every greedy choice is (to tolerance) the oracle's argmax given the same history
+    inputs = np.concatenate([t0[:, None], gen[:, :-1]], 1)
+    _, ref_lg = oracle.decode(cfg, p, prefix, nsteps, forced=inputs, want_logits=True)
+    _check_choice(t0, ref_lg[:, 0])
+    _check_choice(gen, ref_lg[:, 1:])
+
+
+def test_full_size_gqa_model_matches_oracle():
+    """The decode benchmark's model (12 layers, dim 768, 12/4 heads,
+    vocab 32000), two sequences, 64-token prefix, three forced steps."""
+    cfg = ane.decode_gqa()
+    nseq, plen, nsteps = 2, 64, 3
+    p, prefix = _setup(cfg, nseq, plen, 4, std=0.02)
+    forced = np.random.default_rng(41).integers(0, cfg.vocab, (nseq, nsteps)).astype(np.uint16)
+    _, ref_lg = oracle.decode(cfg, p, prefix, nsteps, forced=forced, want_logits=True)
+    dec = ane.Decoder(cfg, p, max_batch=64, max_ctx=1152)
+    try:
+        _, lg0 = dec.Prefill(prefix, want_logits=True)
+        errs = [np.abs(lg0 - ref_lg[:, 0]).max()]
+        for i in range(nsteps):
+            _, lgi = dec.Step(forced[:, i], want_logits=True)
+            errs.append(np.abs(lgi - ref_lg[:, i + 1]).max())
+    finally:
+        dec.Close()
+    print("full-size decode logits max-abs err", [f"{e:.2e}" for e in errs])
+    assert max(errs) <= TOL
+
+
+def test_decoder_errors():
+    cfg = ane.tiny_decode()
+    p, prefix = _setup(cfg, 2, 64, 51)
+    with pytest.raises(ane.EngineError) as ei:
+        ane.Decoder(cfg, p, max_batch=65)
+    assert ei.value.code == _lib.ANE_ERR_ARG
+    dec = ane.Decoder(cfg, p, max_batch=2, max_ctx=128)
+    try:
+        with pytest.raises(ane.EngineError) as ei:
+            dec.Step()
+        assert ei.value.code == _lib.ANE_ERR_STATE
+        with pytest.raises(ane.EngineError) as ei:
+            dec.Prefill(prefix[:, :40])
+        assert ei.value.code == _lib.ANE_ERR_ARG and "multiple of 64" in str(ei.value)
+        with pytest.raises(ane.EngineError):
+            dec.Prefill(np.zeros((3, 64), np.uint16))
+        dec.Prefill(prefix)
+        with pytest.raises(ane.EngineError) as ei:
+            dec.Generate(65)
+        assert ei.value.code == _lib.ANE_ERR_ARG
+        with pytest.raises(ane.EngineError):
+            dec.SetParams(p[:-1])
+    finally:
+        dec.Close()
+    with pytest.raises(ane.EngineError) as ei:
+        dec.Step()
+    assert ei.value.code == _lib.ANE_ERR_CLOSED

@@ -152,3 +152,31 @@ def grads_flat(cfg, P):
         if t.grad is not None:
             g[off:off + t.numel()] = t.grad.detach().numpy().reshape(-1)
     return g
+
+
+def gqa_logits(cfg, P, tokens):
+    """Full causal forward of the Llama2-style model with grouped-query
+    attention (key/value head h // (heads // kv_heads) serves query head h),
+    float64.  tokens: int64 [B, S]; returns logits [B, S, V]."""
+    NH, NKV, D = cfg.heads, cfg.kv_heads, cfg.dim
+    hd = D // NH
+    out = []
+    for b in range(tokens.shape[0]):
+        tok = tokens[b]
+        S = tok.shape[0]
+        x = P["embed"][tok]
+        for l in range(cfg.layers):
+            pre = f"layers.{l}."
+            xn = rms(x) * P[pre + "g_att"]
+            q = rope(xn @ P[pre + "wq"].T, NH, cfg.rope_theta)
+            k = rope(xn @ P[pre + "wk"].T, NKV, cfg.rope_theta)
+            v = xn @ P[pre + "wv"].T
+            rep = NH // NKV
+            kf = k.view(S, NKV, hd).repeat_interleave(rep, dim=1).reshape(S, D)
+            vf = v.view(S, NKV, hd).repeat_interleave(rep, dim=1).reshape(S, D)
+            att = attention(q, kf, vf, NH, 1.0 / math.sqrt(hd))
+            x = x + att @ P[pre + "wo"].T
+            xn2 = rms(x) * P[pre + "g_ffn"]
+            x = x + (F.silu(xn2 @ P[pre + "w1"].T) * (xn2 @ P[pre + "w3"].T)) @ P[pre + "w2"].T
+        out.append((rms(x) * P["g_final"]) @ P["embed"].T)
+    return torch.stack(out)
