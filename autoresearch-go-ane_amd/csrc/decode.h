@@ -18,24 +18,49 @@ namespace ane {
 constexpr int kDecRows = 64;    // token rows of a decode step (max sequences)
 constexpr int kDecChunk = 256;  // keys per decode-attention split
 
-// partial[s][64][N] = X[64, s-th K range] . W[N, same range]^T  (EPI 0)
-// EPI 1 (splits == 1): per 32-column group and row, (max, first index of
-// the max) over columns < nvalid -> amax[N/32][64]; logits (optional)
-// receives the fp32 row [64][N].
+// MFMA-fragment-major layout of the decode-step operands.  A 32x32x16 MFMA
+// operand lane l takes row l%32 and eight k-values; with the k-slot map
+// k = 64*w + 32*(l/32) + 8*s + j (window w, step s = 0..3, j = 0..7) one
+// operand fragment is 64 lanes x 16 B, stored here as 1 KB contiguous so a
+// wave loads it with one fully coalesced instruction (8 whole cache lines)
+// instead of touching 32 rows.
+//   activations [64 rows][K]: fragment (w, s, tile = row/32)
+//   weights     [N rows][K]:  fragment (row group g = row/32, w, s)
+__device__ __host__ __forceinline__ size_t act_frag_off(int t, int k) {
+  const int w = k >> 6, kk = k & 63;
+  const int lane = (t & 31) + 32 * (kk >> 5), s = (kk >> 3) & 3;
+  return ((((size_t)(w * 4 + s) * 2 + (t >> 5)) * 64 + lane) << 3) + (kk & 7);
+}
+// row-major fp16 W [N][K] -> fragment-major (N % 32 == 0, K % 64 == 0)
+hipError_t weight_to_frag(half_t* dst, const half_t* src, int N, int K, hipStream_t s);
+
+// Y = X[64, K] . W[N, K]^T for the rows t < nb, K split over the waves of
+// one block and added in a fixed order (deterministic), epilogue fused:
+enum SkinnyEpi {
+  SK_RESID = 0,   // x[t][n] += Y                        (Wo, W2: residual add)
+  SK_QKV = 1,     // q|k|v rows: RoPE at ctr[0] on q and k; q -> q[t], k, v -> cache
+  SK_SWIGLU = 2,  // W1|W3 interleaved by 32 rows: gate[t][j] = silu(h1) * h3 (fragment layout, K = N/2)
+  SK_ARGMAX = 3,  // per 32-column group: (max, first index) over n < nvalid -> amax[N/32][64]
+};
 struct SkinnyArgs {
-  const half_t* X;  // [64, K], ld = ldx
-  int ldx;
-  const half_t* W;  // [N, K], ld = ldw
-  int ldw;
-  int N, K, splits;  // N % 32 == 0, K % (64 * splits) == 0
-  float* partial;
-  float2* amax;
-  float* logits;
+  const half_t* X;  // [64, K] activation fragments (act_frag_off)
+  const half_t* W;  // [N, K] weight fragments (weight_to_frag)
+  int N, K, nb;     // N % 32 == 0 (64 for SK_SWIGLU), K % 64 == 0, 1 <= nb <= 64
+  float* x;         // SK_RESID: [64][N] fp32
+  const int* ctr;   // SK_QKV: ctr[0] = position
+  const float* rope_cos;
+  const float* rope_sin;
+  half_t* q;        // SK_QKV: [64][NH*64]
+  half_t* kc;       // SK_QKV: layer cache base [Bcap][NKV][max_ctx][64]
+  half_t* vc;
+  int NH, NKV, max_ctx;
+  half_t* gate;     // SK_SWIGLU: [64][N/2]
+  float2* amax;     // SK_ARGMAX
+  float* logits;    // SK_ARGMAX, optional [64][N] fp32
   int nvalid;
 };
+// K <= 2048 (1024 for SK_SWIGLU): one block holds the whole K range
 hipError_t skinny_gemm(const SkinnyArgs& a, int epi, hipStream_t s);
-// smallest split count that gives >= 256 waves with K ranges of whole 64s
-int skinny_splits(int N, int K);
 
 // tok_out[b] = argmax over groups (first index on ties) for b < nb;
 // hist (optional) [..][nb]: row *step receives the same tokens.
@@ -48,31 +73,12 @@ hipError_t dec_advance(int* ctr, hipStream_t s);
 hipError_t dec_set_ctr(int* ctr, int pos, int step, hipStream_t s);
 
 // x[b] = embed[tok_b] (zero row if tok_b >= V); xn[b] = fp16(rmsnorm(x[b]) * g)
+// (xn, att and gate of the decode rows are in the activation fragment layout)
 hipError_t dec_embed_norm(float* x, half_t* xn, const float* embed, const uint16_t* tok, const float* g, int nb,
                           int D, int V, hipStream_t s);
 
-// x[b] += sum_s partial[s][b]; xn[b] = fp16(rmsnorm(x[b]) * g)   (partial may be null: norm only)
-hipError_t dec_resid_norm(float* x, half_t* xn, const float* partial, int splits, const float* g, int nb, int D,
-                          hipStream_t s);
-
-// gate[b][j] = silu(h1) * h3 with h1, h3 the split sums of the W1|W3 rows
-// interleaved in 32-row blocks (col (j/32)*64 + j%32 and +32)
-hipError_t dec_swiglu(half_t* gate, const float* partial, int splits, int nb, int H, hipStream_t s);
-
-// Split sums of the fused q|k|v projection at position *ctr: q (RoPE) ->
-// q_out [64][NH*64]; k (RoPE), v -> cache [.. b][kvh][pos][64] of the layer.
-struct DecQkvArgs {
-  const float* partial;
-  int splits;
-  const int* ctr;
-  const float* rope_cos;  // [max_ctx][32]
-  const float* rope_sin;
-  half_t* q;
-  half_t* kc;  // layer base, [Bcap][NKV][max_ctx][64]
-  half_t* vc;
-  int nb, NH, NKV, max_ctx;
-};
-hipError_t dec_qkv_finish(const DecQkvArgs& a, hipStream_t s);
+// xn[b] = fp16(rmsnorm(x[b]) * g) for b < nb
+hipError_t dec_norm(const float* x, half_t* xn, const float* g, int nb, int D, hipStream_t s);
 
 // Attention of one query token per sequence over keys 0..pos (pos = *ctr)
 // in chunks of kDecChunk keys: partials o (unnormalized), m, l per

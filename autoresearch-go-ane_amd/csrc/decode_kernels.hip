@@ -4,6 +4,8 @@
 // shared by the query heads of a key/value group.
 #include <math.h>
 
+#include <algorithm>
+
 #include "decode.h"
 
 namespace ane {
@@ -13,50 +15,158 @@ namespace {
 constexpr float kL2E = 1.4426950408889634f;
 
 // ---- skinny GEMM ------------------------------------------------------------
-// One wave per (32 weight rows, K range).  MFMA 32x32x16 with rows = tokens
-// (two tiles: tokens 0-31, 32-63) and columns = weight rows.  Lane l owns
-// token / weight row l%32 and, for k-step s of a 64-wide window, the eight
-// k-values 32*(l/32) + 8*s + [0, 8): A and B use the same k-slot map, so
-// each lane reads 64 contiguous bytes of its weight row per window and the
-// two lane halves cover the row's 128-byte line.
-template <int EPI>
-__global__ __launch_bounds__(64) void skinny_kernel(SkinnyArgs a) {
-  const int lane = threadIdx.x;
-  const int cg = blockIdx.x;
-  const int KR = a.K / a.splits, k0 = blockIdx.y * KR;
+// Block = NCG column groups of 32 weight rows x NWK waves splitting K, each
+// wave holding at most two 64-wide k-windows, all loaded in one batch (a
+// decode-step GEMM is bound by dependent memory round trips, not by bytes).
+// MFMA 32x32x16 with rows = tokens (two tiles: tokens 0-31, 32-63) and
+// columns = weight rows; both operands are stored fragment-major
+// (decode.h), so each operand load is one contiguous 1 KB per wave.  The K
+// partial sums meet in LDS and are added in wave order (deterministic);
+// wave 0 of each column group runs the fused epilogue, whose operands
+// (residual rows, RoPE factors) are fetched up front.
+template <int EPI, int NWK, int NCG>
+__global__ __launch_bounds__(64 * NWK * NCG) void skinny_kernel(SkinnyArgs a) {
+  constexpr int NRED = (NWK - 1) * NCG > 0 ? (NWK - 1) * NCG : 1;
+  __shared__ float red[NRED][32 * 64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int cgl = wave % NCG, kw = wave / NCG;
+  const int cg = blockIdx.x * NCG + cgl;
+  const int nwin = a.K / 64;
+  const int w0 = (kw * nwin) / NWK, w1 = ((kw + 1) * nwin) / NWK;  // this wave's windows [w0, w1), <= 2
   const int row = lane & 31, h = lane >> 5;
-  const half_t* wp = a.W + (size_t)(cg * 32 + row) * a.ldw + k0 + 32 * h;
-  const half_t* xp0 = a.X + (size_t)row * a.ldx + k0 + 32 * h;
-  const half_t* xp1 = xp0 + (size_t)32 * a.ldx;
-  floatx16 c0, c1;
-#pragma unroll
-  for (int r = 0; r < 16; r++) { c0[r] = 0.f; c1[r] = 0.f; }
-#pragma unroll 2
-  for (int k = 0; k < KR; k += 64) {
-    half8 w[4], p[4], q[4];
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-      w[s] = ld_h8(wp + k + 8 * s);
-      p[s] = ld_h8(xp0 + k + 8 * s);
-      q[s] = ld_h8(xp1 + k + 8 * s);
-    }
-#pragma unroll
-    for (int s = 0; s < 4; s++) {
-      c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(p[s], w[s], c0, 0, 0, 0);
-      c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(q[s], w[s], c1, 0, 0, 0);
-    }
-  }
-  // c[r]: token 8*(r/4) + 4*h + r%4 (+32 for c1), column cg*32 + row
   const int col = cg * 32 + row;
-  if constexpr (EPI == 0) {
-    float* out = a.partial + (size_t)blockIdx.y * kDecRows * a.N + col;
+  // fragment (w, s): weights at ((cg * nwin + w) * 4 + s) KB, activations at
+  // ((w * 4 + s) * 2 + tile) KB; lane l's 16 B at l * 16
+  const half_t* wp = a.W + (size_t)cg * nwin * 2048 + lane * 8;
+  const half_t* xp0 = a.X + lane * 8;
+
+  // Every load below is unconditional (addresses clamped to valid data,
+  // unused values zeroed by selects): predicated loads compile to branches
+  // whose merges wait for the loads issued so far.
+  // epilogue operands, requested before the weights
+  float ep0[16], ep1[16];
+  float cs = 0.f, sn = 0.f;
+  int pos = 0;
+  if constexpr (EPI == SK_RESID) {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int t = 8 * (r >> 2) + 4 * h + (r & 3);
-      out[(size_t)t * a.N] = c0[r];
-      out[(size_t)(t + 32) * a.N] = c1[r];
+      ep0[r] = a.x[(size_t)min(t, a.nb - 1) * a.N + col];
+      ep1[r] = a.x[(size_t)min(t + 32, a.nb - 1) * a.N + col];
     }
-  } else {
+  } else if constexpr (EPI == SK_QKV) {
+    pos = a.ctr[0];
+    const int i = (col & 63) >> 1;
+    cs = a.rope_cos[pos * 32 + i];
+    sn = a.rope_sin[pos * 32 + i];
+  }
+
+  half8 w[8], p[8], q[8];
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    const int f = min(w0 + (s >> 2), w1 - 1) * 4 + (s & 3);
+    w[s] = ld_h8(wp + (size_t)f * 512);
+    p[s] = ld_h8(xp0 + (size_t)f * 1024);
+    q[s] = ld_h8(xp0 + (size_t)f * 1024 + 512);
+  }
+  if (w1 - w0 < 2) {  // one window: the second copy contributes zero
+#pragma unroll
+    for (int s = 4; s < 8; s++)
+#pragma unroll
+      for (int j = 0; j < 8; j++) w[s][j] = (half_t)0.f;
+  }
+  floatx16 c0, c1;
+#pragma unroll
+  for (int r = 0; r < 16; r++) { c0[r] = 0.f; c1[r] = 0.f; }
+#pragma unroll
+  for (int s = 0; s < 8; s++) {
+    c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(p[s], w[s], c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(q[s], w[s], c1, 0, 0, 0);
+  }
+  if constexpr (NWK > 1) {
+    if (kw > 0) {
+      float* dst = red[(kw - 1) * NCG + cgl];
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        dst[r * 64 + lane] = c0[r];
+        dst[(16 + r) * 64 + lane] = c1[r];
+      }
+    }
+    __syncthreads();
+    if (kw == 0) {
+#pragma unroll 1
+      for (int o = 1; o < NWK; o++) {
+        const float* src = red[(o - 1) * NCG + cgl];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          c0[r] += src[r * 64 + lane];
+          c1[r] += src[(16 + r) * 64 + lane];
+        }
+      }
+    }
+  }
+  // c[r]: token 8*(r/4) + 4*h + r%4 (+32 for c1), column cg*32 + row
+  if constexpr (EPI == SK_SWIGLU) {
+    // group 0 holds W1 rows 32*bx.., group 1 the matching W3 rows
+    if constexpr (NWK > 1) __syncthreads();  // reduction reads of red[] done
+    if (kw == 0 && cgl == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        red[0][r * 64 + lane] = c0[r];
+        red[0][(16 + r) * 64 + lane] = c1[r];
+      }
+    }
+    __syncthreads();
+    if (kw == 0 && cgl == 0) {
+      const int H = a.N / 2, j = blockIdx.x * 32 + row;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int t = 8 * (r >> 2) + 4 * h + (r & 3);
+        const float h1 = c0[r], h3 = red[0][r * 64 + lane];
+        const float g1 = c1[r], g3 = red[0][(16 + r) * 64 + lane];
+        if (t < a.nb) a.gate[act_frag_off(t, j)] = (half_t)(h1 / (1.0f + __expf(-h1)) * h3);
+        if (t + 32 < a.nb) a.gate[act_frag_off(t + 32, j)] = (half_t)(g1 / (1.0f + __expf(-g1)) * g3);
+      }
+    }
+    return;
+  }
+  if (kw != 0) return;
+  if constexpr (EPI == SK_RESID) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int t = 8 * (r >> 2) + 4 * h + (r & 3);
+      if (t < a.nb) a.x[(size_t)t * a.N + col] = ep0[r] + c0[r];
+      if (t + 32 < a.nb) a.x[(size_t)(t + 32) * a.N + col] = ep1[r] + c1[r];
+    }
+  } else if constexpr (EPI == SK_QKV) {
+    // RoPE on interleaved pairs (partner = lane ^ 1), then q -> a.q,
+    // k / v -> the cache at position ctr[0]
+    const int D = a.NH * 64, KVD = a.NKV * 64;
+    const bool rot = col < D + KVD, odd = col & 1;
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int t = 8 * (r >> 2) + 4 * h + (r & 3) + 32 * half;
+        float v = half ? c1[r] : c0[r];
+        const float pv = __shfl_xor(v, 1, 64);
+        if (rot) {
+          const float e = odd ? pv : v, o = odd ? v : pv;
+          v = odd ? (o * cs + e * sn) : (e * cs - o * sn);
+        }
+        if (t < a.nb) {
+          if (col < D) {
+            a.q[(size_t)t * D + col] = (half_t)v;
+          } else {
+            const bool isk = col < D + KVD;
+            const int c = col - (isk ? D : D + KVD);
+            half_t* dst = (isk ? a.kc : a.vc) + (((size_t)t * a.NKV + (c >> 6)) * a.max_ctx + pos) * 64 + (c & 63);
+            *dst = (half_t)v;
+          }
+        }
+      }
+    }
+  } else {  // SK_ARGMAX
     const bool valid = col < a.nvalid;
 #pragma unroll
     for (int half = 0; half < 2; half++) {
@@ -151,13 +261,12 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(float* x, half_t* xn, c
     const int c = tid + 256 * i;
     if (c < D) {
       x[(size_t)b * D + c] = v[i];
-      xn[(size_t)b * D + c] = (half_t)(v[i] * rr * g[c]);
+      xn[act_frag_off(b, c)] = (half_t)(v[i] * rr * g[c]);
     }
   }
 }
 
-__global__ __launch_bounds__(256) void resid_norm_kernel(float* x, half_t* xn, const float* partial, int splits,
-                                                         const float* g, int D) {
+__global__ __launch_bounds__(256) void norm_kernel(const float* x, half_t* xn, const float* g, int D) {
   __shared__ float red[4];
   const int b = blockIdx.x, tid = threadIdx.x;
   float v[4];
@@ -165,13 +274,7 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(float* x, half_t* xn, c
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int c = tid + 256 * i;
-    v[i] = 0.f;
-    if (c < D) {
-      float s = x[(size_t)b * D + c];
-      if (partial)
-        for (int k = 0; k < splits; k++) s += partial[((size_t)k * kDecRows + b) * D + c];
-      v[i] = s;
-    }
+    v[i] = c < D ? x[(size_t)b * D + c] : 0.f;
     ss += v[i] * v[i];
   }
   ss = block_sum_256(ss, red);
@@ -179,58 +282,7 @@ __global__ __launch_bounds__(256) void resid_norm_kernel(float* x, half_t* xn, c
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int c = tid + 256 * i;
-    if (c < D) {
-      x[(size_t)b * D + c] = v[i];
-      xn[(size_t)b * D + c] = (half_t)(v[i] * rr * g[c]);
-    }
-  }
-}
-
-__global__ __launch_bounds__(256) void swiglu_kernel(half_t* gate, const float* partial, int splits, int H) {
-  const int b = blockIdx.x, j = blockIdx.y * 256 + threadIdx.x;
-  if (j >= H) return;
-  const int N = 2 * H;
-  const int c1 = (j >> 5) * 64 + (j & 31);
-  float h1 = 0.f, h3 = 0.f;
-  for (int k = 0; k < splits; k++) {
-    const float* pr = partial + ((size_t)k * kDecRows + b) * N;
-    h1 += pr[c1];
-    h3 += pr[c1 + 32];
-  }
-  gate[(size_t)b * H + j] = (half_t)(h1 / (1.0f + __expf(-h1)) * h3);
-}
-
-__global__ __launch_bounds__(256) void qkv_finish_kernel(DecQkvArgs a) {
-  const int b = blockIdx.x, tid = threadIdx.x;
-  const int D = a.NH * 64, KVD = a.NKV * 64, N1 = D + 2 * KVD;
-  const int pos = a.ctr[0];
-  for (int c2 = tid; c2 < N1 / 2; c2 += 256) {
-    const int col = 2 * c2;
-    float e = 0.f, o = 0.f;
-    for (int k = 0; k < a.splits; k++) {
-      const float* pr = a.partial + ((size_t)k * kDecRows + b) * N1 + col;
-      e += pr[0];
-      o += pr[1];
-    }
-    if (col < D + KVD) {  // RoPE on interleaved pairs
-      const int i = (col & 63) >> 1;
-      const float cs = a.rope_cos[pos * 32 + i], sn = a.rope_sin[pos * 32 + i];
-      const float re = e * cs - o * sn, ro = o * cs + e * sn;
-      e = re;
-      o = ro;
-    }
-    half2v w;
-    w[0] = (half_t)e;
-    w[1] = (half_t)o;
-    if (col < D) {
-      *reinterpret_cast<half2v*>(a.q + (size_t)b * D + col) = w;
-    } else {
-      const bool isk = col < D + KVD;
-      const int c = col - (isk ? D : D + KVD);
-      const int kvh = c >> 6, d = c & 63;
-      half_t* dst = (isk ? a.kc : a.vc) + (((size_t)b * a.NKV + kvh) * a.max_ctx + pos) * 64 + d;
-      *reinterpret_cast<half2v*>(dst) = w;
-    }
+    if (c < D) xn[act_frag_off(b, c)] = (half_t)(v[i] * rr * g[c]);
   }
 }
 
@@ -259,23 +311,34 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
   const half_t* Kb = a.kc + (cache0 + c0) * 64;
   const half_t* Vb = a.vc + (cache0 + c0) * 64;
   const int kl = tid >> 3, d8 = tid & 7;
-  for (int j = kl; j < kDecChunk; j += 32) {
-    const bool ok = j < n;
-    half8 k8;
-    if (ok) k8 = ld_h8(Kb + (size_t)j * 64 + d8 * 8);
-    else
+  constexpr int NIT = kDecChunk / 32;
+  // all of this thread's key and value loads in flight before the first use;
+  // unconditional (rows clamped into the chunk), keys past n are never used
+  half8 kk[NIT], kv[NIT];
 #pragma unroll
-      for (int i = 0; i < 8; i++) k8[i] = (half_t)0.f;
+  for (int it = 0; it < NIT; it++) {
+    const int j = min(kl + 32 * it, n - 1);
+    kk[it] = ld_h8(Kb + (size_t)j * 64 + d8 * 8);
+    kv[it] = ld_h8(Vb + (size_t)j * 64 + d8 * 8);
+  }
+  float qr[kGMax][8];  // this lane's 8 dims of each query head of the group
+#pragma unroll
+  for (int h = 0; h < kGMax; h++)
+#pragma unroll
+    for (int i = 0; i < 8; i++) qr[h][i] = h < G ? qs[h][d8 * 8 + i] : 0.f;
+#pragma unroll
+  for (int it = 0; it < NIT; it++) {
+    const int j = kl + 32 * it;
 #pragma unroll
     for (int h = 0; h < kGMax; h++) {
       if (h < G) {
         float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; i++) s += qs[h][d8 * 8 + i] * (float)k8[i];
+        for (int i = 0; i < 8; i++) s += qr[h][i] * (float)kk[it][i];
         s += __shfl_xor(s, 1, 64);
         s += __shfl_xor(s, 2, 64);
         s += __shfl_xor(s, 4, 64);
-        if (ok && d8 == 0) sc[h][j] = s;
+        if (j < n && d8 == 0) sc[h][j] = s;
       }
     }
   }
@@ -299,14 +362,17 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
   for (int h = 0; h < kGMax; h++)
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
-  for (int j = kl; j < n; j += 32) {
-    const half8 v8 = ld_h8(Vb + (size_t)j * 64 + d8 * 8);
 #pragma unroll
-    for (int h = 0; h < kGMax; h++) {
-      if (h < G) {
-        const float p = sc[h][j];
+  for (int it = 0; it < NIT; it++) {
+    const int j = kl + 32 * it;
+    if (j < n) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) acc[h][i] += p * (float)v8[i];
+      for (int h = 0; h < kGMax; h++) {
+        if (h < G) {
+          const float p = sc[h][j];
+#pragma unroll
+          for (int i = 0; i < 8; i++) acc[h][i] += p * (float)kv[it][i];
+        }
       }
     }
   }
@@ -350,7 +416,7 @@ __global__ __launch_bounds__(64) void dec_combine_kernel(DecAttnArgs a) {
     num += w * p[s * 66 + d];
     den += w * p[s * 66 + 65];
   }
-  a.att[(size_t)b * a.NH * 64 + h * 64 + d] = (half_t)(num / den);
+  a.att[act_frag_off(b, h * 64 + d)] = (half_t)(num / den);
 }
 
 // ---- prefill ------------------------------------------------------------------
@@ -523,6 +589,19 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(PrefillAttnArgs a) {
   }
 }
 
+__global__ __launch_bounds__(256) void weight_frag_kernel(half_t* dst, const half_t* src, int K, size_t nchunks) {
+  const int nf = (K / 64) * 4;  // fragments per 32-row group
+  for (size_t c = (size_t)blockIdx.x * 256 + threadIdx.x; c < nchunks; c += (size_t)gridDim.x * 256) {
+    const int lane = (int)(c & 63);
+    const size_t fg = c >> 6;
+    const int f = (int)(fg % nf);
+    const size_t g = fg / nf;
+    const size_t row = g * 32 + (lane & 31);
+    const int k = (f >> 2) * 64 + 32 * (lane >> 5) + 8 * (f & 3);
+    st_h8(dst + c * 8, ld_h8(src + row * K + k));
+  }
+}
+
 __global__ __launch_bounds__(256) void gather_last_kernel(float* dst, const float* src, int S, int D) {
   const int i = blockIdx.x;
   const float* s = src + ((size_t)i * S + S - 1) * D;
@@ -531,26 +610,45 @@ __global__ __launch_bounds__(256) void gather_last_kernel(float* dst, const floa
 
 }  // namespace
 
-int skinny_splits(int N, int K) {
-  const int groups = N / 32, nk = K / 64;
-  int best = 1;
-  for (int s = 1; s <= nk; s++) {
-    if (nk % s) continue;
-    best = s;
-    if (groups * s >= 256) break;
+template <int EPI, int NCG>
+hipError_t skinny_launch(const SkinnyArgs& a, int nwk, hipStream_t s) {
+  dim3 grid(a.N / (32 * NCG));
+  switch (nwk) {
+    case 1: hipLaunchKernelGGL((skinny_kernel<EPI, 1, NCG>), grid, dim3(64 * NCG), 0, s, a); break;
+    case 2: hipLaunchKernelGGL((skinny_kernel<EPI, 2, NCG>), grid, dim3(128 * NCG), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((skinny_kernel<EPI, 4, NCG>), grid, dim3(256 * NCG), 0, s, a); break;
+    case 8: hipLaunchKernelGGL((skinny_kernel<EPI, 8, NCG>), grid, dim3(512 * NCG), 0, s, a); break;
+    default:
+      if constexpr (NCG == 1) {
+        hipLaunchKernelGGL((skinny_kernel<EPI, 16, 1>), grid, dim3(1024), 0, s, a);
+        break;
+      }
+      return hipErrorInvalidValue;
   }
-  return best;
+  return hipGetLastError();
+}
+
+// waves per column group: enough that no wave holds more than two windows
+int skinny_kwaves(int K, int ncg) {
+  const int nwin = K / 64, cap = 16 / ncg;
+  int w = 1;
+  while (w < cap && (nwin + w - 1) / w > 2) w <<= 1;
+  return w;
 }
 
 hipError_t skinny_gemm(const SkinnyArgs& a, int epi, hipStream_t s) {
-  if (a.N <= 0 || a.N % 32 || a.K <= 0 || a.splits <= 0 || a.K % (64 * a.splits)) return hipErrorInvalidValue;
-  if (epi == 1 && a.splits != 1) return hipErrorInvalidValue;
-  dim3 grid(a.N / 32, a.splits);
-  if (epi == 0)
-    hipLaunchKernelGGL(skinny_kernel<0>, grid, dim3(64), 0, s, a);
-  else
-    hipLaunchKernelGGL(skinny_kernel<1>, grid, dim3(64), 0, s, a);
-  return hipGetLastError();
+  const int ncg = epi == SK_SWIGLU ? 2 : 1;
+  if (a.N <= 0 || a.N % (32 * ncg) || a.K <= 0 || a.K % 64 || a.nb < 1 || a.nb > kDecRows)
+    return hipErrorInvalidValue;
+  const int nwk = skinny_kwaves(a.K, ncg);
+  if ((a.K / 64 + nwk - 1) / nwk > 2) return hipErrorInvalidValue;  // K too long for one block
+  switch (epi) {
+    case SK_RESID: return skinny_launch<SK_RESID, 1>(a, nwk, s);
+    case SK_QKV: return skinny_launch<SK_QKV, 1>(a, nwk, s);
+    case SK_SWIGLU: return skinny_launch<SK_SWIGLU, 2>(a, nwk, s);
+    case SK_ARGMAX: return skinny_launch<SK_ARGMAX, 1>(a, nwk, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t argmax_reduce(uint16_t* tok_out, uint16_t* hist, const int* step, const float2* amax, int ngroups,
@@ -576,20 +674,9 @@ hipError_t dec_embed_norm(float* x, half_t* xn, const float* embed, const uint16
   return hipGetLastError();
 }
 
-hipError_t dec_resid_norm(float* x, half_t* xn, const float* partial, int splits, const float* g, int nb, int D,
-                          hipStream_t s) {
+hipError_t dec_norm(const float* x, half_t* xn, const float* g, int nb, int D, hipStream_t s) {
   if (D > 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(resid_norm_kernel, dim3(nb), dim3(256), 0, s, x, xn, partial, splits, g, D);
-  return hipGetLastError();
-}
-
-hipError_t dec_swiglu(half_t* gate, const float* partial, int splits, int nb, int H, hipStream_t s) {
-  hipLaunchKernelGGL(swiglu_kernel, dim3(nb, (H + 255) / 256), dim3(256), 0, s, gate, partial, splits, H);
-  return hipGetLastError();
-}
-
-hipError_t dec_qkv_finish(const DecQkvArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(qkv_finish_kernel, dim3(a.nb), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(norm_kernel, dim3(nb), dim3(256), 0, s, x, xn, g, D);
   return hipGetLastError();
 }
 
@@ -614,6 +701,14 @@ hipError_t prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
   if (a.S <= 0 || a.S % 32 || a.S > a.max_ctx || a.NH % a.NKV) return hipErrorInvalidValue;
   dim3 grid((a.S + 127) / 128, a.NH, a.nseq);
   hipLaunchKernelGGL(prefill_attn_kernel, grid, dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t weight_to_frag(half_t* dst, const half_t* src, int N, int K, hipStream_t s) {
+  if (N <= 0 || N % 32 || K <= 0 || K % 64) return hipErrorInvalidValue;
+  const size_t nchunks = (size_t)N * K / 8;
+  const int blocks = (int)std::min<size_t>((nchunks + 255) / 256, 4096);
+  hipLaunchKernelGGL(weight_frag_kernel, dim3(blocks), dim3(256), 0, s, dst, src, K, nchunks);
   return hipGetLastError();
 }
 

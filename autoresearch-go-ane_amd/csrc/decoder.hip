@@ -9,6 +9,7 @@
 //   w13      fp16 [L][2H][D]          W1 / W3 interleaved by 32 rows
 //   w2       fp16 [L][D][H]
 //   embed_h  fp16 [V][D]              tied classifier
+//   f*       the same five in MFMA-fragment-major order (decode.h)
 //   kc, vc   fp16 [L][max_batch][kv_heads][max_ctx][64]
 //   decode rows (64 each): x fp32 [64][D], xn/q/att fp16 [64][D],
 //   gate fp16 [64][H], split-K partials, attention partials, argmax partials
@@ -72,11 +73,12 @@ struct ane_decoder {
   bool params_set = false;
   float* P = nullptr;
   half_t *wqkv = nullptr, *wo = nullptr, *w13 = nullptr, *w2 = nullptr, *embed_h = nullptr;
+  // the same weights in MFMA-fragment-major order for the 64-row decode GEMMs
+  half_t *fwqkv = nullptr, *fwo = nullptr, *fw13 = nullptr, *fw2 = nullptr, *fembed = nullptr;
   half_t *kc = nullptr, *vc = nullptr;
   float *rope_cos = nullptr, *rope_sin = nullptr;
   float* x = nullptr;
   half_t *xn = nullptr, *q = nullptr, *att = nullptr, *gate = nullptr;
-  float* part = nullptr;
   float* apart = nullptr;
   int nsplit = 0;
   float2* amax = nullptr;
@@ -86,7 +88,6 @@ struct ane_decoder {
   int TC = 0;
   float* px = nullptr;
   half_t *pxn = nullptr, *pqkv = nullptr, *patt = nullptr, *pgate = nullptr;
-  int s_qkv = 1, s_wo = 1, s_w13 = 1, s_w2 = 1;
   int nseq = 0, pos = 0;  // active batch, filled positions
   hipGraph_t graph = nullptr;
   hipGraphExec_t gexec = nullptr;
@@ -149,8 +150,8 @@ int validate(const ane_decode_cfg& c, std::string* why) {
     snprintf(buf, sizeof buf, "heads=%d must be 1..4 times kv_heads=%d", c.heads, c.kv_heads);
   else if (c.dim > 1024)
     snprintf(buf, sizeof buf, "dim=%d exceeds 1024", c.dim);
-  else if (c.hidden <= 0 || c.hidden % 64)
-    snprintf(buf, sizeof buf, "hidden=%d must be a positive multiple of 64", c.hidden);
+  else if (c.hidden <= 0 || c.hidden % 64 || c.hidden > 2048)
+    snprintf(buf, sizeof buf, "hidden=%d must be a multiple of 64 up to 2048", c.hidden);
   else if (c.vocab <= 0 || c.vocab % 32 || c.vocab > 65536)
     snprintf(buf, sizeof buf, "vocab=%d must be a multiple of 32 up to 65536", c.vocab);
   else if (c.layers <= 0)
@@ -183,6 +184,11 @@ int open_impl(ane_decoder* d) {
   DCHK(op, dalloc(d, &d->w13, (size_t)L * 2 * H * D));
   DCHK(op, dalloc(d, &d->w2, (size_t)L * D * H));
   DCHK(op, dalloc(d, &d->embed_h, (size_t)V * D));
+  DCHK(op, dalloc(d, &d->fwqkv, (size_t)L * N1 * D));
+  DCHK(op, dalloc(d, &d->fwo, (size_t)L * D * D));
+  DCHK(op, dalloc(d, &d->fw13, (size_t)L * 2 * H * D));
+  DCHK(op, dalloc(d, &d->fw2, (size_t)L * D * H));
+  DCHK(op, dalloc(d, &d->fembed, (size_t)V * D));
   const size_t cache = (size_t)L * B * d->NKV * C * 64;
   DCHK(op, dalloc(d, &d->kc, cache));
   DCHK(op, dalloc(d, &d->vc, cache));
@@ -206,15 +212,6 @@ int open_impl(ane_decoder* d) {
   DCHK(op, dalloc(d, &d->q, (size_t)R * D));
   DCHK(op, dalloc(d, &d->att, (size_t)R * D));
   DCHK(op, dalloc(d, &d->gate, (size_t)R * H));
-  d->s_qkv = skinny_splits(N1, D);
-  d->s_wo = skinny_splits(D, D);
-  d->s_w13 = skinny_splits(2 * H, D);
-  d->s_w2 = skinny_splits(D, H);
-  size_t pmax = (size_t)d->s_qkv * N1;
-  pmax = std::max(pmax, (size_t)d->s_wo * D);
-  pmax = std::max(pmax, (size_t)d->s_w13 * 2 * H);
-  pmax = std::max(pmax, (size_t)d->s_w2 * D);
-  DCHK(op, dalloc(d, &d->part, pmax * R));
   d->nsplit = (C + kDecChunk - 1) / kDecChunk;
   DCHK(op, dalloc(d, &d->apart, (size_t)B * d->NH * d->nsplit * 66));
   DCHK(op, dalloc(d, &d->amax, (size_t)(V / 32) * R));
@@ -260,35 +257,32 @@ int enqueue_step(ane_decoder* d, float* logits, uint16_t* hist) {
     half_t* vcl = d->vc + (size_t)l * d->B * d->NKV * d->C * 64;
     SkinnyArgs s;
     memset(&s, 0, sizeof s);
-    s.X = d->xn; s.ldx = D; s.W = d->wqkv + (size_t)l * N1 * D; s.ldw = D; s.N = N1; s.K = D;
-    s.splits = d->s_qkv; s.partial = d->part;
-    DCHK(op, skinny_gemm(s, 0, st));
-    DecQkvArgs qa;
-    qa.partial = d->part; qa.splits = d->s_qkv; qa.ctr = d->ctr_d; qa.rope_cos = d->rope_cos;
-    qa.rope_sin = d->rope_sin; qa.q = d->q; qa.kc = kcl; qa.vc = vcl; qa.nb = nb; qa.NH = d->NH;
-    qa.NKV = d->NKV; qa.max_ctx = d->C;
-    DCHK(op, dec_qkv_finish(qa, st));
+    s.nb = nb;
+    s.X = d->xn; s.W = d->fwqkv + (size_t)l * N1 * D; s.N = N1; s.K = D;
+    s.ctr = d->ctr_d; s.rope_cos = d->rope_cos; s.rope_sin = d->rope_sin; s.q = d->q; s.kc = kcl; s.vc = vcl;
+    s.NH = d->NH; s.NKV = d->NKV; s.max_ctx = d->C;
+    DCHK(op, skinny_gemm(s, SK_QKV, st));
     DecAttnArgs aa;
     aa.q = d->q; aa.kc = kcl; aa.vc = vcl; aa.ctr = d->ctr_d; aa.part = d->apart; aa.att = d->att; aa.nb = nb;
     aa.NH = d->NH; aa.NKV = d->NKV; aa.max_ctx = d->C; aa.nsplit = d->nsplit; aa.scale = 0.125f;
     DCHK(op, dec_attention(aa, st));
-    s.X = d->att; s.ldx = D; s.W = d->wo + (size_t)l * D * D; s.ldw = D; s.N = D; s.K = D; s.splits = d->s_wo;
-    DCHK(op, skinny_gemm(s, 0, st));
-    DCHK(op, dec_resid_norm(d->x, d->xn, d->part, d->s_wo, d->P + o.g_ffn, nb, D, st));
-    s.X = d->xn; s.ldx = D; s.W = d->w13 + (size_t)l * 2 * H * D; s.ldw = D; s.N = 2 * H; s.K = D;
-    s.splits = d->s_w13;
-    DCHK(op, skinny_gemm(s, 0, st));
-    DCHK(op, dec_swiglu(d->gate, d->part, d->s_w13, nb, H, st));
-    s.X = d->gate; s.ldx = H; s.W = d->w2 + (size_t)l * D * H; s.ldw = H; s.N = D; s.K = H; s.splits = d->s_w2;
-    DCHK(op, skinny_gemm(s, 0, st));
+    s.X = d->att; s.W = d->fwo + (size_t)l * D * D; s.N = D; s.K = D; s.x = d->x;
+    DCHK(op, skinny_gemm(s, SK_RESID, st));
+    DCHK(op, dec_norm(d->x, d->xn, d->P + o.g_ffn, nb, D, st));
+    s.X = d->xn; s.W = d->fw13 + (size_t)l * 2 * H * D; s.N = 2 * H; s.K = D;
+    s.gate = d->gate;
+    DCHK(op, skinny_gemm(s, SK_SWIGLU, st));
+    s.X = d->gate; s.W = d->fw2 + (size_t)l * D * H; s.N = D; s.K = H;
+    DCHK(op, skinny_gemm(s, SK_RESID, st));
     const float* gnext = l + 1 < d->L ? d->P + d->off[l + 1].g_att : d->P + d->off_gfinal;
-    DCHK(op, dec_resid_norm(d->x, d->xn, d->part, d->s_w2, gnext, nb, D, st));
+    DCHK(op, dec_norm(d->x, d->xn, gnext, nb, D, st));
   }
   SkinnyArgs s;
   memset(&s, 0, sizeof s);
-  s.X = d->xn; s.ldx = D; s.W = d->embed_h; s.ldw = D; s.N = d->V; s.K = D; s.splits = 1; s.amax = d->amax;
+  s.nb = nb;
+  s.X = d->xn; s.W = d->fembed; s.N = d->V; s.K = D; s.amax = d->amax;
   s.logits = logits; s.nvalid = d->V;
-  DCHK(op, skinny_gemm(s, 1, st));
+  DCHK(op, skinny_gemm(s, SK_ARGMAX, st));
   DCHK(op, argmax_reduce(d->tok_d, hist, d->ctr_d + 1, d->amax, d->V / 32, nb, st));
   DCHK(op, dec_advance(d->ctr_d, st));
   return ANE_OK;
@@ -353,6 +347,13 @@ extern "C" int ane_decode_set_params(ane_decoder* d, const float* params, int64_
     DCHK(op, f32_to_f16(d->w2 + (size_t)l * D * H, d->P + o.w2, (size_t)D * H, st));
   }
   DCHK(op, f32_to_f16(d->embed_h, d->P + d->off_embed, (size_t)d->V * D, st));
+  for (int l = 0; l < d->L; l++) {
+    DCHK(op, weight_to_frag(d->fwqkv + (size_t)l * N1 * D, d->wqkv + (size_t)l * N1 * D, N1, D, st));
+    DCHK(op, weight_to_frag(d->fwo + (size_t)l * D * D, d->wo + (size_t)l * D * D, D, D, st));
+    DCHK(op, weight_to_frag(d->fw13 + (size_t)l * 2 * H * D, d->w13 + (size_t)l * 2 * H * D, 2 * H, D, st));
+    DCHK(op, weight_to_frag(d->fw2 + (size_t)l * D * H, d->w2 + (size_t)l * D * H, D, H, st));
+  }
+  DCHK(op, weight_to_frag(d->fembed, d->embed_h, d->V, D, st));
   DCHK(op, hipStreamSynchronize(st));
   d->params_set = true;
   return ANE_OK;
@@ -413,12 +414,13 @@ extern "C" int ane_decode_prefill(ane_decoder* d, const uint16_t* prefix, int32_
     DCHK(op, gather_last_rows(d->x + (size_t)s0 * D, d->px, n, plen, D, st));
   }
   d->nseq = nseq;
-  DCHK(op, dec_resid_norm(d->x, d->xn, nullptr, 0, d->P + d->off_gfinal, nseq, D, st));
+  DCHK(op, dec_norm(d->x, d->xn, d->P + d->off_gfinal, nseq, D, st));
   SkinnyArgs s;
   memset(&s, 0, sizeof s);
-  s.X = d->xn; s.ldx = D; s.W = d->embed_h; s.ldw = D; s.N = d->V; s.K = D; s.splits = 1; s.amax = d->amax;
+  s.nb = nseq;
+  s.X = d->xn; s.W = d->fembed; s.N = d->V; s.K = D; s.amax = d->amax;
   s.logits = logits ? d->logits_d : nullptr; s.nvalid = d->V;
-  DCHK(op, skinny_gemm(s, 1, st));
+  DCHK(op, skinny_gemm(s, SK_ARGMAX, st));
   DCHK(op, argmax_reduce(d->tok_d, nullptr, nullptr, d->amax, d->V / 32, nseq, st));
   DCHK(op, dec_set_ctr(d->ctr_d, plen, 0, st));
   d->pos = plen;
