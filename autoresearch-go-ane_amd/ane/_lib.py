@@ -58,6 +58,11 @@ class DecodeCfg(C.Structure):
                 ("rope_theta", C.c_double), ("device", C.c_int32)]
 
 
+class MoeCfg(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("hidden", C.c_int32), ("experts", C.c_int32), ("top_k", C.c_int32),
+                ("max_tokens", C.c_int32), ("device", C.c_int32)]
+
+
 class ProfEntry(C.Structure):
     _fields_ = [("launches", C.c_int64), ("ms", C.c_double), ("flops", C.c_double), ("bytes", C.c_double)]
 
@@ -109,6 +114,15 @@ SIGNATURES = {
     "ane_decode_generate": (C.c_int, [_eng, C.c_int32, _u16]),
     "ane_decode_position": (C.c_int32, [_eng]),
     "ane_decode_last_ms": (C.c_double, [_eng]),
+    "ane_moe_open": (C.c_int, [C.POINTER(MoeCfg), C.POINTER(C.c_void_p)]),
+    "ane_moe_destroy": (None, [_eng]),
+    "ane_moe_last_error": (C.c_char_p, [_eng]),
+    "ane_moe_param_count": (C.c_int64, [C.POINTER(MoeCfg)]),
+    "ane_moe_set_params": (C.c_int, [_eng, _fp, C.c_int64]),
+    "ane_moe_load_input": (C.c_int, [_eng, _fp, C.c_int32]),
+    "ane_moe_run": (C.c_int, [_eng]),
+    "ane_moe_read_output": (C.c_int, [_eng, _fp, C.POINTER(C.c_int32), _fp]),
+    "ane_moe_last_ms": (C.c_double, [_eng]),
 }
 
 _lib = None

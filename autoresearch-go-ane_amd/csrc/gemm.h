@@ -30,6 +30,7 @@ enum Epi : int {
   EPI_STORE_W13 = 9, // C (fp32) rows of an interleaved W1|W3 gradient scattered to two outputs
   EPI_SWIGLU_BWD = 10, // acc = dgate [T, H]; C2 (fp16) = h1|h3 interleaved -> C (fp16) = dh1|dh3 interleaved
   EPI_RELU2_BWD = 11,  // acc = dgate [T, H]; C2 (fp16) = h1 -> C (fp16) = dgate * 2 * max(h1, 0)
+  EPI_STORE_RS = 12,   // C (fp32) = acc * rowscale[row]
 };
 
 struct GemmArgs {
@@ -38,6 +39,11 @@ struct GemmArgs {
   int lda, ldb;
   int M, N, K;
   bool a_t, b_t;
+  // Grouped GEMM (layout 0 only): M is the row capacity; grp[0] = number of
+  // valid BM-row tiles, then per tile (first row, group); the B operand of
+  // group g starts at B + g * b_group_stride.  Tiles past grp[0] exit.
+  const int* grp = nullptr;
+  size_t b_group_stride = 0;
 };
 
 struct EpiParams {
@@ -62,6 +68,7 @@ struct EpiParams {
   float cap = 15.f;
   int vocab = 0;                      // rows >= vocab are padding (ignored)
   float* C3 = nullptr;                // second fp32 output (EPI_STORE_W13: W3 grad)
+  const float* rowscale = nullptr;    // [M] (EPI_STORE_RS)
 };
 
 // Launches one GEMM on `stream`.  bm/bn force a block tile (0 = heuristic);

@@ -156,7 +156,14 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) 
   const int gm = min(nbm - first_m, GROUP);
   const int bm = first_m + (bid % group_size) % gm;
   const int bn = (bid % group_size) / gm;
-  const int m0 = bm * BM, n0 = bn * BN;
+  int m0 = bm * BM;
+  const int n0 = bn * BN;
+  const half_t* Bp = g.B;
+  if (g.grp) {  // grouped: row tile bm of the valid tiles, B of its group
+    if (bm >= g.grp[0]) return;  // whole block, before any LDS traffic
+    m0 = g.grp[1 + 2 * bm];
+    Bp += (size_t)g.grp[2 + 2 * bm] * g.b_group_stride;
+  }
 
   floatx16 acc[TM][TN];
 #pragma unroll
@@ -173,7 +180,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) 
   for (int p = 0; p < NS - 1; p++) {
     if (p < nk) {
       sa.issue(g.A, g.lda, m0, p * BK, lds + p * STAGE, tid);
-      sb.issue(g.B, g.ldb, n0, p * BK, lds + p * STAGE + BM * BK, tid);
+      sb.issue(Bp, g.ldb, n0, p * BK, lds + p * STAGE + BM * BK, tid);
     }
   }
   sa.commit(lds, tid);
@@ -202,7 +209,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) 
     half_t* far = lds + ((kt + NS - 1) % NS) * STAGE;        // direct-load target
     if (kt + NS - 1 < nk) {
       sa.issue(g.A, g.lda, m0, (kt + NS - 1) * BK, far, tid);
-      sb.issue(g.B, g.ldb, n0, (kt + NS - 1) * BK, far + BM * BK, tid);
+      sb.issue(Bp, g.ldb, n0, (kt + NS - 1) * BK, far + BM * BK, tid);
     }
     // fragments double-buffered across the four 16-wide k-substeps
     half8 a[2][TM], b[2][TN];
@@ -274,6 +281,18 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) 
 #pragma unroll
         for (int r = 0; r < 16; r++) C[base + (size_t)(8 * (r >> 2) + (r & 3)) * e.ldc] = old[r] + acc[i][j][r] * e.scale;
       }
+  } else if constexpr (EPI == EPI_STORE_RS) {
+    float* C = (float*)e.C;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      float rs[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) rs[r] = e.rowscale[ROW(i, r)];
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) C[(size_t)ROW(i, r) * e.ldc + COL(j)] = acc[i][j][r] * rs[r];
+    }
   } else if constexpr (EPI == EPI_STORE_W13) {
     // rows are 32-row blocks alternating W1 / W3 (block b even -> W1 row
     // (b/2)*32 + r%32, odd -> W3); C = W1 grad, C3 = W3 grad, both [H, ldc]
@@ -617,6 +636,7 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
                    !(bm == 128 && bn == 256)))
     return hipErrorInvalidValue;
   const int lay = (g.a_t ? 2 : 0) | (g.b_t ? 1 : 0);
+  if (g.grp && (lay != 0 || ns != 2)) return hipErrorInvalidValue;
 #define CASE(L, AT, BT, E) \
   if (lay == L && epi == E) return launch<AT, BT, E>(g, e, s, bm, bn, nw, ns);
   // forward (activation x weight^T)
@@ -629,6 +649,7 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
   CASE(0, false, false, EPI_SMEAR)
   CASE(0, false, false, EPI_CE)
   CASE(0, false, false, EPI_DLOGITS)
+  CASE(0, false, false, EPI_STORE_RS)
   // backward dX = dY * W  (B transposed)
   CASE(1, false, true, EPI_STORE_H)
   CASE(1, false, true, EPI_STORE_F)

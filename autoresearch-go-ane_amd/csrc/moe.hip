@@ -1,0 +1,394 @@
+// ane_moe: mixture-of-experts SwiGLU FFN layer (the ane_moe_* C-ABI of
+// include/ane_hip.h).  No counterpart in the reference, whose FFN is dense;
+// the layer is built from the reference's primitives (linearCF order for the
+// router, ane/common.go:91-105) with top-2 routing.
+//
+// Pipeline, all on one stream, inputs resident in HBM:
+//   1. router      logits[t][e] in fp32 with linearCF's operation order
+//                  (ascending inputs, every product and sum separately
+//                  rounded) -> top-2 (ties to the lower expert) and the
+//                  softmax over the two chosen logits
+//   2. permute     one-block counting sort: rows of each expert in token
+//                  order, each expert's group padded to a multiple of 128
+//                  rows; tile table (first row, expert) for the grouped GEMMs
+//   3. gather      xg[row] = fp16(x[token of row]) (zero for padding rows)
+//   4. grouped GEMM  [rows, 2H] = xg . W13_e^T with the SwiGLU epilogue
+//   5. grouped GEMM  yw[row] = (g . W2_e^T) * weight(row)
+//   6. combine     out[t] = yw[row(t, 0)] + yw[row(t, 1)]   (fixed order)
+// Device layout: router fp32 [E][D]; w13 fp16 [E][2H][D] (W1 / W3 rows
+// interleaved by 32, the SwiGLU epilogue's pairing); w2 fp16 [E][D][H].
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <algorithm>
+#include <cmath>
+#include <string>
+#include <vector>
+
+#include "../../include/ane_hip.h"
+#include "gemm.h"
+#include "rowops.h"
+
+using namespace ane;
+
+namespace {
+
+constexpr int kGroupRows = 128;  // expert groups are padded to whole 128-row GEMM tiles
+constexpr int kPermThreads = 1024;
+constexpr int kMaxExperts = 16;
+
+// one thread per (token, expert); E threads per token, 256 / E tokens per block
+__global__ __launch_bounds__(256) void router_kernel(const float* x, const float* wr, int32_t* idx, float* wts,
+                                                     int T, int D, int E) {
+  __shared__ float lg[256];
+  const int tid = threadIdx.x;
+  const int tpb = 256 / E;
+  const int tl = tid / E, e = tid % E;
+  const int t = blockIdx.x * tpb + tl;
+  float s = 0.f;
+  if (t < T) {
+    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * D);
+    const float4* w = reinterpret_cast<const float4*>(wr + (size_t)e * D);
+    for (int i = 0; i < D / 4; i++) {
+      const float4 a = w[i], b = xr[i];
+      s = __fadd_rn(s, __fmul_rn(a.x, b.x));
+      s = __fadd_rn(s, __fmul_rn(a.y, b.y));
+      s = __fadd_rn(s, __fmul_rn(a.z, b.z));
+      s = __fadd_rn(s, __fmul_rn(a.w, b.w));
+    }
+  }
+  lg[tid] = s;
+  __syncthreads();
+  if (e == 0 && t < T) {
+    const float* l = lg + tl * E;
+    int a = 0;
+    for (int k = 1; k < E; k++)
+      if (l[k] > l[a]) a = k;
+    int b = a == 0 ? 1 : 0;
+    for (int k = 0; k < E; k++)
+      if (k != a && l[k] > l[b]) b = k;
+    const double eb = exp((double)l[b] - (double)l[a]);
+    idx[2 * t] = a;
+    idx[2 * t + 1] = b;
+    wts[2 * t] = (float)(1.0 / (1.0 + eb));
+    wts[2 * t + 1] = (float)(eb / (1.0 + eb));
+  }
+}
+
+// Single block.  Thread i owns tokens [i*per, (i+1)*per); per-expert counts
+// are scanned across threads, so rows of one expert come out in token order.
+__global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* idx, const float* wts, int T, int E,
+                                                               int* perm, float* rw, int* rowpos, int* tiles) {
+  __shared__ int sc[kMaxExperts][kPermThreads];
+  __shared__ int start[kMaxExperts + 1], total[kMaxExperts];
+  const int tid = threadIdx.x;
+  const int per = (T + kPermThreads - 1) / kPermThreads;
+  const int t0 = min(T, tid * per), t1 = min(T, t0 + per);
+  int cnt[kMaxExperts];
+#pragma unroll
+  for (int e = 0; e < kMaxExperts; e++) cnt[e] = 0;
+  for (int t = t0; t < t1; t++) {
+#pragma unroll
+    for (int e = 0; e < kMaxExperts; e++) cnt[e] += (idx[2 * t] == e) + (idx[2 * t + 1] == e);
+  }
+  // (expert loops run to the compile-time bound with an e < E guard so the
+  // per-thread arrays stay in registers)
+#pragma unroll
+  for (int e = 0; e < kMaxExperts; e++)
+    if (e < E) sc[e][tid] = cnt[e];
+  __syncthreads();
+  // inclusive Hillis-Steele scan over threads, all experts at once
+  for (int off = 1; off < kPermThreads; off <<= 1) {
+    int v[kMaxExperts];
+#pragma unroll
+    for (int e = 0; e < kMaxExperts; e++) v[e] = (e < E && tid >= off) ? sc[e][tid - off] : 0;
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < kMaxExperts; e++)
+      if (e < E) sc[e][tid] += v[e];
+    __syncthreads();
+  }
+  if (tid == 0) {
+    int p = 0, nt = 0;
+    for (int e = 0; e < E; e++) {
+      const int m = sc[e][kPermThreads - 1];
+      total[e] = m;
+      start[e] = p;
+      const int ntl = (m + kGroupRows - 1) / kGroupRows;
+      for (int j = 0; j < ntl; j++) {
+        tiles[1 + 2 * (nt + j)] = p + j * kGroupRows;
+        tiles[2 + 2 * (nt + j)] = e;
+      }
+      nt += ntl;
+      p += ntl * kGroupRows;
+    }
+    start[E] = p;
+    tiles[0] = nt;
+  }
+  __syncthreads();
+  int run[kMaxExperts];
+#pragma unroll
+  for (int e = 0; e < kMaxExperts; e++) run[e] = e < E ? start[e] + sc[e][tid] - cnt[e] : 0;  // exclusive prefix
+  for (int t = t0; t < t1; t++)
+    for (int k = 0; k < 2; k++) {
+      const int e = idx[2 * t + k];
+      int pos = 0;
+#pragma unroll
+      for (int q = 0; q < kMaxExperts; q++)
+        if (q == e) pos = run[q]++;
+      perm[pos] = t;
+      rw[pos] = wts[2 * t + k];
+      rowpos[2 * t + k] = pos;
+    }
+  // padding rows of every group
+  for (int e = 0; e < E; e++)
+    for (int r = start[e] + total[e] + tid; r < start[e + 1]; r += kPermThreads) {
+      perm[r] = -1;
+      rw[r] = 0.f;
+    }
+}
+
+__global__ __launch_bounds__(256) void gather_kernel(half_t* xg, const float* x, const int* perm, const int* tiles,
+                                                     int D) {
+  const int r = blockIdx.x;
+  if (r >= tiles[0] * kGroupRows) return;
+  const int t = perm[r];
+  for (int c = threadIdx.x * 4; c < D; c += 1024) {
+    half4 h;
+    if (t >= 0) {
+      const float4 v = *reinterpret_cast<const float4*>(x + (size_t)t * D + c);
+      h[0] = (half_t)v.x; h[1] = (half_t)v.y; h[2] = (half_t)v.z; h[3] = (half_t)v.w;
+    } else {
+      h[0] = h[1] = h[2] = h[3] = (half_t)0.f;
+    }
+    *reinterpret_cast<half4*>(xg + (size_t)r * D + c) = h;
+  }
+}
+
+__global__ __launch_bounds__(256) void combine_kernel(float* out, const float* yw, const int* rowpos, int D) {
+  const int t = blockIdx.x;
+  const float* a = yw + (size_t)rowpos[2 * t] * D;
+  const float* b = yw + (size_t)rowpos[2 * t + 1] * D;
+  for (int c = threadIdx.x * 4; c < D; c += 1024) {
+    const float4 u = *reinterpret_cast<const float4*>(a + c), v = *reinterpret_cast<const float4*>(b + c);
+    *reinterpret_cast<float4*>(out + (size_t)t * D + c) = make_float4(u.x + v.x, u.y + v.y, u.z + v.z, u.w + v.w);
+  }
+}
+
+}  // namespace
+
+struct ane_moe {
+  ane_moe_cfg cfg{};
+  int D = 0, H = 0, E = 0, TM = 0, RC = 0, T = 0;
+  std::string err;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  std::vector<void*> allocs;
+  bool params_set = false;
+  double last_ms = 0.0;
+  float* P = nullptr;  // fp32 parameters as given
+  half_t *w13 = nullptr, *w2 = nullptr;
+  float *x = nullptr, *wts = nullptr, *rw = nullptr, *yw = nullptr, *out = nullptr;
+  int32_t* idx = nullptr;
+  int *perm = nullptr, *rowpos = nullptr, *tiles = nullptr;
+  half_t *xg = nullptr, *g = nullptr;
+};
+
+namespace {
+
+int mfail(ane_moe* m, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (m) m->err = buf;
+  return code;
+}
+
+#define MCHK(op, expr)                                                                                \
+  do {                                                                                                \
+    hipError_t _h = (expr);                                                                           \
+    if (_h != hipSuccess)                                                                             \
+      return mfail(m, ANE_ERR_HIP, "storiesane moe %s: %s: %s", op, #expr, hipGetErrorString(_h));    \
+  } while (0)
+
+template <typename T>
+hipError_t malloc_(ane_moe* m, T** p, size_t n) {
+  void* q = nullptr;
+  hipError_t e = hipMalloc(&q, n * sizeof(T) > 0 ? n * sizeof(T) : 16);
+  if (e != hipSuccess) return e;
+  m->allocs.push_back(q);
+  *p = (T*)q;
+  return hipSuccess;
+}
+
+void free_all(ane_moe* m) {
+  (void)hipSetDevice(m->cfg.device);
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  for (void* p : m->allocs) (void)hipFree(p);
+  m->allocs.clear();
+  if (m->ev0) (void)hipEventDestroy(m->ev0);
+  if (m->ev1) (void)hipEventDestroy(m->ev1);
+  m->ev0 = m->ev1 = nullptr;
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  m->stream = nullptr;
+}
+
+int64_t param_count(const ane_moe_cfg& c) {
+  return (int64_t)c.experts * c.dim + (int64_t)c.experts * 3 * c.hidden * c.dim;
+}
+
+}  // namespace
+
+extern "C" int64_t ane_moe_param_count(const ane_moe_cfg* cfg) { return cfg ? param_count(*cfg) : -1; }
+
+extern "C" int ane_moe_open(const ane_moe_cfg* cfg, ane_moe** out) {
+  if (!out) return ANE_ERR_ARG;
+  ane_moe* m = new ane_moe();
+  *out = m;
+  if (!cfg) return mfail(m, ANE_ERR_ARG, "storiesane moe open: no config");
+  m->cfg = *cfg;
+  const ane_moe_cfg& c = *cfg;
+  if (c.dim <= 0 || c.dim % 64 || c.hidden <= 0 || c.hidden % 64)
+    return mfail(m, ANE_ERR_ARG, "storiesane moe open: dim=%d and hidden=%d must be positive multiples of 64", c.dim,
+                 c.hidden);
+  if (c.experts != 2 && c.experts != 4 && c.experts != 8 && c.experts != 16)
+    return mfail(m, ANE_ERR_ARG, "storiesane moe open: experts=%d must be 2, 4, 8 or 16", c.experts);
+  if (c.top_k != 2) return mfail(m, ANE_ERR_ARG, "storiesane moe open: top_k=%d (only 2 is supported)", c.top_k);
+  if (c.max_tokens < 1 || c.max_tokens > (1 << 20))
+    return mfail(m, ANE_ERR_ARG, "storiesane moe open: max_tokens=%d must be 1..%d", c.max_tokens, 1 << 20);
+  const char* op = "open";
+  m->D = c.dim; m->H = c.hidden; m->E = c.experts; m->TM = c.max_tokens;
+  // rows: two per token plus < 128 padding per expert, whole 128-row tiles
+  m->RC = (2 * m->TM + m->E * kGroupRows + kGroupRows - 1) / kGroupRows * kGroupRows;
+  const size_t D = m->D, H = m->H, E = m->E, TM = m->TM, RC = m->RC;
+  int rc = ANE_OK;
+  do {
+    hipError_t h;
+#define OPEN_CHK(expr)                                                                                 \
+    if ((h = (expr)) != hipSuccess) {                                                                 \
+      rc = mfail(m, ANE_ERR_HIP, "storiesane moe %s: %s: %s", op, #expr, hipGetErrorString(h));       \
+      break;                                                                                          \
+    }
+    OPEN_CHK(hipSetDevice(c.device));
+    OPEN_CHK(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+    OPEN_CHK(hipEventCreate(&m->ev0));
+    OPEN_CHK(hipEventCreate(&m->ev1));
+    OPEN_CHK(malloc_(m, &m->P, (size_t)param_count(c)));
+    OPEN_CHK(malloc_(m, &m->w13, E * 2 * H * D));
+    OPEN_CHK(malloc_(m, &m->w2, E * D * H));
+    OPEN_CHK(malloc_(m, &m->x, TM * D));
+    OPEN_CHK(malloc_(m, &m->idx, TM * 2));
+    OPEN_CHK(malloc_(m, &m->wts, TM * 2));
+    OPEN_CHK(malloc_(m, &m->rowpos, TM * 2));
+    OPEN_CHK(malloc_(m, &m->perm, RC));
+    OPEN_CHK(malloc_(m, &m->rw, RC));
+    OPEN_CHK(malloc_(m, &m->tiles, 1 + 2 * (RC / kGroupRows)));
+    OPEN_CHK(malloc_(m, &m->xg, RC * D));
+    OPEN_CHK(malloc_(m, &m->g, RC * H));
+    OPEN_CHK(malloc_(m, &m->yw, RC * D));
+    OPEN_CHK(malloc_(m, &m->out, TM * D));
+#undef OPEN_CHK
+  } while (0);
+  if (rc != ANE_OK) free_all(m);
+  return rc;
+}
+
+extern "C" void ane_moe_destroy(ane_moe* m) {
+  if (!m) return;
+  free_all(m);
+  delete m;
+}
+
+extern "C" const char* ane_moe_last_error(ane_moe* m) { return m ? m->err.c_str() : "no moe layer"; }
+
+extern "C" int ane_moe_set_params(ane_moe* m, const float* params, int64_t n) {
+  const char* op = "set params";
+  if (!m || !m->stream) return ANE_ERR_STATE;
+  const int64_t want = param_count(m->cfg);
+  if (!params || n != want)
+    return mfail(m, ANE_ERR_ARG, "storiesane moe set params: len=%lld want=%lld", (long long)n, (long long)want);
+  const size_t D = m->D, H = m->H;
+  const hipStream_t st = m->stream;
+  MCHK(op, hipSetDevice(m->cfg.device));
+  MCHK(op, hipMemcpyAsync(m->P, params, (size_t)n * 4, hipMemcpyHostToDevice, st));
+  for (int e = 0; e < m->E; e++) {
+    const float* base = m->P + (size_t)m->E * D + (size_t)e * 3 * H * D;
+    MCHK(op, interleave_w13(m->w13 + (size_t)e * 2 * H * D, base, base + H * D, (int)H, (int)D, st));
+    MCHK(op, f32_to_f16(m->w2 + (size_t)e * D * H, base + 2 * H * D, D * H, st));
+  }
+  MCHK(op, hipStreamSynchronize(st));
+  m->params_set = true;
+  return ANE_OK;
+}
+
+extern "C" int ane_moe_load_input(ane_moe* m, const float* x, int32_t tokens) {
+  const char* op = "load input";
+  if (!m || !m->stream) return ANE_ERR_STATE;
+  if (!x || tokens < 1 || tokens > m->TM)
+    return mfail(m, ANE_ERR_ARG, "storiesane moe load input: tokens=%d want 1..%d", tokens, m->TM);
+  MCHK(op, hipSetDevice(m->cfg.device));
+  MCHK(op, hipMemcpyAsync(m->x, x, (size_t)tokens * m->D * 4, hipMemcpyHostToDevice, m->stream));
+  MCHK(op, hipStreamSynchronize(m->stream));
+  m->T = tokens;
+  return ANE_OK;
+}
+
+extern "C" int ane_moe_run(ane_moe* m) {
+  const char* op = "run";
+  if (!m || !m->stream) return ANE_ERR_STATE;
+  if (!m->params_set) return mfail(m, ANE_ERR_STATE, "storiesane moe run: parameters not set");
+  if (m->T == 0) return mfail(m, ANE_ERR_STATE, "storiesane moe run: no input loaded");
+  const int D = m->D, H = m->H, E = m->E, T = m->T;
+  const hipStream_t st = m->stream;
+  MCHK(op, hipSetDevice(m->cfg.device));
+  MCHK(op, hipEventRecord(m->ev0, st));
+  const int tpb = 256 / E;
+  hipLaunchKernelGGL(router_kernel, dim3((T + tpb - 1) / tpb), dim3(256), 0, st, m->x, m->P, m->idx, m->wts, T, D, E);
+  MCHK(op, hipGetLastError());
+  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPermThreads), 0, st, m->idx, m->wts, T, E, m->perm, m->rw,
+                     m->rowpos, m->tiles);
+  MCHK(op, hipGetLastError());
+  hipLaunchKernelGGL(gather_kernel, dim3(m->RC), dim3(256), 0, st, m->xg, m->x, m->perm, m->tiles, D);
+  MCHK(op, hipGetLastError());
+  {
+    GemmArgs g;
+    g.A = m->xg; g.B = m->w13; g.lda = D; g.ldb = D; g.M = m->RC; g.N = 2 * H; g.K = D; g.a_t = false;
+    g.b_t = false; g.grp = m->tiles; g.b_group_stride = (size_t)2 * H * D;
+    EpiParams p;
+    p.C = m->g; p.ldc = H;
+    MCHK(op, gemm_run(g, EPI_SWIGLU, p, st, kGroupRows, 128));
+  }
+  {
+    GemmArgs g;
+    g.A = m->g; g.B = m->w2; g.lda = H; g.ldb = H; g.M = m->RC; g.N = D; g.K = H; g.a_t = false; g.b_t = false;
+    g.grp = m->tiles; g.b_group_stride = (size_t)D * H;
+    EpiParams p;
+    p.C = m->yw; p.ldc = D; p.rowscale = m->rw;
+    MCHK(op, gemm_run(g, EPI_STORE_RS, p, st, kGroupRows, 64));
+  }
+  hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, st, m->out, m->yw, m->rowpos, D);
+  MCHK(op, hipGetLastError());
+  MCHK(op, hipEventRecord(m->ev1, st));
+  MCHK(op, hipEventSynchronize(m->ev1));
+  float ms = 0.f;
+  MCHK(op, hipEventElapsedTime(&ms, m->ev0, m->ev1));
+  m->last_ms = ms;
+  return ANE_OK;
+}
+
+extern "C" int ane_moe_read_output(ane_moe* m, float* out, int32_t* experts, float* weights) {
+  const char* op = "read output";
+  if (!m || !m->stream) return ANE_ERR_STATE;
+  if (m->T == 0) return mfail(m, ANE_ERR_STATE, "storiesane moe read output: no input loaded");
+  MCHK(op, hipSetDevice(m->cfg.device));
+  if (out) MCHK(op, hipMemcpyAsync(out, m->out, (size_t)m->T * m->D * 4, hipMemcpyDeviceToHost, m->stream));
+  if (experts) MCHK(op, hipMemcpyAsync(experts, m->idx, (size_t)m->T * 8, hipMemcpyDeviceToHost, m->stream));
+  if (weights) MCHK(op, hipMemcpyAsync(weights, m->wts, (size_t)m->T * 8, hipMemcpyDeviceToHost, m->stream));
+  MCHK(op, hipStreamSynchronize(m->stream));
+  return ANE_OK;
+}
+
+extern "C" double ane_moe_last_ms(ane_moe* m) { return m ? m->last_ms : 0.0; }

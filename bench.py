@@ -112,6 +112,28 @@ def decode_bench(ane, steps, batch=64, plen=1024):
             "tokens_head": toks[0, :8].tolist()}
 
 
+def moe_bench(ane, iters=10, tokens=8192):
+    """MoE FFN layer (dim 768, 8 SwiGLU experts of
+    hidden 2048, top-2 router; weights N(0, 0.02) and activations N(0, 1)
+    from seed 5), input resident in HBM; device time per forward."""
+    from ane.moe import MoeConfig, MoeLayer, init_moe_params, make_moe_input
+    cfg = MoeConfig()
+    layer = MoeLayer(cfg, init_moe_params(cfg, seed=5, std=0.02), max_tokens=tokens)
+    layer.Load(make_moe_input(cfg, tokens, seed=5))
+    for _ in range(2):
+        layer.Run()
+    ms = []
+    for _ in range(iters):
+        layer.Run()
+        ms.append(layer.LastMs())
+    layer.Close()
+    avg = float(np.mean(ms))
+    flops = 2.0 * tokens * cfg.experts * cfg.dim + 2 * 2.0 * tokens * 3 * cfg.dim * cfg.hidden
+    tf = flops / (avg * 1e-3) / 1e12
+    return {"value": round(tokens / (avg * 1e-3), 1), "unit": "tokens/s", "tokens": tokens, "ms": round(avg, 4),
+            "tflops_alg": round(tf, 1), "mfma_frac": round(tf / PEAK_FP16_TFLOPS, 4), "iters": iters}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -124,6 +146,7 @@ def main():
     ap.add_argument("--no-train", action="store_true", help="skip the B16 training-step leg")
     ap.add_argument("--train-steps", type=int, default=5)
     ap.add_argument("--no-decode", action="store_true", help="skip the GQA decode leg")
+    ap.add_argument("--no-moe", action="store_true", help="skip the MoE FFN leg")
     ap.add_argument("--decode-steps", type=int, default=128)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -188,6 +211,8 @@ def main():
         out["train_step_b16"] = train_bench(ane, args.arch, args.train_steps)
     if not args.no_decode:
         out["decode"] = decode_bench(ane, args.decode_steps)
+    if not args.no_moe:
+        out["moe_ffn"] = moe_bench(ane)
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(cfg, params, tok, tgt, threads)

@@ -265,6 +265,38 @@ int32_t ane_decode_position(ane_decoder *d);
 /* device time of the last ane_decode_generate call (ms, HIP events) */
 double ane_decode_last_ms(ane_decoder *d);
 
+/* ---- mixture-of-experts SwiGLU FFN layer ----------------------------------
+ * No counterpart in the reference (its FFN is dense, ane/common.go:91-105
+ * linearCF is the primitive reused).  Top-2 routing: router logits in fp32
+ * with linearCF's operation order (bit-exact with a CPU evaluation of the
+ * same order), the two largest logits (ties to the lower expert), weights =
+ * softmax over those two; out[t] = w0 * FFN_e0(x[t]) + w1 * FFN_e1(x[t]),
+ * FFN_e(x) = W2_e (silu(W1_e x) * W3_e x).  No capacity limit.  Parameters
+ * (flat fp32): router [E][D], then per expert W1 [H][D], W3 [H][D],
+ * W2 [D][H]. */
+typedef struct {
+  int32_t dim, hidden; /* multiples of 64 */
+  int32_t experts;     /* 2, 4, 8 or 16 */
+  int32_t top_k;       /* 2 */
+  int32_t max_tokens;
+  int32_t device;
+} ane_moe_cfg;
+
+typedef struct ane_moe ane_moe;
+
+int ane_moe_open(const ane_moe_cfg *cfg, ane_moe **out);
+void ane_moe_destroy(ane_moe *m);
+const char *ane_moe_last_error(ane_moe *m);
+int64_t ane_moe_param_count(const ane_moe_cfg *cfg);
+int ane_moe_set_params(ane_moe *m, const float *params, int64_t n);
+/* copies x [tokens][dim] fp32 to device memory; ane_moe_run then works on it */
+int ane_moe_load_input(ane_moe *m, const float *x, int32_t tokens);
+/* route, group, expert GEMMs, combine on the resident input (device time: ane_moe_last_ms) */
+int ane_moe_run(ane_moe *m);
+/* out [tokens][dim] fp32; experts / weights [tokens][2] (either may be NULL) */
+int ane_moe_read_output(ane_moe *m, float *out, int32_t *experts, float *weights);
+double ane_moe_last_ms(ane_moe *m);
+
 #ifdef __cplusplus
 }
 #endif

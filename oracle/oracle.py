@@ -32,6 +32,10 @@ class OrcDecCfg(C.Structure):
                 ("layers", C.c_int32), ("vocab", C.c_int32), ("rope_theta", C.c_double)]
 
 
+class OrcMoeCfg(C.Structure):
+    _fields_ = [("dim", C.c_int32), ("hidden", C.c_int32), ("experts", C.c_int32)]
+
+
 class OrcAdam(C.Structure):
     _fields_ = [(n, C.c_float) for n in (
         "lr", "beta1", "beta2", "eps", "weight_decay", "grad_clip", "embed_lr_mult",
@@ -84,6 +88,13 @@ def lib():
         L.orc_dec_param_count.argtypes = [C.POINTER(OrcDecCfg)]
         L.orc_decode.restype = None
         L.orc_decode.argtypes = [C.POINTER(OrcDecCfg), fp, u16, C.c_int, C.c_int, u16, C.c_int, C.c_int, u16, fp]
+        i32 = C.POINTER(C.c_int32)
+        L.orc_moe_param_count.restype = C.c_size_t
+        L.orc_moe_param_count.argtypes = [C.POINTER(OrcMoeCfg)]
+        L.orc_moe_route.restype = None
+        L.orc_moe_route.argtypes = [C.POINTER(OrcMoeCfg), fp, fp, C.c_int, i32, fp]
+        L.orc_moe_forward.restype = None
+        L.orc_moe_forward.argtypes = [C.POINTER(OrcMoeCfg), fp, fp, C.c_int, C.c_int, fp, i32, fp]
         ncpu = os.cpu_count() or 1
         L.orc_set_threads(min(ncpu, 64))
         L.orc_set_parallel_linear(1)
@@ -241,6 +252,38 @@ def decode(cfg, params, prefix, nsteps, forced=None, want_logits=False, threads=
                      _u16(forced) if forced is not None else None, int(nsteps), int(th), _u16(toks),
                      _f(lg) if lg is not None else None)
     return toks, lg
+
+
+def _moe_cfg(dim, hidden, experts):
+    return OrcMoeCfg(int(dim), int(hidden), int(experts))
+
+
+def moe_param_count(dim, hidden, experts) -> int:
+    return int(lib().orc_moe_param_count(C.byref(_moe_cfg(dim, hidden, experts))))
+
+
+def moe_route(params, x, hidden, experts):
+    """x fp32 [T, D] -> (expert ids int32 [T, 2], weights fp32 [T, 2])."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, D = x.shape
+    idx = np.zeros((T, 2), np.int32)
+    w = np.zeros((T, 2), np.float32)
+    lib().orc_moe_route(C.byref(_moe_cfg(D, hidden, experts)), _f(params), _f(x), T,
+                        idx.ctypes.data_as(C.POINTER(C.c_int32)), _f(w))
+    return idx, w
+
+
+def moe_forward(params, x, hidden, experts, threads=None):
+    """Mixture-of-experts FFN (oracle/refmoe.c): returns (out [T, D], idx, w)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, D = x.shape
+    out = np.zeros((T, D), np.float32)
+    idx = np.zeros((T, 2), np.int32)
+    w = np.zeros((T, 2), np.float32)
+    lib().orc_moe_forward(C.byref(_moe_cfg(D, hidden, experts)), _f(params), _f(x), T,
+                          int(threads or os.cpu_count() or 1), _f(out),
+                          idx.ctypes.data_as(C.POINTER(C.c_int32)), _f(w))
+    return out, idx, w
 
 
 def drand48_stream(seed, n):

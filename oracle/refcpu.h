@@ -112,6 +112,19 @@ size_t orc_dec_param_count(const orc_dec_cfg *c);
 void orc_decode(const orc_dec_cfg *c, const float *params, const uint16_t *prefix, int nseq, int plen,
                 const uint16_t *forced, int nsteps, int threads, uint16_t *tokens_out, float *logits_out);
 
+/* --- mixture-of-experts FFN layer (refmoe.c) ---------------------------
+ * params: router [E][D], then per expert W1 [H][D], W3 [H][D], W2 [D][H].
+ * x, out: [T][D] fp32.  idx / wts: [T][2] (chosen experts, ties to the
+ * lower index; weights = softmax over the two chosen logits). */
+typedef struct {
+  int32_t dim, hidden, experts;
+} orc_moe_cfg;
+
+size_t orc_moe_param_count(const orc_moe_cfg *c);
+void orc_moe_route(const orc_moe_cfg *c, const float *params, const float *x, int T, int32_t *idx, float *wts);
+void orc_moe_forward(const orc_moe_cfg *c, const float *params, const float *x, int T, int threads, float *out,
+                     int32_t *idx, float *wts);
+
 #ifdef __cplusplus
 }
 #endif
