@@ -7,14 +7,22 @@ token ids uniform in [0, 32000) from seed 2, fp16 weights/activations with
 fp32 accumulation.  The token windows are resident in HBM before timing
 starts (Options.Tokens + per-call window positions).
 
-Prints ONE JSON line.  Besides the throughput it carries:
-  roofline      the dominant kernel's achieved TFLOP/s (algorithmic FLOPs per
-                launch / mean launch time from HIP events recorded on the
-                engine's stream during the timed steps) against the MI355X
-                dense fp16 MFMA peak;
-  cpu_baseline  the reference's CPU path (the C oracle, with the reference's
-                threading: serial linearCF, parallel norms / classifier / CE)
-                timed on a bounded sample of the same workload on this host.
+Prints ONE JSON line.  Besides the throughput (timed without instrumentation)
+it carries:
+  roofline        the dominant kernel's achieved TFLOP/s (algorithmic FLOPs
+                  per launch / mean launch time from HIP events recorded on
+                  the engine's stream in a second pass of the same steps)
+                  against the MI355X dense fp16 MFMA peak; `traffic` is its
+                  HBM bytes per launch from the committed rocprofv3 --pmc
+                  summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated);
+  train_step_b16  BASELINE configs[2]: fwd + bwd + clip + AdamW, B16 x 256;
+  decode          BASELINE configs[3]: GQA KV-cache greedy decode, tokens/s
+                  and achieved GB/s against HBM peak;
+  moe_ffn         BASELINE configs[4]: top-2 MoE FFN layer, 8192 tokens;
+  cpu_baseline    the reference's CPU path (the C oracle, with the reference's
+                  threading: serial linearCF, parallel norms / classifier /
+                  CE) timed on a bounded sample of the same workload on this
+                  host.
 """
 import argparse
 import json
@@ -32,6 +40,23 @@ import numpy as np  # noqa: E402
 METRIC = "fwd+loss tokens/s (stories110M, B32x256, fp16) + MFMA util %; decode tok/s"
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+
+
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fwd_gemm_b32_llama2_pmc_traffic.md")
+
+
+def measured_traffic(kernel_class):
+    """HBM bytes per launch of a forward GEMM class, as measured by the two
+    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE, copy-calibrated) whose
+    summary is committed in profiles/; None when not measured."""
+    try:
+        for line in open(TRAFFIC_SUMMARY):
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic:" and parts[1] == kernel_class:
+                return int(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(cfg, params, tok, tgt, threads):
@@ -134,6 +159,21 @@ def moe_bench(ane, iters=10, tokens=8192):
             "tflops_alg": round(tf, 1), "mfma_frac": round(tf / PEAK_FP16_TFLOPS, 4), "iters": iters}
 
 
+def copy_calibration(mb):
+    """A plain device-to-device copy of `mb` MiB (HIP's blit kernel), the
+    reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings into
+    bytes: run under --pmc, the copy's readings divided by mb MiB give the
+    counters' bytes-per-unit factor."""
+    import torch
+    n = mb * (1 << 20) // 2
+    src = torch.ones(n, dtype=torch.float16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n * 2, "copies": 3}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -148,7 +188,12 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the GQA decode leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE FFN leg")
     ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the forward shards "
               "by sequence with no exchange, so N GPUs would each run this same single-GPU workload.",
@@ -201,7 +246,8 @@ def main():
         achieved = per_launch / (avg_ms * 1e-3) / 1e12
         out["roofline"] = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
                            "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-                           "traffic": None, "avg_launch_ms": round(avg_ms, 5), "flops_per_launch": per_launch}
+                           "traffic": measured_traffic(dom) if args.arch == "llama2" and B == 32 else None,
+                           "avg_launch_ms": round(avg_ms, 5), "flops_per_launch": per_launch}
         g_ms = sum(prof[k]["ms"] for k in gemm_cls)
         g_fl = sum(prof[k]["flops"] for k in gemm_cls)
         out["mfma_util_projection_gemms"] = round(g_fl / (g_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)
