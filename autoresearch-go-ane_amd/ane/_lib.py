@@ -95,6 +95,9 @@ SIGNATURES = {
     "ane_grads": (C.c_int, [_eng, _u16, _u16, C.c_int32, _fp, _fp]),
     "ane_set_grads": (C.c_int, [_eng, _fp, C.c_int64, C.c_uint32]),
     "ane_get_opt_state": (C.c_int, [_eng, _fp, _fp, C.c_int64]),
+    "ane_set_opt_state": (C.c_int, [_eng, _fp, _fp, C.c_int64]),
+    "ane_get_accum_grads": (C.c_int, [_eng, _fp, C.c_int64]),
+    "ane_seed_sampler": (C.c_int, [_eng, C.c_int64]),
     "ane_profile_enable": (C.c_int, [_eng, C.c_int]),
     "ane_profile_read": (C.c_int, [_eng, C.POINTER(ProfEntry), C.c_int, C.c_int]),
     "ane_sync": (C.c_int, [_eng]),
@@ -103,7 +106,7 @@ SIGNATURES = {
     "ane_debug_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, C.c_float, C.c_int, _u16,
                                       _u16, _fp]),
     "ane_debug_last_error": (C.c_char_p, []),
-    "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 11 + [_fp]),
+    "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 11 + [_u16, _u16, _fp]),
     "ane_decode_open": (C.c_int, [C.POINTER(DecodeCfg), C.POINTER(C.c_void_p)]),
     "ane_decode_destroy": (None, [_eng]),
     "ane_decode_last_error": (C.c_char_p, [_eng]),

@@ -124,6 +124,7 @@ class Engine:
         self._h = handle
         self.cfg = cfg
         self.max_batch = opts.max_batch
+        self.seed = opts.seed or 42  # Open's default (ane/engine.go:201-203)
         self._ntokens = 0
 
     # -- weights ---------------------------------------------------------
@@ -221,6 +222,61 @@ class Engine:
         v = np.zeros(n, np.float32)
         _check(self._lib, self._h, self._lib.ane_get_opt_state(self._h, _f32(m), _f32(v), n))
         return m, v
+
+    def SetOptState(self, m, v):
+        n = param_count(self.cfg)
+        m = np.ascontiguousarray(m, dtype=np.float32).reshape(-1)
+        v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+        _check(self._lib, self._h, self._lib.ane_set_opt_state(self._h, _f32(m), _f32(v), n))
+
+    def AccumGrads(self) -> np.ndarray:
+        """The pending loss-scaled gradient sum (what the checkpoint trailer stores)."""
+        g = np.zeros(param_count(self.cfg), np.float32)
+        _check(self._lib, self._h, self._lib.ane_get_accum_grads(self._h, _f32(g), g.size))
+        return g
+
+    # -- checkpoints (ane/engine.go:515-564) -------------------------------
+    def SaveCheckpoint(self, path: str, meta=None):
+        """V5 file + SANE trailer; meta's LR / loss / counters come from the engine."""
+        from .checkpoint import TrainMeta, write_checkpoint
+        if not self._h:
+            raise EngineError(_lib.ANE_ERR_CLOSED, "storiesane save checkpoint: engine is closed")
+        meta = dataclasses.replace(meta) if meta is not None else TrainMeta()
+        st = self.State()
+        meta.LR = self.LR()
+        meta.Loss = st.last_loss
+        meta.CumTrain = st.cum_train_ms
+        meta.CumWall = st.cum_wall_ms
+        meta.CumSteps = int(st.cum_steps)
+        meta.CumBatches = int(st.cum_batches)
+        meta.AdamT = int(st.adam_t)
+        m, v = self.OptState()
+        write_checkpoint(path, self.cfg, meta, self.Params(), m, v, token_pos=int(st.token_pos),
+                         pending=int(st.pending_steps), accum=self.AccumGrads())
+
+    def LoadCheckpoint(self, path: str):
+        """Restores weights, moments, LR, counters and the pending gradients;
+        re-seeds the window sampler with Options.Seed + meta.Step."""
+        from .checkpoint import read_checkpoint
+        if not self._h:
+            raise EngineError(_lib.ANE_ERR_CLOSED, "storiesane load checkpoint: engine is closed")
+        meta, params, m, v, trailer = read_checkpoint(path, self.cfg)
+        self.SetParams(params)
+        self.SetOptState(m, v)
+        self.SetLR(meta.LR)
+        pending, token_pos, accum = 0, 0, None
+        if trailer is not None:
+            pending, token_pos, accum = trailer["pending"], trailer["token_pos"], trailer["accum"]
+        self.SetGrads(accum if accum is not None else np.zeros(param_count(self.cfg), np.float32),
+                      pending if accum is not None else 0)
+        st = _lib.State(token_pos, meta.Loss, meta.CumTrain, meta.CumWall, meta.CumSteps, meta.CumBatches,
+                        meta.AdamT, pending if accum is not None else 0)
+        self.LoadState(st)
+        _check(self._lib, self._h, self._lib.ane_seed_sampler(self._h, int(self.seed) + int(meta.Step)))
+        return meta
+
+    def Prepare(self):
+        """ane/runtime.go:10: nothing to compile ahead of time on this engine."""
 
     # -- diagnostics -----------------------------------------------------
     def ProfileEnable(self, on: bool = True):

@@ -707,11 +707,11 @@ __global__ void debug_fill_kernel(half_t* p, size_t n, uint32_t seed) {
   }
 }
 
-// Times `iters` launches of one GEMM (device-resident operands filled with
-// pseudo-random values in [-0.5, 0.5)) with HIP events; *avg_ms receives
-// the mean launch time.
+// Times `iters` launches of one GEMM with HIP events; *avg_ms receives the
+// mean launch time.  Operands: the host arrays A, B (stored as for
+// ane_debug_gemm) when given, else pseudo-random values in [-0.5, 0.5).
 extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw,
-                                    int ns, int iters, float* avg_ms) {
+                                    int ns, int iters, const uint16_t* A, const uint16_t* B, float* avg_ms) {
   if (epi != EPI_STORE_F && epi != EPI_STORE_H) {
     g_debug_err = "storiesane debug: epilogue must be STORE_F or STORE_H";
     return ANE_ERR_ARG;
@@ -725,8 +725,10 @@ extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int
   DBGCHK(hipMalloc(&dA, (size_t)M * K * 2));
   DBGCHK(hipMalloc(&dB, (size_t)N * K * 2));
   DBGCHK(hipMalloc(&dC, (size_t)M * N * (epi == EPI_STORE_F ? 4 : 2)));
-  hipLaunchKernelGGL(debug_fill_kernel, dim3(1024), dim3(256), 0, nullptr, (half_t*)dA, (size_t)M * K, 1u);
-  hipLaunchKernelGGL(debug_fill_kernel, dim3(1024), dim3(256), 0, nullptr, (half_t*)dB, (size_t)N * K, 2u);
+  if (A) DBGCHK(hipMemcpy(dA, A, (size_t)M * K * 2, hipMemcpyHostToDevice));
+  else hipLaunchKernelGGL(debug_fill_kernel, dim3(1024), dim3(256), 0, nullptr, (half_t*)dA, (size_t)M * K, 1u);
+  if (B) DBGCHK(hipMemcpy(dB, B, (size_t)N * K * 2, hipMemcpyHostToDevice));
+  else hipLaunchKernelGGL(debug_fill_kernel, dim3(1024), dim3(256), 0, nullptr, (half_t*)dB, (size_t)N * K, 2u);
   DBGCHK(hipGetLastError());
   DBGCHK(hipEventCreate(&e0));
   DBGCHK(hipEventCreate(&e1));

@@ -548,6 +548,41 @@ extern "C" int ane_get_opt_state(ane_engine* e, float* m, float* v, int64_t n) {
   return ANE_OK;
 }
 
+extern "C" int ane_set_opt_state(ane_engine* e, const float* m, const float* v, int64_t n) {
+  CLOSED_CHECK("set optimizer state");
+  const char* op = "set optimizer state";
+  if (n != e->pm.total)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane set optimizer state: len=%lld want=%lld", (long long)n,
+                    (long long)e->pm.total);
+  int rc = ensure_train(e, op);
+  if (rc) return rc;
+  if (m) HIPCHK(op, hipMemcpyAsync(e->tr.M, m, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
+  else HIPCHK(op, hipMemsetAsync(e->tr.M, 0, (size_t)n * 4, e->stream));
+  if (v) HIPCHK(op, hipMemcpyAsync(e->tr.Vv, v, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
+  else HIPCHK(op, hipMemsetAsync(e->tr.Vv, 0, (size_t)n * 4, e->stream));
+  HIPCHK(op, hipStreamSynchronize(e->stream));
+  return ANE_OK;
+}
+
+extern "C" int ane_get_accum_grads(ane_engine* e, float* grads, int64_t n) {
+  CLOSED_CHECK("accumulated grads");
+  const char* op = "accumulated grads";
+  if (!grads || n != e->pm.total)
+    return eng_fail(e, ANE_ERR_ARG, "storiesane accumulated grads: len=%lld want=%lld", (long long)n,
+                    (long long)e->pm.total);
+  int rc = ensure_train(e, op);
+  if (rc) return rc;
+  HIPCHK(op, hipMemcpyAsync(grads, e->tr.G, (size_t)n * 4, hipMemcpyDeviceToHost, e->stream));
+  HIPCHK(op, hipStreamSynchronize(e->stream));
+  return ANE_OK;
+}
+
+extern "C" int ane_seed_sampler(ane_engine* e, int64_t seed) {
+  CLOSED_CHECK("seed sampler");
+  e->rng = drand48_seed(seed);
+  return ANE_OK;
+}
+
 extern "C" float ane_lr(const ane_engine* e) { return (e && !e->closed) ? e->lr : 0.f; }
 
 extern "C" int ane_set_lr(ane_engine* e, float lr) {

@@ -181,6 +181,18 @@ int ane_set_grads(ane_engine *e, const float *grads, int64_t n, uint32_t pending
 /* Reads the AdamW moments (OptimState, ane/stories/cpu.go:294-301). */
 int ane_get_opt_state(ane_engine *e, float *m, float *v, int64_t n);
 
+/* Checkpoint support (SaveCheckpoint / LoadCheckpoint, ane/engine.go:515-564,
+ * the V5 file of ane/stories/ckpt.go:77-269 and the "SANE" trailer,
+ * ane/engine.go:684-767; the file I/O lives with the host caller):
+ * ane_set_opt_state restores the moments (NULL = zeros);
+ * ane_get_accum_grads reads the pending loss-scaled gradient sum the trailer
+ * stores (restored with ane_set_grads); ane_seed_sampler re-seeds the
+ * window sampler the way LoadCheckpoint does (drand48Seed(seed + step),
+ * ane/engine.go:560). */
+int ane_set_opt_state(ane_engine *e, const float *m, const float *v, int64_t n);
+int ane_get_accum_grads(ane_engine *e, float *grads, int64_t n);
+int ane_seed_sampler(ane_engine *e, int64_t seed);
+
 /* ---- diagnostics -------------------------------------------------------- */
 
 /* Per-kernel-class device timing with HIP events on the engine's stream.
@@ -218,9 +230,9 @@ int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_
 int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float scale, int hilo,
                         const uint16_t *qkv, uint16_t *out, float *lse);
 /* Mean time of `iters` launches of one GEMM on device-resident operands
- * (arguments as ane_debug_gemm). */
+ * (arguments as ane_debug_gemm; A / B NULL: pseudo-random in [-0.5, 0.5)). */
 int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw, int ns,
-                         int iters, float *avg_ms);
+                         int iters, const uint16_t *A, const uint16_t *B, float *avg_ms);
 const char *ane_debug_last_error(void);
 
 /* ---- greedy KV-cache decoder (grouped-query attention) --------------------
