@@ -1,11 +1,12 @@
 // MFMA GEMM kernels (gfx950, v_mfma_f32_32x32x16_f16) with fused epilogues.
 //
-// Block = 256 threads = 4 waves in a 2x2 grid; block tile BM x BN, k-tile 64.
-// Each wave owns a (BM/2) x (BN/2) sub-tile made of 32x32 MFMA tiles, so a
-// 256x256 block keeps 256 fp32 accumulators per lane (AGPRs) and reads
-// 8 fragments of 16 B from LDS per 16 MFMAs.  The k-loop double-buffers LDS:
-// the next k-tile is fetched from HBM into registers while the current one
-// is consumed, then written to the other LDS stage; one barrier per k-tile.
+// Block = 4 waves in a 2x2 grid (or 8 in 2x4 for 256x256); block tile
+// BM x BN, k-tile 64, each wave a sub-tile of 32x32 MFMA tiles.  The k-loop
+// runs over NS LDS stages: K-major operands go HBM -> LDS directly
+// (global_load_lds), transposed ones through registers and a transposing
+// LDS write.  One barrier per k-tile, placed before the tile's last
+// 16-wide substep; right after it the freed stage is refilled with tile
+// kt+NS, and LDS fragments are read one substep ahead of their MFMAs.
 //
 // MFMA 32x32 accumulator layout (CDNA3/CDNA4): lane l, register r holds
 // row 8*(r/4) + 4*(l/32) + (r%4), column l%32.  Operand fragments: lane l
@@ -71,7 +72,28 @@ __device__ __forceinline__ void store_tmajor(half_t* tile, const half8 (&v)[8], 
 // One wave instruction fills 1 KB of LDS = 8 swizzled rows; lane l lands at
 // slot l (row l/8, physical chunk l%8), so it fetches the logical chunk that
 // the swizzle maps to that slot (the XOR swizzle is its own inverse).
+//
+// The load is issued from inline asm rather than __builtin_amdgcn_global_load_lds:
+// the compiler's wait-count model treats a pending LDS DMA as an
+// out-of-order LGKM event and then waits for lgkmcnt(0) before every use
+// of an LDS fragment -- including the reads just issued for the next
+// k-substep -- which exposes the full LDS latency on every substep.  The
+// kernel waits for these loads itself (vmcnt, before the barrier that
+// publishes the tile).
+// M0 is named as clobbered (these kernels keep nothing else in it; clang
+// warns that it is a reserved register).
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// lds_addr: the destination's LDS byte address, wave-uniform
+__device__ __forceinline__ void dma16_at(const half_t* gp, unsigned lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_addr), "v"(gp)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma16(const half_t* gp, half_t* lds_dst) {
+  dma16_at(gp, __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)lds_dst));
+}
+#pragma clang diagnostic pop
 template <int R, int NW>
 __device__ __forceinline__ void load_direct(half_t* tile, const half_t* base, int ld, int row0, int k0, int tid) {
   static_assert(R % (8 * NW) == 0, "each wave fills whole 8-row groups");
@@ -81,8 +103,7 @@ __device__ __forceinline__ void load_direct(half_t* tile, const half_t* base, in
     const int gi = wave + NW * it;
     const int r = gi * 8 + (lane >> 3);
     const int lc = swz(r, lane & 7);
-    const half_t* gp = base + (size_t)(row0 + r) * ld + k0 + lc * 8;
-    __builtin_amdgcn_global_load_lds((const void*)gp, (lds_ptr_t)(tile + gi * 8 * BK), 16, 0, 0);
+    dma16(base + (size_t)(row0 + r) * ld + k0 + lc * 8, tile + gi * 8 * BK);
   }
 }
 
@@ -126,131 +147,32 @@ __device__ __forceinline__ void barrier_keep_loads() { asm volatile("s_waitcnt l
 
 __device__ __forceinline__ float softcap_f(float v, float cap) { return cap * tanhf(v / cap); }
 
-// NW = 4: waves 2 x 2, one wave per SIMD.  NW = 8: waves 2 x 4, two waves
-// per SIMD, so one wave's barrier wait and LDS reads overlap the other's
-// MFMAs (wave tile (BM/2) x (BN/4)).  NS = LDS stages: with NS = 3 the
-// HBM->LDS loads run two k-tiles ahead of the MFMAs (K-major operands only).
-template <int BM, int BN, bool AT, bool BT, int EPI, int NW, int NS>
-__global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) {
-  constexpr int WN = NW / 2;                 // waves along N (2 along M)
-  constexpr int WTM = BM / 2, WTN = BN / WN; // wave tile
-  constexpr int TM = WTM / 32, TN = WTN / 32;
-  static_assert(TN >= 1 && TM >= 1, "wave tile must hold 32x32 MFMA tiles");
-  static_assert(NS == 2 || (NS == 3 && !AT && !BT), "3 stages need direct loads on both operands");
-  constexpr int STAGE = (BM + BN) * BK;
-  constexpr int LPT = (BM + BN) / (8 * NW);  // direct-load instructions per wave per k-tile
-  __shared__ __attribute__((aligned(16))) half_t lds[NS * STAGE];
+// logistic function with the hardware reciprocal (1 ulp) instead of an IEEE
+// division sequence; its results feed fp16 stores or fp32 gates
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-
-  // block -> tile: spread consecutive tiles of one XCD over a contiguous
-  // range (hardware deals block i to XCD i % 8), then walk groups of 8
-  // M-tiles so neighbouring blocks share A rows and B columns in L2.
-  const int nbm = g.M / BM, nbn = g.N / BN, nb = nbm * nbn;
+// Block -> output tile: spread consecutive tiles of one XCD over a
+// contiguous range (hardware deals block i to XCD i % 8), then walk groups
+// of 8 M-tiles so neighbouring blocks share A rows and B columns in L2.
+__device__ __forceinline__ void block_tile(int nbm, int nbn, int& bm, int& bn) {
+  const int nb = nbm * nbn;
   int bid = blockIdx.x;
   if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
   constexpr int GROUP = 8;
   const int group_size = GROUP * nbn;
   const int first_m = (bid / group_size) * GROUP;
   const int gm = min(nbm - first_m, GROUP);
-  const int bm = first_m + (bid % group_size) % gm;
-  const int bn = (bid % group_size) / gm;
-  int m0 = bm * BM;
-  const int n0 = bn * BN;
-  const half_t* Bp = g.B;
-  if (g.grp) {  // grouped: row tile bm of the valid tiles, B of its group
-    if (bm >= g.grp[0]) return;  // whole block, before any LDS traffic
-    m0 = g.grp[1 + 2 * bm];
-    Bp += (size_t)g.grp[2 + 2 * bm] * g.b_group_stride;
-  }
+  bm = first_m + (bid % group_size) % gm;
+  bn = (bid % group_size) / gm;
+}
 
-  floatx16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-#pragma unroll
-    for (int j = 0; j < TN; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-
-  Stage<BM, AT, NW> sa;
-  Stage<BN, BT, NW> sb;
-  const int nk = g.K / BK;
-#pragma unroll
-  for (int p = 0; p < NS - 1; p++) {
-    if (p < nk) {
-      sa.issue(g.A, g.lda, m0, p * BK, lds + p * STAGE, tid);
-      sb.issue(Bp, g.ldb, n0, p * BK, lds + p * STAGE + BM * BK, tid);
-    }
-  }
-  sa.commit(lds, tid);
-  sb.commit(lds + BM * BK, tid);
-  if constexpr (NS == 3) {
-    if (nk > 1)
-      wait_vm<LPT>();  // tile 0 landed, tile 1 may still fly
-    else
-      wait_tile();
-    barrier_keep_loads();
-  } else {
-    wait_tile();
-    __syncthreads();
-  }
-
-  const int frow = lane & 31, fch = lane >> 5;
-  int arow[TM], brow[TN];
-#pragma unroll
-  for (int i = 0; i < TM; i++) arow[i] = wm * WTM + i * 32 + frow;
-#pragma unroll
-  for (int j = 0; j < TN; j++) brow[j] = wn * WTN + j * 32 + frow;
-
-  for (int kt = 0; kt < nk; kt++) {
-    const half_t* cur = lds + (kt % NS) * STAGE;
-    half_t* nxt = lds + ((kt + 1) % NS) * STAGE;             // register-path target (NS == 2)
-    half_t* far = lds + ((kt + NS - 1) % NS) * STAGE;        // direct-load target
-    if (kt + NS - 1 < nk) {
-      sa.issue(g.A, g.lda, m0, (kt + NS - 1) * BK, far, tid);
-      sb.issue(Bp, g.ldb, n0, (kt + NS - 1) * BK, far + BM * BK, tid);
-    }
-    // fragments double-buffered across the four 16-wide k-substeps
-    half8 a[2][TM], b[2][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++) a[0][i] = ld_h8(cur + arow[i] * BK + swz(arow[i], fch) * 8);
-#pragma unroll
-    for (int j = 0; j < TN; j++) b[0][j] = ld_h8(cur + BM * BK + brow[j] * BK + swz(brow[j], fch) * 8);
-#pragma unroll
-    for (int s = 0; s < BK / 16; s++) {
-      const int c = s & 1;
-      if (s + 1 < BK / 16) {
-        const int ch = (s + 1) * 2 + fch;
-#pragma unroll
-        for (int i = 0; i < TM; i++) a[c ^ 1][i] = ld_h8(cur + arow[i] * BK + swz(arow[i], ch) * 8);
-#pragma unroll
-        for (int j = 0; j < TN; j++) b[c ^ 1][j] = ld_h8(cur + BM * BK + brow[j] * BK + swz(brow[j], ch) * 8);
-      }
-#pragma unroll
-      for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[c][i], b[c][j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) {
-      sa.commit(nxt, tid);
-      sb.commit(nxt + BM * BK, tid);
-    }
-    // tile kt+1 must have landed; with 3 stages tile kt+2 may stay in flight
-    if constexpr (NS == 3) {
-      if (kt + 2 < nk)
-        wait_vm<LPT>();
-      else
-        wait_tile();
-      barrier_keep_loads();
-    } else {
-      wait_tile();
-      __syncthreads();
-    }
-  }
-
-  // ---------------------------------------------------------------- epilogue
+// Fused epilogue of one wave's TM x TN grid of 32x32 accumulator tiles.
+// The wave owns rows m0 + wm*WTM + [0, WTM) and columns n0 + wn*WTN + [0, WTN)
+// of C; bm is the block's row-tile index (classifier partials); lds is
+// free scratch once the main loop is done (classifier reduction).
+template <int BN, int WTM, int WTN, int TM, int TN, int EPI>
+__device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs& g, const EpiParams& e, int m0,
+                                         int n0, int bm, int wm, int wn, int lane, half_t* lds) {
   const int rbase = m0 + wm * WTM + 4 * (lane >> 5);
   const int cbase = n0 + wn * WTN + (lane & 31);
 #define ROW(i, r) (rbase + (i) * 32 + 8 * ((r) >> 2) + ((r) & 3))
@@ -360,7 +282,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) 
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           float h1 = acc[i][j][r], h3 = acc[i][j + 1][r];
-          float sg = 1.0f / (1.0f + __expf(-h1));
+          float sg = sigmoid_f(h1);
           size_t row = (size_t)ROW(i, r);
           C[row * e.ldc + hcol] = (half_t)(h1 * sg * h3);
           if (C2) {
@@ -406,7 +328,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) 
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const float dg = acc[i][j][r];
-          const float sg = 1.0f / (1.0f + __expf(-h1v[r]));
+          const float sg = sigmoid_f(h1v[r]);
           const size_t row = (size_t)ROW(i, r) * e.ldc;
           C[row + c1] = (half_t)(dg * h3v[r] * (sg + h1v[r] * sg * (1.f - sg)));
           C[row + c1 + 32] = (half_t)(dg * h1v[r] * sg);
@@ -448,7 +370,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) 
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const size_t idx = (size_t)ROW(i, r) * e.ldc + COL(j);
-          const float ga = 1.0f / (1.0f + __expf(-acc[i][j][r]));
+          const float ga = sigmoid_f(acc[i][j][r]);
           C[idx] = cur[r] + alpha * ga * prev[r];
           if (C2) C2[idx] = ga;
         }
@@ -530,6 +452,289 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) 
 #undef COL
 }
 
+// NW = 4: waves 2 x 2, one wave per SIMD.  NW = 8: waves 2 x 4, two waves
+// per SIMD, so one wave's barrier wait and LDS reads overlap the other's
+// MFMAs (wave tile (BM/2) x (BN/4)).  NS = LDS stages: with NS = 3 the
+// HBM->LDS loads run two k-tiles ahead of the MFMAs (K-major operands only).
+template <int BM, int BN, bool AT, bool BT, int EPI, int NW, int NS>
+__global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) {
+  constexpr int WN = NW / 2;                 // waves along N (2 along M)
+  constexpr int WTM = BM / 2, WTN = BN / WN; // wave tile
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(TN >= 1 && TM >= 1, "wave tile must hold 32x32 MFMA tiles");
+  static_assert(NS == 2 || (NS == 3 && !AT && !BT), "3 stages need direct loads on both operands");
+  constexpr int STAGE = (BM + BN) * BK;
+  constexpr int LPT = (BM + BN) / (8 * NW);  // direct-load instructions per wave per k-tile
+  __shared__ __attribute__((aligned(16))) half_t lds[NS * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  int bm, bn;
+  block_tile(g.M / BM, g.N / BN, bm, bn);
+  int m0 = bm * BM;
+  const int n0 = bn * BN;
+  const half_t* Bp = g.B;
+  if (g.grp) {  // grouped: row tile bm of the valid tiles, B of its group
+    if (bm >= g.grp[0]) return;  // whole block, before any LDS traffic
+    m0 = g.grp[1 + 2 * bm];
+    Bp += (size_t)g.grp[2 + 2 * bm] * g.b_group_stride;
+  }
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  Stage<BM, AT, NW> sa;
+  Stage<BN, BT, NW> sb;
+  const int nk = g.K / BK;
+  // Prologue: tile 0 in LDS stage 0; tiles 1 .. NS-1 also fetched (direct
+  // path: into their stages; register path: tile 1 waits in registers for
+  // the first iteration's commit).
+  sa.issue(g.A, g.lda, m0, 0, lds, tid);
+  sb.issue(Bp, g.ldb, n0, 0, lds + BM * BK, tid);
+  sa.commit(lds, tid);
+  sb.commit(lds + BM * BK, tid);
+#pragma unroll
+  for (int p = 1; p < NS; p++) {
+    if (p < nk) {
+      sa.issue(g.A, g.lda, m0, p * BK, lds + p * STAGE, tid);
+      sb.issue(Bp, g.ldb, n0, p * BK, lds + p * STAGE + BM * BK, tid);
+    }
+  }
+  wait_tile();
+  __syncthreads();
+
+  const int frow = lane & 31, fch = lane >> 5;
+  int arow[TM], brow[TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++) arow[i] = wm * WTM + i * 32 + frow;
+#pragma unroll
+  for (int j = 0; j < TN; j++) brow[j] = wn * WTN + j * 32 + frow;
+
+  // Fragments are double-buffered one 16-wide k-substep ahead of the MFMAs
+  // that use them.  sched_barrier fences keep the compiler from sinking the
+  // LDS reads next to their first use (which it otherwise does to save
+  // registers, exposing the LDS latency every two MFMAs).
+  half8 fa[2][TM], fb[2][TN];
+  auto load_frags = [&](half8 (&a)[TM], half8 (&b)[TN], const half_t* st, int s) {
+    const int ch = 2 * s + fch;
+#pragma unroll
+    for (int i = 0; i < TM; i++) a[i] = ld_h8(st + arow[i] * BK + swz(arow[i], ch) * 8);
+#pragma unroll
+    for (int j = 0; j < TN; j++) b[j] = ld_h8(st + BM * BK + brow[j] * BK + swz(brow[j], ch) * 8);
+  };
+  auto mfmas = [&](const half8 (&a)[TM], const half8 (&b)[TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+  };
+  load_frags(fa[0], fb[0], lds, 0);
+
+  for (int kt = 0; kt < nk; kt++) {
+    half_t* cur = lds + (kt % NS) * STAGE;
+    half_t* nxt = lds + ((kt + 1) % NS) * STAGE;
+#pragma unroll
+    for (int s = 0; s + 1 < BK / 16; s++) {
+      load_frags(fa[(s + 1) & 1], fb[(s + 1) & 1], cur, s + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      mfmas(fa[s & 1], fb[s & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // The last substep's fragments are in registers: once every wave has
+    // passed this barrier, stage kt is free.  So the barrier sits before the
+    // last substep's MFMAs, which then hide the first LDS reads of tile
+    // kt+1 and the issue of the HBM reads of tile kt+NS into stage kt --
+    // those get four substeps of MFMA work to land.
+    if (kt + 1 < nk) {
+      sa.commit(nxt, tid);  // register path: tile kt+1, fetched one iteration ago
+      sb.commit(nxt + BM * BK, tid);
+      // tile kt+1 must have landed; with 3 stages tile kt+2 may stay in flight
+      if constexpr (NS == 3) {
+        if (kt + 2 < nk)
+          wait_vm<LPT>();
+        else
+          wait_tile();
+        barrier_keep_loads();
+      } else {
+        wait_tile();
+        __syncthreads();
+      }
+      load_frags(fa[0], fb[0], nxt, 0);
+      if (kt + NS < nk) {
+        sa.issue(g.A, g.lda, m0, (kt + NS) * BK, cur, tid);
+        sb.issue(Bp, g.ldb, n0, (kt + NS) * BK, cur + BM * BK, tid);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    mfmas(fa[1], fb[1]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the epilogue of the CE variant reuses LDS as scratch
+  if constexpr (EPI == EPI_CE) __syncthreads();
+
+  epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, e, m0, n0, bm, wm, wn, lane, lds);
+}
+
+// ---- 256x256 tile, 4 waves, hand-ordered k-loop ---------------------------
+// Waves 2 x 2, wave tile 128x128: 16 MFMAs per 16-wide k-substep against 8
+// LDS fragment reads (0.5 KB of LDS reads per MFMA, the least a 4-wave
+// 256x256 tile allows), 256 fp32 accumulators per lane (AGPRs).  Both
+// operands K-major, HBM -> LDS by DMA, 2 stages of 64 KB.
+//
+// One wave per SIMD, so nothing hides a stall of this wave's MFMA stream:
+// the instruction order inside each substep is fixed by sched_barrier
+// fences -- MFMAs go out in pairs and each pair is followed by at most one
+// LDS read (the next substep's fragments) and one HBM -> LDS load (16 per
+// wave per k-tile).  Per tile kt:
+//   s0: reads of s1; second half (B) of tile kt+1's loads into stage kt+1
+//   s1: reads of s2
+//   s2: reads of s3, all in the first half (they must land before the barrier)
+//   wait for tile kt+1, barrier (stage kt is free from here)
+//   s3: reads of s0 of tile kt+1; first half (A) of tile kt+2's loads into
+//       stage kt
+// so a tile's loads are issued 2-3 substeps (1000-1500 MFMA cycles) before
+// the barrier that needs them.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_p256_kernel(GemmArgs g, EpiParams e) {
+  constexpr int BM = 256, BN = 256, TM = 4, TN = 4, WTM = 128, WTN = 128;
+  constexpr int STAGE = (BM + BN) * BK;  // halves
+  __shared__ __attribute__((aligned(16))) half_t lds[2 * STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int bm, bn;
+  block_tile(g.M / BM, g.N / BN, bm, bn);
+  const int m0 = bm * BM, n0 = bn * BN;
+  const int nk = g.K / BK;
+
+  // HBM -> LDS: load q (0..7) of a wave fills rows 8*gi .. 8*gi+7 of the
+  // operand's 256-row tile, gi = wave + 4q (same swizzled slot mapping as
+  // load_direct); per-lane source pointers at k = 0.
+  const half_t* pa[8];
+  const half_t* pb[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    const int r = (wave + 4 * q) * 8 + (lane >> 3);
+    const int lc = swz(r, lane & 7);
+    pa[q] = g.A + (size_t)(m0 + r) * g.lda + lc * 8;
+    pb[q] = g.B + (size_t)(n0 + r) * g.ldb + lc * 8;
+  }
+  // LDS byte addresses in scalar registers: the wave index made uniform
+  // once, so each load costs one 64-bit address add and the M0 write
+  const unsigned lds0 = (unsigned)(size_t)(lds_ptr_t)lds;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  auto dma_a = [&](int q, int kt, int st) {
+    dma16_at(pa[q] + kt * BK, lds0 + 2u * (unsigned)(st * STAGE + (wave_s + 4 * q) * 8 * BK));
+  };
+  auto dma_b = [&](int q, int kt, int st) {
+    dma16_at(pb[q] + kt * BK, lds0 + 2u * (unsigned)(st * STAGE + BM * BK + (wave_s + 4 * q) * 8 * BK));
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+  const int frow = lane & 31, fch = lane >> 5;
+  // fragment reads of one substep, in the order the MFMAs consume them:
+  // a0, b0..b3 (the i = 0 row of MFMAs), then a1..a3
+  auto read_frag = [&](half8 (&a)[TM], half8 (&b)[TN], const half_t* st, int s, int q) {
+    const int ch = 2 * s + fch;
+    if (q == 0 || q >= 5) {
+      const int i = q == 0 ? 0 : q - 4;
+      const int row = wm * WTM + i * 32 + frow;
+      a[i] = ld_h8(st + row * BK + swz(row, ch) * 8);
+    } else {
+      const int j = q - 1;
+      const int row = wn * WTN + j * 32 + frow;
+      b[j] = ld_h8(st + BM * BK + row * BK + swz(row, ch) * 8);
+    }
+  };
+  // one substep: MFMAs on (ca, cb), each MFMA pair followed by reads of
+  // the next substep's fragments (EARLY: two per pair in the first four
+  // pairs, else one per pair) and, when dma_on, one HBM -> LDS load
+  // (DMA 1: A half of tile dkt into LDS stage dst, 2: B half)
+  auto substep = [&](auto early_c, auto dma_c, const half8 (&ca)[TM], const half8 (&cb)[TN], half8 (&na)[TM],
+                     half8 (&nb)[TN], const half_t* rs, int rsub, bool dma_on, int dkt, int dst) {
+    constexpr bool EARLY = decltype(early_c)::value;
+    constexpr int DMA = decltype(dma_c)::value;
+#pragma unroll
+    for (int p = 0; p < 8; p++) {
+      const int i = p >> 1, j = (p & 1) * 2;
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ca[i], cb[j], acc[i][j], 0, 0, 0);
+      acc[i][j + 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ca[i], cb[j + 1], acc[i][j + 1], 0, 0, 0);
+      if constexpr (EARLY) {
+        if (p < 4) {
+          read_frag(na, nb, rs, rsub, 2 * p);
+          read_frag(na, nb, rs, rsub, 2 * p + 1);
+        }
+      } else {
+        read_frag(na, nb, rs, rsub, p);
+      }
+      if constexpr (DMA == 1) {
+        if (dma_on) dma_a(p, dkt, dst);
+      }
+      if constexpr (DMA == 2) {
+        if (dma_on) dma_b(p, dkt, dst);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  using F = std::false_type;
+  using T = std::true_type;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+
+  // prologue: tiles 0 and 1 in flight, wait for both
+#pragma unroll
+  for (int q = 0; q < 8; q++) {
+    dma_a(q, 0, 0);
+    dma_b(q, 0, 0);
+  }
+  if (nk > 1) {
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      dma_a(q, 1, 1);
+      dma_b(q, 1, 1);
+    }
+  }
+  wait_tile();
+  __syncthreads();
+  half8 fa[2][TM], fb[2][TN];
+#pragma unroll
+  for (int q = 0; q < 8; q++) read_frag(fa[0], fb[0], lds, 0, q);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // One straight-line body for every tile (the register allocator keeps
+  // the 256 accumulators in place only without diverging copies of the
+  // MFMA stream): the last tile's s3 still reads the other stage (in
+  // bounds, unused) and still passes the barrier.
+  for (int kt = 0; kt < nk; kt++) {
+    half_t* cur = lds + (kt & 1) * STAGE;
+    half_t* nxt = lds + ((kt + 1) & 1) * STAGE;
+    substep(F{}, I2{}, fa[0], fb[0], fa[1], fb[1], cur, 1, kt >= 1 && kt + 1 < nk, kt + 1, (kt + 1) & 1);
+    substep(F{}, I0{}, fa[1], fb[1], fa[0], fb[0], cur, 2, false, 0, 0);
+    substep(T{}, I0{}, fa[0], fb[0], fa[1], fb[1], cur, 3, false, 0, 0);
+    wait_tile();           // this wave's loads of tile kt+1
+    barrier_keep_loads();  // everyone's, and every read of stage kt is done
+    substep(F{}, I1{}, fa[1], fb[1], fa[0], fb[0], nxt, 0, kt + 2 < nk, kt + 2, kt & 1);
+  }
+  // the epilogue of the CE variant reuses LDS as scratch
+  if constexpr (EPI == EPI_CE) __syncthreads();
+  epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, e, m0, n0, bm, wm, wn, lane, lds);
+}
+
 template <bool AT, bool BT, int EPI, int BM, int BN, int NW = 4, int NS = 2>
 hipError_t launch_tile(const GemmArgs& g, const EpiParams& e, hipStream_t s) {
   dim3 grid((g.M / BM) * (g.N / BN));
@@ -542,6 +747,10 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
   const int key = bm * 1000 + bn;
   if (nw == 8) return launch_tile<AT, BT, EPI, 256, 256, 8>(g, e, s);  // caller checked the tile
   if constexpr (!AT && !BT) {
+    if (key == 256256 && ns == 2 && !g.grp) {
+      hipLaunchKernelGGL(gemm_p256_kernel<EPI>, dim3((g.M / 256) * (g.N / 256)), dim3(256), 0, s, g, e);
+      return hipGetLastError();
+    }
     if (ns == 3) {  // caller checked the tile
       switch (key) {
         case 256128: return launch_tile<AT, BT, EPI, 256, 128, 4, 3>(g, e, s);

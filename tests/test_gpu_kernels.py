@@ -51,6 +51,21 @@ def test_gemm_layouts_and_tiles(a_t, b_t, bm, bn, nw):
     np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-4)
 
 
+@pytest.mark.parametrize("bm,bn,nw", [(256, 256, 4), (256, 256, 8), (128, 128, 4)])
+@pytest.mark.parametrize("K", [64, 128, 192, 256, 832])
+def test_gemm_every_k_tile_count(bm, bn, nw, K):
+    """Prefetch schedules (loads of tile kt+2 issued around tile kt's
+    barrier): 1, 2, 3, 4 and 13 k-tiles; the 4-wave 256x256 tile is the
+    hand-ordered kernel."""
+    r = np.random.default_rng(bm + nw + K)
+    M, N = 512, 512
+    A = r.standard_normal((M, K)).astype(np.float16)
+    B = r.standard_normal((N, K)).astype(np.float16)
+    got = run_gemm(A, B, False, False, bm, bn, nw=nw)
+    ref = A.astype(np.float64) @ B.astype(np.float64).T
+    np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-4)
+
+
 @pytest.mark.parametrize("bm,bn", TILES_3STAGE)
 @pytest.mark.parametrize("K", [64, 128, 192, 640])
 def test_gemm_three_stage_pipeline(bm, bn, K):
