@@ -699,6 +699,65 @@ done:
   return rc;
 }
 
+// One K-major GEMM (A [M, K], B [N, K]) with a fused forward epilogue on
+// host buffers.  Element types and shapes by epilogue:
+//   STORE_H, RELU2: C fp16 [M, N];  RELU2: C2 fp16 [M, N] (pre-activation)
+//   SWIGLU: C fp16 [M, N/2] over 32-column interleaved W1|W3, C2 fp16 [M, N]
+//   STORE_F, LOGITS (softcap = 15 when seq < 0), RESID, SMEAR: C fp32 [M, N]
+//   RESID: R fp32 [M, N] (C = alpha R + acc + beta X0; X0 optional; C2 fp32
+//          copy optional);  SMEAR: X0 fp32 [M, N], rows t with t % seq == 0
+//          have no predecessor, C2 fp32 gate
+// C2 / X0 / R may be NULL where optional.
+extern "C" int ane_debug_gemm_epi(int epi, int M, int N, int K, const uint16_t* A, const uint16_t* B, void* C,
+                                  void* C2, const float* X0, const float* R, float alpha, float beta, int seq, int bm,
+                                  int bn, int nw) {
+  const bool f32 = epi == EPI_STORE_F || epi == EPI_LOGITS || epi == EPI_RESID || epi == EPI_SMEAR;
+  if (!f32 && epi != EPI_STORE_H && epi != EPI_RELU2 && epi != EPI_SWIGLU) {
+    g_debug_err = "storiesane debug: unsupported epilogue";
+    return ANE_ERR_ARG;
+  }
+  if ((epi == EPI_RESID && !R) || (epi == EPI_SMEAR && (!X0 || seq <= 0))) {
+    g_debug_err = "storiesane debug: missing epilogue operand";
+    return ANE_ERR_ARG;
+  }
+  int rc = ANE_OK;
+  void *dA = nullptr, *dB = nullptr, *dC = nullptr, *dC2 = nullptr, *dX0 = nullptr, *dR = nullptr;
+  const size_t MN = (size_t)M * N;
+  const size_t cbytes = epi == EPI_SWIGLU ? MN : (f32 ? MN * 4 : MN * 2);
+  const size_t c2bytes = (epi == EPI_RESID || epi == EPI_SMEAR) ? MN * 4 : MN * 2;
+  GemmArgs g;
+  EpiParams p;
+  DBGCHK(hipMalloc(&dA, (size_t)M * K * 2));
+  DBGCHK(hipMalloc(&dB, (size_t)N * K * 2));
+  DBGCHK(hipMalloc(&dC, cbytes));
+  DBGCHK(hipMemcpy(dA, A, (size_t)M * K * 2, hipMemcpyHostToDevice));
+  DBGCHK(hipMemcpy(dB, B, (size_t)N * K * 2, hipMemcpyHostToDevice));
+  if (C2) DBGCHK(hipMalloc(&dC2, c2bytes));
+  if (X0) {
+    DBGCHK(hipMalloc(&dX0, MN * 4));
+    DBGCHK(hipMemcpy(dX0, X0, MN * 4, hipMemcpyHostToDevice));
+  }
+  if (R) {
+    DBGCHK(hipMalloc(&dR, MN * 4));
+    DBGCHK(hipMemcpy(dR, R, MN * 4, hipMemcpyHostToDevice));
+  }
+  g.A = (const half_t*)dA; g.B = (const half_t*)dB;
+  g.lda = K; g.ldb = K; g.M = M; g.N = N; g.K = K; g.a_t = false; g.b_t = false;
+  p.C = dC; p.ldc = epi == EPI_SWIGLU ? N / 2 : N;
+  p.C2 = dC2; p.ldc2 = N;
+  p.X0 = (const float*)dX0; p.R = (const float*)dR;
+  p.alpha = alpha; p.beta = beta; p.seq = seq;
+  if (epi == EPI_LOGITS && seq < 0) { p.softcap = 1; p.cap = 15.f; }
+  DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn, nw, 0));
+  DBGCHK(hipDeviceSynchronize());
+  DBGCHK(hipMemcpy(C, dC, cbytes, hipMemcpyDeviceToHost));
+  if (C2) DBGCHK(hipMemcpy(C2, dC2, c2bytes, hipMemcpyDeviceToHost));
+done:
+  for (void* q : {dA, dB, dC, dC2, dX0, dR})
+    if (q) (void)hipFree(q);
+  return rc;
+}
+
 __global__ void debug_fill_kernel(half_t* p, size_t n, uint32_t seed) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
     uint32_t x = (uint32_t)i * 2654435761u ^ seed;
@@ -712,19 +771,24 @@ __global__ void debug_fill_kernel(half_t* p, size_t n, uint32_t seed) {
 // ane_debug_gemm) when given, else pseudo-random values in [-0.5, 0.5).
 extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw,
                                     int ns, int iters, const uint16_t* A, const uint16_t* B, float* avg_ms) {
-  if (epi != EPI_STORE_F && epi != EPI_STORE_H) {
-    g_debug_err = "storiesane debug: epilogue must be STORE_F or STORE_H";
+  if (epi != EPI_STORE_F && epi != EPI_STORE_H && epi != EPI_RESID && epi != EPI_SWIGLU && epi != EPI_CE) {
+    g_debug_err = "storiesane debug: epilogue must be STORE_F, STORE_H, RESID, SWIGLU or CE";
     return ANE_ERR_ARG;
   }
   int rc = ANE_OK;
-  void *dA = nullptr, *dB = nullptr, *dC = nullptr;
+  void *dA = nullptr, *dB = nullptr, *dC = nullptr, *dX = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   GemmArgs g;
   EpiParams p;
   float ms = 0.f;
   DBGCHK(hipMalloc(&dA, (size_t)M * K * 2));
   DBGCHK(hipMalloc(&dB, (size_t)N * K * 2));
-  DBGCHK(hipMalloc(&dC, (size_t)M * N * (epi == EPI_STORE_F ? 4 : 2)));
+  DBGCHK(hipMalloc(&dC, (size_t)M * N * 4));
+  // CE side buffers: targets (zeros), per-64-row-block partials, target logits
+  if (epi == EPI_CE) {
+    DBGCHK(hipMalloc(&dX, (size_t)N * 2 + (size_t)(M / 64) * N * sizeof(float2) + (size_t)N * 4 + 256));
+    DBGCHK(hipMemset(dX, 0, (size_t)N * 2));
+  }
   if (A) DBGCHK(hipMemcpy(dA, A, (size_t)M * K * 2, hipMemcpyHostToDevice));
   else hipLaunchKernelGGL(debug_fill_kernel, dim3(1024), dim3(256), 0, nullptr, (half_t*)dA, (size_t)M * K, 1u);
   if (B) DBGCHK(hipMemcpy(dB, B, (size_t)N * K * 2, hipMemcpyHostToDevice));
@@ -736,6 +800,15 @@ extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int
   g.lda = a_t ? M : K; g.ldb = b_t ? N : K;
   g.M = M; g.N = N; g.K = K; g.a_t = a_t != 0; g.b_t = b_t != 0;
   p.C = dC; p.ldc = N;
+  if (epi == EPI_RESID) p.R = (const float*)dC;
+  if (epi == EPI_SWIGLU) p.ldc = N / 2;
+  if (epi == EPI_CE) {
+    char* x = (char*)dX;
+    p.targets = (const uint16_t*)x;
+    p.partial = (float2*)(x + (((size_t)N * 2 + 255) & ~(size_t)255));
+    p.tgt_logit = (float*)((char*)p.partial + (size_t)(M / 64) * N * sizeof(float2));
+    p.vocab = M;
+  }
   DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn, nw, ns));
   DBGCHK(hipDeviceSynchronize());
   DBGCHK(hipEventRecord(e0, nullptr));
@@ -750,6 +823,7 @@ done:
   if (dA) (void)hipFree(dA);
   if (dB) (void)hipFree(dB);
   if (dC) (void)hipFree(dC);
+  if (dX) (void)hipFree(dX);
   return rc;
 }
 

@@ -836,8 +836,12 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0) return hipErrorInvalidValue;
   if (bm == 0 || bn == 0) gemm_pick_tile(g.M, g.N, g.K, epi, &bm, &bn);
   if (bm == 0 || bn == 0 || (g.M % bm) || (g.N % bn)) return hipErrorInvalidValue;
-  // 256x256 tiles run with 8 waves unless 4 are asked for (measured faster on every shape)
-  if (nw == 0) nw = (bm == 256 && bn == 256) ? 8 : 4;
+  // 256x256 tiles: K-major operands run the hand-ordered 4-wave kernel, the
+  // transposed layouts and the classifier epilogues (whose reductions over
+  // 128-row wave tiles spill next to 256 accumulators) 8 waves -- each
+  // measured fastest for its case
+  if (nw == 0)
+    nw = (bm == 256 && bn == 256 && (g.a_t || g.b_t || g.grp || epi == EPI_CE || epi == EPI_DLOGITS)) ? 8 : 4;
   if (nw != 4 && !(nw == 8 && bm == 256 && bn == 256)) return hipErrorInvalidValue;
   if (ns == 0) ns = 2;
   // three LDS stages: both operands K-major, 4 waves, tiles whose 3 stages fit the 160 KB LDS

@@ -177,8 +177,10 @@ def copy_calibration(mb):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=30)
+    # ~100 ms of untimed work: the MI355X shader clock ramps from ~1.4 GHz to
+    # its sustained ~2.0 GHz over the first tens of milliseconds of load
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--arch", default="llama2", choices=["llama2", "nanochat"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")

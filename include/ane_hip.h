@@ -227,10 +227,20 @@ int ane_sync(ane_engine *e);
  * Messages: ane_debug_last_error(). */
 int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_t *A, const uint16_t *B,
                    void *C, int bm, int bn, int nw, int ns);
+/* One K-major GEMM (A [M, K], B [N, K]) with a fused forward epilogue on host
+ * buffers (epi: 0 fp16 store, 1 fp32 store, 2 logits (softcap 15 when
+ * seq < 0), 3 residual C = alpha R + acc + beta X0 (+ copy to C2), 4 SwiGLU
+ * over 32-column interleaved W1|W3 (C fp16 [M, N/2], C2 fp16 h1|h3), 5
+ * relu^2 (C2 = pre-activation), 6 smear (X0, seq; C2 = gate)).  Optional
+ * operands may be NULL. */
+int ane_debug_gemm_epi(int epi, int M, int N, int K, const uint16_t *A, const uint16_t *B, void *C, void *C2,
+                       const float *X0, const float *R, float alpha, float beta, int seq, int bm, int bn, int nw);
 int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float scale, int hilo,
                         const uint16_t *qkv, uint16_t *out, float *lse);
 /* Mean time of `iters` launches of one GEMM on device-resident operands
- * (arguments as ane_debug_gemm; A / B NULL: pseudo-random in [-0.5, 0.5)). */
+ * (arguments as ane_debug_gemm; A / B NULL: pseudo-random in [-0.5, 0.5)).
+ * epi: 0 fp16 store, 1 fp32 store, 3 in-place residual add, 4 SwiGLU over
+ * interleaved W1|W3 columns, 7 classifier cross-entropy partials. */
 int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw, int ns,
                          int iters, const uint16_t *A, const uint16_t *B, float *avg_ms);
 const char *ane_debug_last_error(void);

@@ -1,0 +1,121 @@
+"""Fused GEMM epilogues of the forward pass, one GEMM each, against a float64
+reference of the same formula: fp16 / fp32 stores, logits (plain and
+softcapped), the residual add (alpha R + acc + beta X0, with its copy), the
+SwiGLU over 32-column interleaved W1|W3 (gate and the saved h1|h3), relu^2
+(and the saved pre-activation) and the smear gate (per-sequence first rows
+have no predecessor).  Every block tile the dispatcher offers for the
+epilogue, including the hand-ordered 4-wave 256x256 kernel."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from ane import _lib
+
+pytestmark = pytest.mark.gpu
+
+EPI_STORE_H, EPI_STORE_F, EPI_LOGITS, EPI_RESID, EPI_SWIGLU, EPI_RELU2, EPI_SMEAR = 0, 1, 2, 3, 4, 5, 6
+TILES = [(256, 256, 4), (256, 256, 8), (128, 128, 4), (64, 128, 4), (128, 64, 4), (64, 64, 4)]
+M, N, K = 512, 512, 192
+
+
+def _u16(a):
+    return a.ctypes.data_as(C.POINTER(C.c_uint16))
+
+
+def _fp(a):
+    return None if a is None else a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def _vp(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+def run(epi, A, B, C_out, C2=None, X0=None, R=None, alpha=1.0, beta=0.0, seq=0, tile=(0, 0, 0)):
+    lib = _lib.load()
+    bm, bn, nw = tile
+    rc = lib.ane_debug_gemm_epi(epi, M, N, K, _u16(A.view(np.uint16)), _u16(B.view(np.uint16)), _vp(C_out), _vp(C2),
+                                _fp(X0), _fp(R), alpha, beta, seq, bm, bn, nw)
+    assert rc == 0, lib.ane_debug_last_error()
+
+
+def operands(seed):
+    r = np.random.default_rng(seed)
+    A = (r.standard_normal((M, K)) * 0.5).astype(np.float16)
+    B = (r.standard_normal((N, K)) * 0.5).astype(np.float16)
+    return r, A, B, A.astype(np.float64) @ B.astype(np.float64).T
+
+
+def close16(got, ref):
+    np.testing.assert_allclose(got.astype(np.float64), ref, rtol=2e-3, atol=2e-3)
+
+
+def close32(got, ref):
+    np.testing.assert_allclose(got.astype(np.float64), ref, rtol=1e-5, atol=5e-4)
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_store_and_logits(tile):
+    _, A, B, acc = operands(1)
+    h = np.zeros((M, N), np.float16)
+    run(EPI_STORE_H, A, B, h, tile=tile)
+    close16(h, acc)
+    f = np.zeros((M, N), np.float32)
+    run(EPI_STORE_F, A, B, f, tile=tile)
+    close32(f, acc)
+    run(EPI_LOGITS, A, B, f, seq=-1, tile=tile)
+    close32(f, 15.0 * np.tanh(acc / 15.0))
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_residual(tile):
+    r, A, B, acc = operands(2)
+    R = r.standard_normal((M, N)).astype(np.float32)
+    X0 = r.standard_normal((M, N)).astype(np.float32)
+    out = np.zeros((M, N), np.float32)
+    copy = np.zeros((M, N), np.float32)
+    run(EPI_RESID, A, B, out, C2=copy, X0=X0, R=R, alpha=0.75, beta=-0.5, tile=tile)
+    ref = 0.75 * R.astype(np.float64) + acc - 0.5 * X0.astype(np.float64)
+    close32(out, ref)
+    np.testing.assert_array_equal(copy, out)
+    run(EPI_RESID, A, B, out, R=R, tile=tile)  # plain residual, no X0 / copy
+    close32(out, R.astype(np.float64) + acc)
+
+
+@pytest.mark.parametrize("tile", [t for t in TILES if t[1] >= 128])
+def test_swiglu(tile):
+    _, A, B, acc = operands(3)
+    gate = np.zeros((M, N // 2), np.float16)
+    h13 = np.zeros((M, N), np.float16)
+    run(EPI_SWIGLU, A, B, gate, C2=h13, tile=tile)
+    blk = acc.reshape(M, N // 64, 2, 32)          # [m, pair, W1|W3, 32]
+    h1, h3 = blk[:, :, 0, :], blk[:, :, 1, :]
+    ref = (h1 / (1.0 + np.exp(-h1)) * h3).reshape(M, N // 2)
+    close16(gate, ref)
+    close16(h13, acc)
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_relu2(tile):
+    _, A, B, acc = operands(4)
+    out = np.zeros((M, N), np.float16)
+    pre = np.zeros((M, N), np.float16)
+    run(EPI_RELU2, A, B, out, C2=pre, tile=tile)
+    close16(out, np.maximum(acc, 0.0) ** 2)
+    close16(pre, acc)
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_smear(tile):
+    r, A, B, acc = operands(5)
+    seq = 128
+    X0 = r.standard_normal((M, N)).astype(np.float32)
+    out = np.zeros((M, N), np.float32)
+    gate = np.zeros((M, N), np.float32)
+    run(EPI_SMEAR, A, B, out, C2=gate, X0=X0, alpha=0.3, seq=seq, tile=tile)
+    g = 1.0 / (1.0 + np.exp(-acc))
+    prev = np.zeros_like(X0, dtype=np.float64)
+    prev[1:] = X0[:-1]
+    prev[::seq] = 0.0
+    close32(gate, g)
+    close32(out, X0.astype(np.float64) + 0.3 * g * prev)
