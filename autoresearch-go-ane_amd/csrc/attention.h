@@ -22,6 +22,8 @@ struct AttnArgs {
   half_t* qkvt;           // optional [T, 3*D]: q, k after RoPE (+ QK-norm) and v after VE, as used
   half_t* qkvt_lo;        // optional [T, 2*D]: fp16 residuals q - q_hi | k - k_hi of those q, k
   int hilo;               // scores from hi+lo split operands (~fp32); S <= 256
+  const void* pf;         // optional: weights of the next GEMM, streamed through the caches
+  size_t pf_bytes;
 };
 
 hipError_t attention_fwd(const AttnArgs& a, hipStream_t stream);

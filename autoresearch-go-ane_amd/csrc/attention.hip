@@ -35,6 +35,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) half_t Vt[HD * VST];
 
   const int S = a.S, NH = a.NH, D = NH * HD, D3 = 3 * D;
+  prefetch_slice(a.pf, a.pf_bytes, ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x,
+                 (size_t)gridDim.x * gridDim.y * gridDim.z);
   const int h = blockIdx.y, b = blockIdx.z;
   const int nthr = blockDim.x, tid = threadIdx.x;
   const size_t tok0 = (size_t)b * S;

@@ -461,7 +461,11 @@ int forward_body(ane_engine* e, int nseq, int train) {
     }
     float* xout = train ? (l + 1 < L ? tb.L[l + 1].xin : tb.xlast) : e->x;
     prof_begin(e, 6);
-    HIPCHK(op, rmsnorm_f16(A.xn, A.xin, nullptr, nullptr, llama ? P + o.g_att : nullptr, T, D, st));
+    // each memory-bound kernel also streams the next GEMM's weights through
+    // the caches (prefetch_slice): QKV here, Wo in attention, W1|W3 + W2 in
+    // the FFN norm, the classifier in the final norm
+    HIPCHK(op, rmsnorm_f16(A.xn, A.xin, nullptr, nullptr, llama ? P + o.g_att : nullptr, T, D, st, s.wqkv,
+                           (size_t)3 * D * D * sizeof(half_t)));
     prof_end(e, 0, (double)T * D * 6);
     {
       EpiParams p;
@@ -476,6 +480,7 @@ int forward_body(ane_engine* e, int nseq, int train) {
       a.nseq = nseq; a.S = S; a.NH = NH;
       a.qknorm = llama ? 0 : 1;
       a.scale = 0.125f;
+      a.pf = s.wo; a.pf_bytes = (size_t)D * D * sizeof(half_t);
       if (o.ve_embed >= 0) {
         a.ve_x = A.xin; a.ve_gate = P + o.ve_gate; a.ve_embed = P + o.ve_embed; a.tokens = e->tok; a.vocab = V;
       }
@@ -491,7 +496,8 @@ int forward_body(ane_engine* e, int nseq, int train) {
       HIPCHK(op, eng_gemm(e, 1, A.att, D, false, s.wo, D, false, T, D, D, EPI_RESID, p));
     }
     prof_begin(e, 6);
-    HIPCHK(op, rmsnorm_f16(A.xn2, A.x2, nullptr, nullptr, llama ? P + o.g_ffn : nullptr, T, D, st));
+    HIPCHK(op, rmsnorm_f16(A.xn2, A.x2, nullptr, nullptr, llama ? P + o.g_ffn : nullptr, T, D, st, s.w13,
+                           ((size_t)(llama ? 2 : 1) * H * D + (size_t)D * H) * sizeof(half_t)));  // W1|W3, W2
     prof_end(e, 0, (double)T * D * 6);
     {
       EpiParams p;
@@ -516,13 +522,16 @@ int forward_body(ane_engine* e, int nseq, int train) {
   float* xl = train ? tb.xlast : e->x;
   prof_begin(e, 6);
   if (llama) {
-    HIPCHK(op, rmsnorm_f16(e->xh, xl, nullptr, nullptr, P + e->pm.g_final, T, D, st));
+    HIPCHK(op, rmsnorm_f16(e->xh, xl, nullptr, nullptr, P + e->pm.g_final, T, D, st, e->embed_h,
+                           (size_t)V * D * sizeof(half_t)));
   } else if (train) {
     // keep the post-backout state for the final norm's backward
     HIPCHK(op, backout_fwd(tb.xfinal, xl, e->xmid, P + e->pm.backout_lambda, (size_t)T * D, st));
-    HIPCHK(op, rmsnorm_f16(e->xh, tb.xfinal, nullptr, nullptr, nullptr, T, D, st));
+    HIPCHK(op, rmsnorm_f16(e->xh, tb.xfinal, nullptr, nullptr, nullptr, T, D, st, e->embed_h,
+                           (size_t)V * D * sizeof(half_t)));
   } else {
-    HIPCHK(op, rmsnorm_f16(e->xh, xl, e->xmid, P + e->pm.backout_lambda, nullptr, T, D, st));
+    HIPCHK(op, rmsnorm_f16(e->xh, xl, e->xmid, P + e->pm.backout_lambda, nullptr, T, D, st, e->embed_h,
+                           (size_t)V * D * sizeof(half_t)));
   }
   prof_end(e, 0, (double)T * D * (llama ? 6 : 10));
   return ANE_OK;

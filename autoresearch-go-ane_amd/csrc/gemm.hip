@@ -1,12 +1,16 @@
 // MFMA GEMM kernels (gfx950, v_mfma_f32_32x32x16_f16) with fused epilogues.
 //
 // Block = 4 waves in a 2x2 grid (or 8 in 2x4 for 256x256); block tile
-// BM x BN, k-tile 64, each wave a sub-tile of 32x32 MFMA tiles.  The k-loop
-// runs over NS LDS stages: K-major operands go HBM -> LDS directly
-// (global_load_lds), transposed ones through registers and a transposing
-// LDS write.  One barrier per k-tile, placed before the tile's last
-// 16-wide substep; right after it the freed stage is refilled with tile
-// kt+NS, and LDS fragments are read one substep ahead of their MFMAs.
+// BM x BN, k-tile 64, each wave a sub-tile of 32x32 MFMA tiles.  Two k-loops:
+//   gemm_ho_kernel  both operands K-major (forward, classifier, grouped MoE):
+//                   HBM -> LDS by DMA, 2 stages, a hand-ordered instruction
+//                   stream per 16-wide substep (see there);
+//   gemm_kernel     transposed operands (the backward's dX / dW), staged
+//                   through registers and a transposing LDS write, or the
+//                   3-stage K-major variant.
+// Both place the k-tile's one barrier before its last 16-wide substep;
+// right after it the freed stage is refilled with a later k-tile, and LDS
+// fragments are read one substep ahead of their MFMAs.
 //
 // MFMA 32x32 accumulator layout (CDNA3/CDNA4): lane l, register r holds
 // row 8*(r/4) + 4*(l/32) + (r%4), column l%32.  Operand fragments: lane l
@@ -582,59 +586,86 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) 
   epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, e, m0, n0, bm, wm, wn, lane, lds);
 }
 
-// ---- 256x256 tile, 4 waves, hand-ordered k-loop ---------------------------
-// Waves 2 x 2, wave tile 128x128: 16 MFMAs per 16-wide k-substep against 8
-// LDS fragment reads (0.5 KB of LDS reads per MFMA, the least a 4-wave
-// 256x256 tile allows), 256 fp32 accumulators per lane (AGPRs).  Both
-// operands K-major, HBM -> LDS by DMA, 2 stages of 64 KB.
-//
-// One wave per SIMD, so nothing hides a stall of this wave's MFMA stream:
-// the instruction order inside each substep is fixed by sched_barrier
-// fences -- MFMAs go out in pairs and each pair is followed by at most one
-// LDS read (the next substep's fragments) and one HBM -> LDS load (16 per
-// wave per k-tile).  Per tile kt:
-//   s0: reads of s1; second half (B) of tile kt+1's loads into stage kt+1
+// ---- K-major operands: hand-ordered k-loop ---------------------------------
+// Both operands K-major (the forward, the classifier and the grouped MoE
+// GEMMs), HBM -> LDS by DMA, 2 LDS stages.  Waves 2 x NW/2; each 16-wide
+// k-substep is TM x TN MFMAs, TM + TN LDS fragment reads (the next
+// substep's) and, in two of the four substeps, the HBM -> LDS loads of a
+// later k-tile.  The instruction order inside a substep is fixed by
+// sched_barrier fences: the reads and loads are spread evenly between the
+// MFMAs, so the MFMA stream never waits behind a burst of memory
+// instructions -- with one wave per SIMD (the 4-wave 256x256 tile) nothing
+// else would hide such a stall.  Per tile kt:
+//   s0: reads of s1; B half of tile kt+1's loads into stage kt+1
 //   s1: reads of s2
 //   s2: reads of s3, all in the first half (they must land before the barrier)
 //   wait for tile kt+1, barrier (stage kt is free from here)
-//   s3: reads of s0 of tile kt+1; first half (A) of tile kt+2's loads into
-//       stage kt
-// so a tile's loads are issued 2-3 substeps (1000-1500 MFMA cycles) before
-// the barrier that needs them.
-template <int EPI>
-__global__ __launch_bounds__(256) void gemm_p256_kernel(GemmArgs g, EpiParams e) {
-  constexpr int BM = 256, BN = 256, TM = 4, TN = 4, WTM = 128, WTN = 128;
+//   s3: reads of s0 of tile kt+1; A half of tile kt+2's loads into stage kt
+// so a tile's loads are issued 2-3 substeps before the barrier that needs
+// them.  One straight-line body serves every tile (the register allocator
+// keeps the accumulators in place only without diverging copies of the MFMA
+// stream): the last tile's s3 still reads the other stage (in bounds,
+// unused) and still passes the barrier.
+//
+// Loads use the scalar-base form of global_load_lds: load q of a wave
+// fills rows 8 (w + NW q) .. +7 of the operand's tile (w = the wave), so the
+// row part of the address is wave-uniform (an SGPR pair) and the per-lane
+// part -- row lane/8 of the 8, the swizzled 16-byte chunk -- is a fixed
+// 32-bit offset; the chunk's swizzle depends on q only through
+// (w + NW q) mod 8, i.e. on q mod 8/NW.
+__device__ __forceinline__ void dma16_s(const half_t* sbase, unsigned voff, unsigned lds_addr) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_addr), "v"(voff),
+               "s"(sbase)
+               : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
+template <int BM, int BN, int EPI, int NW>
+__global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams e) {
+  constexpr int WN = NW / 2;
+  constexpr int WTM = BM / 2, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   constexpr int STAGE = (BM + BN) * BK;  // halves
+  constexpr int LA = BM / (8 * NW), LB = BN / (8 * NW);  // loads per wave per k-tile
+  constexpr int NMF = TM * TN, NRD = TM + TN;             // per substep
+  constexpr int NV = 8 / NW;
+  static_assert(TM >= 1 && TN >= 1 && LA >= 1 && LB >= 1, "tile too small for the wave grid");
   __shared__ __attribute__((aligned(16))) half_t lds[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   int bm, bn;
   block_tile(g.M / BM, g.N / BN, bm, bn);
-  const int m0 = bm * BM, n0 = bn * BN;
+  int m0 = bm * BM;
+  const int n0 = bn * BN;
+  const half_t* Bp = g.B;
+  if (g.grp) {  // grouped: row tile bm of the valid tiles, B of its group
+    if (bm >= g.grp[0]) return;  // whole block, before any LDS traffic
+    m0 = g.grp[1 + 2 * bm];
+    Bp += (size_t)g.grp[2 + 2 * bm] * g.b_group_stride;
+  }
   const int nk = g.K / BK;
 
-  // HBM -> LDS: load q (0..7) of a wave fills rows 8*gi .. 8*gi+7 of the
-  // operand's 256-row tile, gi = wave + 4q (same swizzled slot mapping as
-  // load_direct); per-lane source pointers at k = 0.
-  const half_t* pa[8];
-  const half_t* pb[8];
-#pragma unroll
-  for (int q = 0; q < 8; q++) {
-    const int r = (wave + 4 * q) * 8 + (lane >> 3);
-    const int lc = swz(r, lane & 7);
-    pa[q] = g.A + (size_t)(m0 + r) * g.lda + lc * 8;
-    pb[q] = g.B + (size_t)(n0 + r) * g.ldb + lc * 8;
-  }
-  // LDS byte addresses in scalar registers: the wave index made uniform
-  // once, so each load costs one 64-bit address add and the M0 write
-  const unsigned lds0 = (unsigned)(size_t)(lds_ptr_t)lds;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const unsigned lds0 = (unsigned)(size_t)(lds_ptr_t)lds;
+  unsigned voa[NV], vob[NV];
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const int lc = (lane & 7) ^ (((lane >> 3) ^ (wave + NW * v)) & 7);
+    voa[v] = (unsigned)(((lane >> 3) * g.lda + lc * 8) * 2);
+    vob[v] = (unsigned)(((lane >> 3) * g.ldb + lc * 8) * 2);
+  }
+  const half_t* abase = g.A + (size_t)m0 * g.lda;
+  const half_t* bbase = Bp + (size_t)n0 * g.ldb;
   auto dma_a = [&](int q, int kt, int st) {
-    dma16_at(pa[q] + kt * BK, lds0 + 2u * (unsigned)(st * STAGE + (wave_s + 4 * q) * 8 * BK));
+    const int gi = wave_s + NW * q;
+    dma16_s(abase + (size_t)(gi * 8) * g.lda + kt * BK, voa[q % NV], lds0 + 2u * (unsigned)(st * STAGE + gi * 8 * BK));
   };
   auto dma_b = [&](int q, int kt, int st) {
-    dma16_at(pb[q] + kt * BK, lds0 + 2u * (unsigned)(st * STAGE + BM * BK + (wave_s + 4 * q) * 8 * BK));
+    const int gi = wave_s + NW * q;
+    dma16_s(bbase + (size_t)(gi * 8) * g.ldb + kt * BK, vob[q % NV],
+            lds0 + 2u * (unsigned)(st * STAGE + BM * BK + gi * 8 * BK));
   };
 
   floatx16 acc[TM][TN];
@@ -646,46 +677,42 @@ __global__ __launch_bounds__(256) void gemm_p256_kernel(GemmArgs g, EpiParams e)
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
   const int frow = lane & 31, fch = lane >> 5;
-  // fragment reads of one substep, in the order the MFMAs consume them:
-  // a0, b0..b3 (the i = 0 row of MFMAs), then a1..a3
+  // fragment reads of one substep, in the order the MFMAs (i-major)
+  // consume them: a0, b0 .. b(TN-1), then a1 .. a(TM-1)
   auto read_frag = [&](half8 (&a)[TM], half8 (&b)[TN], const half_t* st, int s, int q) {
     const int ch = 2 * s + fch;
-    if (q == 0 || q >= 5) {
-      const int i = q == 0 ? 0 : q - 4;
+    if (q == 0 || q > TN) {
+      const int i = q == 0 ? 0 : q - TN;
       const int row = wm * WTM + i * 32 + frow;
       a[i] = ld_h8(st + row * BK + swz(row, ch) * 8);
     } else {
-      const int j = q - 1;
-      const int row = wn * WTN + j * 32 + frow;
-      b[j] = ld_h8(st + BM * BK + row * BK + swz(row, ch) * 8);
+      const int row = wn * WTN + (q - 1) * 32 + frow;
+      b[q - 1] = ld_h8(st + BM * BK + row * BK + swz(row, ch) * 8);
     }
   };
-  // one substep: MFMAs on (ca, cb), each MFMA pair followed by reads of
-  // the next substep's fragments (EARLY: two per pair in the first four
-  // pairs, else one per pair) and, when dma_on, one HBM -> LDS load
-  // (DMA 1: A half of tile dkt into LDS stage dst, 2: B half)
+  // one substep: MFMA p of the TM x TN grid is followed by the reads r with
+  // r * NMF / NRD == p (EARLY: r * NMF / (2 NRD) == p) and, when dma_on, the
+  // loads d with d * NMF / ND == p (DMA 1: A half of tile dkt into stage
+  // dst, 2: B half)
   auto substep = [&](auto early_c, auto dma_c, const half8 (&ca)[TM], const half8 (&cb)[TN], half8 (&na)[TM],
                      half8 (&nb)[TN], const half_t* rs, int rsub, bool dma_on, int dkt, int dst) {
     constexpr bool EARLY = decltype(early_c)::value;
     constexpr int DMA = decltype(dma_c)::value;
+    constexpr int ND = DMA == 1 ? LA : (DMA == 2 ? LB : 0);
 #pragma unroll
-    for (int p = 0; p < 8; p++) {
-      const int i = p >> 1, j = (p & 1) * 2;
+    for (int p = 0; p < NMF; p++) {
+      const int i = p / TN, j = p % TN;
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ca[i], cb[j], acc[i][j], 0, 0, 0);
-      acc[i][j + 1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ca[i], cb[j + 1], acc[i][j + 1], 0, 0, 0);
-      if constexpr (EARLY) {
-        if (p < 4) {
-          read_frag(na, nb, rs, rsub, 2 * p);
-          read_frag(na, nb, rs, rsub, 2 * p + 1);
-        }
-      } else {
-        read_frag(na, nb, rs, rsub, p);
-      }
-      if constexpr (DMA == 1) {
-        if (dma_on) dma_a(p, dkt, dst);
-      }
-      if constexpr (DMA == 2) {
-        if (dma_on) dma_b(p, dkt, dst);
+#pragma unroll
+      for (int r = 0; r < NRD; r++)
+        if ((EARLY ? r * NMF / (2 * NRD) : r * NMF / NRD) == p) read_frag(na, nb, rs, rsub, r);
+      if (dma_on) {
+#pragma unroll
+        for (int d = 0; d < ND; d++)
+          if (d * NMF / ND == p) {
+            if constexpr (DMA == 1) dma_a(d, dkt, dst);
+            if constexpr (DMA == 2) dma_b(d, dkt, dst);
+          }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -698,31 +725,25 @@ __global__ __launch_bounds__(256) void gemm_p256_kernel(GemmArgs g, EpiParams e)
 
   // prologue: tiles 0 and 1 in flight, wait for both
 #pragma unroll
-  for (int q = 0; q < 8; q++) {
-    dma_a(q, 0, 0);
-    dma_b(q, 0, 0);
-  }
+  for (int q = 0; q < LA; q++) dma_a(q, 0, 0);
+#pragma unroll
+  for (int q = 0; q < LB; q++) dma_b(q, 0, 0);
   if (nk > 1) {
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
-      dma_a(q, 1, 1);
-      dma_b(q, 1, 1);
-    }
+    for (int q = 0; q < LA; q++) dma_a(q, 1, 1);
+#pragma unroll
+    for (int q = 0; q < LB; q++) dma_b(q, 1, 1);
   }
   wait_tile();
   __syncthreads();
   half8 fa[2][TM], fb[2][TN];
 #pragma unroll
-  for (int q = 0; q < 8; q++) read_frag(fa[0], fb[0], lds, 0, q);
+  for (int q = 0; q < NRD; q++) read_frag(fa[0], fb[0], lds, 0, q);
   __builtin_amdgcn_sched_barrier(0);
 
-  // One straight-line body for every tile (the register allocator keeps
-  // the 256 accumulators in place only without diverging copies of the
-  // MFMA stream): the last tile's s3 still reads the other stage (in
-  // bounds, unused) and still passes the barrier.
   for (int kt = 0; kt < nk; kt++) {
-    half_t* cur = lds + (kt & 1) * STAGE;
-    half_t* nxt = lds + ((kt + 1) & 1) * STAGE;
+    const half_t* cur = lds + (kt & 1) * STAGE;
+    const half_t* nxt = lds + ((kt + 1) & 1) * STAGE;
     substep(F{}, I2{}, fa[0], fb[0], fa[1], fb[1], cur, 1, kt >= 1 && kt + 1 < nk, kt + 1, (kt + 1) & 1);
     substep(F{}, I0{}, fa[1], fb[1], fa[0], fb[0], cur, 2, false, 0, 0);
     substep(T{}, I0{}, fa[0], fb[0], fa[1], fb[1], cur, 3, false, 0, 0);
@@ -742,13 +763,41 @@ hipError_t launch_tile(const GemmArgs& g, const EpiParams& e, hipStream_t s) {
   return hipGetLastError();
 }
 
+#define LAUNCH_HO(BM_, BN_, NW_) \
+  hipLaunchKernelGGL((gemm_ho_kernel<BM_, BN_, EPI, NW_>), grid, dim3(64 * NW_), 0, s, g, e)
+
 template <bool AT, bool BT, int EPI>
 hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, int bn, int nw, int ns) {
   const int key = bm * 1000 + bn;
+  if constexpr (!AT && !BT) {
+    if (nw == 8 && ns == 2) {  // caller checked the tile
+      const dim3 grid((g.M / 256) * (g.N / 256));
+      LAUNCH_HO(256, 256, 8);
+      return hipGetLastError();
+    }
+  }
   if (nw == 8) return launch_tile<AT, BT, EPI, 256, 256, 8>(g, e, s);  // caller checked the tile
   if constexpr (!AT && !BT) {
-    if (key == 256256 && ns == 2 && !g.grp) {
-      hipLaunchKernelGGL(gemm_p256_kernel<EPI>, dim3((g.M / 256) * (g.N / 256)), dim3(256), 0, s, g, e);
+    if (ns == 2) {  // hand-ordered kernel for every K-major tile
+      const dim3 grid((g.M / bm) * (g.N / bn));
+      switch (key) {
+        case 256256: LAUNCH_HO(256, 256, 4); break;
+        case 256128: LAUNCH_HO(256, 128, 4); break;
+        case 128256: LAUNCH_HO(128, 256, 4); break;
+        case 128128: LAUNCH_HO(128, 128, 4); break;
+        case 64128: LAUNCH_HO(64, 128, 4); break;
+        default:
+          if constexpr (EPI != EPI_SWIGLU) {
+            switch (key) {
+              case 128064: LAUNCH_HO(128, 64, 4); break;
+              case 256064: LAUNCH_HO(256, 64, 4); break;
+              case 64064: LAUNCH_HO(64, 64, 4); break;
+              default: return hipErrorInvalidValue;
+            }
+          } else {
+            return hipErrorInvalidValue;
+          }
+      }
       return hipGetLastError();
     }
     if (ns == 3) {  // caller checked the tile
@@ -836,12 +885,10 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0) return hipErrorInvalidValue;
   if (bm == 0 || bn == 0) gemm_pick_tile(g.M, g.N, g.K, epi, &bm, &bn);
   if (bm == 0 || bn == 0 || (g.M % bm) || (g.N % bn)) return hipErrorInvalidValue;
-  // 256x256 tiles: K-major operands run the hand-ordered 4-wave kernel, the
-  // transposed layouts and the classifier epilogues (whose reductions over
-  // 128-row wave tiles spill next to 256 accumulators) 8 waves -- each
-  // measured fastest for its case
-  if (nw == 0)
-    nw = (bm == 256 && bn == 256 && (g.a_t || g.b_t || g.grp || epi == EPI_CE || epi == EPI_DLOGITS)) ? 8 : 4;
+  // 256x256 tiles run with 8 waves unless 4 are asked for (measured faster
+  // on every shape and layout: two waves per SIMD hide each other's barrier
+  // and LDS waits; the 4-wave tile's classifier reductions also spill)
+  if (nw == 0) nw = (bm == 256 && bn == 256) ? 8 : 4;
   if (nw != 4 && !(nw == 8 && bm == 256 && bn == 256)) return hipErrorInvalidValue;
   if (ns == 0) ns = 2;
   // three LDS stages: both operands K-major, 4 waves, tiles whose 3 stages fit the 160 KB LDS

@@ -56,4 +56,23 @@ __device__ __forceinline__ void st_h8(half_t* p, half8 v) {
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+// Streams slice `part` of `nparts` equal slices of [p, p + bytes) through
+// the cache hierarchy with ordinary loads and discards the data (an empty
+// asm consumes it, so the loads stay).  Memory-bound kernels call it on the
+// weights of the GEMM that runs next: by then those weights have been
+// evicted from the memory-side cache by the rest of the step's traffic, and
+// every block of the GEMM would otherwise wait on HBM latency for the same
+// weight tiles at once.  p must be 16-byte aligned; NULL is a no-op.
+__device__ __forceinline__ void prefetch_slice(const void* p, size_t bytes, size_t part, size_t nparts) {
+  if (!p || bytes < 16) return;
+  const uint4* q = reinterpret_cast<const uint4*>(p);
+  const size_t n = bytes / 16;
+  uint32_t x = 0;
+  for (size_t i = part * blockDim.x + threadIdx.x; i < n; i += nparts * blockDim.x) {
+    const uint4 v = q[i];
+    x ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  asm volatile("" ::"v"(x));
+}
+
 }  // namespace ane

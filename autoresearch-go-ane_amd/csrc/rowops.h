@@ -17,8 +17,10 @@ hipError_t embed_norm(float* xpre, float* x0, half_t* xh, const float* embed, co
 // out = fp16((x - *lam * xsub) / rms(x - lam * xsub) * gain); xsub, gain optional.
 // Gain-free form: rmsNormNoWeightCF (ane/common.go:157-174); gain form:
 // stories.RMSNorm (ane/stories/cpu.go:97-111); backout: ane/common.go:385-389.
+// pf / pf_bytes: weights of the GEMM that follows, streamed through the
+// caches alongside (prefetch_slice); NULL for none.
 hipError_t rmsnorm_f16(half_t* out, const float* x, const float* xsub, const float* lam, const float* gain,
-                       int T, int D, hipStream_t s);
+                       int T, int D, hipStream_t s, const void* pf = nullptr, size_t pf_bytes = 0);
 
 // tok[b*S + t] = data[pos[b] + t]; tgt[b*S + t] = data[pos[b] + t + 1]   ane/engine.go:403-404
 hipError_t gather_windows(uint16_t* tok, uint16_t* tgt, const uint16_t* data, const uint64_t* pos, int nseq,

@@ -43,7 +43,9 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(float* xpre, float* x0,
 }
 
 __global__ __launch_bounds__(256) void rmsnorm_kernel(half_t* out, const float* x, const float* xsub,
-                                                      const float* lamp, const float* gain, int T, int D) {
+                                                      const float* lamp, const float* gain, int T, int D,
+                                                      const void* pf, size_t pf_bytes) {
+  prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (t >= T) return;
   const float lam = xsub ? *lamp : 0.f;
@@ -205,8 +207,9 @@ hipError_t embed_norm(float* xpre, float* x0, half_t* xh, const float* E, const 
 }
 
 hipError_t rmsnorm_f16(half_t* out, const float* x, const float* xsub, const float* lam, const float* gain, int T,
-                       int D, hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows_grid(T)), dim3(256), 0, s, out, x, xsub, lam, gain, T, D);
+                       int D, hipStream_t s, const void* pf, size_t pf_bytes) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows_grid(T)), dim3(256), 0, s, out, x, xsub, lam, gain, T, D, pf,
+                     pf_bytes);
   return hipGetLastError();
 }
 
