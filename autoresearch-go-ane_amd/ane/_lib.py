@@ -102,13 +102,13 @@ SIGNATURES = {
     "ane_profile_read": (C.c_int, [_eng, C.POINTER(ProfEntry), C.c_int, C.c_int]),
     "ane_sync": (C.c_int, [_eng]),
     "ane_debug_gemm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _u16, _u16, C.c_void_p,
-                                 C.c_int, C.c_int, C.c_int, C.c_int]),
+                                 C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "ane_debug_gemm_epi": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _u16, _u16, C.c_void_p, C.c_void_p,
                                      _fp, _fp, C.c_float, C.c_float, C.c_int, C.c_int, C.c_int, C.c_int]),
     "ane_debug_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, C.c_float, C.c_int, _u16,
                                       _u16, _fp]),
     "ane_debug_last_error": (C.c_char_p, []),
-    "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 11 + [_u16, _u16, _fp]),
+    "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 12 + [_u16, _u16, _fp]),
     "ane_decode_open": (C.c_int, [C.POINTER(DecodeCfg), C.POINTER(C.c_void_p)]),
     "ane_decode_destroy": (None, [_eng]),
     "ane_decode_last_error": (C.c_char_p, [_eng]),

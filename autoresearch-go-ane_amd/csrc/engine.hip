@@ -145,6 +145,15 @@ hipError_t eng_gemm(ane_engine* e, int cls, const half_t* A, int lda, bool at, c
                     int M, int N, int K, int epi, const EpiParams& p, int bm, int bn) {
   GemmArgs g;
   g.A = A; g.B = B; g.lda = lda; g.ldb = ldb; g.M = M; g.N = N; g.K = K; g.a_t = at; g.b_t = bt;
+  // training: GEMMs whose output is too small to fill the chip split K
+  if (!at && !bt && e->tr.splitk_ws && bm == 0 && bn == 0) {
+    int sp = 1;
+    gemm_pick_split(M, N, K, epi, e->tr.splitk_cap, &bm, &bn, &sp);
+    if (sp > 1) {
+      g.splits = sp;
+      g.ws = e->tr.splitk_ws;
+    }
+  }
   prof_begin(e, cls);
   hipError_t r = gemm_run(g, epi, p, e->stream, bm, bn);
   prof_end(e, 2.0 * M * N * K, 2.0 * ((double)M * K + (double)N * K));
@@ -171,6 +180,11 @@ static void free_all(ane_engine* e) {
     }
   e->train_ready = false;
   e->tr = TrainBufs();
+  e->ls.clear();
+  e->embed_h = e->smear_h = e->embed_t = e->smear_t = nullptr;
+  e->shadow_jobs = nullptr;
+  e->n_shadow_jobs = e->n_shadow_tiles = 0;
+  e->shadow_jobs_t = false;
   if (e->stream) (void)hipStreamDestroy(e->stream);
   e->stream = nullptr;
 }
@@ -351,24 +365,56 @@ extern "C" int ane_sync(ane_engine* e) {
 // ---------------------------------------------------------------------------
 // weights
 // ---------------------------------------------------------------------------
-int refresh_shadows(ane_engine* e) {
+// Job table of shadow_refresh: every fp16 shadow (and, once training has
+// allocated them, its transpose) from the fp32 masters in one launch.
+static int build_shadow_jobs(ane_engine* e) {
   const char* op = "refresh weights";
   const ane_model_cfg& c = e->cfg;
   const int D = c.dim, H = c.hidden, V = c.vocab;
   const bool llama = c.arch == ANE_ARCH_LLAMA2;
+  std::vector<ShadowJob> jobs;
+  int tiles = 0;
+  auto add = [&](const float* src, half_t* dst, half_t* dst_t, int R, int C, int stride, int off, int ldt) {
+    ShadowJob j;
+    j.src = src; j.dst = dst; j.dst_t = dst_t; j.R = R; j.C = C; j.blk_stride = stride; j.blk_off = off;
+    j.ldt = ldt; j.tile0 = tiles;
+    tiles += (R / 64) * (C / 64);
+    jobs.push_back(j);
+  };
   for (int l = 0; l < c.layers; l++) {
     const LayerOff& o = e->pm.L[l];
-    LayerShadow& s = e->ls[l];
-    HIPCHK(op, f32_to_f16(s.wqkv, e->P + o.wq, (size_t)3 * D * D, e->stream));  // Wq|Wk|Wv are adjacent
-    HIPCHK(op, f32_to_f16(s.wo, e->P + o.wo, (size_t)D * D, e->stream));
-    if (llama)
-      HIPCHK(op, interleave_w13(s.w13, e->P + o.w1, e->P + o.w3, H, D, e->stream));
-    else
-      HIPCHK(op, f32_to_f16(s.w13, e->P + o.w1, (size_t)H * D, e->stream));
-    HIPCHK(op, f32_to_f16(s.w2, e->P + o.w2, (size_t)D * H, e->stream));
+    const LayerShadow& s = e->ls[l];
+    add(e->P + o.wq, s.wqkv, s.wqkv_t, 3 * D, D, 32, 0, 3 * D);  // Wq|Wk|Wv are adjacent
+    add(e->P + o.wo, s.wo, s.wo_t, D, D, 32, 0, D);
+    if (llama) {  // W1 / W3 rows interleaved by 32
+      add(e->P + o.w1, s.w13, s.w13_t, H, D, 64, 0, 2 * H);
+      add(e->P + o.w3, s.w13, s.w13_t, H, D, 64, 32, 2 * H);
+    } else {
+      add(e->P + o.w1, s.w13, s.w13_t, H, D, 32, 0, H);
+    }
+    add(e->P + o.w2, s.w2, s.w2_t, D, H, 32, 0, D);
   }
-  HIPCHK(op, f32_to_f16(e->embed_h, e->P + e->pm.embed, (size_t)V * D, e->stream));
-  if (!llama) HIPCHK(op, f32_to_f16(e->smear_h, e->P + e->pm.smear_gate, (size_t)D * D, e->stream));
+  add(e->P + e->pm.embed, e->embed_h, e->embed_t, V, D, 32, 0, V);
+  if (!llama) add(e->P + e->pm.smear_gate, e->smear_h, e->smear_t, D, D, 32, 0, D);
+  if (!e->shadow_jobs || (int)jobs.size() > e->n_shadow_jobs) {
+    // sized once for the largest table this engine builds (same count with or without transposes)
+    HIPCHK(op, dalloc(e, &e->shadow_jobs, jobs.size()));
+  }
+  HIPCHK(op, hipStreamSynchronize(e->stream));  // no launch still reads the old table
+  HIPCHK(op, hipMemcpy(e->shadow_jobs, jobs.data(), jobs.size() * sizeof(ShadowJob), hipMemcpyHostToDevice));
+  e->n_shadow_jobs = (int)jobs.size();
+  e->n_shadow_tiles = tiles;
+  e->shadow_jobs_t = e->embed_t != nullptr;
+  return ANE_OK;
+}
+
+int refresh_shadows(ane_engine* e) {
+  const char* op = "refresh weights";
+  if (!e->shadow_jobs || e->shadow_jobs_t != (e->embed_t != nullptr)) {
+    int rc = build_shadow_jobs(e);
+    if (rc) return rc;
+  }
+  HIPCHK(op, shadow_refresh(e->shadow_jobs, e->n_shadow_jobs, e->n_shadow_tiles, e->stream));
   return ANE_OK;
 }
 
@@ -679,19 +725,23 @@ static int debug_fail(const char* what, hipError_t h) {
 extern "C" const char* ane_debug_last_error(void) { return g_debug_err.c_str(); }
 
 extern "C" int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_t* A, const uint16_t* B,
-                              void* C, int bm, int bn, int nw, int ns) {
+                              void* C, int bm, int bn, int nw, int ns, int splits) {
   if (epi != EPI_STORE_F && epi != EPI_STORE_H) {
     g_debug_err = "storiesane debug: epilogue must be STORE_F or STORE_H";
     return ANE_ERR_ARG;
   }
   int rc = ANE_OK;
-  void *dA = nullptr, *dB = nullptr, *dC = nullptr;
+  void *dA = nullptr, *dB = nullptr, *dC = nullptr, *dW = nullptr;
   const size_t esz = epi == EPI_STORE_F ? 4 : 2;
   GemmArgs g;
   EpiParams p;
+  if (splits < 1) splits = 1;
   DBGCHK(hipMalloc(&dA, (size_t)M * K * 2));
   DBGCHK(hipMalloc(&dB, (size_t)N * K * 2));
   DBGCHK(hipMalloc(&dC, (size_t)M * N * esz));
+  if (splits > 1) DBGCHK(hipMalloc(&dW, (size_t)splits * M * N * 4));
+  g.splits = splits;
+  g.ws = (float*)dW;
   DBGCHK(hipMemcpy(dA, A, (size_t)M * K * 2, hipMemcpyHostToDevice));
   DBGCHK(hipMemcpy(dB, B, (size_t)N * K * 2, hipMemcpyHostToDevice));
   g.A = (const half_t*)dA; g.B = (const half_t*)dB;
@@ -705,6 +755,7 @@ done:
   if (dA) (void)hipFree(dA);
   if (dB) (void)hipFree(dB);
   if (dC) (void)hipFree(dC);
+  if (dW) (void)hipFree(dW);
   return rc;
 }
 
@@ -779,20 +830,25 @@ __global__ void debug_fill_kernel(half_t* p, size_t n, uint32_t seed) {
 // mean launch time.  Operands: the host arrays A, B (stored as for
 // ane_debug_gemm) when given, else pseudo-random values in [-0.5, 0.5).
 extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw,
-                                    int ns, int iters, const uint16_t* A, const uint16_t* B, float* avg_ms) {
+                                    int ns, int splits, int iters, const uint16_t* A, const uint16_t* B,
+                                    float* avg_ms) {
   if (epi != EPI_STORE_F && epi != EPI_STORE_H && epi != EPI_RESID && epi != EPI_SWIGLU && epi != EPI_CE) {
     g_debug_err = "storiesane debug: epilogue must be STORE_F, STORE_H, RESID, SWIGLU or CE";
     return ANE_ERR_ARG;
   }
   int rc = ANE_OK;
-  void *dA = nullptr, *dB = nullptr, *dC = nullptr, *dX = nullptr;
+  void *dA = nullptr, *dB = nullptr, *dC = nullptr, *dX = nullptr, *dW = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   GemmArgs g;
   EpiParams p;
   float ms = 0.f;
+  if (splits < 1) splits = 1;
   DBGCHK(hipMalloc(&dA, (size_t)M * K * 2));
   DBGCHK(hipMalloc(&dB, (size_t)N * K * 2));
   DBGCHK(hipMalloc(&dC, (size_t)M * N * 4));
+  if (splits > 1) DBGCHK(hipMalloc(&dW, (size_t)splits * M * N * 4));
+  g.splits = splits;
+  g.ws = (float*)dW;
   // CE side buffers: targets (zeros), per-64-row-block partials, target logits
   if (epi == EPI_CE) {
     DBGCHK(hipMalloc(&dX, (size_t)N * 2 + (size_t)(M / 64) * N * sizeof(float2) + (size_t)N * 4 + 256));
@@ -833,6 +889,7 @@ done:
   if (dB) (void)hipFree(dB);
   if (dC) (void)hipFree(dC);
   if (dX) (void)hipFree(dX);
+  if (dW) (void)hipFree(dW);
   return rc;
 }
 

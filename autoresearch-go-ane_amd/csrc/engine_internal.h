@@ -7,6 +7,7 @@
 
 #include "../../include/ane_hip.h"
 #include "gemm.h"
+#include "train_ops.h"
 
 struct LayerOff {
   int64_t wq = -1, wk = -1, wv = -1, wo = -1, w1 = -1, w2 = -1, w3 = -1, g_att = -1, g_ffn = -1, ve_embed = -1,
@@ -24,6 +25,12 @@ struct LayerShadow {
   ane::half_t* wo = nullptr;    // [D, D]
   ane::half_t* w13 = nullptr;   // llama2: [2H, D] W1/W3 interleaved by 32 rows; nanochat: W1 [H, D]
   ane::half_t* w2 = nullptr;    // [D, H]
+  // transposes for the backward's dX GEMMs (training only): B operands
+  // read K-major with K = the forward's output dimension
+  ane::half_t* wqkv_t = nullptr;  // [D, 3D]
+  ane::half_t* wo_t = nullptr;    // [D, D]
+  ane::half_t* w13_t = nullptr;   // [D, 2H] (columns in the interleaved W1|W3 order) or [D, H]
+  ane::half_t* w2_t = nullptr;    // [H, D]
 };
 
 // activations one layer keeps for its backward ([T, C] token-major)
@@ -64,6 +71,12 @@ struct TrainBufs {
   ane::half_t* att1 = nullptr;  // compat: scale-1 attention output
   float* lse1 = nullptr;
   ane::half_t* dl = nullptr;    // [V, T] dlogits
+  ane::half_t* dl_t = nullptr;  // [T, V] the same, token-major
+  // transposed GEMM operands of the weight gradients ([C, T], K = T)
+  ane::half_t* op_a = nullptr;  // [max(2H, 3D), T]
+  ane::half_t* op_b = nullptr;  // [max(H, D), T]
+  float* splitk_ws = nullptr;   // split-K partials of the backward GEMMs
+  size_t splitk_cap = 0;        // floats
   float* colscale = nullptr;
   float* gx0 = nullptr;
   float* ginj = nullptr;
@@ -105,6 +118,12 @@ struct ane_engine {
   std::vector<LayerShadow> ls;
   ane::half_t* embed_h = nullptr;  // [V, D]
   ane::half_t* smear_h = nullptr;  // [D, D]
+  ane::half_t* embed_t = nullptr;  // [D, V] (training)
+  ane::half_t* smear_t = nullptr;  // [D, D] (training)
+  // shadow refresh job table (device), rebuilt when the transposes appear
+  ane::ShadowJob* shadow_jobs = nullptr;
+  int n_shadow_jobs = 0, n_shadow_tiles = 0;
+  bool shadow_jobs_t = false;
   float* rope_cos = nullptr;
   float* rope_sin = nullptr;
 

@@ -44,6 +44,12 @@ struct GemmArgs {
   // group g starts at B + g * b_group_stride.  Tiles past grp[0] exit.
   const int* grp = nullptr;
   size_t b_group_stride = 0;
+  // Split-K (layout 0, epilogues STORE_F / STORE_H / STORE_W13): split s of
+  // `splits` reduces k in [s K/splits, (s+1) K/splits) into the fp32
+  // workspace ws[s][M][N]; a second kernel sums the splits in a fixed order
+  // and applies the epilogue, so results do not depend on block timing.
+  int splits = 1;
+  float* ws = nullptr;
 };
 
 struct EpiParams {
@@ -77,6 +83,12 @@ struct EpiParams {
 // tiles 256x128, 128x128, 64x128, 128x64, 64x64).
 hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t stream,
                     int bm = 0, int bn = 0, int nw = 0, int ns = 0);
+
+// Tile and split count for a K-major GEMM whose output is too small to
+// fill the chip with one block per tile (the backward's dW = dY^T X with
+// K = tokens, dX with K = 2048..32000); *splits = 1 when no split pays.
+// ws_cap = workspace floats available (splits * M * N must fit).
+void gemm_pick_split(int M, int N, int K, int epi, size_t ws_cap, int* bm, int* bn, int* splits);
 
 // Tile the heuristic picks; nonzero *bm / *bn on entry are kept as
 // constraints (set both to 0 for a free choice).  0 = no tile fits.

@@ -158,9 +158,8 @@ __device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rc
 // Block -> output tile: spread consecutive tiles of one XCD over a
 // contiguous range (hardware deals block i to XCD i % 8), then walk groups
 // of 8 M-tiles so neighbouring blocks share A rows and B columns in L2.
-__device__ __forceinline__ void block_tile(int nbm, int nbn, int& bm, int& bn) {
+__device__ __forceinline__ void block_tile(int nbm, int nbn, int bid, int& bm, int& bn) {
   const int nb = nbm * nbn;
-  int bid = blockIdx.x;
   if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
   constexpr int GROUP = 8;
   const int group_size = GROUP * nbn;
@@ -428,15 +427,19 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
       }
     }
   } else if constexpr (EPI == EPI_DLOGITS) {
-    // d = (softmax - onehot) * colscale[n], times (1 - tanh^2) under softcap
+    // d = (softmax - onehot) * colscale[n], times (1 - tanh^2) under softcap.
+    // C2 (optional): the same values transposed, [N, ldc2]; registers
+    // 4q .. 4q+3 hold 4 consecutive rows, stored as one 8-byte chunk.
     half_t* C = (half_t*)e.C;
+    half_t* C2 = (half_t*)e.C2;
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       const int n = COL(j);
       const int tg = e.targets[n];
       const float lse = e.lse[n], cs = e.colscale[n];
 #pragma unroll
-      for (int i = 0; i < TM; i++)
+      for (int i = 0; i < TM; i++) {
+        half_t hv[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int m = ROW(i, r);
@@ -448,8 +451,18 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
           }
           float d = __expf(v - lse) - (m == tg ? 1.f : 0.f);
           d = (m < e.vocab) ? d * cs * dsc : 0.f;
-          C[(size_t)m * e.ldc + n] = (half_t)d;
+          hv[r] = (half_t)d;
+          C[(size_t)m * e.ldc + n] = hv[r];
         }
+        if (C2) {
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            half4 w;
+            w[0] = hv[4 * q]; w[1] = hv[4 * q + 1]; w[2] = hv[4 * q + 2]; w[3] = hv[4 * q + 3];
+            *reinterpret_cast<half4*>(C2 + (size_t)n * e.ldc2 + ROW(i, 4 * q)) = w;
+          }
+        }
+      }
     }
   }
 #undef ROW
@@ -475,7 +488,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_kernel(GemmArgs g, EpiParams e) 
   const int wm = wave / WN, wn = wave % WN;
 
   int bm, bn;
-  block_tile(g.M / BM, g.N / BN, bm, bn);
+  block_tile(g.M / BM, g.N / BN, blockIdx.x, bm, bn);
   int m0 = bm * BM;
   const int n0 = bn * BN;
   const half_t* Bp = g.B;
@@ -635,8 +648,15 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
+  // split-K: blocks [s * tiles, (s+1) * tiles) reduce the s-th K range
+  const int ntiles = (g.M / BM) * (g.N / BN);
+  int bid = blockIdx.x, ks = 0;
+  if (g.splits > 1) {
+    ks = bid / ntiles;
+    bid -= ks * ntiles;
+  }
   int bm, bn;
-  block_tile(g.M / BM, g.N / BN, bm, bn);
+  block_tile(g.M / BM, g.N / BN, bid, bm, bn);
   int m0 = bm * BM;
   const int n0 = bn * BN;
   const half_t* Bp = g.B;
@@ -645,7 +665,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
     m0 = g.grp[1 + 2 * bm];
     Bp += (size_t)g.grp[2 + 2 * bm] * g.b_group_stride;
   }
-  const int nk = g.K / BK;
+  const int nk = g.K / BK / g.splits;
+  const size_t koff = (size_t)ks * nk * BK;
 
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const unsigned lds0 = (unsigned)(size_t)(lds_ptr_t)lds;
@@ -656,8 +677,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
     voa[v] = (unsigned)(((lane >> 3) * g.lda + lc * 8) * 2);
     vob[v] = (unsigned)(((lane >> 3) * g.ldb + lc * 8) * 2);
   }
-  const half_t* abase = g.A + (size_t)m0 * g.lda;
-  const half_t* bbase = Bp + (size_t)n0 * g.ldb;
+  const half_t* abase = g.A + (size_t)m0 * g.lda + koff;
+  const half_t* bbase = Bp + (size_t)n0 * g.ldb + koff;
   auto dma_a = [&](int q, int kt, int st) {
     const int gi = wave_s + NW * q;
     dma16_s(abase + (size_t)(gi * 8) * g.lda + kt * BK, voa[q % NV], lds0 + 2u * (unsigned)(st * STAGE + gi * 8 * BK));
@@ -753,7 +774,59 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
   }
   // the epilogue of the CE variant reuses LDS as scratch
   if constexpr (EPI == EPI_CE) __syncthreads();
+  if constexpr (EPI == EPI_STORE_F) {
+    if (g.splits > 1) {  // this split's slice of the workspace (C = ws, ldc = N)
+      EpiParams es = e;
+      es.C = (float*)e.C + (size_t)ks * g.M * g.N;
+      epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, es, m0, n0, bm, wm, wn, lane, lds);
+      return;
+    }
+  }
   epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, e, m0, n0, bm, wm, wn, lane, lds);
+}
+
+// Sum of the split-K workspace slices in split order, then the epilogue:
+// STORE_F (C = [C +] scale * sum), STORE_H, STORE_W13 (interleaved W1|W3
+// rows scattered to C / C3).  Four consecutive columns per thread.
+template <int EPI, bool VEC>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* ws, int splits, int M, int N, EpiParams e) {
+  const size_t MN = (size_t)M * N;
+  const size_t i4 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i4 >= MN) return;
+  const int m = (int)(i4 / N), n = (int)(i4 % N);
+  float4 v = *reinterpret_cast<const float4*>(ws + i4);
+  for (int s = 1; s < splits; s++) {
+    const float4 w = *reinterpret_cast<const float4*>(ws + (size_t)s * MN + i4);
+    v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+  }
+  float o[4] = {v.x * e.scale, v.y * e.scale, v.z * e.scale, v.w * e.scale};
+  if constexpr (EPI == EPI_STORE_H) {
+    half4 h;
+#pragma unroll
+    for (int u = 0; u < 4; u++) h[u] = (half_t)o[u];
+    *reinterpret_cast<half4*>((half_t*)e.C + (size_t)m * e.ldc + n) = h;
+    return;
+  } else {
+    float* dst = (float*)e.C;
+    int row = m;
+    if constexpr (EPI == EPI_STORE_W13) {
+      const int b = m >> 5;
+      dst = (b & 1) ? e.C3 : (float*)e.C;
+      row = (b >> 1) * 32 + (m & 31);
+    }
+    float* p = dst + (size_t)row * e.ldc + n;
+    if constexpr (VEC) {
+      float4 r = make_float4(o[0], o[1], o[2], o[3]);
+      if (e.accumulate) {
+        const float4 old = *reinterpret_cast<const float4*>(p);
+        r.x += old.x; r.y += old.y; r.z += old.z; r.w += old.w;
+      }
+      *reinterpret_cast<float4*>(p) = r;
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; u++) p[u] = e.accumulate ? p[u] + o[u] : o[u];
+    }
+  }
 }
 
 template <bool AT, bool BT, int EPI, int BM, int BN, int NW = 4, int NS = 2>
@@ -771,7 +844,7 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
   const int key = bm * 1000 + bn;
   if constexpr (!AT && !BT) {
     if (nw == 8 && ns == 2) {  // caller checked the tile
-      const dim3 grid((g.M / 256) * (g.N / 256));
+      const dim3 grid((g.M / 256) * (g.N / 256) * g.splits);
       LAUNCH_HO(256, 256, 8);
       return hipGetLastError();
     }
@@ -779,7 +852,7 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
   if (nw == 8) return launch_tile<AT, BT, EPI, 256, 256, 8>(g, e, s);  // caller checked the tile
   if constexpr (!AT && !BT) {
     if (ns == 2) {  // hand-ordered kernel for every K-major tile
-      const dim3 grid((g.M / bm) * (g.N / bn));
+      const dim3 grid((g.M / bm) * (g.N / bn) * g.splits);
       switch (key) {
         case 256256: LAUNCH_HO(256, 256, 4); break;
         case 256128: LAUNCH_HO(256, 128, 4); break;
@@ -880,9 +953,89 @@ void gemm_pick_tile(int M, int N, int K, int epi, int* pbm, int* pbn) {
   (void)K;
 }
 
+void gemm_pick_split(int M, int N, int K, int epi, size_t ws_cap, int* pbm, int* pbn, int* psplits) {
+  // Rules from a sweep of the training shapes on MI355X (B16 x 256, so
+  // K = tokens = 4096 for the weight gradients):
+  //  (a) very long K (dy = dlogits Embed, K = vocab): 256x256 tiles split
+  //      until >= 160 blocks (4 splits: 838 TFLOP/s vs 537 for 64x64);
+  //  (b) long K and room for >= 256 blocks of 256x256: one pass of the big
+  //      tile (classifier weight gradient: 953 vs 832 for 128x128);
+  //  (c) long K with fewer than 512 blocks of the default tile (dW of
+  //      Wq|Wk|Wv, Wo, W2): the largest tile and fewest splits reaching 384
+  //      blocks with >= 512 k per split (Wo: 18.5 us vs 32.3; W2 28.0 vs
+  //      34.6; QKV 29.3 vs 36.5).
+  // Otherwise the plain heuristic, one pass.
+  int bm = 0, bn = 0;
+  gemm_pick_tile(M, N, K, epi, &bm, &bn);
+  *pbm = bm;
+  *pbn = bn;
+  *psplits = 1;
+  if (bm == 0 || (epi != EPI_STORE_F && epi != EPI_STORE_H && epi != EPI_STORE_W13)) return;
+  auto fits = [&](int sp) { return K % (sp * BK) == 0 && (size_t)sp * M * N <= ws_cap; };
+  const bool big = M % 256 == 0 && N % 256 == 0;
+  const long t256 = big ? (long)(M / 256) * (N / 256) : 0;
+  if (big && K >= 16384) {
+    for (int sp : {1, 2, 3, 4, 5, 6, 8}) {
+      if (!fits(sp)) continue;
+      if (t256 * sp >= 160) {
+        *pbm = 256; *pbn = 256; *psplits = sp;
+        return;
+      }
+    }
+  }
+  if (big && K >= 2048 && t256 >= 256) {
+    *pbm = 256; *pbn = 256;
+    return;
+  }
+  if (K < 2048 || (long)(M / bm) * (N / bn) >= 512) return;
+  static const int cand[][2] = {{128, 128}, {64, 128}, {128, 64}, {64, 64}};
+  for (const auto& c : cand) {
+    if (M % c[0] || N % c[1]) continue;
+    const long t = (long)(M / c[0]) * (N / c[1]);
+    for (int sp = 2; sp <= 16; sp++) {
+      if (K / sp < 512) break;
+      if (!fits(sp)) continue;
+      if (t * sp >= 384) {
+        *pbm = c[0]; *pbn = c[1]; *psplits = sp;
+        return;
+      }
+    }
+  }
+}
+
+template <int EPI>
+static hipError_t splitk_reduce(const GemmArgs& g, const EpiParams& e, hipStream_t s) {
+  const size_t MN = (size_t)g.M * g.N;
+  const dim3 grid((unsigned)((MN / 4 + 255) / 256));
+  const bool vec = EPI != EPI_STORE_H && (e.ldc % 4) == 0 && ((uintptr_t)e.C % 16) == 0 &&
+                   (EPI != EPI_STORE_W13 || ((uintptr_t)e.C3 % 16) == 0);
+  if (vec)
+    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, true>), grid, dim3(256), 0, s, g.ws, g.splits, g.M, g.N, e);
+  else
+    hipLaunchKernelGGL((splitk_reduce_kernel<EPI, false>), grid, dim3(256), 0, s, g.ws, g.splits, g.M, g.N, e);
+  return hipGetLastError();
+}
+
 hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t s, int bm, int bn, int nw,
                     int ns) {
-  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0) return hipErrorInvalidValue;
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0 || g.splits < 1) return hipErrorInvalidValue;
+  if (g.splits > 1) {
+    if (g.a_t || g.b_t || g.grp || !g.ws || (g.K % (g.splits * BK)) != 0 || (ns != 0 && ns != 2) ||
+        (epi != EPI_STORE_F && epi != EPI_STORE_H && epi != EPI_STORE_W13) || (g.N % 4) != 0)
+      return hipErrorInvalidValue;
+    if (bm == 0 || bn == 0) gemm_pick_tile(g.M, g.N, g.K, epi, &bm, &bn);
+    if (bm == 0 || bn == 0 || (g.M % bm) || (g.N % bn)) return hipErrorInvalidValue;
+    if (nw == 0) nw = (bm == 256 && bn == 256) ? 8 : 4;
+    if (nw != 4 && !(nw == 8 && bm == 256 && bn == 256)) return hipErrorInvalidValue;
+    EpiParams pw;  // fp32 partials, ws[s][M][N]
+    pw.C = g.ws;
+    pw.ldc = g.N;
+    hipError_t r = launch<false, false, EPI_STORE_F>(g, pw, s, bm, bn, nw, 2);
+    if (r != hipSuccess) return r;
+    if (epi == EPI_STORE_F) return splitk_reduce<EPI_STORE_F>(g, e, s);
+    if (epi == EPI_STORE_H) return splitk_reduce<EPI_STORE_H>(g, e, s);
+    return splitk_reduce<EPI_STORE_W13>(g, e, s);
+  }
   if (bm == 0 || bn == 0) gemm_pick_tile(g.M, g.N, g.K, epi, &bm, &bn);
   if (bm == 0 || bn == 0 || (g.M % bm) || (g.N % bn)) return hipErrorInvalidValue;
   // 256x256 tiles run with 8 waves unless 4 are asked for (measured faster
@@ -910,6 +1063,10 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
   CASE(0, false, false, EPI_CE)
   CASE(0, false, false, EPI_DLOGITS)
   CASE(0, false, false, EPI_STORE_RS)
+  // backward with transposed weight shadows / operands (all K-major)
+  CASE(0, false, false, EPI_SWIGLU_BWD)
+  CASE(0, false, false, EPI_RELU2_BWD)
+  CASE(0, false, false, EPI_STORE_W13)
   // backward dX = dY * W  (B transposed)
   CASE(1, false, true, EPI_STORE_H)
   CASE(1, false, true, EPI_STORE_F)

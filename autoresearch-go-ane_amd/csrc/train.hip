@@ -93,13 +93,36 @@ int ensure_train(ane_engine* e, const char* op) {
   HIPCHK(op, dalloc(e, &tb.dqkv, T * 3 * D));
   HIPCHK(op, dalloc(e, &tb.delta, T * NH));
   HIPCHK(op, dalloc(e, &tb.dl, V * T));
+  HIPCHK(op, dalloc(e, &tb.dl_t, V * T));
+  {
+    const size_t ca = KH > 3 * D ? KH : 3 * D, cb = H > D ? H : D;
+    HIPCHK(op, dalloc(e, &tb.op_a, ca * T));
+    HIPCHK(op, dalloc(e, &tb.op_b, cb * T));
+    // split-K workspace: 8 slices of the largest backward output
+    size_t mx = T * D;
+    for (size_t v : {(size_t)D * H, (size_t)KH * D, (size_t)3 * D * D}) mx = v > mx ? v : mx;
+    tb.splitk_cap = 8 * mx;
+    HIPCHK(op, dalloc(e, &tb.splitk_ws, tb.splitk_cap));
+  }
+  // transposed weight shadows, filled by the refresh below
+  for (int l = 0; l < c.layers; l++) {
+    LayerShadow& s = e->ls[l];
+    HIPCHK(op, dalloc(e, &s.wqkv_t, 3 * D * D));
+    HIPCHK(op, dalloc(e, &s.wo_t, D * D));
+    HIPCHK(op, dalloc(e, &s.w13_t, KH * D));
+    HIPCHK(op, dalloc(e, &s.w2_t, H * D));
+  }
+  if (!llama) HIPCHK(op, dalloc(e, &e->smear_t, D * D));
+  HIPCHK(op, dalloc(e, &e->embed_t, V * D));
   HIPCHK(op, dalloc(e, &tb.colscale, T));
   const size_t nblk = (size_t)norm_bwd_blocks((int)T);
   HIPCHK(op, dalloc(e, &tb.dgain_part, nblk * D));
   HIPCHK(op, dalloc(e, &tb.dot_part, (nblk > 256 ? nblk : 256) * 2));
   HIPCHK(op, dalloc(e, &tb.sumsq, 1));
-  HIPCHK(op, dalloc(e, &tb.sumsq_part, 256));
+  HIPCHK(op, dalloc(e, &tb.sumsq_part, kSumsqBlocks));
   for (int i = 0; i < 4; i++) HIPCHK(op, hipEventCreate(&e->step_ev[i]));
+  int rc = refresh_shadows(e);
+  if (rc) return rc;
   e->train_ready = true;
   return ANE_OK;
 }
@@ -130,19 +153,20 @@ int backward_pass(ane_engine* e, int nseq) {
   if (rc) return rc;
   {
     EpiParams p;
-    p.C = tb.dl; p.ldc = T; p.targets = e->tgt; p.lse = e->lse; p.colscale = tb.colscale;
+    p.C = tb.dl; p.ldc = T; p.C2 = tb.dl_t; p.ldc2 = V; p.targets = e->tgt; p.lse = e->lse; p.colscale = tb.colscale;
     p.softcap = !llama; p.cap = 15.f; p.vocab = V;
     HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_DLOGITS, p));
   }
   {  // dy = Embed^T dlogits (MatMulEmbedTScale, ane/stories/cpu.go:333-360)
     EpiParams p;
     p.C = tb.dxn; p.ldc = D; p.scale = 1.f / kDlScale;
-    HIPCHK(op, eng_gemm(e, 7, tb.dl, T, true, e->embed_h, D, true, T, D, V, EPI_STORE_F, p));
+    HIPCHK(op, eng_gemm(e, 7, tb.dl_t, V, false, e->embed_t, V, false, T, D, V, EPI_STORE_F, p));
   }
   {  // classifier part of the embedding gradient (MatMulGradEmbedScale, ane/stories/cpu.go:366-385)
     EpiParams p;
     p.C = G + pm.embed; p.ldc = D; p.scale = 1.f / kDlScale; p.accumulate = 1;
-    HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, e->xh, D, true, V, D, T, EPI_STORE_F, p));
+    HIPCHK(op, transpose_h(tb.op_b, e->xh, T, D, D, T, st));
+    HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, tb.op_b, T, false, V, D, T, EPI_STORE_F, p));
   }
   {  // final RMSNorm backward (+ backout backward for nanochat)
     NormBwdArgs a;
@@ -174,27 +198,31 @@ int backward_pass(ane_engine* e, int nseq) {
     {
       EpiParams p;
       p.C = tb.dh13; p.ldc = KH; p.C2 = A.h13; p.ldc2 = KH;
-      HIPCHK(op, eng_gemm(e, 3, tb.dcur_h, D, false, s.w2, H, true, T, H, D, llama ? EPI_SWIGLU_BWD : EPI_RELU2_BWD,
-                          p));
+      HIPCHK(op, eng_gemm(e, 3, tb.dcur_h, D, false, s.w2_t, D, false, T, H, D,
+                          llama ? EPI_SWIGLU_BWD : EPI_RELU2_BWD, p));
     }
     {
       EpiParams p;
       p.C = tb.dxn; p.ldc = D;
-      HIPCHK(op, eng_gemm(e, 2, tb.dh13, KH, false, s.w13, D, true, T, D, KH, EPI_STORE_F, p));
+      HIPCHK(op, eng_gemm(e, 2, tb.dh13, KH, false, s.w13_t, KH, false, T, D, KH, EPI_STORE_F, p));
     }
     {  // dW2 += dOut gate^T
       EpiParams p;
       p.C = G + o.w2; p.ldc = H; p.accumulate = 1;
-      HIPCHK(op, eng_gemm(e, 3, tb.dcur_h, D, true, A.gate, H, true, D, H, T, EPI_STORE_F, p));
+      HIPCHK(op, transpose_h(tb.op_a, tb.dcur_h, T, D, D, T, st));
+      HIPCHK(op, transpose_h(tb.op_b, A.gate, T, H, H, T, st));
+      HIPCHK(op, eng_gemm(e, 3, tb.op_a, T, false, tb.op_b, T, false, D, H, T, EPI_STORE_F, p));
     }
     {  // dW1 (| dW3) += dh x2Norm^T
       EpiParams p;
       p.C = G + o.w1; p.ldc = D; p.accumulate = 1;
+      HIPCHK(op, transpose_h(tb.op_a, tb.dh13, T, KH, KH, T, st));
+      HIPCHK(op, transpose_h(tb.op_b, A.xn2, T, D, D, T, st));
       if (llama) {
         p.C3 = G + o.w3;
-        HIPCHK(op, eng_gemm(e, 2, tb.dh13, KH, true, A.xn2, D, true, KH, D, T, EPI_STORE_W13, p));
+        HIPCHK(op, eng_gemm(e, 2, tb.op_a, T, false, tb.op_b, T, false, KH, D, T, EPI_STORE_W13, p));
       } else {
-        HIPCHK(op, eng_gemm(e, 2, tb.dh13, KH, true, A.xn2, D, true, KH, D, T, EPI_STORE_F, p));
+        HIPCHK(op, eng_gemm(e, 2, tb.op_a, T, false, tb.op_b, T, false, KH, D, T, EPI_STORE_F, p));
       }
     }
     {  // dx2 = rl * dOut + RMSNorm-backward(dxn2; x2)
@@ -216,12 +244,14 @@ int backward_pass(ane_engine* e, int nseq) {
     {
       EpiParams p;
       p.C = tb.datt; p.ldc = D;
-      HIPCHK(op, eng_gemm(e, 1, tb.dx2_h, D, false, s.wo, D, true, T, D, D, EPI_STORE_H, p));
+      HIPCHK(op, eng_gemm(e, 1, tb.dx2_h, D, false, s.wo_t, D, false, T, D, D, EPI_STORE_H, p));
     }
     {
       EpiParams p;
       p.C = G + o.wo; p.ldc = D; p.accumulate = 1;
-      HIPCHK(op, eng_gemm(e, 1, tb.dx2_h, D, true, A.att, D, true, D, D, T, EPI_STORE_F, p));
+      HIPCHK(op, transpose_h(tb.op_a, tb.dx2_h, T, D, D, T, st));
+      HIPCHK(op, transpose_h(tb.op_b, A.att, T, D, D, T, st));
+      HIPCHK(op, eng_gemm(e, 1, tb.op_a, T, false, tb.op_b, T, false, D, D, T, EPI_STORE_F, p));
     }
     {
       AttnBwdArgs b;
@@ -260,12 +290,14 @@ int backward_pass(ane_engine* e, int nseq) {
     {
       EpiParams p;
       p.C = tb.dxn; p.ldc = D;
-      HIPCHK(op, eng_gemm(e, 0, tb.dqkv, 3 * D, false, s.wqkv, D, true, T, D, 3 * D, EPI_STORE_F, p));
+      HIPCHK(op, eng_gemm(e, 0, tb.dqkv, 3 * D, false, s.wqkv_t, 3 * D, false, T, D, 3 * D, EPI_STORE_F, p));
     }
     {  // dWq | dWk | dWv += dqkv xNorm^T
       EpiParams p;
       p.C = G + o.wq; p.ldc = D; p.accumulate = 1;
-      HIPCHK(op, eng_gemm(e, 0, tb.dqkv, 3 * D, true, A.xn, D, true, 3 * D, D, T, EPI_STORE_F, p));
+      HIPCHK(op, transpose_h(tb.op_a, tb.dqkv, T, 3 * D, 3 * D, T, st));
+      HIPCHK(op, transpose_h(tb.op_b, A.xn, T, D, D, T, st));
+      HIPCHK(op, eng_gemm(e, 0, tb.op_a, T, false, tb.op_b, T, false, 3 * D, D, T, EPI_STORE_F, p));
     }
     {  // dPrev = rl * dx2 + RMSNorm-backward(dxn; x) (+ VE gate grads, + backout injection)
       NormBwdArgs a;
@@ -297,12 +329,14 @@ int backward_pass(ane_engine* e, int nseq) {
     {
       EpiParams p;
       p.C = G + pm.smear_gate; p.ldc = D; p.accumulate = 1;
-      HIPCHK(op, eng_gemm(e, 7, tb.dgp, D, true, tb.x0h, D, true, D, D, T, EPI_STORE_F, p));
+      HIPCHK(op, transpose_h(tb.op_a, tb.dgp, T, D, D, T, st));
+      HIPCHK(op, transpose_h(tb.op_b, tb.x0h, T, D, D, T, st));
+      HIPCHK(op, eng_gemm(e, 7, tb.op_a, T, false, tb.op_b, T, false, D, D, T, EPI_STORE_F, p));
     }
     {
       EpiParams p;
       p.C = tb.dx2; p.ldc = D; p.accumulate = 1;
-      HIPCHK(op, eng_gemm(e, 7, tb.dgp, D, false, e->smear_h, D, true, T, D, D, EPI_STORE_F, p));
+      HIPCHK(op, eng_gemm(e, 7, tb.dgp, D, false, e->smear_t, D, false, T, D, D, EPI_STORE_F, p));
     }
     if (!compat) HIPCHK(op, axpy_inplace(tb.dx2, tb.gx0, nullptr, (size_t)T * D, st));
     NormBwdArgs a;  // embedding RMSNorm backward (ane/train_full.go:921-925)

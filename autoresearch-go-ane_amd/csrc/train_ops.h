@@ -67,7 +67,26 @@ hipError_t ve_bwd(float* gve_embed, float* gve_gate, float* ve_dx, const half_t*
 
 hipError_t fill_f32(float* p, size_t n, float v, hipStream_t s);
 
-// sum of squares of g[0, n) in double -> *out (two passes through part[256])
+// out[c * ldo + r] = in[r * ldi + c] for r < R, c < C (fp16); R and C
+// multiples of 64.  Turns a token-major [T, C] operand into the [C, T]
+// form the weight-gradient GEMMs read K-major (K = T).
+hipError_t transpose_h(half_t* out, const half_t* in, int R, int C, int ldi, int ldo, hipStream_t s);
+
+// fp16 weight shadows from the fp32 masters in one launch.  Job j converts
+// src [R, C] (row-major fp32) into dst row dr(r) = (r / 32) * blk_stride +
+// blk_off + r % 32 of a row-major [*, C] fp16 matrix and, when dst_t is set,
+// into column dr(r) of its transpose dst_t [C, ldt].  R and C are multiples
+// of 64; tile0 = the job's first 64x64 tile in the launch's tile numbering.
+struct ShadowJob {
+  const float* src;
+  half_t* dst;
+  half_t* dst_t;
+  int R, C, blk_stride, blk_off, ldt, tile0;
+};
+hipError_t shadow_refresh(const ShadowJob* jobs_dev, int njobs, int ntiles, hipStream_t s);
+
+// sum of squares of g[0, n) in double -> *out (two passes through part[kSumsqBlocks])
+constexpr int kSumsqBlocks = 1024;
 hipError_t sumsq(double* out, double* part, const float* g, size_t n, hipStream_t s);
 
 // AdamW over parameter segments (adamUpdateCFWithInv, ane/train_full.go:1113-1150):

@@ -117,12 +117,32 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(NormBwdArgs a) {
         lsh[0][threadIdx.x] + lsh[1][threadIdx.x] + lsh[2][threadIdx.x] + lsh[3][threadIdx.x];
 }
 
-__global__ void reduce_partials_kernel(float* dst, const float* part, int nblocks, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  float s = 0.f;
-  for (int b = 0; b < nblocks; b++) s += part[(size_t)b * n + i];
-  dst[i] += s;
+// One block per 64 columns: 16 waves each sum every 16th partial row of
+// the block's columns (independent loads, four in flight per lane), then
+// the 16 wave sums are added in a fixed order.
+__global__ __launch_bounds__(1024) void reduce_partials_kernel(float* dst, const float* part, int nblocks, int n) {
+  __shared__ float sh[16][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int i = blockIdx.x * 64 + lane;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (i < n) {
+    int b = wave;
+    for (; b + 48 < nblocks; b += 64) {
+      s0 += part[(size_t)b * n + i];
+      s1 += part[(size_t)(b + 16) * n + i];
+      s2 += part[(size_t)(b + 32) * n + i];
+      s3 += part[(size_t)(b + 48) * n + i];
+    }
+    for (; b < nblocks; b += 16) s0 += part[(size_t)b * n + i];
+  }
+  sh[wave][lane] = (s0 + s1) + (s2 + s3);
+  __syncthreads();
+  if (wave == 0 && i < n) {
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < 16; w++) s += sh[w][lane];
+    dst[i] += s;
+  }
 }
 
 __global__ __launch_bounds__(256) void reduce_dots_kernel(float* d0, float* d1, const double* part, int nblocks,
@@ -262,13 +282,27 @@ __global__ void fill_kernel(float* p, size_t n, float v) {
   for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
 }
 
+// float4 loads, two in flight per lane; the n % 4 tail is summed by block 0
 __global__ __launch_bounds__(256) void sumsq_kernel(double* part, const float* g, size_t n) {
   __shared__ double sh[256];
-  double acc = 0.0;
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-    const double f = g[i];
+  double acc = 0.0, acc2 = 0.0;
+  const size_t n4 = n / 4, stride = (size_t)gridDim.x * 256;
+  const float4* g4 = reinterpret_cast<const float4*>(g);
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  for (; i + stride < n4; i += 2 * stride) {
+    const float4 a = g4[i], b = g4[i + stride];
+    acc += (double)a.x * a.x + (double)a.y * a.y + (double)a.z * a.z + (double)a.w * a.w;
+    acc2 += (double)b.x * b.x + (double)b.y * b.y + (double)b.z * b.z + (double)b.w * b.w;
+  }
+  if (i < n4) {
+    const float4 a = g4[i];
+    acc += (double)a.x * a.x + (double)a.y * a.y + (double)a.z * a.z + (double)a.w * a.w;
+  }
+  if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+    const double f = g[4 * n4 + threadIdx.x];
     acc += f * f;
   }
+  acc += acc2;
   sh[threadIdx.x] = acc;
   __syncthreads();
   for (int o = 128; o > 0; o >>= 1) {
@@ -322,6 +356,68 @@ inline int flat_grid(size_t n, int cap = 4096) {
   return (int)(g > (size_t)cap ? cap : (g == 0 ? 1 : g));
 }
 
+// 64x64 tile through LDS: 16-byte loads along C, 16-byte stores along R
+// (each group of 8 lanes writes 128 contiguous bytes of one output row).
+// LDS rows are 72 halves (144 B, 16-byte aligned).
+constexpr int kTp = 72;
+__global__ __launch_bounds__(256) void transpose_h_kernel(half_t* out, const half_t* in, int C, int ldi, int ldo) {
+  __shared__ __attribute__((aligned(16))) half_t tile[64 * kTp];
+  const int tiles_c = C >> 6;
+  const int r0 = (blockIdx.x / tiles_c) * 64, c0 = (blockIdx.x % tiles_c) * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const int idx = tid + 256 * p, row = idx >> 3, ch = idx & 7;
+    st_h8(tile + row * kTp + ch * 8, ld_h8(in + (size_t)(r0 + row) * ldi + c0 + ch * 8));
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const int idx = tid + 256 * p, c = idx >> 3, rch = idx & 7;
+    half8 w;
+#pragma unroll
+    for (int j = 0; j < 8; j++) w[j] = tile[(rch * 8 + j) * kTp + c];
+    st_h8(out + (size_t)(c0 + c) * ldo + r0 + rch * 8, w);
+  }
+}
+
+__device__ __forceinline__ int shadow_row(const ShadowJob& jb, int r) {
+  return (r >> 5) * jb.blk_stride + jb.blk_off + (r & 31);
+}
+
+// One 64x64 tile of one job per block; jobs are sorted by tile0.
+__global__ __launch_bounds__(256) void shadow_kernel(const ShadowJob* jobs, int njobs) {
+  __shared__ __attribute__((aligned(16))) half_t tile[64 * kTp];
+  int j = 0;
+  for (int k = 1; k < njobs; k++)
+    if (jobs[k].tile0 <= (int)blockIdx.x) j = k;
+  const ShadowJob jb = jobs[j];
+  const int t = (int)blockIdx.x - jb.tile0;
+  const int tiles_c = jb.C >> 6;
+  const int r0 = (t / tiles_c) * 64, c0 = (t % tiles_c) * 64;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    const int idx = tid + 256 * p, row = idx >> 4, ch = idx & 15;
+    const float4 v = *reinterpret_cast<const float4*>(jb.src + (size_t)(r0 + row) * jb.C + c0 + ch * 4);
+    half4 h;
+    h[0] = (half_t)v.x; h[1] = (half_t)v.y; h[2] = (half_t)v.z; h[3] = (half_t)v.w;
+    *reinterpret_cast<half4*>(jb.dst + (size_t)shadow_row(jb, r0 + row) * jb.C + c0 + ch * 4) = h;
+    *reinterpret_cast<half4*>(tile + row * kTp + ch * 4) = h;
+  }
+  if (!jb.dst_t) return;  // block-uniform
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 2; p++) {
+    const int idx = tid + 256 * p, c = idx >> 3, rch = idx & 7;
+    half8 w;
+#pragma unroll
+    for (int q = 0; q < 8; q++) w[q] = tile[(rch * 8 + q) * kTp + c];
+    // 8 consecutive source rows never straddle a 32-row block
+    st_h8(jb.dst_t + (size_t)(c0 + c) * jb.ldt + shadow_row(jb, r0 + rch * 8), w);
+  }
+}
+
 }  // namespace
 
 hipError_t norm_bwd(const NormBwdArgs& a, hipStream_t s) {
@@ -331,7 +427,7 @@ hipError_t norm_bwd(const NormBwdArgs& a, hipStream_t s) {
 }
 
 hipError_t reduce_partials_add(float* dst, const float* part, int nblocks, int n, hipStream_t s) {
-  hipLaunchKernelGGL(reduce_partials_kernel, dim3((n + 255) / 256), dim3(256), 0, s, dst, part, nblocks, n);
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((n + 63) / 64), dim3(1024), 0, s, dst, part, nblocks, n);
   return hipGetLastError();
 }
 
@@ -375,14 +471,26 @@ hipError_t ve_bwd(float* gemb, float* ggate, float* ve_dx, const half_t* dv, int
   return hipGetLastError();
 }
 
+hipError_t transpose_h(half_t* out, const half_t* in, int R, int C, int ldi, int ldo, hipStream_t s) {
+  if (R <= 0 || C <= 0 || R % 64 || C % 64 || ldi < C || ldo < R || ldi % 8 || ldo % 8) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(transpose_h_kernel, dim3((R / 64) * (C / 64)), dim3(256), 0, s, out, in, C, ldi, ldo);
+  return hipGetLastError();
+}
+
+hipError_t shadow_refresh(const ShadowJob* jobs_dev, int njobs, int ntiles, hipStream_t s) {
+  if (njobs <= 0 || ntiles <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(shadow_kernel, dim3(ntiles), dim3(256), 0, s, jobs_dev, njobs);
+  return hipGetLastError();
+}
+
 hipError_t fill_f32(float* p, size_t n, float v, hipStream_t s) {
   hipLaunchKernelGGL(fill_kernel, dim3(flat_grid(n)), dim3(256), 0, s, p, n, v);
   return hipGetLastError();
 }
 
 hipError_t sumsq(double* out, double* part, const float* g, size_t n, hipStream_t s) {
-  hipLaunchKernelGGL(sumsq_kernel, dim3(256), dim3(256), 0, s, part, g, n);
-  hipLaunchKernelGGL(sumsq_final_kernel, dim3(1), dim3(256), 0, s, out, part, 256);
+  hipLaunchKernelGGL(sumsq_kernel, dim3(kSumsqBlocks), dim3(256), 0, s, part, g, n);
+  hipLaunchKernelGGL(sumsq_final_kernel, dim3(1), dim3(256), 0, s, out, part, kSumsqBlocks);
   return hipGetLastError();
 }
 

@@ -220,13 +220,14 @@ int ane_sync(ane_engine *e);
  * [M, K], B stored [K, N] when b_t else [N, K] (fp16 bit patterns); C is
  * [M, N] fp32 (epi 1) or fp16 (epi 0); bm/bn force a block tile (0 = auto);
  * nw: waves per block, 0 = default (4), 8 = two waves per SIMD (256x256);
- * ns: LDS pipeline stages, 0 = default (2), 3 (K-major operands only).
+ * ns: LDS pipeline stages, 0 = default (2), 3 (K-major operands only);
+ * splits: split-K factor (K-major operands, 2-stage pipeline; <= 1: none).
  * ane_debug_attention: causal attention over qkv [nseq*S, 3*64*NH] (fp16,
  * q|k|v per row, pre-RoPE) with score scale `scale` (hilo: split-operand
  * scores) -> out [nseq*S, 64*NH] fp16 and lse [nseq*S, NH].
  * Messages: ane_debug_last_error(). */
 int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_t *A, const uint16_t *B,
-                   void *C, int bm, int bn, int nw, int ns);
+                   void *C, int bm, int bn, int nw, int ns, int splits);
 /* One K-major GEMM (A [M, K], B [N, K]) with a fused forward epilogue on host
  * buffers (epi: 0 fp16 store, 1 fp32 store, 2 logits (softcap 15 when
  * seq < 0), 3 residual C = alpha R + acc + beta X0 (+ copy to C2), 4 SwiGLU
@@ -242,7 +243,7 @@ int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float
  * epi: 0 fp16 store, 1 fp32 store, 3 in-place residual add, 4 SwiGLU over
  * interleaved W1|W3 columns, 7 classifier cross-entropy partials. */
 int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw, int ns,
-                         int iters, const uint16_t *A, const uint16_t *B, float *avg_ms);
+                         int splits, int iters, const uint16_t *A, const uint16_t *B, float *avg_ms);
 const char *ane_debug_last_error(void);
 
 /* ---- greedy KV-cache decoder (grouped-query attention) --------------------

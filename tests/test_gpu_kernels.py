@@ -20,7 +20,7 @@ def _u16(a):
     return a.ctypes.data_as(C.POINTER(C.c_uint16))
 
 
-def run_gemm(A, B, a_t, b_t, bm=0, bn=0, out_f16=False, nw=0, ns=0):
+def run_gemm(A, B, a_t, b_t, bm=0, bn=0, out_f16=False, nw=0, ns=0, splits=1):
     """A: (M,K) logical, B: (N,K) logical, both float16 arrays."""
     lib = _lib.load()
     M, K = A.shape
@@ -29,7 +29,7 @@ def run_gemm(A, B, a_t, b_t, bm=0, bn=0, out_f16=False, nw=0, ns=0):
     Bs = np.ascontiguousarray(B.T if b_t else B).view(np.uint16)
     out = np.zeros((M, N), np.float16 if out_f16 else np.float32)
     rc = lib.ane_debug_gemm(int(a_t), int(b_t), 0 if out_f16 else 1, M, N, K, _u16(As), _u16(Bs),
-                            out.ctypes.data_as(C.c_void_p), bm, bn, nw, ns)
+                            out.ctypes.data_as(C.c_void_p), bm, bn, nw, ns, splits)
     assert rc == 0, lib.ane_debug_last_error()
     return out
 
@@ -86,7 +86,39 @@ def test_gemm_three_stage_rejects_unsupported():
     out = np.zeros((256, 256), np.float32)
     for (bm, bn, nw, at) in [(256, 256, 4, 0), (128, 128, 4, 1), (256, 256, 8, 0)]:
         rc = lib.ane_debug_gemm(at, 0, 1, 256, 256, 64, _u16(A.view(np.uint16)), _u16(B.view(np.uint16)),
-                                out.ctypes.data_as(C.c_void_p), bm, bn, nw, 3)
+                                out.ctypes.data_as(C.c_void_p), bm, bn, nw, 3, 1)
+        assert rc != 0
+
+
+@pytest.mark.parametrize("bm,bn,nw", [(256, 256, 8), (128, 128, 4), (128, 64, 4), (64, 128, 4), (64, 64, 4)])
+@pytest.mark.parametrize("splits", [2, 3, 4, 8])
+@pytest.mark.parametrize("out_f16", [False, True])
+def test_gemm_split_k(bm, bn, nw, splits, out_f16):
+    """Split-K: fp32 partials per K range, summed in split order, then the
+    epilogue; 1, 2 and 3 k-tiles per split."""
+    r = np.random.default_rng(bm + bn + splits + out_f16)
+    M, N = 512, 256
+    for kps in (1, 2, 3):
+        K = 64 * kps * splits
+        A = r.standard_normal((M, K)).astype(np.float16)
+        B = r.standard_normal((N, K)).astype(np.float16)
+        got = run_gemm(A, B, False, False, bm, bn, out_f16=out_f16, nw=nw, splits=splits)
+        ref = A.astype(np.float64) @ B.astype(np.float64).T
+        if out_f16:
+            np.testing.assert_allclose(got.astype(np.float64), ref, rtol=2e-3, atol=2e-2)
+        else:
+            np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-4)
+
+
+def test_gemm_split_k_rejects_unsupported():
+    lib = _lib.load()
+    A = np.zeros((256, 256), np.float16)
+    B = np.zeros((256, 256), np.float16)
+    out = np.zeros((256, 256), np.float32)
+    # transposed operand; K not divisible into 64-wide splits
+    for (at, K, sp) in [(1, 256, 2), (0, 192, 2), (0, 256, 8)]:
+        rc = lib.ane_debug_gemm(at, 0, 1, 256, 256, K, _u16(A.view(np.uint16)), _u16(B.view(np.uint16)),
+                                out.ctypes.data_as(C.c_void_p), 128, 128, 0, 0, sp)
         assert rc != 0
 
 
