@@ -15,6 +15,8 @@
 // The reference fills masked scores with -65504 and takes exp in float64,
 // which yields exactly 0 for every masked key; skipping masked keys is the
 // same function.
+#include <type_traits>
+
 #include "attention.h"
 
 namespace ane {
@@ -43,39 +45,59 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const half_t* base = a.qkv + tok0 * D3;
 
   // ---- stage K: RoPE (+ QK-norm), swizzled rows of 64 halves ----------------
-  for (int c = tid; c < S * 8; c += nthr) {
-    const int j = c >> 3, ch = c & 7;
-    half8 raw = ld_h8(base + (size_t)j * D3 + D + h * HD + ch * 8);
-    float f[8];
+  // Batches of KB chunks per thread: every global load of a batch (the K
+  // chunk and its cos / sin as float4) is issued before the first use, so
+  // the batch pays one memory latency instead of one per chunk.
+  constexpr int KB = 8;
+  for (int c0 = tid; c0 < S * 8; c0 += KB * nthr) {
+    half8 raw[KB];
+    float4 cs4[KB], sn4[KB];
 #pragma unroll
-    for (int p = 0; p < 4; p++) {
-      const int i = ch * 4 + p;
-      const float cs = a.rope_cos[j * 32 + i], sn = a.rope_sin[j * 32 + i];
-      const float e = (float)raw[2 * p], o = (float)raw[2 * p + 1];
-      f[2 * p] = e * cs - o * sn;
-      f[2 * p + 1] = o * cs + e * sn;
+    for (int u = 0; u < KB; u++) {
+      const int c = c0 + u * nthr;
+      if (c < S * 8) {
+        const int j = c >> 3, ch = c & 7;
+        raw[u] = ld_h8(base + (size_t)j * D3 + D + h * HD + ch * 8);
+        cs4[u] = *reinterpret_cast<const float4*>(a.rope_cos + j * 32 + ch * 4);
+        sn4[u] = *reinterpret_cast<const float4*>(a.rope_sin + j * 32 + ch * 4);
+      }
     }
-    if (a.qknorm) {
-      float ss = 0.f;
 #pragma unroll
-      for (int p = 0; p < 8; p++) ss += f[p] * f[p];
-      ss += __shfl_xor(ss, 1, 64);
-      ss += __shfl_xor(ss, 2, 64);
-      ss += __shfl_xor(ss, 4, 64);
-      const float sc = 1.2f / sqrtf(ss * (1.0f / HD) + 1e-5f);
+    for (int u = 0; u < KB; u++) {
+      const int c = c0 + u * nthr;
+      if (c >= S * 8) break;
+      const int j = c >> 3, ch = c & 7;
+      const float csv[4] = {cs4[u].x, cs4[u].y, cs4[u].z, cs4[u].w};
+      const float snv[4] = {sn4[u].x, sn4[u].y, sn4[u].z, sn4[u].w};
+      float f[8];
 #pragma unroll
-      for (int p = 0; p < 8; p++) f[p] *= sc;
+      for (int p = 0; p < 4; p++) {
+        const float e = (float)raw[u][2 * p], o = (float)raw[u][2 * p + 1];
+        f[2 * p] = e * csv[p] - o * snv[p];
+        f[2 * p + 1] = o * csv[p] + e * snv[p];
+      }
+      if (a.qknorm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int p = 0; p < 8; p++) ss += f[p] * f[p];
+        ss += __shfl_xor(ss, 1, 64);
+        ss += __shfl_xor(ss, 2, 64);
+        ss += __shfl_xor(ss, 4, 64);
+        const float sc = 1.2f / sqrtf(ss * (1.0f / HD) + 1e-5f);
+#pragma unroll
+        for (int p = 0; p < 8; p++) f[p] *= sc;
+      }
+      half8 w, wl;
+#pragma unroll
+      for (int p = 0; p < 8; p++) {
+        w[p] = (half_t)f[p];
+        wl[p] = (half_t)(f[p] - (float)w[p]);
+      }
+      st_h8(Ks + j * HD + swz(j, ch) * 8, w);
+      if constexpr (HILO) st_h8(Ks_lo + j * HD + swz(j, ch) * 8, wl);
+      if (a.qkvt && blockIdx.x == 0) st_h8(a.qkvt + (tok0 + j) * D3 + D + h * HD + ch * 8, w);
+      if (a.qkvt_lo && blockIdx.x == 0) st_h8(a.qkvt_lo + (tok0 + j) * 2 * D + D + h * HD + ch * 8, wl);
     }
-    half8 w, wl;
-#pragma unroll
-    for (int p = 0; p < 8; p++) {
-      w[p] = (half_t)f[p];
-      wl[p] = (half_t)(f[p] - (float)w[p]);
-    }
-    st_h8(Ks + j * HD + swz(j, ch) * 8, w);
-    if constexpr (HILO) st_h8(Ks_lo + j * HD + swz(j, ch) * 8, wl);
-    if (a.qkvt && blockIdx.x == 0) st_h8(a.qkvt + (tok0 + j) * D3 + D + h * HD + ch * 8, w);
-    if (a.qkvt_lo && blockIdx.x == 0) st_h8(a.qkvt_lo + (tok0 + j) * 2 * D + D + h * HD + ch * 8, wl);
   }
 
   // ---- stage V^T (8 keys x 8 dims per thread), value embeddings added --------
@@ -142,17 +164,24 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     // Q fragment (B operand of S^T = K Q^T): dims s*16 + 8g + [0..7]
     float qf[4][8];
     const half_t* qrow = base + (size_t)q * D3 + h * HD;
+    half8 qraw[4];
+    float4 qcs[4], qsn[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {  // all loads first
+      const int d0 = s * 16 + g * 8;
+      qraw[s] = ld_h8(qrow + d0);
+      qcs[s] = *reinterpret_cast<const float4*>(a.rope_cos + q * 32 + d0 / 2);
+      qsn[s] = *reinterpret_cast<const float4*>(a.rope_sin + q * 32 + d0 / 2);
+    }
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      const int d0 = s * 16 + g * 8;
-      half8 raw = ld_h8(qrow + d0);
+      const float csv[4] = {qcs[s].x, qcs[s].y, qcs[s].z, qcs[s].w};
+      const float snv[4] = {qsn[s].x, qsn[s].y, qsn[s].z, qsn[s].w};
 #pragma unroll
       for (int p = 0; p < 4; p++) {
-        const int i = d0 / 2 + p;
-        const float cs = a.rope_cos[q * 32 + i], sn = a.rope_sin[q * 32 + i];
-        const float e = (float)raw[2 * p], o = (float)raw[2 * p + 1];
-        qf[s][2 * p] = e * cs - o * sn;
-        qf[s][2 * p + 1] = o * cs + e * sn;
+        const float e = (float)qraw[s][2 * p], o = (float)qraw[s][2 * p + 1];
+        qf[s][2 * p] = e * csv[p] - o * snv[p];
+        qf[s][2 * p + 1] = o * csv[p] + e * snv[p];
       }
     }
     if (a.qknorm) {
@@ -188,69 +217,94 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     floatx16 o0, o1;
 #pragma unroll
     for (int r = 0; r < 16; r++) { o0[r] = 0.f; o1[r] = 0.f; }
+    // m: the reference maximum (scaled, log2 units) of the exponentials in
+    // lsum and o.  It is raised only when a block's maximum exceeds it by
+    // more than kRescale (or on the first block), so o is rescaled rarely;
+    // in between the exponentials stay below 2^kRescale.  Any m gives the
+    // same o / lsum; the final lse uses the m actually applied.
+    constexpr float kRescale = 8.f;
     float m = -INFINITY, lsum = 0.f;
 
-    for (int kb = 0; kb <= qb; kb++) {
+    // K fragments are read one key block ahead (issued before the softmax
+    // of the current block) and V fragments right after the score MFMAs, so
+    // the LDS latency hides behind the softmax instead of stalling the MFMAs.
+    half8 kf[4];
+    auto load_k = [&](int kb) {
+      const int krow = kb * 32 + ql;
+#pragma unroll
+      for (int s = 0; s < 4; s++) kf[s] = ld_h8(Ks + krow * HD + swz(krow, s * 2 + g) * 8);
+    };
+    auto block = [&](auto diag_c, int kb) {
+      constexpr bool DIAG = decltype(diag_c)::value;
       floatx16 sacc;
 #pragma unroll
       for (int r = 0; r < 16; r++) sacc[r] = 0.f;
       const int krow = kb * 32 + ql;
 #pragma unroll
       for (int s = 0; s < 4; s++) {
-        const int off = krow * HD + swz(krow, s * 2 + g) * 8;
-        half8 kf = ld_h8(Ks + off);
-        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qfrag[s], sacc, 0, 0, 0);
+        sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[s], qfrag[s], sacc, 0, 0, 0);
         if constexpr (HILO) {
+          const int off = krow * HD + swz(krow, s * 2 + g) * 8;
           sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ld_h8(Ks_lo + off), qfrag[s], sacc, 0, 0, 0);
-          sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qlo[s], sacc, 0, 0, 0);
+          sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[s], qlo[s], sacc, 0, 0, 0);
         }
       }
-      // sacc[r]: key kb*32 + 8*(r/4) + 4g + r%4, query q (scores * log2 e)
-      float mloc = -INFINITY;
+      half8 v0[2], v1[2];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        float sv = sacc[r] * sl2;
-        if (kb == qb && (8 * (r >> 2) + 4 * g + (r & 3)) > ql) sv = -INFINITY;
-        sacc[r] = sv;
-        mloc = fmaxf(mloc, sv);
+      for (int jh = 0; jh < 2; jh++) {
+        const int k0 = kb * 32 + 16 * jh + 4 * g;
+        const half_t* r0 = Vt + ql * VST + k0;
+        const half_t* r1 = Vt + (32 + ql) * VST + k0;
+        const half4 a0 = *reinterpret_cast<const half4*>(r0), a1 = *reinterpret_cast<const half4*>(r0 + 8);
+        const half4 b0 = *reinterpret_cast<const half4*>(r1), b1 = *reinterpret_cast<const half4*>(r1 + 8);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          v0[jh][u] = a0[u]; v0[jh][u + 4] = a1[u];
+          v1[jh][u] = b0[u]; v1[jh][u + 4] = b1[u];
+        }
       }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-      const float mnew = fmaxf(m, mloc);
-      const float alpha = exp2f(m - mnew);
+      if constexpr (!DIAG) load_k(kb + 1);  // kb < qb: the next block exists
+      // sacc[r]: raw score of key kb*32 + 8*(r/4) + 4g + r%4, query q; the
+      // diagonal block masks keys after q (their exponentials are exactly 0,
+      // as the reference's -65504 fill gives after its float64 exp)
+      if constexpr (DIAG) {
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          if ((8 * (r >> 2) + 4 * g + (r & 3)) > ql) sacc[r] = -INFINITY;
+      }
+      float mloc = sacc[0];
+#pragma unroll
+      for (int r = 1; r < 16; r++) mloc = fmaxf(mloc, sacc[r]);
+      mloc = fmaxf(mloc, xor32_f(mloc)) * sl2;  // scale > 0 keeps the order
+      if (__any(mloc > m + kRescale)) {
+        const float mnew = fmaxf(m, mloc);
+        const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+        lsum *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; r++) { o0[r] *= alpha; o1[r] *= alpha; }
+        m = mnew;
+      }
       float ps = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        float p = exp2f(sacc[r] - mnew);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], sl2, -m));
         sacc[r] = p;
         ps += p;
       }
-      lsum = lsum * alpha + ps;
-#pragma unroll
-      for (int r = 0; r < 16; r++) { o0[r] *= alpha; o1[r] *= alpha; }
-      m = mnew;
+      lsum += ps;
 #pragma unroll
       for (int jh = 0; jh < 2; jh++) {
         half8 pf;
 #pragma unroll
         for (int u = 0; u < 8; u++) pf[u] = (half_t)sacc[8 * jh + u];
-        const int k0 = kb * 32 + 16 * jh + 4 * g;
-        half8 v0, v1;
-        {
-          const half_t* r0 = Vt + ql * VST + k0;
-          const half_t* r1 = Vt + (32 + ql) * VST + k0;
-          half4 a0 = *reinterpret_cast<const half4*>(r0), a1 = *reinterpret_cast<const half4*>(r0 + 8);
-          half4 b0 = *reinterpret_cast<const half4*>(r1), b1 = *reinterpret_cast<const half4*>(r1 + 8);
-#pragma unroll
-          for (int u = 0; u < 4; u++) {
-            v0[u] = a0[u]; v0[u + 4] = a1[u];
-            v1[u] = b0[u]; v1[u + 4] = b1[u];
-          }
-        }
-        o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0, pf, o0, 0, 0, 0);
-        o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1, pf, o1, 0, 0, 0);
+        o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0[jh], pf, o0, 0, 0, 0);
+        o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1[jh], pf, o1, 0, 0, 0);
       }
-    }
-    lsum += __shfl_xor(lsum, 32, 64);
+    };
+    load_k(0);
+    for (int kb = 0; kb < qb; kb++) block(std::false_type{}, kb);
+    block(std::true_type{}, qb);
+    lsum += xor32_f(lsum);
     const float inv = 1.0f / lsum;
     half_t* orow = a.out + (tok0 + q) * D + h * HD;
 #pragma unroll

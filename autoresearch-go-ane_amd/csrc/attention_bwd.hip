@@ -32,11 +32,22 @@ namespace {
 constexpr int HD = 64;
 constexpr float kL2E = 1.4426950408889634f;
 
-// rows [0, S) of a [*, ld] fp16 matrix (64 columns at src) -> swizzled [S][64]
+// rows [0, S) of a [*, ld] fp16 matrix (64 columns at src) -> swizzled [S][64];
+// batches of 8 chunks per thread, all loads of a batch issued before its stores
 __device__ __forceinline__ void stage_rows(half_t* dst, const half_t* src, size_t ld, int S, int tid, int nthr) {
-  for (int c = tid; c < S * 8; c += nthr) {
-    const int j = c >> 3, ch = c & 7;
-    st_h8(dst + j * HD + swz(j, ch) * 8, ld_h8(src + (size_t)j * ld + ch * 8));
+  constexpr int KB = 8;
+  for (int c0 = tid; c0 < S * 8; c0 += KB * nthr) {
+    half8 v[KB];
+#pragma unroll
+    for (int u = 0; u < KB; u++) {
+      const int c = c0 + u * nthr;
+      if (c < S * 8) v[u] = ld_h8(src + (size_t)(c >> 3) * ld + (c & 7) * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < KB; u++) {
+      const int c = c0 + u * nthr;
+      if (c < S * 8) st_h8(dst + (c >> 3) * HD + swz(c >> 3, c & 7) * 8, v[u]);
+    }
   }
 }
 
@@ -217,7 +228,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const bool masked = kb == qb && (8 * (r >> 2) + 4 * g + (r & 3)) > ql;
-        const float p = masked ? 0.f : exp2f(sacc[r] * sp - lse2);
+        const float p = masked ? 0.f : __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], sp, -lse2));
         ds[r] = p * (dpacc[r] - dd) * a.scale_ds;
       }
 #pragma unroll
@@ -312,7 +323,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
         for (int u = 0; u < 4; u++) {
           const int r = 4 * rq + u;
           const bool masked = qb == kb && kl > (8 * rq + 4 * g + u);
-          const float p = masked ? 0.f : exp2f(sacc[r] * sp - lv[u]);
+          const float p = masked ? 0.f : __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], sp, -lv[u]));
           pr[r] = p;
           ds[r] = p * (dpacc[r] - dl[u]) * a.scale_ds;
         }

@@ -33,6 +33,15 @@ __device__ __forceinline__ float wave_max(float v) {
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
 }
+// The value lane l ^ 32 holds, by v_permlane32_swap (a VALU exchange of
+// the two 32-lane halves) instead of an LDS permute: with both operands x,
+// the swap leaves the upper half's values in element 1 for lanes 0..31 and
+// the lower half's in element 0 for lanes 32..63.
+__device__ __forceinline__ float xor32_f(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(__lane_id() < 32 ? r[1] : r[0]);
+}
+
 __device__ __forceinline__ double wave_sum_d(double v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
