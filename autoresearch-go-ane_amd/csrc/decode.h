@@ -62,6 +62,22 @@ struct SkinnyArgs {
 // K <= 2048 (1024 for SK_SWIGLU): one block holds the whole K range
 hipError_t skinny_gemm(const SkinnyArgs& a, int epi, hipStream_t s);
 
+// Split-K form of the decode-step GEMMs (Y = X[64, K] . W[N, K]^T, same
+// fragment-major operands): skinny_partials writes ks = skinny_splits(N, K)
+// fp32 partials part[ks][64][N] from (N/32) x ks one-wave blocks; a finish
+// kernel per token row sums them in split order and applies the epilogue:
+//   resid_norm: x[t] += Y[t]; xn[t] = fp16(rmsnorm(x[t]) * g)  (N = D <= 1024)
+//   qkv:        RoPE at ctr[0] on q, k; q -> q[t], k / v -> cache  (N = (NH + 2 NKV) * 64)
+//   swiglu:     gate[t][j] = silu(h1) * h3 over W1|W3 interleaved by 32 rows (fragment layout)
+int skinny_splits(int N, int K);
+hipError_t skinny_partials(const half_t* X, const half_t* W, float* part, size_t part_cap, int N, int K,
+                           hipStream_t s);
+hipError_t skinny_finish_resid_norm(const float* part, int N, int K, float* x, half_t* xn, const float* g, int nb,
+                                    hipStream_t s);
+hipError_t skinny_finish_qkv(const float* part, int K, const int* ctr, const float* rope_cos, const float* rope_sin,
+                             half_t* q, half_t* kc, half_t* vc, int NH, int NKV, int max_ctx, int nb, hipStream_t s);
+hipError_t skinny_finish_swiglu(const float* part, int N, int K, half_t* gate, int nb, hipStream_t s);
+
 // tok_out[b] = argmax over groups (first index on ties) for b < nb;
 // hist (optional) [..][nb]: row *step receives the same tokens.
 hipError_t argmax_reduce(uint16_t* tok_out, uint16_t* hist, const int* step, const float2* amax, int ngroups,

@@ -286,34 +286,175 @@ __global__ __launch_bounds__(256) void norm_kernel(const float* x, half_t* xn, c
   }
 }
 
+// ---- split-K skinny GEMM -------------------------------------------------------
+// One wave per block: column group cg (32 weight rows) x WPW consecutive
+// 64-wide k-windows.  Every operand load is issued before the first MFMA;
+// the 64 x 32 fp32 partial goes to part[kc][t][n].  The finish kernels
+// below sum the K splits of a row in split order (deterministic) and apply
+// the epilogue, so a decode-step GEMM spreads over hundreds of CUs instead
+// of one block per column group.
+template <int WPW>
+__global__ __launch_bounds__(64) void skinny_part_kernel(const half_t* X, const half_t* W, float* part, int N,
+                                                         int K) {
+  const int cg = blockIdx.x, kc = blockIdx.y, lane = threadIdx.x;
+  const int nwin = K / 64;
+  const half_t* wp = W + (size_t)cg * nwin * 2048 + lane * 8;
+  const half_t* xp = X + lane * 8;
+  const int f0 = kc * WPW * 4;
+  half8 w[4 * WPW], p[4 * WPW], q[4 * WPW];
+#pragma unroll
+  for (int s = 0; s < 4 * WPW; s++) {
+    w[s] = ld_h8(wp + (size_t)(f0 + s) * 512);
+    p[s] = ld_h8(xp + (size_t)(f0 + s) * 1024);
+    q[s] = ld_h8(xp + (size_t)(f0 + s) * 1024 + 512);
+  }
+  floatx16 c0, c1;
+#pragma unroll
+  for (int r = 0; r < 16; r++) { c0[r] = 0.f; c1[r] = 0.f; }
+#pragma unroll
+  for (int s = 0; s < 4 * WPW; s++) {
+    c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(p[s], w[s], c0, 0, 0, 0);
+    c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(q[s], w[s], c1, 0, 0, 0);
+  }
+  // c[r]: token 8*(r/4) + 4*h + r%4 (+32 for c1), column cg*32 + lane%32
+  float* dst = part + (size_t)kc * kDecRows * N + cg * 32 + (lane & 31);
+  const int h = lane >> 5;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int t = 8 * (r >> 2) + 4 * h + (r & 3);
+    dst[(size_t)t * N] = c0[r];
+    dst[(size_t)(t + 32) * N] = c1[r];
+  }
+}
+
+// sum over the ks <= kMaxSplits splits of part[.][t][c], in split order;
+// every load is issued before the first add (unconditional: the index is
+// clamped and the surplus values are dropped), so the row pays one memory
+// latency, not one per split
+constexpr int kMaxSplits = 16;
+__device__ __forceinline__ float split_sum(const float* part, int ks, int N, int t, int c) {
+  float v[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; s++) v[s] = part[((size_t)min(s, ks - 1) * kDecRows + t) * N + c];
+  float acc = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; s++) acc += s < ks ? v[s] : 0.f;
+  return acc;
+}
+
+// Wo / W2 finish: x[t] += sum of the splits (residual), then
+// xn[t] = fp16(rmsnorm(x[t]) * g) in the fragment layout (the next GEMM's
+// input: the FFN norm after Wo, the next layer's attention norm -- or the
+// final norm -- after W2).  One block of 256 per row, D <= 1024.
+__global__ __launch_bounds__(256) void finish_resid_norm_kernel(const float* part, int ks, float* x, half_t* xn,
+                                                                const float* g, int D) {
+  __shared__ float red[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  float v[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int c = tid + 256 * i;
+    v[i] = 0.f;
+    if (c < D) {
+      v[i] = x[(size_t)b * D + c] + split_sum(part, ks, D, b, c);
+      x[(size_t)b * D + c] = v[i];
+    }
+    ss += v[i] * v[i];
+  }
+  ss = block_sum_256(ss, red);
+  const float rr = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int c = tid + 256 * i;
+    if (c < D) xn[act_frag_off(b, c)] = (half_t)(v[i] * rr * g[c]);
+  }
+}
+
+// QKV finish: RoPE at position ctr[0] on q and k (interleaved pairs), q ->
+// q[t], k / v -> the layer's cache at that position.  One thread per
+// column pair.
+__global__ __launch_bounds__(256) void finish_qkv_kernel(const float* part, int ks, const int* ctr,
+                                                         const float* rope_cos, const float* rope_sin, half_t* q,
+                                                         half_t* kc, half_t* vc, int NH, int NKV, int max_ctx) {
+  const int t = blockIdx.x;
+  const int D = NH * 64, KVD = NKV * 64, N1 = D + 2 * KVD;
+  const int pos = ctr[0];
+  for (int c2 = threadIdx.x; c2 < N1 / 2; c2 += blockDim.x) {
+    const int col = 2 * c2;
+    float e = split_sum(part, ks, N1, t, col), o = split_sum(part, ks, N1, t, col + 1);
+    if (col < D + KVD) {
+      const int i = (col & 63) >> 1;
+      const float cs = rope_cos[pos * 32 + i], sn = rope_sin[pos * 32 + i];
+      const float e2 = e * cs - o * sn, o2 = o * cs + e * sn;
+      e = e2;
+      o = o2;
+    }
+    half2v w;
+    w[0] = (half_t)e;
+    w[1] = (half_t)o;
+    if (col < D) {
+      *reinterpret_cast<half2v*>(q + (size_t)t * D + col) = w;
+    } else {
+      const bool isk = col < D + KVD;
+      const int c = col - (isk ? D : D + KVD);
+      half_t* dst = (isk ? kc : vc) + (((size_t)t * NKV + (c >> 6)) * max_ctx + pos) * 64 + (c & 63);
+      *reinterpret_cast<half2v*>(dst) = w;
+    }
+  }
+}
+
+// W1|W3 finish: gate[t][j] = silu(h1) * h3 with W1 / W3 rows interleaved by
+// 32 (h1 at column (j/32)*64 + j%32, h3 at +32), fragment layout.
+__global__ __launch_bounds__(256) void finish_swiglu_kernel(const float* part, int ks, half_t* gate, int H) {
+  const int t = blockIdx.x;
+  for (int j = threadIdx.x; j < H; j += blockDim.x) {
+    const int c1 = (j >> 5) * 64 + (j & 31);
+    const float h1 = split_sum(part, ks, 2 * H, t, c1), h3 = split_sum(part, ks, 2 * H, t, c1 + 32);
+    gate[act_frag_off(t, j)] = (half_t)(h1 / (1.0f + __expf(-h1)) * h3);
+  }
+}
+
 // ---- decode attention ---------------------------------------------------------
-// Block (b, kv head, chunk): 8 lanes per key (16 B each), 32 keys per pass;
-// scores of the G query heads of the group in LDS; per-head max / sum by
-// one wave each; P.V with the same lane map, reduced over keys by shuffles
-// and across waves through LDS.
+// Block (b, kv head, chunk) for a group of G query heads: 8 lanes per key
+// (16 B each), 32 keys per pass, all K/V loads of the chunk in flight
+// before the first use.  q.k by v_dot2_f32_f16 summed over the key's 8
+// lanes with DPP row operations (no LDS traffic); scores of the G heads in
+// LDS; per-head max / sum by one wave each; P.V by v_dot2 over key pairs,
+// each thread's sums reduced across the 32 key lanes through LDS.
 constexpr int kGMax = 4;
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// sum over the aligned 8-lane group: quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror
+__device__ __forceinline__ float sum8_dpp(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  return v;
+}
+
+template <int G>
 __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
   const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int G = a.NH / a.NKV, D = a.NH * 64;
+  const int D = a.NH * 64;
   const int ctx = a.ctr[0] + 1;
   const int c0 = sp * kDecChunk;
   if (c0 >= ctx) return;  // uniform over the block, before any barrier
   const int n = min(kDecChunk, ctx - c0);
-  __shared__ float qs[kGMax][64];
-  __shared__ float sc[kGMax][kDecChunk];
-  __shared__ float red[4][kGMax][64];
-  __shared__ float stat[kGMax][2];
+  __shared__ half_t qs[G][64];
+  __shared__ float sc[G][kDecChunk];
+  __shared__ __attribute__((aligned(16))) float pv[G][32][64];
+  __shared__ float stat[G][2];
   const float sl2 = a.scale * kL2E;
-  if (tid < G * 64) qs[tid >> 6][tid & 63] = (float)a.q[(size_t)b * D + (kvh * G) * 64 + tid] * sl2;
-  __syncthreads();
   const size_t cache0 = ((size_t)b * a.NKV + kvh) * a.max_ctx;
   const half_t* Kb = a.kc + (cache0 + c0) * 64;
   const half_t* Vb = a.vc + (cache0 + c0) * 64;
   const int kl = tid >> 3, d8 = tid & 7;
   constexpr int NIT = kDecChunk / 32;
-  // all of this thread's key and value loads in flight before the first use;
-  // unconditional (rows clamped into the chunk), keys past n are never used
+  // unconditional loads (rows clamped into the chunk; keys past n unused)
   half8 kk[NIT], kv[NIT];
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
@@ -321,25 +462,32 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
     kk[it] = ld_h8(Kb + (size_t)j * 64 + d8 * 8);
     kv[it] = ld_h8(Vb + (size_t)j * 64 + d8 * 8);
   }
-  float qr[kGMax][8];  // this lane's 8 dims of each query head of the group
+  if (tid < G * 64) qs[tid >> 6][tid & 63] = a.q[(size_t)b * D + (kvh * G) * 64 + tid];
+  __syncthreads();
+  // this lane's 8 dims of each head as fp16 pairs (fp16 products exact in fp32)
+  half2v qr[G][4];
 #pragma unroll
-  for (int h = 0; h < kGMax; h++)
+  for (int h = 0; h < G; h++)
 #pragma unroll
-    for (int i = 0; i < 8; i++) qr[h][i] = h < G ? qs[h][d8 * 8 + i] : 0.f;
+    for (int i = 0; i < 4; i++) {
+      qr[h][i][0] = qs[h][d8 * 8 + 2 * i];
+      qr[h][i][1] = qs[h][d8 * 8 + 2 * i + 1];
+    }
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
     const int j = kl + 32 * it;
 #pragma unroll
-    for (int h = 0; h < kGMax; h++) {
-      if (h < G) {
-        float s = 0.f;
+    for (int h = 0; h < G; h++) {
+      float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 8; i++) s += qr[h][i] * (float)kk[it][i];
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        s += __shfl_xor(s, 4, 64);
-        if (j < n && d8 == 0) sc[h][j] = s;
+      for (int i = 0; i < 4; i++) {
+        half2v kp;
+        kp[0] = kk[it][2 * i];
+        kp[1] = kk[it][2 * i + 1];
+        s = __builtin_amdgcn_fdot2(qr[h][i], kp, s, false);
       }
+      s = sum8_dpp(s);
+      if (j < n && d8 == 0) sc[h][j] = s * sl2;
     }
   }
   __syncthreads();
@@ -349,7 +497,9 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
     m = wave_max(m);
     float l = 0.f;
     for (int j = lane; j < n; j += 64) {
-      const float p = exp2f(sc[wave][j] - m);
+      // probabilities rounded to fp16 (they feed fp16 dot products below);
+      // the normaliser sums the same rounded values
+      const float p = (float)(half_t)__builtin_amdgcn_exp2f(sc[wave][j] - m);
       sc[wave][j] = p;
       l += p;
     }
@@ -357,46 +507,44 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
     if (lane == 0) { stat[wave][0] = m; stat[wave][1] = l; }
   }
   __syncthreads();
-  float acc[kGMax][8];
+  // P.V over this thread's key pairs (it, it + 1): v_dot2 of (p_it, p_it+1)
+  // with (v_it[i], v_it+1[i]); keys past n have p = 0
+  float acc[G][8];
 #pragma unroll
-  for (int h = 0; h < kGMax; h++)
+  for (int h = 0; h < G; h++)
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
 #pragma unroll
-  for (int it = 0; it < NIT; it++) {
-    const int j = kl + 32 * it;
-    if (j < n) {
-#pragma unroll
-      for (int h = 0; h < kGMax; h++) {
-        if (h < G) {
-          const float p = sc[h][j];
-#pragma unroll
-          for (int i = 0; i < 8; i++) acc[h][i] += p * (float)kv[it][i];
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int h = 0; h < kGMax; h++)
+  for (int it = 0; it < NIT; it += 2) {
+    const int j0 = kl + 32 * it, j1 = j0 + 32;
+    half2v vp[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      float v = acc[h][i];
-      v += __shfl_xor(v, 8, 64);
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      acc[h][i] = v;
+      vp[i][0] = kv[it][i];
+      vp[i][1] = kv[it + 1][i];
     }
-  if (lane < 8) {
 #pragma unroll
-    for (int h = 0; h < kGMax; h++)
-      if (h < G)
+    for (int h = 0; h < G; h++) {
+      half2v pp;
+      pp[0] = (half_t)(j0 < n ? sc[h][j0] : 0.f);
+      pp[1] = (half_t)(j1 < n ? sc[h][j1] : 0.f);
 #pragma unroll
-        for (int i = 0; i < 8; i++) red[wave][h][lane * 8 + i] = acc[h][i];
+      for (int i = 0; i < 8; i++) acc[h][i] = __builtin_amdgcn_fdot2(pp, vp[i], acc[h][i], false);
+    }
+  }
+  // sums over the 32 key lanes kl, through LDS
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    float4* dst = reinterpret_cast<float4*>(&pv[h][kl][d8 * 8]);
+    dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+    dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
   }
   __syncthreads();
   if (tid < G * 64) {
     const int h = tid >> 6, d = tid & 63;
-    const float o = red[0][h][d] + red[1][h][d] + red[2][h][d] + red[3][h][d];
+    float o = 0.f;
+#pragma unroll
+    for (int k = 0; k < 32; k++) o += pv[h][k][d];
     float* out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nsplit + sp) * 66;
     out[d] = o;
     if (d == 0) { out[64] = stat[h][0]; out[65] = stat[h][1]; }
@@ -651,6 +799,53 @@ hipError_t skinny_gemm(const SkinnyArgs& a, int epi, hipStream_t s) {
   }
 }
 
+int skinny_splits(int N, int K) {
+  const int nwin = K / 64, ng = N / 32;
+  for (int wpw : {4, 2, 1})
+    if (nwin % wpw == 0 && nwin / wpw <= kMaxSplits && (long)ng * (nwin / wpw) >= 256) return nwin / wpw;
+  for (int wpw : {1, 2, 4})  // fewest windows per wave within kMaxSplits splits
+    if (nwin % wpw == 0 && nwin / wpw <= kMaxSplits) return nwin / wpw;
+  return -1;  // skinny_partials refuses
+}
+
+hipError_t skinny_partials(const half_t* X, const half_t* W, float* part, size_t part_cap, int N, int K,
+                           hipStream_t s) {
+  if (N <= 0 || N % 32 || K <= 0 || K % 64) return hipErrorInvalidValue;
+  const int ks = skinny_splits(N, K);
+  if (ks <= 0 || (size_t)ks * kDecRows * N > part_cap) return hipErrorInvalidValue;
+  const int wpw = (K / 64) / ks;
+  const dim3 grid(N / 32, ks);
+  switch (wpw) {
+    case 1: hipLaunchKernelGGL((skinny_part_kernel<1>), grid, dim3(64), 0, s, X, W, part, N, K); break;
+    case 2: hipLaunchKernelGGL((skinny_part_kernel<2>), grid, dim3(64), 0, s, X, W, part, N, K); break;
+    case 4: hipLaunchKernelGGL((skinny_part_kernel<4>), grid, dim3(64), 0, s, X, W, part, N, K); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t skinny_finish_resid_norm(const float* part, int N, int K, float* x, half_t* xn, const float* g, int nb,
+                                    hipStream_t s) {
+  if (N > 1024 || nb < 1 || nb > kDecRows) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(finish_resid_norm_kernel, dim3(nb), dim3(256), 0, s, part, skinny_splits(N, K), x, xn, g, N);
+  return hipGetLastError();
+}
+
+hipError_t skinny_finish_qkv(const float* part, int K, const int* ctr, const float* rope_cos, const float* rope_sin,
+                             half_t* q, half_t* kc, half_t* vc, int NH, int NKV, int max_ctx, int nb, hipStream_t s) {
+  if (nb < 1 || nb > kDecRows) return hipErrorInvalidValue;
+  const int N1 = (NH + 2 * NKV) * 64;
+  hipLaunchKernelGGL(finish_qkv_kernel, dim3(nb), dim3(256), 0, s, part, skinny_splits(N1, K), ctr, rope_cos,
+                     rope_sin, q, kc, vc, NH, NKV, max_ctx);
+  return hipGetLastError();
+}
+
+hipError_t skinny_finish_swiglu(const float* part, int N, int K, half_t* gate, int nb, hipStream_t s) {
+  if (N % 64 || nb < 1 || nb > kDecRows) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(finish_swiglu_kernel, dim3(nb), dim3(256), 0, s, part, skinny_splits(N, K), gate, N / 2);
+  return hipGetLastError();
+}
+
 hipError_t argmax_reduce(uint16_t* tok_out, uint16_t* hist, const int* step, const float2* amax, int ngroups,
                          int nb, hipStream_t s) {
   hipLaunchKernelGGL(argmax_kernel, dim3(nb), dim3(256), 0, s, tok_out, hist, step, amax, ngroups, nb);
@@ -683,7 +878,13 @@ hipError_t dec_norm(const float* x, half_t* xn, const float* g, int nb, int D, h
 hipError_t dec_attention(const DecAttnArgs& a, hipStream_t s) {
   const int G = a.NH / a.NKV;
   if (a.NH % a.NKV || G > kGMax) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(dec_attn_kernel, dim3(a.nb, a.NKV, a.nsplit), dim3(256), 0, s, a);
+  const dim3 grid(a.nb, a.NKV, a.nsplit);
+  switch (G) {
+    case 1: hipLaunchKernelGGL(dec_attn_kernel<1>, grid, dim3(256), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(dec_attn_kernel<2>, grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(dec_attn_kernel<3>, grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(dec_attn_kernel<4>, grid, dim3(256), 0, s, a); break;
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(dec_combine_kernel, dim3(a.nb, a.NH), dim3(64), 0, s, a);

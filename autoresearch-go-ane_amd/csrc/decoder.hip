@@ -20,6 +20,7 @@
 
 #include <cmath>
 #include <string>
+#include <algorithm>
 #include <vector>
 
 #include "../../include/ane_hip.h"
@@ -80,6 +81,8 @@ struct ane_decoder {
   float* x = nullptr;
   half_t *xn = nullptr, *q = nullptr, *att = nullptr, *gate = nullptr;
   float* apart = nullptr;
+  float* kpart = nullptr;  // split-K partials of the decode-step GEMMs
+  size_t kpart_cap = 0;
   int nsplit = 0;
   float2* amax = nullptr;
   float* logits_d = nullptr;
@@ -214,6 +217,17 @@ int open_impl(ane_decoder* d) {
   DCHK(op, dalloc(d, &d->gate, (size_t)R * H));
   d->nsplit = (C + kDecChunk - 1) / kDecChunk;
   DCHK(op, dalloc(d, &d->apart, (size_t)B * d->NH * d->nsplit * 66));
+  {
+    const int NK[4][2] = {{N1, D}, {D, D}, {2 * H, D}, {D, H}};  // QKV, Wo, W1|W3, W2
+    size_t cap = 0;
+    for (const auto& nk : NK) {
+      const int ks = skinny_splits(nk[0], nk[1]);
+      if (ks <= 0) return dfail(d, ANE_ERR_ARG, "storiesane decode open: K=%d too long for the split-K GEMMs", nk[1]);
+      cap = std::max(cap, (size_t)ks * kDecRows * nk[0]);
+    }
+    d->kpart_cap = cap;
+    DCHK(op, dalloc(d, &d->kpart, cap));
+  }
   DCHK(op, dalloc(d, &d->amax, (size_t)(V / 32) * R));
   DCHK(op, dalloc(d, &d->logits_d, (size_t)R * V));
   DCHK(op, dalloc(d, &d->tok_d, (size_t)R));
@@ -255,27 +269,22 @@ int enqueue_step(ane_decoder* d, float* logits, uint16_t* hist) {
     const DecLayerOff& o = d->off[l];
     half_t* kcl = d->kc + (size_t)l * d->B * d->NKV * d->C * 64;
     half_t* vcl = d->vc + (size_t)l * d->B * d->NKV * d->C * 64;
-    SkinnyArgs s;
-    memset(&s, 0, sizeof s);
-    s.nb = nb;
-    s.X = d->xn; s.W = d->fwqkv + (size_t)l * N1 * D; s.N = N1; s.K = D;
-    s.ctr = d->ctr_d; s.rope_cos = d->rope_cos; s.rope_sin = d->rope_sin; s.q = d->q; s.kc = kcl; s.vc = vcl;
-    s.NH = d->NH; s.NKV = d->NKV; s.max_ctx = d->C;
-    DCHK(op, skinny_gemm(s, SK_QKV, st));
+    // each GEMM: split-K partials from (N/32) x ks one-wave blocks, then a
+    // per-row finish that sums the splits and applies the epilogue
+    DCHK(op, skinny_partials(d->xn, d->fwqkv + (size_t)l * N1 * D, d->kpart, d->kpart_cap, N1, D, st));
+    DCHK(op, skinny_finish_qkv(d->kpart, D, d->ctr_d, d->rope_cos, d->rope_sin, d->q, kcl, vcl, d->NH, d->NKV, d->C,
+                               nb, st));
     DecAttnArgs aa;
     aa.q = d->q; aa.kc = kcl; aa.vc = vcl; aa.ctr = d->ctr_d; aa.part = d->apart; aa.att = d->att; aa.nb = nb;
     aa.NH = d->NH; aa.NKV = d->NKV; aa.max_ctx = d->C; aa.nsplit = d->nsplit; aa.scale = 0.125f;
     DCHK(op, dec_attention(aa, st));
-    s.X = d->att; s.W = d->fwo + (size_t)l * D * D; s.N = D; s.K = D; s.x = d->x;
-    DCHK(op, skinny_gemm(s, SK_RESID, st));
-    DCHK(op, dec_norm(d->x, d->xn, d->P + o.g_ffn, nb, D, st));
-    s.X = d->xn; s.W = d->fw13 + (size_t)l * 2 * H * D; s.N = 2 * H; s.K = D;
-    s.gate = d->gate;
-    DCHK(op, skinny_gemm(s, SK_SWIGLU, st));
-    s.X = d->gate; s.W = d->fw2 + (size_t)l * D * H; s.N = D; s.K = H;
-    DCHK(op, skinny_gemm(s, SK_RESID, st));
+    DCHK(op, skinny_partials(d->att, d->fwo + (size_t)l * D * D, d->kpart, d->kpart_cap, D, D, st));
+    DCHK(op, skinny_finish_resid_norm(d->kpart, D, D, d->x, d->xn, d->P + o.g_ffn, nb, st));
+    DCHK(op, skinny_partials(d->xn, d->fw13 + (size_t)l * 2 * H * D, d->kpart, d->kpart_cap, 2 * H, D, st));
+    DCHK(op, skinny_finish_swiglu(d->kpart, 2 * H, D, d->gate, nb, st));
+    DCHK(op, skinny_partials(d->gate, d->fw2 + (size_t)l * D * H, d->kpart, d->kpart_cap, D, H, st));
     const float* gnext = l + 1 < d->L ? d->P + d->off[l + 1].g_att : d->P + d->off_gfinal;
-    DCHK(op, dec_norm(d->x, d->xn, gnext, nb, D, st));
+    DCHK(op, skinny_finish_resid_norm(d->kpart, D, H, d->x, d->xn, gnext, nb, st));
   }
   SkinnyArgs s;
   memset(&s, 0, sizeof s);

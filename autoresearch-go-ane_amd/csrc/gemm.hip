@@ -865,6 +865,22 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
               case 128064: LAUNCH_HO(128, 64, 4); break;
               case 256064: LAUNCH_HO(256, 64, 4); break;
               case 64064: LAUNCH_HO(64, 64, 4); break;
+              // 192-wide tiles (three 32-column MFMA tiles per wave): N = 768
+              // and 2304 split into whole waves of blocks
+              case 128192:
+                if constexpr (EPI == EPI_STORE_H || EPI == EPI_STORE_F || EPI == EPI_RESID) {
+                  LAUNCH_HO(128, 192, 4);
+                  break;
+                } else {
+                  return hipErrorInvalidValue;
+                }
+              case 256192:
+                if constexpr (EPI == EPI_STORE_H || EPI == EPI_STORE_F || EPI == EPI_RESID) {
+                  LAUNCH_HO(256, 192, 4);
+                  break;
+                } else {
+                  return hipErrorInvalidValue;
+                }
               default: return hipErrorInvalidValue;
             }
           } else {
@@ -925,6 +941,16 @@ void gemm_pick_tile(int M, int N, int K, int epi, int* pbm, int* pbn) {
                                 {256, 128, 600},  {128, 256, 600},  {256, 64, 600}, {64, 64, 0}};
   constexpr int NCAND = 8;
   const int want_bm = *pbm, want_bn = *pbn;
+  // Widths that are a multiple of 192 but not of 256 (the fused Wq|Wk|Wv
+  // output, 2304): 128x192 blocks split N into whole waves; measured
+  // 33.6 us vs 38.5 for 128x128 at M = 8192, 19.9 vs 21.3 for 128x64 at 4096
+  if ((epi == EPI_STORE_H || epi == EPI_STORE_F || epi == EPI_RESID) && N % 192 == 0 && N % 256 != 0 &&
+      M % 128 == 0 && (long)(M / 128) * (N / 192) >= 384 && (!want_bm || want_bm == 128) &&
+      (!want_bn || want_bn == 192)) {
+    *pbm = 128;
+    *pbn = 192;
+    return;
+  }
   int fbm = 0, fbn = 0;
   for (int c = 0; c < NCAND; c++) {
     const int bm = cand[c][0], bn = cand[c][1];

@@ -34,7 +34,9 @@ def _vp(a):
 def run(epi, A, B, C_out, C2=None, X0=None, R=None, alpha=1.0, beta=0.0, seq=0, tile=(0, 0, 0)):
     lib = _lib.load()
     bm, bn, nw = tile
-    rc = lib.ane_debug_gemm_epi(epi, M, N, K, _u16(A.view(np.uint16)), _u16(B.view(np.uint16)), _vp(C_out), _vp(C2),
+    m, k = A.shape
+    n = B.shape[0]
+    rc = lib.ane_debug_gemm_epi(epi, m, n, k, _u16(A.view(np.uint16)), _u16(B.view(np.uint16)), _vp(C_out), _vp(C2),
                                 _fp(X0), _fp(R), alpha, beta, seq, bm, bn, nw)
     assert rc == 0, lib.ane_debug_last_error()
 
@@ -119,3 +121,25 @@ def test_smear(tile):
     prev[::seq] = 0.0
     close32(gate, g)
     close32(out, X0.astype(np.float64) + 0.3 * g * prev)
+
+
+@pytest.mark.parametrize("tile", [(128, 192, 4), (256, 192, 4)])
+def test_192_wide_tiles(tile):
+    """The 192-wide tiles (three 32-column MFMA tiles per wave) with the
+    epilogues they serve: fp16 / fp32 store (QKV) and the residual add."""
+    r = np.random.default_rng(7)
+    m, n, k = 512, 384, 320
+    A = (r.standard_normal((m, k)) * 0.5).astype(np.float16)
+    B = (r.standard_normal((n, k)) * 0.5).astype(np.float16)
+    acc = A.astype(np.float64) @ B.astype(np.float64).T
+    h = np.zeros((m, n), np.float16)
+    run(EPI_STORE_H, A, B, h, tile=tile)
+    close16(h, acc)
+    f = np.zeros((m, n), np.float32)
+    run(EPI_STORE_F, A, B, f, tile=tile)
+    close32(f, acc)
+    R = r.standard_normal((m, n)).astype(np.float32)
+    X0 = r.standard_normal((m, n)).astype(np.float32)
+    out = np.zeros((m, n), np.float32)
+    run(EPI_RESID, A, B, out, X0=X0, R=R, alpha=0.75, beta=-0.5, tile=tile)
+    close32(out, 0.75 * R.astype(np.float64) + acc - 0.5 * X0.astype(np.float64))
