@@ -34,33 +34,19 @@ __device__ __host__ __forceinline__ size_t act_frag_off(int t, int k) {
 // row-major fp16 W [N][K] -> fragment-major (N % 32 == 0, K % 64 == 0)
 hipError_t weight_to_frag(half_t* dst, const half_t* src, int N, int K, hipStream_t s);
 
-// Y = X[64, K] . W[N, K]^T for the rows t < nb, K split over the waves of
-// one block and added in a fixed order (deterministic), epilogue fused:
-enum SkinnyEpi {
-  SK_RESID = 0,   // x[t][n] += Y                        (Wo, W2: residual add)
-  SK_QKV = 1,     // q|k|v rows: RoPE at ctr[0] on q and k; q -> q[t], k, v -> cache
-  SK_SWIGLU = 2,  // W1|W3 interleaved by 32 rows: gate[t][j] = silu(h1) * h3 (fragment layout, K = N/2)
-  SK_ARGMAX = 3,  // per 32-column group: (max, first index) over n < nvalid -> amax[N/32][64]
-};
+// Classifier of the decode rows: Y = X[64, K] . W[N, K]^T (fragment-major
+// operands), K split over the waves of one block per 32 vocabulary rows
+// and added in a fixed order; epilogue: per 32-column group (max, first
+// index) over n < nvalid -> amax[N/32][64], optionally logits [64][N] fp32.
 struct SkinnyArgs {
   const half_t* X;  // [64, K] activation fragments (act_frag_off)
   const half_t* W;  // [N, K] weight fragments (weight_to_frag)
-  int N, K, nb;     // N % 32 == 0 (64 for SK_SWIGLU), K % 64 == 0, 1 <= nb <= 64
-  float* x;         // SK_RESID: [64][N] fp32
-  const int* ctr;   // SK_QKV: ctr[0] = position
-  const float* rope_cos;
-  const float* rope_sin;
-  half_t* q;        // SK_QKV: [64][NH*64]
-  half_t* kc;       // SK_QKV: layer cache base [Bcap][NKV][max_ctx][64]
-  half_t* vc;
-  int NH, NKV, max_ctx;
-  half_t* gate;     // SK_SWIGLU: [64][N/2]
-  float2* amax;     // SK_ARGMAX
-  float* logits;    // SK_ARGMAX, optional [64][N] fp32
+  int N, K, nb;     // N % 32 == 0, K % 64 == 0 (K <= 2048), 1 <= nb <= 64
+  float2* amax;
+  float* logits;
   int nvalid;
 };
-// K <= 2048 (1024 for SK_SWIGLU): one block holds the whole K range
-hipError_t skinny_gemm(const SkinnyArgs& a, int epi, hipStream_t s);
+hipError_t classifier_argmax(const SkinnyArgs& a, hipStream_t s);
 
 // Split-K form of the decode-step GEMMs (Y = X[64, K] . W[N, K]^T, same
 // fragment-major operands): skinny_partials writes ks = skinny_splits(N, K)

@@ -14,23 +14,21 @@ namespace {
 
 constexpr float kL2E = 1.4426950408889634f;
 
-// ---- skinny GEMM ------------------------------------------------------------
-// Block = NCG column groups of 32 weight rows x NWK waves splitting K, each
-// wave holding at most two 64-wide k-windows, all loaded in one batch (a
-// decode-step GEMM is bound by dependent memory round trips, not by bytes).
+// ---- classifier GEMM with the argmax epilogue ---------------------------------
+// Block = one column group of 32 vocabulary rows x NWK waves splitting K,
+// each wave holding at most two 64-wide k-windows, all loaded in one batch.
 // MFMA 32x32x16 with rows = tokens (two tiles: tokens 0-31, 32-63) and
 // columns = weight rows; both operands are stored fragment-major
 // (decode.h), so each operand load is one contiguous 1 KB per wave.  The K
 // partial sums meet in LDS and are added in wave order (deterministic);
-// wave 0 of each column group runs the fused epilogue, whose operands
-// (residual rows, RoPE factors) are fetched up front.
-template <int EPI, int NWK, int NCG>
-__global__ __launch_bounds__(64 * NWK * NCG) void skinny_kernel(SkinnyArgs a) {
-  constexpr int NRED = (NWK - 1) * NCG > 0 ? (NWK - 1) * NCG : 1;
+// wave 0 then transposes the 64 x 32 logits through LDS and each lane scans
+// the 32 columns of its token: (max, first index) per token and group.
+template <int NWK>
+__global__ __launch_bounds__(64 * NWK) void classifier_argmax_kernel(SkinnyArgs a) {
+  constexpr int NRED = NWK > 1 ? NWK - 1 : 1;
   __shared__ float red[NRED][32 * 64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int cgl = wave % NCG, kw = wave / NCG;
-  const int cg = blockIdx.x * NCG + cgl;
+  const int tid = threadIdx.x, lane = tid & 63, kw = tid >> 6;
+  const int cg = blockIdx.x;
   const int nwin = a.K / 64;
   const int w0 = (kw * nwin) / NWK, w1 = ((kw + 1) * nwin) / NWK;  // this wave's windows [w0, w1), <= 2
   const int row = lane & 31, h = lane >> 5;
@@ -39,28 +37,7 @@ __global__ __launch_bounds__(64 * NWK * NCG) void skinny_kernel(SkinnyArgs a) {
   // ((w * 4 + s) * 2 + tile) KB; lane l's 16 B at l * 16
   const half_t* wp = a.W + (size_t)cg * nwin * 2048 + lane * 8;
   const half_t* xp0 = a.X + lane * 8;
-
-  // Every load below is unconditional (addresses clamped to valid data,
-  // unused values zeroed by selects): predicated loads compile to branches
-  // whose merges wait for the loads issued so far.
-  // epilogue operands, requested before the weights
-  float ep0[16], ep1[16];
-  float cs = 0.f, sn = 0.f;
-  int pos = 0;
-  if constexpr (EPI == SK_RESID) {
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int t = 8 * (r >> 2) + 4 * h + (r & 3);
-      ep0[r] = a.x[(size_t)min(t, a.nb - 1) * a.N + col];
-      ep1[r] = a.x[(size_t)min(t + 32, a.nb - 1) * a.N + col];
-    }
-  } else if constexpr (EPI == SK_QKV) {
-    pos = a.ctr[0];
-    const int i = (col & 63) >> 1;
-    cs = a.rope_cos[pos * 32 + i];
-    sn = a.rope_sin[pos * 32 + i];
-  }
-
+  // unconditional loads (window index clamped, the surplus copy zeroed)
   half8 w[8], p[8], q[8];
 #pragma unroll
   for (int s = 0; s < 8; s++) {
@@ -85,7 +62,7 @@ __global__ __launch_bounds__(64 * NWK * NCG) void skinny_kernel(SkinnyArgs a) {
   }
   if constexpr (NWK > 1) {
     if (kw > 0) {
-      float* dst = red[(kw - 1) * NCG + cgl];
+      float* dst = red[kw - 1];
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         dst[r * 64 + lane] = c0[r];
@@ -93,100 +70,42 @@ __global__ __launch_bounds__(64 * NWK * NCG) void skinny_kernel(SkinnyArgs a) {
       }
     }
     __syncthreads();
-    if (kw == 0) {
-#pragma unroll 1
-      for (int o = 1; o < NWK; o++) {
-        const float* src = red[(o - 1) * NCG + cgl];
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          c0[r] += src[r * 64 + lane];
-          c1[r] += src[(16 + r) * 64 + lane];
-        }
-      }
-    }
-  }
-  // c[r]: token 8*(r/4) + 4*h + r%4 (+32 for c1), column cg*32 + row
-  if constexpr (EPI == SK_SWIGLU) {
-    // group 0 holds W1 rows 32*bx.., group 1 the matching W3 rows
-    if constexpr (NWK > 1) __syncthreads();  // reduction reads of red[] done
-    if (kw == 0 && cgl == 1) {
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        red[0][r * 64 + lane] = c0[r];
-        red[0][(16 + r) * 64 + lane] = c1[r];
-      }
-    }
-    __syncthreads();
-    if (kw == 0 && cgl == 0) {
-      const int H = a.N / 2, j = blockIdx.x * 32 + row;
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int t = 8 * (r >> 2) + 4 * h + (r & 3);
-        const float h1 = c0[r], h3 = red[0][r * 64 + lane];
-        const float g1 = c1[r], g3 = red[0][(16 + r) * 64 + lane];
-        if (t < a.nb) a.gate[act_frag_off(t, j)] = (half_t)(h1 / (1.0f + __expf(-h1)) * h3);
-        if (t + 32 < a.nb) a.gate[act_frag_off(t + 32, j)] = (half_t)(g1 / (1.0f + __expf(-g1)) * g3);
-      }
-    }
-    return;
   }
   if (kw != 0) return;
-  if constexpr (EPI == SK_RESID) {
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const int t = 8 * (r >> 2) + 4 * h + (r & 3);
-      if (t < a.nb) a.x[(size_t)t * a.N + col] = ep0[r] + c0[r];
-      if (t + 32 < a.nb) a.x[(size_t)(t + 32) * a.N + col] = ep1[r] + c1[r];
-    }
-  } else if constexpr (EPI == SK_QKV) {
-    // RoPE on interleaved pairs (partner = lane ^ 1), then q -> a.q,
-    // k / v -> the cache at position ctr[0]
-    const int D = a.NH * 64, KVD = a.NKV * 64;
-    const bool rot = col < D + KVD, odd = col & 1;
-#pragma unroll
-    for (int half = 0; half < 2; half++) {
+  if constexpr (NWK > 1) {
+#pragma unroll 1
+    for (int o = 1; o < NWK; o++) {
+      const float* src = red[o - 1];
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int t = 8 * (r >> 2) + 4 * h + (r & 3) + 32 * half;
-        float v = half ? c1[r] : c0[r];
-        const float pv = __shfl_xor(v, 1, 64);
-        if (rot) {
-          const float e = odd ? pv : v, o = odd ? v : pv;
-          v = odd ? (o * cs + e * sn) : (e * cs - o * sn);
-        }
-        if (t < a.nb) {
-          if (col < D) {
-            a.q[(size_t)t * D + col] = (half_t)v;
-          } else {
-            const bool isk = col < D + KVD;
-            const int c = col - (isk ? D : D + KVD);
-            half_t* dst = (isk ? a.kc : a.vc) + (((size_t)t * a.NKV + (c >> 6)) * a.max_ctx + pos) * 64 + (c & 63);
-            *dst = (half_t)v;
-          }
-        }
-      }
-    }
-  } else {  // SK_ARGMAX
-    const bool valid = col < a.nvalid;
-#pragma unroll
-    for (int half = 0; half < 2; half++) {
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int t = 8 * (r >> 2) + 4 * h + (r & 3) + 32 * half;
-        const float v0 = half ? c1[r] : c0[r];
-        if (a.logits && valid) a.logits[(size_t)t * a.N + col] = v0;
-        float v = valid ? v0 : -INFINITY;
-        int idx = col;
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) {
-          const float ov = __shfl_xor(v, o, 64);
-          const int oi = __shfl_xor(idx, o, 64);
-          if (ov > v || (ov == v && oi < idx)) { v = ov; idx = oi; }
-        }
-        if (row == 0) a.amax[(size_t)cg * kDecRows + t] = make_float2(v, __int_as_float(idx));
+        c0[r] += src[r * 64 + lane];
+        c1[r] += src[(16 + r) * 64 + lane];
       }
     }
   }
+  // c[r]: token 8*(r/4) + 4*h + r%4 (+32 for c1), column col.  Transpose
+  // into tile[t][c] (row stride 33: conflict-free both ways; red[0] is this
+  // wave's own, its reads above are done), then lane t scans its row.
+  float* tile = red[0];
+  const bool valid = col < a.nvalid;
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    const int t = 8 * (r >> 2) + 4 * h + (r & 3);
+    tile[t * 33 + row] = valid ? c0[r] : -INFINITY;
+    tile[(t + 32) * 33 + row] = valid ? c1[r] : -INFINITY;
+    if (a.logits && valid) {
+      a.logits[(size_t)t * a.N + col] = c0[r];
+      a.logits[(size_t)(t + 32) * a.N + col] = c1[r];
+    }
+  }
+  float v = tile[lane * 33];
+  int idx = 0;
+#pragma unroll
+  for (int c = 1; c < 32; c++) {
+    const float x = tile[lane * 33 + c];
+    if (x > v) { v = x; idx = c; }  // strict: the first index wins ties
+  }
+  a.amax[(size_t)cg * kDecRows + lane] = make_float2(v, __int_as_float(cg * 32 + idx));
 }
 
 __global__ __launch_bounds__(256) void argmax_kernel(uint16_t* tok_out, uint16_t* hist, const int* step,
@@ -758,45 +677,27 @@ __global__ __launch_bounds__(256) void gather_last_kernel(float* dst, const floa
 
 }  // namespace
 
-template <int EPI, int NCG>
-hipError_t skinny_launch(const SkinnyArgs& a, int nwk, hipStream_t s) {
-  dim3 grid(a.N / (32 * NCG));
-  switch (nwk) {
-    case 1: hipLaunchKernelGGL((skinny_kernel<EPI, 1, NCG>), grid, dim3(64 * NCG), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((skinny_kernel<EPI, 2, NCG>), grid, dim3(128 * NCG), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((skinny_kernel<EPI, 4, NCG>), grid, dim3(256 * NCG), 0, s, a); break;
-    case 8: hipLaunchKernelGGL((skinny_kernel<EPI, 8, NCG>), grid, dim3(512 * NCG), 0, s, a); break;
-    default:
-      if constexpr (NCG == 1) {
-        hipLaunchKernelGGL((skinny_kernel<EPI, 16, 1>), grid, dim3(1024), 0, s, a);
-        break;
-      }
-      return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
-}
-
-// waves per column group: enough that no wave holds more than two windows
-int skinny_kwaves(int K, int ncg) {
-  const int nwin = K / 64, cap = 16 / ncg;
+// waves splitting K: enough that no wave holds more than two windows
+int classifier_kwaves(int K) {
+  const int nwin = K / 64;
   int w = 1;
-  while (w < cap && (nwin + w - 1) / w > 2) w <<= 1;
+  while (w < 16 && (nwin + w - 1) / w > 2) w <<= 1;
   return w;
 }
 
-hipError_t skinny_gemm(const SkinnyArgs& a, int epi, hipStream_t s) {
-  const int ncg = epi == SK_SWIGLU ? 2 : 1;
-  if (a.N <= 0 || a.N % (32 * ncg) || a.K <= 0 || a.K % 64 || a.nb < 1 || a.nb > kDecRows)
-    return hipErrorInvalidValue;
-  const int nwk = skinny_kwaves(a.K, ncg);
+hipError_t classifier_argmax(const SkinnyArgs& a, hipStream_t s) {
+  if (a.N <= 0 || a.N % 32 || a.K <= 0 || a.K % 64 || a.nb < 1 || a.nb > kDecRows) return hipErrorInvalidValue;
+  const int nwk = classifier_kwaves(a.K);
   if ((a.K / 64 + nwk - 1) / nwk > 2) return hipErrorInvalidValue;  // K too long for one block
-  switch (epi) {
-    case SK_RESID: return skinny_launch<SK_RESID, 1>(a, nwk, s);
-    case SK_QKV: return skinny_launch<SK_QKV, 1>(a, nwk, s);
-    case SK_SWIGLU: return skinny_launch<SK_SWIGLU, 2>(a, nwk, s);
-    case SK_ARGMAX: return skinny_launch<SK_ARGMAX, 1>(a, nwk, s);
-    default: return hipErrorInvalidValue;
+  const dim3 grid(a.N / 32);
+  switch (nwk) {
+    case 1: hipLaunchKernelGGL(classifier_argmax_kernel<1>, grid, dim3(64), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(classifier_argmax_kernel<2>, grid, dim3(128), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(classifier_argmax_kernel<4>, grid, dim3(256), 0, s, a); break;
+    case 8: hipLaunchKernelGGL(classifier_argmax_kernel<8>, grid, dim3(512), 0, s, a); break;
+    default: hipLaunchKernelGGL(classifier_argmax_kernel<16>, grid, dim3(1024), 0, s, a); break;
   }
+  return hipGetLastError();
 }
 
 int skinny_splits(int N, int K) {

@@ -291,7 +291,7 @@ int enqueue_step(ane_decoder* d, float* logits, uint16_t* hist) {
   s.nb = nb;
   s.X = d->xn; s.W = d->fembed; s.N = d->V; s.K = D; s.amax = d->amax;
   s.logits = logits; s.nvalid = d->V;
-  DCHK(op, skinny_gemm(s, SK_ARGMAX, st));
+  DCHK(op, classifier_argmax(s, st));
   DCHK(op, argmax_reduce(d->tok_d, hist, d->ctr_d + 1, d->amax, d->V / 32, nb, st));
   DCHK(op, dec_advance(d->ctr_d, st));
   return ANE_OK;
@@ -429,7 +429,7 @@ extern "C" int ane_decode_prefill(ane_decoder* d, const uint16_t* prefix, int32_
   s.nb = nseq;
   s.X = d->xn; s.W = d->fembed; s.N = d->V; s.K = D; s.amax = d->amax;
   s.logits = logits ? d->logits_d : nullptr; s.nvalid = d->V;
-  DCHK(op, skinny_gemm(s, SK_ARGMAX, st));
+  DCHK(op, classifier_argmax(s, st));
   DCHK(op, argmax_reduce(d->tok_d, nullptr, nullptr, d->amax, d->V / 32, nseq, st));
   DCHK(op, dec_set_ctr(d->ctr_d, plen, 0, st));
   d->pos = plen;
