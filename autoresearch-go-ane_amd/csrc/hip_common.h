@@ -84,4 +84,64 @@ __device__ __forceinline__ void prefetch_slice(const void* p, size_t bytes, size
   asm volatile("" ::"v"(x));
 }
 
+// prefetch_slice in two halves for kernels with loads of their own: the
+// first kPrefetchEarly 16-byte loads of the slice are issued by
+// prefetch_begin (after the kernel has issued its own loads, so waiting
+// for those does not wait for these) and consumed by prefetch_end, after
+// the kernel's work; any rest of the slice is streamed by prefetch_end.
+constexpr int kPrefetchEarly = 4;
+struct Prefetch {
+  uint4 v[kPrefetchEarly];
+};
+__device__ __forceinline__ Prefetch prefetch_begin(const void* p, size_t bytes, size_t part, size_t nparts) {
+  Prefetch f;
+  const size_t n = bytes / 16;
+  if (!p || n == 0) {
+#pragma unroll
+    for (int u = 0; u < kPrefetchEarly; u++) f.v[u] = make_uint4(0, 0, 0, 0);
+    return f;
+  }
+  const uint4* q = reinterpret_cast<const uint4*>(p);
+  const size_t i0 = part * blockDim.x + threadIdx.x, stride = nparts * blockDim.x;
+#pragma unroll
+  for (int u = 0; u < kPrefetchEarly; u++) {  // unconditional: the index is clamped
+    const size_t i = i0 + u * stride;
+    f.v[u] = q[i < n ? i : n - 1];
+  }
+  return f;
+}
+__device__ __forceinline__ void prefetch_end(const Prefetch& f, const void* p, size_t bytes, size_t part,
+                                             size_t nparts) {
+  uint32_t x = 0;
+#pragma unroll
+  for (int u = 0; u < kPrefetchEarly; u++) x ^= f.v[u].x ^ f.v[u].y ^ f.v[u].z ^ f.v[u].w;
+  const size_t n = bytes / 16;
+  if (p && n > 0) {
+    const uint4* q = reinterpret_cast<const uint4*>(p);
+    const size_t stride = nparts * blockDim.x;
+    for (size_t i = part * blockDim.x + threadIdx.x + kPrefetchEarly * stride; i < n; i += stride) {
+      const uint4 v = q[i];
+      x ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+  }
+  asm volatile("" ::"v"(x));
+}
+
+// Sum over the 64 lanes: DPP within each 16-lane row (quad_perm [1,0,3,2],
+// [2,3,0,1], row_half_mirror, row_mirror), then the rows by one lane
+// permute and one half swap; every lane ends with the total.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_row_f<0xB1>(v);
+  v += dpp_row_f<0x4E>(v);
+  v += dpp_row_f<0x141>(v);
+  v += dpp_row_f<0x140>(v);
+  v += __shfl_xor(v, 16, 64);
+  v += xor32_f(v);
+  return v;
+}
+
 }  // namespace ane

@@ -45,48 +45,60 @@ __global__ __launch_bounds__(256) void embed_norm_kernel(float* xpre, float* x0,
 __global__ __launch_bounds__(256) void rmsnorm_kernel(half_t* out, const float* x, const float* xsub,
                                                       const float* lamp, const float* gain, int T, int D,
                                                       const void* pf, size_t pf_bytes) {
-  prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (t >= T) return;
-  const float lam = xsub ? *lamp : 0.f;
   // D is a multiple of 64: each lane owns float4 groups i = 4*lane + 256*k,
   // held in registers between the reduction and the store (D <= 1024).
-  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * D);
-  const float4* sr = xsub ? reinterpret_cast<const float4*>(xsub + (size_t)t * D) : nullptr;
+  // The row, its subtrahend and the gains are requested first, then this
+  // block's share of the next GEMM's weights (consumed after the stores).
   const int nv = D / 4;
-  float4 v[4];
+  const bool row_ok = t < T;
+  const float4* xr = reinterpret_cast<const float4*>(x + (size_t)(row_ok ? t : 0) * D);
+  const float4* sr = xsub ? reinterpret_cast<const float4*>(xsub + (size_t)(row_ok ? t : 0) * D) : nullptr;
+  const float4* g4 = reinterpret_cast<const float4*>(gain);
+  float4 v[4], sb[4], gg[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int i = lane + 64 * k;
+    if (i < nv) {
+      v[k] = xr[i];
+      if (sr) sb[k] = sr[i];
+      gg[k] = gain ? g4[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+  }
+  const Prefetch pfd = prefetch_begin(pf, pf_bytes, blockIdx.x, gridDim.x);
+  const float lam = xsub ? *lamp : 0.f;
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < 4; k++) {
     const int i = lane + 64 * k;
     if (i < nv) {
-      float4 a = xr[i];
+      float4 a = v[k];
       if (sr) {
-        const float4 b = sr[i];
-        a.x -= lam * b.x; a.y -= lam * b.y; a.z -= lam * b.z; a.w -= lam * b.w;
+        a.x -= lam * sb[k].x; a.y -= lam * sb[k].y; a.z -= lam * sb[k].z; a.w -= lam * sb[k].w;
       }
       v[k] = a;
       ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
     }
   }
-  ss = wave_sum(ss);
+  ss = wave_sum_dpp(ss);
   const float sc = 1.0f / sqrtf(ss / (float)D + 1e-5f);
-  half4* orow = reinterpret_cast<half4*>(out + (size_t)t * D);
-  const float4* g4 = reinterpret_cast<const float4*>(gain);
+  if (row_ok) {
+    half4* orow = reinterpret_cast<half4*>(out + (size_t)t * D);
 #pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const int i = lane + 64 * k;
-    if (i < nv) {
-      float4 a = v[k];
-      float4 gg = gain ? g4[i] : make_float4(1.f, 1.f, 1.f, 1.f);
-      half4 h;
-      h[0] = (half_t)(a.x * sc * gg.x);
-      h[1] = (half_t)(a.y * sc * gg.y);
-      h[2] = (half_t)(a.z * sc * gg.z);
-      h[3] = (half_t)(a.w * sc * gg.w);
-      orow[i] = h;
+    for (int k = 0; k < 4; k++) {
+      const int i = lane + 64 * k;
+      if (i < nv) {
+        const float4 a = v[k], g = gg[k];
+        half4 h;
+        h[0] = (half_t)(a.x * sc * g.x);
+        h[1] = (half_t)(a.y * sc * g.y);
+        h[2] = (half_t)(a.z * sc * g.z);
+        h[3] = (half_t)(a.w * sc * g.w);
+        orow[i] = h;
+      }
     }
   }
+  prefetch_end(pfd, pf, pf_bytes, blockIdx.x, gridDim.x);
 }
 
 __global__ void gather_kernel(uint16_t* tok, uint16_t* tgt, const uint16_t* data, const uint64_t* pos, int nseq,
