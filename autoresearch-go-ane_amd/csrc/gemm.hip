@@ -931,20 +931,23 @@ void gemm_pick_tile(int M, int N, int K, int epi, int* pbm, int* pbn) {
   // Preference order with a minimum block count each: a tile is taken only
   // if it yields enough blocks to keep the 256 CUs (and 2-3 resident blocks
   // per CU for the smaller tiles) busy.  Thresholds come from a sweep of
-  // the stories110M shapes on MI355X (M = 8192 tokens, random operands):
-  // 256x256 with 8 waves wins from 512 blocks (W1|W3: 925 vs 817 TFLOP/s
-  // for 128x128; classifier 885 vs 801), 128x128 at N >= 2048, 128x64 at
-  // N = 768 with K <= 2048, 64x64 for narrow outputs with long K.  A nonzero
+  // the stories110M shapes on MI355X (M = 8192 and 4096 tokens, random
+  // operands): 256x256 with 8 waves wins from 256 blocks (W1|W3 at M = 8192:
+  // 925 vs 817 TFLOP/s for 128x128, at M = 4096: 953 vs 809; classifier 885
+  // vs 801), 128x128 from 512 blocks (the SwiGLU-backward GEMM at M = 4096:
+  // 18.0 vs 21.4 us for 128x64), 128x64 at N = 768 with K <= 2048, 64x64
+  // for narrow outputs with long K.  A nonzero
   // *pbm / *pbn on entry is a constraint the chosen tile keeps (callers
   // size buffers by it).
-  static const int cand[][3] = {{256, 256, 512}, {128, 128, 1024}, {128, 64, 600}, {64, 128, 600},
+  static const int cand[][3] = {{256, 256, 256}, {128, 128, 512}, {128, 64, 600}, {64, 128, 600},
                                 {256, 128, 600},  {128, 256, 600},  {256, 64, 600}, {64, 64, 0}};
   constexpr int NCAND = 8;
   const int want_bm = *pbm, want_bn = *pbn;
-  // Widths that are a multiple of 192 but not of 256 (the fused Wq|Wk|Wv
-  // output, 2304): 128x192 blocks split N into whole waves; measured
-  // 33.6 us vs 38.5 for 128x128 at M = 8192, 19.9 vs 21.3 for 128x64 at 4096
-  if ((epi == EPI_STORE_H || epi == EPI_STORE_F || epi == EPI_RESID) && N % 192 == 0 && N % 256 != 0 &&
+  // Wide outputs that are a multiple of 192 but not of 1024 (the fused
+  // Wq|Wk|Wv output, 2304 = 12 x 192): 128x192 blocks split N into whole
+  // waves; measured 33.6 us vs 38.5 for 128x128 at M = 8192, 19.9 vs 21.3
+  // for 128x64 at 4096
+  if ((epi == EPI_STORE_H || epi == EPI_STORE_F || epi == EPI_RESID) && N % 192 == 0 && N >= 1536 && N % 1024 != 0 &&
       M % 128 == 0 && (long)(M / 128) * (N / 192) >= 384 && (!want_bm || want_bm == 128) &&
       (!want_bn || want_bn == 192)) {
     *pbm = 128;
