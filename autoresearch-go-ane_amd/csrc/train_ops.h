@@ -4,7 +4,7 @@
 
 namespace ane {
 
-constexpr int kNormBwdRows = 16;  // rows per block of norm_bwd (4 waves x 4 rows)
+constexpr int kNormBwdRows = 8;  // rows per block of norm_bwd (4 waves x 2 rows)
 
 // out = alpha * addend + addend2 + RMSNorm-backward(dy; x, gain) (+ ve_dx on
 // channels 0..11), fp32 and optionally fp16.  Gain-free form:
