@@ -354,15 +354,23 @@ __device__ __forceinline__ float sum8_dpp(float v) {
   return v;
 }
 
+// Keys per split for ctx keys over nsplit splits: an even share rounded up
+// to 32 (<= kDecChunk, as nsplit covers max_ctx in kDecChunk-key chunks),
+// so no split is left with a short tail while the others run full.
+__device__ __forceinline__ int dec_chunk(int ctx, int nsplit) {
+  return ((ctx + nsplit - 1) / nsplit + 31) & ~31;
+}
+
 template <int G>
 __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
   const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int D = a.NH * 64;
   const int ctx = a.ctr[0] + 1;
-  const int c0 = sp * kDecChunk;
+  const int chunk = dec_chunk(ctx, a.nsplit);
+  const int c0 = sp * chunk;
   if (c0 >= ctx) return;  // uniform over the block, before any barrier
-  const int n = min(kDecChunk, ctx - c0);
+  const int n = min(chunk, ctx - c0);
   __shared__ half_t qs[G][64];
   __shared__ float sc[G][kDecChunk];
   __shared__ __attribute__((aligned(16))) float pv[G][32][64];
@@ -473,7 +481,8 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
 __global__ __launch_bounds__(64) void dec_combine_kernel(DecAttnArgs a) {
   const int b = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
   const int ctx = a.ctr[0] + 1;
-  const int ns = (ctx + kDecChunk - 1) / kDecChunk;
+  const int chunk = dec_chunk(ctx, a.nsplit);
+  const int ns = (ctx + chunk - 1) / chunk;
   const float* p = a.part + ((size_t)b * a.NH + h) * a.nsplit * 66;
   float M = -INFINITY;
   for (int s = 0; s < ns; s++) M = fmaxf(M, p[s * 66 + 64]);
