@@ -381,15 +381,21 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
   const half_t* Vb = a.vc + (cache0 + c0) * 64;
   const int kl = tid >> 3, d8 = tid & 7;
   constexpr int NIT = kDecChunk / 32;
-  // unconditional loads (rows clamped into the chunk; keys past n unused)
+  // Load order: this thread's q element first (the staging barrier waits
+  // for it alone), then every K row, then every V row, so the scores can be
+  // formed while the values are still arriving.  Unconditional loads
+  // (indices clamped; keys past n unused).
+  // (sched_barrier fences keep the scheduler from sinking the q load)
+  const half_t qv = a.q[(size_t)b * D + (kvh * G) * 64 + min(tid, G * 64 - 1)];
+  __builtin_amdgcn_sched_barrier(0);
   half8 kk[NIT], kv[NIT];
 #pragma unroll
-  for (int it = 0; it < NIT; it++) {
-    const int j = min(kl + 32 * it, n - 1);
-    kk[it] = ld_h8(Kb + (size_t)j * 64 + d8 * 8);
-    kv[it] = ld_h8(Vb + (size_t)j * 64 + d8 * 8);
-  }
-  if (tid < G * 64) qs[tid >> 6][tid & 63] = a.q[(size_t)b * D + (kvh * G) * 64 + tid];
+  for (int it = 0; it < NIT; it++) kk[it] = ld_h8(Kb + (size_t)min(kl + 32 * it, n - 1) * 64 + d8 * 8);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int it = 0; it < NIT; it++) kv[it] = ld_h8(Vb + (size_t)min(kl + 32 * it, n - 1) * 64 + d8 * 8);
+  __builtin_amdgcn_sched_barrier(0);
+  if (tid < G * 64) qs[tid >> 6][tid & 63] = qv;
   __syncthreads();
   // this lane's 8 dims of each head as fp16 pairs (fp16 products exact in fp32)
   half2v qr[G][4];
