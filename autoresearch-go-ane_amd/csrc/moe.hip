@@ -8,9 +8,10 @@
 //                  (ascending inputs, every product and sum separately
 //                  rounded) -> top-2 (ties to the lower expert) and the
 //                  softmax over the two chosen logits
-//   2. permute     one-block counting sort: rows of each expert in token
-//                  order, each expert's group padded to a multiple of 128
-//                  rows; tile table (first row, expert) for the grouped GEMMs
+//   2. permute     stable counting sort over blocks of 256 tokens (count,
+//                  scan, scatter): rows of each expert in token order, each
+//                  expert's group padded to a multiple of 128 rows; tile
+//                  table (first row, expert) for the grouped GEMMs
 //   3. gather      xg[row] = fp16(x[token of row]) (zero for padding rows)
 //   4. grouped GEMM  [rows, 2H] = xg . W13_e^T with the SwiGLU epilogue
 //   5. grouped GEMM  yw[row] = (g . W2_e^T) * weight(row)
@@ -35,33 +36,84 @@ using namespace ane;
 namespace {
 
 constexpr int kGroupRows = 128;  // expert groups are padded to whole 128-row GEMM tiles
-constexpr int kPermThreads = 1024;
 constexpr int kMaxExperts = 16;
 
-// one thread per (token, expert); E threads per token, 256 / E tokens per block
+// Router: one thread per (token, expert) for kRouterTok tokens per block.
+// The logit is linearCF's sequential sum (ascending inputs, every product
+// and sum separately rounded), so it stays a serial chain per thread; what
+// the block does in parallel is feed it.  Chunks of up to kRChunk inputs of
+// the block's token rows and of the router rows are staged in LDS
+// (double-buffered: chunk c + 1's global loads are in flight while chunk c
+// is summed, which takes longer than their latency), with rows padded by 4
+// floats so the tokens / experts read one float4 column from distinct banks.
+constexpr int kRouterTok = 16;
+constexpr int kRChunk = 256, kRPad = kRChunk + 4;
+constexpr int kRStage = (kRouterTok + kMaxExperts) * (kRChunk / 4) / 256;  // float4 per thread per chunk
 __global__ __launch_bounds__(256) void router_kernel(const float* x, const float* wr, int32_t* idx, float* wts,
                                                      int T, int D, int E) {
-  __shared__ float lg[256];
+  __shared__ __attribute__((aligned(16))) float xs[2][kRouterTok][kRPad];
+  __shared__ __attribute__((aligned(16))) float ws[2][kMaxExperts][kRPad];
+  __shared__ float lg[kRouterTok][kMaxExperts];
   const int tid = threadIdx.x;
-  const int tpb = 256 / E;
+  const int t0 = blockIdx.x * kRouterTok;
   const int tl = tid / E, e = tid % E;
-  const int t = blockIdx.x * tpb + tl;
-  float s = 0.f;
-  if (t < T) {
-    const float4* xr = reinterpret_cast<const float4*>(x + (size_t)t * D);
-    const float4* w = reinterpret_cast<const float4*>(wr + (size_t)e * D);
-    for (int i = 0; i < D / 4; i++) {
-      const float4 a = w[i], b = xr[i];
-      s = __fadd_rn(s, __fmul_rn(a.x, b.x));
-      s = __fadd_rn(s, __fmul_rn(a.y, b.y));
-      s = __fadd_rn(s, __fmul_rn(a.z, b.z));
-      s = __fadd_rn(s, __fmul_rn(a.w, b.w));
+  const bool active = tid < kRouterTok * E;
+  const int nch = (D + kRChunk - 1) / kRChunk;
+  // chunk c covers inputs [c * kRChunk, c * kRChunk + len), len a multiple of 64
+  auto chunk_len = [&](int c) { return min(kRChunk, D - c * kRChunk); };
+  auto fetch = [&](int c, float4 (&v)[kRStage]) {
+    const int q4 = chunk_len(c) / 4, nst = (kRouterTok + E) * q4;
+#pragma unroll
+    for (int u = 0; u < kRStage; u++) {
+      const int i = tid + 256 * u;
+      if (i < nst) {
+        const int r = i / q4, q = i % q4;
+        const float* src = r < kRouterTok ? x + (size_t)min(t0 + r, T - 1) * D : wr + (size_t)(r - kRouterTok) * D;
+        v[u] = *reinterpret_cast<const float4*>(src + c * kRChunk + q * 4);
+      }
     }
-  }
-  lg[tid] = s;
+  };
+  auto store = [&](int c, int buf, const float4 (&v)[kRStage]) {
+    const int q4 = chunk_len(c) / 4, nst = (kRouterTok + E) * q4;
+#pragma unroll
+    for (int u = 0; u < kRStage; u++) {
+      const int i = tid + 256 * u;
+      if (i < nst) {
+        const int r = i / q4, q = i % q4;
+        float* dst = r < kRouterTok ? &xs[buf][r][q * 4] : &ws[buf][r - kRouterTok][q * 4];
+        *reinterpret_cast<float4*>(dst) = v[u];
+      }
+    }
+  };
+  float4 v[kRStage];
+  fetch(0, v);
+  store(0, 0, v);
   __syncthreads();
-  if (e == 0 && t < T) {
-    const float* l = lg + tl * E;
+  float s = 0.f;
+  for (int c = 0; c < nch; c++) {
+    const int buf = c & 1, len = chunk_len(c);
+    if (c + 1 < nch) fetch(c + 1, v);
+    if (active) {
+      for (int i = 0; i < len; i += 16) {
+#pragma unroll
+        for (int j = 0; j < 16; j += 4) {
+          const float4 a = *reinterpret_cast<const float4*>(&ws[buf][e][i + j]);
+          const float4 b = *reinterpret_cast<const float4*>(&xs[buf][tl][i + j]);
+          s = __fadd_rn(s, __fmul_rn(a.x, b.x));
+          s = __fadd_rn(s, __fmul_rn(a.y, b.y));
+          s = __fadd_rn(s, __fmul_rn(a.z, b.z));
+          s = __fadd_rn(s, __fmul_rn(a.w, b.w));
+        }
+      }
+    }
+    if (c + 1 < nch) store(c + 1, buf ^ 1, v);  // buffer buf ^ 1 was last read in chunk c - 1
+    __syncthreads();
+  }
+  if (active) lg[tl][e] = s;
+  __syncthreads();
+  const int t = t0 + tl;
+  if (active && e == 0 && t < T) {
+    const float* l = lg[tl];
     int a = 0;
     for (int k = 1; k < E; k++)
       if (l[k] > l[a]) a = k;
@@ -76,77 +128,136 @@ __global__ __launch_bounds__(256) void router_kernel(const float* x, const float
   }
 }
 
-// Single block.  Thread i owns tokens [i*per, (i+1)*per); per-expert counts
-// are scanned across threads, so rows of one expert come out in token order.
-__global__ __launch_bounds__(kPermThreads) void permute_kernel(const int32_t* idx, const float* wts, int T, int E,
-                                                               int* perm, float* rw, int* rowpos, int* tiles) {
-  __shared__ int sc[kMaxExperts][kPermThreads];
-  __shared__ int start[kMaxExperts + 1], total[kMaxExperts];
-  const int tid = threadIdx.x;
-  const int per = (T + kPermThreads - 1) / kPermThreads;
-  const int t0 = min(T, tid * per), t1 = min(T, t0 + per);
-  int cnt[kMaxExperts];
-#pragma unroll
-  for (int e = 0; e < kMaxExperts; e++) cnt[e] = 0;
-  for (int t = t0; t < t1; t++) {
-#pragma unroll
-    for (int e = 0; e < kMaxExperts; e++) cnt[e] += (idx[2 * t] == e) + (idx[2 * t + 1] == e);
+// Permutation as a stable counting sort in three launches (blocks of 256
+// tokens; the rows of each expert come out in token order):
+//   perm_count: per block and expert, the tokens that chose the expert
+//               (wave ballots), counts[e][block];
+//   perm_scan:  one block: exclusive scan of counts[e][.] over blocks, each
+//               expert's group padded to whole 128-row tiles, tile table,
+//               padding rows;
+//   perm_scatter: row = group base + block base + rank inside the block
+//               (ballot prefix counts), perm / rw / rowpos.
+constexpr int kPermTok = 256;
+__device__ __forceinline__ bool chose(const int32_t* idx, int t, int T, int e) {
+  return t < T && (idx[2 * t] == e || idx[2 * t + 1] == e);
+}
+
+__global__ __launch_bounds__(kPermTok) void perm_count_kernel(const int32_t* idx, int T, int E, int* counts,
+                                                              int nblk) {
+  __shared__ int wc[kPermTok / 64][kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t = blockIdx.x * kPermTok + tid;
+  const int a = t < T ? idx[2 * t] : -1, b = t < T ? idx[2 * t + 1] : -1;
+  for (int e = 0; e < E; e++) {
+    const unsigned long long m = __ballot(a == e || b == e);
+    if (lane == 0) wc[wave][e] = __popcll(m);
   }
-  // (expert loops run to the compile-time bound with an e < E guard so the
-  // per-thread arrays stay in registers)
-#pragma unroll
-  for (int e = 0; e < kMaxExperts; e++)
-    if (e < E) sc[e][tid] = cnt[e];
   __syncthreads();
-  // inclusive Hillis-Steele scan over threads, all experts at once
-  for (int off = 1; off < kPermThreads; off <<= 1) {
+  if (tid < E) {
+    int c = 0;
+    for (int w = 0; w < kPermTok / 64; w++) c += wc[w][tid];
+    counts[(size_t)tid * nblk + blockIdx.x] = c;
+  }
+}
+
+// counts[e][b] -> exclusive block offsets (in place); grp[e] = group start,
+// grp[E + e] = rows of expert e; tiles[0] = number of 128-row tiles, then
+// (first row, expert) per tile
+__global__ __launch_bounds__(256) void perm_scan_kernel(int* counts, int nblk, int E, int* grp, int* tiles,
+                                                        int* perm, float* rw) {
+  __shared__ int part[kMaxExperts][256];
+  __shared__ int tot[kMaxExperts], start[kMaxExperts + 1], tstart[kMaxExperts + 1];
+  const int tid = threadIdx.x;
+  const int per = (nblk + 255) / 256;
+  const int b0 = min(nblk, tid * per), b1 = min(nblk, b0 + per);
+  int sum[kMaxExperts];
+#pragma unroll
+  for (int e = 0; e < kMaxExperts; e++) {
+    sum[e] = 0;
+    if (e < E)
+      for (int b = b0; b < b1; b++) sum[e] += counts[(size_t)e * nblk + b];
+    part[e][tid] = sum[e];
+  }
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {  // inclusive scan of the thread sums, every expert at once
     int v[kMaxExperts];
 #pragma unroll
-    for (int e = 0; e < kMaxExperts; e++) v[e] = (e < E && tid >= off) ? sc[e][tid - off] : 0;
+    for (int e = 0; e < kMaxExperts; e++) v[e] = (e < E && tid >= off) ? part[e][tid - off] : 0;
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < kMaxExperts; e++)
-      if (e < E) sc[e][tid] += v[e];
+      if (e < E) part[e][tid] += v[e];
     __syncthreads();
   }
+#pragma unroll
+  for (int e = 0; e < kMaxExperts; e++) {
+    if (e >= E) continue;
+    int* c = counts + (size_t)e * nblk;
+    int run = part[e][tid] - sum[e];  // exclusive
+    for (int b = b0; b < b1; b++) {
+      const int n = c[b];
+      c[b] = run;
+      run += n;
+    }
+  }
+  if (tid < E) tot[tid] = part[tid][255];
+  __syncthreads();
   if (tid == 0) {
     int p = 0, nt = 0;
     for (int e = 0; e < E; e++) {
-      const int m = sc[e][kPermThreads - 1];
-      total[e] = m;
       start[e] = p;
-      const int ntl = (m + kGroupRows - 1) / kGroupRows;
-      for (int j = 0; j < ntl; j++) {
-        tiles[1 + 2 * (nt + j)] = p + j * kGroupRows;
-        tiles[2 + 2 * (nt + j)] = e;
-      }
+      tstart[e] = nt;
+      const int ntl = (tot[e] + kGroupRows - 1) / kGroupRows;
       nt += ntl;
       p += ntl * kGroupRows;
+      grp[e] = start[e];
+      grp[E + e] = tot[e];
     }
     start[E] = p;
+    tstart[E] = nt;
     tiles[0] = nt;
   }
   __syncthreads();
-  int run[kMaxExperts];
-#pragma unroll
-  for (int e = 0; e < kMaxExperts; e++) run[e] = e < E ? start[e] + sc[e][tid] - cnt[e] : 0;  // exclusive prefix
-  for (int t = t0; t < t1; t++)
-    for (int k = 0; k < 2; k++) {
-      const int e = idx[2 * t + k];
-      int pos = 0;
-#pragma unroll
-      for (int q = 0; q < kMaxExperts; q++)
-        if (q == e) pos = run[q]++;
-      perm[pos] = t;
-      rw[pos] = wts[2 * t + k];
-      rowpos[2 * t + k] = pos;
-    }
-  // padding rows of every group
-  for (int e = 0; e < E; e++)
-    for (int r = start[e] + total[e] + tid; r < start[e + 1]; r += kPermThreads) {
+  for (int j = tid; j < tstart[E]; j += 256) {
+    int e = 0;
+    while (j >= tstart[e + 1]) e++;
+    tiles[1 + 2 * j] = start[e] + (j - tstart[e]) * kGroupRows;
+    tiles[2 + 2 * j] = e;
+  }
+  for (int e = 0; e < E; e++)  // padding rows of every group
+    for (int r = start[e] + tot[e] + tid; r < start[e + 1]; r += 256) {
       perm[r] = -1;
       rw[r] = 0.f;
     }
+}
+
+__global__ __launch_bounds__(kPermTok) void perm_scatter_kernel(const int32_t* idx, const float* wts, int T, int E,
+                                                                const int* offs, int nblk, const int* grp, int* perm,
+                                                                float* rw, int* rowpos) {
+  __shared__ int wc[kPermTok / 64][kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t = blockIdx.x * kPermTok + tid;
+  const int a = t < T ? idx[2 * t] : -1, b = t < T ? idx[2 * t + 1] : -1;
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int ra = 0, rb = 0;  // rank of this token among the wave's tokens of expert a / b
+  for (int e = 0; e < E; e++) {
+    const unsigned long long m = __ballot(a == e || b == e);
+    if (lane == 0) wc[wave][e] = __popcll(m);
+    const int r = __popcll(m & below);
+    if (a == e) ra = r;
+    if (b == e) rb = r;
+  }
+  __syncthreads();
+  if (t >= T) return;
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int e = k == 0 ? a : b;
+    int pos = grp[e] + offs[(size_t)e * nblk + blockIdx.x] + (k == 0 ? ra : rb);
+    for (int w = 0; w < wave; w++) pos += wc[w][e];
+    perm[pos] = t;
+    rw[pos] = wts[2 * t + k];
+    rowpos[2 * t + k] = pos;
+  }
 }
 
 __global__ __launch_bounds__(256) void gather_kernel(half_t* xg, const float* x, const int* perm, const int* tiles,
@@ -192,6 +303,7 @@ struct ane_moe {
   float *x = nullptr, *wts = nullptr, *rw = nullptr, *yw = nullptr, *out = nullptr;
   int32_t* idx = nullptr;
   int *perm = nullptr, *rowpos = nullptr, *tiles = nullptr;
+  int *counts = nullptr, *grp = nullptr;  // permutation: per-block counts / offsets, group starts and sizes
   half_t *xg = nullptr, *g = nullptr;
 };
 
@@ -286,6 +398,8 @@ extern "C" int ane_moe_open(const ane_moe_cfg* cfg, ane_moe** out) {
     OPEN_CHK(malloc_(m, &m->perm, RC));
     OPEN_CHK(malloc_(m, &m->rw, RC));
     OPEN_CHK(malloc_(m, &m->tiles, 1 + 2 * (RC / kGroupRows)));
+    OPEN_CHK(malloc_(m, &m->counts, E * ((TM + kPermTok - 1) / kPermTok)));
+    OPEN_CHK(malloc_(m, &m->grp, 2 * E));
     OPEN_CHK(malloc_(m, &m->xg, RC * D));
     OPEN_CHK(malloc_(m, &m->g, RC * H));
     OPEN_CHK(malloc_(m, &m->yw, RC * D));
@@ -345,11 +459,17 @@ extern "C" int ane_moe_run(ane_moe* m) {
   const hipStream_t st = m->stream;
   MCHK(op, hipSetDevice(m->cfg.device));
   MCHK(op, hipEventRecord(m->ev0, st));
-  const int tpb = 256 / E;
-  hipLaunchKernelGGL(router_kernel, dim3((T + tpb - 1) / tpb), dim3(256), 0, st, m->x, m->P, m->idx, m->wts, T, D, E);
+  hipLaunchKernelGGL(router_kernel, dim3((T + kRouterTok - 1) / kRouterTok), dim3(256), 0, st, m->x, m->P, m->idx,
+                     m->wts, T, D, E);
   MCHK(op, hipGetLastError());
-  hipLaunchKernelGGL(permute_kernel, dim3(1), dim3(kPermThreads), 0, st, m->idx, m->wts, T, E, m->perm, m->rw,
-                     m->rowpos, m->tiles);
+  const int nblk = (T + kPermTok - 1) / kPermTok;
+  hipLaunchKernelGGL(perm_count_kernel, dim3(nblk), dim3(kPermTok), 0, st, m->idx, T, E, m->counts, nblk);
+  MCHK(op, hipGetLastError());
+  hipLaunchKernelGGL(perm_scan_kernel, dim3(1), dim3(256), 0, st, m->counts, nblk, E, m->grp, m->tiles, m->perm,
+                     m->rw);
+  MCHK(op, hipGetLastError());
+  hipLaunchKernelGGL(perm_scatter_kernel, dim3(nblk), dim3(kPermTok), 0, st, m->idx, m->wts, T, E, m->counts, nblk,
+                     m->grp, m->perm, m->rw, m->rowpos);
   MCHK(op, hipGetLastError());
   hipLaunchKernelGGL(gather_kernel, dim3(m->RC), dim3(256), 0, st, m->xg, m->x, m->perm, m->tiles, D);
   MCHK(op, hipGetLastError());
@@ -367,7 +487,7 @@ extern "C" int ane_moe_run(ane_moe* m) {
     g.grp = m->tiles; g.b_group_stride = (size_t)D * H;
     EpiParams p;
     p.C = m->yw; p.ldc = D; p.rowscale = m->rw;
-    MCHK(op, gemm_run(g, EPI_STORE_RS, p, st, kGroupRows, 64));
+    MCHK(op, gemm_run(g, EPI_STORE_RS, p, st, kGroupRows, 128));
   }
   hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, st, m->out, m->yw, m->rowpos, D);
   MCHK(op, hipGetLastError());
