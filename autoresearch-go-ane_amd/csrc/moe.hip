@@ -487,7 +487,8 @@ extern "C" int ane_moe_run(ane_moe* m) {
     g.grp = m->tiles; g.b_group_stride = (size_t)D * H;
     EpiParams p;
     p.C = m->yw; p.ldc = D; p.rowscale = m->rw;
-    MCHK(op, gemm_run(g, EPI_STORE_RS, p, st, kGroupRows, 128));
+    // 128-column tiles where dim allows (0.308 -> 0.294 ms per layer at dim 768 vs 64)
+    MCHK(op, gemm_run(g, EPI_STORE_RS, p, st, kGroupRows, D % 128 == 0 ? 128 : 64));
   }
   hipLaunchKernelGGL(combine_kernel, dim3(T), dim3(256), 0, st, m->out, m->yw, m->rowpos, D);
   MCHK(op, hipGetLastError());

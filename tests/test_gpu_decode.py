@@ -55,6 +55,31 @@ def test_prefill_and_forced_steps_match_oracle():
     assert max(errs) <= TOL
 
 
+@pytest.mark.parametrize("heads,kv_heads", [(4, 4), (4, 1), (6, 2)])
+def test_query_head_groups(heads, kv_heads):
+    """Every head-group size the attention kernel is built for (1, 4, 3
+    query heads per key/value head) through prefill and forced steps, with
+    hidden 256 and dim 64 * heads (K of 1, 4 and 6 windows per split-K
+    GEMM) and a context that crosses a 256-key split."""
+    cfg = ane.tiny_decode(heads=heads, kv_heads=kv_heads, dim=64 * heads, hidden=256, layers=1)
+    nseq, plen, nsteps = 2, 320, 3
+    p, prefix = _setup(cfg, nseq, plen, 41)
+    forced = np.random.default_rng(42).integers(0, cfg.vocab, (nseq, nsteps)).astype(np.uint16)
+    ref_tok, ref_lg = oracle.decode(cfg, p, prefix, nsteps, forced=forced, want_logits=True)
+    dec = ane.Decoder(cfg, p, max_batch=2, max_ctx=384)
+    try:
+        t0, lg0 = dec.Prefill(prefix, want_logits=True)
+        errs = [np.abs(lg0 - ref_lg[:, 0]).max()]
+        for i in range(nsteps):
+            ti, lgi = dec.Step(forced[:, i], want_logits=True)
+            errs.append(np.abs(lgi - ref_lg[:, i + 1]).max())
+            _check_choice(ti, ref_lg[:, i + 1])
+    finally:
+        dec.Close()
+    print(f"G={heads // kv_heads} decode logits max-abs err per step", [f"{e:.2e}" for e in errs])
+    assert max(errs) <= TOL
+
+
 def test_long_prefix_multi_chunk_attention():
     """1024-token prefix: prefill attention streams 8 key chunks, decode
     attention merges 5 context splits (max_ctx 1152)."""

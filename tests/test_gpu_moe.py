@@ -44,6 +44,25 @@ def test_small_layer_matches_oracle():
     np.testing.assert_array_equal(out, out2)  # deterministic
 
 
+@pytest.mark.parametrize("experts,tokens", [(2, 513), (4, 1000), (16, 777), (16, 4096)])
+def test_expert_counts_and_ragged_token_counts(experts, tokens):
+    """Every supported expert count, token counts that leave a partial
+    256-token permutation block, and (16 x 4096) several full blocks and
+    tile groups per expert."""
+    cfg = MoeConfig(dim=128, hidden=192, experts=experts)
+    p = init_moe_params(cfg, seed=31 + experts, std=0.05)
+    x = make_moe_input(cfg, tokens, seed=32 + tokens)
+    layer = MoeLayer(cfg, p, max_tokens=tokens)
+    try:
+        out, idx, w = layer.Forward(x)
+    finally:
+        layer.Close()
+    ref, ridx, rw = oracle.moe_forward(p, x, cfg.hidden, cfg.experts)
+    np.testing.assert_array_equal(idx, ridx)
+    np.testing.assert_allclose(w, rw, rtol=1e-6, atol=1e-7)
+    _check_out(out, ref)
+
+
 def test_full_size_routing_bit_exact_and_sampled_outputs():
     """dim 768, 8 experts of SwiGLU 2048, 8192 tokens,
     router and experts N(0, 0.02), activations N(0, 1), seed 5."""
