@@ -51,17 +51,15 @@ hipError_t classifier_argmax(const SkinnyArgs& a, hipStream_t s);
 // Split-K form of the decode-step GEMMs (Y = X[64, K] . W[N, K]^T, same
 // fragment-major operands): skinny_partials writes ks = skinny_splits(N, K)
 // fp32 partials part[ks][64][N] from (N/32) x ks one-wave blocks; a finish
-// kernel per token row sums them in split order and applies the epilogue:
+// kernel per token row sums them in split order and applies the epilogue
+// (the QKV partials are finished inside dec_attention):
 //   resid_norm: x[t] += Y[t]; xn[t] = fp16(rmsnorm(x[t]) * g)  (N = D <= 1024)
-//   qkv:        RoPE at ctr[0] on q, k; q -> q[t], k / v -> cache  (N = (NH + 2 NKV) * 64)
 //   swiglu:     gate[t][j] = silu(h1) * h3 over W1|W3 interleaved by 32 rows (fragment layout)
 int skinny_splits(int N, int K);
 hipError_t skinny_partials(const half_t* X, const half_t* W, float* part, size_t part_cap, int N, int K,
                            hipStream_t s);
 hipError_t skinny_finish_resid_norm(const float* part, int N, int K, float* x, half_t* xn, const float* g, int nb,
                                     hipStream_t s);
-hipError_t skinny_finish_qkv(const float* part, int K, const int* ctr, const float* rope_cos, const float* rope_sin,
-                             half_t* q, half_t* kc, half_t* vc, int NH, int NKV, int max_ctx, int nb, hipStream_t s);
 hipError_t skinny_finish_swiglu(const float* part, int N, int K, half_t* gate, int nb, hipStream_t s);
 
 // tok_out[b] = argmax over groups (first index on ties) for b < nb;
@@ -85,10 +83,18 @@ hipError_t dec_norm(const float* x, half_t* xn, const float* g, int nb, int D, h
 // Attention of one query token per sequence over keys 0..pos (pos = *ctr)
 // in chunks of kDecChunk keys: partials o (unnormalized), m, l per
 // (b, head, chunk); then the merge into att [64][NH*64] fp16.
+// The step's q, k, v come straight from the QKV GEMM's split-K partials
+// (skinny_partials, N = (NH + 2 NKV) * 64): every block sums the q columns
+// of its heads and applies RoPE at ctr[0]; the block whose key split holds
+// that position also forms the new k (RoPE) and v rows, writes them to the
+// cache and uses them in place of the row it read.
 struct DecAttnArgs {
-  const half_t* q;   // [64][NH*64]
-  const half_t* kc;  // layer base
-  const half_t* vc;
+  const float* qkv_part;  // [qkv_ks][64][(NH + 2 NKV) * 64]
+  int qkv_ks;
+  const float* rope_cos;
+  const float* rope_sin;
+  half_t* kc;        // layer base [Bcap][NKV][max_ctx][64]
+  half_t* vc;
   const int* ctr;
   float* part;       // [nb][NH][nsplit][66]
   half_t* att;       // [64][NH*64]

@@ -290,39 +290,6 @@ __global__ __launch_bounds__(256) void finish_resid_norm_kernel(const float* par
   }
 }
 
-// QKV finish: RoPE at position ctr[0] on q and k (interleaved pairs), q ->
-// q[t], k / v -> the layer's cache at that position.  One thread per
-// column pair.
-__global__ __launch_bounds__(256) void finish_qkv_kernel(const float* part, int ks, const int* ctr,
-                                                         const float* rope_cos, const float* rope_sin, half_t* q,
-                                                         half_t* kc, half_t* vc, int NH, int NKV, int max_ctx) {
-  const int t = blockIdx.x;
-  const int D = NH * 64, KVD = NKV * 64, N1 = D + 2 * KVD;
-  const int pos = ctr[0];
-  for (int c2 = threadIdx.x; c2 < N1 / 2; c2 += blockDim.x) {
-    const int col = 2 * c2;
-    float e = split_sum(part, ks, N1, t, col), o = split_sum(part, ks, N1, t, col + 1);
-    if (col < D + KVD) {
-      const int i = (col & 63) >> 1;
-      const float cs = rope_cos[pos * 32 + i], sn = rope_sin[pos * 32 + i];
-      const float e2 = e * cs - o * sn, o2 = o * cs + e * sn;
-      e = e2;
-      o = o2;
-    }
-    half2v w;
-    w[0] = (half_t)e;
-    w[1] = (half_t)o;
-    if (col < D) {
-      *reinterpret_cast<half2v*>(q + (size_t)t * D + col) = w;
-    } else {
-      const bool isk = col < D + KVD;
-      const int c = col - (isk ? D : D + KVD);
-      half_t* dst = (isk ? kc : vc) + (((size_t)t * NKV + (c >> 6)) * max_ctx + pos) * 64 + (c & 63);
-      *reinterpret_cast<half2v*>(dst) = w;
-    }
-  }
-}
-
 // W1|W3 finish: gate[t][j] = silu(h1) * h3 with W1 / W3 rows interleaved by
 // 32 (h1 at column (j/32)*64 + j%32, h3 at +32), fragment layout.
 __global__ __launch_bounds__(256) void finish_swiglu_kernel(const float* part, int ks, half_t* gate, int H) {
@@ -375,18 +342,41 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
   __shared__ float sc[G][kDecChunk];
   __shared__ __attribute__((aligned(16))) float pv[G][32][64];
   __shared__ float stat[G][2];
+  __shared__ __attribute__((aligned(16))) half_t knew[64], vnew[64];
   const float sl2 = a.scale * kL2E;
   const size_t cache0 = ((size_t)b * a.NKV + kvh) * a.max_ctx;
-  const half_t* Kb = a.kc + (cache0 + c0) * 64;
-  const half_t* Vb = a.vc + (cache0 + c0) * 64;
+  half_t* Kb = a.kc + (cache0 + c0) * 64;
+  half_t* Vb = a.vc + (cache0 + c0) * 64;
   const int kl = tid >> 3, d8 = tid & 7;
   constexpr int NIT = kDecChunk / 32;
-  // Load order: this thread's q element first (the staging barrier waits
-  // for it alone), then every K row, then every V row, so the scores can be
-  // formed while the values are still arriving.  Unconditional loads
-  // (indices clamped; keys past n unused).
-  // (sched_barrier fences keep the scheduler from sinking the q load)
-  const half_t qv = a.q[(size_t)b * D + (kvh * G) * 64 + min(tid, G * 64 - 1)];
+  // Projections of this step from the QKV partials, one column pair per
+  // thread: q of the G heads (threads < 32 G) and, in the block whose split
+  // holds position pos, the new k (next 32) and v (next 32).  Sum in split
+  // order as the finish kernels do, RoPE on q and k.
+  const int pos = ctx - 1;
+  const bool own = pos - c0 < n;
+  const int KVD = a.NKV * 64, N1 = D + 2 * KVD;
+  int col = -1;
+  if (tid < G * 32) col = kvh * G * 64 + 2 * tid;
+  else if (own && tid < G * 32 + 32) col = D + kvh * 64 + 2 * (tid - G * 32);
+  else if (own && tid < G * 32 + 64) col = D + KVD + kvh * 64 + 2 * (tid - G * 32 - 32);
+  const bool rot = col >= 0 && col < D + KVD;
+  // Load order: the partials and RoPE factors first (the staging barrier
+  // waits for them alone), then every K row, then every V row, so the
+  // scores can be formed while the values are still arriving.
+  // Unconditional loads (indices clamped; keys past n unused); sched_barrier
+  // fences keep the scheduler from reordering the groups.
+  const int cc = col < 0 ? 0 : col;
+  const float* pp = a.qkv_part + (size_t)b * N1 + cc;
+  float pe[kMaxSplits], po[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; s++) {
+    const size_t o = (size_t)min(s, a.qkv_ks - 1) * kDecRows * N1;
+    pe[s] = pp[o];
+    po[s] = pp[o + 1];
+  }
+  const int ri = (cc & 63) >> 1;
+  const float cs = a.rope_cos[pos * 32 + ri], sn = a.rope_sin[pos * 32 + ri];
   __builtin_amdgcn_sched_barrier(0);
   half8 kk[NIT], kv[NIT];
 #pragma unroll
@@ -395,8 +385,42 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
 #pragma unroll
   for (int it = 0; it < NIT; it++) kv[it] = ld_h8(Vb + (size_t)min(kl + 32 * it, n - 1) * 64 + d8 * 8);
   __builtin_amdgcn_sched_barrier(0);
-  if (tid < G * 64) qs[tid >> 6][tid & 63] = qv;
+  if (col >= 0) {
+    float e = 0.f, o = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMaxSplits; s++) {
+      e += s < a.qkv_ks ? pe[s] : 0.f;
+      o += s < a.qkv_ks ? po[s] : 0.f;
+    }
+    if (rot) {
+      const float e2 = e * cs - o * sn, o2 = o * cs + e * sn;
+      e = e2;
+      o = o2;
+    }
+    half2v w;
+    w[0] = (half_t)e;
+    w[1] = (half_t)o;
+    if (tid < G * 32) {
+      *reinterpret_cast<half2v*>(&qs[tid >> 5][2 * (tid & 31)]) = w;
+    } else {
+      const bool isk = tid < G * 32 + 32;
+      const int d = 2 * ((tid - G * 32) & 31);
+      *reinterpret_cast<half2v*>((isk ? knew : vnew) + d) = w;
+      *reinterpret_cast<half2v*>((isk ? Kb : Vb) + (size_t)(pos - c0) * 64 + d) = w;  // cache row pos
+    }
+  }
   __syncthreads();
+  // the lanes holding row pos take the new k / v (the row they read is stale)
+  if (own && kl == ((pos - c0) & 31)) {
+    const int itp = (pos - c0) >> 5;
+    const half8 kn = ld_h8(knew + d8 * 8), vn = ld_h8(vnew + d8 * 8);
+#pragma unroll
+    for (int it = 0; it < NIT; it++)
+      if (it == itp) {
+        kk[it] = kn;
+        kv[it] = vn;
+      }
+  }
   // this lane's 8 dims of each head as fp16 pairs (fp16 products exact in fp32)
   half2v qr[G][4];
 #pragma unroll
@@ -744,15 +768,6 @@ hipError_t skinny_finish_resid_norm(const float* part, int N, int K, float* x, h
                                     hipStream_t s) {
   if (N > 1024 || nb < 1 || nb > kDecRows) return hipErrorInvalidValue;
   hipLaunchKernelGGL(finish_resid_norm_kernel, dim3(nb), dim3(256), 0, s, part, skinny_splits(N, K), x, xn, g, N);
-  return hipGetLastError();
-}
-
-hipError_t skinny_finish_qkv(const float* part, int K, const int* ctr, const float* rope_cos, const float* rope_sin,
-                             half_t* q, half_t* kc, half_t* vc, int NH, int NKV, int max_ctx, int nb, hipStream_t s) {
-  if (nb < 1 || nb > kDecRows) return hipErrorInvalidValue;
-  const int N1 = (NH + 2 * NKV) * 64;
-  hipLaunchKernelGGL(finish_qkv_kernel, dim3(nb), dim3(256), 0, s, part, skinny_splits(N1, K), ctr, rope_cos,
-                     rope_sin, q, kc, vc, NH, NKV, max_ctx);
   return hipGetLastError();
 }
 

@@ -79,7 +79,7 @@ struct ane_decoder {
   half_t *kc = nullptr, *vc = nullptr;
   float *rope_cos = nullptr, *rope_sin = nullptr;
   float* x = nullptr;
-  half_t *xn = nullptr, *q = nullptr, *att = nullptr, *gate = nullptr;
+  half_t *xn = nullptr, *att = nullptr, *gate = nullptr;
   float* apart = nullptr;
   float* kpart = nullptr;  // split-K partials of the decode-step GEMMs
   size_t kpart_cap = 0;
@@ -212,7 +212,6 @@ int open_impl(ane_decoder* d) {
   const int R = kDecRows;
   DCHK(op, dalloc(d, &d->x, (size_t)R * D));
   DCHK(op, dalloc(d, &d->xn, (size_t)R * D));
-  DCHK(op, dalloc(d, &d->q, (size_t)R * D));
   DCHK(op, dalloc(d, &d->att, (size_t)R * D));
   DCHK(op, dalloc(d, &d->gate, (size_t)R * H));
   d->nsplit = (C + kDecChunk - 1) / kDecChunk;
@@ -245,7 +244,6 @@ int open_impl(ane_decoder* d) {
   DCHK(op, hipMemset(d->att, 0, (size_t)R * D * 2));
   DCHK(op, hipMemset(d->gate, 0, (size_t)R * H * 2));
   DCHK(op, hipMemset(d->x, 0, (size_t)R * D * 4));
-  DCHK(op, hipMemset(d->q, 0, (size_t)R * D * 2));
   DCHK(op, hipMemset(d->tok_d, 0, (size_t)R * 2));
   DCHK(op, hipMemset(d->ctr_d, 0, 8));
   DCHK(op, hipDeviceSynchronize());
@@ -270,12 +268,12 @@ int enqueue_step(ane_decoder* d, float* logits, uint16_t* hist) {
     half_t* kcl = d->kc + (size_t)l * d->B * d->NKV * d->C * 64;
     half_t* vcl = d->vc + (size_t)l * d->B * d->NKV * d->C * 64;
     // each GEMM: split-K partials from (N/32) x ks one-wave blocks, then a
-    // per-row finish that sums the splits and applies the epilogue
+    // per-row finish that sums the splits and applies the epilogue (the QKV
+    // partials are finished by the attention kernel)
     DCHK(op, skinny_partials(d->xn, d->fwqkv + (size_t)l * N1 * D, d->kpart, d->kpart_cap, N1, D, st));
-    DCHK(op, skinny_finish_qkv(d->kpart, D, d->ctr_d, d->rope_cos, d->rope_sin, d->q, kcl, vcl, d->NH, d->NKV, d->C,
-                               nb, st));
     DecAttnArgs aa;
-    aa.q = d->q; aa.kc = kcl; aa.vc = vcl; aa.ctr = d->ctr_d; aa.part = d->apart; aa.att = d->att; aa.nb = nb;
+    aa.qkv_part = d->kpart; aa.qkv_ks = skinny_splits(N1, D); aa.rope_cos = d->rope_cos; aa.rope_sin = d->rope_sin;
+    aa.kc = kcl; aa.vc = vcl; aa.ctr = d->ctr_d; aa.part = d->apart; aa.att = d->att; aa.nb = nb;
     aa.NH = d->NH; aa.NKV = d->NKV; aa.max_ctx = d->C; aa.nsplit = d->nsplit; aa.scale = 0.125f;
     DCHK(op, dec_attention(aa, st));
     DCHK(op, skinny_partials(d->att, d->fwo + (size_t)l * D * D, d->kpart, d->kpart_cap, D, D, st));
