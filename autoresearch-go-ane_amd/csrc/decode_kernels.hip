@@ -293,8 +293,8 @@ __global__ __launch_bounds__(256) void finish_resid_norm_kernel(const float* par
 // W1|W3 finish: gate[t][j] = silu(h1) * h3 with W1 / W3 rows interleaved by
 // 32 (h1 at column (j/32)*64 + j%32, h3 at +32), fragment layout.
 __global__ __launch_bounds__(256) void finish_swiglu_kernel(const float* part, int ks, half_t* gate, int H) {
-  const int t = blockIdx.x;
-  for (int j = threadIdx.x; j < H; j += blockDim.x) {
+  const int t = blockIdx.x;  // blockIdx.y: a 256-column slice of the row
+  for (int j = blockIdx.y * 256 + threadIdx.x; j < min(H, (int)(blockIdx.y + 1) * 256); j += blockDim.x) {
     const int c1 = (j >> 5) * 64 + (j & 31);
     const float h1 = split_sum(part, ks, 2 * H, t, c1), h3 = split_sum(part, ks, 2 * H, t, c1 + 32);
     gate[act_frag_off(t, j)] = (half_t)(h1 / (1.0f + __expf(-h1)) * h3);
@@ -773,7 +773,8 @@ hipError_t skinny_finish_resid_norm(const float* part, int N, int K, float* x, h
 
 hipError_t skinny_finish_swiglu(const float* part, int N, int K, half_t* gate, int nb, hipStream_t s) {
   if (N % 64 || nb < 1 || nb > kDecRows) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(finish_swiglu_kernel, dim3(nb), dim3(256), 0, s, part, skinny_splits(N, K), gate, N / 2);
+  hipLaunchKernelGGL(finish_swiglu_kernel, dim3(nb, (N / 2 + 255) / 256), dim3(256), 0, s, part, skinny_splits(N, K),
+                     gate, N / 2);
   return hipGetLastError();
 }
 
