@@ -99,6 +99,11 @@ class Decoder:
         self._live()
         return int(self._lib.ane_decode_position(self._h))
 
+    def DebugFillCache(self, byte: int = 0xFF):
+        """Test-only: every byte of the KV cache set to `byte` (0xFF: NaN)."""
+        self._live()
+        self._check(self._lib.ane_decode_debug_fill_cache(self._h, int(byte)))
+
     def LastMs(self) -> float:
         self._live()
         return float(self._lib.ane_decode_last_ms(self._h))

@@ -410,13 +410,16 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
     }
   }
   __syncthreads();
-  // the lanes holding row pos take the new k / v (the row they read is stale)
-  if (own && kl == ((pos - c0) & 31)) {
-    const int itp = (pos - c0) >> 5;
+  // Row pos is the last row of its split (pos - c0 = n - 1), and every
+  // lane whose key index is >= n read it too (clamped): all of them take the
+  // new k / v, because the row they read is stale -- in a fresh cache it may
+  // hold any bit pattern, and a NaN there would survive the zero
+  // probability those lanes carry into P.V.
+  if (own) {
     const half8 kn = ld_h8(knew + d8 * 8), vn = ld_h8(vnew + d8 * 8);
 #pragma unroll
     for (int it = 0; it < NIT; it++)
-      if (it == itp) {
+      if (kl + 32 * it >= pos - c0) {
         kk[it] = kn;
         kv[it] = vn;
       }

@@ -492,3 +492,14 @@ extern "C" int ane_decode_generate(ane_decoder* d, int32_t nsteps, uint16_t* out
 extern "C" int32_t ane_decode_position(ane_decoder* d) { return d ? d->pos : -1; }
 
 extern "C" double ane_decode_last_ms(ane_decoder* d) { return d ? d->last_ms : 0.0; }
+
+extern "C" int ane_decode_debug_fill_cache(ane_decoder* d, int byte) {
+  const char* op = "debug fill cache";
+  if (!d || !d->stream) return ANE_ERR_STATE;
+  const size_t bytes = (size_t)d->L * d->B * d->NKV * d->C * 64 * sizeof(half_t);
+  DCHK(op, hipSetDevice(d->cfg.device));
+  DCHK(op, hipMemsetAsync(d->kc, byte & 0xff, bytes, d->stream));
+  DCHK(op, hipMemsetAsync(d->vc, byte & 0xff, bytes, d->stream));
+  DCHK(op, hipStreamSynchronize(d->stream));
+  return ANE_OK;
+}

@@ -287,6 +287,10 @@ int ane_decode_generate(ane_decoder *d, int32_t nsteps, uint16_t *out_tok);
 int32_t ane_decode_position(ane_decoder *d);
 /* device time of the last ane_decode_generate call (ms, HIP events) */
 double ane_decode_last_ms(ane_decoder *d);
+/* Test-only (no reference counterpart): fills every byte of the KV cache
+ * with `byte` (0xFF: fp16 NaN everywhere), so a test can show that no
+ * position is read before it is written. */
+int ane_decode_debug_fill_cache(ane_decoder *d, int byte);
 
 /* ---- mixture-of-experts SwiGLU FFN layer ----------------------------------
  * No counterpart in the reference (its FFN is dense, ane/common.go:91-105

@@ -80,6 +80,29 @@ def test_query_head_groups(heads, kv_heads):
     assert max(errs) <= TOL
 
 
+@pytest.mark.parametrize("plen,max_ctx", [(64, 128), (256, 512)])
+def test_cache_positions_never_read_before_written(plen, max_ctx):
+    """The KV cache starts as NaN bit patterns: prefill, every decode step
+    (whose new k/v row is formed and used inside the attention kernel) and
+    the key splits past the context must never let a stale row reach the
+    logits -- a NaN anywhere would show."""
+    cfg = ane.tiny_decode()
+    nseq, nsteps = 2, 3
+    p, prefix = _setup(cfg, nseq, plen, 71)
+    forced = np.random.default_rng(72).integers(0, cfg.vocab, (nseq, nsteps)).astype(np.uint16)
+    ref_tok, ref_lg = oracle.decode(cfg, p, prefix, nsteps, forced=forced, want_logits=True)
+    dec = ane.Decoder(cfg, p, max_batch=2, max_ctx=max_ctx)
+    try:
+        dec.DebugFillCache(0xFF)
+        _, lg0 = dec.Prefill(prefix, want_logits=True)
+        lgs = [lg0] + [dec.Step(forced[:, i], want_logits=True)[1] for i in range(nsteps)]
+    finally:
+        dec.Close()
+    lg = np.stack(lgs, 1)
+    assert np.isfinite(lg).all()
+    assert np.abs(lg - ref_lg).max() <= TOL
+
+
 def test_long_prefix_multi_chunk_attention():
     """1024-token prefix: prefill attention streams 8 key chunks, decode
     attention merges 5 context splits (max_ctx 1152)."""
