@@ -10,6 +10,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 #include <time.h>
 
@@ -185,6 +186,7 @@ static void free_all(ane_engine* e) {
   e->shadow_jobs = nullptr;
   e->n_shadow_jobs = e->n_shadow_tiles = 0;
   e->shadow_jobs_t = false;
+  drop_fwd_graph(e);
   if (e->stream) (void)hipStreamDestroy(e->stream);
   e->stream = nullptr;
 }
@@ -328,6 +330,7 @@ extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_e
   if (opts) e->opt = *opts;
   apply_option_defaults(&e->opt);
   e->device = e->opt.device;
+  if (const char* g = getenv("ANE_GRAPHS")) e->use_graph = atoi(g) != 0;
   e->lr = e->opt.lr;
   int rc = validate_cfg(e, e->cfg);
   if (rc == ANE_OK) rc = open_impl(e);
@@ -605,6 +608,46 @@ int head_loss(ane_engine* e, int nseq, float* colscale, float dscale) {
   return ANE_OK;
 }
 
+void drop_fwd_graph(ane_engine* e) {
+  if (e->fwd_exec) (void)hipGraphExecDestroy(e->fwd_exec);
+  e->fwd_exec = nullptr;
+  e->fwd_graph_nseq = 0;
+}
+
+// Eval forward + classifier loss of nseq sequences whose tokens and targets
+// are already in e->tok / e->tgt.  The ~90 launches of one call are captured
+// once per batch size and replayed as a graph, which removes their host-side
+// launch cost and the gaps it leaves between dependent kernels.  Profiling
+// (events between the kernels) runs eagerly.
+static int fwd_loss(ane_engine* e, int nseq) {
+  const char* op = "eval loss";
+  if (!e->use_graph || e->prof_on) {
+    int rc = forward_body(e, nseq, 0);
+    if (!rc) rc = head_loss(e, nseq, nullptr, 0.f);
+    return rc;
+  }
+  if (!e->fwd_exec || e->fwd_graph_nseq != nseq) {
+    drop_fwd_graph(e);
+    HIPCHK(op, hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    int rc = forward_body(e, nseq, 0);
+    if (!rc) rc = head_loss(e, nseq, nullptr, 0.f);
+    hipGraph_t g = nullptr;
+    const hipError_t h = hipStreamEndCapture(e->stream, &g);  // always leaves capture mode
+    if (rc) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    HIPCHK(op, h);
+    const hipError_t hi = hipGraphInstantiate(&e->fwd_exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (hi != hipSuccess) e->fwd_exec = nullptr;
+    HIPCHK(op, hi);
+    e->fwd_graph_nseq = nseq;
+  }
+  HIPCHK(op, hipGraphLaunch(e->fwd_exec, e->stream));
+  return ANE_OK;
+}
+
 static int finish_loss(ane_engine* e, int nseq, float* loss_per_seq, float* mean_loss) {
   const char* op = "eval loss";
   std::vector<float> ls(nseq);
@@ -627,8 +670,7 @@ extern "C" int ane_eval_loss(ane_engine* e, const uint16_t* tokens, const uint16
   const size_t T = (size_t)nseq * e->cfg.seq;
   HIPCHK("eval loss", hipMemcpyAsync(e->tok, tokens, T * 2, hipMemcpyHostToDevice, e->stream));
   HIPCHK("eval loss", hipMemcpyAsync(e->tgt, targets, T * 2, hipMemcpyHostToDevice, e->stream));
-  int rc = forward_body(e, nseq, 0);
-  if (!rc) rc = head_loss(e, nseq, nullptr, 0.f);
+  int rc = fwd_loss(e, nseq);
   if (!rc) rc = finish_loss(e, nseq, loss_per_seq, mean_loss);
   return rc;
 }
@@ -652,8 +694,7 @@ extern "C" int ane_eval_loss_windows(ane_engine* e, const uint64_t* positions, i
   if (nseq <= 0 || nseq > e->opt.max_batch || !positions)
     return eng_fail(e, ANE_ERR_ARG, "storiesane eval loss: nseq=%d must be in [1, %d]", nseq, e->opt.max_batch);
   int rc = load_windows(e, positions, nseq);
-  if (!rc) rc = forward_body(e, nseq, 0);
-  if (!rc) rc = head_loss(e, nseq, nullptr, 0.f);
+  if (!rc) rc = fwd_loss(e, nseq);
   if (!rc) rc = finish_loss(e, nseq, loss_per_seq, mean_loss);
   return rc;
 }

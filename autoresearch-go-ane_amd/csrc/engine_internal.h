@@ -161,6 +161,12 @@ struct ane_engine {
   hipEvent_t step_ev[4] = {nullptr, nullptr, nullptr, nullptr};  // step start, head start/end, adam start
   bool flushed = false;
 
+  // eval forward + loss replayed as one HIP graph per batch size (the
+  // kernels read only buffers fixed at open; ANE_GRAPHS=0 runs them eagerly)
+  bool use_graph = true;
+  hipGraphExec_t fwd_exec = nullptr;
+  int fwd_graph_nseq = 0;
+
   // profiling
   bool prof_on = false;
   std::vector<ProfEvent> prof_events;
@@ -188,6 +194,7 @@ hipError_t eng_gemm(ane_engine* e, int cls, const ane::half_t* A, int lda, bool 
                     bool bt, int M, int N, int K, int epi, const ane::EpiParams& p, int bm = 0, int bn = 0);
 int refresh_shadows(ane_engine* e);
 int forward_body(ane_engine* e, int nseq, int train);
+void drop_fwd_graph(ane_engine* e);
 template <class T>
 hipError_t dalloc(ane_engine* e, T** p, size_t n) {
   void* q = nullptr;

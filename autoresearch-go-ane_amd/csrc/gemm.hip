@@ -730,7 +730,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
       if (dma_on) {
 #pragma unroll
         for (int d = 0; d < ND; d++)
-          if (d * NMF / ND == p) {
+          if (d * NMF / (ND > 0 ? ND : 1) == p) {
             if constexpr (DMA == 1) dma_a(d, dkt, dst);
             if constexpr (DMA == 2) dma_b(d, dkt, dst);
           }

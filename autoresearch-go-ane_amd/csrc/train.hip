@@ -41,6 +41,7 @@ double now_s() {
 
 int ensure_train(ane_engine* e, const char* op) {
   if (e->train_ready) return ANE_OK;
+  drop_fwd_graph(e);  // eng_gemm may pick other shapes once the split-K workspace exists
   const ane_model_cfg& c = e->cfg;
   const bool llama = c.arch == ANE_ARCH_LLAMA2;
   const size_t D = c.dim, H = c.hidden, V = c.vocab, NH = c.heads;

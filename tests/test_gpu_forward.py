@@ -131,3 +131,43 @@ def test_params_round_trip_and_profile():
     assert prof["attention"]["launches"] == cfg.layers
     assert prof["classifier_gemm"]["ms"] > 0
     eng.Destroy()
+
+
+def test_graph_replay_matches_eager(monkeypatch):
+    """Eval loss replays a captured graph per batch size.  Every replay must
+    equal the same engine run eagerly (ANE_GRAPHS=0), bit for bit, across
+    changing windows, batch sizes, new parameters, eager work in between
+    (EvalLogits, a training step that allocates its buffers) and profiling."""
+    cfg = ane.tiny("llama2", layers=4)
+    p = ane.init_params(cfg, seed=11, std=0.08)
+    stream = np.random.default_rng(12).integers(0, cfg.vocab, 6000).astype(np.uint16)
+    eng_g = open_engine(cfg, p, max_batch=4, tokens=stream)
+    monkeypatch.setenv("ANE_GRAPHS", "0")
+    eng_e = open_engine(cfg, p, max_batch=4, tokens=stream)
+    monkeypatch.delenv("ANE_GRAPHS")
+    rng = np.random.default_rng(13)
+
+    def check(nseq):
+        pos = rng.integers(0, 6000 - cfg.seq - 1, nseq).astype(np.uint64)
+        mg, pg = eng_g.EvalLossWindows(pos)
+        me, pe = eng_e.EvalLossWindows(pos)
+        np.testing.assert_array_equal(pg, pe)
+        assert mg == me
+
+    for nseq in (4, 4, 2, 4, 1):
+        check(nseq)
+        eng_g.EvalLogits(stream[:cfg.seq])
+    p2 = ane.init_params(cfg, seed=14, std=0.08)
+    eng_g.SetParams(p2)
+    eng_e.SetParams(p2)
+    check(4)
+    eng_g.Step()  # training buffers, split-K workspace, new weights
+    eng_e.SetParams(eng_g.Params())
+    for nseq in (4, 3, 3):
+        check(nseq)
+    eng_g.ProfileEnable(True)
+    check(2)
+    eng_g.ProfileEnable(False)
+    check(2)
+    eng_g.Destroy()
+    eng_e.Destroy()
