@@ -328,8 +328,8 @@ __device__ __forceinline__ int dec_chunk(int ctx, int nsplit) {
   return ((ctx + nsplit - 1) / nsplit + 31) & ~31;
 }
 
-template <int G>
-__global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
+template <int G, int QS>
+__device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int D = a.NH * 64;
@@ -368,9 +368,9 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
   // fences keep the scheduler from reordering the groups.
   const int cc = col < 0 ? 0 : col;
   const float* pp = a.qkv_part + (size_t)b * N1 + cc;
-  float pe[kMaxSplits], po[kMaxSplits];
+  float pe[QS], po[QS];  // QS >= qkv_ks: 8 keeps the kernel at 5 blocks per CU
 #pragma unroll
-  for (int s = 0; s < kMaxSplits; s++) {
+  for (int s = 0; s < QS; s++) {
     const size_t o = (size_t)min(s, a.qkv_ks - 1) * kDecRows * N1;
     pe[s] = pp[o];
     po[s] = pp[o + 1];
@@ -388,7 +388,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
   if (col >= 0) {
     float e = 0.f, o = 0.f;
 #pragma unroll
-    for (int s = 0; s < kMaxSplits; s++) {
+    for (int s = 0; s < QS; s++) {
       e += s < a.qkv_ks ? pe[s] : 0.f;
       o += s < a.qkv_ks ? po[s] : 0.f;
     }
@@ -509,6 +509,17 @@ __global__ __launch_bounds__(256) void dec_attn_kernel(DecAttnArgs a) {
     out[d] = o;
     if (d == 0) { out[64] = stat[h][0]; out[65] = stat[h][1]; }
   }
+}
+
+// QS = 8 fits 96 VGPRs: 5 blocks of 4 waves per CU, so the 64 x 4 x 5
+// blocks of the bench shape (1024-token prefix) are resident at once.
+template <int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void dec_attn_kernel8(DecAttnArgs a) {
+  dec_attn_body<G, 8>(a);
+}
+template <int G>
+__global__ __launch_bounds__(256) void dec_attn_kernel16(DecAttnArgs a) {
+  dec_attn_body<G, kMaxSplits>(a);
 }
 
 __global__ __launch_bounds__(64) void dec_combine_kernel(DecAttnArgs a) {
@@ -816,13 +827,19 @@ hipError_t dec_norm(const float* x, half_t* xn, const float* g, int nb, int D, h
 hipError_t dec_attention(const DecAttnArgs& a, hipStream_t s) {
   const int G = a.NH / a.NKV;
   if (a.NH % a.NKV || G > kGMax) return hipErrorInvalidValue;
+  if (a.qkv_ks < 1 || a.qkv_ks > kMaxSplits) return hipErrorInvalidValue;
   const dim3 grid(a.nb, a.NKV, a.nsplit);
+  const bool qs8 = a.qkv_ks <= 8;
+#define DEC_ATTN(G_)                                                                   \
+  if (qs8) hipLaunchKernelGGL((dec_attn_kernel8<G_>), grid, dim3(256), 0, s, a);        \
+  else hipLaunchKernelGGL((dec_attn_kernel16<G_>), grid, dim3(256), 0, s, a);
   switch (G) {
-    case 1: hipLaunchKernelGGL(dec_attn_kernel<1>, grid, dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(dec_attn_kernel<2>, grid, dim3(256), 0, s, a); break;
-    case 3: hipLaunchKernelGGL(dec_attn_kernel<3>, grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL(dec_attn_kernel<4>, grid, dim3(256), 0, s, a); break;
+    case 1: DEC_ATTN(1); break;
+    case 2: DEC_ATTN(2); break;
+    case 3: DEC_ATTN(3); break;
+    default: DEC_ATTN(4); break;
   }
+#undef DEC_ATTN
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(dec_combine_kernel, dim3(a.nb, a.NH), dim3(64), 0, s, a);
