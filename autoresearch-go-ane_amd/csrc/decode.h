@@ -17,6 +17,8 @@ namespace ane {
 
 constexpr int kDecRows = 64;    // token rows of a decode step (max sequences)
 constexpr int kDecChunk = 256;  // keys per decode-attention split
+constexpr int kDecWideChunk = 1152;   // keys per split of the 1024-thread form (9 passes of 128)
+constexpr int kDecWideMinBlocks = 192;  // batch x kv heads from which that form is chosen
 
 // MFMA-fragment-major layout of the decode-step operands.  A 32x32x16 MFMA
 // operand lane l takes row l%32 and eight k-values; with the k-slot map
@@ -98,8 +100,9 @@ struct DecAttnArgs {
   const int* ctr;
   float* part;       // [nb][NH][nsplit][66]
   half_t* att;       // [64][NH*64]
-  int nb, NH, NKV, max_ctx, nsplit;
+  int nb, NH, NKV, max_ctx, nsplit;  // nsplit: partial slots per head (max_ctx / kDecChunk)
   float scale;
+  int form = 0;  // 0: by batch size, 1: 1024-thread blocks, 2: 256-thread splits
 };
 hipError_t dec_attention(const DecAttnArgs& a, hipStream_t s);
 

@@ -322,14 +322,21 @@ __device__ __forceinline__ float sum8_dpp(float v) {
 }
 
 // Keys per split for ctx keys over nsplit splits: an even share rounded up
-// to 32 (<= kDecChunk, as nsplit covers max_ctx in kDecChunk-key chunks),
-// so no split is left with a short tail while the others run full.
+// to 32 (<= the kernel's chunk, as nsplit covers max_ctx in chunk-key
+// pieces), so no split is left with a short tail while the others run full.
 __device__ __forceinline__ int dec_chunk(int ctx, int nsplit) {
   return ((ctx + nsplit - 1) / nsplit + 31) & ~31;
 }
 
-template <int G, int QS>
+// One block of NT threads per (sequence, kv head, key split): KP = NT / 8
+// keys per pass, NIT passes, so a split holds at most KP * NIT keys.  With
+// DIRECT (one split covers the context) the block normalises and writes att
+// itself; otherwise it leaves (o, m, l) partials for dec_combine_kernel.
+template <int G, int QS, int NT, int NIT, bool DIRECT>
 __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
+  constexpr int KP = NT / 8, CH = KP * NIT;
+  // pv reduction: NR groups of threads each sum KP / NR key lanes per output
+  constexpr int NR = NT / (G * 64) < 8 ? NT / (G * 64) : 8;
   const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int D = a.NH * 64;
@@ -339,8 +346,9 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   if (c0 >= ctx) return;  // uniform over the block, before any barrier
   const int n = min(chunk, ctx - c0);
   __shared__ half_t qs[G][64];
-  __shared__ float sc[G][kDecChunk];
-  __shared__ __attribute__((aligned(16))) float pv[G][32][64];
+  __shared__ float sc[G][CH];
+  __shared__ __attribute__((aligned(16))) float pv[G][KP][64];
+  __shared__ float red[NR > 1 ? NR : 1][G * 64];
   __shared__ float stat[G][2];
   __shared__ __attribute__((aligned(16))) half_t knew[64], vnew[64];
   const float sl2 = a.scale * kL2E;
@@ -348,7 +356,6 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   half_t* Kb = a.kc + (cache0 + c0) * 64;
   half_t* Vb = a.vc + (cache0 + c0) * 64;
   const int kl = tid >> 3, d8 = tid & 7;
-  constexpr int NIT = kDecChunk / 32;
   // Projections of this step from the QKV partials, one column pair per
   // thread: q of the G heads (threads < 32 G) and, in the block whose split
   // holds position pos, the new k (next 32) and v (next 32).  Sum in split
@@ -368,7 +375,7 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   // fences keep the scheduler from reordering the groups.
   const int cc = col < 0 ? 0 : col;
   const float* pp = a.qkv_part + (size_t)b * N1 + cc;
-  float pe[QS], po[QS];  // QS >= qkv_ks: 8 keeps the kernel at 5 blocks per CU
+  float pe[QS], po[QS];
 #pragma unroll
   for (int s = 0; s < QS; s++) {
     const size_t o = (size_t)min(s, a.qkv_ks - 1) * kDecRows * N1;
@@ -380,10 +387,10 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   __builtin_amdgcn_sched_barrier(0);
   half8 kk[NIT], kv[NIT];
 #pragma unroll
-  for (int it = 0; it < NIT; it++) kk[it] = ld_h8(Kb + (size_t)min(kl + 32 * it, n - 1) * 64 + d8 * 8);
+  for (int it = 0; it < NIT; it++) kk[it] = ld_h8(Kb + (size_t)min(kl + KP * it, n - 1) * 64 + d8 * 8);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int it = 0; it < NIT; it++) kv[it] = ld_h8(Vb + (size_t)min(kl + 32 * it, n - 1) * 64 + d8 * 8);
+  for (int it = 0; it < NIT; it++) kv[it] = ld_h8(Vb + (size_t)min(kl + KP * it, n - 1) * 64 + d8 * 8);
   __builtin_amdgcn_sched_barrier(0);
   if (col >= 0) {
     float e = 0.f, o = 0.f;
@@ -419,7 +426,7 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
     const half8 kn = ld_h8(knew + d8 * 8), vn = ld_h8(vnew + d8 * 8);
 #pragma unroll
     for (int it = 0; it < NIT; it++)
-      if (kl + 32 * it >= pos - c0) {
+      if (kl + KP * it >= pos - c0) {
         kk[it] = kn;
         kv[it] = vn;
       }
@@ -435,7 +442,7 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
     }
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
-    const int j = kl + 32 * it;
+    const int j = kl + KP * it;
 #pragma unroll
     for (int h = 0; h < G; h++) {
       float s = 0.f;
@@ -468,7 +475,7 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   }
   __syncthreads();
   // P.V over this thread's key pairs (it, it + 1): v_dot2 of (p_it, p_it+1)
-  // with (v_it[i], v_it+1[i]); keys past n have p = 0
+  // with (v_it[i], v_it+1[i]); keys past n (and a missing last pass) have p = 0
   float acc[G][8];
 #pragma unroll
   for (int h = 0; h < G; h++)
@@ -476,23 +483,25 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
     for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
 #pragma unroll
   for (int it = 0; it < NIT; it += 2) {
-    const int j0 = kl + 32 * it, j1 = j0 + 32;
+    const bool pair = it + 1 < NIT;
+    const int j0 = kl + KP * it, j1 = j0 + KP;
     half2v vp[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       vp[i][0] = kv[it][i];
-      vp[i][1] = kv[it + 1][i];
+      vp[i][1] = pair ? kv[pair ? it + 1 : it][i] : (half_t)0.f;
     }
 #pragma unroll
     for (int h = 0; h < G; h++) {
       half2v pp;
       pp[0] = (half_t)(j0 < n ? sc[h][j0] : 0.f);
-      pp[1] = (half_t)(j1 < n ? sc[h][j1] : 0.f);
+      pp[1] = (half_t)(pair && j1 < n ? sc[h][j1] : 0.f);
 #pragma unroll
       for (int i = 0; i < 8; i++) acc[h][i] = __builtin_amdgcn_fdot2(pp, vp[i], acc[h][i], false);
     }
   }
-  // sums over the 32 key lanes kl, through LDS
+  // sums over the KP key lanes kl, through LDS: NR groups of G*64 threads
+  // each add KP / NR lanes, then the groups' sums are added in order
 #pragma unroll
   for (int h = 0; h < G; h++) {
     float4* dst = reinterpret_cast<float4*>(&pv[h][kl][d8 * 8]);
@@ -500,26 +509,47 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
     dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
   }
   __syncthreads();
+  constexpr int KPR = (KP + NR - 1) / NR;
+  if (tid < NR * G * 64) {
+    const int r = tid / (G * 64), hd = tid % (G * 64), h = hd >> 6, d = hd & 63;
+    float o = 0.f;
+#pragma unroll 8
+    for (int k = r * KPR; k < min(KP, (r + 1) * KPR); k++) o += pv[h][k][d];
+    if constexpr (NR > 1) red[r][hd] = o;
+    else red[0][hd] = o;
+  }
+  __syncthreads();
   if (tid < G * 64) {
     const int h = tid >> 6, d = tid & 63;
     float o = 0.f;
 #pragma unroll
-    for (int k = 0; k < 32; k++) o += pv[h][k][d];
-    float* out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nsplit + sp) * 66;
-    out[d] = o;
-    if (d == 0) { out[64] = stat[h][0]; out[65] = stat[h][1]; }
+    for (int r = 0; r < NR; r++) o += red[r][tid];
+    if constexpr (DIRECT) {
+      a.att[act_frag_off(b, (kvh * G + h) * 64 + d)] = (half_t)(o / stat[h][1]);
+    } else {
+      float* out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nsplit + sp) * 66;
+      out[d] = o;
+      if (d == 0) { out[64] = stat[h][0]; out[65] = stat[h][1]; }
+    }
   }
 }
 
-// QS = 8 fits 96 VGPRs: 5 blocks of 4 waves per CU, so the 64 x 4 x 5
-// blocks of the bench shape (1024-token prefix) are resident at once.
+// Narrow form: 256 threads, 8 passes of 32 keys = kDecChunk keys per split,
+// QS = 8 fits 96 VGPRs (5 blocks of 4 waves per CU).
 template <int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void dec_attn_kernel8(DecAttnArgs a) {
-  dec_attn_body<G, 8>(a);
+  dec_attn_body<G, 8, 256, kDecChunk / 32, false>(a);
 }
 template <int G>
 __global__ __launch_bounds__(256) void dec_attn_kernel16(DecAttnArgs a) {
-  dec_attn_body<G, kMaxSplits>(a);
+  dec_attn_body<G, kMaxSplits, 256, kDecChunk / 32, false>(a);
+}
+// Wide form: one 1024-thread block (one per CU) per (sequence, kv head)
+// holds up to kDecWideChunk keys with every K / V load in flight at once;
+// used when the batch alone gives enough blocks to fill the chip.
+template <int G, bool DIRECT>
+__global__ __launch_bounds__(1024) void dec_attn_wide_kernel(DecAttnArgs a) {
+  dec_attn_body<G, 8, 1024, kDecWideChunk / 128, DIRECT>(a);
 }
 
 __global__ __launch_bounds__(64) void dec_combine_kernel(DecAttnArgs a) {
@@ -828,8 +858,31 @@ hipError_t dec_attention(const DecAttnArgs& a, hipStream_t s) {
   const int G = a.NH / a.NKV;
   if (a.NH % a.NKV || G > kGMax) return hipErrorInvalidValue;
   if (a.qkv_ks < 1 || a.qkv_ks > kMaxSplits) return hipErrorInvalidValue;
-  const dim3 grid(a.nb, a.NKV, a.nsplit);
   const bool qs8 = a.qkv_ks <= 8;
+  // wide form: enough (sequence, kv head) blocks to fill the chip, or forced
+  const int wsplit = (a.max_ctx + kDecWideChunk - 1) / kDecWideChunk;
+  const bool wide = qs8 && wsplit <= a.nsplit &&
+                    (a.form == 1 || (a.form == 0 && a.nb * a.NKV >= kDecWideMinBlocks));
+  if (wide) {
+    DecAttnArgs w = a;
+    w.nsplit = wsplit;
+    const dim3 gw(a.nb, a.NKV, wsplit);
+#define DEC_WIDE(G_)                                                                        \
+  if (wsplit == 1) hipLaunchKernelGGL((dec_attn_wide_kernel<G_, true>), gw, dim3(1024), 0, s, w); \
+  else hipLaunchKernelGGL((dec_attn_wide_kernel<G_, false>), gw, dim3(1024), 0, s, w);
+    switch (G) {
+      case 1: DEC_WIDE(1); break;
+      case 2: DEC_WIDE(2); break;
+      case 3: DEC_WIDE(3); break;
+      default: DEC_WIDE(4); break;
+    }
+#undef DEC_WIDE
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || wsplit == 1) return e;
+    hipLaunchKernelGGL(dec_combine_kernel, dim3(a.nb, a.NH), dim3(64), 0, s, w);
+    return hipGetLastError();
+  }
+  const dim3 grid(a.nb, a.NKV, a.nsplit);
 #define DEC_ATTN(G_)                                                                   \
   if (qs8) hipLaunchKernelGGL((dec_attn_kernel8<G_>), grid, dim3(256), 0, s, a);        \
   else hipLaunchKernelGGL((dec_attn_kernel16<G_>), grid, dim3(256), 0, s, a);

@@ -16,6 +16,7 @@
 //   prefill chunk (<= 8192 tokens): px fp32, pxn/pqkv/patt/pgate fp16
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <cmath>
@@ -84,6 +85,7 @@ struct ane_decoder {
   float* kpart = nullptr;  // split-K partials of the decode-step GEMMs
   size_t kpart_cap = 0;
   int nsplit = 0;
+  int attn_form = 0;  // decode attention form: 0 by batch size; ANE_DEC_ATTN=wide (1) / split (2)
   float2* amax = nullptr;
   float* logits_d = nullptr;
   uint16_t *tok_d = nullptr, *hist_d = nullptr, *prefix_d = nullptr;
@@ -215,6 +217,7 @@ int open_impl(ane_decoder* d) {
   DCHK(op, dalloc(d, &d->att, (size_t)R * D));
   DCHK(op, dalloc(d, &d->gate, (size_t)R * H));
   d->nsplit = (C + kDecChunk - 1) / kDecChunk;
+  if (const char* f = getenv("ANE_DEC_ATTN")) d->attn_form = !strcmp(f, "wide") ? 1 : !strcmp(f, "split") ? 2 : 0;
   DCHK(op, dalloc(d, &d->apart, (size_t)B * d->NH * d->nsplit * 66));
   {
     const int NK[4][2] = {{N1, D}, {D, D}, {2 * H, D}, {D, H}};  // QKV, Wo, W1|W3, W2
@@ -275,6 +278,7 @@ int enqueue_step(ane_decoder* d, float* logits, uint16_t* hist) {
     aa.qkv_part = d->kpart; aa.qkv_ks = skinny_splits(N1, D); aa.rope_cos = d->rope_cos; aa.rope_sin = d->rope_sin;
     aa.kc = kcl; aa.vc = vcl; aa.ctr = d->ctr_d; aa.part = d->apart; aa.att = d->att; aa.nb = nb;
     aa.NH = d->NH; aa.NKV = d->NKV; aa.max_ctx = d->C; aa.nsplit = d->nsplit; aa.scale = 0.125f;
+    aa.form = d->attn_form;
     DCHK(op, dec_attention(aa, st));
     DCHK(op, skinny_partials(d->att, d->fwo + (size_t)l * D * D, d->kpart, d->kpart_cap, D, D, st));
     DCHK(op, skinny_finish_resid_norm(d->kpart, D, D, d->x, d->xn, d->P + o.g_ffn, nb, st));

@@ -80,12 +80,14 @@ def test_query_head_groups(heads, kv_heads):
     assert max(errs) <= TOL
 
 
+@pytest.mark.parametrize("form", ["split", "wide"])
 @pytest.mark.parametrize("plen,max_ctx", [(64, 128), (256, 512)])
-def test_cache_positions_never_read_before_written(plen, max_ctx):
+def test_cache_positions_never_read_before_written(plen, max_ctx, form, monkeypatch):
     """The KV cache starts as NaN bit patterns: prefill, every decode step
     (whose new k/v row is formed and used inside the attention kernel) and
     the key splits past the context must never let a stale row reach the
     logits -- a NaN anywhere would show."""
+    monkeypatch.setenv("ANE_DEC_ATTN", form)
     cfg = ane.tiny_decode()
     nseq, nsteps = 2, 3
     p, prefix = _setup(cfg, nseq, plen, 71)
@@ -103,15 +105,20 @@ def test_cache_positions_never_read_before_written(plen, max_ctx):
     assert np.abs(lg - ref_lg).max() <= TOL
 
 
-def test_long_prefix_multi_chunk_attention():
-    """1024-token prefix: prefill attention streams 8 key chunks, decode
-    attention merges 5 context splits (max_ctx 1152)."""
+@pytest.mark.parametrize("form", ["split", "wide"])
+@pytest.mark.parametrize("plen,max_ctx", [(1024, 1152), (1280, 2304)])
+def test_long_prefix_multi_chunk_attention(form, plen, max_ctx, monkeypatch):
+    """Long prefixes: prefill attention streams 8-10 key chunks.  Decode
+    attention in both forms: 256-thread blocks over 5 or 9 context splits,
+    and 1024-thread blocks holding up to 1152 keys (one split written
+    directly, or two merged; the bench batch picks this form by itself)."""
+    monkeypatch.setenv("ANE_DEC_ATTN", form)
     cfg = ane.tiny_decode(layers=1)
-    nseq, plen, nsteps = 2, 1024, 3
+    nseq, nsteps = 2, 3
     p, prefix = _setup(cfg, nseq, plen, 21)
     forced = np.random.default_rng(22).integers(0, cfg.vocab, (nseq, nsteps)).astype(np.uint16)
     ref_tok, ref_lg = oracle.decode(cfg, p, prefix, nsteps, forced=forced, want_logits=True)
-    dec = ane.Decoder(cfg, p, max_batch=2, max_ctx=1152)
+    dec = ane.Decoder(cfg, p, max_batch=2, max_ctx=max_ctx)
     try:
         _, lg0 = dec.Prefill(prefix, want_logits=True)
         errs = [np.abs(lg0 - ref_lg[:, 0]).max()]
@@ -149,9 +156,12 @@ def test_generate_graph_equals_eager_steps_and_oracle_choices():
     _check_choice(gen, ref_lg[:, 1:])
 
 
-def test_full_size_gqa_model_matches_oracle():
+@pytest.mark.parametrize("form", ["split", "wide"])
+def test_full_size_gqa_model_matches_oracle(form, monkeypatch):
     """The decode benchmark's model (12 layers, dim 768, 12/4 heads,
-    vocab 32000), two sequences, 64-token prefix, three forced steps."""
+    vocab 32000), two sequences, 64-token prefix, three forced steps, in
+    both decode-attention forms."""
+    monkeypatch.setenv("ANE_DEC_ATTN", form)
     cfg = ane.decode_gqa()
     nseq, plen, nsteps = 2, 64, 3
     p, prefix = _setup(cfg, nseq, plen, 4, std=0.02)
