@@ -321,6 +321,19 @@ __device__ __forceinline__ float sum8_dpp(float v) {
   return v;
 }
 
+// Over the 8 key groups of a wave (lanes l, l ^ 8, l ^ 16, l ^ 32 ...): each
+// 8-lane group holds one value in all its lanes; every lane gets the result.
+__device__ __forceinline__ float grp_max8(float v) {
+  v = fmaxf(v, dpp_f<0x128>(v));  // row_ror:8 -- the other group of the 16-lane row
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, xor32_f(v));
+}
+__device__ __forceinline__ float grp_sum8(float v) {
+  v += dpp_f<0x128>(v);
+  v += __shfl_xor(v, 16, 64);
+  return v + xor32_f(v);
+}
+
 // Keys per split for ctx keys over nsplit splits: an even share rounded up
 // to 32 (<= the kernel's chunk, as nsplit covers max_ctx in chunk-key
 // pieces), so no split is left with a short tail while the others run full.
@@ -334,7 +347,7 @@ __device__ __forceinline__ int dec_chunk(int ctx, int nsplit) {
 // itself; otherwise it leaves (o, m, l) partials for dec_combine_kernel.
 template <int G, int QS, int NT, int NIT, bool DIRECT>
 __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
-  constexpr int KP = NT / 8, CH = KP * NIT;
+  constexpr int KP = NT / 8;
   // pv reduction: NR groups of threads each sum KP / NR key lanes per output
   constexpr int NR = NT / (G * 64) < 8 ? NT / (G * 64) : 8;
   const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
@@ -346,10 +359,10 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   if (c0 >= ctx) return;  // uniform over the block, before any barrier
   const int n = min(chunk, ctx - c0);
   __shared__ half_t qs[G][64];
-  __shared__ float sc[G][CH];
+  constexpr int NW = NT / 64;
   __shared__ __attribute__((aligned(16))) float pv[G][KP][64];
-  __shared__ float red[NR > 1 ? NR : 1][G * 64];
-  __shared__ float stat[G][2];
+  __shared__ float red[NR][G * 64];
+  __shared__ float wred[G][NW];  // per-wave maxima, then per-wave sums
   __shared__ __attribute__((aligned(16))) half_t knew[64], vnew[64];
   const float sl2 = a.scale * kL2E;
   const size_t cache0 = ((size_t)b * a.NKV + kvh) * a.max_ctx;
@@ -440,6 +453,12 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
       qr[h][i][0] = qs[h][d8 * 8 + 2 * i];
       qr[h][i][1] = qs[h][d8 * 8 + 2 * i + 1];
     }
+  // Scores stay in registers (every lane of a key's 8-lane group holds the
+  // key's score); keys past n score -inf.  The block maximum per head comes
+  // from a cross-group wave max and one LDS pass over the waves.
+  float sreg[NIT][G], mx[G];
+#pragma unroll
+  for (int h = 0; h < G; h++) mx[h] = -INFINITY;
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
     const int j = kl + KP * it;
@@ -454,37 +473,37 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
         s = __builtin_amdgcn_fdot2(qr[h][i], kp, s, false);
       }
       s = sum8_dpp(s);
-      if (j < n && d8 == 0) sc[h][j] = s * sl2;
+      sreg[it][h] = j < n ? s * sl2 : -INFINITY;
+      mx[h] = fmaxf(mx[h], sreg[it][h]);
     }
   }
-  __syncthreads();
-  if (wave < G) {
-    float m = -INFINITY;
-    for (int j = lane; j < n; j += 64) m = fmaxf(m, sc[wave][j]);
-    m = wave_max(m);
-    float l = 0.f;
-    for (int j = lane; j < n; j += 64) {
-      // probabilities rounded to fp16 (they feed fp16 dot products below);
-      // the normaliser sums the same rounded values
-      const float p = (float)(half_t)__builtin_amdgcn_exp2f(sc[wave][j] - m);
-      sc[wave][j] = p;
-      l += p;
-    }
-    l = wave_sum(l);
-    if (lane == 0) { stat[wave][0] = m; stat[wave][1] = l; }
-  }
-  __syncthreads();
-  // P.V over this thread's key pairs (it, it + 1): v_dot2 of (p_it, p_it+1)
-  // with (v_it[i], v_it+1[i]); keys past n (and a missing last pass) have p = 0
-  float acc[G][8];
 #pragma unroll
-  for (int h = 0; h < G; h++)
+  for (int h = 0; h < G; h++) {
+    mx[h] = grp_max8(mx[h]);
+    if (lane == 0) wred[h][wave] = mx[h];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    float m = wred[h][0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) m = fmaxf(m, wred[h][w]);
+    mx[h] = m;
+  }
+  // P.V over this thread's key pairs (it, it + 1): v_dot2 of (p_it, p_it+1)
+  // with (v_it[i], v_it+1[i]).  Probabilities are rounded to fp16 (they feed
+  // fp16 dot products); the normaliser sums the same rounded values.  Keys
+  // past n (and a missing last pass) have p = 0.
+  float acc[G][8], ls[G];
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    ls[h] = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
+  }
 #pragma unroll
   for (int it = 0; it < NIT; it += 2) {
     const bool pair = it + 1 < NIT;
-    const int j0 = kl + KP * it, j1 = j0 + KP;
     half2v vp[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -494,50 +513,57 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
 #pragma unroll
     for (int h = 0; h < G; h++) {
       half2v pp;
-      pp[0] = (half_t)(j0 < n ? sc[h][j0] : 0.f);
-      pp[1] = (half_t)(pair && j1 < n ? sc[h][j1] : 0.f);
+      pp[0] = (half_t)__builtin_amdgcn_exp2f(sreg[it][h] - mx[h]);
+      pp[1] = pair ? (half_t)__builtin_amdgcn_exp2f(sreg[pair ? it + 1 : it][h] - mx[h]) : (half_t)0.f;
+      ls[h] += (float)pp[0] + (float)pp[1];
 #pragma unroll
       for (int i = 0; i < 8; i++) acc[h][i] = __builtin_amdgcn_fdot2(pp, vp[i], acc[h][i], false);
     }
   }
   // sums over the KP key lanes kl, through LDS: NR groups of G*64 threads
-  // each add KP / NR lanes, then the groups' sums are added in order
+  // each add KP / NR lanes, then the groups' sums are added in order; the
+  // normaliser by a cross-group wave sum and the per-wave sums
 #pragma unroll
   for (int h = 0; h < G; h++) {
     float4* dst = reinterpret_cast<float4*>(&pv[h][kl][d8 * 8]);
     dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
     dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+    ls[h] = grp_sum8(ls[h]);
   }
-  __syncthreads();
+  __syncthreads();  // wred (the maxima) fully read above: reuse it for the sums
+#pragma unroll
+  for (int h = 0; h < G; h++)
+    if (lane == 0) wred[h][wave] = ls[h];
   constexpr int KPR = (KP + NR - 1) / NR;
   if (tid < NR * G * 64) {
     const int r = tid / (G * 64), hd = tid % (G * 64), h = hd >> 6, d = hd & 63;
     float o = 0.f;
 #pragma unroll 8
     for (int k = r * KPR; k < min(KP, (r + 1) * KPR); k++) o += pv[h][k][d];
-    if constexpr (NR > 1) red[r][hd] = o;
-    else red[0][hd] = o;
+    red[r][hd] = o;
   }
   __syncthreads();
   if (tid < G * 64) {
     const int h = tid >> 6, d = tid & 63;
-    float o = 0.f;
+    float o = 0.f, l = 0.f;
 #pragma unroll
     for (int r = 0; r < NR; r++) o += red[r][tid];
+#pragma unroll
+    for (int w = 0; w < NW; w++) l += wred[h][w];
     if constexpr (DIRECT) {
-      a.att[act_frag_off(b, (kvh * G + h) * 64 + d)] = (half_t)(o / stat[h][1]);
+      a.att[act_frag_off(b, (kvh * G + h) * 64 + d)] = (half_t)(o / l);
     } else {
       float* out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nsplit + sp) * 66;
       out[d] = o;
-      if (d == 0) { out[64] = stat[h][0]; out[65] = stat[h][1]; }
+      if (d == 0) { out[64] = mx[h]; out[65] = l; }
     }
   }
 }
 
 // Narrow form: 256 threads, 8 passes of 32 keys = kDecChunk keys per split,
-// QS = 8 fits 96 VGPRs (5 blocks of 4 waves per CU).
+// QS = 8 fits 96 VGPRs (5 blocks of 4 waves per CU) for G < 4.
 template <int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 8))) void dec_attn_kernel8(DecAttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G < 4 ? 5 : 4, 8))) void dec_attn_kernel8(DecAttnArgs a) {
   dec_attn_body<G, 8, 256, kDecChunk / 32, false>(a);
 }
 template <int G>
