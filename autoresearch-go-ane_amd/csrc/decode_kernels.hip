@@ -434,15 +434,14 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   // lane whose key index is >= n read it too (clamped): all of them take the
   // new k / v, because the row they read is stale -- in a fresh cache it may
   // hold any bit pattern, and a NaN there would survive the zero
-  // probability those lanes carry into P.V.
+  // probability those lanes carry into P.V.  The substitution is a select
+  // at each use: writing into kk / kv here would first wait for every load
+  // still in flight into those registers.
+  const int jrep = own ? pos - c0 : 1 << 30;
+  half8 kn = {}, vn = {};
   if (own) {
-    const half8 kn = ld_h8(knew + d8 * 8), vn = ld_h8(vnew + d8 * 8);
-#pragma unroll
-    for (int it = 0; it < NIT; it++)
-      if (kl + KP * it >= pos - c0) {
-        kk[it] = kn;
-        kv[it] = vn;
-      }
+    kn = ld_h8(knew + d8 * 8);
+    vn = ld_h8(vnew + d8 * 8);
   }
   // this lane's 8 dims of each head as fp16 pairs (fp16 products exact in fp32)
   half2v qr[G][4];
@@ -462,14 +461,15 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
 #pragma unroll
   for (int it = 0; it < NIT; it++) {
     const int j = kl + KP * it;
+    const half8 kx = j >= jrep ? kn : kk[it];
 #pragma unroll
     for (int h = 0; h < G; h++) {
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         half2v kp;
-        kp[0] = kk[it][2 * i];
-        kp[1] = kk[it][2 * i + 1];
+        kp[0] = kx[2 * i];
+        kp[1] = kx[2 * i + 1];
         s = __builtin_amdgcn_fdot2(qr[h][i], kp, s, false);
       }
       s = sum8_dpp(s);
@@ -504,11 +504,14 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
 #pragma unroll
   for (int it = 0; it < NIT; it += 2) {
     const bool pair = it + 1 < NIT;
+    const int j0 = kl + KP * it, j1 = j0 + KP;
+    const half8 v0 = j0 >= jrep ? vn : kv[it];
+    const half8 v1 = pair ? (j1 >= jrep ? vn : kv[pair ? it + 1 : it]) : half8{};
     half2v vp[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      vp[i][0] = kv[it][i];
-      vp[i][1] = pair ? kv[pair ? it + 1 : it][i] : (half_t)0.f;
+      vp[i][0] = v0[i];
+      vp[i][1] = v1[i];
     }
 #pragma unroll
     for (int h = 0; h < G; h++) {
