@@ -386,17 +386,24 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   // scores can be formed while the values are still arriving.
   // Unconditional loads (indices clamped; keys past n unused); sched_barrier
   // fences keep the scheduler from reordering the groups.
+  // Only the waves holding projection columns load partials: a CU's
+  // memory pipeline serves its waves' loads in order, so partial loads
+  // queued behind other waves' K / V rows would hold the staging barrier
+  // until most of the context had arrived.
   const int cc = col < 0 ? 0 : col;
   const float* pp = a.qkv_part + (size_t)b * N1 + cc;
-  float pe[QS], po[QS];
+  float pe[QS], po[QS], cs = 0.f, sn = 0.f;
+  if (tid < G * 32 + 64) {
 #pragma unroll
-  for (int s = 0; s < QS; s++) {
-    const size_t o = (size_t)min(s, a.qkv_ks - 1) * kDecRows * N1;
-    pe[s] = pp[o];
-    po[s] = pp[o + 1];
+    for (int s = 0; s < QS; s++) {
+      const size_t o = (size_t)min(s, a.qkv_ks - 1) * kDecRows * N1;
+      pe[s] = pp[o];
+      po[s] = pp[o + 1];
+    }
+    const int ri = (cc & 63) >> 1;
+    cs = a.rope_cos[pos * 32 + ri];
+    sn = a.rope_sin[pos * 32 + ri];
   }
-  const int ri = (cc & 63) >> 1;
-  const float cs = a.rope_cos[pos * 32 + ri], sn = a.rope_sin[pos * 32 + ri];
   __builtin_amdgcn_sched_barrier(0);
   half8 kk[NIT], kv[NIT];
 #pragma unroll
@@ -563,10 +570,10 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   }
 }
 
-// Narrow form: 256 threads, 8 passes of 32 keys = kDecChunk keys per split,
-// QS = 8 fits 96 VGPRs (5 blocks of 4 waves per CU) for G < 4.
+// Narrow form (batches too small for the wide one): 256 threads, 8 passes
+// of 32 keys = kDecChunk keys per split, QS = 8 or kMaxSplits.
 template <int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G < 4 ? 5 : 4, 8))) void dec_attn_kernel8(DecAttnArgs a) {
+__global__ __launch_bounds__(256) void dec_attn_kernel8(DecAttnArgs a) {
   dec_attn_body<G, 8, 256, kDecChunk / 32, false>(a);
 }
 template <int G>
