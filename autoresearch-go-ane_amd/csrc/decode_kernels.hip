@@ -341,6 +341,68 @@ __device__ __forceinline__ int dec_chunk(int ctx, int nsplit) {
   return ((ctx + nsplit - 1) / nsplit + 31) & ~31;
 }
 
+// The step's projections from the QKV partials, one column pair per thread:
+// q of the G heads (threads < 32 G) and, in the block whose split holds
+// position pos, the new k (next 32) and v (next 32).  Summed in split order
+// as the finish kernels do, RoPE on q and k.  issue() loads the partials and
+// RoPE factors -- only in the waves holding projection columns: a CU's
+// memory pipeline serves its waves' loads in order, so partial loads queued
+// behind other waves' K / V rows would hold the staging barrier until most
+// of the context had arrived.  finish() sums, rotates and writes q, the new
+// k / v rows to LDS and the new rows to cache row `row` of the split.
+template <int G, int QS>
+struct QkvProj {
+  float pe[QS], po[QS], cs = 0.f, sn = 0.f;
+  int col = -1;
+  bool rot = false;
+  __device__ __forceinline__ void issue(const DecAttnArgs& a, int b, int kvh, int tid, int pos, bool own) {
+    const int D = a.NH * 64, KVD = a.NKV * 64, N1 = D + 2 * KVD;
+    if (tid < G * 32) col = kvh * G * 64 + 2 * tid;
+    else if (own && tid < G * 32 + 32) col = D + kvh * 64 + 2 * (tid - G * 32);
+    else if (own && tid < G * 32 + 64) col = D + KVD + kvh * 64 + 2 * (tid - G * 32 - 32);
+    rot = col >= 0 && col < D + KVD;
+    const int cc = col < 0 ? 0 : col;
+    const float* pp = a.qkv_part + (size_t)b * N1 + cc;
+    if (tid < G * 32 + 64) {
+#pragma unroll
+      for (int s = 0; s < QS; s++) {  // unconditional loads, split index clamped
+        const size_t o = (size_t)min(s, a.qkv_ks - 1) * kDecRows * N1;
+        pe[s] = pp[o];
+        po[s] = pp[o + 1];
+      }
+      const int ri = (cc & 63) >> 1;
+      cs = a.rope_cos[pos * 32 + ri];
+      sn = a.rope_sin[pos * 32 + ri];
+    }
+  }
+  __device__ __forceinline__ void finish(const DecAttnArgs& a, int tid, half_t (*qs)[64], half_t* knew, half_t* vnew,
+                                         half_t* Kb, half_t* Vb, int row) const {
+    if (col < 0) return;
+    float e = 0.f, o = 0.f;
+#pragma unroll
+    for (int s = 0; s < QS; s++) {
+      e += s < a.qkv_ks ? pe[s] : 0.f;
+      o += s < a.qkv_ks ? po[s] : 0.f;
+    }
+    if (rot) {
+      const float e2 = e * cs - o * sn, o2 = o * cs + e * sn;
+      e = e2;
+      o = o2;
+    }
+    half2v w;
+    w[0] = (half_t)e;
+    w[1] = (half_t)o;
+    if (tid < G * 32) {
+      *reinterpret_cast<half2v*>(&qs[tid >> 5][2 * (tid & 31)]) = w;
+    } else {
+      const bool isk = tid < G * 32 + 32;
+      const int d = 2 * ((tid - G * 32) & 31);
+      *reinterpret_cast<half2v*>((isk ? knew : vnew) + d) = w;
+      *reinterpret_cast<half2v*>((isk ? Kb : Vb) + (size_t)row * 64 + d) = w;  // cache row pos
+    }
+  }
+};
+
 // One block of NT threads per (sequence, kv head, key split): KP = NT / 8
 // keys per pass, NIT passes, so a split holds at most KP * NIT keys.  With
 // DIRECT (one split covers the context) the block normalises and writes att
@@ -352,7 +414,6 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   constexpr int NR = NT / (G * 64) < 8 ? NT / (G * 64) : 8;
   const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int D = a.NH * 64;
   const int ctx = a.ctr[0] + 1;
   const int chunk = dec_chunk(ctx, a.nsplit);
   const int c0 = sp * chunk;
@@ -375,35 +436,13 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   // order as the finish kernels do, RoPE on q and k.
   const int pos = ctx - 1;
   const bool own = pos - c0 < n;
-  const int KVD = a.NKV * 64, N1 = D + 2 * KVD;
-  int col = -1;
-  if (tid < G * 32) col = kvh * G * 64 + 2 * tid;
-  else if (own && tid < G * 32 + 32) col = D + kvh * 64 + 2 * (tid - G * 32);
-  else if (own && tid < G * 32 + 64) col = D + KVD + kvh * 64 + 2 * (tid - G * 32 - 32);
-  const bool rot = col >= 0 && col < D + KVD;
   // Load order: the partials and RoPE factors first (the staging barrier
   // waits for them alone), then every K row, then every V row, so the
-  // scores can be formed while the values are still arriving.
-  // Unconditional loads (indices clamped; keys past n unused); sched_barrier
-  // fences keep the scheduler from reordering the groups.
-  // Only the waves holding projection columns load partials: a CU's
-  // memory pipeline serves its waves' loads in order, so partial loads
-  // queued behind other waves' K / V rows would hold the staging barrier
-  // until most of the context had arrived.
-  const int cc = col < 0 ? 0 : col;
-  const float* pp = a.qkv_part + (size_t)b * N1 + cc;
-  float pe[QS], po[QS], cs = 0.f, sn = 0.f;
-  if (tid < G * 32 + 64) {
-#pragma unroll
-    for (int s = 0; s < QS; s++) {
-      const size_t o = (size_t)min(s, a.qkv_ks - 1) * kDecRows * N1;
-      pe[s] = pp[o];
-      po[s] = pp[o + 1];
-    }
-    const int ri = (cc & 63) >> 1;
-    cs = a.rope_cos[pos * 32 + ri];
-    sn = a.rope_sin[pos * 32 + ri];
-  }
+  // scores can be formed while the values are still arriving.  Unconditional
+  // loads (indices clamped; keys past n unused); sched_barrier fences keep
+  // the scheduler from reordering the groups.
+  QkvProj<G, QS> qp;
+  qp.issue(a, b, kvh, tid, pos, own);
   __builtin_amdgcn_sched_barrier(0);
   half8 kk[NIT], kv[NIT];
 #pragma unroll
@@ -412,30 +451,7 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
 #pragma unroll
   for (int it = 0; it < NIT; it++) kv[it] = ld_h8(Vb + (size_t)min(kl + KP * it, n - 1) * 64 + d8 * 8);
   __builtin_amdgcn_sched_barrier(0);
-  if (col >= 0) {
-    float e = 0.f, o = 0.f;
-#pragma unroll
-    for (int s = 0; s < QS; s++) {
-      e += s < a.qkv_ks ? pe[s] : 0.f;
-      o += s < a.qkv_ks ? po[s] : 0.f;
-    }
-    if (rot) {
-      const float e2 = e * cs - o * sn, o2 = o * cs + e * sn;
-      e = e2;
-      o = o2;
-    }
-    half2v w;
-    w[0] = (half_t)e;
-    w[1] = (half_t)o;
-    if (tid < G * 32) {
-      *reinterpret_cast<half2v*>(&qs[tid >> 5][2 * (tid & 31)]) = w;
-    } else {
-      const bool isk = tid < G * 32 + 32;
-      const int d = 2 * ((tid - G * 32) & 31);
-      *reinterpret_cast<half2v*>((isk ? knew : vnew) + d) = w;
-      *reinterpret_cast<half2v*>((isk ? Kb : Vb) + (size_t)(pos - c0) * 64 + d) = w;  // cache row pos
-    }
-  }
+  qp.finish(a, tid, qs, knew, vnew, Kb, Vb, pos - c0);
   __syncthreads();
   // Row pos is the last row of its split (pos - c0 = n - 1), and every
   // lane whose key index is >= n read it too (clamped): all of them take the
@@ -570,6 +586,182 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   }
 }
 
+// Wide form, one 1024-thread block per (sequence, kv head, split of up to
+// kDecWideChunk keys), scores on MFMA: S^T = K Q^T over 16-key tiles with
+// v_mfma_f32_16x16x32_f16 -- A = 16 keys x 32 dims read straight from the
+// cache rows (lane: key lane % 16, dims 8 (lane / 16) + [0, 8)), B = the G
+// query heads padded to 16 columns.  Tile t goes to wave t % 16, pass t / 16.
+// Every (key, head) score then sits in one lane (C layout: head lane % 16,
+// keys 4 (lane / 16) + [0, 4)), so each probability is formed once, rounded
+// to fp16 into LDS; P.V runs on v_dot2 with 8 lanes per key as in the
+// narrow form, reading the probabilities back.
+template <int G, bool DIRECT>
+__device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a) {
+  constexpr int NT = 1024, NW = NT / 64, KP = NT / 8, NIT = kDecWideChunk / KP;
+  constexpr int TW = (kDecWideChunk / 16 + NW - 1) / NW;  // K tiles per wave
+  constexpr int NR = NT / (G * 64) < 8 ? NT / (G * 64) : 8;
+  const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ctx = a.ctr[0] + 1;
+  const int chunk = dec_chunk(ctx, a.nsplit);
+  const int c0 = sp * chunk;
+  if (c0 >= ctx) return;  // uniform over the block, before any barrier
+  const int n = min(chunk, ctx - c0);
+  __shared__ half_t qs[G][64];
+  __shared__ half_t ps[G][kDecWideChunk];
+  __shared__ __attribute__((aligned(16))) float pv[G][KP][64];
+  __shared__ float red[NR][G * 64];
+  __shared__ float wmax[G][NW], wsum[G][NW];
+  __shared__ __attribute__((aligned(16))) half_t knew[64], vnew[64];
+  const float sl2 = a.scale * kL2E;
+  const size_t cache0 = ((size_t)b * a.NKV + kvh) * a.max_ctx;
+  half_t* Kb = a.kc + (cache0 + c0) * 64;
+  half_t* Vb = a.vc + (cache0 + c0) * 64;
+  const int pos = ctx - 1;
+  const bool own = pos - c0 < n;
+  const int kr = lane & 15, kq = lane >> 4;
+  const int kl = tid >> 3, d8 = tid & 7;
+  QkvProj<G, 8> qp;
+  qp.issue(a, b, kvh, tid, pos, own);
+  __builtin_amdgcn_sched_barrier(0);
+  half8 ka[TW][2];
+#pragma unroll
+  for (int u = 0; u < TW; u++) {
+    const half_t* row = Kb + (size_t)min((wave + NW * u) * 16 + kr, n - 1) * 64 + kq * 8;
+    ka[u][0] = ld_h8(row);
+    ka[u][1] = ld_h8(row + 32);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  half8 kv[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; it++) kv[it] = ld_h8(Vb + (size_t)min(kl + KP * it, n - 1) * 64 + d8 * 8);
+  __builtin_amdgcn_sched_barrier(0);
+  qp.finish(a, tid, qs, knew, vnew, Kb, Vb, pos - c0);
+  __syncthreads();
+  // Row pos is the last row of the split and every key index past n read it
+  // too (clamped): those take the new k / v (the row read may be stale, and
+  // a NaN there must not reach the sums), by a select at each use.
+  const int jrep = own ? pos - c0 : 1 << 30;
+  half8 kn0 = {}, kn1 = {}, vn = {};
+  if (own) {
+    kn0 = ld_h8(knew + kq * 8);
+    kn1 = ld_h8(knew + 32 + kq * 8);
+    vn = ld_h8(vnew + d8 * 8);
+  }
+  half8 qb0, qb1;  // B operand: head kr (zero columns past G), dims as A
+  {
+    const int h = kr < G ? kr : 0;
+    const half8 z = {};
+    qb0 = kr < G ? ld_h8(&qs[h][kq * 8]) : z;
+    qb1 = kr < G ? ld_h8(&qs[h][32 + kq * 8]) : z;
+  }
+  floatx4 st[TW];
+  float m = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < TW; u++) {
+    const int kb = (wave + NW * u) * 16;
+    const bool rep = kb + kr >= jrep;
+    floatx4 c = {0.f, 0.f, 0.f, 0.f};
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(rep ? kn0 : ka[u][0], qb0, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(rep ? kn1 : ka[u][1], qb1, c, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int j = kb + 4 * kq + i;
+      st[u][i] = j < n && kr < G ? c[i] * sl2 : -INFINITY;
+      m = fmaxf(m, st[u][i]);
+    }
+  }
+  // per-head maximum: lanes of one head (lane % 16) across the wave, then the waves
+  m = fmaxf(m, __shfl_xor(m, 16, 64));
+  m = fmaxf(m, xor32_f(m));
+  if (lane < G) wmax[lane][wave] = m;
+  __syncthreads();
+  float mh = kr < G ? -INFINITY : 0.f;  // padding columns: p = exp2(-inf) = 0
+  if (kr < G) {
+#pragma unroll
+    for (int w = 0; w < NW; w++) mh = fmaxf(mh, wmax[kr][w]);
+  }
+  // probabilities rounded to fp16 (they feed fp16 dot products), once per
+  // (key, head); the normaliser sums the same rounded values
+  float l = 0.f;
+#pragma unroll
+  for (int u = 0; u < TW; u++) {
+    const int kb = (wave + NW * u) * 16;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int j = kb + 4 * kq + i;
+      const half_t p = (half_t)__builtin_amdgcn_exp2f(st[u][i] - mh);  // 0 for masked scores
+      if (kr < G && j < kDecWideChunk) ps[kr < G ? kr : 0][j] = p;
+      l += (float)p;
+    }
+  }
+  l += __shfl_xor(l, 16, 64);
+  l += xor32_f(l);
+  if (lane < G) wsum[lane][wave] = l;
+  __syncthreads();
+  // P.V over this thread's key pairs (it, it + 1) with v_dot2
+  float acc[G][8];
+#pragma unroll
+  for (int h = 0; h < G; h++)
+#pragma unroll
+    for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
+#pragma unroll
+  for (int it = 0; it < NIT; it += 2) {
+    const bool pair = it + 1 < NIT;
+    const int j0 = kl + KP * it, j1 = j0 + KP;
+    const half8 v0 = j0 >= jrep ? vn : kv[it];
+    const half8 v1 = pair ? (j1 >= jrep ? vn : kv[pair ? it + 1 : it]) : half8{};
+    half2v vp[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      vp[i][0] = v0[i];
+      vp[i][1] = v1[i];
+    }
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+      half2v pp;
+      pp[0] = j0 < n ? ps[h][j0] : (half_t)0.f;
+      pp[1] = pair && j1 < n ? ps[h][pair ? j1 : j0] : (half_t)0.f;
+#pragma unroll
+      for (int i = 0; i < 8; i++) acc[h][i] = __builtin_amdgcn_fdot2(pp, vp[i], acc[h][i], false);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; h++) {
+    float4* dst = reinterpret_cast<float4*>(&pv[h][kl][d8 * 8]);
+    dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+    dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+  }
+  __syncthreads();
+  constexpr int KPR = (KP + NR - 1) / NR;
+  if (tid < NR * G * 64) {
+    const int r = tid / (G * 64), hd = tid % (G * 64), h = hd >> 6, d = hd & 63;
+    float o = 0.f;
+#pragma unroll 8
+    for (int k = r * KPR; k < min(KP, (r + 1) * KPR); k++) o += pv[h][k][d];
+    red[r][hd] = o;
+  }
+  __syncthreads();
+  if (tid < G * 64) {
+    const int h = tid >> 6, d = tid & 63;
+    float o = 0.f, lt = 0.f, mt = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < NR; r++) o += red[r][tid];
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+      lt += wsum[h][w];
+      mt = fmaxf(mt, wmax[h][w]);
+    }
+    if constexpr (DIRECT) {
+      a.att[act_frag_off(b, (kvh * G + h) * 64 + d)] = (half_t)(o / lt);
+    } else {
+      float* out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nsplit + sp) * 66;
+      out[d] = o;
+      if (d == 0) { out[64] = mt; out[65] = lt; }
+    }
+  }
+}
+
 // Narrow form (batches too small for the wide one): 256 threads, 8 passes
 // of 32 keys = kDecChunk keys per split, QS = 8 or kMaxSplits.
 template <int G>
@@ -585,7 +777,7 @@ __global__ __launch_bounds__(256) void dec_attn_kernel16(DecAttnArgs a) {
 // used when the batch alone gives enough blocks to fill the chip.
 template <int G, bool DIRECT>
 __global__ __launch_bounds__(1024) void dec_attn_wide_kernel(DecAttnArgs a) {
-  dec_attn_body<G, 8, 1024, kDecWideChunk / 128, DIRECT>(a);
+  dec_attn_wide_body<G, DIRECT>(a);
 }
 
 __global__ __launch_bounds__(64) void dec_combine_kernel(DecAttnArgs a) {
