@@ -107,6 +107,7 @@ SIGNATURES = {
                                      _fp, _fp, C.c_float, C.c_float, C.c_int, C.c_int, C.c_int, C.c_int]),
     "ane_debug_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, C.c_float, C.c_int, _u16,
                                       _u16, _fp]),
+    "ane_debug_transpose2": (C.c_int, [C.c_int, C.c_int, _u16, _u16, C.c_int, C.c_int, _u16, _u16]),
     "ane_debug_last_error": (C.c_char_p, []),
     "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 12 + [_u16, _u16, _fp]),
     "ane_decode_open": (C.c_int, [C.POINTER(DecodeCfg), C.POINTER(C.c_void_p)]),

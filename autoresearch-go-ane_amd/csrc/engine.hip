@@ -934,6 +934,35 @@ done:
   return rc;
 }
 
+extern "C" int ane_debug_transpose2(int Ra, int Ca, const uint16_t* in_a, uint16_t* out_a, int Rb, int Cb,
+                                    const uint16_t* in_b, uint16_t* out_b) {
+  int rc = ANE_OK;
+  const size_t na = (size_t)Ra * Ca, nb = in_b ? (size_t)Rb * Cb : 0;
+  void *dia = nullptr, *doa = nullptr, *dib = nullptr, *dob = nullptr;
+  if (Ra <= 0 || Ca <= 0 || Ra % 64 || Ca % 64 || !in_a || !out_a ||
+      (in_b && (Rb <= 0 || Cb <= 0 || Rb % 64 || Cb % 64 || !out_b)))
+    return debug_fail("transpose2: shapes must be positive multiples of 64", hipErrorInvalidValue);
+  DBGCHK(hipMalloc(&dia, na * 2));
+  DBGCHK(hipMalloc(&doa, na * 2));
+  DBGCHK(hipMemcpy(dia, in_a, na * 2, hipMemcpyHostToDevice));
+  if (nb) {
+    DBGCHK(hipMalloc(&dib, nb * 2));
+    DBGCHK(hipMalloc(&dob, nb * 2));
+    DBGCHK(hipMemcpy(dib, in_b, nb * 2, hipMemcpyHostToDevice));
+  }
+  DBGCHK(transpose2_h((half_t*)doa, (const half_t*)dia, Ra, Ca, Ca, Ra, (half_t*)dob, (const half_t*)dib, Rb, Cb, Cb,
+                      Rb, nullptr));
+  DBGCHK(hipDeviceSynchronize());
+  DBGCHK(hipMemcpy(out_a, doa, na * 2, hipMemcpyDeviceToHost));
+  if (nb) DBGCHK(hipMemcpy(out_b, dob, nb * 2, hipMemcpyDeviceToHost));
+done:
+  if (dia) (void)hipFree(dia);
+  if (doa) (void)hipFree(doa);
+  if (dib) (void)hipFree(dib);
+  if (dob) (void)hipFree(dob);
+  return rc;
+}
+
 extern "C" int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float scale, int hilo,
                                    const uint16_t* qkv, uint16_t* out, float* lse) {
   int rc = ANE_OK;

@@ -210,15 +210,13 @@ int backward_pass(ane_engine* e, int nseq) {
     {  // dW2 += dOut gate^T
       EpiParams p;
       p.C = G + o.w2; p.ldc = H; p.accumulate = 1;
-      HIPCHK(op, transpose_h(tb.op_a, tb.dcur_h, T, D, D, T, st));
-      HIPCHK(op, transpose_h(tb.op_b, A.gate, T, H, H, T, st));
+      HIPCHK(op, transpose2_h(tb.op_a, tb.dcur_h, T, D, D, T, tb.op_b, A.gate, T, H, H, T, st));
       HIPCHK(op, eng_gemm(e, 3, tb.op_a, T, false, tb.op_b, T, false, D, H, T, EPI_STORE_F, p));
     }
     {  // dW1 (| dW3) += dh x2Norm^T
       EpiParams p;
       p.C = G + o.w1; p.ldc = D; p.accumulate = 1;
-      HIPCHK(op, transpose_h(tb.op_a, tb.dh13, T, KH, KH, T, st));
-      HIPCHK(op, transpose_h(tb.op_b, A.xn2, T, D, D, T, st));
+      HIPCHK(op, transpose2_h(tb.op_a, tb.dh13, T, KH, KH, T, tb.op_b, A.xn2, T, D, D, T, st));
       if (llama) {
         p.C3 = G + o.w3;
         HIPCHK(op, eng_gemm(e, 2, tb.op_a, T, false, tb.op_b, T, false, KH, D, T, EPI_STORE_W13, p));
@@ -250,8 +248,7 @@ int backward_pass(ane_engine* e, int nseq) {
     {
       EpiParams p;
       p.C = G + o.wo; p.ldc = D; p.accumulate = 1;
-      HIPCHK(op, transpose_h(tb.op_a, tb.dx2_h, T, D, D, T, st));
-      HIPCHK(op, transpose_h(tb.op_b, A.att, T, D, D, T, st));
+      HIPCHK(op, transpose2_h(tb.op_a, tb.dx2_h, T, D, D, T, tb.op_b, A.att, T, D, D, T, st));
       HIPCHK(op, eng_gemm(e, 1, tb.op_a, T, false, tb.op_b, T, false, D, D, T, EPI_STORE_F, p));
     }
     {
@@ -296,8 +293,7 @@ int backward_pass(ane_engine* e, int nseq) {
     {  // dWq | dWk | dWv += dqkv xNorm^T
       EpiParams p;
       p.C = G + o.wq; p.ldc = D; p.accumulate = 1;
-      HIPCHK(op, transpose_h(tb.op_a, tb.dqkv, T, 3 * D, 3 * D, T, st));
-      HIPCHK(op, transpose_h(tb.op_b, A.xn, T, D, D, T, st));
+      HIPCHK(op, transpose2_h(tb.op_a, tb.dqkv, T, 3 * D, 3 * D, T, tb.op_b, A.xn, T, D, D, T, st));
       HIPCHK(op, eng_gemm(e, 0, tb.op_a, T, false, tb.op_b, T, false, 3 * D, D, T, EPI_STORE_F, p));
     }
     {  // dPrev = rl * dx2 + RMSNorm-backward(dxn; x) (+ VE gate grads, + backout injection)
@@ -330,8 +326,7 @@ int backward_pass(ane_engine* e, int nseq) {
     {
       EpiParams p;
       p.C = G + pm.smear_gate; p.ldc = D; p.accumulate = 1;
-      HIPCHK(op, transpose_h(tb.op_a, tb.dgp, T, D, D, T, st));
-      HIPCHK(op, transpose_h(tb.op_b, tb.x0h, T, D, D, T, st));
+      HIPCHK(op, transpose2_h(tb.op_a, tb.dgp, T, D, D, T, tb.op_b, tb.x0h, T, D, D, T, st));
       HIPCHK(op, eng_gemm(e, 7, tb.op_a, T, false, tb.op_b, T, false, D, D, T, EPI_STORE_F, p));
     }
     {

@@ -71,6 +71,9 @@ hipError_t fill_f32(float* p, size_t n, float v, hipStream_t s);
 // multiples of 64.  Turns a token-major [T, C] operand into the [C, T]
 // form the weight-gradient GEMMs read K-major (K = T).
 hipError_t transpose_h(half_t* out, const half_t* in, int R, int C, int ldi, int ldo, hipStream_t s);
+// Two independent transposes in one launch (out_b == nullptr: only the first).
+hipError_t transpose2_h(half_t* out_a, const half_t* in_a, int Ra, int Ca, int ldi_a, int ldo_a, half_t* out_b,
+                        const half_t* in_b, int Rb, int Cb, int ldi_b, int ldo_b, hipStream_t s);
 
 // fp16 weight shadows from the fp32 masters in one launch.  Job j converts
 // src [R, C] (row-major fp32) into dst row dr(r) = (r / 32) * blk_stride +

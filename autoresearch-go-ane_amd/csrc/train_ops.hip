@@ -356,28 +356,37 @@ inline int flat_grid(size_t n, int cap = 4096) {
   return (int)(g > (size_t)cap ? cap : (g == 0 ? 1 : g));
 }
 
-// 64x64 tile through LDS: 16-byte loads along C, 16-byte stores along R
-// (each group of 8 lanes writes 128 contiguous bytes of one output row).
-// LDS rows are 72 halves (144 B, 16-byte aligned).
+// LDS tile rows of the shadow kernel: 72 halves (144 B, 16-byte aligned).
 constexpr int kTp = 72;
-__global__ __launch_bounds__(256) void transpose_h_kernel(half_t* out, const half_t* in, int C, int ldi, int ldo) {
-  __shared__ __attribute__((aligned(16))) half_t tile[64 * kTp];
-  const int tiles_c = C >> 6;
-  const int r0 = (blockIdx.x / tiles_c) * 64, c0 = (blockIdx.x % tiles_c) * 64;
-  const int tid = threadIdx.x;
+// Transposes by 8x8 register blocks, one wave per 64x64 tile: lane (rb, cb)
+// reads rows 8 rb + [0, 8) at columns 8 cb + [0, 8) of the tile (every load
+// instruction covers 8 rows x 128 contiguous bytes), swaps the block in
+// registers and writes rows 8 cb + [0, 8) of the output at columns
+// 8 rb + [0, 8) (every store: 8 rows x 128 bytes).  No LDS and no barrier;
+// a launch carries two independent jobs (the two operands of one GEMM).
+struct TransposeJob {
+  half_t* out;
+  const half_t* in;
+  int C, ldi, ldo, ntiles;
+};
+__global__ __launch_bounds__(256) void transpose2_kernel(TransposeJob ja, TransposeJob jb) {
+  int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  const bool second = t >= ja.ntiles;
+  const TransposeJob& j = second ? jb : ja;
+  if (second) t -= ja.ntiles;
+  if (t >= j.ntiles) return;  // whole wave
+  const int lane = threadIdx.x & 63, rb = lane >> 3, cb = lane & 7;
+  const int tiles_c = j.C >> 6;
+  const int r0 = (t / tiles_c) * 64 + rb * 8, c0 = (t % tiles_c) * 64 + cb * 8;
+  half8 v[8];
 #pragma unroll
-  for (int p = 0; p < 2; p++) {
-    const int idx = tid + 256 * p, row = idx >> 3, ch = idx & 7;
-    st_h8(tile + row * kTp + ch * 8, ld_h8(in + (size_t)(r0 + row) * ldi + c0 + ch * 8));
-  }
-  __syncthreads();
+  for (int i = 0; i < 8; i++) v[i] = ld_h8(j.in + (size_t)(r0 + i) * j.ldi + c0);
 #pragma unroll
-  for (int p = 0; p < 2; p++) {
-    const int idx = tid + 256 * p, c = idx >> 3, rch = idx & 7;
+  for (int k = 0; k < 8; k++) {
     half8 w;
 #pragma unroll
-    for (int j = 0; j < 8; j++) w[j] = tile[(rch * 8 + j) * kTp + c];
-    st_h8(out + (size_t)(c0 + c) * ldo + r0 + rch * 8, w);
+    for (int i = 0; i < 8; i++) w[i] = v[i][k];
+    st_h8(j.out + (size_t)(c0 + k) * j.ldo + r0, w);
   }
 }
 
@@ -471,10 +480,26 @@ hipError_t ve_bwd(float* gemb, float* ggate, float* ve_dx, const half_t* dv, int
   return hipGetLastError();
 }
 
-hipError_t transpose_h(half_t* out, const half_t* in, int R, int C, int ldi, int ldo, hipStream_t s) {
-  if (R <= 0 || C <= 0 || R % 64 || C % 64 || ldi < C || ldo < R || ldi % 8 || ldo % 8) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(transpose_h_kernel, dim3((R / 64) * (C / 64)), dim3(256), 0, s, out, in, C, ldi, ldo);
+static bool transpose_ok(int R, int C, int ldi, int ldo) {
+  return R > 0 && C > 0 && R % 64 == 0 && C % 64 == 0 && ldi >= C && ldo >= R && ldi % 8 == 0 && ldo % 8 == 0;
+}
+
+hipError_t transpose2_h(half_t* out_a, const half_t* in_a, int Ra, int Ca, int ldi_a, int ldo_a, half_t* out_b,
+                        const half_t* in_b, int Rb, int Cb, int ldi_b, int ldo_b, hipStream_t s) {
+  if (!transpose_ok(Ra, Ca, ldi_a, ldo_a)) return hipErrorInvalidValue;
+  TransposeJob ja{out_a, in_a, Ca, ldi_a, ldo_a, (Ra / 64) * (Ca / 64)};
+  TransposeJob jb{nullptr, nullptr, 64, 64, 64, 0};
+  if (out_b) {
+    if (!transpose_ok(Rb, Cb, ldi_b, ldo_b)) return hipErrorInvalidValue;
+    jb = TransposeJob{out_b, in_b, Cb, ldi_b, ldo_b, (Rb / 64) * (Cb / 64)};
+  }
+  const int tiles = ja.ntiles + jb.ntiles;
+  hipLaunchKernelGGL(transpose2_kernel, dim3((tiles + 3) / 4), dim3(256), 0, s, ja, jb);
   return hipGetLastError();
+}
+
+hipError_t transpose_h(half_t* out, const half_t* in, int R, int C, int ldi, int ldo, hipStream_t s) {
+  return transpose2_h(out, in, R, C, ldi, ldo, nullptr, nullptr, 0, 0, 0, 0, s);
 }
 
 hipError_t shadow_refresh(const ShadowJob* jobs_dev, int njobs, int ntiles, hipStream_t s) {

@@ -238,6 +238,11 @@ int ane_debug_gemm_epi(int epi, int M, int N, int K, const uint16_t *A, const ui
                        const float *X0, const float *R, float alpha, float beta, int seq, int bm, int bn, int nw);
 int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float scale, int hilo,
                         const uint16_t *qkv, uint16_t *out, float *lse);
+/* Two fp16 transposes in one launch of the training step's transpose kernel:
+ * out_a [Ca, Ra] = in_a [Ra, Ca]^T, and the same for b when in_b is not NULL
+ * (rows and columns multiples of 64). */
+int ane_debug_transpose2(int Ra, int Ca, const uint16_t *in_a, uint16_t *out_a, int Rb, int Cb,
+                         const uint16_t *in_b, uint16_t *out_b);
 /* Mean time of `iters` launches of one GEMM on device-resident operands
  * (arguments as ane_debug_gemm; A / B NULL: pseudo-random in [-0.5, 0.5)).
  * epi: 0 fp16 store, 1 fp32 store, 3 in-place residual add, 4 SwiGLU over

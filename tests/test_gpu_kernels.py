@@ -203,3 +203,23 @@ def test_attention_split_scores_at_scale_1():
     print("scale-1 (lse err, out err): fp16", errs[0], "split", errs[1])
     assert errs[1][0] < 1e-3 and errs[1][1] < 4e-3
     assert errs[1][0] < errs[0][0] / 5
+
+
+@pytest.mark.parametrize("ra,ca,rb,cb", [(64, 64, 0, 0), (4096, 768, 4096, 4096), (256, 2304, 128, 64),
+                                         (192, 64, 64, 320)])
+def test_transpose_pairs_bit_exact(ra, ca, rb, cb):
+    """The training step's transpose (8x8 register blocks, two jobs per
+    launch) against numpy, bit for bit, on random fp16 bit patterns."""
+    lib = _lib.load()
+    rng = np.random.default_rng(ra + ca + rb + cb)
+    a = rng.integers(0, 1 << 16, (ra, ca), dtype=np.uint16)
+    oa = np.zeros((ca, ra), np.uint16)
+    b = rng.integers(0, 1 << 16, (rb, cb), dtype=np.uint16) if rb else None
+    ob = np.zeros((cb, rb), np.uint16) if rb else None
+    u16 = lambda x: x.ctypes.data_as(C.POINTER(C.c_uint16)) if x is not None else None
+    rc = lib.ane_debug_transpose2(ra, ca, u16(a), u16(oa), rb, cb, u16(b), u16(ob))
+    assert rc == 0, lib.ane_debug_last_error()
+    np.testing.assert_array_equal(oa, a.T)
+    if rb:
+        np.testing.assert_array_equal(ob, b.T)
+    assert lib.ane_debug_transpose2(100, 64, u16(a), u16(oa), 0, 0, None, None) != 0  # rows not a multiple of 64
