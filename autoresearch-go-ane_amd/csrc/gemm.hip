@@ -388,9 +388,11 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
     for (int j = 0; j < TN; j++) {
       const int nl = wn * WTN + j * 32 + (lane & 31);
       const int n = n0 + nl;
-      const int tg = e.targets[n];
+      // the target's row relative to this lane's first row: a match is one
+      // compare against a constant per register
+      const int tsel = e.targets[n] - ROW(0, 0);
+      const bool hit = tsel >= 0 && tsel < 32 * TM && (tsel & 4) == 0;
       float mx = -INFINITY, tv = 0.f;
-      bool hit = false;
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -399,16 +401,17 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
           if (e.softcap) v = softcap_f(v, e.cap);
           acc[i][j][r] = v;
           mx = fmaxf(mx, v);
-          const bool h = ROW(i, r) == tg;
-          tv = h ? v : tv;
-          hit = hit || h;
+          tv = (32 * i + 8 * (r >> 2) + (r & 3)) == tsel ? v : tv;
         }
       mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      // sum exp(v - max) as exp2(v log2e - max log2e): one FMA per value
+      constexpr float kLog2e = 1.4426950408889634f;
+      const float mxl = mx * kLog2e;
       float s = 0.f;
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) s += __expf(acc[i][j][r] - mx);
+        for (int r = 0; r < 16; r++) s += __builtin_amdgcn_exp2f(__builtin_fmaf(acc[i][j][r], kLog2e, -mxl));
       s += __shfl_xor(s, 32, 64);
       if (hit) e.tgt_logit[n] = tv;  // exactly one lane of the grid holds (tg, n)
       if (lane < 32) red[wm * BN + nl] = make_float2(mx, s);
