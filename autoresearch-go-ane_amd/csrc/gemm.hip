@@ -435,27 +435,30 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
     // 4q .. 4q+3 hold 4 consecutive rows, stored as one 8-byte chunk.
     half_t* C = (half_t*)e.C;
     half_t* C2 = (half_t*)e.C2;
+    constexpr float kLog2e = 1.4426950408889634f;
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       const int n = COL(j);
-      const int tg = e.targets[n];
-      const float lse = e.lse[n], cs = e.colscale[n];
+      // target row and vocabulary end relative to this lane's first row:
+      // per register one compare against a constant each
+      const int tsel = e.targets[n] - ROW(0, 0), vend = e.vocab - ROW(0, 0);
+      const float lsel = e.lse[n] * kLog2e, cs = e.colscale[n];
 #pragma unroll
       for (int i = 0; i < TM; i++) {
         half_t hv[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const int m = ROW(i, r);
+          const int mo = 32 * i + 8 * (r >> 2) + (r & 3);
           float v = acc[i][j][r], dsc = 1.f;
           if (e.softcap) {
             float th = tanhf(v / e.cap);
             v = e.cap * th;
             dsc = 1.f - th * th;
           }
-          float d = __expf(v - lse) - (m == tg ? 1.f : 0.f);
-          d = (m < e.vocab) ? d * cs * dsc : 0.f;
+          float d = __builtin_amdgcn_exp2f(__builtin_fmaf(v, kLog2e, -lsel)) - (mo == tsel ? 1.f : 0.f);
+          d = mo < vend ? d * cs * dsc : 0.f;
           hv[r] = (half_t)d;
-          C[(size_t)m * e.ldc + n] = hv[r];
+          C[(size_t)ROW(i, r) * e.ldc + n] = hv[r];
         }
         if (C2) {
 #pragma unroll
