@@ -94,15 +94,18 @@ __global__ __launch_bounds__(256) void router_kernel(const float* x, const float
     const int buf = c & 1, len = chunk_len(c);
     if (c + 1 < nch) fetch(c + 1, v);
     if (active) {
+      // separately rounded products and sums, as the reference's linearCF
+      // (the default fp-contract=fast would fuse them into FMAs)
+#pragma clang fp contract(off)
       for (int i = 0; i < len; i += 16) {
 #pragma unroll
         for (int j = 0; j < 16; j += 4) {
           const float4 a = *reinterpret_cast<const float4*>(&ws[buf][e][i + j]);
           const float4 b = *reinterpret_cast<const float4*>(&xs[buf][tl][i + j]);
-          s = __fadd_rn(s, __fmul_rn(a.x, b.x));
-          s = __fadd_rn(s, __fmul_rn(a.y, b.y));
-          s = __fadd_rn(s, __fmul_rn(a.z, b.z));
-          s = __fadd_rn(s, __fmul_rn(a.w, b.w));
+          s = s + a.x * b.x;
+          s = s + a.y * b.y;
+          s = s + a.z * b.z;
+          s = s + a.w * b.w;
         }
       }
     }

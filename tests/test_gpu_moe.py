@@ -106,6 +106,35 @@ def test_ties_go_to_lower_expert():
     np.testing.assert_array_equal(idx, ridx)
 
 
+def test_router_products_and_sums_separately_rounded():
+    """linearCF rounds every product and every partial sum.  With row 1 =
+    (1, a) and x = (1, x1): fl(a * x1) is exactly 2^-24 while the exact
+    product is a little larger, so 1 + fl(a * x1) is a tie that rounds to
+    even (1.0, equal to row 0's logit: the lower expert comes first), whereas
+    a fused multiply-add would round up to 1 + 2^-23 and put expert 1 first."""
+    cfg = MoeConfig(dim=64, hidden=64, experts=4)
+    p = init_moe_params(cfg, seed=22, std=0.05)
+    router = p[:cfg.experts * cfg.dim].reshape(cfg.experts, cfg.dim)
+    router[...] = 0.0
+    a = np.float32(1 + 2049 * 2.0 ** -23)
+    x1 = np.float32(2.0 ** -24 * (1 - 2048 * 2.0 ** -23))
+    assert a * x1 == np.float32(2.0 ** -24)                    # product rounds down onto 2^-24
+    assert np.float32(1) + a * x1 == np.float32(1)             # and the sum ties to even
+    router[0, 0] = 1.0
+    router[1, 0], router[1, 1] = 1.0, a
+    x = np.zeros((2, cfg.dim), np.float32)
+    x[0, 0], x[0, 1] = 1.0, x1
+    x[1, 0], x[1, 1] = 1.0, np.float32(2.0 ** -22)  # a clear win for expert 1
+    layer = MoeLayer(cfg, p, max_tokens=64)
+    try:
+        _, idx, _ = layer.Forward(x)
+    finally:
+        layer.Close()
+    assert idx.tolist() == [[0, 1], [1, 0]]
+    ridx, _ = oracle.moe_route(p, x, cfg.hidden, cfg.experts)
+    np.testing.assert_array_equal(idx, ridx)
+
+
 def test_moe_errors():
     lib = _lib.load()
     for bad in (_lib.MoeCfg(768, 2048, 8, 3, 16, 0), _lib.MoeCfg(768, 2048, 6, 2, 16, 0),
