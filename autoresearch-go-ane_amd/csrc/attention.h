@@ -24,6 +24,7 @@ struct AttnArgs {
   int hilo;               // scores from hi+lo split operands (~fp32); S <= 256
   const void* pf;         // optional: weights of the next GEMM, streamed through the caches
   size_t pf_bytes;
+  int split_from;         // set by attention_fwd (block decomposition)
 };
 
 hipError_t attention_fwd(const AttnArgs& a, hipStream_t stream);

@@ -39,8 +39,23 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const int S = a.S, NH = a.NH, D = NH * HD, D3 = 3 * D;
   prefetch_slice(a.pf, a.pf_bytes, ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x,
                  (size_t)gridDim.x * gridDim.y * gridDim.z);
-  const int h = blockIdx.y, b = blockIdx.z;
   const int nthr = blockDim.x, tid = threadIdx.x;
+  // Block -> (sequence b, head h, q-block pairs [p0, p0 + np)).  Grid
+  // (pair groups, NH, nseq), or with split_from > 0 a 1-D grid: heads below
+  // split_from whole, the rest as two half blocks each.
+  int hl, p0, np;
+  if (a.split_from > 0) {
+    const int u = blockIdx.x, half = (S / 64) / 2;
+    if (u < a.split_from) {
+      hl = u; p0 = 0; np = 2 * half;
+    } else {
+      hl = a.split_from + (u - a.split_from) / 2; p0 = ((u - a.split_from) & 1) * half; np = half;
+    }
+  } else {
+    hl = blockIdx.z * NH + blockIdx.y; p0 = blockIdx.x * (nthr >> 6); np = nthr >> 6;
+  }
+  const int h = hl % NH, b = hl / NH;
+  const bool first = p0 == 0;  // the block that writes qkvt of its head
   const size_t tok0 = (size_t)b * S;
   const half_t* base = a.qkv + tok0 * D3;
 
@@ -95,8 +110,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       }
       st_h8(Ks + j * HD + swz(j, ch) * 8, w);
       if constexpr (HILO) st_h8(Ks_lo + j * HD + swz(j, ch) * 8, wl);
-      if (a.qkvt && blockIdx.x == 0) st_h8(a.qkvt + (tok0 + j) * D3 + D + h * HD + ch * 8, w);
-      if (a.qkvt_lo && blockIdx.x == 0) st_h8(a.qkvt_lo + (tok0 + j) * 2 * D + D + h * HD + ch * 8, wl);
+      if (a.qkvt && first) st_h8(a.qkvt + (tok0 + j) * D3 + D + h * HD + ch * 8, w);
+      if (a.qkvt_lo && first) st_h8(a.qkvt_lo + (tok0 + j) * 2 * D + D + h * HD + ch * 8, wl);
     }
   }
 
@@ -137,7 +152,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       *reinterpret_cast<half4*>(dst) = lo;
       *reinterpret_cast<half4*>(dst + 4) = hi;
     }
-    if (a.qkvt && blockIdx.x == 0) {
+    if (a.qkvt && first) {
 #pragma unroll
       for (int jj = 0; jj < 8; jj++) {
         half8 w;
@@ -152,8 +167,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   // ---- per wave: q-block pair ------------------------------------------------
   const int lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;
   const int nqb = S / 32, npairs = nqb / 2;
-  const int pair = blockIdx.x * nw + wave;
-  if (pair >= npairs) return;
+  const int pair = p0 + wave;
+  if (wave >= np || pair >= npairs) return;
   const int g = lane >> 5, ql = lane & 31;
   const float l2e = 1.4426950408889634f;
   const float sl2 = a.scale * l2e;
@@ -329,13 +344,23 @@ hipError_t attention_fwd(const AttnArgs& a, hipStream_t stream) {
   const int npairs = a.S / 64;
   const int nw = npairs < 4 ? npairs : 4;
   dim3 grid((npairs + nw - 1) / nw, a.NH, a.nseq);
+  // One block of 4 pairs per head leaves 256 < heads < 512 unevenly spread
+  // over the 256 CUs (two blocks on some, one on the rest): the heads past
+  // 256 run as two half blocks, one beside each whole block.
+  AttnArgs k = a;
+  k.split_from = 0;
+  const int heads = a.nseq * a.NH;
+  if (npairs == 4 && heads > 256 && heads < 512) {
+    k.split_from = 256;
+    grid = dim3(256 + 2 * (heads - 256), 1, 1);
+  }
   if (a.hilo && a.S > 256) return hipErrorInvalidValue;
   if (a.hilo)
-    hipLaunchKernelGGL((attn_fwd_kernel<256, true>), grid, dim3(64 * nw), 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<256, true>), grid, dim3(64 * nw), 0, stream, k);
   else if (a.S <= 256)
-    hipLaunchKernelGGL((attn_fwd_kernel<256, false>), grid, dim3(64 * nw), 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<256, false>), grid, dim3(64 * nw), 0, stream, k);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<512, false>), grid, dim3(64 * nw), 0, stream, a);
+    hipLaunchKernelGGL((attn_fwd_kernel<512, false>), grid, dim3(64 * nw), 0, stream, k);
   return hipGetLastError();
 }
 
