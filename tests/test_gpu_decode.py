@@ -55,12 +55,15 @@ def test_prefill_and_forced_steps_match_oracle():
     assert max(errs) <= TOL
 
 
+@pytest.mark.parametrize("form", ["split", "wide"])
 @pytest.mark.parametrize("heads,kv_heads", [(4, 4), (4, 1), (6, 2)])
-def test_query_head_groups(heads, kv_heads):
-    """Every head-group size the attention kernel is built for (1, 4, 3
-    query heads per key/value head) through prefill and forced steps, with
-    hidden 256 and dim 64 * heads (K of 1, 4 and 6 windows per split-K
-    GEMM) and a context that crosses a 256-key split."""
+def test_query_head_groups(heads, kv_heads, form, monkeypatch):
+    """Every head-group size the attention kernels are built for (1, 4, 3
+    query heads per key/value head), in both decode-attention forms, through
+    prefill and forced steps, with hidden 256 and dim 64 * heads (K of 1, 4
+    and 6 windows per split-K GEMM) and a context that crosses a 256-key
+    split."""
+    monkeypatch.setenv("ANE_DEC_ATTN", form)
     cfg = ane.tiny_decode(heads=heads, kv_heads=kv_heads, dim=64 * heads, hidden=256, layers=1)
     nseq, plen, nsteps = 2, 320, 3
     p, prefix = _setup(cfg, nseq, plen, 41)
