@@ -989,8 +989,13 @@ __global__ __launch_bounds__(256) void gather_last_kernel(float* dst, const floa
 }  // namespace
 
 // waves splitting K: enough that no wave holds more than two windows
+// Waves per block: exactly two k-windows each when the window count allows
+// one of the built sizes (no zeroed surplus window, whose weights and
+// activations would still be read), else the smallest power of two that
+// leaves at most two.
 int classifier_kwaves(int K) {
   const int nwin = K / 64;
+  if (nwin % 2 == 0 && (nwin == 2 || nwin == 6 || nwin == 12 || nwin == 24)) return nwin / 2;
   int w = 1;
   while (w < 16 && (nwin + w - 1) / w > 2) w <<= 1;
   return w;
@@ -1005,7 +1010,10 @@ hipError_t classifier_argmax(const SkinnyArgs& a, hipStream_t s) {
     case 1: hipLaunchKernelGGL(classifier_argmax_kernel<1>, grid, dim3(64), 0, s, a); break;
     case 2: hipLaunchKernelGGL(classifier_argmax_kernel<2>, grid, dim3(128), 0, s, a); break;
     case 4: hipLaunchKernelGGL(classifier_argmax_kernel<4>, grid, dim3(256), 0, s, a); break;
+    case 3: hipLaunchKernelGGL(classifier_argmax_kernel<3>, grid, dim3(192), 0, s, a); break;
+    case 6: hipLaunchKernelGGL(classifier_argmax_kernel<6>, grid, dim3(384), 0, s, a); break;
     case 8: hipLaunchKernelGGL(classifier_argmax_kernel<8>, grid, dim3(512), 0, s, a); break;
+    case 12: hipLaunchKernelGGL(classifier_argmax_kernel<12>, grid, dim3(768), 0, s, a); break;
     default: hipLaunchKernelGGL(classifier_argmax_kernel<16>, grid, dim3(1024), 0, s, a); break;
   }
   return hipGetLastError();
