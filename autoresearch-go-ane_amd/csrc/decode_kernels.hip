@@ -345,10 +345,10 @@ __device__ __forceinline__ int dec_chunk(int ctx, int nsplit) {
 // q of the G heads (threads < 32 G) and, in the block whose split holds
 // position pos, the new k (next 32) and v (next 32).  Summed in split order
 // as the finish kernels do, RoPE on q and k.  issue() loads the partials and
-// RoPE factors -- only in the waves holding projection columns: a CU's
-// memory pipeline serves its waves' loads in order, so partial loads queued
-// behind other waves' K / V rows would hold the staging barrier until most
-// of the context had arrived.  finish() sums, rotates and writes q, the new
+// RoPE factors -- only in the waves holding projection columns, so fewer
+// loads share the CU's memory pipeline with the K / V rows (the q loads
+// still return late under a block's worth of K / V misses: the staging
+// barrier waits for them).  finish() sums, rotates and writes q, the new
 // k / v rows to LDS and the new rows to cache row `row` of the split.
 template <int G, int QS>
 struct QkvProj {
