@@ -43,7 +43,7 @@ hipError_t weight_to_frag(half_t* dst, const half_t* src, int N, int K, hipStrea
 struct SkinnyArgs {
   const half_t* X;  // [64, K] activation fragments (act_frag_off)
   const half_t* W;  // [N, K] weight fragments (weight_to_frag)
-  int N, K, nb;     // N % 32 == 0, K % 64 == 0 (K <= 2048), 1 <= nb <= 64
+  int N, K, nb;     // N % 32 == 0, K % 64 == 0 (classifier: K <= 1024), 1 <= nb <= 64
   float2* amax;
   float* logits;
   int nvalid;

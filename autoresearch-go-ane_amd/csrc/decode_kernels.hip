@@ -25,8 +25,12 @@ constexpr float kL2E = 1.4426950408889634f;
 // the 32 columns of its token: (max, first index) per token and group.
 template <int NWK>
 __global__ __launch_bounds__(64 * NWK) void classifier_argmax_kernel(SkinnyArgs a) {
+  // LDS: the partial sums of waves 1..NWK-1 (2048 floats each), then --
+  // reusing the same array -- the 64 x 33 transpose tile, which is larger
+  // than one wave's partials
   constexpr int NRED = NWK > 1 ? NWK - 1 : 1;
-  __shared__ float red[NRED][32 * 64];
+  constexpr int kTile = 64 * 33;
+  __shared__ float lds[NRED * 2048 > kTile ? NRED * 2048 : kTile];
   const int tid = threadIdx.x, lane = tid & 63, kw = tid >> 6;
   const int cg = blockIdx.x;
   const int nwin = a.K / 64;
@@ -62,7 +66,7 @@ __global__ __launch_bounds__(64 * NWK) void classifier_argmax_kernel(SkinnyArgs 
   }
   if constexpr (NWK > 1) {
     if (kw > 0) {
-      float* dst = red[kw - 1];
+      float* dst = lds + (kw - 1) * 2048;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         dst[r * 64 + lane] = c0[r];
@@ -75,7 +79,7 @@ __global__ __launch_bounds__(64 * NWK) void classifier_argmax_kernel(SkinnyArgs 
   if constexpr (NWK > 1) {
 #pragma unroll 1
     for (int o = 1; o < NWK; o++) {
-      const float* src = red[o - 1];
+      const float* src = lds + (o - 1) * 2048;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         c0[r] += src[r * 64 + lane];
@@ -84,9 +88,10 @@ __global__ __launch_bounds__(64 * NWK) void classifier_argmax_kernel(SkinnyArgs 
     }
   }
   // c[r]: token 8*(r/4) + 4*h + r%4 (+32 for c1), column col.  Transpose
-  // into tile[t][c] (row stride 33: conflict-free both ways; red[0] is this
-  // wave's own, its reads above are done), then lane t scans its row.
-  float* tile = red[0];
+  // into tile[t][c] (row stride 33: conflict-free both ways), then lane t
+  // scans its row.  Wave 0 is the only one left, and its reads of the other
+  // waves' partials above are done.
+  float* tile = lds;
   const bool valid = col < a.nvalid;
 #pragma unroll
   for (int r = 0; r < 16; r++) {
@@ -988,21 +993,22 @@ __global__ __launch_bounds__(256) void gather_last_kernel(float* dst, const floa
 
 }  // namespace
 
-// waves splitting K: enough that no wave holds more than two windows
-// Waves per block: exactly two k-windows each when the window count allows
-// one of the built sizes (no zeroed surplus window, whose weights and
+// Waves per block splitting K (K <= 1024, the decoder's dim limit: at most
+// 16 windows): exactly two k-windows each when the window count allows one
+// of the built sizes (no zeroed surplus window, whose weights and
 // activations would still be read), else the smallest power of two that
-// leaves at most two.
+// leaves at most two.  Results: 1, 2, 3, 4, 6 or 8.
 int classifier_kwaves(int K) {
   const int nwin = K / 64;
-  if (nwin % 2 == 0 && (nwin == 2 || nwin == 6 || nwin == 12 || nwin == 24)) return nwin / 2;
+  if (nwin == 2 || nwin == 6 || nwin == 12) return nwin / 2;
   int w = 1;
-  while (w < 16 && (nwin + w - 1) / w > 2) w <<= 1;
+  while (w < 8 && (nwin + w - 1) / w > 2) w <<= 1;
   return w;
 }
 
 hipError_t classifier_argmax(const SkinnyArgs& a, hipStream_t s) {
-  if (a.N <= 0 || a.N % 32 || a.K <= 0 || a.K % 64 || a.nb < 1 || a.nb > kDecRows) return hipErrorInvalidValue;
+  if (a.N <= 0 || a.N % 32 || a.K <= 0 || a.K % 64 || a.K > 1024 || a.nb < 1 || a.nb > kDecRows)
+    return hipErrorInvalidValue;
   const int nwk = classifier_kwaves(a.K);
   if ((a.K / 64 + nwk - 1) / nwk > 2) return hipErrorInvalidValue;  // K too long for one block
   const dim3 grid(a.N / 32);
@@ -1013,8 +1019,7 @@ hipError_t classifier_argmax(const SkinnyArgs& a, hipStream_t s) {
     case 3: hipLaunchKernelGGL(classifier_argmax_kernel<3>, grid, dim3(192), 0, s, a); break;
     case 6: hipLaunchKernelGGL(classifier_argmax_kernel<6>, grid, dim3(384), 0, s, a); break;
     case 8: hipLaunchKernelGGL(classifier_argmax_kernel<8>, grid, dim3(512), 0, s, a); break;
-    case 12: hipLaunchKernelGGL(classifier_argmax_kernel<12>, grid, dim3(768), 0, s, a); break;
-    default: hipLaunchKernelGGL(classifier_argmax_kernel<16>, grid, dim3(1024), 0, s, a); break;
+    default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }

@@ -15,7 +15,24 @@ refdecode.c, refmoe.c) on small seeded cases and stored as little-endian
   moe_small                   16 tokens of a dim-64 MoE layer: expert ids,
                               weights, outputs
 
-Usage:  python tests/golden/make_golden.py
+Benchmark-shape fixtures (--bench; several minutes of oracle time), the
+exact inputs bench.py measures:
+
+  bench_fwd_b32_llama2        stories110M-llama2, weights seed 0, 32 x 256
+                              tokens seed 2: the oracle's 32 per-sequence
+                              losses
+  bench_grads_b16_{llama2_true,nanochat_compat}
+                              stories110M, weights seed 0, 16 x 256 tokens
+                              seed 3: per-segment L2 norms of the mean
+                              gradient and a few sampled rows of every
+                              segment (token rows for the embeddings)
+  bench_decode_b64            the decode model (weights seed 4), 64
+                              sequences of 1024 prefix ids seed 4: for 4
+                              sampled sequences the oracle's greedy tokens
+                              after the prefix and 3 steps and the fp16
+                              logits of those 4 positions
+
+Usage:  python tests/golden/make_golden.py [--bench | --all]
 """
 import json
 import os
@@ -28,12 +45,72 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 for p in (os.path.join(ROOT, "autoresearch-go-ane_amd"), os.path.join(ROOT, "oracle")):
     sys.path.insert(0, p)
 
+sys.path.insert(0, os.path.dirname(HERE))
 import ane  # noqa: E402
 import oracle  # noqa: E402
+from golden_io import sampled_rows  # noqa: E402
 from ane.moe import MoeConfig, init_moe_params, make_moe_input  # noqa: E402
 
 
+BENCH_DECODE_SEQS = (0, 21, 42, 63)
+
+
+def grad_fingerprint(cfg, g, tokens, seed=90):
+    """(norms [segments] f64, rows: concatenated sampled rows f32)."""
+    norms, rows = [], []
+    for i, (name, off, shape) in enumerate(ane.param_layout(cfg)):
+        seg = g[off:off + int(np.prod(shape))]
+        norms.append(np.linalg.norm(seg.astype(np.float64)))
+        idx = sampled_rows(cfg, name.split(".")[-1], shape, tokens, seed + i)
+        rows.append(seg if idx is None else seg.reshape(shape)[idx].reshape(-1))
+    return np.array(norms, np.float64), np.concatenate(rows).astype(np.float32)
+
+
+def bench_fixtures(put):
+    import time
+    oracle.set_threads(os.cpu_count() or 1, parallel_linear=True)
+    t0 = time.time()
+    cfg = ane.stories110m("llama2")
+    p = ane.init_params(cfg, seed=0, std=0.02)
+    tok, tgt = ane.make_tokens(cfg, 32, seed=2)
+    mean, per, _ = oracle.forward_loss(cfg, p, tok, tgt)
+    put("bench_fwd_b32_llama2_loss_per_seq", per, 2, 1e-3,
+        "stories110m('llama2'), init_params(seed 0, std 0.02), make_tokens(batch 32, seed 2): oracle loss per sequence")
+    print(f"forward B32: mean {mean:.6f} ({time.time() - t0:.0f} s)", flush=True)
+    for arch, mode in (("llama2", "true"), ("nanochat", "compat")):
+        t0 = time.time()
+        cfg = ane.stories110m(arch, grad_mode=mode)
+        p = ane.init_params(cfg, seed=0, std=0.02)
+        tok, tgt = ane.make_tokens(cfg, 16, seed=3)
+        loss, g = oracle.grads(cfg, p, tok, tgt)
+        norms, rows = grad_fingerprint(cfg, g, tok)
+        put(f"bench_grads_b16_{arch}_{mode}_norms", norms, 3, 1e-2,
+            f"stories110m('{arch}', grad_mode '{mode}'), init_params(seed 0), make_tokens(batch 16, seed 3): "
+            "per-segment L2 norm of the mean gradient")
+        put(f"bench_grads_b16_{arch}_{mode}_rows", rows, 3, 1e-2,
+            "sampled rows of every segment, concatenated in layout order (tests/golden/make_golden.py "
+            "sampled_rows)")
+        put(f"bench_grads_b16_{arch}_{mode}_loss", np.array([loss], np.float32), 3, 1e-3, "mean loss")
+        print(f"grads B16 {arch}/{mode}: loss {loss:.6f} ({time.time() - t0:.0f} s)", flush=True)
+    t0 = time.time()
+    dcfg = ane.decode_gqa()
+    dp = ane.init_params(dcfg, seed=4, std=0.02)
+    prefix = np.random.default_rng(4).integers(0, dcfg.vocab, (64, 1024)).astype(np.uint16)
+    sel = np.array(BENCH_DECODE_SEQS, np.int64)
+    toks, lg = oracle.decode(dcfg, dp, prefix[sel], 3, want_logits=True, threads=len(sel))
+    put("bench_decode_b64_seqs", sel.astype(np.int32), 4, 0, "sampled sequences of the 64")
+    put("bench_decode_b64_tokens", toks.astype(np.uint16), 4, 0,
+        "decode_gqa(), init_params(seed 4, std 0.02), prefix rng(4).integers(0, 32000, (64, 1024)): oracle "
+        "greedy tokens after the prefix and after each of 3 steps")
+    put("bench_decode_b64_logits", lg.astype(np.float16), 4, 2e-2, "[seq, position, vocab] logits (fp16)")
+    print(f"decode B64: ({time.time() - t0:.0f} s)", flush=True)
+
+
 def main():
+    bench = "--bench" in sys.argv or "--all" in sys.argv
+    small = "--bench" not in sys.argv
+    path = os.path.join(HERE, "manifest.json")
+    old = json.load(open(path)) if os.path.exists(path) else []
     manifest = []
 
     def put(name, arr, seed, tol, note):
@@ -43,6 +120,12 @@ def main():
         manifest.append({"name": name, "file": fn, "dtype": str(arr.dtype), "shape": list(arr.shape),
                          "seed": seed, "tolerance": tol, "note": note})
 
+    if bench:
+        bench_fixtures(put)
+    if not small:
+        # keep the small fixtures written earlier
+        manifest.extend(m for m in old if not m["name"].startswith("bench_"))
+        return finish(manifest, path)
     oracle.set_threads(1, parallel_linear=False)
     for arch in ("llama2", "nanochat"):
         cfg = ane.tiny(arch)
@@ -91,10 +174,17 @@ def main():
     put("moe_small_weights", w, 71, 1e-6, "router weights")
     put("moe_small_out", out, 71, 5e-3, "layer output (relative L2 on a GPU)")
 
-    with open(os.path.join(HERE, "manifest.json"), "w") as f:
+    if not bench:
+        # keep the benchmark-shape fixtures written earlier
+        manifest.extend(m for m in old if m["name"].startswith("bench_"))
+    finish(manifest, path)
+
+
+def finish(manifest, path):
+    with open(path, "w") as f:
         json.dump(manifest, f, indent=1)
     total = sum(os.path.getsize(os.path.join(HERE, m["file"])) for m in manifest)
-    print(f"wrote {len(manifest)} fixtures, {total / 1024:.0f} KiB")
+    print(f"manifest: {len(manifest)} fixtures, {total / 1024:.0f} KiB")
 
 
 if __name__ == "__main__":

@@ -210,3 +210,37 @@ def test_decoder_errors():
     with pytest.raises(ane.EngineError) as ei:
         dec.Step()
     assert ei.value.code == _lib.ANE_ERR_CLOSED
+
+
+@pytest.mark.parametrize("heads,kv_heads", [(4, 2), (6, 2), (3, 1)])
+def test_full_batch_of_64_every_sequence(heads, kv_heads):
+    """64 sequences (every decode row) at dims 256, 384 and 192: the
+    classifier splits K over 2, 3 and 2 waves (4, 6 and 3 windows; one wave
+    holding a single zeroed-surplus window at 192), and the argmax transpose
+    covers tokens 62-63 of the last MFMA tile.  Prefill, forced steps, and
+    greedy Generate, every sequence against the oracle."""
+    cfg = ane.tiny_decode(heads=heads, kv_heads=kv_heads, dim=64 * heads, layers=1)
+    nseq, plen, nsteps = 64, 64, 2
+    p, prefix = _setup(cfg, nseq, plen, 81)
+    forced = np.random.default_rng(82).integers(0, cfg.vocab, (nseq, nsteps)).astype(np.uint16)
+    ref_tok, ref_lg = oracle.decode(cfg, p, prefix, nsteps, forced=forced, want_logits=True)
+    dec = ane.Decoder(cfg, p, max_batch=64, max_ctx=128)
+    try:
+        t0, lg0 = dec.Prefill(prefix, want_logits=True)
+        errs = [np.abs(lg0 - ref_lg[:, 0]).max()]
+        _check_choice(t0, ref_lg[:, 0])
+        np.testing.assert_array_equal(t0, lg0.argmax(-1))
+        for i in range(nsteps):
+            ti, lgi = dec.Step(forced[:, i], want_logits=True)
+            errs.append(np.abs(lgi - ref_lg[:, i + 1]).max())
+            _check_choice(ti, ref_lg[:, i + 1])
+            np.testing.assert_array_equal(ti, lgi.argmax(-1))
+        dec.Prefill(prefix)
+        gen = dec.Generate(3)
+    finally:
+        dec.Close()
+    print(f"dim {cfg.dim}, 64 sequences: logits max-abs err per step", [f"{e:.2e}" for e in errs])
+    assert max(errs) <= TOL
+    inputs = np.concatenate([t0[:, None], gen[:, :-1]], 1)
+    _, g_lg = oracle.decode(cfg, p, prefix, 3, forced=inputs, want_logits=True)
+    _check_choice(gen, g_lg[:, 1:])

@@ -269,3 +269,53 @@ def test_adam_closed_form_and_groups():
     np.testing.assert_allclose(g2[lo:hi], g[lo:hi] * (1.0 / norm), rtol=1e-5)
     o, k = lay["smear_gate"]
     np.testing.assert_array_equal(g2[o:o + k], g[o:o + k])
+
+
+def test_adam_moment_decay_closed_forms():
+    """AdamW past the first step, pinned by two closed forms that exercise the
+    moment decay and bias correction of every parameter group
+    (ane/train_full.go:1107-1150, groups ane/engine.go:659-673):
+      (a) a constant gradient g at every step keeps m_hat = g and
+          v_hat = g^2, so each step is w -= lr (g / (|g| + eps) + wd w);
+      (b) g at step 1 and 0 at step 2 give m_hat = b1 g / (1 + b1) and
+          v_hat = b2 g^2 / (1 + b2) at step 2, with each group's own betas
+          (the lambdas use lambda_beta1/2)."""
+    cfg = _tiny("nanochat")
+    n = ane.param_count(cfg)
+    r = rng(11)
+    w0 = r.standard_normal(n, dtype=np.float32)
+    g = r.standard_normal(n, dtype=np.float32)
+    hp = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, grad_clip=0.0,
+              embed_lr_mult=2.0, scalar_lr_mult=0.5, lambda_lr_mult=0.01, lambda_beta1=0.8, lambda_beta2=0.7)
+    lay = {nm: (o, int(np.prod(s))) for nm, o, s in ane.param_layout(cfg)}
+    groups = (("layers.0.wq", 3e-4, 0.1, 0.9, 0.95), ("layers.1.ve_embed", 6e-4, 0.0, 0.9, 0.95),
+              ("embed", 6e-4, 0.0, 0.9, 0.95), ("smear_gate", 3e-4, 0.1, 0.9, 0.95),
+              ("smear_lambda", 1.5e-4, 0.0, 0.9, 0.95), ("resid_lambdas", 1.5e-6, 0.0, 0.8, 0.7),
+              ("x0_lambdas", 1.5e-6, 0.0, 0.8, 0.7))
+    # (a) five steps of the same gradient
+    w = w0.copy()
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    for t in range(1, 6):
+        oracle.adam_update(cfg, w, g.copy(), m, v, t, hp)
+    for name, lr, wd, _, _ in groups:
+        o, k = lay[name]
+        ref = w0[o:o + k].astype(np.float64)
+        gg = g[o:o + k].astype(np.float64)
+        for _ in range(5):
+            ref = ref - lr * (gg / (np.abs(gg) + 1e-8) + wd * ref)
+        np.testing.assert_allclose(w[o:o + k], ref, rtol=2e-6, atol=2e-7, err_msg=name)
+    # (b) g, then a zero gradient
+    w = w0.copy()
+    m = np.zeros(n, np.float32)
+    v = np.zeros(n, np.float32)
+    oracle.adam_update(cfg, w, g.copy(), m, v, 1, hp)
+    w1 = w.copy()
+    oracle.adam_update(cfg, w, np.zeros(n, np.float32), m, v, 2, hp)
+    for name, lr, wd, b1, b2 in groups:
+        o, k = lay[name]
+        gg = g[o:o + k].astype(np.float64)
+        mh = b1 * gg / (1 + b1)
+        vh = b2 * gg * gg / (1 + b2)
+        ref = w1[o:o + k] - lr * (mh / (np.sqrt(vh) + 1e-8) + wd * w1[o:o + k].astype(np.float64))
+        np.testing.assert_allclose(w[o:o + k], ref, rtol=2e-6, atol=2e-7, err_msg=name)
