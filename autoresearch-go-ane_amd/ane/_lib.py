@@ -108,8 +108,13 @@ SIGNATURES = {
     "ane_debug_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, C.c_float, C.c_int, _u16,
                                       _u16, _fp]),
     "ane_debug_transpose2": (C.c_int, [C.c_int, C.c_int, _u16, _u16, C.c_int, C.c_int, _u16, _u16]),
+    "ane_debug_classifier": (C.c_int, [C.c_int, C.c_int, C.c_int, _u16, _u16, _u16, C.c_int, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, _fp, _fp, _fp, _fp, _fp, _u16, _u16]),
     "ane_debug_last_error": (C.c_char_p, []),
     "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 12 + [_u16, _u16, _fp]),
+    "ane_head_loss": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "ane_op_last_error": (C.c_char_p, []),
     "ane_decode_open": (C.c_int, [C.POINTER(DecodeCfg), C.POINTER(C.c_void_p)]),
     "ane_decode_destroy": (None, [_eng]),
     "ane_decode_last_error": (C.c_char_p, [_eng]),

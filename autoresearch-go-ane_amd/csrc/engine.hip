@@ -142,6 +142,44 @@ void prof_end(ane_engine* e, double flops, double bytes) {
   e->prof_next++;
 }
 
+// Phase timers: a pair of events per kernel group of one training call.
+// The pool only grows (hipEventCreate on the host; training never runs
+// under graph capture); a failed create or record leaves the phase untimed.
+void phase_reset(ane_engine* e) {
+  e->ph_used = 0;
+  e->ph_open = false;
+  e->ph_cls.clear();
+}
+
+void phase_begin(ane_engine* e, int phase) {
+  e->ph_open = false;
+  while ((int)e->ph_ev.size() < e->ph_used + 2) {
+    hipEvent_t ev = nullptr;
+    if (hipEventCreate(&ev) != hipSuccess) return;
+    e->ph_ev.push_back(ev);
+  }
+  if (hipEventRecord(e->ph_ev[e->ph_used], e->stream) != hipSuccess) return;
+  e->ph_cls.push_back(phase);
+  e->ph_used += 2;
+  e->ph_open = true;
+}
+
+void phase_end(ane_engine* e) {
+  if (!e->ph_open) return;
+  e->ph_open = false;
+  if (hipEventRecord(e->ph_ev[e->ph_used - 1], e->stream) != hipSuccess) e->ph_cls.back() = -1;
+}
+
+void phase_sum(ane_engine* e, double ms[PH_COUNT]) {
+  for (int p = 0; p < PH_COUNT; p++) ms[p] = 0.0;
+  for (size_t i = 0; i < e->ph_cls.size(); i++) {
+    const int p = e->ph_cls[i];
+    float t = 0.f;
+    if (p >= 0 && p < PH_COUNT && hipEventElapsedTime(&t, e->ph_ev[2 * i], e->ph_ev[2 * i + 1]) == hipSuccess)
+      ms[p] += t;
+  }
+}
+
 hipError_t eng_gemm(ane_engine* e, int cls, const half_t* A, int lda, bool at, const half_t* B, int ldb, bool bt,
                     int M, int N, int K, int epi, const EpiParams& p, int bm, int bn) {
   GemmArgs g;
@@ -179,6 +217,10 @@ static void free_all(ane_engine* e) {
       (void)hipEventDestroy(ev);
       ev = nullptr;
     }
+  for (hipEvent_t ev : e->ph_ev) (void)hipEventDestroy(ev);
+  e->ph_ev.clear();
+  e->ph_cls.clear();
+  e->ph_used = 0;
   e->train_ready = false;
   e->tr = TrainBufs();
   e->ls.clear();
@@ -855,6 +897,70 @@ extern "C" int ane_debug_gemm_epi(int epi, int M, int N, int K, const uint16_t* 
   if (C2) DBGCHK(hipMemcpy(C2, dC2, c2bytes, hipMemcpyDeviceToHost));
 done:
   for (void* q : {dA, dB, dC, dC2, dX0, dR})
+    if (q) (void)hipFree(q);
+  return rc;
+}
+
+// The classifier epilogues on one forced tile (host buffers): EPI_CE writes
+// per-(block row, column) partials (max, sum exp(v - max)) and the target
+// logit of every column; with lse given, EPI_DLOGITS then writes the
+// vocab-major dlogits dl [M, N] and, when dl_t is given, the token-major
+// copy [N, M].  A [M, K] = classifier rows (vocabulary), B [N, K] = tokens.
+extern "C" int ane_debug_classifier(int M, int N, int K, const uint16_t* A, const uint16_t* B,
+                                    const uint16_t* targets, int softcap, int vocab, int bm, int bn, int nw,
+                                    float* part_max, float* part_sum, float* tgt_logit, const float* lse,
+                                    const float* colscale, uint16_t* dl, uint16_t* dl_t) {
+  if (bm <= 0 || bn <= 0 || M % bm || N % bn || !A || !B || !targets || !part_max || !part_sum || !tgt_logit ||
+      (lse && (!colscale || !dl))) {
+    g_debug_err = "storiesane debug classifier: tile must divide M, N; operands missing";
+    return ANE_ERR_ARG;
+  }
+  int rc = ANE_OK;
+  const size_t MN = (size_t)M * N, np = (size_t)(M / bm) * N;
+  void *dA = nullptr, *dB = nullptr, *dT = nullptr, *dP = nullptr, *dTL = nullptr, *dL = nullptr, *dS = nullptr,
+       *dC = nullptr, *dC2 = nullptr;
+  std::vector<float2> part(np);
+  GemmArgs g;
+  EpiParams p;
+  DBGCHK(hipMalloc(&dA, (size_t)M * K * 2));
+  DBGCHK(hipMalloc(&dB, (size_t)N * K * 2));
+  DBGCHK(hipMalloc(&dT, (size_t)N * 2));
+  DBGCHK(hipMalloc(&dP, np * sizeof(float2)));
+  DBGCHK(hipMalloc(&dTL, (size_t)N * 4));
+  DBGCHK(hipMemcpy(dA, A, (size_t)M * K * 2, hipMemcpyHostToDevice));
+  DBGCHK(hipMemcpy(dB, B, (size_t)N * K * 2, hipMemcpyHostToDevice));
+  DBGCHK(hipMemcpy(dT, targets, (size_t)N * 2, hipMemcpyHostToDevice));
+  DBGCHK(hipMemset(dTL, 0xff, (size_t)N * 4));  // NaN: a column whose target no lane claimed stays NaN
+  g.A = (const half_t*)dA; g.B = (const half_t*)dB;
+  g.lda = K; g.ldb = K; g.M = M; g.N = N; g.K = K; g.a_t = false; g.b_t = false;
+  p.targets = (const uint16_t*)dT; p.partial = (float2*)dP; p.tgt_logit = (float*)dTL;
+  p.softcap = softcap != 0; p.cap = 15.f; p.vocab = vocab;
+  DBGCHK(gemm_run(g, EPI_CE, p, nullptr, bm, bn, nw, 0));
+  DBGCHK(hipDeviceSynchronize());
+  DBGCHK(hipMemcpy(part.data(), dP, np * sizeof(float2), hipMemcpyDeviceToHost));
+  DBGCHK(hipMemcpy(tgt_logit, dTL, (size_t)N * 4, hipMemcpyDeviceToHost));
+  for (size_t i = 0; i < np; i++) {
+    part_max[i] = part[i].x;
+    part_sum[i] = part[i].y;
+  }
+  if (lse) {
+    DBGCHK(hipMalloc(&dL, (size_t)N * 4));
+    DBGCHK(hipMalloc(&dS, (size_t)N * 4));
+    DBGCHK(hipMalloc(&dC, MN * 2));
+    if (dl_t) DBGCHK(hipMalloc(&dC2, MN * 2));
+    DBGCHK(hipMemcpy(dL, lse, (size_t)N * 4, hipMemcpyHostToDevice));
+    DBGCHK(hipMemcpy(dS, colscale, (size_t)N * 4, hipMemcpyHostToDevice));
+    EpiParams q;
+    q.targets = (const uint16_t*)dT; q.lse = (const float*)dL; q.colscale = (const float*)dS;
+    q.softcap = softcap != 0; q.cap = 15.f; q.vocab = vocab;
+    q.C = dC; q.ldc = N; q.C2 = dC2; q.ldc2 = M;
+    DBGCHK(gemm_run(g, EPI_DLOGITS, q, nullptr, bm, bn, nw, 0));
+    DBGCHK(hipDeviceSynchronize());
+    DBGCHK(hipMemcpy(dl, dC, MN * 2, hipMemcpyDeviceToHost));
+    if (dl_t) DBGCHK(hipMemcpy(dl_t, dC2, MN * 2, hipMemcpyDeviceToHost));
+  }
+done:
+  for (void* q : {dA, dB, dT, dP, dTL, dL, dS, dC, dC2})
     if (q) (void)hipFree(q);
   return rc;
 }

@@ -158,8 +158,17 @@ struct ane_engine {
   bool train_ready = false;
   TrainBufs tr;
   double start_s = 0.0;  // wall clock at open (CumWallMS)
-  hipEvent_t step_ev[4] = {nullptr, nullptr, nullptr, nullptr};  // step start, head start/end, adam start
+  // step start, final head start / end, end of the backward, Adam start / end
+  enum { EV_STEP0 = 0, EV_HEAD0, EV_HEAD1, EV_BWD1, EV_ADAM0, EV_ADAM1, EV_COUNT };
+  hipEvent_t step_ev[EV_COUNT] = {};
   bool flushed = false;
+  // phase timers of one training call (StepResult, ane/engine.go:55-69):
+  // event pairs around kernel groups, summed per phase after the call
+  std::vector<hipEvent_t> ph_ev;  // pool, grown on the host outside any graph capture
+  std::vector<int> ph_cls;        // phase of each recorded pair
+  int ph_used = 0;
+  bool ph_open = false;
+  int64_t startup_ns = 0;  // host time of this call's one-time training set-up
 
   // eval forward + loss replayed as one HIP graph per batch size (the
   // kernels read only buffers fixed at open; ANE_GRAPHS=0 runs them eagerly)
@@ -206,4 +215,10 @@ hipError_t dalloc(ane_engine* e, T** p, size_t n) {
   return r;
 }
 int head_loss(ane_engine* e, int nseq, float* colscale, float dscale);
+enum StepPhase { PH_EMBED_GRAD = 0, PH_RMS_DW, PH_DW_GEMM, PH_REFRESH, PH_COUNT };
+void phase_reset(ane_engine* e);
+void phase_begin(ane_engine* e, int phase);
+void phase_end(ane_engine* e);
+// after the stream has drained: milliseconds per phase
+void phase_sum(ane_engine* e, double ms[PH_COUNT]);
 int load_windows(ane_engine* e, const uint64_t* positions, int nseq);

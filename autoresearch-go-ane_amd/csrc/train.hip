@@ -41,6 +41,7 @@ double now_s() {
 
 int ensure_train(ane_engine* e, const char* op) {
   if (e->train_ready) return ANE_OK;
+  const double t_start = now_s();
   drop_fwd_graph(e);  // eng_gemm may pick other shapes once the split-K workspace exists
   const ane_model_cfg& c = e->cfg;
   const bool llama = c.arch == ANE_ARCH_LLAMA2;
@@ -121,10 +122,13 @@ int ensure_train(ane_engine* e, const char* op) {
   HIPCHK(op, dalloc(e, &tb.dot_part, (nblk > 256 ? nblk : 256) * 2));
   HIPCHK(op, dalloc(e, &tb.sumsq, 1));
   HIPCHK(op, dalloc(e, &tb.sumsq_part, kSumsqBlocks));
-  for (int i = 0; i < 4; i++) HIPCHK(op, hipEventCreate(&e->step_ev[i]));
+  for (hipEvent_t& ev : e->step_ev) HIPCHK(op, hipEventCreate(&ev));
   int rc = refresh_shadows(e);
   if (rc) return rc;
+  HIPCHK(op, hipStreamSynchronize(e->stream));
   e->train_ready = true;
+  // the one-time set-up the reference's Prepare() does (StartupCompileDuration)
+  e->startup_ns += (int64_t)((now_s() - t_start) * 1e9);
   return ANE_OK;
 }
 
@@ -149,7 +153,7 @@ int backward_pass(ane_engine* e, int nseq) {
   if (rc) return rc;
 
   // ---- final head (runFinalHead, ane/train_full.go:480-558) ----------------
-  (void)hipEventRecord(e->step_ev[1], st);
+  (void)hipEventRecord(e->step_ev[ane_engine::EV_HEAD0], st);
   rc = head_loss(e, nseq, tb.colscale, e->opt.loss_scale * kDlScale);
   if (rc) return rc;
   {
@@ -166,8 +170,10 @@ int backward_pass(ane_engine* e, int nseq) {
   {  // classifier part of the embedding gradient (MatMulGradEmbedScale, ane/stories/cpu.go:366-385)
     EpiParams p;
     p.C = G + pm.embed; p.ldc = D; p.scale = 1.f / kDlScale; p.accumulate = 1;
+    phase_begin(e, PH_EMBED_GRAD);
     HIPCHK(op, transpose_h(tb.op_b, e->xh, T, D, D, T, st));
     HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, tb.op_b, T, false, V, D, T, EPI_STORE_F, p));
+    phase_end(e);
   }
   {  // final RMSNorm backward (+ backout backward for nanochat)
     NormBwdArgs a;
@@ -179,14 +185,16 @@ int backward_pass(ane_engine* e, int nseq) {
     }
     HIPCHK(op, norm_bwd(a, st));
     if (llama) {
+      phase_begin(e, PH_RMS_DW);
       HIPCHK(op, reduce_partials_add(G + pm.g_final, tb.dgain_part, nblk, D, st));
+      phase_end(e);
     } else {
       HIPCHK(op, backout_bwd(tb.ginj, tb.dot_part, tb.dcur, e->xmid, P + pm.backout_lambda, T, D, st));
       HIPCHK(op, reduce_dots_add(G + pm.backout_lambda, nullptr, tb.dot_part, 256, -1.f, st));
       HIPCHK(op, fill_f32(tb.gx0, (size_t)T * D, 0.f, st));
     }
   }
-  (void)hipEventRecord(e->step_ev[2], st);
+  (void)hipEventRecord(e->step_ev[ane_engine::EV_HEAD1], st);
 
   // ---- layers, last to first ------------------------------------------------
   for (int l = L - 1; l >= 0; l--) {
@@ -210,12 +218,15 @@ int backward_pass(ane_engine* e, int nseq) {
     {  // dW2 += dOut gate^T
       EpiParams p;
       p.C = G + o.w2; p.ldc = H; p.accumulate = 1;
+      phase_begin(e, PH_DW_GEMM);
       HIPCHK(op, transpose2_h(tb.op_a, tb.dcur_h, T, D, D, T, tb.op_b, A.gate, T, H, H, T, st));
       HIPCHK(op, eng_gemm(e, 3, tb.op_a, T, false, tb.op_b, T, false, D, H, T, EPI_STORE_F, p));
+      phase_end(e);
     }
     {  // dW1 (| dW3) += dh x2Norm^T
       EpiParams p;
       p.C = G + o.w1; p.ldc = D; p.accumulate = 1;
+      phase_begin(e, PH_DW_GEMM);
       HIPCHK(op, transpose2_h(tb.op_a, tb.dh13, T, KH, KH, T, tb.op_b, A.xn2, T, D, D, T, st));
       if (llama) {
         p.C3 = G + o.w3;
@@ -223,6 +234,7 @@ int backward_pass(ane_engine* e, int nseq) {
       } else {
         HIPCHK(op, eng_gemm(e, 2, tb.op_a, T, false, tb.op_b, T, false, KH, D, T, EPI_STORE_F, p));
       }
+      phase_end(e);
     }
     {  // dx2 = rl * dOut + RMSNorm-backward(dxn2; x2)
       NormBwdArgs a;
@@ -234,9 +246,11 @@ int backward_pass(ane_engine* e, int nseq) {
         a.lam_x = A.x2; a.lam_x0 = e->x0; a.lam_part = tb.dot_part; a.gx0 = tb.gx0; a.xl_p = xl_p;
       }
       HIPCHK(op, norm_bwd(a, st));
-      if (llama)
+      if (llama) {
+        phase_begin(e, PH_RMS_DW);
         HIPCHK(op, reduce_partials_add(G + o.g_ffn, tb.dgain_part, nblk, D, st));
-      else
+        phase_end(e);
+      } else
         HIPCHK(op, reduce_dots_add(G + pm.resid + l, G + pm.x0l + l, tb.dot_part, nblk, 1.f, st));
     }
     // attention (backwardAttentionCPU, ane/train_full.go:644-675)
@@ -248,8 +262,10 @@ int backward_pass(ane_engine* e, int nseq) {
     {
       EpiParams p;
       p.C = G + o.wo; p.ldc = D; p.accumulate = 1;
+      phase_begin(e, PH_DW_GEMM);
       HIPCHK(op, transpose2_h(tb.op_a, tb.dx2_h, T, D, D, T, tb.op_b, A.att, T, D, D, T, st));
       HIPCHK(op, eng_gemm(e, 1, tb.op_a, T, false, tb.op_b, T, false, D, D, T, EPI_STORE_F, p));
+      phase_end(e);
     }
     {
       AttnBwdArgs b;
@@ -293,8 +309,10 @@ int backward_pass(ane_engine* e, int nseq) {
     {  // dWq | dWk | dWv += dqkv xNorm^T
       EpiParams p;
       p.C = G + o.wq; p.ldc = D; p.accumulate = 1;
+      phase_begin(e, PH_DW_GEMM);
       HIPCHK(op, transpose2_h(tb.op_a, tb.dqkv, T, 3 * D, 3 * D, T, tb.op_b, A.xn, T, D, D, T, st));
       HIPCHK(op, eng_gemm(e, 0, tb.op_a, T, false, tb.op_b, T, false, 3 * D, D, T, EPI_STORE_F, p));
+      phase_end(e);
     }
     {  // dPrev = rl * dx2 + RMSNorm-backward(dxn; x) (+ VE gate grads, + backout injection)
       NormBwdArgs a;
@@ -308,9 +326,11 @@ int backward_pass(ane_engine* e, int nseq) {
         if (l == L / 2) a.addend2 = tb.ginj;  // ane/train_full.go:784-787
       }
       HIPCHK(op, norm_bwd(a, st));
-      if (llama)
+      if (llama) {
+        phase_begin(e, PH_RMS_DW);
         HIPCHK(op, reduce_partials_add(G + o.g_att, tb.dgain_part, nblk, D, st));
-      else
+        phase_end(e);
+      } else
         HIPCHK(op, reduce_dots_add(G + pm.resid + l, G + pm.x0l + l, tb.dot_part, nblk, 1.f, st));
     }
   }
@@ -326,8 +346,10 @@ int backward_pass(ane_engine* e, int nseq) {
     {
       EpiParams p;
       p.C = G + pm.smear_gate; p.ldc = D; p.accumulate = 1;
+      phase_begin(e, PH_DW_GEMM);
       HIPCHK(op, transpose2_h(tb.op_a, tb.dgp, T, D, D, T, tb.op_b, tb.x0h, T, D, D, T, st));
       HIPCHK(op, eng_gemm(e, 7, tb.op_a, T, false, tb.op_b, T, false, D, D, T, EPI_STORE_F, p));
+      phase_end(e);
     }
     {
       EpiParams p;
@@ -339,7 +361,10 @@ int backward_pass(ane_engine* e, int nseq) {
     a.dy = tb.dx2; a.x = e->xpre; a.T = T; a.D = D; a.out = tb.dcur;
     HIPCHK(op, norm_bwd(a, st));
   }
+  phase_begin(e, PH_EMBED_GRAD);  // EmbedBackward (ane/train_full.go:930-933)
   HIPCHK(op, embed_bwd(G + pm.embed, tb.dcur, e->tok, T, D, V, st));
+  phase_end(e);
+  (void)hipEventRecord(e->step_ev[ane_engine::EV_BWD1], st);
   return ANE_OK;
 }
 
@@ -408,9 +433,14 @@ int flush_pending(ane_engine* e) {
     add_seg(a, pm.resid, 2 * L, lambda_lr, 0.f, O.lambda_beta1, O.lambda_beta2, l1, l2, 0);
   }
   if (a.nseg > kMaxAdamSegs) return eng_fail(e, ANE_ERR_ARG, "storiesane flush: too many parameter groups");
-  (void)hipEventRecord(e->step_ev[3], st);
+  (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM0], st);
   HIPCHK(op, adam_update(a, st));
+  (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM1], st);
+  // the fp16 shadows the next forward reads: the weight refresh
+  // (refreshANERuntimeForWeights, ane/runtime.go:25-69)
+  phase_begin(e, PH_REFRESH);
   int rc = refresh_shadows(e);
+  phase_end(e);
   if (rc) return rc;
   HIPCHK(op, fill_f32(tb.G, (size_t)pm.total, 0.f, st));
   e->state.pending_steps = 0;
@@ -419,9 +449,14 @@ int flush_pending(ane_engine* e) {
   return ANE_OK;
 }
 
-int read_losses(ane_engine* e, int nseq, float* per, double* mean) {
+// *wait_s (optional): host time spent blocked until the queued device work
+// (forward, backward, weight-gradient GEMMs, update) had finished
+int read_losses(ane_engine* e, int nseq, float* per, double* mean, double* wait_s = nullptr) {
   const char* op = "step";
   std::vector<float> ls(nseq);
+  const double t0 = now_s();
+  HIPCHK(op, hipStreamSynchronize(e->stream));
+  if (wait_s) *wait_s = now_s() - t0;
   HIPCHK(op, hipMemcpyAsync(ls.data(), e->loss_seq, (size_t)nseq * 4, hipMemcpyDeviceToHost, e->stream));
   HIPCHK(op, hipStreamSynchronize(e->stream));
   double tot = 0;
@@ -442,8 +477,10 @@ int train_windows(ane_engine* e, int nseq, ane_step_result* res) {
   if (!e->data || e->ndata < (int64_t)e->cfg.seq + 1) return eng_fail(e, ANE_ERR_STATE, "storiesane step: not enough tokens");
   if (nseq <= 0 || nseq > e->opt.max_batch)
     return eng_fail(e, ANE_ERR_ARG, "storiesane step: nseq=%d must be in [1, %d]", nseq, e->opt.max_batch);
+  e->startup_ns = 0;
   int rc = ensure_train(e, op);
   if (rc) return rc;
+  phase_reset(e);
   const uint64_t S = (uint64_t)e->cfg.seq;
   const uint64_t limit = (uint64_t)e->ndata - S - 1;
   std::vector<uint64_t> pos(nseq);
@@ -459,7 +496,7 @@ int train_windows(ane_engine* e, int nseq, ane_step_result* res) {
   rc = load_windows(e, pos.data(), nseq);
   if (rc) return rc;
   e->flushed = false;
-  (void)hipEventRecord(e->step_ev[0], e->stream);
+  (void)hipEventRecord(e->step_ev[ane_engine::EV_STEP0], e->stream);
   rc = backward_pass(e, nseq);
   if (rc) return rc;
   e->state.pending_steps += (uint32_t)nseq;
@@ -467,8 +504,8 @@ int train_windows(ane_engine* e, int nseq, ane_step_result* res) {
     rc = flush_pending(e);
     if (rc) return rc;
   }
-  double mean = 0;
-  rc = read_losses(e, nseq, nullptr, &mean);
+  double mean = 0, wait_s = 0;
+  rc = read_losses(e, nseq, nullptr, &mean, &wait_s);
   if (rc) return rc;
   const double dt = now_s() - t0;
   e->state.last_loss = (float)mean;
@@ -476,21 +513,31 @@ int train_windows(ane_engine* e, int nseq, ane_step_result* res) {
   e->state.cum_train_ms += dt * 1e3;
   e->state.cum_wall_ms = (now_s() - e->start_s) * 1e3;
   if (res) {
+    // StepResult (ane/engine.go:416-441): device phases from HIP events,
+    // host durations from the wall clock
     memset(res, 0, sizeof *res);
+    auto ev_ns = [&](int a, int b) -> int64_t {
+      float ms = 0.f;
+      return hipEventElapsedTime(&ms, e->step_ev[a], e->step_ev[b]) == hipSuccess ? (int64_t)((double)ms * 1e6) : 0;
+    };
+    double ph[PH_COUNT];
+    phase_sum(e, ph);
     res->loss = (float)mean;
     res->step_ns = (int64_t)(dt * 1e9);
-    float ms = 0.f;
-    if (hipEventElapsedTime(&ms, e->step_ev[0], e->step_ev[e->flushed ? 3 : 2]) == hipSuccess)
-      res->ane_eval_ns = (int64_t)((double)ms * 1e6);
-    if (hipEventElapsedTime(&ms, e->step_ev[1], e->step_ev[2]) == hipSuccess)
-      res->final_head_ns = (int64_t)((double)ms * 1e6);
+    res->startup_compile_ns = e->startup_ns;
+    res->ane_eval_ns = ev_ns(ane_engine::EV_STEP0, ane_engine::EV_BWD1);  // forward + backward kernels
+    res->final_head_ns = ev_ns(ane_engine::EV_HEAD0, ane_engine::EV_HEAD1);
+    res->embed_grad_ns = (int64_t)(ph[PH_EMBED_GRAD] * 1e6);
+    res->rms_dw_ns = (int64_t)(ph[PH_RMS_DW] * 1e6);
+    res->dw_gemm_ns = (int64_t)(ph[PH_DW_GEMM] * 1e6);
+    res->dw_wait_ns = (int64_t)(wait_s * 1e9);
     if (e->flushed) {
-      (void)hipEventRecord(e->step_ev[1], e->stream);  // reuse: end of Adam + refresh
-      (void)hipEventSynchronize(e->step_ev[1]);
-      if (hipEventElapsedTime(&ms, e->step_ev[3], e->step_ev[1]) == hipSuccess)
-        res->adam_ns = (int64_t)((double)ms * 1e6);
+      res->adam_ns = ev_ns(ane_engine::EV_ADAM0, ane_engine::EV_ADAM1);
+      res->weight_refresh_ns = (int64_t)(ph[PH_REFRESH] * 1e6);
     }
-    res->cpu_work_ns = res->step_ns - res->ane_eval_ns - res->adam_ns;
+    res->compile_ns = res->startup_compile_ns + res->weight_refresh_ns;
+    res->cpu_work_ns = res->step_ns - res->startup_compile_ns - res->weight_refresh_ns - res->ane_eval_ns -
+                       res->adam_ns;
     if (res->cpu_work_ns < 0) res->cpu_work_ns = 0;
   }
   return ANE_OK;
@@ -511,13 +558,22 @@ extern "C" int ane_train_batch(ane_engine* e, int32_t nseq, ane_step_result* res
   return train_windows(e, nseq, res);
 }
 
+// Flush (ane/engine.go:484-496): returns the weight-refresh duration (the
+// reference's waitAsyncRefresh) and adds it to CumTrainMS / CumWallMS.
 extern "C" int ane_flush(ane_engine* e, int64_t* ns) {
   CLOSED_CHECK("flush");
-  const double t0 = now_s();
+  phase_reset(e);
   int rc = flush_pending(e);
   if (rc) return rc;
   HIPCHK("flush", hipStreamSynchronize(e->stream));
-  if (ns) *ns = (int64_t)((now_s() - t0) * 1e9);
+  double ph[PH_COUNT];
+  phase_sum(e, ph);
+  const int64_t refresh_ns = (int64_t)(ph[PH_REFRESH] * 1e6);
+  if (refresh_ns > 0) {
+    e->state.cum_train_ms += (double)refresh_ns / 1e6;
+    e->state.cum_wall_ms = (now_s() - e->start_s) * 1e3;
+  }
+  if (ns) *ns = refresh_ns;
   return ANE_OK;
 }
 

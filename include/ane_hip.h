@@ -82,8 +82,23 @@ typedef struct ane_state {
 } ane_state;
 
 /* StepResult (ane/engine.go:55-69); durations in nanoseconds.  The ANE /
- * compile fields keep their names; on this engine "ane_eval_ns" is the
- * device time of the forward and backward kernels (HIP events). */
+ * compile fields keep their names.  On this engine (device times from HIP
+ * events on the engine's stream, host times from the wall clock):
+ *   step_ns             host wall time of the call
+ *   startup_compile_ns  one-time training set-up (buffers, transposed
+ *                       shadows) when this call did it, else 0
+ *   compile_ns          startup_compile_ns + weight_refresh_ns
+ *   ane_eval_ns         device time of the forward and backward kernels
+ *   weight_refresh_ns   device time of the fp16 shadow rebuild after an update
+ *   final_head_ns       classifier, cross-entropy, dlogits, dy, classifier
+ *                       weight gradient, final-norm backward
+ *   embed_grad_ns       classifier weight gradient + embedding scatter-add
+ *   rms_dw_ns           norm-gain gradient reductions (llama2; 0 for nanochat,
+ *                       whose norms have no weights)
+ *   dw_gemm_ns          weight-gradient GEMMs with their operand transposes
+ *   dw_wait_ns          host time blocked until the queued device work ended
+ *   adam_ns             clip + AdamW kernels when the call flushed
+ *   cpu_work_ns         step_ns minus the set-up, refresh, eval and Adam times */
 typedef struct ane_step_result {
   float loss;
   int64_t step_ns, compile_ns, startup_compile_ns, ane_eval_ns, cpu_work_ns, weight_refresh_ns,
@@ -157,7 +172,10 @@ int ane_step(ane_engine *e, ane_step_result *res);
  * sequence per call).  res->loss is the mean over the nseq windows. */
 int ane_train_batch(ane_engine *e, int32_t nseq, ane_step_result *res);
 /* Flush (ane/engine.go:484-496): applies pending accumulated gradients;
- * *ns receives the wall time. */
+ * *ns receives the weight-refresh duration (the device time of the fp16
+ * shadow rebuild after the update; the reference returns its asynchronous
+ * refresh time), which is also added to cum_train_ms / cum_wall_ms; 0 when
+ * nothing was pending. */
 int ane_flush(ane_engine *e, int64_t *ns);
 /* LR / SetLR (ane/engine.go:358-376); SetLR rejects lr <= 0 with
  * "storiesane set lr: lr must be > 0". */
@@ -243,6 +261,19 @@ int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float
  * (rows and columns multiples of 64). */
 int ane_debug_transpose2(int Ra, int Ca, const uint16_t *in_a, uint16_t *out_a, int Rb, int Cb,
                          const uint16_t *in_b, uint16_t *out_b);
+/* The classifier epilogues on one forced block tile (bm x bn, nw waves):
+ * A [M, K] classifier rows, B [N, K] token rows (fp16), targets [N].
+ * Cross-entropy partials (the loss path of runFinalHead /
+ * stories.CrossEntropyLoss, ane/train_full.go:480-508, ane/stories/cpu.go:
+ * 212-292): part_max / part_sum [M/bm][N] receive each block row's
+ * (max, sum exp(v - max)) of every column (v = 15 tanh(acc/15) when
+ * softcap), tgt_logit [N] the target's logit.  With lse [N] and colscale [N]
+ * given, the dlogits epilogue then writes dl [M, N] (fp16, vocab-major:
+ * (softmax - onehot) * colscale, rows >= vocab zero) and, if dl_t is not
+ * NULL, the token-major copy [N, M]. */
+int ane_debug_classifier(int M, int N, int K, const uint16_t *A, const uint16_t *B, const uint16_t *targets,
+                         int softcap, int vocab, int bm, int bn, int nw, float *part_max, float *part_sum,
+                         float *tgt_logit, const float *lse, const float *colscale, uint16_t *dl, uint16_t *dl_t);
 /* Mean time of `iters` launches of one GEMM on device-resident operands
  * (arguments as ane_debug_gemm; A / B NULL: pseudo-random in [-0.5, 0.5)).
  * epi: 0 fp16 store, 1 fp32 store, 3 in-place residual add, 4 SwiGLU over
@@ -250,6 +281,29 @@ int ane_debug_transpose2(int Ra, int Ca, const uint16_t *in_a, uint16_t *out_a, 
 int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw, int ns,
                          int splits, int iters, const uint16_t *A, const uint16_t *B, float *avg_ms);
 const char *ane_debug_last_error(void);
+
+/* ---- classifier-head loss on device buffers -------------------------------
+ * The loss half of runFinalHead (ane/train_full.go:480-508) as a standalone
+ * operation on caller-owned device memory: tied-classifier logits
+ * embed . xn (ane/stories/cpu.go:303-327), the 15*tanh softcap when softcap
+ * != 0 (ane/common.go:272-287), and stories.CrossEntropyLoss
+ * (ane/stories/cpu.go:212-292): per token -log(max(p_target, 1e-10)),
+ * averaged over the valid targets (< vocab) of each sequence (0 when a
+ * sequence has none).  No logit is materialised.
+ *   xn      [ntok][dim] fp16   normalised final hidden states (token-major)
+ *   embed   [vocab][dim] fp16  classifier rows
+ *   targets [ntok] uint16
+ *   loss_seq [ntok/seq] fp32   per-sequence mean cross-entropy (output)
+ *   lse      [ntok] fp32       per-token log-sum-exp (output; may be NULL)
+ * ntok a multiple of seq and of 64; dim, vocab multiples of 64.  stream: a
+ * hipStream_t (NULL: the default stream).  The call allocates its scratch
+ * (cross-entropy partials) with hipMalloc, waits for the stream and frees
+ * it.  Errors: ANE_ERR_ARG / ANE_ERR_NOMEM / ANE_ERR_HIP, message in
+ * ane_op_last_error() (per thread).  No counterpart in the reference, whose
+ * loss runs on host slices inside Step / EvalLogits. */
+int ane_head_loss(const uint16_t *xn, const uint16_t *embed, const uint16_t *targets, int32_t ntok, int32_t dim,
+                  int32_t vocab, int32_t seq, int32_t softcap, float *loss_seq, float *lse, void *stream);
+const char *ane_op_last_error(void);
 
 /* ---- greedy KV-cache decoder (grouped-query attention) --------------------
  * No counterpart in the reference, which evaluates whole windows only

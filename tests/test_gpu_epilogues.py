@@ -143,3 +143,69 @@ def test_192_wide_tiles(tile):
     out = np.zeros((m, n), np.float32)
     run(EPI_RESID, A, B, out, X0=X0, R=R, alpha=0.75, beta=-0.5, tile=tile)
     close32(out, 0.75 * R.astype(np.float64) + acc - 0.5 * X0.astype(np.float64))
+
+
+CE_TILES = [(256, 256, 8), (256, 256, 4), (256, 128, 4), (128, 256, 4), (128, 128, 4), (64, 128, 4),
+            (128, 64, 4), (64, 64, 4)]
+
+
+@pytest.mark.parametrize("softcap", [0, 1])
+@pytest.mark.parametrize("tile", CE_TILES)
+def test_classifier_ce_and_dlogits(tile, softcap):
+    """The classifier's cross-entropy epilogue (per-block (max, sum exp)
+    partials and the target logit) and the dlogits epilogue, on every tile
+    the dispatcher offers for them, including the 8-wave 256x256 tile the
+    engine picks at B32 x 256 (rows = vocabulary, columns = tokens), against
+    float64 log-sum-exp and softmax of the same fp16 operands."""
+    lib = _lib.load()
+    bm, bn, nw = tile
+    Mv, Nt, Kd = 1024, 512, 192
+    r = np.random.default_rng(70 + bm + bn + nw + softcap)
+    A = (r.standard_normal((Mv, Kd)) * (1.0 if softcap else 0.35)).astype(np.float16)
+    B = (r.standard_normal((Nt, Kd)) * 0.5).astype(np.float16)
+    tg = r.integers(0, Mv, Nt).astype(np.uint16)
+    tg[::37] = 65535                       # excluded targets: no lane claims them
+    tg[1], tg[2], tg[3] = 0, Mv - 1, bm    # first, last row, first row of the second block row
+    acc = A.astype(np.float64) @ B.astype(np.float64).T   # [Mv, Nt]
+    v = 15.0 * np.tanh(acc / 15.0) if softcap else acc
+    nb = Mv // bm
+    pm = np.zeros((nb, Nt), np.float32)
+    ps = np.zeros((nb, Nt), np.float32)
+    tl = np.zeros(Nt, np.float32)
+    rc = lib.ane_debug_classifier(Mv, Nt, Kd, _u16(A.view(np.uint16)), _u16(B.view(np.uint16)), _u16(tg), softcap,
+                                  Mv, bm, bn, nw, _fp(pm), _fp(ps), _fp(tl), None, None, None, None)
+    assert rc == 0, lib.ane_debug_last_error()
+    # each block row's partial against its own rows
+    for b in range(nb):
+        blk = v[b * bm:(b + 1) * bm]
+        mx = blk.max(axis=0)
+        np.testing.assert_allclose(pm[b], mx, rtol=1e-5, atol=5e-4)
+        np.testing.assert_allclose(ps[b], np.exp(blk - pm[b].astype(np.float64)).sum(axis=0), rtol=2e-4)
+    M_ = pm.astype(np.float64).max(axis=0)
+    lse = M_ + np.log((ps.astype(np.float64) * np.exp(pm.astype(np.float64) - M_)).sum(axis=0))
+    mref = v.max(axis=0)
+    lse_ref = mref + np.log(np.exp(v - mref).sum(axis=0))
+    np.testing.assert_allclose(lse, lse_ref, rtol=0, atol=2e-4)
+    ok = tg < Mv
+    np.testing.assert_allclose(tl[ok], v[tg[ok].astype(np.int64), np.nonzero(ok)[0]], rtol=1e-5, atol=5e-4)
+    assert np.isnan(tl[~ok]).all()
+    # dlogits with a vocabulary end short of the padded rows
+    vocab = Mv - 40
+    cs = (r.random(Nt) * 64.0).astype(np.float32)
+    lse32 = lse_ref.astype(np.float32)
+    dl = np.zeros((Mv, Nt), np.float16)
+    dlt = np.zeros((Nt, Mv), np.float16)
+    rc = lib.ane_debug_classifier(Mv, Nt, Kd, _u16(A.view(np.uint16)), _u16(B.view(np.uint16)), _u16(tg), softcap,
+                                  vocab, bm, bn, nw, _fp(pm), _fp(ps), _fp(tl), _fp(lse32), _fp(cs),
+                                  _u16(dl.view(np.uint16)), _u16(dlt.view(np.uint16)))
+    assert rc == 0, lib.ane_debug_last_error()
+    p = np.exp(v - lse32.astype(np.float64))
+    onehot = np.zeros_like(p)
+    onehot[tg[ok].astype(np.int64), np.nonzero(ok)[0]] = 1.0
+    ref = (p - onehot) * cs.astype(np.float64)
+    if softcap:
+        ref *= 1.0 - np.tanh(acc / 15.0) ** 2
+    ref[vocab:] = 0.0
+    np.testing.assert_allclose(dl.astype(np.float64), ref, rtol=3e-3, atol=2e-3)
+    assert (dl[vocab:] == 0).all()
+    np.testing.assert_array_equal(dlt, dl.T)

@@ -192,3 +192,36 @@ def test_training_error_behaviour():
     with pytest.raises(ane.EngineError, match="storiesane step: engine is closed"):
         eng.Step()
     eng.Destroy()
+
+
+@pytest.mark.parametrize("arch", ["llama2", "nanochat"])
+def test_step_result_phase_timers_and_flush_duration(arch):
+    """StepResult's phase durations (ane/engine.go:416-441) and Flush's
+    return value (the weight-refresh time, added to CumTrainMS,
+    ane/engine.go:484-496)."""
+    cfg = ane.tiny(arch, layers=2)
+    p = ane.init_params(cfg, seed=61, std=0.05)
+    stream = np.random.default_rng(62).integers(0, cfg.vocab, 4000).astype(np.uint16)
+    eng = open_engine(cfg, p, max_batch=2, tokens=stream, AccumSteps=3)
+    try:
+        r1 = eng.TrainBatch(2)           # first call: set-up, no update yet
+        assert r1.startup_compile_ns > 0 and r1.compile_ns == r1.startup_compile_ns
+        assert r1.weight_refresh_ns == 0 and r1.adam_ns == 0
+        for f in ("ane_eval_ns", "final_head_ns", "embed_grad_ns", "dw_gemm_ns"):
+            assert getattr(r1, f) > 0, f
+        assert (r1.rms_dw_ns > 0) == (arch == "llama2")
+        assert r1.dw_gemm_ns + r1.embed_grad_ns < r1.ane_eval_ns <= r1.step_ns
+        assert r1.final_head_ns < r1.ane_eval_ns
+        r2 = eng.TrainBatch(2)           # 4 pending >= 3: clip + AdamW + refresh
+        assert r2.startup_compile_ns == 0
+        assert r2.adam_ns > 0 and r2.weight_refresh_ns > 0 and r2.compile_ns == r2.weight_refresh_ns
+        assert eng.State().pending_steps == 0
+        assert eng.Flush() == 0          # nothing pending
+        eng.Step()                       # one pending window
+        before = eng.State().cum_train_ms
+        ns = eng.Flush()
+        st = eng.State()
+        assert ns > 0 and st.pending_steps == 0 and st.adam_t == 2
+        assert abs((st.cum_train_ms - before) - ns / 1e6) < 1e-6
+    finally:
+        eng.Destroy()
