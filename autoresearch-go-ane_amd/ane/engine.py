@@ -76,20 +76,42 @@ def _u16(a):
     return a.ctypes.data_as(C.POINTER(C.c_uint16))
 
 
+def _load_model(path: str, cfg: Config, training: bool):
+    """Open's weight load (ane/engine.go:240-248): a llama2.c file
+    (LoadPretrained), else a training checkpoint of any version
+    (stories.LoadCheckpoint into fresh weights; its Adam moments too when the
+    engine trains, i.e. Options.Tokens is set).  -> (params, moments|None)."""
+    from .checkpoint import load_pretrained, read_checkpoint
+    try:
+        params, _ = load_pretrained(path, cfg)
+        return params, None
+    except (OSError, ValueError) as err:
+        if cfg.arch == "nanochat":
+            try:
+                _, params, m, v, _ = read_checkpoint(path, cfg)
+                return params, ((m, v) if training else None)
+            except (OSError, ValueError):
+                pass
+        raise EngineError(_lib.ANE_ERR_ARG, f"storiesane open: load model: {err}") from None
+
+
 def Open(opts: Options) -> "Engine":
-    """ane/engine.go:184-355.  Weights come from ``opts.Params``."""
+    """ane/engine.go:184-355.  Weights come from ``opts.Params`` or, as in the
+    reference, from the file at ``opts.ModelPath``: llama2.c weights or a
+    V2-V5 training checkpoint (see ane.checkpoint); the model shape is
+    ``opts.Config`` (stories110M by default), which the file must match."""
     lib = _lib.load()
     if opts.Params is None and not opts.ModelPath:
         raise EngineError(_lib.ANE_ERR_ARG, "storiesane open: model path is empty")
-    if opts.Params is None:
-        raise EngineError(_lib.ANE_ERR_ARG, f"storiesane open: load model: {opts.ModelPath}: "
-                                            "model files are not supported by this engine; pass Params")
     cfg = opts.Config or Config()
     if cfg.kv_heads != cfg.heads:
         raise EngineError(_lib.ANE_ERR_ARG, "storiesane open: grouped-query attention (kv_heads != heads) "
                                             "is served by ane.decode.Decoder only")
     if opts.Seq and opts.Seq != cfg.seq:
         cfg = dataclasses.replace(cfg, seq=opts.Seq)
+    params, moments = opts.Params, None
+    if params is None:
+        params, moments = _load_model(opts.ModelPath, cfg, opts.Tokens is not None and len(opts.Tokens) > 0)
     tokens = None
     if opts.Tokens is not None and len(opts.Tokens) > 0:
         tokens = np.ascontiguousarray(opts.Tokens, dtype=np.uint16)
@@ -108,7 +130,9 @@ def Open(opts: Options) -> "Engine":
         raise EngineError(rc, msg.decode())
     eng = Engine(lib, h, cfg, o)
     try:
-        eng.SetParams(opts.Params)
+        eng.SetParams(params)
+        if moments is not None:
+            eng.SetOptState(*moments)
         if tokens is not None:
             _check(lib, h, lib.ane_set_tokens(h, _u16(tokens), len(tokens)))
             eng._ntokens = len(tokens)
@@ -183,7 +207,8 @@ class Engine:
         return r
 
     def Flush(self) -> int:
-        """ane/engine.go:484-496; returns nanoseconds."""
+        """ane/engine.go:484-496: applies pending gradients; returns the
+        weight-refresh duration in nanoseconds (0 when nothing was pending)."""
         ns = C.c_int64()
         _check(self._lib, self._h, self._lib.ane_flush(self._h, C.byref(ns)))
         return int(ns.value)
@@ -260,7 +285,8 @@ class Engine:
         from .checkpoint import read_checkpoint
         if not self._h:
             raise EngineError(_lib.ANE_ERR_CLOSED, "storiesane load checkpoint: engine is closed")
-        meta, params, m, v, trailer = read_checkpoint(path, self.cfg)
+        # tensors an older version lacks keep the engine's current values
+        meta, params, m, v, trailer = read_checkpoint(path, self.cfg, base=self.Params())
         self.SetParams(params)
         self.SetOptState(m, v)
         self.SetLR(meta.LR)

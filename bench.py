@@ -59,16 +59,36 @@ def measured_traffic(kernel_class):
     return None
 
 
-def cpu_baseline(cfg, params, tok, tgt, threads):
-    """Times the oracle (reference CPU-path semantics) on one sequence."""
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(cfg, params, tok, tgt, threads, k=2, repeats=3):
+    """The reference's CPU path (the C oracle with the reference's threading:
+    serial linearCF, parallelFor over tokens / vocabulary elsewhere) on k of
+    the 32 sequences: one warm-up run, then the median of `repeats` timed
+    runs; tokens/s = k * seq / median.  Sequences are independent, so the
+    B32 cost is 32 / k times this sample's."""
     import oracle
     oracle.set_threads(threads, parallel_linear=False)
-    t0 = time.perf_counter()
-    oracle.forward_loss(cfg, params, tok[:1], tgt[:1])
-    dt = time.perf_counter() - t0
-    return {"value": round(cfg.seq / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"1 of the 32 sequences ({cfg.seq} tokens), {dt:.1f} s; oracle/refcpu.c with the "
-                      "reference's threading (serial linearCF, parallelFor over tokens/vocab elsewhere)"}
+    oracle.forward_loss(cfg, params, tok[:k], tgt[:k])  # warm-up
+    times = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        oracle.forward_loss(cfg, params, tok[:k], tgt[:k])
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": round(k * cfg.seq / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "nproc": os.cpu_count(), "cpu_model": cpu_model(),
+            "sample": f"{k} of the 32 sequences ({k * cfg.seq} tokens), median of {repeats} runs after one warm-up "
+                      f"({', '.join(f'{t:.2f}' for t in times)} s); oracle/refcpu.c with the reference's threading "
+                      "(serial linearCF, parallelFor over tokens/vocab elsewhere) on the CPUs this process may use"}
 
 
 def train_bench(ane, arch, steps, batch=16):
@@ -262,7 +282,9 @@ def main():
     if not args.no_moe:
         out["moe_ffn"] = moe_bench(ane)
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
+        # every CPU this process may run on (on the GPU pool: the 16-CPU share
+        # of one GPU, whatever nproc reports for the whole host)
+        threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
         out["cpu_baseline"] = cpu_baseline(cfg, params, tok, tgt, threads)
         out["gpu_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
     print(json.dumps(out), flush=True)

@@ -58,3 +58,67 @@ def test_checkpoint_round_trip(tmp_path):
             b.Destroy()
     assert losses[0] == losses[1]
     np.testing.assert_allclose(params[0], params[1], rtol=1e-6, atol=1e-7)
+
+
+def test_open_from_model_files(tmp_path):
+    """Open(ModelPath=...) as the reference's Open (ane/engine.go:240-248):
+    a llama2.c file (LoadPretrained) for both architectures, and a training
+    checkpoint, whose Adam moments come along when the engine trains; the
+    device then computes exactly what it computes from the same weights
+    passed directly."""
+    import struct
+    from ane import checkpoint as ck
+    for arch in ("llama2", "nanochat"):
+        cfg = ane.tiny(arch)
+        p = ane.init_params(cfg, seed=8, std=0.08)
+        w = ane.views(cfg, p)
+        path = tmp_path / f"{arch}.bin"
+        with open(path, "wb") as f:
+            f.write(struct.pack("<7i", cfg.dim, cfg.hidden, cfg.layers, cfg.heads, cfg.heads, cfg.vocab, cfg.seq))
+            f.write(w["embed"].tobytes())
+            ones = np.ones(cfg.dim, np.float32)
+            for l in range(cfg.layers):
+                f.write((w[f"layers.{l}.g_att"] if arch == "llama2" else ones).tobytes())
+            for nm in ("wq", "wk", "wv", "wo"):
+                for l in range(cfg.layers):
+                    f.write(w[f"layers.{l}.{nm}"].tobytes())
+            for l in range(cfg.layers):
+                f.write((w[f"layers.{l}.g_ffn"] if arch == "llama2" else ones).tobytes())
+            for nm in ("w1", "w2"):
+                for l in range(cfg.layers):
+                    f.write(w[f"layers.{l}.{nm}"].tobytes())
+            for l in range(cfg.layers):
+                f.write((w[f"layers.{l}.w3"] if arch == "llama2" else np.zeros(cfg.hidden * cfg.dim, np.float32))
+                        .tobytes())
+            f.write((w["g_final"] if arch == "llama2" else ones).tobytes())
+        want, _ = ck.load_pretrained(str(path), cfg)
+        tok, tgt = ane.make_tokens(cfg, 2, seed=9)
+        a = ane.Open(ane.Options(Config=cfg, ModelPath=str(path), MaxBatch=2))
+        b = ane.Open(ane.Options(Config=cfg, Params=want, MaxBatch=2))
+        try:
+            np.testing.assert_array_equal(a.Params(), want)
+            np.testing.assert_array_equal(a.EvalLoss(tok, tgt)[1], b.EvalLoss(tok, tgt)[1])
+        finally:
+            a.Destroy()
+            b.Destroy()
+        if arch == "llama2":   # the file held every llama2 tensor: the model is the one written
+            np.testing.assert_array_equal(want, p)
+    cfg = ane.tiny("nanochat")
+    p = ane.init_params(cfg, seed=10, std=0.08)
+    r = np.random.default_rng(11)
+    m = r.standard_normal(p.size).astype(np.float32)
+    v = r.random(p.size).astype(np.float32)
+    cp = tmp_path / "train.ckpt"
+    ck.write_checkpoint(str(cp), cfg, ck.TrainMeta(Step=2, AdamT=1), p, m, v)
+    stream = r.integers(0, cfg.vocab, 500).astype(np.uint16)
+    e = ane.Open(ane.Options(Config=cfg, ModelPath=str(cp), MaxBatch=1, Tokens=stream))
+    try:
+        np.testing.assert_array_equal(e.Params(), p)
+        m2, v2 = e.OptState()
+        np.testing.assert_array_equal(m2, m)
+        np.testing.assert_array_equal(v2, v)
+        assert e.State().adam_t == 0          # Open keeps fresh counters, as the reference's
+    finally:
+        e.Destroy()
+    with pytest.raises(ane.EngineError, match="storiesane open: load model: "):
+        ane.Open(ane.Options(Config=cfg, ModelPath=str(tmp_path / "missing.bin")))
