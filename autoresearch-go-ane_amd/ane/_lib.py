@@ -114,6 +114,8 @@ SIGNATURES = {
     "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 12 + [_u16, _u16, _fp]),
     "ane_head_loss": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                 C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]),
+    "ane_head_loss_noalloc": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32,
+                                        C.c_int32, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]),
     "ane_op_last_error": (C.c_char_p, []),
     "ane_decode_open": (C.c_int, [C.POINTER(DecodeCfg), C.POINTER(C.c_void_p)]),
     "ane_decode_destroy": (None, [_eng]),

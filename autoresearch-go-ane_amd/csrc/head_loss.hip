@@ -10,10 +10,12 @@
 // then the per-token merge and the per-sequence mean (ce_reduce).  Their
 // scratch -- partials, target logits, per-token losses and, when the caller
 // passes no lse buffer, the log-sum-exps -- is allocated by the library for
-// the duration of the call.
+// the duration of the call (ane_head_loss), or is a fixed array in device
+// global memory (ane_head_loss_noalloc, for callers that cannot allocate).
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
 #include <string>
 
 #include "../../include/ane_hip.h"
@@ -113,6 +115,67 @@ extern "C" int ane_head_loss(const uint16_t* xn, const uint16_t* embed, const ui
   const hipError_t hs = hipStreamSynchronize(st);  // the workspace is freed below
   (void)hipFree(ws);
   if (h == hipSuccess) h = hs;
+  if (h != hipSuccess) return op_fail(ANE_ERR_HIP, "storiesane %s: %s", op, hipGetErrorString(h));
+  return ANE_OK;
+}
+
+// ---- allocation-free variant --------------------------------------------------
+// The scratch of ane_head_loss_noalloc: a fixed array in this library's code
+// object, one copy per GPU (each device that loads the library holds it
+// until the process ends).  8 MiB holds the stories110M head (vocabulary
+// 32000) at up to 8192 tokens when the classifier runs 256-row blocks
+// (from 1024 tokens on), up to 4096 with the 128-row blocks of fewer tokens.
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+// The array's name is a host-side stand-in, not a device address: each
+// device's address comes from hipGetSymbolAddress, taken once per device on
+// its first call with that device current, and only that address reaches a
+// kernel.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+int scratch_address(const char* op, void** out) {
+  int dev = -1;
+  hipError_t h = hipGetDevice(&dev);
+  if (h != hipSuccess) return op_fail(ANE_ERR_HIP, "storiesane %s: hipGetDevice: %s", op, hipGetErrorString(h));
+  if (dev < 0 || dev >= kMaxDevices) return op_fail(ANE_ERR_ARG, "storiesane %s: device %d out of range", op, dev);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    h = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (h != hipSuccess || !p)
+      return op_fail(ANE_ERR_HIP, "storiesane %s: hipGetSymbolAddress(scratch) on device %d: %s", op, dev,
+                     hipGetErrorString(h));
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return ANE_OK;
+}
+
+}  // namespace
+
+extern "C" int ane_head_loss_noalloc(const uint16_t* xn, const uint16_t* embed, const uint16_t* targets,
+                                     int32_t ntok, int32_t dim, int32_t vocab, int32_t seq, int32_t softcap,
+                                     float* loss_seq, float* lse, void* stream) {
+  const char* op = "head loss noalloc";
+  if (!xn || !embed || !targets || !loss_seq) return op_fail(ANE_ERR_ARG, "storiesane %s: null buffer", op);
+  HeadPlan pl;
+  int rc = head_plan(op, ntok, dim, vocab, seq, &pl);
+  if (rc) return rc;
+  if (pl.bytes > kNoAllocScratchBytes)
+    return op_fail(ANE_ERR_ARG,
+                   "storiesane %s: ntok=%d vocab=%d needs %zu bytes of scratch; this entry point holds %zu "
+                   "(use ane_head_loss)",
+                   op, ntok, vocab, pl.bytes, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  rc = scratch_address(op, &ws);
+  if (rc) return rc;
+  const hipError_t h = head_run(pl, xn, embed, targets, ntok, dim, vocab, seq, softcap, loss_seq, lse, (char*)ws,
+                                (hipStream_t)stream);
   if (h != hipSuccess) return op_fail(ANE_ERR_HIP, "storiesane %s: %s", op, hipGetErrorString(h));
   return ANE_OK;
 }

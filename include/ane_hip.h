@@ -304,6 +304,17 @@ const char *ane_debug_last_error(void);
 int ane_head_loss(const uint16_t *xn, const uint16_t *embed, const uint16_t *targets, int32_t ntok, int32_t dim,
                   int32_t vocab, int32_t seq, int32_t softcap, float *loss_seq, float *lse, void *stream);
 const char *ane_op_last_error(void);
+/* ane_head_loss without any allocation: no counterpart in the reference.
+ * For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results; the scratch is a fixed 8 MiB array per GPU (vocab
+ * 32000: up to 8192 tokens); larger requests fail with ANE_ERR_ARG.  The call is asynchronous on `stream` (it does not wait).
+ * Every call on one GPU shares that GPU's array: calls that overlap in time
+ * on one GPU (other streams, other threads) race on it.  Calls no hipMalloc,
+ * hipFree or allocating library routine. */
+int ane_head_loss_noalloc(const uint16_t *xn, const uint16_t *embed, const uint16_t *targets, int32_t ntok,
+                          int32_t dim, int32_t vocab, int32_t seq, int32_t softcap, float *loss_seq, float *lse,
+                          void *stream);
 
 /* ---- greedy KV-cache decoder (grouped-query attention) --------------------
  * No counterpart in the reference, which evaluates whole windows only
