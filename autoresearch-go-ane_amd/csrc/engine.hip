@@ -153,6 +153,7 @@ void phase_reset(ane_engine* e) {
 
 void phase_begin(ane_engine* e, int phase) {
   e->ph_open = false;
+  if (!e->ph_sample && phase != PH_REFRESH) return;
   while ((int)e->ph_ev.size() < e->ph_used + 2) {
     hipEvent_t ev = nullptr;
     if (hipEventCreate(&ev) != hipSuccess) return;
@@ -373,6 +374,7 @@ extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_e
   apply_option_defaults(&e->opt);
   e->device = e->opt.device;
   if (const char* g = getenv("ANE_GRAPHS")) e->use_graph = atoi(g) != 0;
+  if (const char* g = getenv("ANE_PHASE_EVERY")) e->ph_period = atoi(g) > 0 ? atoi(g) : 1;
   e->lr = e->opt.lr;
   int rc = validate_cfg(e, e->cfg);
   if (rc == ANE_OK) rc = open_impl(e);

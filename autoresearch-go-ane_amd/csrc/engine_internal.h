@@ -168,6 +168,15 @@ struct ane_engine {
   std::vector<int> ph_cls;        // phase of each recorded pair
   int ph_used = 0;
   bool ph_open = false;
+  // An event recorded between kernels costs ~4 us of idle GPU (0.47 ms on an
+  // 8.4 ms B16 step), so the kernel-group phases are timed on the first
+  // training call and every ph_period-th after it (ANE_PHASE_EVERY, default
+  // 16); the other calls report the latest measurement.  The weight refresh
+  // (one pair per update) is timed on every call.
+  bool ph_sample = false;
+  int ph_period = 16;
+  uint64_t ph_calls = 0;
+  int64_t ph_last_ns[4] = {0, 0, 0, 0};  // latest embed_grad, rms_dw, dw_gemm, per window
   int64_t startup_ns = 0;  // host time of this call's one-time training set-up
 
   // eval forward + loss replayed as one HIP graph per batch size (the

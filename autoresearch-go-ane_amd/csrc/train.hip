@@ -481,6 +481,7 @@ int train_windows(ane_engine* e, int nseq, ane_step_result* res) {
   int rc = ensure_train(e, op);
   if (rc) return rc;
   phase_reset(e);
+  e->ph_sample = e->ph_calls++ % (uint64_t)e->ph_period == 0;
   const uint64_t S = (uint64_t)e->cfg.seq;
   const uint64_t limit = (uint64_t)e->ndata - S - 1;
   std::vector<uint64_t> pos(nseq);
@@ -527,9 +528,14 @@ int train_windows(ane_engine* e, int nseq, ane_step_result* res) {
     res->startup_compile_ns = e->startup_ns;
     res->ane_eval_ns = ev_ns(ane_engine::EV_STEP0, ane_engine::EV_BWD1);  // forward + backward kernels
     res->final_head_ns = ev_ns(ane_engine::EV_HEAD0, ane_engine::EV_HEAD1);
-    res->embed_grad_ns = (int64_t)(ph[PH_EMBED_GRAD] * 1e6);
-    res->rms_dw_ns = (int64_t)(ph[PH_RMS_DW] * 1e6);
-    res->dw_gemm_ns = (int64_t)(ph[PH_DW_GEMM] * 1e6);
+    if (e->ph_sample) {  // this call's kernel-group phases were timed; per window
+      e->ph_last_ns[PH_EMBED_GRAD] = (int64_t)(ph[PH_EMBED_GRAD] * 1e6 / nseq);
+      e->ph_last_ns[PH_RMS_DW] = (int64_t)(ph[PH_RMS_DW] * 1e6 / nseq);
+      e->ph_last_ns[PH_DW_GEMM] = (int64_t)(ph[PH_DW_GEMM] * 1e6 / nseq);
+    }
+    res->embed_grad_ns = e->ph_last_ns[PH_EMBED_GRAD] * nseq;
+    res->rms_dw_ns = e->ph_last_ns[PH_RMS_DW] * nseq;
+    res->dw_gemm_ns = e->ph_last_ns[PH_DW_GEMM] * nseq;
     res->dw_wait_ns = (int64_t)(wait_s * 1e9);
     if (e->flushed) {
       res->adam_ns = ev_ns(ane_engine::EV_ADAM0, ane_engine::EV_ADAM1);

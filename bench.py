@@ -243,13 +243,29 @@ def main():
     ms = dt / args.steps * 1e3
     tps = B * S * args.steps / dt
 
+    # board power and utilisation over a separate pass of the same calls
+    # (the aneperf watts / compute-% of the reference's benchmarks)
+    from ane.perf import Sampler
+    sampler = Sampler()
+    power = {}
+    if sampler.available:
+        n_pw = max(args.steps, 200)
+        snap = sampler.Start()
+        for _ in range(n_pw):
+            eng.EvalLossWindows(pos)
+        eng.Sync()
+        d = sampler.Stop(snap)
+        power = d.metrics()
+        if d.energy_j > 0:
+            power["tokens_per_joule"] = round(B * S * n_pw / d.energy_j, 1)
+        power["steps"] = n_pw
     out = {"metric": METRIC, "value": round(tps, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "fp16",
            "data": "synthetic: token ids uniform [0,32000) seed 2; random-init N(0,0.02) weights seed 0",
            "config": {"workload": f"stories110M-{args.arch} forward+loss, batch {B} x seq {S} (BASELINE configs[1])",
                       "arch": args.arch, "batch": B, "seq": S, "tokens_per_step": B * S},
-           "loss": round(loss, 6)}
+           "loss": round(loss, 6), "power": power}
     if not args.no_profile:
         # a second pass of the same steps with HIP events around every launch
         # (the timed pass above runs without them)

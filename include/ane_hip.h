@@ -96,6 +96,12 @@ typedef struct ane_state {
  *   rms_dw_ns           norm-gain gradient reductions (llama2; 0 for nanochat,
  *                       whose norms have no weights)
  *   dw_gemm_ns          weight-gradient GEMMs with their operand transposes
+ *                       (these three: events around each kernel group cost
+ *                       ~4 us of idle GPU apiece, so they are measured on the
+ *                       first training call and every 16th after it --
+ *                       ANE_PHASE_EVERY=n changes the period -- and the other
+ *                       calls report the latest measurement, per window,
+ *                       times their window count)
  *   dw_wait_ns          host time blocked until the queued device work ended
  *   adam_ns             clip + AdamW kernels when the call flushed
  *   cpu_work_ns         step_ns minus the set-up, refresh, eval and Adam times */
