@@ -47,6 +47,7 @@ struct SkinnyArgs {
   float2* amax;
   float* logits;
   int nvalid;
+  const float* rr = nullptr;  // [64] per-token scale of the logits written (argmax is unaffected: rr > 0)
 };
 hipError_t classifier_argmax(const SkinnyArgs& a, hipStream_t s);
 
@@ -69,8 +70,10 @@ hipError_t skinny_finish_swiglu(const float* part, int N, int K, half_t* gate, i
 hipError_t argmax_reduce(uint16_t* tok_out, uint16_t* hist, const int* step, const float2* amax, int ngroups,
                          int nb, hipStream_t s);
 
-// ctr = {position of the current step's token, step index}: advance both /
-// set both (kernels, so the counters never depend on host memory lifetimes)
+// ctr = {position of the current step's token, step index of this call,
+// steps since open}: advance all three / set the first two (kernels, so the
+// counters never depend on host memory lifetimes).  The third never resets:
+// it numbers the uses of the tail kernel's counters and flags.
 hipError_t dec_advance(int* ctr, hipStream_t s);
 hipError_t dec_set_ctr(int* ctr, int pos, int step, hipStream_t s);
 
@@ -103,8 +106,47 @@ struct DecAttnArgs {
   int nb, NH, NKV, max_ctx, nsplit;  // nsplit: partial slots per head (max_ctx / kDecChunk)
   float scale;
   int form = 0;  // 0: by batch size, 1: 1024-thread blocks, 2: 256-thread splits
+  const float* rr = nullptr;  // [64] 1 / rms of each row's input when the partials are of fp16(x * gain)
 };
 hipError_t dec_attention(const DecAttnArgs& a, hipStream_t s);
+
+// ---- the per-layer GEMM chain in one launch (decode_tail.hip) ---------------
+// Wo + residual, W1|W3 + SwiGLU, W2 + residual, the next layer's QKV
+// projection and its 1 / rms: one 16-wave block per 32-column group (per
+// W1|W3 pair) over the whole K, blocks ordered by phase; a block waits on the
+// done counter of the phase it reads (no grid barrier).  Requires every block
+// resident at once: dec_tail_blocks_per_cu() x CUs >= the block count.
+struct TailArgs {
+  const half_t* att;        // [64][D] activation fragments: the attention output
+  float* x;                 // [64][D] residual stream (fp32, row-major)
+  const half_t* wo;         // fragment-major [D][D]
+  const half_t* w13;        // fragment-major [2H][D], W1 / W3 interleaved by 32 rows
+  const half_t* w2;         // fragment-major [D][H]
+  const half_t* wqkv_next;  // fragment-major [N1][D] of the next layer (unused when b_q == 0)
+  const float* g_ffn;       // [D] gain of the FFN norm
+  const float* g_next;      // [D] gain of the next norm (next layer's attention norm, or the final norm)
+  half_t* xg_ffn;           // [64][D] fragments: fp16(x * g_ffn) after Wo
+  half_t* gate;             // [64][H] fragments
+  half_t* xg_next;          // [64][D] fragments: fp16(x * g_next) after W2
+  float* rr_next;           // [64] 1 / rms of x after W2
+  float* p_q;               // [64][N1] the next layer's q | k | v, before 1 / rms and RoPE
+  float* ssq_wo;            // [D/32][64] per column group sum of squares of the residual
+  float* ssq_w2;
+  unsigned* sync;           // done counters (kDecTailSync words, zero at open)
+  const int* gstep;         // steps since open (ctr[2])
+  int* err;                 // set when a wait times out; later launches exit at once
+  unsigned spin_limit;      // polls before a wait times out (kDecTailSpin; 0: every wait fails)
+  int D, H, N1, layer, L;
+  int b_wo, b_13, b_w2, b_q;  // blocks per phase: D/32, H/32, D/32, N1/32 (0 on the last layer)
+};
+constexpr int kDecTailSync = 64;
+constexpr unsigned kDecTailSpin = 1u << 20;  // polls of ~100 cycles: ~50 ms
+hipError_t dec_tail(const TailArgs& a, hipStream_t s);
+int dec_tail_blocks_per_cu();
+// x [64][D] (or, with tok, x = embed[tok]) -> xg = fp16(x * g) fragments and
+// rr = 1 / rms(x), for rows < nb
+hipError_t dec_row_xg(float* x, half_t* xg, float* rr, const float* embed, const uint16_t* tok, const float* g,
+                      int nb, int D, int V, hipStream_t s);
 
 // ---- prefill ---------------------------------------------------------------
 // qkv [T][N1] (T = nseq * S tokens of sequences seq0..): RoPE q in place;

@@ -93,14 +93,20 @@ __global__ __launch_bounds__(64 * NWK) void classifier_argmax_kernel(SkinnyArgs 
   // waves' partials above are done.
   float* tile = lds;
   const bool valid = col < a.nvalid;
+  // logits of inputs fp16(x * gain) carry the norm's per-token 1 / rms as a
+  // factor; it is positive, so the argmax below is taken on the unscaled sums
+  const float rr_lane = a.rr ? a.rr[lane] : 1.f;
 #pragma unroll
   for (int r = 0; r < 16; r++) {
     const int t = 8 * (r >> 2) + 4 * h + (r & 3);
     tile[t * 33 + row] = valid ? c0[r] : -INFINITY;
     tile[(t + 32) * 33 + row] = valid ? c1[r] : -INFINITY;
-    if (a.logits && valid) {
-      a.logits[(size_t)t * a.N + col] = c0[r];
-      a.logits[(size_t)(t + 32) * a.N + col] = c1[r];
+    if (a.logits) {  // uniform: the shuffles run on every lane
+      const float s0 = __shfl(rr_lane, t, 64), s1 = __shfl(rr_lane, t + 32, 64);
+      if (valid) {
+        a.logits[(size_t)t * a.N + col] = c0[r] * s0;
+        a.logits[(size_t)(t + 32) * a.N + col] = c1[r] * s1;
+      }
     }
   }
   float v = tile[lane * 33];
@@ -145,6 +151,7 @@ __global__ void advance_kernel(int* ctr) {
   if (threadIdx.x == 0) {
     ctr[0] += 1;
     ctr[1] += 1;
+    ctr[2] += 1;
   }
 }
 
@@ -357,7 +364,7 @@ __device__ __forceinline__ int dec_chunk(int ctx, int nsplit) {
 // k / v rows to LDS and the new rows to cache row `row` of the split.
 template <int G, int QS>
 struct QkvProj {
-  float pe[QS], po[QS], cs = 0.f, sn = 0.f;
+  float pe[QS], po[QS], cs = 0.f, sn = 0.f, rr = 1.f;
   int col = -1;
   bool rot = false;
   __device__ __forceinline__ void issue(const DecAttnArgs& a, int b, int kvh, int tid, int pos, bool own) {
@@ -378,6 +385,7 @@ struct QkvProj {
       const int ri = (cc & 63) >> 1;
       cs = a.rope_cos[pos * 32 + ri];
       sn = a.rope_sin[pos * 32 + ri];
+      if (a.rr) rr = a.rr[b];
     }
   }
   __device__ __forceinline__ void finish(const DecAttnArgs& a, int tid, half_t (*qs)[64], half_t* knew, half_t* vnew,
@@ -389,6 +397,8 @@ struct QkvProj {
       e += s < a.qkv_ks ? pe[s] : 0.f;
       o += s < a.qkv_ks ? po[s] : 0.f;
     }
+    e *= rr;  // the partials are of fp16(x * gain): the norm's 1 / rms applied here
+    o *= rr;
     if (rot) {
       const float e2 = e * cs - o * sn, o2 = o * cs + e * sn;
       e = e2;

@@ -1,0 +1,405 @@
+// The decode step's per-layer GEMM chain in one launch: Wo (+ residual),
+// W1|W3 (+ SwiGLU), W2 (+ residual) and the next layer's QKV projection.
+//
+// A grid-wide barrier costs ~11 us on MI355X (one device-scope atomic per
+// block, serialised) against ~1.7 us for a kernel boundary in a replayed
+// graph, so the phases are not separated by barriers.  Instead every block
+// (16 waves) owns one 32-column group of a GEMM over the whole K -- the waves
+// split K and meet in LDS, in wave order -- applies the epilogue itself and
+// counts itself done; a consumer block waits only on the done counter of the
+// phase it reads:
+//   * blocks are laid out phase by phase (Wo, W13, W2, QKV, then one block
+//     that forms the next 1/rms), one per CU and all resident at once (the
+//     host checks the occupancy), so a wait never blocks its own producer;
+//   * every load a block needs after its wait is issued together (the
+//     activations, the residual slice, the norm sums): one device-coherent
+//     round trip per phase;
+//   * each block loads its weight fragments before it waits: the layer's
+//     weights stream from HBM while the first phase computes;
+//   * counters only grow: a use is identified by the epoch
+//     E = global step * layers + layer + 1, so nothing is cleared between uses.
+// (Splitting K over blocks with a last-arriver fix-up per group kept more
+// blocks busy but cost two more device-coherent round trips per GEMM:
+// measured 31 us per layer against 25 for one launch per GEMM.)
+// RMSNorm is applied after the GEMMs it feeds: a block's activations are
+// fp16(x * gain), and the per-token 1 / rms -- which needs every column group
+// of the residual -- scales the (linear) GEMM output instead: in the SwiGLU
+// epilogue (W1|W3) and in the attention's QKV finish (via rr_next).
+// Every wait is bounded; a timeout sets *err, and later launches exit at once.
+//
+// Memory: the data blocks exchange inside the launch (the residual, the norm
+// sums, the fp16 activation fragments) is stored and loaded device-coherent
+// (cache policy sc1: written through to, and read from, the level shared by
+// all XCDs), and a block drains its own stores (s_waitcnt vmcnt(0)) before it
+// counts an arrival.  The agent-scope release / acquire fences would instead
+// write back / invalidate the whole XCD L2 at every arrival: measured 1.7 ms
+// per decode step against 0.62 for one launch per GEMM.
+#include <math.h>
+
+#include "decode.h"
+
+namespace ane {
+
+namespace {
+
+__device__ __forceinline__ unsigned ld_relaxed(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- device-coherent accesses of shared data (uniform base + per-lane byte offset)
+constexpr int kSc1 = 16;  // cache policy bit sc1: device scope
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ float ld_c1(const float* base, uint32_t elem) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc(base), elem * 4u, 0, kSc1));
+}
+__device__ __forceinline__ void st_c1(float* base, uint32_t elem, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rsrc(base), elem * 4u, 0, kSc1);
+}
+__device__ __forceinline__ half8 ld_ch8(const half_t* base, uint32_t elem) {
+  const u32x4v a = __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), elem * 2u, 0, kSc1);
+  return __builtin_bit_cast(half8, a);
+}
+// this wave's stores have completed (s_waitcnt vmcnt(0)); the empty asm keeps
+// the compiler from moving memory operations across
+__device__ __forceinline__ void drain_stores() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  asm volatile("" ::: "memory");
+}
+
+// Polls *c until it reaches `target` (wave 0; at most `limit` polls of ~100
+// cycles); the block reads the producers' data afterwards with
+// device-coherent loads.  Returns false (block-uniform) after a timeout or
+// when another block has failed; limit 0 fails at once (the host's way to
+// exercise the error path).
+__device__ bool wait_count(const unsigned* c, unsigned target, unsigned limit, int* err, int* sh) {
+  if (threadIdx.x < 64) {
+    int ok = limit != 0;
+    unsigned spins = 0;
+    while (ok && ld_relaxed(c) < target) {
+      if (++spins > limit || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    if (threadIdx.x == 0) {
+      if (!ok) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *sh = ok;
+    }
+  }
+  __syncthreads();
+  const bool ok = *sh != 0;
+  asm volatile("" ::: "memory");
+  return ok;
+}
+
+// After the block's epilogue stores: drain them, then count the block done.
+__device__ void publish(unsigned* done) {
+  drain_stores();
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Windows [w0, w0 + nw) of wave `wave` when nwin windows are split over
+// nwave waves (nw <= MAXW).
+struct Span {
+  int w0, nw;
+};
+template <int MAXW>
+__device__ __forceinline__ Span wave_span(int nwin, int nwave, int wave) {
+  const int a = wave * nwin / nwave, b = (wave + 1) * nwin / nwave;
+  return Span{a, min(b - a, MAXW)};
+}
+
+// One wave's 64 x 32 partial over its windows: weights of column group cg
+// (fragment-major, nwin windows per group) preloaded by load_w, activations
+// X (activation fragments) loaded after the dependency wait by mma.
+template <int MAXW>
+struct WaveGemm {
+  half8 w[4 * MAXW];
+  floatx16 c0, c1;
+  __device__ __forceinline__ void load_w(const half_t* W, int cg, int nwin, Span sp) {
+    const half_t* wp = W + (size_t)cg * nwin * 2048 + threadIdx.x % 64 * 8;
+#pragma unroll
+    for (int s = 0; s < 4 * MAXW; s++) {
+      const int f = (sp.w0 + min(s >> 2, max(sp.nw - 1, 0))) * 4 + (s & 3);
+      w[s] = ld_h8(wp + (size_t)f * 512);
+    }
+  }
+  // coherent: X was written inside this launch (device-coherent loads)
+  __device__ __forceinline__ void mma(const half_t* X, Span sp, bool coherent) {
+    const int lane8 = threadIdx.x % 64 * 8;
+    half8 p[4 * MAXW], q[4 * MAXW];
+#pragma unroll
+    for (int s = 0; s < 4 * MAXW; s++) {
+      const int f = (sp.w0 + min(s >> 2, max(sp.nw - 1, 0))) * 4 + (s & 3);
+      if (coherent) {
+        p[s] = ld_ch8(X, (uint32_t)(f * 1024 + lane8));
+        q[s] = ld_ch8(X, (uint32_t)(f * 1024 + 512 + lane8));
+      } else {
+        p[s] = ld_h8(X + (size_t)f * 1024 + lane8);
+        q[s] = ld_h8(X + (size_t)f * 1024 + 512 + lane8);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; r++) { c0[r] = 0.f; c1[r] = 0.f; }
+#pragma unroll
+    for (int s = 0; s < 4 * MAXW; s++) {
+      if ((s >> 2) < sp.nw) {  // wave-uniform: surplus windows contribute nothing
+        c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(p[s], w[s], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(q[s], w[s], c1, 0, 0, 0);
+      }
+    }
+  }
+  // this wave's partial into red[wave] ([64 rows][32 columns])
+  __device__ __forceinline__ void to_lds(float (*red)[64][32]) const {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, col = lane & 31;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int t = 8 * (r >> 2) + 4 * h + (r & 3);
+      red[wave][t][col] = c0[r];
+      red[wave][t + 32][col] = c1[r];
+    }
+  }
+};
+
+// element pair i (of 1024) of a 64 x 32 tile: row i / 16, columns 2 (i % 16), +1
+__device__ __forceinline__ float2 sum_waves(float (*red)[64][32], int w0, int w1) {
+  const int row = threadIdx.x >> 4, col = (threadIdx.x & 15) * 2;
+  float2 v = make_float2(red[w0][row][col], red[w0][row][col + 1]);
+  for (int w = w0 + 1; w < w1; w++) {
+    v.x += red[w][row][col];
+    v.y += red[w][row][col + 1];
+  }
+  return v;
+}
+
+__device__ __forceinline__ void st_frag2(half_t* X, int t, int k, float a, float b) {
+  half2v h;
+  h[0] = (half_t)a;
+  h[1] = (half_t)b;
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, h), rsrc(X), (uint32_t)act_frag_off(t, k) * 2u,
+                                        0, kSc1);
+}
+
+// This thread's element pair of a 64 x 32 tile of column group cg: row
+// tid / 16, columns 32 cg + 2 (tid % 16), +1; its index in x [64][D].
+__device__ __forceinline__ int x_index(int cg, int D) {
+  return (threadIdx.x >> 4) * D + cg * 32 + (threadIdx.x & 15) * 2;
+}
+
+// Residual epilogue of column group cg (Wo, W2): xv (this thread's element
+// pair of x[:, cg], loaded before the GEMM) += acc and is stored; ssq[cg][t] = sum
+// over the group's 32 columns of the new x^2; xg = fp16(x * gain) fragments
+// for the consumer.
+__device__ void resid_epilogue(float2 acc, float2 xv, int cg, float* x, int D, float* ssq, half_t* xg,
+                               const float* gain) {
+  const int row = threadIdx.x >> 4, c = cg * 32 + (threadIdx.x & 15) * 2;
+  const uint32_t xi = (uint32_t)x_index(cg, D);
+  const __amdgpu_buffer_rsrc_t rx = rsrc(x);
+  xv.x += acc.x;
+  xv.y += acc.y;
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(xv.x), rx, xi * 4u, 0, kSc1);
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(xv.y), rx, xi * 4u + 4u, 0, kSc1);
+  float ss = xv.x * xv.x + xv.y * xv.y;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);  // the row's 16 threads
+  if ((threadIdx.x & 15) == 0) st_c1(ssq, (uint32_t)(cg * 64 + row), ss);
+  st_frag2(xg, row, c, xv.x * gain[c], xv.y * gain[c + 1]);
+}
+
+// 1 / rms of row `row` from the ncg <= 32 column-group sums of squares: all
+// loads in flight together, added in group order
+__device__ __forceinline__ float rr_of(const float* ssq, int ncg, int row, int D) {
+  float v[32];
+#pragma unroll
+  for (int g = 0; g < 32; g++) v[g] = ld_c1(ssq, (uint32_t)(min(g, ncg - 1) * 64 + row));
+  float s = 0.f;
+#pragma unroll
+  for (int g = 0; g < 32; g++) s += g < ncg ? v[g] : 0.f;
+  return 1.0f / sqrtf(s / (float)D + 1e-5f);
+}
+
+constexpr int kTailWaves = 16;
+
+// This thread's x element pair of column group cg (x_index) -> xs[0][tid],
+// xs[1][tid]: device-coherent loads straight into LDS (global_load_lds), so
+// that no register is held while the GEMM's loads are in flight.  They are
+// not in the compiler's wait counts: the caller waits (vmcnt(0)) before
+// reading xs.  Lane l of wave w lands at xs[j][64 w + l].
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+__device__ __forceinline__ void x_to_lds(const float* x, int cg, int D, float (*xs)[64 * kTailWaves]) {
+  const float* gp = x + x_index(cg, D);
+  const int wave = threadIdx.x >> 6;
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)&xs[j][wave * 64]);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off sc1" ::"s"(lds), "v"(gp + j)
+                 : "memory", "m0");
+  }
+#pragma clang diagnostic pop
+}
+
+__global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
+  __shared__ float red[kTailWaves][64][32];
+  __shared__ float ssq_s[32][kDecRows];
+  __shared__ float xs[2][64 * kTailWaves];
+  __shared__ int sh;
+  if (__hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;  // an earlier wait failed
+  const int D = a.D, H = a.H, N1 = a.N1, ncg = D / 32, npair = H / 32;
+  const int nwd = D / 64, nwh = H / 64;
+  const int wave = threadIdx.x >> 6;
+  const unsigned E = (unsigned)(*a.gstep) * (unsigned)a.L + (unsigned)a.layer + 1u;
+  unsigned* done_wo = a.sync;
+  unsigned* done_13 = a.sync + 1;
+  unsigned* done_w2 = a.sync + 2;
+  int b = blockIdx.x;
+
+  if (b < a.b_wo) {  // ---- Wo: x += Wo att --------------------------------------
+    const int cg = b;
+    // x was last written before this launch (by the previous layer's W2 or the
+    // embedding): a plain load, issued with the weights
+    float2 xv = *reinterpret_cast<const float2*>(a.x + x_index(cg, D));
+    const Span sp = wave_span<1>(nwd, kTailWaves, wave);
+    WaveGemm<1> g;
+    g.load_w(a.wo, cg, nwd, sp);
+    g.mma(a.att, sp, false);  // the attention kernel finished before this launch
+    g.to_lds(red);
+    __syncthreads();
+    resid_epilogue(sum_waves(red, 0, kTailWaves), xv, cg, a.x, D, a.ssq_wo, a.xg_ffn, a.g_ffn);
+    publish(done_wo);
+    return;
+  }
+  b -= a.b_wo;
+  if (b < a.b_13) {  // ---- W1|W3 pair: SwiGLU ------------------------------------
+    // pair p: W1 rows of hidden units 32 p.. (group 2 p) on waves 0-7, W3 (2 p + 1) on 8-15
+    const int pr = b, half = wave >> 3;
+    const Span sp = wave_span<2>(nwd, kTailWaves / 2, wave & 7);
+    WaveGemm<2> g;
+    g.load_w(a.w13, 2 * pr + half, nwd, sp);
+    if (!wait_count(done_wo, (unsigned)ncg * E, a.spin_limit, a.err, &sh)) return;  // x, its sums of squares, xg_ffn
+    // the residual's column-group sums of squares (ncg * 64 <= 2 per thread),
+    // in flight with the activations
+    const int t0 = threadIdx.x, t1 = threadIdx.x + 64 * kTailWaves;
+    const float s0 = t0 < ncg * kDecRows ? ld_c1(a.ssq_wo, (uint32_t)t0) : 0.f;
+    const float s1 = t1 < ncg * kDecRows ? ld_c1(a.ssq_wo, (uint32_t)t1) : 0.f;
+    g.mma(a.xg_ffn, sp, true);
+    g.to_lds(red);
+    if (t0 < ncg * kDecRows) ssq_s[t0 / kDecRows][t0 % kDecRows] = s0;
+    if (t1 < ncg * kDecRows) ssq_s[t1 / kDecRows][t1 % kDecRows] = s1;
+    __syncthreads();
+    const float2 h1 = sum_waves(red, 0, kTailWaves / 2), h3 = sum_waves(red, kTailWaves / 2, kTailWaves);
+    const int row = threadIdx.x >> 4, c = (threadIdx.x & 15) * 2;
+    float ss = 0.f;
+    for (int q = 0; q < ncg; q++) ss += ssq_s[q][row];
+    const float rr = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+    const float u0 = h1.x * rr, u1 = h1.y * rr;
+    st_frag2(a.gate, row, 32 * pr + c, u0 / (1.0f + __expf(-u0)) * (h3.x * rr), u1 / (1.0f + __expf(-u1)) * (h3.y * rr));
+    publish(done_13);
+    return;
+  }
+  b -= a.b_13;
+  if (b < a.b_w2) {  // ---- W2: x += W2 gate -----------------------------------
+    const int cg = b;
+    const Span sp = wave_span<2>(nwh, kTailWaves, wave);
+    WaveGemm<2> g;
+    g.load_w(a.w2, cg, nwh, sp);
+    // done_13 implies done_wo: x (written by the Wo block of this group) is
+    // read device-coherent, in flight with the activations
+    if (!wait_count(done_13, (unsigned)npair * E, a.spin_limit, a.err, &sh)) return;
+    x_to_lds(a.x, cg, D, xs);
+    g.mma(a.gate, sp, true);
+    g.to_lds(red);
+    drain_stores();  // (also the loads: x_to_lds is not in the compiler's count)
+    __syncthreads();
+    const float2 xv = make_float2(xs[0][threadIdx.x], xs[1][threadIdx.x]);
+    resid_epilogue(sum_waves(red, 0, kTailWaves), xv, cg, a.x, D, a.ssq_w2, a.xg_next, a.g_next);
+    publish(done_w2);
+    return;
+  }
+  b -= a.b_w2;
+  if (b < a.b_q) {  // ---- next layer's QKV (finished by the attention) ----------------
+    const int cg = b;
+    const Span sp = wave_span<1>(nwd, kTailWaves, wave);
+    WaveGemm<1> g;
+    g.load_w(a.wqkv_next, cg, nwd, sp);
+    if (!wait_count(done_w2, (unsigned)ncg * E, a.spin_limit, a.err, &sh)) return;
+    g.mma(a.xg_next, sp, true);
+    g.to_lds(red);
+    __syncthreads();
+    const float2 v = sum_waves(red, 0, kTailWaves);
+    const int row = threadIdx.x >> 4, c = cg * 32 + (threadIdx.x & 15) * 2;
+    *reinterpret_cast<float2*>(a.p_q + (size_t)row * N1 + c) = v;
+    return;
+  }
+  // ---- 1 / rms of the new residual, for the next consumer ------------------------
+  if (!wait_count(done_w2, (unsigned)ncg * E, a.spin_limit, a.err, &sh)) return;
+  if (threadIdx.x < kDecRows) a.rr_next[threadIdx.x] = rr_of(a.ssq_w2, ncg, threadIdx.x, D);
+}
+
+// x [64][D] -> xg = fp16(x * g) fragments and rr = 1 / rms(x); with tok, x is
+// first the embedding row (zero for tok >= V).  One block of 256 per row.
+__global__ __launch_bounds__(256) void row_xg_kernel(float* x, half_t* xg, float* rr, const float* embed,
+                                                     const uint16_t* tok, const float* g, int D, int V) {
+  __shared__ float red[4];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int tk = tok ? tok[b] : 0;
+  float v[4];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int c = tid + 256 * i;
+    v[i] = 0.f;
+    if (c < D) {
+      if (tok) v[i] = tk < V ? embed[(size_t)tk * D + c] : 0.f;
+      else v[i] = x[(size_t)b * D + c];
+    }
+    ss += v[i] * v[i];
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  ss = red[0] + red[1] + red[2] + red[3];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int c = tid + 256 * i;
+    if (c < D) {
+      if (tok) x[(size_t)b * D + c] = v[i];
+      xg[act_frag_off(b, c)] = (half_t)(v[i] * g[c]);
+    }
+  }
+  if (tid == 0) rr[b] = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+}
+
+}  // namespace
+
+hipError_t dec_tail(const TailArgs& a, hipStream_t s) {
+  // one window per wave for K = D (<= 16 windows), two for K = H (<= 32)
+  if (a.D % 64 || a.D > 1024 || a.H % 64 || a.H > 2048 || a.N1 % 32) return hipErrorInvalidValue;
+  if (a.b_wo != a.D / 32 || a.b_13 != a.H / 32 || a.b_w2 != a.D / 32 || (a.b_q && a.b_q != a.N1 / 32))
+    return hipErrorInvalidValue;
+  const int blocks = a.b_wo + a.b_13 + a.b_w2 + a.b_q + 1;
+  hipLaunchKernelGGL(tail_kernel, dim3(blocks), dim3(64 * kTailWaves), 0, s, a);
+  return hipGetLastError();
+}
+
+int dec_tail_blocks_per_cu() {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, tail_kernel, 64 * kTailWaves, 0) != hipSuccess) return 0;
+  return n;
+}
+
+hipError_t dec_row_xg(float* x, half_t* xg, float* rr, const float* embed, const uint16_t* tok, const float* g,
+                      int nb, int D, int V, hipStream_t s) {
+  if (D > 1024 || nb < 1 || nb > kDecRows) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(row_xg_kernel, dim3(nb), dim3(256), 0, s, x, xg, rr, embed, tok, g, D, V);
+  return hipGetLastError();
+}
+
+}  // namespace ane

@@ -88,6 +88,16 @@ struct ane_decoder {
   int attn_form = 0;  // decode attention form: 0 by batch size; ANE_DEC_ATTN=wide (1) / split (2)
   float2* amax = nullptr;
   float* logits_d = nullptr;
+  // the per-layer GEMM chain as one launch (decode_tail.hip); ANE_DEC_TAIL=0
+  // keeps one launch per GEMM and finish
+  bool use_tail = false;
+  half_t *xg_att = nullptr, *xg_ffn = nullptr;  // fp16(x * gain) fragments
+  float* rr_d = nullptr;                        // [64] 1 / rms of the current norm input
+  float *ssq_wo = nullptr, *ssq_w2 = nullptr;
+  unsigned* sync = nullptr;
+  int* err_d = nullptr;
+  int b_tail = 0;
+  unsigned tail_spin = 0;
   uint16_t *tok_d = nullptr, *hist_d = nullptr, *prefix_d = nullptr;
   int* ctr_d = nullptr;
   int TC = 0;
@@ -235,7 +245,7 @@ int open_impl(ane_decoder* d) {
   DCHK(op, dalloc(d, &d->tok_d, (size_t)R));
   DCHK(op, dalloc(d, &d->hist_d, (size_t)C * R));
   DCHK(op, dalloc(d, &d->prefix_d, (size_t)B * C));
-  DCHK(op, dalloc(d, &d->ctr_d, 2));
+  DCHK(op, dalloc(d, &d->ctr_d, 3));
   d->TC = std::max(kPrefillTokens, (C + 63) / 64 * 64);
   DCHK(op, dalloc(d, &d->px, (size_t)d->TC * D));
   DCHK(op, dalloc(d, &d->pxn, (size_t)d->TC * D));
@@ -248,7 +258,35 @@ int open_impl(ane_decoder* d) {
   DCHK(op, hipMemset(d->gate, 0, (size_t)R * H * 2));
   DCHK(op, hipMemset(d->x, 0, (size_t)R * D * 4));
   DCHK(op, hipMemset(d->tok_d, 0, (size_t)R * 2));
-  DCHK(op, hipMemset(d->ctr_d, 0, 8));
+  DCHK(op, hipMemset(d->ctr_d, 0, 12));
+  // The fused GEMM chain: one block per column group of each phase, all
+  // resident at once, or the chain keeps one launch per GEMM.
+  {
+    d->b_tail = D / 32 + H / 32 + D / 32 + N1 / 32 + 1;
+    int ncu = 0;
+    DCHK(op, hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, c.device));
+    const int per_cu = dec_tail_blocks_per_cu();
+    d->use_tail = per_cu > 0 && (long)per_cu * ncu >= d->b_tail;
+    if (const char* f = getenv("ANE_DEC_TAIL")) d->use_tail = d->use_tail && atoi(f) != 0;
+    // ANE_DEC_TAIL_SPIN: polls before a dependency wait times out (0: every
+    // wait fails at once; for tests of the timeout path)
+    d->tail_spin = kDecTailSpin;
+    if (const char* f = getenv("ANE_DEC_TAIL_SPIN")) d->tail_spin = (unsigned)strtoul(f, nullptr, 10);
+    if (d->use_tail) {
+      DCHK(op, dalloc(d, &d->xg_att, (size_t)R * D));
+      DCHK(op, dalloc(d, &d->xg_ffn, (size_t)R * D));
+      DCHK(op, dalloc(d, &d->rr_d, (size_t)R));
+      DCHK(op, dalloc(d, &d->ssq_wo, (size_t)(D / 32) * R));
+      DCHK(op, dalloc(d, &d->ssq_w2, (size_t)(D / 32) * R));
+      DCHK(op, dalloc(d, &d->sync, (size_t)kDecTailSync));
+      DCHK(op, dalloc(d, &d->err_d, 1));
+      DCHK(op, hipMemset(d->xg_att, 0, (size_t)R * D * 2));
+      DCHK(op, hipMemset(d->xg_ffn, 0, (size_t)R * D * 2));
+      DCHK(op, hipMemset(d->rr_d, 0, (size_t)R * 4));
+      DCHK(op, hipMemset(d->sync, 0, (size_t)kDecTailSync * 4));
+      DCHK(op, hipMemset(d->err_d, 0, 4));
+    }
+  }
   DCHK(op, hipDeviceSynchronize());
   return ANE_OK;
 }
@@ -261,7 +299,10 @@ hipError_t gemm(ane_decoder* d, const half_t* A, const half_t* Bw, int M, int N,
 
 // One decode step for the active batch; every position/step index is read
 // from ctr_d on the device, so the same launches replay as a graph.
+int enqueue_step_tail(ane_decoder* d, float* logits, uint16_t* hist);
+
 int enqueue_step(ane_decoder* d, float* logits, uint16_t* hist) {
+  if (d->use_tail) return enqueue_step_tail(d, logits, hist);
   const char* op = "step";
   const int D = d->D, H = d->H, N1 = d->N1, nb = d->nseq;
   const hipStream_t st = d->stream;
@@ -299,13 +340,76 @@ int enqueue_step(ane_decoder* d, float* logits, uint16_t* hist) {
   return ANE_OK;
 }
 
+// The same step with each layer's GEMM chain fused into one launch
+// (decode_tail.hip): per layer the attention kernel, then the tail kernel
+// (Wo, W1|W3, W2 and the next layer's QKV partials).  Norm inputs are
+// fp16(x * gain) with the 1 / rms applied to the GEMM outputs.
+int enqueue_step_tail(ane_decoder* d, float* logits, uint16_t* hist) {
+  const char* op = "step";
+  const int D = d->D, H = d->H, N1 = d->N1, nb = d->nseq, L = d->L;
+  const hipStream_t st = d->stream;
+  DCHK(op, dec_row_xg(d->x, d->xg_att, d->rr_d, d->P + d->off_embed, d->tok_d, d->P + d->off[0].g_att, nb, D, d->V,
+                      st));
+  DCHK(op, skinny_partials(d->xg_att, d->fwqkv, d->kpart, d->kpart_cap, N1, D, st));
+  for (int l = 0; l < L; l++) {
+    const DecLayerOff& o = d->off[l];
+    DecAttnArgs aa;
+    aa.qkv_part = d->kpart; aa.qkv_ks = l == 0 ? skinny_splits(N1, D) : 1; aa.rr = d->rr_d;
+    aa.rope_cos = d->rope_cos; aa.rope_sin = d->rope_sin;
+    aa.kc = d->kc + (size_t)l * d->B * d->NKV * d->C * 64;
+    aa.vc = d->vc + (size_t)l * d->B * d->NKV * d->C * 64;
+    aa.ctr = d->ctr_d; aa.part = d->apart; aa.att = d->att; aa.nb = nb;
+    aa.NH = d->NH; aa.NKV = d->NKV; aa.max_ctx = d->C; aa.nsplit = d->nsplit; aa.scale = 0.125f;
+    aa.form = d->attn_form;
+    DCHK(op, dec_attention(aa, st));
+    const bool last = l + 1 == L;
+    TailArgs t;
+    t.att = d->att; t.x = d->x;
+    t.wo = d->fwo + (size_t)l * D * D; t.w13 = d->fw13 + (size_t)l * 2 * H * D; t.w2 = d->fw2 + (size_t)l * D * H;
+    t.wqkv_next = last ? nullptr : d->fwqkv + (size_t)(l + 1) * N1 * D;
+    t.g_ffn = d->P + o.g_ffn;
+    t.g_next = last ? d->P + d->off_gfinal : d->P + d->off[l + 1].g_att;
+    t.xg_ffn = d->xg_ffn; t.gate = d->gate; t.xg_next = d->xg_att; t.rr_next = d->rr_d;
+    t.p_q = d->kpart;
+    t.ssq_wo = d->ssq_wo; t.ssq_w2 = d->ssq_w2; t.sync = d->sync; t.gstep = d->ctr_d + 2; t.err = d->err_d;
+    t.spin_limit = d->tail_spin;
+    t.D = D; t.H = H; t.N1 = N1; t.layer = l; t.L = L;
+    t.b_wo = D / 32; t.b_13 = H / 32; t.b_w2 = D / 32; t.b_q = last ? 0 : N1 / 32;
+    DCHK(op, dec_tail(t, st));
+  }
+  SkinnyArgs s;
+  memset(&s, 0, sizeof s);
+  s.nb = nb;
+  s.X = d->xg_att; s.W = d->fembed; s.N = d->V; s.K = D; s.amax = d->amax;
+  s.logits = logits; s.nvalid = d->V; s.rr = d->rr_d;
+  DCHK(op, classifier_argmax(s, st));
+  DCHK(op, argmax_reduce(d->tok_d, hist, d->ctr_d + 1, d->amax, d->V / 32, nb, st));
+  DCHK(op, dec_advance(d->ctr_d, st));
+  return ANE_OK;
+}
+
+// After a synchronised step: a dependency wait of the fused chain that timed
+// out leaves *err set (and every later launch exits at once); report it and
+// clear the chain's state so the decoder can run again.
+int check_tail(ane_decoder* d, const char* op) {
+  if (!d->use_tail) return ANE_OK;
+  int err = 0;
+  DCHK(op, hipMemcpy(&err, d->err_d, 4, hipMemcpyDeviceToHost));
+  if (!err) return ANE_OK;
+  DCHK(op, hipMemset(d->sync, 0, (size_t)kDecTailSync * 4));
+  DCHK(op, hipMemset(d->ctr_d + 2, 0, 4));
+  DCHK(op, hipMemset(d->err_d, 0, 4));
+  DCHK(op, hipDeviceSynchronize());
+  return dfail(d, ANE_ERR_HIP, "storiesane decode %s: a dependency wait of the fused layer kernel timed out", op);
+}
+
 int copy_out(ane_decoder* d, uint16_t* next_tok, float* logits) {
   const char* op = "copy out";
   if (next_tok) DCHK(op, hipMemcpyAsync(next_tok, d->tok_d, (size_t)d->nseq * 2, hipMemcpyDeviceToHost, d->stream));
   if (logits)
     DCHK(op, hipMemcpyAsync(logits, d->logits_d, (size_t)d->nseq * d->V * 4, hipMemcpyDeviceToHost, d->stream));
   DCHK(op, hipStreamSynchronize(d->stream));
-  return ANE_OK;
+  return check_tail(d, op);
 }
 
 }  // namespace
@@ -490,7 +594,7 @@ extern "C" int ane_decode_generate(ane_decoder* d, int32_t nsteps, uint16_t* out
   DCHK(op, hipEventElapsedTime(&ms, d->ev0, d->ev1));
   d->last_ms = ms;
   d->pos += nsteps;
-  return ANE_OK;
+  return check_tail(d, op);
 }
 
 extern "C" int32_t ane_decode_position(ane_decoder* d) { return d ? d->pos : -1; }

@@ -1,6 +1,10 @@
 """Greedy KV-cache decoding on the GPU against the CPU decode oracle
 (oracle/refdecode.c, pinned in tests/test_oracle_decode.py).
 
+The per-layer GEMM chain has two implementations -- one fused launch per
+layer (the default where every block of it fits on the GPU at once) and one
+launch per GEMM (ANE_DEC_TAIL=0) -- and the model-level tests run both.
+
 Logits are compared at max-abs <= 2e-2 (fp16 weights, activations and KV
 cache; fp32 accumulation), the contract's logit tolerance.  Greedy choices
 are checked the way a tolerance allows: the token the GPU picks must have an
@@ -134,7 +138,9 @@ def test_long_prefix_multi_chunk_attention(form, plen, max_ctx, monkeypatch):
     assert max(errs) <= TOL
 
 
-def test_generate_graph_equals_eager_steps_and_oracle_choices():
+@pytest.mark.parametrize("tail", ["1", "0"])
+def test_generate_graph_equals_eager_steps_and_oracle_choices(tail, monkeypatch):
+    monkeypatch.setenv("ANE_DEC_TAIL", tail)
     cfg = ane.tiny_decode()
     nseq, plen, nsteps = 4, 64, 12
     p, prefix = _setup(cfg, nseq, plen, 31, std=0.08)
@@ -159,12 +165,14 @@ def test_generate_graph_equals_eager_steps_and_oracle_choices():
     _check_choice(gen, ref_lg[:, 1:])
 
 
+@pytest.mark.parametrize("tail", ["1", "0"])
 @pytest.mark.parametrize("form", ["split", "wide"])
-def test_full_size_gqa_model_matches_oracle(form, monkeypatch):
+def test_full_size_gqa_model_matches_oracle(form, tail, monkeypatch):
     """The decode benchmark's model (12 layers, dim 768, 12/4 heads,
     vocab 32000), two sequences, 64-token prefix, three forced steps, in
-    both decode-attention forms."""
+    both decode-attention forms and both GEMM-chain forms."""
     monkeypatch.setenv("ANE_DEC_ATTN", form)
+    monkeypatch.setenv("ANE_DEC_TAIL", tail)
     cfg = ane.decode_gqa()
     nseq, plen, nsteps = 2, 64, 3
     p, prefix = _setup(cfg, nseq, plen, 4, std=0.02)
@@ -212,13 +220,15 @@ def test_decoder_errors():
     assert ei.value.code == _lib.ANE_ERR_CLOSED
 
 
+@pytest.mark.parametrize("tail", ["1", "0"])
 @pytest.mark.parametrize("heads,kv_heads", [(4, 2), (6, 2), (3, 1)])
-def test_full_batch_of_64_every_sequence(heads, kv_heads):
+def test_full_batch_of_64_every_sequence(heads, kv_heads, tail, monkeypatch):
     """64 sequences (every decode row) at dims 256, 384 and 192: the
     classifier splits K over 2, 3 and 2 waves (4, 6 and 3 windows; one wave
     holding a single zeroed-surplus window at 192), and the argmax transpose
     covers tokens 62-63 of the last MFMA tile.  Prefill, forced steps, and
     greedy Generate, every sequence against the oracle."""
+    monkeypatch.setenv("ANE_DEC_TAIL", tail)
     cfg = ane.tiny_decode(heads=heads, kv_heads=kv_heads, dim=64 * heads, layers=1)
     nseq, plen, nsteps = 64, 64, 2
     p, prefix = _setup(cfg, nseq, plen, 81)
@@ -244,3 +254,32 @@ def test_full_batch_of_64_every_sequence(heads, kv_heads):
     inputs = np.concatenate([t0[:, None], gen[:, :-1]], 1)
     _, g_lg = oracle.decode(cfg, p, prefix, 3, forced=inputs, want_logits=True)
     _check_choice(gen, g_lg[:, 1:])
+
+
+def test_fused_chain_wait_timeout_is_reported(monkeypatch):
+    """A dependency wait of the fused layer kernel that times out is an
+    error of the call (the host forces it: a poll limit of 0 fails every
+    wait at once, and every block still exits); the decoder's counters are
+    reset, and another decoder of the same process decodes normally."""
+    cfg = ane.tiny_decode()
+    p, prefix = _setup(cfg, 2, 64, 61)
+    monkeypatch.setenv("ANE_DEC_TAIL", "1")
+    monkeypatch.setenv("ANE_DEC_TAIL_SPIN", "0")
+    dec = ane.Decoder(cfg, p, max_batch=2, max_ctx=128)
+    try:
+        with pytest.raises(ane.EngineError) as ei:
+            dec.Prefill(prefix)
+            dec.Step()
+        assert ei.value.code == _lib.ANE_ERR_HIP and "timed out" in str(ei.value)
+    finally:
+        dec.Close()
+    monkeypatch.delenv("ANE_DEC_TAIL_SPIN")
+    forced = np.random.default_rng(62).integers(0, cfg.vocab, (2, 1)).astype(np.uint16)
+    _, ref_lg = oracle.decode(cfg, p, prefix, 1, forced=forced, want_logits=True)
+    dec = ane.Decoder(cfg, p, max_batch=2, max_ctx=128)
+    try:
+        _, lg0 = dec.Prefill(prefix, want_logits=True)
+        _, lg1 = dec.Step(forced[:, 0], want_logits=True)
+    finally:
+        dec.Close()
+    assert max(np.abs(lg0 - ref_lg[:, 0]).max(), np.abs(lg1 - ref_lg[:, 1]).max()) <= TOL
