@@ -37,8 +37,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) half_t Vt[HD * VST];
 
   const int S = a.S, NH = a.NH, D = NH * HD, D3 = 3 * D;
-  prefetch_slice(a.pf, a.pf_bytes, ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x,
-                 (size_t)gridDim.x * gridDim.y * gridDim.z);
+  const size_t pf_part = ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  const size_t pf_parts = (size_t)gridDim.x * gridDim.y * gridDim.z;
   const int nthr = blockDim.x, tid = threadIdx.x;
   // Block -> (sequence b, head h, q-block pairs [p0, p0 + np)).  Grid
   // (pair groups, NH, nseq), or with split_from > 0 a 1-D grid: heads below
@@ -59,11 +59,23 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const size_t tok0 = (size_t)b * S;
   const half_t* base = a.qkv + tok0 * D3;
 
+  // The thread's first V block (8 keys x 8 dims) is loaded ahead, in flight
+  // with the first K batch; the prefetch of the next GEMM's weights is
+  // issued after both and consumed once the staging is done.
+  const int nkc = S / 8;
+  half8 vpre[8];
+  if (tid < S) {
+    const int kc = tid % nkc, dc = tid / nkc;
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) vpre[jj] = ld_h8(base + (size_t)(kc * 8 + jj) * D3 + 2 * D + h * HD + dc * 8);
+  }
+
   // ---- stage K: RoPE (+ QK-norm), swizzled rows of 64 halves ----------------
   // Batches of KB chunks per thread: every global load of a batch (the K
   // chunk and its cos / sin as float4) is issued before the first use, so
   // the batch pays one memory latency instead of one per chunk.
   constexpr int KB = 8;
+  Prefetch pf{};
   for (int c0 = tid; c0 < S * 8; c0 += KB * nthr) {
     half8 raw[KB];
     float4 cs4[KB], sn4[KB];
@@ -77,6 +89,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
         sn4[u] = *reinterpret_cast<const float4*>(a.rope_sin + j * 32 + ch * 4);
       }
     }
+    if (c0 == tid) pf = prefetch_begin(a.pf, a.pf_bytes, pf_part, pf_parts);
 #pragma unroll
     for (int u = 0; u < KB; u++) {
       const int c = c0 + u * nthr;
@@ -117,16 +130,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 
   // ---- stage V^T (8 keys x 8 dims per thread), value embeddings added --------
   for (int blk = tid; blk < S; blk += nthr) {
-    const int nkc = S / 8;
     const int kc = blk % nkc, dc = blk / nkc;
-    float v[8][8];
+    half8 raw[8];
 #pragma unroll
-    for (int jj = 0; jj < 8; jj++) {
-      const int j = kc * 8 + jj;
-      half8 raw = ld_h8(base + (size_t)j * D3 + 2 * D + h * HD + dc * 8);
+    for (int jj = 0; jj < 8; jj++)
+      raw[jj] = blk == tid ? vpre[jj] : ld_h8(base + (size_t)(kc * 8 + jj) * D3 + 2 * D + h * HD + dc * 8);
+    if (a.ve_x) {
+      float v[8][8];
 #pragma unroll
-      for (int i = 0; i < 8; i++) v[jj][i] = (float)raw[i];
-      if (a.ve_x) {
+      for (int jj = 0; jj < 8; jj++) {
+        const int j = kc * 8 + jj;
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[jj][i] = (float)raw[jj][i];
         const float* xr = a.ve_x + (tok0 + j) * D;
         float gp = 0.f;
 #pragma unroll
@@ -138,15 +153,18 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
           for (int i = 0; i < 8; i++) v[jj][i] += gate * er[i];
         }
+#pragma unroll
+        for (int i = 0; i < 8; i++) raw[jj][i] = (half_t)v[jj][i];
       }
     }
+    // 8 x 8 transpose of fp16 values (no conversion without value embeddings)
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       half4 lo, hi;
 #pragma unroll
       for (int jj = 0; jj < 4; jj++) {
-        lo[jj] = (half_t)v[jj][i];
-        hi[jj] = (half_t)v[jj + 4][i];
+        lo[jj] = raw[jj][i];
+        hi[jj] = raw[jj + 4][i];
       }
       half_t* dst = Vt + (dc * 8 + i) * VST + kc * 8;
       *reinterpret_cast<half4*>(dst) = lo;
@@ -154,15 +172,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     }
     if (a.qkvt && first) {
 #pragma unroll
-      for (int jj = 0; jj < 8; jj++) {
-        half8 w;
-#pragma unroll
-        for (int i = 0; i < 8; i++) w[i] = (half_t)v[jj][i];
-        st_h8(a.qkvt + (tok0 + kc * 8 + jj) * D3 + 2 * D + h * HD + dc * 8, w);
-      }
+      for (int jj = 0; jj < 8; jj++) st_h8(a.qkvt + (tok0 + kc * 8 + jj) * D3 + 2 * D + h * HD + dc * 8, raw[jj]);
     }
   }
   __syncthreads();
+  prefetch_end(pf, a.pf, a.pf_bytes, pf_part, pf_parts);
 
   // ---- per wave: q-block pair ------------------------------------------------
   const int lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;

@@ -209,6 +209,10 @@ def main():
     ap.add_argument("--train-steps", type=int, default=5)
     ap.add_argument("--no-decode", action="store_true", help="skip the GQA decode leg")
     ap.add_argument("--no-moe", action="store_true", help="skip the MoE FFN leg")
+    ap.add_argument("--no-fwd", action="store_true",
+                    help="skip the forward+loss leg (the headline line then carries only the other legs; for "
+                         "profiling those legs alone)")
+    ap.add_argument("--no-power", action="store_true", help="skip the board-power pass of the forward")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
@@ -227,6 +231,28 @@ def main():
     B, S = args.batch, cfg.seq
     params = ane.init_params(cfg, seed=0, std=0.02)
     tok, tgt = ane.make_tokens(cfg, B, seed=2)
+    out = forward_leg(ane, args, cfg, params, tok, tgt) if not args.no_fwd else {"metric": METRIC, "value": None}
+    if not args.no_train:
+        out["train_step_b16"] = train_bench(ane, args.arch, args.train_steps)
+    if not args.no_decode:
+        out["decode"] = decode_bench(ane, args.decode_steps)
+    if not args.no_moe:
+        out["moe_ffn"] = moe_bench(ane)
+    if not args.no_cpu:
+        # every CPU this process may run on (on the GPU pool: the 16-CPU share
+        # of one GPU, whatever nproc reports for the whole host)
+        threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+        out["cpu_baseline"] = cpu_baseline(cfg, params, tok, tgt, threads)
+        if out["value"]:
+            out["gpu_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
+    print(json.dumps(out), flush=True)
+
+
+def forward_leg(ane, args, cfg, params, tok, tgt):
+    """The headline: stories110M forward + loss at batch x 256, timed over
+    args.steps calls after args.warmup untimed ones; then the power pass and
+    the per-launch HIP-event pass."""
+    B, S = args.batch, cfg.seq
     # resident token stream: window b = stream[b*(S+1) : b*(S+1)+S+1]
     stream = np.concatenate([np.concatenate([tok[b], tgt[b][-1:]]) for b in range(B)]).astype(np.uint16)
     pos = np.arange(B, dtype=np.uint64) * np.uint64(S + 1)
@@ -248,7 +274,7 @@ def main():
     from ane.perf import Sampler
     sampler = Sampler()
     power = {}
-    if sampler.available:
+    if sampler.available and not args.no_power:
         n_pw = max(args.steps, 200)
         snap = sampler.Start()
         for _ in range(n_pw):
@@ -291,19 +317,7 @@ def main():
         out["mfma_util_projection_gemms"] = round(g_fl / (g_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)
         out["kernel_ms_per_step"] = {k: round(v["ms"] / args.steps, 4) for k, v in prof.items()}
     eng.Destroy()
-    if not args.no_train:
-        out["train_step_b16"] = train_bench(ane, args.arch, args.train_steps)
-    if not args.no_decode:
-        out["decode"] = decode_bench(ane, args.decode_steps)
-    if not args.no_moe:
-        out["moe_ffn"] = moe_bench(ane)
-    if not args.no_cpu:
-        # every CPU this process may run on (on the GPU pool: the 16-CPU share
-        # of one GPU, whatever nproc reports for the whole host)
-        threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-        out["cpu_baseline"] = cpu_baseline(cfg, params, tok, tgt, threads)
-        out["gpu_over_cpu"] = round(out["value"] / out["cpu_baseline"]["value"], 1)
-    print(json.dumps(out), flush=True)
+    return out
 
 
 if __name__ == "__main__":
