@@ -13,8 +13,13 @@ it carries:
                   per launch / mean launch time from HIP events recorded on
                   the engine's stream in a second pass of the same steps)
                   against the MI355X dense fp16 MFMA peak; `traffic` is its
-                  HBM bytes per launch from the committed rocprofv3 --pmc
-                  summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated);
+                  HBM bytes per launch and `mfma_busy` the fraction of its
+                  cycles with the matrix cores busy, both from the committed
+                  rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE,
+                  copy-calibrated; SQ_VALU_MFMA_BUSY_CYCLES over
+                  GRBM_GUI_ACTIVE);
+  mfma_busy_projection_gemms  the same counter over the five projection
+                  GEMM classes, weighted by their measured time;
   train_step_b16  BASELINE configs[2]: fwd + bwd + clip + AdamW, B16 x 256;
   decode          BASELINE configs[3]: GQA KV-cache greedy decode, tokens/s
                   and achieved GB/s against HBM peak;
@@ -42,21 +47,27 @@ PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
-TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "fwd_gemm_b32_llama2_pmc_traffic.md")
+COUNTER_SUMMARY = os.path.join(ROOT, "profiles", "fwd_b32_llama2_pmc_counters.md")
 
 
-def measured_traffic(kernel_class):
-    """HBM bytes per launch of a forward GEMM class, as measured by the two
-    rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE, copy-calibrated) whose
-    summary is committed in profiles/; None when not measured."""
+def measured_counter(key, kernel_class, cast=float):
+    """A per-launch figure of a forward kernel class from the committed
+    rocprofv3 --pmc summary (lines `traffic: <class> <bytes>` and
+    `mfma_busy: <class> <fraction>`); None when not measured."""
     try:
-        for line in open(TRAFFIC_SUMMARY):
+        for line in open(COUNTER_SUMMARY):
             parts = line.split()
-            if len(parts) == 3 and parts[0] == "traffic:" and parts[1] == kernel_class:
-                return int(parts[2])
+            if len(parts) == 3 and parts[0] == key + ":" and parts[1] == kernel_class:
+                return cast(parts[2])
     except OSError:
         pass
     return None
+
+
+def measured_traffic(kernel_class):
+    """HBM bytes per launch of a forward kernel class (FETCH_SIZE +
+    WRITE_SIZE, copy-calibrated)."""
+    return measured_counter("traffic", kernel_class, int)
 
 
 def cpu_model():
@@ -304,17 +315,22 @@ def forward_leg(ane, args, cfg, params, tok, tgt):
         eng.ProfileEnable(False)
         gemm_cls = ["qkv_gemm", "wo_gemm", "ffn_up_gemm", "ffn_down_gemm", "classifier_gemm"]
         dom = max(prof, key=lambda k: prof[k]["ms"])
+        counted = args.arch == "llama2" and B == 32  # the configuration the counter summary was taken on
         d = prof[dom]
         avg_ms = d["ms"] / max(1, d["launches"])
         per_launch = d["flops"] / max(1, d["launches"])
         achieved = per_launch / (avg_ms * 1e-3) / 1e12
         out["roofline"] = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
                            "peak": PEAK_FP16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-                           "traffic": measured_traffic(dom) if args.arch == "llama2" and B == 32 else None,
+                           "traffic": measured_traffic(dom) if counted else None,
+                           "mfma_busy": measured_counter("mfma_busy", dom) if counted else None,
                            "avg_launch_ms": round(avg_ms, 5), "flops_per_launch": per_launch}
         g_ms = sum(prof[k]["ms"] for k in gemm_cls)
         g_fl = sum(prof[k]["flops"] for k in gemm_cls)
         out["mfma_util_projection_gemms"] = round(g_fl / (g_ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS, 4)
+        busy = {k: measured_counter("mfma_busy", k) for k in gemm_cls} if counted else {}
+        if busy and all(v is not None for v in busy.values()):
+            out["mfma_busy_projection_gemms"] = round(sum(busy[k] * prof[k]["ms"] for k in gemm_cls) / g_ms, 4)
         out["kernel_ms_per_step"] = {k: round(v["ms"] / args.steps, 4) for k, v in prof.items()}
     eng.Destroy()
     return out
