@@ -105,6 +105,8 @@ SIGNATURES = {
                                  C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "ane_debug_gemm_epi": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _u16, _u16, C.c_void_p, C.c_void_p,
                                      _fp, _fp, C.c_float, C.c_float, C.c_int, C.c_int, C.c_int, C.c_int]),
+    "ane_debug_gemm_norm": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, _u16, _u16, _fp, _u16, _fp, _fp, _fp,
+                                      C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]),
     "ane_debug_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, C.c_float, C.c_int, _u16,
                                       _u16, _fp]),
     "ane_debug_transpose2": (C.c_int, [C.c_int, C.c_int, _u16, _u16, C.c_int, C.c_int, _u16, _u16]),

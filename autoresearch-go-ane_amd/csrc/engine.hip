@@ -347,6 +347,7 @@ static int open_impl(ane_engine* e) {
     HIPCHK(op, dalloc(e, &e->xmid, T * D));
   }
   HIPCHK(op, dalloc(e, &e->xh, T * D));
+  if (llama) HIPCHK(op, dalloc(e, &e->ssq_part, (size_t)kRrMaxParts * T));
   HIPCHK(op, dalloc(e, &e->qkv, T * 3 * D));
   HIPCHK(op, dalloc(e, &e->att, T * D));
   HIPCHK(op, dalloc(e, &e->gate, T * H));
@@ -374,6 +375,10 @@ extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_e
   apply_option_defaults(&e->opt);
   e->device = e->opt.device;
   if (const char* g = getenv("ANE_GRAPHS")) e->use_graph = atoi(g) != 0;
+  // ANE_FUSED_NORM=1: the llama2 eval forward defers each RMSNorm into the
+  // GEMMs around it instead of launching it
+  if (const char* g = getenv("ANE_FUSED_NORM")) e->fused_norm = atoi(g) != 0;
+  if (const char* g = getenv("ANE_FUSED_PF")) e->fused_pf = atoi(g) != 0;
   if (const char* g = getenv("ANE_PHASE_EVERY")) e->ph_period = atoi(g) > 0 ? atoi(g) : 1;
   e->lr = e->opt.lr;
   int rc = validate_cfg(e, e->cfg);
@@ -517,7 +522,20 @@ extern "C" int ane_set_tokens(ane_engine* e, const uint16_t* tokens, int64_t n) 
 // In training mode (train != 0, buffers of ensure_train) every layer keeps
 // its activations: the residual GEMMs write out-of-place into the next
 // layer's input buffer, so nothing is copied.
-int forward_body(ane_engine* e, int nseq, int train) {
+//
+// defer_norm (llama2 eval forward, with ANE_FUSED_NORM=1): no RMSNorm
+// launch.  Each norm's input x comes with xh = fp16(x * gain) and per-row
+// partial sums of x^2 (from the embedding, or from the residual GEMM's
+// epilogue, one partial per column block); the GEMM that consumes xh scales
+// its (linear) output rows by rr = 1 / rms(x) in its epilogue.  The final
+// norm is left to the classifier (e->fwd_rr_nparts > 0).  Off by default:
+// the norm launches also stream the next GEMM's weights through the caches;
+// without any such launch the GEMMs lose more than the norms cost (B32:
+// 2.88 ms per forward against 2.82), and with launches that only stream the
+// weights (ANE_FUSED_PF, default on) the two paths are within the ~3%
+// box-to-box spread (2.78 against 2.82 ms on one box, 2.75 against 2.67 on
+// another).
+int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
   const char* op = "forward";
   const ane_model_cfg& c = e->cfg;
   const int D = c.dim, H = c.hidden, V = c.vocab, S = c.seq, NH = c.heads, L = c.layers;
@@ -526,9 +544,28 @@ int forward_body(ane_engine* e, int nseq, int train) {
   const float* P = e->P;
   hipStream_t st = e->stream;
   TrainBufs& tb = e->tr;
+  const bool fused = defer_norm && !train && llama && e->fused_norm && e->ssq_part;
+  e->fwd_rr_nparts = 0;
+  // the residual GEMMs' tile fixes how many partials each norm has
+  int res_bm = 0, res_bn = 0;
+  if (fused) {
+    gemm_pick_tile(T, D, H, EPI_RESID_NORM, &res_bm, &res_bn);
+    if (!res_bn || D / res_bn > kRrMaxParts)
+      return eng_fail(e, ANE_ERR_ARG, "storiesane forward: no residual tile for dim=%d", D);
+  }
+  // RR epilogue parameters over the current partials
+  auto rr = [&](EpiParams& p, int nparts) {
+    p.rr_part = e->ssq_part; p.rr_ld = T; p.rr_nparts = nparts; p.rr_dim = D;
+  };
+  int nparts = 1;
 
   float* x_first = train ? tb.L[0].xin : e->x;
-  if (llama) {
+  if (llama && fused) {
+    prof_begin(e, 7);
+    HIPCHK(op, embed_xg(x_first, e->xh, e->ssq_part, P + e->pm.embed, e->tok, P + e->pm.L[0].g_att, T, D, V, st,
+                        e->ls[0].wqkv, (size_t)3 * D * D * sizeof(half_t)));
+    prof_end(e, 0, (double)T * D * 10);
+  } else if (llama) {
     prof_begin(e, 7);
     HIPCHK(op, embed_lookup(x_first, P + e->pm.embed, e->tok, T, D, V, st));
     prof_end(e, 0, (double)T * D * 8);
@@ -553,17 +590,26 @@ int forward_body(ane_engine* e, int nseq, int train) {
       A.xin = e->x; A.x2 = e->x; A.xn = e->xh; A.xn2 = e->xh; A.qkv = e->qkv; A.att = e->att; A.gate = e->gate;
     }
     float* xout = train ? (l + 1 < L ? tb.L[l + 1].xin : tb.xlast) : e->x;
-    prof_begin(e, 6);
-    // each memory-bound kernel also streams the next GEMM's weights through
-    // the caches (prefetch_slice): QKV here, Wo in attention, W1|W3 + W2 in
-    // the FFN norm, the classifier in the final norm
-    HIPCHK(op, rmsnorm_f16(A.xn, A.xin, nullptr, nullptr, llama ? P + o.g_att : nullptr, T, D, st, s.wqkv,
-                           (size_t)3 * D * D * sizeof(half_t)));
-    prof_end(e, 0, (double)T * D * 6);
+    if (!fused) {
+      prof_begin(e, 6);
+      // each memory-bound kernel also streams the next GEMM's weights through
+      // the caches (prefetch_slice): QKV here, Wo in attention, W1|W3 + W2 in
+      // the FFN norm, the classifier in the final norm
+      HIPCHK(op, rmsnorm_f16(A.xn, A.xin, nullptr, nullptr, llama ? P + o.g_att : nullptr, T, D, st, s.wqkv,
+                             (size_t)3 * D * D * sizeof(half_t)));
+      prof_end(e, 0, (double)T * D * 6);
+    }
+    if (fused && l > 0 && e->fused_pf) {
+      prof_begin(e, 6);
+      HIPCHK(op, prefetch_weights(s.wqkv, (size_t)3 * D * D * sizeof(half_t), st));
+      prof_end(e, 0, (double)3 * D * D * 2);
+    }
     {
       EpiParams p;
       p.C = A.qkv; p.ldc = 3 * D;
-      HIPCHK(op, eng_gemm(e, 0, A.xn, D, false, s.wqkv, D, false, T, 3 * D, D, EPI_STORE_H, p));
+      if (fused) rr(p, nparts);
+      HIPCHK(op, eng_gemm(e, 0, A.xn, D, false, s.wqkv, D, false, T, 3 * D, D, fused ? EPI_STORE_H_RR : EPI_STORE_H,
+                          p));
     }
     {
       AttnArgs a;
@@ -586,20 +632,37 @@ int forward_body(ane_engine* e, int nseq, int train) {
       EpiParams p;
       p.C = A.x2; p.ldc = D; p.R = A.xin;
       if (!llama) { p.alpha_ptr = P + e->pm.resid + l; p.X0 = e->x0; p.beta_ptr = P + e->pm.x0l + l; }
-      HIPCHK(op, eng_gemm(e, 1, A.att, D, false, s.wo, D, false, T, D, D, EPI_RESID, p));
+      if (fused) {
+        p.C2 = A.xn2; p.ldc2 = D; p.gain = P + o.g_ffn; p.ssq_part = e->ssq_part; p.ssq_ld = T;
+        HIPCHK(op, eng_gemm(e, 1, A.att, D, false, s.wo, D, false, T, D, D, EPI_RESID_NORM, p, res_bm, res_bn));
+        nparts = D / res_bn;
+      } else {
+        HIPCHK(op, eng_gemm(e, 1, A.att, D, false, s.wo, D, false, T, D, D, EPI_RESID, p));
+      }
     }
-    prof_begin(e, 6);
-    HIPCHK(op, rmsnorm_f16(A.xn2, A.x2, nullptr, nullptr, llama ? P + o.g_ffn : nullptr, T, D, st, s.w13,
-                           ((size_t)(llama ? 2 : 1) * H * D + (size_t)D * H) * sizeof(half_t)));  // W1|W3, W2
-    prof_end(e, 0, (double)T * D * 6);
+    if (!fused) {
+      prof_begin(e, 6);
+      HIPCHK(op, rmsnorm_f16(A.xn2, A.x2, nullptr, nullptr, llama ? P + o.g_ffn : nullptr, T, D, st, s.w13,
+                             ((size_t)(llama ? 2 : 1) * H * D + (size_t)D * H) * sizeof(half_t)));  // W1|W3, W2
+      prof_end(e, 0, (double)T * D * 6);
+    }
     {
       EpiParams p;
       p.C = A.gate; p.ldc = H;
       p.C2 = A.h13; p.ldc2 = llama ? 2 * H : H;
-      if (llama)
+      if (fused) {
+        if (e->fused_pf) {
+          prof_begin(e, 6);
+          HIPCHK(op, prefetch_weights(s.w13, ((size_t)2 * H * D + (size_t)D * H) * sizeof(half_t), st));  // W1|W3, W2
+          prof_end(e, 0, (double)3 * H * D * 2);
+        }
+        rr(p, nparts);
+        HIPCHK(op, eng_gemm(e, 2, A.xn2, D, false, s.w13, D, false, T, 2 * H, D, EPI_SWIGLU_RR, p));
+      } else if (llama) {
         HIPCHK(op, eng_gemm(e, 2, A.xn2, D, false, s.w13, D, false, T, 2 * H, D, EPI_SWIGLU, p));
-      else
+      } else {
         HIPCHK(op, eng_gemm(e, 2, A.xn2, D, false, s.w13, D, false, T, H, D, EPI_RELU2, p));
+      }
     }
     {
       EpiParams p;
@@ -608,8 +671,25 @@ int forward_body(ane_engine* e, int nseq, int train) {
         p.alpha_ptr = P + e->pm.resid + l; p.X0 = e->x0; p.beta_ptr = P + e->pm.x0l + l;
         if (l == L / 2 - 1) p.C2 = e->xmid;  // backout snapshot (ane/train_full.go:447-449)
       }
-      HIPCHK(op, eng_gemm(e, 3, A.gate, H, false, s.w2, H, false, T, D, H, EPI_RESID, p));
+      if (fused) {
+        // the next norm's inputs: the next layer's attention norm, or the final norm
+        p.C2 = A.xn; p.ldc2 = D; p.gain = P + (l + 1 < L ? e->pm.L[l + 1].g_att : e->pm.g_final);
+        p.ssq_part = e->ssq_part; p.ssq_ld = T;
+        HIPCHK(op, eng_gemm(e, 3, A.gate, H, false, s.w2, H, false, T, D, H, EPI_RESID_NORM, p, res_bm, res_bn));
+        nparts = D / res_bn;
+      } else {
+        HIPCHK(op, eng_gemm(e, 3, A.gate, H, false, s.w2, H, false, T, D, H, EPI_RESID, p));
+      }
     }
+  }
+  if (fused) {  // xh = fp16(x * g_final); the classifier applies 1 / rms
+    if (e->fused_pf) {
+      prof_begin(e, 6);
+      HIPCHK(op, prefetch_weights(e->embed_h, (size_t)V * D * sizeof(half_t), st));
+      prof_end(e, 0, (double)V * D * 2);
+    }
+    e->fwd_rr_nparts = nparts;
+    return ANE_OK;
   }
   // final norm (backout first for nanochat, ane/common.go:385-389)
   float* xl = train ? tb.xlast : e->x;
@@ -644,7 +724,12 @@ int head_loss(ane_engine* e, int nseq, float* colscale, float dscale) {
   int bm = e->ce_bm, bn = 0;
   if (V % 256 == 0 && T % 256 == 0 && (long)(V / 256) * (T / 256) >= 512) bm = bn = 256;
   const int np = V / bm;
-  HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_CE, p, bm, bn));
+  if (e->fwd_rr_nparts > 0) {  // the final norm deferred into the classifier
+    p.rr_part = e->ssq_part; p.rr_ld = T; p.rr_nparts = e->fwd_rr_nparts; p.rr_dim = D;
+    HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_CE_RR, p, bm, bn));
+  } else {
+    HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_CE, p, bm, bn));
+  }
   prof_begin(e, 7);
   HIPCHK(op, ce_reduce(e->loss_seq, e->lse, e->tok_loss, colscale, dscale, e->partial, np, e->tgt_logit, e->tgt, V, nseq,
                        S, e->stream));
@@ -666,14 +751,14 @@ void drop_fwd_graph(ane_engine* e) {
 static int fwd_loss(ane_engine* e, int nseq) {
   const char* op = "eval loss";
   if (!e->use_graph || e->prof_on) {
-    int rc = forward_body(e, nseq, 0);
+    int rc = forward_body(e, nseq, 0, true);
     if (!rc) rc = head_loss(e, nseq, nullptr, 0.f);
     return rc;
   }
   if (!e->fwd_exec || e->fwd_graph_nseq != nseq) {
     drop_fwd_graph(e);
     HIPCHK(op, hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
-    int rc = forward_body(e, nseq, 0);
+    int rc = forward_body(e, nseq, 0, true);
     if (!rc) rc = head_loss(e, nseq, nullptr, 0.f);
     hipGraph_t g = nullptr;
     const hipError_t h = hipStreamEndCapture(e->stream, &g);  // always leaves capture mode
@@ -903,6 +988,62 @@ done:
   return rc;
 }
 
+// The deferred-RMSNorm epilogues on one forced tile (host buffers).
+// epi 13 (EPI_RESID_NORM): X [M, N] fp32 in/out (X += acc), C [M, N] fp16 =
+// X * gain[col], ssq [N / bn][M] = per-row sums of X^2 over each block's bn
+// columns.  epi 14 (EPI_STORE_H_RR): C [M, N] fp16 = acc * rr[row]; epi 15
+// (EPI_SWIGLU_RR): C [M, N / 2] fp16 = SwiGLU of the interleaved W1|W3
+// columns of acc * rr[row]; rr = 1 / sqrt(sum of rr_part[p][row] over
+// p < nparts / rr_dim + 1e-5).
+extern "C" int ane_debug_gemm_norm(int epi, int M, int N, int K, const uint16_t* A, const uint16_t* B, float* X,
+                                   uint16_t* C, const float* gain, float* ssq, const float* rr_part, int nparts,
+                                   int rr_dim, int bm, int bn, int nw) {
+  if ((epi != EPI_RESID_NORM && epi != EPI_STORE_H_RR && epi != EPI_SWIGLU_RR) || bm <= 0 || bn <= 0 ||
+      (epi == EPI_RESID_NORM && (!X || !gain || !ssq)) || (epi != EPI_RESID_NORM && (!rr_part || nparts < 1))) {
+    g_debug_err = "storiesane debug: unsupported deferred-norm epilogue or missing operand";
+    return ANE_ERR_ARG;
+  }
+  int rc = ANE_OK;
+  void *dA = nullptr, *dB = nullptr, *dC = nullptr, *dX = nullptr, *dG = nullptr, *dS = nullptr, *dP = nullptr;
+  const size_t MN = (size_t)M * N;
+  const size_t cbytes = epi == EPI_SWIGLU_RR ? MN : MN * 2;
+  const size_t sbytes = (size_t)(N / bn) * M * 4;
+  GemmArgs g;
+  EpiParams p;
+  DBGCHK(hipMalloc(&dA, (size_t)M * K * 2));
+  DBGCHK(hipMalloc(&dB, (size_t)N * K * 2));
+  DBGCHK(hipMalloc(&dC, cbytes));
+  DBGCHK(hipMemcpy(dA, A, (size_t)M * K * 2, hipMemcpyHostToDevice));
+  DBGCHK(hipMemcpy(dB, B, (size_t)N * K * 2, hipMemcpyHostToDevice));
+  if (epi == EPI_RESID_NORM) {
+    DBGCHK(hipMalloc(&dX, MN * 4));
+    DBGCHK(hipMalloc(&dG, (size_t)N * 4));
+    DBGCHK(hipMalloc(&dS, sbytes));
+    DBGCHK(hipMemcpy(dX, X, MN * 4, hipMemcpyHostToDevice));
+    DBGCHK(hipMemcpy(dG, gain, (size_t)N * 4, hipMemcpyHostToDevice));
+    p.C = dX; p.ldc = N; p.R = (const float*)dX; p.C2 = dC; p.ldc2 = N; p.gain = (const float*)dG;
+    p.ssq_part = (float*)dS; p.ssq_ld = M;
+  } else {
+    DBGCHK(hipMalloc(&dP, (size_t)nparts * M * 4));
+    DBGCHK(hipMemcpy(dP, rr_part, (size_t)nparts * M * 4, hipMemcpyHostToDevice));
+    p.C = dC; p.ldc = epi == EPI_SWIGLU_RR ? N / 2 : N;
+    p.rr_part = (const float*)dP; p.rr_ld = M; p.rr_nparts = nparts; p.rr_dim = rr_dim;
+  }
+  g.A = (const half_t*)dA; g.B = (const half_t*)dB;
+  g.lda = K; g.ldb = K; g.M = M; g.N = N; g.K = K; g.a_t = false; g.b_t = false;
+  DBGCHK(gemm_run(g, epi, p, nullptr, bm, bn, nw, 0));
+  DBGCHK(hipDeviceSynchronize());
+  DBGCHK(hipMemcpy(C, dC, cbytes, hipMemcpyDeviceToHost));
+  if (epi == EPI_RESID_NORM) {
+    DBGCHK(hipMemcpy(X, dX, MN * 4, hipMemcpyDeviceToHost));
+    DBGCHK(hipMemcpy(ssq, dS, sbytes, hipMemcpyDeviceToHost));
+  }
+done:
+  for (void* q : {dA, dB, dC, dX, dG, dS, dP})
+    if (q) (void)hipFree(q);
+  return rc;
+}
+
 // The classifier epilogues on one forced tile (host buffers): EPI_CE writes
 // per-(block row, column) partials (max, sum exp(v - max)) and the target
 // logit of every column; with lse given, EPI_DLOGITS then writes the
@@ -981,12 +1122,13 @@ __global__ void debug_fill_kernel(half_t* p, size_t n, uint32_t seed) {
 extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw,
                                     int ns, int splits, int iters, const uint16_t* A, const uint16_t* B,
                                     float* avg_ms) {
-  if (epi != EPI_STORE_F && epi != EPI_STORE_H && epi != EPI_RESID && epi != EPI_SWIGLU && epi != EPI_CE) {
-    g_debug_err = "storiesane debug: epilogue must be STORE_F, STORE_H, RESID, SWIGLU or CE";
+  if (epi != EPI_STORE_F && epi != EPI_STORE_H && epi != EPI_RESID && epi != EPI_SWIGLU && epi != EPI_CE &&
+      epi != EPI_RESID_NORM && !epi_rr(epi)) {
+    g_debug_err = "storiesane debug: epilogue must be STORE_F, STORE_H, RESID, SWIGLU, CE or a deferred-norm form";
     return ANE_ERR_ARG;
   }
   int rc = ANE_OK;
-  void *dA = nullptr, *dB = nullptr, *dC = nullptr, *dX = nullptr, *dW = nullptr;
+  void *dA = nullptr, *dB = nullptr, *dC = nullptr, *dX = nullptr, *dW = nullptr, *dN = nullptr;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   GemmArgs g;
   EpiParams p;
@@ -999,9 +1141,15 @@ extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int
   g.splits = splits;
   g.ws = (float*)dW;
   // CE side buffers: targets (zeros), per-64-row-block partials, target logits
-  if (epi == EPI_CE) {
+  if (epi == EPI_CE || epi == EPI_CE_RR) {
     DBGCHK(hipMalloc(&dX, (size_t)N * 2 + (size_t)(M / 64) * N * sizeof(float2) + (size_t)N * 4 + 256));
     DBGCHK(hipMemset(dX, 0, (size_t)N * 2));
+  }
+  // deferred-norm side buffers (zeros): partials [16][max(M, N)], gain [N], ssq [16][M], fp16 copy [M, N]
+  if (epi == EPI_RESID_NORM || epi_rr(epi)) {
+    const size_t nside = (size_t)kRrMaxParts * (M > N ? M : N) + (size_t)N + (size_t)kRrMaxParts * M + (size_t)M * N;
+    DBGCHK(hipMalloc(&dN, nside * 4));
+    DBGCHK(hipMemset(dN, 0, nside * 4));
   }
   if (A) DBGCHK(hipMemcpy(dA, A, (size_t)M * K * 2, hipMemcpyHostToDevice));
   else hipLaunchKernelGGL(debug_fill_kernel, dim3(1024), dim3(256), 0, nullptr, (half_t*)dA, (size_t)M * K, 1u);
@@ -1014,9 +1162,19 @@ extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int
   g.lda = a_t ? M : K; g.ldb = b_t ? N : K;
   g.M = M; g.N = N; g.K = K; g.a_t = a_t != 0; g.b_t = b_t != 0;
   p.C = dC; p.ldc = N;
-  if (epi == EPI_RESID) p.R = (const float*)dC;
-  if (epi == EPI_SWIGLU) p.ldc = N / 2;
-  if (epi == EPI_CE) {
+  if (epi == EPI_RESID || epi == EPI_RESID_NORM) p.R = (const float*)dC;
+  if (epi == EPI_SWIGLU || epi == EPI_SWIGLU_RR) p.ldc = N / 2;
+  if (dN) {
+    float* f = (float*)dN;
+    p.rr_part = f; p.rr_ld = M > N ? M : N; p.rr_nparts = 12; p.rr_dim = 768;
+    f += (size_t)kRrMaxParts * p.rr_ld;
+    p.gain = f;
+    f += N;
+    p.ssq_part = f; p.ssq_ld = M;
+    f += (size_t)kRrMaxParts * M;
+    p.C2 = f; p.ldc2 = N;
+  }
+  if (epi == EPI_CE || epi == EPI_CE_RR) {
     char* x = (char*)dX;
     p.targets = (const uint16_t*)x;
     p.partial = (float2*)(x + (((size_t)N * 2 + 255) & ~(size_t)255));
@@ -1039,6 +1197,7 @@ done:
   if (dC) (void)hipFree(dC);
   if (dX) (void)hipFree(dX);
   if (dW) (void)hipFree(dW);
+  if (dN) (void)hipFree(dN);
   return rc;
 }
 

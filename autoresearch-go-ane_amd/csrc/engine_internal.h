@@ -143,6 +143,14 @@ struct ane_engine {
   ane::half_t* qkv = nullptr;
   ane::half_t* att = nullptr;
   ane::half_t* gate = nullptr;
+  // deferred RMSNorm of the llama2 eval forward (ANE_FUSED_NORM=1; off by
+  // default: measured slower, see forward_body): per-row partial sums of
+  // squares [kRrMaxParts][T] behind xh = fp16(x * gain); fwd_rr_nparts > 0
+  // when the last forward left its final norm to the classifier this way
+  float* ssq_part = nullptr;
+  bool fused_norm = false;
+  bool fused_pf = true;
+  int fwd_rr_nparts = 0;
   int ce_bm = 256, ce_np = 0;  // smallest classifier block row and the partial rows it needs
   float2* partial = nullptr;
   float* tgt_logit = nullptr;
@@ -211,7 +219,7 @@ void prof_end(ane_engine* e, double flops, double bytes);
 hipError_t eng_gemm(ane_engine* e, int cls, const ane::half_t* A, int lda, bool at, const ane::half_t* B, int ldb,
                     bool bt, int M, int N, int K, int epi, const ane::EpiParams& p, int bm = 0, int bn = 0);
 int refresh_shadows(ane_engine* e);
-int forward_body(ane_engine* e, int nseq, int train);
+int forward_body(ane_engine* e, int nseq, int train, bool defer_norm = false);
 void drop_fwd_graph(ane_engine* e);
 template <class T>
 hipError_t dalloc(ane_engine* e, T** p, size_t n) {

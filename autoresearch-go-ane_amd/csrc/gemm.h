@@ -31,7 +31,28 @@ enum Epi : int {
   EPI_SWIGLU_BWD = 10, // acc = dgate [T, H]; C2 (fp16) = h1|h3 interleaved -> C (fp16) = dh1|dh3 interleaved
   EPI_RELU2_BWD = 11,  // acc = dgate [T, H]; C2 (fp16) = h1 -> C (fp16) = dgate * 2 * max(h1, 0)
   EPI_STORE_RS = 12,   // C (fp32) = acc * rowscale[row]
+  // Deferred RMSNorm (llama2 eval forward): the residual GEMM leaves its
+  // consumers fp16(x * gain) and per-row partial sums of x^2; the consumer
+  // GEMMs scale their (linear) outputs by rr = 1 / rms(x) per token.
+  EPI_RESID_NORM = 13, // C (fp32) = R + acc; C2 (fp16, ld ldc2) = C * gain[col];
+                       // ssq_part[(n0 / BN) * ssq_ld + row] = sum over the block's BN columns of C^2
+  EPI_STORE_H_RR = 14, // EPI_STORE_H of acc * rr[row]
+  EPI_SWIGLU_RR = 15,  // EPI_SWIGLU of acc * rr[row]
+  EPI_CE_RR = 16,      // EPI_CE of acc * rr[col] (columns = tokens)
 };
+// Partial sums of squares a consumer combines (rr_nparts <= kRrMaxParts).
+constexpr int kRrMaxParts = 16;
+__host__ __device__ constexpr bool epi_rr(int epi) {
+  return epi == EPI_STORE_H_RR || epi == EPI_SWIGLU_RR || epi == EPI_CE_RR;
+}
+// The epilogue an rr variant shares with its plain form.
+__host__ __device__ constexpr int epi_base(int epi) {
+  return epi == EPI_STORE_H_RR ? EPI_STORE_H
+         : epi == EPI_SWIGLU_RR ? EPI_SWIGLU
+         : epi == EPI_CE_RR     ? EPI_CE
+         : epi == EPI_RESID_NORM ? EPI_RESID
+                                 : epi;
+}
 
 struct GemmArgs {
   const half_t* A;
@@ -75,6 +96,12 @@ struct EpiParams {
   int vocab = 0;                      // rows >= vocab are padding (ignored)
   float* C3 = nullptr;                // second fp32 output (EPI_STORE_W13: W3 grad)
   const float* rowscale = nullptr;    // [M] (EPI_STORE_RS)
+  // deferred RMSNorm
+  const float* gain = nullptr;        // [N] (EPI_RESID_NORM)
+  float* ssq_part = nullptr;          // [N / BN][ssq_ld] out (EPI_RESID_NORM)
+  int ssq_ld = 0;
+  const float* rr_part = nullptr;     // [rr_nparts][rr_ld] in (rr variants): rr = 1 / sqrt(sum / rr_dim + 1e-5)
+  int rr_ld = 0, rr_nparts = 0, rr_dim = 0;
 };
 
 // Launches one GEMM on `stream`.  bm/bn force a block tile (0 = heuristic);

@@ -173,22 +173,44 @@ __device__ __forceinline__ void block_tile(int nbm, int nbn, int bid, int& bm, i
 // The wave owns rows m0 + wm*WTM + [0, WTM) and columns n0 + wn*WTN + [0, WTN)
 // of C; bm is the block's row-tile index (classifier partials); lds is
 // free scratch once the main loop is done (classifier reduction).
+// rr_s (rr variants): LDS, 1 / rms of the block's rows (EPI_CE_RR: columns),
+// indexed from m0 (n0).
 template <int BN, int WTM, int WTN, int TM, int TN, int EPI>
 __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs& g, const EpiParams& e, int m0,
-                                         int n0, int bm, int wm, int wn, int lane, half_t* lds) {
+                                         int n0, int bm, int wm, int wn, int lane, half_t* lds,
+                                         const float* rr_s = nullptr) {
   const int rbase = m0 + wm * WTM + 4 * (lane >> 5);
   const int cbase = n0 + wn * WTN + (lane & 31);
 #define ROW(i, r) (rbase + (i) * 32 + 8 * ((r) >> 2) + ((r) & 3))
 #define COL(j) (cbase + (j) * 32)
+#define LROW(i, r) (wm * WTM + 4 * (lane >> 5) + (i) * 32 + 8 * ((r) >> 2) + ((r) & 3))
 
-  if constexpr (EPI == EPI_STORE_H) {
+  // rr of this lane's 16 rows of row tile i (rows 8 q + 4 (lane / 32) + 0..3
+  // are consecutive: four 16-byte LDS reads, all issued before any use)
+  auto rr_rows = [&](int i, float (&v)[16]) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float4 f = *reinterpret_cast<const float4*>(rr_s + LROW(i, 4 * q));
+      v[4 * q] = f.x; v[4 * q + 1] = f.y; v[4 * q + 2] = f.z; v[4 * q + 3] = f.w;
+    }
+  };
+  if constexpr (EPI == EPI_STORE_H || EPI == EPI_STORE_H_RR) {
     half_t* C = (half_t*)e.C;
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+    for (int i = 0; i < TM; i++) {
+      float sc[16];
+#pragma unroll
+      for (int r = 0; r < 16; r++) sc[r] = e.scale;
+      if constexpr (EPI == EPI_STORE_H_RR) {
+        rr_rows(i, sc);
+#pragma unroll
+        for (int r = 0; r < 16; r++) sc[r] *= e.scale;
+      }
 #pragma unroll
       for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) C[(size_t)ROW(i, r) * e.ldc + COL(j)] = (half_t)(acc[i][j][r] * e.scale);
+        for (int r = 0; r < 16; r++) C[(size_t)ROW(i, r) * e.ldc + COL(j)] = (half_t)(acc[i][j][r] * sc[r]);
+    }
   } else if constexpr (EPI == EPI_STORE_F) {
     // Loads of a tile's 16 old values are issued before any of its stores:
     // C may alias nothing else, but the compiler cannot know that, and a
@@ -272,12 +294,14 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
           if (C2) C2[idx] = v;
         }
       }
-  } else if constexpr (EPI == EPI_SWIGLU) {
+  } else if constexpr (EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_RR) {
     static_assert(TN % 2 == 0, "SwiGLU epilogue pairs 32-column tiles");
     half_t* C = (half_t*)e.C;
     half_t* C2 = (half_t*)e.C2;
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+    for (int i = 0; i < TM; i++) {
+      float rrv[16];
+      if constexpr (EPI == EPI_SWIGLU_RR) rr_rows(i, rrv);
 #pragma unroll
       for (int j = 0; j < TN; j += 2) {
         const int b = (COL(j) - (lane & 31)) >> 5;  // even 32-column block of W1
@@ -285,6 +309,10 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           float h1 = acc[i][j][r], h3 = acc[i][j + 1][r];
+          if constexpr (EPI == EPI_SWIGLU_RR) {
+            h1 *= rrv[r];
+            h3 *= rrv[r];
+          }
           float sg = sigmoid_f(h1);
           size_t row = (size_t)ROW(i, r);
           C[row * e.ldc + hcol] = (half_t)(h1 * sg * h3);
@@ -294,6 +322,7 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
           }
         }
       }
+    }
   } else if constexpr (EPI == EPI_RELU2) {
     half_t* C = (half_t*)e.C;
     half_t* C2 = (half_t*)e.C2;
@@ -378,7 +407,50 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
           if (C2) C2[idx] = ga;
         }
       }
-  } else if constexpr (EPI == EPI_CE) {
+  } else if constexpr (EPI == EPI_RESID_NORM) {
+    // llama2 residual (alpha 1, no x0) + the deferred norm's inputs: this
+    // block's per-row sum of squares over its BN columns goes through LDS
+    // (lane partials, then the WN waves of a row range) in a fixed order.
+    float* C = (float*)e.C;
+    half_t* C2 = (half_t*)e.C2;
+    constexpr int WN = BN / WTN;
+    constexpr int RS = WN * 32 + 1;  // padded LDS row of the lane partials
+    float rs[TM][16];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) rs[i][r] = 0.f;
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const float gc = e.gain[COL(j)];
+#pragma unroll
+      for (int i = 0; i < TM; i++) {
+        const size_t base = (size_t)(rbase + i * 32) * e.ldc + COL(j);
+        float rv[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) rv[r] = e.R[base + (size_t)(8 * (r >> 2) + (r & 3)) * e.ldc];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float v = rv[r] + acc[i][j][r];
+          C[base + (size_t)(8 * (r >> 2) + (r & 3)) * e.ldc] = v;
+          C2[(size_t)ROW(i, r) * e.ldc2 + COL(j)] = (half_t)(v * gc);
+          rs[i][r] += v * v;
+        }
+      }
+    }
+    __syncthreads();  // every wave is past its last read of the LDS stages
+    float* red = reinterpret_cast<float*>(lds);  // [2 WTM][RS]
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) red[LROW(i, r) * RS + wn * 32 + (lane & 31)] = rs[i][r];
+    __syncthreads();
+    for (int row = threadIdx.x; row < 2 * WTM; row += blockDim.x) {
+      float sum = 0.f;
+      for (int c = 0; c < WN * 32; c++) sum += red[row * RS + c];
+      e.ssq_part[(size_t)(n0 / BN) * e.ssq_ld + m0 + row] = sum;
+    }
+  } else if constexpr (EPI == EPI_CE || EPI == EPI_CE_RR) {
     // rows = vocab ids (M == vocab), columns = tokens.  Each wave reduces
     // its BM/2 rows of every column to (max, sum exp(v - max)); lanes l and
     // l^32 hold the two row halves of one column; the two waves sharing a
@@ -392,12 +464,14 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
       // compare against a constant per register
       const int tsel = e.targets[n] - ROW(0, 0);
       const bool hit = tsel >= 0 && tsel < 32 * TM && (tsel & 4) == 0;
+      const float rr_col = EPI == EPI_CE_RR ? rr_s[nl] : 1.f;
       float mx = -INFINITY, tv = 0.f;
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           float v = acc[i][j][r];
+          if constexpr (EPI == EPI_CE_RR) v *= rr_col;
           if (e.softcap) v = softcap_f(v, e.cap);
           acc[i][j][r] = v;
           mx = fmaxf(mx, v);
@@ -473,6 +547,7 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
   }
 #undef ROW
 #undef COL
+#undef LROW
 }
 
 // NW = 4: waves 2 x 2, one wave per SIMD.  NW = 8: waves 2 x 4, two waves
@@ -650,6 +725,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
   constexpr int NMF = TM * TN, NRD = TM + TN;             // per substep
   constexpr int NV = 8 / NW;
   static_assert(TM >= 1 && TN >= 1 && LA >= 1 && LB >= 1, "tile too small for the wave grid");
+  static_assert(!epi_rr(EPI) || (kRrMaxParts + 1) * (EPI == EPI_CE_RR ? BN : BM) * 4 <= 4 * STAGE,
+                "rr staging exceeds the LDS stages");
+  static_assert(EPI != EPI_RESID_NORM || BM * (WN * 32 + 1) * 4 <= 4 * STAGE, "row sums exceed the LDS stages");
   __shared__ __attribute__((aligned(16))) half_t lds[2 * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -694,6 +772,22 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
     dma16_s(bbase + (size_t)(gi * 8) * g.ldb + kt * BK, vob[q % NV],
             lds0 + 2u * (unsigned)(st * STAGE + BM * BK + gi * 8 * BK));
   };
+
+  // rr variants: the partial sums of squares of the block's rows (EPI_CE_RR:
+  // token columns) are loaded into registers before the prologue (the
+  // prologue's wait covers them) and combined in LDS after the main loop.
+  constexpr bool RR = epi_rr(EPI);
+  constexpr int NRR = EPI == EPI_CE_RR ? BN : BM;
+  constexpr int RPER = RR ? (NRR * kRrMaxParts + 64 * NW - 1) / (64 * NW) : 1;
+  float rrv[RPER];
+  if constexpr (RR) {
+    const int r0 = EPI == EPI_CE_RR ? n0 : m0;
+#pragma unroll
+    for (int k = 0; k < RPER; k++) {
+      const int idx = tid + k * 64 * NW, p = idx / NRR;
+      rrv[k] = p < e.rr_nparts ? e.rr_part[(size_t)p * e.rr_ld + r0 + idx % NRR] : 0.f;
+    }
+  }
 
   floatx16 acc[TM][TN];
 #pragma unroll
@@ -779,7 +873,28 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
     substep(F{}, I1{}, fa[1], fb[1], fa[0], fb[0], nxt, 0, kt + 2 < nk, kt + 2, kt & 1);
   }
   // the epilogue of the CE variant reuses LDS as scratch
-  if constexpr (EPI == EPI_CE) __syncthreads();
+  if constexpr (EPI == EPI_CE || EPI == EPI_CE_RR) __syncthreads();
+  const float* rr_s = nullptr;
+  if constexpr (RR) {
+    // LDS: partials [kRrMaxParts][NRR], then rr [NRR]; rr = 1 / rms over
+    // rr_dim columns, the parts added in order
+    if constexpr (EPI != EPI_CE_RR) __syncthreads();
+    float* pl = reinterpret_cast<float*>(lds);
+    float* rs = pl + kRrMaxParts * NRR;
+#pragma unroll
+    for (int k = 0; k < RPER; k++) {
+      const int idx = tid + k * 64 * NW;
+      if (idx < kRrMaxParts * NRR) pl[idx] = rrv[k];
+    }
+    __syncthreads();
+    for (int row = tid; row < NRR; row += 64 * NW) {
+      float sum = 0.f;
+      for (int p = 0; p < e.rr_nparts; p++) sum += pl[p * NRR + row];
+      rs[row] = 1.0f / sqrtf(sum / (float)e.rr_dim + 1e-5f);
+    }
+    __syncthreads();
+    rr_s = rs;
+  }
   if constexpr (EPI == EPI_STORE_F) {
     if (g.splits > 1) {  // this split's slice of the workspace (C = ws, ldc = N)
       EpiParams es = e;
@@ -788,7 +903,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
       return;
     }
   }
-  epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, e, m0, n0, bm, wm, wn, lane, lds);
+  epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, e, m0, n0, bm, wm, wn, lane, lds, rr_s);
 }
 
 // Sum of the split-K workspace slices in split order, then the epilogue:
@@ -848,14 +963,20 @@ hipError_t launch_tile(const GemmArgs& g, const EpiParams& e, hipStream_t s) {
 template <bool AT, bool BT, int EPI>
 hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, int bn, int nw, int ns) {
   const int key = bm * 1000 + bn;
-  if constexpr (!AT && !BT) {
+  // the deferred-norm epilogues exist for the hand-ordered K-major kernel only
+  constexpr bool HO_ONLY = epi_rr(EPI) || EPI == EPI_RESID_NORM;
+  if constexpr (!AT && !BT && EPI != EPI_RESID_NORM) {
     if (nw == 8 && ns == 2) {  // caller checked the tile
       const dim3 grid((g.M / 256) * (g.N / 256) * g.splits);
       LAUNCH_HO(256, 256, 8);
       return hipGetLastError();
     }
   }
-  if (nw == 8) return launch_tile<AT, BT, EPI, 256, 256, 8>(g, e, s);  // caller checked the tile
+  if constexpr (HO_ONLY) {
+    if (nw == 8 || ns != 2) return hipErrorInvalidValue;
+  } else {
+    if (nw == 8) return launch_tile<AT, BT, EPI, 256, 256, 8>(g, e, s);  // caller checked the tile
+  }
   if constexpr (!AT && !BT) {
     if (ns == 2) {  // hand-ordered kernel for every K-major tile
       const dim3 grid((g.M / bm) * (g.N / bn) * g.splits);
@@ -866,7 +987,7 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
         case 128128: LAUNCH_HO(128, 128, 4); break;
         case 64128: LAUNCH_HO(64, 128, 4); break;
         default:
-          if constexpr (EPI != EPI_SWIGLU) {
+          if constexpr (EPI != EPI_SWIGLU && EPI != EPI_SWIGLU_RR) {
             switch (key) {
               case 128064: LAUNCH_HO(128, 64, 4); break;
               case 256064: LAUNCH_HO(256, 64, 4); break;
@@ -874,14 +995,16 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
               // 192-wide tiles (three 32-column MFMA tiles per wave): N = 768
               // and 2304 split into whole waves of blocks
               case 128192:
-                if constexpr (EPI == EPI_STORE_H || EPI == EPI_STORE_F || EPI == EPI_RESID) {
+                if constexpr (EPI == EPI_STORE_H || EPI == EPI_STORE_F || EPI == EPI_RESID || EPI == EPI_STORE_H_RR ||
+                              EPI == EPI_RESID_NORM) {
                   LAUNCH_HO(128, 192, 4);
                   break;
                 } else {
                   return hipErrorInvalidValue;
                 }
               case 256192:
-                if constexpr (EPI == EPI_STORE_H || EPI == EPI_STORE_F || EPI == EPI_RESID) {
+                if constexpr (EPI == EPI_STORE_H || EPI == EPI_STORE_F || EPI == EPI_RESID || EPI == EPI_STORE_H_RR ||
+                              EPI == EPI_RESID_NORM) {
                   LAUNCH_HO(256, 192, 4);
                   break;
                 } else {
@@ -895,6 +1018,7 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
       }
       return hipGetLastError();
     }
+    if constexpr (!HO_ONLY) {
     if (ns == 3) {  // caller checked the tile
       switch (key) {
         case 256128: return launch_tile<AT, BT, EPI, 256, 128, 4, 3>(g, e, s);
@@ -911,7 +1035,11 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
       }
       return hipErrorInvalidValue;
     }
+    }
   }
+  if constexpr (HO_ONLY) {
+    return hipErrorInvalidValue;
+  } else {
   switch (key) {
     case 256256: return launch_tile<AT, BT, EPI, 256, 256>(g, e, s);
     case 256128: return launch_tile<AT, BT, EPI, 256, 128>(g, e, s);
@@ -929,6 +1057,7 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
     }
   }
   return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
@@ -953,6 +1082,7 @@ void gemm_pick_tile(int M, int N, int K, int epi, int* pbm, int* pbn) {
   // Wq|Wk|Wv output, 2304 = 12 x 192): 128x192 blocks split N into whole
   // waves; measured 33.6 us vs 38.5 for 128x128 at M = 8192, 19.9 vs 21.3
   // for 128x64 at 4096
+  epi = epi_base(epi);  // the deferred-norm variants tile as their plain forms
   if ((epi == EPI_STORE_H || epi == EPI_STORE_F || epi == EPI_RESID) && N % 192 == 0 && N >= 1536 && N % 1024 != 0 &&
       M % 128 == 0 && (long)(M / 128) * (N / 192) >= 384 && (!want_bm || want_bm == 128) &&
       (!want_bn || want_bn == 192)) {
@@ -1054,6 +1184,12 @@ static hipError_t splitk_reduce(const GemmArgs& g, const EpiParams& e, hipStream
 hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t s, int bm, int bn, int nw,
                     int ns) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0 || g.splits < 1) return hipErrorInvalidValue;
+  if (epi == EPI_RESID_NORM &&
+      (!e.R || !e.C2 || !e.gain || !e.ssq_part || e.ssq_ld < g.M || g.splits != 1 || g.grp || g.a_t || g.b_t))
+    return hipErrorInvalidValue;
+  if (epi_rr(epi) && (!e.rr_part || e.rr_nparts < 1 || e.rr_nparts > kRrMaxParts || e.rr_dim <= 0 ||
+                      e.rr_ld < (epi == EPI_CE_RR ? g.N : g.M) || g.splits != 1 || g.grp || g.a_t || g.b_t))
+    return hipErrorInvalidValue;
   if (g.splits > 1) {
     if (g.a_t || g.b_t || g.grp || !g.ws || (g.K % (g.splits * BK)) != 0 || (ns != 0 && ns != 2) ||
         (epi != EPI_STORE_F && epi != EPI_STORE_H && epi != EPI_STORE_W13) || (g.N % 4) != 0)
@@ -1098,6 +1234,10 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
   CASE(0, false, false, EPI_CE)
   CASE(0, false, false, EPI_DLOGITS)
   CASE(0, false, false, EPI_STORE_RS)
+  CASE(0, false, false, EPI_RESID_NORM)
+  CASE(0, false, false, EPI_STORE_H_RR)
+  CASE(0, false, false, EPI_SWIGLU_RR)
+  CASE(0, false, false, EPI_CE_RR)
   // backward with transposed weight shadows / operands (all K-major)
   CASE(0, false, false, EPI_SWIGLU_BWD)
   CASE(0, false, false, EPI_RELU2_BWD)

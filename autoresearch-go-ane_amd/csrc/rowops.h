@@ -8,6 +8,14 @@ namespace ane {
 // x[t, :] = embed[tok_t, :] (zero row for tok_t >= vocab)      ane/stories/cpu.go:41-72
 hipError_t embed_lookup(float* x, const float* embed, const uint16_t* tok, int T, int D, int V,
                         hipStream_t s);
+// Streams [p, p + bytes) through the cache hierarchy (prefetch_slice over up
+// to 1024 blocks): the weights of the GEMM that runs next.
+hipError_t prefetch_weights(const void* p, size_t bytes, hipStream_t s);
+// x = embed[tok] (0 for tok >= V), xg = fp16(x * gain) and ssq[t] = sum of
+// x[t]^2: the inputs of a GEMM that applies the RMSNorm after its product
+// (EPI_*_RR with one partial per row); pf: weights streamed alongside.
+hipError_t embed_xg(float* x, half_t* xg, float* ssq, const float* embed, const uint16_t* tok, const float* gain,
+                    int T, int D, int V, hipStream_t s, const void* pf = nullptr, size_t pf_bytes = 0);
 
 // nanochat entry: xpre = embed[tok]; x0 = xpre / rms(xpre) (fp32 scale);
 // xh = fp16(x0)                      ane/train_full.go:386-390, ane/common.go:157-174

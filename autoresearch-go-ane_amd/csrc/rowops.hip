@@ -1,6 +1,8 @@
 // Row-wise and elementwise kernels (HBM-bound).  One wave per token row:
 // lanes stride the channel dimension, so every load and store is
 // coalesced across the wave.
+#include <algorithm>
+
 #include "rowops.h"
 
 namespace ane {
@@ -17,6 +19,33 @@ __global__ __launch_bounds__(256) void embed_kernel(float* x, const float* E, co
   float* xr = x + (size_t)t * D;
   const float* er = E + (size_t)tk * D;
   for (int i = lane; i < D; i += 64) xr[i] = tk < V ? er[i] : 0.f;
+}
+
+__global__ __launch_bounds__(256) void prefetch_kernel(const void* pf, size_t pf_bytes) {
+  prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
+}
+
+// x = E[tok] (0 for tok >= V), xg = fp16(x * gain), ssq[t] = sum of x^2 (the
+// deferred norm's one partial per row); the next GEMM's weights streamed
+// through the caches alongside.
+__global__ __launch_bounds__(256) void embed_xg_kernel(float* x, half_t* xg, float* ssq, const float* E,
+                                                       const uint16_t* tok, const float* gain, int T, int D, int V,
+                                                       const void* pf, size_t pf_bytes) {
+  prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
+  const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const int tk = tok[t];
+  const float* er = E + (size_t)tk * D;
+  float ss = 0.f;
+  for (int i = lane; i < D; i += 64) {
+    const float v = tk < V ? er[i] : 0.f;
+    const size_t idx = (size_t)t * D + i;
+    x[idx] = v;
+    xg[idx] = (half_t)(v * gain[i]);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) ssq[t] = ss;
 }
 
 __global__ __launch_bounds__(256) void embed_norm_kernel(float* xpre, float* x0, half_t* xh, const float* E,
@@ -209,6 +238,21 @@ inline int flat_grid(size_t n) {
 
 hipError_t embed_lookup(float* x, const float* E, const uint16_t* tok, int T, int D, int V, hipStream_t s) {
   hipLaunchKernelGGL(embed_kernel, dim3(rows_grid(T)), dim3(256), 0, s, x, E, tok, T, D, V);
+  return hipGetLastError();
+}
+
+hipError_t prefetch_weights(const void* p, size_t bytes, hipStream_t s) {
+  if (!p || bytes < 16) return hipSuccess;
+  const size_t n16 = bytes / 16;
+  const unsigned blocks = (unsigned)std::min<size_t>(1024, (n16 + 255) / 256);
+  hipLaunchKernelGGL(prefetch_kernel, dim3(blocks), dim3(256), 0, s, p, bytes);
+  return hipGetLastError();
+}
+
+hipError_t embed_xg(float* x, half_t* xg, float* ssq, const float* E, const uint16_t* tok, const float* gain, int T,
+                    int D, int V, hipStream_t s, const void* pf, size_t pf_bytes) {
+  hipLaunchKernelGGL(embed_xg_kernel, dim3(rows_grid(T)), dim3(256), 0, s, x, xg, ssq, E, tok, gain, T, D, V, pf,
+                     pf_bytes);
   return hipGetLastError();
 }
 

@@ -260,6 +260,16 @@ int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_
  * operands may be NULL. */
 int ane_debug_gemm_epi(int epi, int M, int N, int K, const uint16_t *A, const uint16_t *B, void *C, void *C2,
                        const float *X0, const float *R, float alpha, float beta, int seq, int bm, int bn, int nw);
+/* The deferred-RMSNorm epilogues of the llama2 eval forward on one forced
+ * tile (bm x bn, nw waves): epi 13: X [M, N] fp32 in/out (X += A B^T),
+ * C [M, N] fp16 = X * gain[col], ssq [N/bn][M] = per-row sums of X^2 over
+ * each block's bn columns; epi 14: C [M, N] fp16 = (A B^T) * rr[row]; epi 15:
+ * C [M, N/2] fp16 = SwiGLU over 32-column interleaved W1|W3 of (A B^T) *
+ * rr[row]; rr = 1 / sqrt(sum_{p < nparts} rr_part[p][row] / rr_dim + 1e-5)
+ * (the RMSNorm of ane/stories/cpu.go applied after the projection). */
+int ane_debug_gemm_norm(int epi, int M, int N, int K, const uint16_t *A, const uint16_t *B, float *X, uint16_t *C,
+                        const float *gain, float *ssq, const float *rr_part, int nparts, int rr_dim, int bm, int bn,
+                        int nw);
 int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float scale, int hilo,
                         const uint16_t *qkv, uint16_t *out, float *lse);
 /* Two fp16 transposes in one launch of the training step's transpose kernel:
@@ -283,7 +293,8 @@ int ane_debug_classifier(int M, int N, int K, const uint16_t *A, const uint16_t 
 /* Mean time of `iters` launches of one GEMM on device-resident operands
  * (arguments as ane_debug_gemm; A / B NULL: pseudo-random in [-0.5, 0.5)).
  * epi: 0 fp16 store, 1 fp32 store, 3 in-place residual add, 4 SwiGLU over
- * interleaved W1|W3 columns, 7 classifier cross-entropy partials. */
+ * interleaved W1|W3 columns, 7 classifier cross-entropy partials, 13-16 the
+ * deferred-RMSNorm forms (zero partials and gains, 12 partials per row). */
 int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int K, int bm, int bn, int nw, int ns,
                          int splits, int iters, const uint16_t *A, const uint16_t *B, float *avg_ms);
 const char *ane_debug_last_error(void);
