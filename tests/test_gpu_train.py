@@ -76,8 +76,39 @@ def test_full_size_grads_match_oracle(arch, mode):
     # 10% apart, while every weight matrix stays within 0.5% of the other
     # build; the oracle's own value moves 1.2% when the parameters are merely
     # rounded to fp16.  Its bound is set by that conditioning, not by the
-    # weight-gradient contract.
+    # weight-gradient contract; the finite-difference test below pins it.
     check_grads(cfg, g, g_ref, overrides={"smear_lambda": 0.25})
+
+
+def test_full_size_smear_lambda_gradient_by_finite_difference():
+    """smear_lambda's full-size gradient nearly cancels (see above), so it is
+    pinned against the device's own loss instead: central differences of
+    EvalLoss over smear_lambda +- eps at eps = 1/8 and 1/16, extrapolated
+    (Richardson: the eps^2 term cancels; the loss is strongly curved in
+    lambda, so a single difference at a larger eps is biased), against
+    Grads in the exact gradient mode, one sequence (the same per-token mean
+    loss in both)."""
+    cfg = ane.stories110m("nanochat", grad_mode="true")
+    p = ane.init_params(cfg, seed=0)
+    tok, tgt = ane.make_tokens(cfg, 1, seed=3)
+    off = {name: o for name, o, _ in ane.param_layout(cfg)}["smear_lambda"]
+    eng = open_engine(cfg, p, max_batch=1)
+    try:
+        _, g = eng.Grads(tok, tgt)
+        fd = {}
+        for eps in (0.125, 0.0625):
+            lp = []
+            for sgn in (1.0, -1.0):
+                q = p.copy()
+                q[off] += np.float32(sgn * eps)
+                eng.SetParams(q)
+                lp.append(float(eng.EvalLoss(tok, tgt)[0]))
+            fd[eps] = (lp[0] - lp[1]) / (2 * eps)
+    finally:
+        eng.Destroy()
+    rich = (4.0 * fd[0.0625] - fd[0.125]) / 3.0
+    print(f"smear_lambda grad: device {g[off]:.6e}, central differences {fd}, extrapolated {rich:.6e}")
+    assert abs(g[off] - rich) <= 0.05 * abs(rich)
 
 
 @pytest.mark.parametrize("arch", ["llama2", "nanochat"])
