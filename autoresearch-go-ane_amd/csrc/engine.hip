@@ -186,7 +186,8 @@ hipError_t eng_gemm(ane_engine* e, int cls, const half_t* A, int lda, bool at, c
   GemmArgs g;
   g.A = A; g.B = B; g.lda = lda; g.ldb = ldb; g.M = M; g.N = N; g.K = K; g.a_t = at; g.b_t = bt;
   // training: GEMMs whose output is too small to fill the chip split K
-  if (!at && !bt && e->tr.splitk_ws && bm == 0 && bn == 0) {
+  // (K-major operands, or M-major ones as the weight gradients read them)
+  if (!(at && !bt) && e->tr.splitk_ws && bm == 0 && bn == 0) {
     int sp = 1;
     gemm_pick_split(M, N, K, epi, e->tr.splitk_cap, &bm, &bn, &sp);
     if (sp > 1) {
@@ -379,6 +380,7 @@ extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_e
   // GEMMs around it instead of launching it
   if (const char* g = getenv("ANE_FUSED_NORM")) e->fused_norm = atoi(g) != 0;
   if (const char* g = getenv("ANE_FUSED_PF")) e->fused_pf = atoi(g) != 0;
+  if (const char* g = getenv("ANE_TR_DW")) e->tr_dw = atoi(g) != 0;
   if (const char* g = getenv("ANE_PHASE_EVERY")) e->ph_period = atoi(g) > 0 ? atoi(g) : 1;
   e->lr = e->opt.lr;
   int rc = validate_cfg(e, e->cfg);

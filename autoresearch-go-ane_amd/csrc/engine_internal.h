@@ -150,6 +150,7 @@ struct ane_engine {
   float* ssq_part = nullptr;
   bool fused_norm = false;
   bool fused_pf = true;
+  bool tr_dw = true;  // weight gradients read token-major operands directly (ANE_TR_DW=0: transposes)
   int fwd_rr_nparts = 0;
   int ce_bm = 256, ce_np = 0;  // smallest classifier block row and the partial rows it needs
   float2* partial = nullptr;

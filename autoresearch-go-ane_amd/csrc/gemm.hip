@@ -716,7 +716,38 @@ __device__ __forceinline__ void dma16_s(const half_t* sbase, unsigned voff, unsi
 #pragma clang diagnostic pop
 }
 
-template <int BM, int BN, int EPI, int NW>
+// ds_read_b64_tr_b16 (gfx950): lane 16 g + j receives element j % 4 of the 4
+// halves that lane 16 g + 4 e + j / 4 addresses, as its element e.  Two
+// such reads give an MFMA operand from a tile stored with the MFMA row
+// index contiguous ("M-major", [k][m]): see tr_frag.
+typedef short short4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ short4v ds_read_tr16(const half_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(lds_ptr_t)p);
+}
+// Chunk swizzle of an M-major LDS tile (rows of CPR 16-byte chunks): the
+// four 16-byte chunks a transposed read takes from one row move with the row
+// (rows r and r + 4 share a position: a two-way bank conflict at most).
+template <int CPR>
+__device__ __forceinline__ int swt(int row) {
+  return CPR >= 16 ? 4 * (row & 3) : 4 * (row & 1);
+}
+// The 32 x 16 operand (rows r0 + lane % 32, k = 16 s + 8 (lane / 32) + [0, 8))
+// of an M-major tile [64 k][W] (W halves per row, swizzled by swt):
+// lane 16 g + 4 e + q points at k-row 16 s + 8 (g / 2) + e (+ 4 for the
+// second read), halves r0 + 16 (g % 2) + 4 q .. + 3.
+template <int W>
+__device__ __forceinline__ half8 tr_frag(const half_t* tile, int r0, int s, int lane) {
+  constexpr int CPR = W / 8;
+  const int g = lane >> 4, e = (lane >> 2) & 3, q = lane & 3;
+  const int col = r0 + 16 * (g & 1) + 4 * q;
+  const int row0 = 16 * s + 8 * (g >> 1) + e, row1 = row0 + 4;
+  const short4v lo = ds_read_tr16(tile + row0 * W + (((col >> 3) ^ swt<CPR>(row0)) << 3) + (col & 7));
+  const short4v hi = ds_read_tr16(tile + row1 * W + (((col >> 3) ^ swt<CPR>(row1)) << 3) + (col & 7));
+  const short4v lohi[2] = {lo, hi};
+  return __builtin_bit_cast(half8, lohi);
+}
+
+template <int BM, int BN, int EPI, int NW, bool TRA = false, bool TRB = false>
 __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams e) {
   constexpr int WN = NW / 2;
   constexpr int WTM = BM / 2, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
@@ -761,16 +792,36 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
     voa[v] = (unsigned)(((lane >> 3) * g.lda + lc * 8) * 2);
     vob[v] = (unsigned)(((lane >> 3) * g.ldb + lc * 8) * 2);
   }
-  const half_t* abase = g.A + (size_t)m0 * g.lda + koff;
-  const half_t* bbase = Bp + (size_t)n0 * g.ldb + koff;
+  // M-major operands (TRA / TRB: stored [K][M], the tile kept [64 k][BM] in
+  // LDS): one load instruction fills 1 KB = RPI whole k-rows; lane l lands
+  // at row l / CPR, physical chunk l % CPR, so it fetches the logical chunk
+  // swt maps there.  Row gi * RPI + r has the swizzle of r (RPI >= 4), or of
+  // r and the parity of gi, which is the wave's (RPI == 2: gi = wave + NW q).
+  auto tr_voff = [&](int W, int ld) {
+    const int cpr = W / 8, r = lane / cpr, row = (512 / W) * wave + r;
+    const int c = (lane % cpr) ^ (cpr >= 16 ? 4 * (row & 3) : 4 * (row & 1));
+    return (unsigned)((r * ld + c * 8) * 2);
+  };
+  if constexpr (TRA) voa[0] = tr_voff(BM, g.lda);
+  if constexpr (TRB) vob[0] = tr_voff(BN, g.ldb);
+  const half_t* abase = TRA ? g.A + koff * g.lda + m0 : g.A + (size_t)m0 * g.lda + koff;
+  const half_t* bbase = TRB ? Bp + koff * g.ldb + n0 : Bp + (size_t)n0 * g.ldb + koff;
   auto dma_a = [&](int q, int kt, int st) {
     const int gi = wave_s + NW * q;
-    dma16_s(abase + (size_t)(gi * 8) * g.lda + kt * BK, voa[q % NV], lds0 + 2u * (unsigned)(st * STAGE + gi * 8 * BK));
+    if constexpr (TRA)
+      dma16_s(abase + (size_t)(kt * BK + gi * (512 / BM)) * g.lda, voa[0], lds0 + 2u * (unsigned)(st * STAGE + gi * 512));
+    else
+      dma16_s(abase + (size_t)(gi * 8) * g.lda + kt * BK, voa[q % NV],
+              lds0 + 2u * (unsigned)(st * STAGE + gi * 8 * BK));
   };
   auto dma_b = [&](int q, int kt, int st) {
     const int gi = wave_s + NW * q;
-    dma16_s(bbase + (size_t)(gi * 8) * g.ldb + kt * BK, vob[q % NV],
-            lds0 + 2u * (unsigned)(st * STAGE + BM * BK + gi * 8 * BK));
+    if constexpr (TRB)
+      dma16_s(bbase + (size_t)(kt * BK + gi * (512 / BN)) * g.ldb, vob[0],
+              lds0 + 2u * (unsigned)(st * STAGE + BM * BK + gi * 512));
+    else
+      dma16_s(bbase + (size_t)(gi * 8) * g.ldb + kt * BK, vob[q % NV],
+              lds0 + 2u * (unsigned)(st * STAGE + BM * BK + gi * 8 * BK));
   };
 
   // rr variants: the partial sums of squares of the block's rows (EPI_CE_RR:
@@ -804,11 +855,19 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
     const int ch = 2 * s + fch;
     if (q == 0 || q > TN) {
       const int i = q == 0 ? 0 : q - TN;
-      const int row = wm * WTM + i * 32 + frow;
-      a[i] = ld_h8(st + row * BK + swz(row, ch) * 8);
+      if constexpr (TRA) {
+        a[i] = tr_frag<BM>(st, wm * WTM + i * 32, s, lane);
+      } else {
+        const int row = wm * WTM + i * 32 + frow;
+        a[i] = ld_h8(st + row * BK + swz(row, ch) * 8);
+      }
     } else {
-      const int row = wn * WTN + (q - 1) * 32 + frow;
-      b[q - 1] = ld_h8(st + BM * BK + row * BK + swz(row, ch) * 8);
+      if constexpr (TRB) {
+        b[q - 1] = tr_frag<BN>(st + BM * BK, wn * WTN + (q - 1) * 32, s, lane);
+      } else {
+        const int row = wn * WTN + (q - 1) * 32 + frow;
+        b[q - 1] = ld_h8(st + BM * BK + row * BK + swz(row, ch) * 8);
+      }
     }
   };
   // one substep: MFMA p of the TM x TN grid is followed by the reads r with
@@ -959,10 +1018,35 @@ hipError_t launch_tile(const GemmArgs& g, const EpiParams& e, hipStream_t s) {
 
 #define LAUNCH_HO(BM_, BN_, NW_) \
   hipLaunchKernelGGL((gemm_ho_kernel<BM_, BN_, EPI, NW_>), grid, dim3(64 * NW_), 0, s, g, e)
+#define LAUNCH_HOT(BM_, BN_, NW_) \
+  hipLaunchKernelGGL((gemm_ho_kernel<BM_, BN_, EPI, NW_, AT, BT>), grid, dim3(64 * NW_), 0, s, g, e)
 
 template <bool AT, bool BT, int EPI>
 hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, int bn, int nw, int ns) {
   const int key = bm * 1000 + bn;
+  // M-major operands of the weight gradients (dW = dY^T X with dY, X
+  // token-major): the hand-ordered kernel with transposed LDS reads
+  if constexpr ((AT || BT) && (EPI == EPI_STORE_F || EPI == EPI_STORE_W13)) {
+    if (ns == 2 && !g.grp) {
+      const dim3 grid((g.M / bm) * (g.N / bn) * g.splits);
+      if (nw == 8) {
+        LAUNCH_HOT(256, 256, 8);
+        return hipGetLastError();
+      }
+      switch (key) {
+        case 256256: LAUNCH_HOT(256, 256, 4); break;
+        case 256128: LAUNCH_HOT(256, 128, 4); break;
+        case 128256: LAUNCH_HOT(128, 256, 4); break;
+        case 128128: LAUNCH_HOT(128, 128, 4); break;
+        case 64128: LAUNCH_HOT(64, 128, 4); break;
+        case 128064: LAUNCH_HOT(128, 64, 4); break;
+        case 256064: LAUNCH_HOT(256, 64, 4); break;
+        case 64064: LAUNCH_HOT(64, 64, 4); break;
+        default: return hipErrorInvalidValue;
+      }
+      return hipGetLastError();
+    }
+  }
   // the deferred-norm epilogues exist for the hand-ordered K-major kernel only
   constexpr bool HO_ONLY = epi_rr(EPI) || EPI == EPI_RESID_NORM;
   if constexpr (!AT && !BT && EPI != EPI_RESID_NORM) {
@@ -1191,7 +1275,8 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
                       e.rr_ld < (epi == EPI_CE_RR ? g.N : g.M) || g.splits != 1 || g.grp || g.a_t || g.b_t))
     return hipErrorInvalidValue;
   if (g.splits > 1) {
-    if (g.a_t || g.b_t || g.grp || !g.ws || (g.K % (g.splits * BK)) != 0 || (ns != 0 && ns != 2) ||
+    // layouts 0 (K-major), 1 (B M-major) and 3 (both M-major)
+    if ((g.a_t && !g.b_t) || g.grp || !g.ws || (g.K % (g.splits * BK)) != 0 || (ns != 0 && ns != 2) ||
         (epi != EPI_STORE_F && epi != EPI_STORE_H && epi != EPI_STORE_W13) || (g.N % 4) != 0)
       return hipErrorInvalidValue;
     if (bm == 0 || bn == 0) gemm_pick_tile(g.M, g.N, g.K, epi, &bm, &bn);
@@ -1201,7 +1286,9 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
     EpiParams pw;  // fp32 partials, ws[s][M][N]
     pw.C = g.ws;
     pw.ldc = g.N;
-    hipError_t r = launch<false, false, EPI_STORE_F>(g, pw, s, bm, bn, nw, 2);
+    hipError_t r = g.a_t   ? launch<true, true, EPI_STORE_F>(g, pw, s, bm, bn, nw, 2)
+                   : g.b_t ? launch<false, true, EPI_STORE_F>(g, pw, s, bm, bn, nw, 2)
+                           : launch<false, false, EPI_STORE_F>(g, pw, s, bm, bn, nw, 2);
     if (r != hipSuccess) return r;
     if (epi == EPI_STORE_F) return splitk_reduce<EPI_STORE_F>(g, e, s);
     if (epi == EPI_STORE_H) return splitk_reduce<EPI_STORE_H>(g, e, s);

@@ -135,6 +135,21 @@ int ensure_train(ane_engine* e, const char* op) {
 // Forward + backward of the nseq sequences in e->tok / e->tgt; ADDS the
 // loss-scaled gradient sum to tr.G and leaves per-sequence losses in
 // e->loss_seq.
+// Weight gradient dW += dY^T X over the T tokens of the step, dY [T][M] and
+// X [T][N] token-major as the backward leaves them.  By default the GEMM
+// reads them as they are (M-major operands through transposing LDS reads);
+// with ANE_TR_DW=0 both are first transposed into K-major staging buffers
+// and the K-major kernel runs (the same products; measured slower by the
+// transposes' HBM round trip).
+hipError_t dw_gemm(ane_engine* e, int cls, const half_t* dY, int M, const half_t* X, int N, int T, int epi,
+                   const EpiParams& p) {
+  TrainBufs& tb = e->tr;
+  if (e->tr_dw) return eng_gemm(e, cls, dY, M, true, X, N, true, M, N, T, epi, p);
+  hipError_t h = transpose2_h(tb.op_a, dY, T, M, M, T, tb.op_b, X, T, N, N, T, e->stream);
+  if (h != hipSuccess) return h;
+  return eng_gemm(e, cls, tb.op_a, T, false, tb.op_b, T, false, M, N, T, epi, p);
+}
+
 int backward_pass(ane_engine* e, int nseq) {
   const char* op = "step";
   const ane_model_cfg& c = e->cfg;
@@ -171,8 +186,12 @@ int backward_pass(ane_engine* e, int nseq) {
     EpiParams p;
     p.C = G + pm.embed; p.ldc = D; p.scale = 1.f / kDlScale; p.accumulate = 1;
     phase_begin(e, PH_EMBED_GRAD);
-    HIPCHK(op, transpose_h(tb.op_b, e->xh, T, D, D, T, st));
-    HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, tb.op_b, T, false, V, D, T, EPI_STORE_F, p));
+    if (e->tr_dw) {  // dl is vocab-major (K-major); xh token-major read through transposing LDS loads
+      HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, e->xh, D, true, V, D, T, EPI_STORE_F, p));
+    } else {
+      HIPCHK(op, transpose_h(tb.op_b, e->xh, T, D, D, T, st));
+      HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, tb.op_b, T, false, V, D, T, EPI_STORE_F, p));
+    }
     phase_end(e);
   }
   {  // final RMSNorm backward (+ backout backward for nanochat)
@@ -219,21 +238,15 @@ int backward_pass(ane_engine* e, int nseq) {
       EpiParams p;
       p.C = G + o.w2; p.ldc = H; p.accumulate = 1;
       phase_begin(e, PH_DW_GEMM);
-      HIPCHK(op, transpose2_h(tb.op_a, tb.dcur_h, T, D, D, T, tb.op_b, A.gate, T, H, H, T, st));
-      HIPCHK(op, eng_gemm(e, 3, tb.op_a, T, false, tb.op_b, T, false, D, H, T, EPI_STORE_F, p));
+      HIPCHK(op, dw_gemm(e, 3, tb.dcur_h, D, A.gate, H, T, EPI_STORE_F, p));
       phase_end(e);
     }
     {  // dW1 (| dW3) += dh x2Norm^T
       EpiParams p;
       p.C = G + o.w1; p.ldc = D; p.accumulate = 1;
       phase_begin(e, PH_DW_GEMM);
-      HIPCHK(op, transpose2_h(tb.op_a, tb.dh13, T, KH, KH, T, tb.op_b, A.xn2, T, D, D, T, st));
-      if (llama) {
-        p.C3 = G + o.w3;
-        HIPCHK(op, eng_gemm(e, 2, tb.op_a, T, false, tb.op_b, T, false, KH, D, T, EPI_STORE_W13, p));
-      } else {
-        HIPCHK(op, eng_gemm(e, 2, tb.op_a, T, false, tb.op_b, T, false, KH, D, T, EPI_STORE_F, p));
-      }
+      if (llama) p.C3 = G + o.w3;
+      HIPCHK(op, dw_gemm(e, 2, tb.dh13, KH, A.xn2, D, T, llama ? EPI_STORE_W13 : EPI_STORE_F, p));
       phase_end(e);
     }
     {  // dx2 = rl * dOut + RMSNorm-backward(dxn2; x2)
@@ -263,8 +276,7 @@ int backward_pass(ane_engine* e, int nseq) {
       EpiParams p;
       p.C = G + o.wo; p.ldc = D; p.accumulate = 1;
       phase_begin(e, PH_DW_GEMM);
-      HIPCHK(op, transpose2_h(tb.op_a, tb.dx2_h, T, D, D, T, tb.op_b, A.att, T, D, D, T, st));
-      HIPCHK(op, eng_gemm(e, 1, tb.op_a, T, false, tb.op_b, T, false, D, D, T, EPI_STORE_F, p));
+      HIPCHK(op, dw_gemm(e, 1, tb.dx2_h, D, A.att, D, T, EPI_STORE_F, p));
       phase_end(e);
     }
     {
@@ -310,8 +322,7 @@ int backward_pass(ane_engine* e, int nseq) {
       EpiParams p;
       p.C = G + o.wq; p.ldc = D; p.accumulate = 1;
       phase_begin(e, PH_DW_GEMM);
-      HIPCHK(op, transpose2_h(tb.op_a, tb.dqkv, T, 3 * D, 3 * D, T, tb.op_b, A.xn, T, D, D, T, st));
-      HIPCHK(op, eng_gemm(e, 0, tb.op_a, T, false, tb.op_b, T, false, 3 * D, D, T, EPI_STORE_F, p));
+      HIPCHK(op, dw_gemm(e, 0, tb.dqkv, 3 * D, A.xn, D, T, EPI_STORE_F, p));
       phase_end(e);
     }
     {  // dPrev = rl * dx2 + RMSNorm-backward(dxn; x) (+ VE gate grads, + backout injection)
@@ -347,8 +358,7 @@ int backward_pass(ane_engine* e, int nseq) {
       EpiParams p;
       p.C = G + pm.smear_gate; p.ldc = D; p.accumulate = 1;
       phase_begin(e, PH_DW_GEMM);
-      HIPCHK(op, transpose2_h(tb.op_a, tb.dgp, T, D, D, T, tb.op_b, tb.x0h, T, D, D, T, st));
-      HIPCHK(op, eng_gemm(e, 7, tb.op_a, T, false, tb.op_b, T, false, D, D, T, EPI_STORE_F, p));
+      HIPCHK(op, dw_gemm(e, 7, tb.dgp, D, tb.x0h, D, T, EPI_STORE_F, p));
       phase_end(e);
     }
     {

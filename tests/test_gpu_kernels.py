@@ -110,6 +110,24 @@ def test_gemm_split_k(bm, bn, nw, splits, out_f16):
             np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-4)
 
 
+@pytest.mark.parametrize("a_t,b_t", [(False, True), (True, True)])
+@pytest.mark.parametrize("bm,bn,nw", [(256, 256, 8), (128, 128, 4), (128, 64, 4), (64, 64, 4)])
+@pytest.mark.parametrize("splits", [2, 5])
+def test_gemm_split_k_m_major(a_t, b_t, bm, bn, nw, splits):
+    """Split-K over M-major operands (the weight gradients dW = dY^T X with
+    dY and X token-major, read through transposing LDS loads): each split's
+    K range is a range of rows of the stored operands."""
+    r = np.random.default_rng(bm + bn + splits + 11 * a_t + 13 * b_t)
+    M, N = 512, 256
+    for kps in (1, 3):
+        K = 64 * kps * splits
+        A = r.standard_normal((M, K)).astype(np.float16)
+        B = r.standard_normal((N, K)).astype(np.float16)
+        got = run_gemm(A, B, a_t, b_t, bm, bn, nw=nw, splits=splits)
+        ref = A.astype(np.float64) @ B.astype(np.float64).T
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=2e-4)
+
+
 def test_gemm_split_k_rejects_unsupported():
     lib = _lib.load()
     A = np.zeros((256, 256), np.float16)
