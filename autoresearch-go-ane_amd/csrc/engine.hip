@@ -121,7 +121,7 @@ int eng_fail(ane_engine* e, int code, const char* fmt, ...) {
 // ---------------------------------------------------------------------------
 // profiling (HIP events bracketing tracked launches)
 // ---------------------------------------------------------------------------
-void prof_begin(ane_engine* e, int cls) {
+void prof_begin(ane_engine* e, int cls, hipStream_t s) {
   if (!e->prof_on) return;
   if (e->prof_next >= e->prof_events.size()) {
     ProfEvent pe;
@@ -131,14 +131,14 @@ void prof_begin(ane_engine* e, int cls) {
   }
   ProfEvent& pe = e->prof_events[e->prof_next];
   pe.cls = cls;
-  (void)hipEventRecord(pe.a, e->stream);
+  (void)hipEventRecord(pe.a, s ? s : e->stream);
 }
-void prof_end(ane_engine* e, double flops, double bytes) {
+void prof_end(ane_engine* e, double flops, double bytes, hipStream_t s) {
   if (!e->prof_on) return;
   ProfEvent& pe = e->prof_events[e->prof_next];
   pe.flops = flops;
   pe.bytes = bytes;
-  (void)hipEventRecord(pe.b, e->stream);
+  (void)hipEventRecord(pe.b, s ? s : e->stream);
   e->prof_next++;
 }
 
@@ -151,7 +151,7 @@ void phase_reset(ane_engine* e) {
   e->ph_cls.clear();
 }
 
-void phase_begin(ane_engine* e, int phase) {
+void phase_begin(ane_engine* e, int phase, hipStream_t s) {
   e->ph_open = false;
   if (!e->ph_sample && phase != PH_REFRESH) return;
   while ((int)e->ph_ev.size() < e->ph_used + 2) {
@@ -159,16 +159,16 @@ void phase_begin(ane_engine* e, int phase) {
     if (hipEventCreate(&ev) != hipSuccess) return;
     e->ph_ev.push_back(ev);
   }
-  if (hipEventRecord(e->ph_ev[e->ph_used], e->stream) != hipSuccess) return;
+  if (hipEventRecord(e->ph_ev[e->ph_used], s ? s : e->stream) != hipSuccess) return;
   e->ph_cls.push_back(phase);
   e->ph_used += 2;
   e->ph_open = true;
 }
 
-void phase_end(ane_engine* e) {
+void phase_end(ane_engine* e, hipStream_t s) {
   if (!e->ph_open) return;
   e->ph_open = false;
-  if (hipEventRecord(e->ph_ev[e->ph_used - 1], e->stream) != hipSuccess) e->ph_cls.back() = -1;
+  if (hipEventRecord(e->ph_ev[e->ph_used - 1], s ? s : e->stream) != hipSuccess) e->ph_cls.back() = -1;
 }
 
 void phase_sum(ane_engine* e, double ms[PH_COUNT]) {
@@ -182,22 +182,25 @@ void phase_sum(ane_engine* e, double ms[PH_COUNT]) {
 }
 
 hipError_t eng_gemm(ane_engine* e, int cls, const half_t* A, int lda, bool at, const half_t* B, int ldb, bool bt,
-                    int M, int N, int K, int epi, const EpiParams& p, int bm, int bn) {
+                    int M, int N, int K, int epi, const EpiParams& p, int bm, int bn, bool side) {
+  if (side && (!e->dw_stream || !e->tr.splitk_ws2)) return hipErrorInvalidValue;
+  hipStream_t s = side ? e->dw_stream : e->stream;
+  float* ws = side ? e->tr.splitk_ws2 : e->tr.splitk_ws;
   GemmArgs g;
   g.A = A; g.B = B; g.lda = lda; g.ldb = ldb; g.M = M; g.N = N; g.K = K; g.a_t = at; g.b_t = bt;
   // training: GEMMs whose output is too small to fill the chip split K
   // (K-major operands, or M-major ones as the weight gradients read them)
-  if (!(at && !bt) && e->tr.splitk_ws && bm == 0 && bn == 0) {
+  if (!(at && !bt) && ws && bm == 0 && bn == 0) {
     int sp = 1;
     gemm_pick_split(M, N, K, epi, e->tr.splitk_cap, &bm, &bn, &sp);
     if (sp > 1) {
       g.splits = sp;
-      g.ws = e->tr.splitk_ws;
+      g.ws = ws;
     }
   }
-  prof_begin(e, cls);
-  hipError_t r = gemm_run(g, epi, p, e->stream, bm, bn);
-  prof_end(e, 2.0 * M * N * K, 2.0 * ((double)M * K + (double)N * K));
+  prof_begin(e, cls, s);
+  hipError_t r = gemm_run(g, epi, p, s, bm, bn);
+  prof_end(e, 2.0 * M * N * K, 2.0 * ((double)M * K + (double)N * K), s);
   return r;
 }
 
@@ -206,6 +209,7 @@ hipError_t eng_gemm(ane_engine* e, int cls, const half_t* A, int lda, bool at, c
 // ---------------------------------------------------------------------------
 static void free_all(ane_engine* e) {
   if (e->dev_set) (void)hipSetDevice(e->device);
+  if (e->dw_stream) (void)hipStreamSynchronize(e->dw_stream);
   if (e->stream) (void)hipStreamSynchronize(e->stream);
   for (void* p : e->allocs) (void)hipFree(p);
   e->allocs.clear();
@@ -231,6 +235,11 @@ static void free_all(ane_engine* e) {
   e->n_shadow_jobs = e->n_shadow_tiles = 0;
   e->shadow_jobs_t = false;
   drop_fwd_graph(e);
+  for (hipEvent_t ev : e->xev) (void)hipEventDestroy(ev);
+  e->xev.clear();
+  e->xev_next = 0;
+  if (e->dw_stream) (void)hipStreamDestroy(e->dw_stream);
+  e->dw_stream = nullptr;
   if (e->stream) (void)hipStreamDestroy(e->stream);
   e->stream = nullptr;
 }
@@ -381,6 +390,7 @@ extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_e
   if (const char* g = getenv("ANE_FUSED_NORM")) e->fused_norm = atoi(g) != 0;
   if (const char* g = getenv("ANE_FUSED_PF")) e->fused_pf = atoi(g) != 0;
   if (const char* g = getenv("ANE_TR_DW")) e->tr_dw = atoi(g) != 0;
+  if (const char* g = getenv("ANE_DW_ASYNC")) e->dw_async = atoi(g) != 0;
   if (const char* g = getenv("ANE_PHASE_EVERY")) e->ph_period = atoi(g) > 0 ? atoi(g) : 1;
   e->lr = e->opt.lr;
   int rc = validate_cfg(e, e->cfg);

@@ -77,6 +77,14 @@ struct TrainBufs {
   ane::half_t* op_b = nullptr;  // [max(H, D), T]
   float* splitk_ws = nullptr;   // split-K partials of the backward GEMMs
   size_t splitk_cap = 0;        // floats
+  // weight gradients on the dW stream: its own split-K workspace, and a
+  // second copy of each activation gradient they read, so that layer l and
+  // layer l - 1 use different buffers (index = layer parity)
+  float* splitk_ws2 = nullptr;
+  ane::half_t* dcur_h2 = nullptr;
+  ane::half_t* dh13_2 = nullptr;
+  ane::half_t* dx2_h2 = nullptr;
+  ane::half_t* dqkv2 = nullptr;
   float* colscale = nullptr;
   float* gx0 = nullptr;
   float* ginj = nullptr;
@@ -151,6 +159,15 @@ struct ane_engine {
   bool fused_norm = false;
   bool fused_pf = true;
   bool tr_dw = true;  // weight gradients read token-major operands directly (ANE_TR_DW=0: transposes)
+  // The backward's weight-gradient GEMMs run on a second stream beside the
+  // activation-gradient chain (ANE_DW_ASYNC=0: all on one stream).  Events
+  // order the two: the dW stream waits for the producer of each dY, and the
+  // main stream waits, once per layer, for the dW work of the layer above
+  // before it overwrites a buffer that work reads.
+  bool dw_async = true;
+  hipStream_t dw_stream = nullptr;
+  std::vector<hipEvent_t> xev;  // fork / join events (timing disabled), reused per call
+  size_t xev_next = 0;
   int fwd_rr_nparts = 0;
   int ce_bm = 256, ce_np = 0;  // smallest classifier block row and the partial rows it needs
   float2* partial = nullptr;
@@ -215,10 +232,12 @@ int eng_fail(ane_engine* e, int code, const char* fmt, ...);
     if (!e) return ANE_ERR_CLOSED;                                                                \
     if (e->closed) return eng_fail(e, ANE_ERR_CLOSED, "storiesane %s: engine is closed", op);     \
   } while (0)
-void prof_begin(ane_engine* e, int cls);
-void prof_end(ane_engine* e, double flops, double bytes);
+void prof_begin(ane_engine* e, int cls, hipStream_t s = nullptr);
+void prof_end(ane_engine* e, double flops, double bytes, hipStream_t s = nullptr);
+// side = run on the dW stream with its own split-K workspace
 hipError_t eng_gemm(ane_engine* e, int cls, const ane::half_t* A, int lda, bool at, const ane::half_t* B, int ldb,
-                    bool bt, int M, int N, int K, int epi, const ane::EpiParams& p, int bm = 0, int bn = 0);
+                    bool bt, int M, int N, int K, int epi, const ane::EpiParams& p, int bm = 0, int bn = 0,
+                    bool side = false);
 int refresh_shadows(ane_engine* e);
 int forward_body(ane_engine* e, int nseq, int train, bool defer_norm = false);
 void drop_fwd_graph(ane_engine* e);
@@ -235,8 +254,8 @@ hipError_t dalloc(ane_engine* e, T** p, size_t n) {
 int head_loss(ane_engine* e, int nseq, float* colscale, float dscale);
 enum StepPhase { PH_EMBED_GRAD = 0, PH_RMS_DW, PH_DW_GEMM, PH_REFRESH, PH_COUNT };
 void phase_reset(ane_engine* e);
-void phase_begin(ane_engine* e, int phase);
-void phase_end(ane_engine* e);
+void phase_begin(ane_engine* e, int phase, hipStream_t s = nullptr);
+void phase_end(ane_engine* e, hipStream_t s = nullptr);
 // after the stream has drained: milliseconds per phase
 void phase_sum(ane_engine* e, double ms[PH_COUNT]);
 int load_windows(ane_engine* e, const uint64_t* positions, int nseq);

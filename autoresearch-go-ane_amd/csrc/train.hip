@@ -106,6 +106,15 @@ int ensure_train(ane_engine* e, const char* op) {
     tb.splitk_cap = 8 * mx;
     HIPCHK(op, dalloc(e, &tb.splitk_ws, tb.splitk_cap));
   }
+  if (e->dw_async && e->tr_dw) {
+    // default priority, like the main stream
+    if (!e->dw_stream) HIPCHK(op, hipStreamCreateWithFlags(&e->dw_stream, hipStreamNonBlocking));
+    HIPCHK(op, dalloc(e, &tb.splitk_ws2, tb.splitk_cap));
+    HIPCHK(op, dalloc(e, &tb.dcur_h2, T * D));
+    HIPCHK(op, dalloc(e, &tb.dh13_2, T * KH));
+    HIPCHK(op, dalloc(e, &tb.dx2_h2, T * D));
+    HIPCHK(op, dalloc(e, &tb.dqkv2, T * 3 * D));
+  }
   // transposed weight shadows, filled by the refresh below
   for (int l = 0; l < c.layers; l++) {
     LayerShadow& s = e->ls[l];
@@ -142,15 +151,66 @@ int ensure_train(ane_engine* e, const char* op) {
 // and the K-major kernel runs (the same products; measured slower by the
 // transposes' HBM round trip).
 hipError_t dw_gemm(ane_engine* e, int cls, const half_t* dY, int M, const half_t* X, int N, int T, int epi,
-                   const EpiParams& p) {
+                   const EpiParams& p, bool side = false) {
   TrainBufs& tb = e->tr;
-  if (e->tr_dw) return eng_gemm(e, cls, dY, M, true, X, N, true, M, N, T, epi, p);
+  if (e->tr_dw) return eng_gemm(e, cls, dY, M, true, X, N, true, M, N, T, epi, p, 0, 0, side);
+  if (side) return hipErrorInvalidValue;  // the staging buffers belong to the main stream
   hipError_t h = transpose2_h(tb.op_a, dY, T, M, M, T, tb.op_b, X, T, N, N, T, e->stream);
   if (h != hipSuccess) return h;
   return eng_gemm(e, cls, tb.op_a, T, false, tb.op_b, T, false, M, N, T, epi, p);
 }
 
+// An event of the fork / join pool: created on first use (on the host,
+// never under capture), handed out in order and reused by the next call.
+hipError_t next_xev(ane_engine* e, hipEvent_t* ev) {
+  if (e->xev_next >= e->xev.size()) {
+    hipEvent_t x = nullptr;
+    // ordering between two streams of one device only: no system-scope
+    // fence (each kernel's own release / acquire makes its results visible;
+    // the fence costs ~3 us of idle GPU per record, 0.14 ms per B16 step)
+    hipError_t h = hipEventCreateWithFlags(&x, hipEventDisableTiming | hipEventDisableSystemFence);
+    if (h != hipSuccess) return h;
+    e->xev.push_back(x);
+  }
+  *ev = e->xev[e->xev_next++];
+  return hipSuccess;
+}
+
+// Marks the work given to stream `s` so far; *ev (if given) receives the
+// event so that another stream can wait for it later.
+hipError_t mark(ane_engine* e, hipStream_t s, hipEvent_t* ev) {
+  hipEvent_t x = nullptr;
+  hipError_t h = next_xev(e, &x);
+  if (h == hipSuccess) h = hipEventRecord(x, s);
+  if (h == hipSuccess && ev) *ev = x;
+  return h;
+}
+
+// Stream `to` runs its later work after what `from` has been given so far.
+hipError_t stream_after(ane_engine* e, hipStream_t to, hipStream_t from) {
+  hipEvent_t x = nullptr;
+  hipError_t h = mark(e, from, &x);
+  return h == hipSuccess ? hipStreamWaitEvent(to, x, 0) : h;
+}
+
+int backward_body(ane_engine* e, int nseq, bool async);
+
+// The backward with the weight gradients on the dW stream when enabled: the
+// main stream waits for all of them before it returns, also on an error
+// return, so that no later launch overwrites what they still read.
 int backward_pass(ane_engine* e, int nseq) {
+  const bool async = e->dw_async && e->tr_dw && e->dw_stream && e->tr.splitk_ws2;
+  e->xev_next = 0;
+  int rc = backward_body(e, nseq, async);
+  if (async) {
+    const hipError_t h = stream_after(e, e->stream, e->dw_stream);
+    if (h != hipSuccess && rc == ANE_OK)
+      rc = eng_fail(e, ANE_ERR_HIP, "storiesane step: dW stream join: %s", hipGetErrorString(h));
+  }
+  return rc;
+}
+
+int backward_body(ane_engine* e, int nseq, bool async) {
   const char* op = "step";
   const ane_model_cfg& c = e->cfg;
   const bool llama = c.arch == ANE_ARCH_LLAMA2;
@@ -162,7 +222,14 @@ int backward_pass(ane_engine* e, int nseq) {
   const float* P = e->P;
   float* G = tb.G;
   hipStream_t st = e->stream;
+  // weight gradients: on the dW stream (ds) or in line on the main stream
+  hipStream_t ds = async ? e->dw_stream : st;
   const ParamMap& pm = e->pm;
+  // activation gradients the dW GEMMs read: layer l uses copy (l & 1), so the
+  // main stream may write layer l - 1's while layer l's dW GEMMs still run;
+  // dcur_h(l) is the dY that enters layer l from above
+  auto by_parity = [&](half_t* a, half_t* b, int l) { return async && (l & 1) ? b : a; };
+  auto dcur_h_of = [&](int l) { return by_parity(tb.dcur_h, tb.dcur_h2, l); };
 
   int rc = forward_body(e, nseq, 1);
   if (rc) return rc;
@@ -177,6 +244,7 @@ int backward_pass(ane_engine* e, int nseq) {
     p.softcap = !llama; p.cap = 15.f; p.vocab = V;
     HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_DLOGITS, p));
   }
+  if (async) HIPCHK(op, stream_after(e, ds, st));  // dl, dl_t written
   {  // dy = Embed^T dlogits (MatMulEmbedTScale, ane/stories/cpu.go:333-360)
     EpiParams p;
     p.C = tb.dxn; p.ldc = D; p.scale = 1.f / kDlScale;
@@ -185,18 +253,18 @@ int backward_pass(ane_engine* e, int nseq) {
   {  // classifier part of the embedding gradient (MatMulGradEmbedScale, ane/stories/cpu.go:366-385)
     EpiParams p;
     p.C = G + pm.embed; p.ldc = D; p.scale = 1.f / kDlScale; p.accumulate = 1;
-    phase_begin(e, PH_EMBED_GRAD);
+    phase_begin(e, PH_EMBED_GRAD, ds);
     if (e->tr_dw) {  // dl is vocab-major (K-major); xh token-major read through transposing LDS loads
-      HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, e->xh, D, true, V, D, T, EPI_STORE_F, p));
+      HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, e->xh, D, true, V, D, T, EPI_STORE_F, p, 0, 0, async));
     } else {
       HIPCHK(op, transpose_h(tb.op_b, e->xh, T, D, D, T, st));
       HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, tb.op_b, T, false, V, D, T, EPI_STORE_F, p));
     }
-    phase_end(e);
+    phase_end(e, ds);
   }
   {  // final RMSNorm backward (+ backout backward for nanochat)
     NormBwdArgs a;
-    a.dy = tb.dxn; a.T = T; a.D = D; a.out = tb.dcur; a.out_h = tb.dcur_h;
+    a.dy = tb.dxn; a.T = T; a.D = D; a.out = tb.dcur; a.out_h = dcur_h_of(L - 1);
     if (llama) {
       a.x = tb.xlast; a.gain = P + pm.g_final; a.dgain_part = tb.dgain_part;
     } else {
@@ -216,49 +284,60 @@ int backward_pass(ane_engine* e, int nseq) {
   (void)hipEventRecord(e->step_ev[ane_engine::EV_HEAD1], st);
 
   // ---- layers, last to first ------------------------------------------------
+  // dW stream order per layer: dW2, dW13 (after the SwiGLU-backward GEMM),
+  // dWo (after the FFN norm backward), dWqkv (after the attention backward);
+  // above_done marks the end of the layer above's dW work
+  hipEvent_t above_done = nullptr;
   for (int l = L - 1; l >= 0; l--) {
     const LayerOff& o = pm.L[l];
     const LayerShadow& s = e->ls[l];
     const LayerActs& A = tb.L[l];
     const float* rl_p = llama ? nullptr : P + pm.resid + l;
     const float* xl_p = llama ? nullptr : P + pm.x0l + l;
+    half_t* dcur_in = dcur_h_of(l);
+    half_t* dcur_out = dcur_h_of(l - 1);
+    half_t* dh13 = by_parity(tb.dh13, tb.dh13_2, l);
+    half_t* dx2_h = by_parity(tb.dx2_h, tb.dx2_h2, l);
+    half_t* dqkv = by_parity(tb.dqkv, tb.dqkv2, l);
     // FFN (backwardFFNCPU, ane/train_full.go:592-601)
     {
       EpiParams p;
-      p.C = tb.dh13; p.ldc = KH; p.C2 = A.h13; p.ldc2 = KH;
-      HIPCHK(op, eng_gemm(e, 3, tb.dcur_h, D, false, s.w2_t, D, false, T, H, D,
+      p.C = dh13; p.ldc = KH; p.C2 = A.h13; p.ldc2 = KH;
+      HIPCHK(op, eng_gemm(e, 3, dcur_in, D, false, s.w2_t, D, false, T, H, D,
                           llama ? EPI_SWIGLU_BWD : EPI_RELU2_BWD, p));
     }
-    {
-      EpiParams p;
-      p.C = tb.dxn; p.ldc = D;
-      HIPCHK(op, eng_gemm(e, 2, tb.dh13, KH, false, s.w13_t, KH, false, T, D, KH, EPI_STORE_F, p));
-    }
+    if (async) HIPCHK(op, stream_after(e, ds, st));  // dcur_in, dh13 written
     {  // dW2 += dOut gate^T
       EpiParams p;
       p.C = G + o.w2; p.ldc = H; p.accumulate = 1;
-      phase_begin(e, PH_DW_GEMM);
-      HIPCHK(op, dw_gemm(e, 3, tb.dcur_h, D, A.gate, H, T, EPI_STORE_F, p));
-      phase_end(e);
+      phase_begin(e, PH_DW_GEMM, ds);
+      HIPCHK(op, dw_gemm(e, 3, dcur_in, D, A.gate, H, T, EPI_STORE_F, p, async));
+      phase_end(e, ds);
     }
     {  // dW1 (| dW3) += dh x2Norm^T
       EpiParams p;
       p.C = G + o.w1; p.ldc = D; p.accumulate = 1;
-      phase_begin(e, PH_DW_GEMM);
       if (llama) p.C3 = G + o.w3;
-      HIPCHK(op, dw_gemm(e, 2, tb.dh13, KH, A.xn2, D, T, llama ? EPI_STORE_W13 : EPI_STORE_F, p));
-      phase_end(e);
+      phase_begin(e, PH_DW_GEMM, ds);
+      HIPCHK(op, dw_gemm(e, 2, dh13, KH, A.xn2, D, T, llama ? EPI_STORE_W13 : EPI_STORE_F, p, async));
+      phase_end(e, ds);
+    }
+    {
+      EpiParams p;
+      p.C = tb.dxn; p.ldc = D;
+      HIPCHK(op, eng_gemm(e, 2, dh13, KH, false, s.w13_t, KH, false, T, D, KH, EPI_STORE_F, p));
     }
     {  // dx2 = rl * dOut + RMSNorm-backward(dxn2; x2)
       NormBwdArgs a;
       a.dy = tb.dxn; a.x = A.x2; a.T = T; a.D = D; a.addend = tb.dcur; a.alpha_p = rl_p;
-      a.out = tb.dx2; a.out_h = tb.dx2_h;
+      a.out = tb.dx2; a.out_h = dx2_h;
       if (llama) {
         a.gain = P + o.g_ffn; a.dgain_part = tb.dgain_part;
       } else {
         a.lam_x = A.x2; a.lam_x0 = e->x0; a.lam_part = tb.dot_part; a.gx0 = tb.gx0; a.xl_p = xl_p;
       }
       HIPCHK(op, norm_bwd(a, st));
+      if (async) HIPCHK(op, stream_after(e, ds, st));  // dx2_h written
       if (llama) {
         phase_begin(e, PH_RMS_DW);
         HIPCHK(op, reduce_partials_add(G + o.g_ffn, tb.dgain_part, nblk, D, st));
@@ -269,20 +348,20 @@ int backward_pass(ane_engine* e, int nseq) {
     // attention (backwardAttentionCPU, ane/train_full.go:644-675)
     {
       EpiParams p;
-      p.C = tb.datt; p.ldc = D;
-      HIPCHK(op, eng_gemm(e, 1, tb.dx2_h, D, false, s.wo_t, D, false, T, D, D, EPI_STORE_H, p));
+      p.C = G + o.wo; p.ldc = D; p.accumulate = 1;
+      phase_begin(e, PH_DW_GEMM, ds);
+      HIPCHK(op, dw_gemm(e, 1, dx2_h, D, A.att, D, T, EPI_STORE_F, p, async));
+      phase_end(e, ds);
     }
     {
       EpiParams p;
-      p.C = G + o.wo; p.ldc = D; p.accumulate = 1;
-      phase_begin(e, PH_DW_GEMM);
-      HIPCHK(op, dw_gemm(e, 1, tb.dx2_h, D, A.att, D, T, EPI_STORE_F, p));
-      phase_end(e);
+      p.C = tb.datt; p.ldc = D;
+      HIPCHK(op, eng_gemm(e, 1, dx2_h, D, false, s.wo_t, D, false, T, D, D, EPI_STORE_H, p));
     }
     {
       AttnBwdArgs b;
       memset(&b, 0, sizeof b);
-      b.qkv = A.qkv; b.qkvt = A.qkvt; b.dout = tb.datt; b.delta = tb.delta; b.dqkv = tb.dqkv;
+      b.qkv = A.qkv; b.qkvt = A.qkvt; b.dout = tb.datt; b.delta = tb.delta; b.dqkv = dqkv;
       b.rope_cos = e->rope_cos; b.rope_sin = e->rope_sin; b.nseq = nseq; b.S = S; b.NH = NH;
       b.qknorm = llama ? 0 : 1;
       if (compat) {
@@ -310,25 +389,33 @@ int backward_pass(ane_engine* e, int nseq) {
       HIPCHK(op, attention_bwd(b, st));
       prof_end(e, 2.5 * 4.0 * 64 * NH * (double)nseq * ((double)S * (S + 1) / 2), 0);
     }
+    if (async) HIPCHK(op, stream_after(e, ds, st));  // dqkv written
+    {  // dWq | dWk | dWv += dqkv xNorm^T
+      EpiParams p;
+      p.C = G + o.wq; p.ldc = D; p.accumulate = 1;
+      phase_begin(e, PH_DW_GEMM, ds);
+      HIPCHK(op, dw_gemm(e, 0, dqkv, 3 * D, A.xn, D, T, EPI_STORE_F, p, async));
+      phase_end(e, ds);
+    }
+    hipEvent_t this_done = nullptr;
+    if (async) HIPCHK(op, mark(e, ds, &this_done));
     if (o.ve_embed >= 0)
-      HIPCHK(op, ve_bwd(G + o.ve_embed, G + o.ve_gate, tb.ve_dx, tb.dqkv + 2 * D, 3 * D, A.xin, P + o.ve_embed,
+      HIPCHK(op, ve_bwd(G + o.ve_embed, G + o.ve_gate, tb.ve_dx, dqkv + 2 * D, 3 * D, A.xin, P + o.ve_embed,
                         P + o.ve_gate, e->tok, T, D, NH, V, st));
     {
       EpiParams p;
       p.C = tb.dxn; p.ldc = D;
-      HIPCHK(op, eng_gemm(e, 0, tb.dqkv, 3 * D, false, s.wqkv_t, 3 * D, false, T, D, 3 * D, EPI_STORE_F, p));
+      HIPCHK(op, eng_gemm(e, 0, dqkv, 3 * D, false, s.wqkv_t, 3 * D, false, T, D, 3 * D, EPI_STORE_F, p));
     }
-    {  // dWq | dWk | dWv += dqkv xNorm^T
-      EpiParams p;
-      p.C = G + o.wq; p.ldc = D; p.accumulate = 1;
-      phase_begin(e, PH_DW_GEMM);
-      HIPCHK(op, dw_gemm(e, 0, tb.dqkv, 3 * D, A.xn, D, T, EPI_STORE_F, p));
-      phase_end(e);
-    }
+    // dcur_out is the copy the layer above's dW2 read: wait for that layer's
+    // dW work (which also covers its dh13, dx2_h and dqkv copies, written
+    // again by the layer below)
+    if (above_done) HIPCHK(op, hipStreamWaitEvent(st, above_done, 0));
+    above_done = this_done;
     {  // dPrev = rl * dx2 + RMSNorm-backward(dxn; x) (+ VE gate grads, + backout injection)
       NormBwdArgs a;
       a.dy = tb.dxn; a.x = A.xin; a.T = T; a.D = D; a.addend = tb.dx2; a.alpha_p = rl_p;
-      a.out = tb.dcur; a.out_h = tb.dcur_h;
+      a.out = tb.dcur; a.out_h = dcur_out;
       if (llama) {
         a.gain = P + o.g_att; a.dgain_part = tb.dgain_part;
       } else {
@@ -345,6 +432,9 @@ int backward_pass(ane_engine* e, int nseq) {
         HIPCHK(op, reduce_dots_add(G + pm.resid + l, G + pm.x0l + l, tb.dot_part, nblk, 1.f, st));
     }
   }
+  // every dW launch is done before the embedding side (embed_bwd adds into
+  // the embedding gradient the classifier's dW GEMM wrote)
+  if (async) HIPCHK(op, stream_after(e, st, ds));
 
   // ---- embedding side ---------------------------------------------------------
   if (!llama) {
