@@ -391,6 +391,7 @@ extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_e
   if (const char* g = getenv("ANE_FUSED_PF")) e->fused_pf = atoi(g) != 0;
   if (const char* g = getenv("ANE_TR_DW")) e->tr_dw = atoi(g) != 0;
   if (const char* g = getenv("ANE_DW_ASYNC")) e->dw_async = atoi(g) != 0;
+  if (const char* g = getenv("ANE_BWD_PREFETCH")) e->bwd_prefetch = atoi(g) != 0;
   if (const char* g = getenv("ANE_PHASE_EVERY")) e->ph_period = atoi(g) > 0 ? atoi(g) : 1;
   e->lr = e->opt.lr;
   int rc = validate_cfg(e, e->cfg);

@@ -165,6 +165,7 @@ struct ane_engine {
   // main stream waits, once per layer, for the dW work of the layer above
   // before it overwrites a buffer that work reads.
   bool dw_async = true;
+  bool bwd_prefetch = true;  // ANE_BWD_PREFETCH=0: no prefetch of the backward's GEMM operands
   hipStream_t dw_stream = nullptr;
   std::vector<hipEvent_t> xev;  // fork / join events (timing disabled), reused per call
   size_t xev_next = 0;

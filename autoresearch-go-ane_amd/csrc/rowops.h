@@ -11,6 +11,22 @@ hipError_t embed_lookup(float* x, const float* embed, const uint16_t* tok, int T
 // Streams [p, p + bytes) through the cache hierarchy (prefetch_slice over up
 // to 1024 blocks): the weights of the GEMM that runs next.
 hipError_t prefetch_weights(const void* p, size_t bytes, hipStream_t s);
+// The same for up to kPrefetchRegions regions in one launch (null or empty
+// regions are skipped): brings the operands of GEMMs a few kernels ahead
+// into the device's last-level cache.
+constexpr int kPrefetchRegions = 6;
+struct PrefetchList {
+  const void* p[kPrefetchRegions] = {};
+  size_t bytes[kPrefetchRegions] = {};
+  int n = 0;
+  void add(const void* q, size_t b) {
+    if (q && b >= 16 && n < kPrefetchRegions) {
+      p[n] = q;
+      bytes[n++] = b;
+    }
+  }
+};
+hipError_t prefetch_list(const PrefetchList& l, hipStream_t s);
 // x = embed[tok] (0 for tok >= V), xg = fp16(x * gain) and ssq[t] = sum of
 // x[t]^2: the inputs of a GEMM that applies the RMSNorm after its product
 // (EPI_*_RR with one partial per row); pf: weights streamed alongside.

@@ -25,6 +25,26 @@ __global__ __launch_bounds__(256) void prefetch_kernel(const void* pf, size_t pf
   prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
 }
 
+// Each thread keeps four 16-byte loads in flight per region pass.
+__global__ __launch_bounds__(256) void prefetch_list_kernel(PrefetchList l) {
+  uint32_t x = 0;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (int r = 0; r < l.n; r++) {
+    const uint4* q = reinterpret_cast<const uint4*>(l.p[r]);
+    const size_t n = l.bytes[r] / 16;
+    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; i + 3 * stride < n; i += 4 * stride) {
+      const uint4 a = q[i], b = q[i + stride], c = q[i + 2 * stride], d = q[i + 3 * stride];
+      x ^= (a.x ^ a.y ^ a.z ^ a.w) ^ (b.x ^ b.y ^ b.z ^ b.w) ^ (c.x ^ c.y ^ c.z ^ c.w) ^ (d.x ^ d.y ^ d.z ^ d.w);
+    }
+    for (; i < n; i += stride) {
+      const uint4 a = q[i];
+      x ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+  }
+  asm volatile("" ::"v"(x));
+}
+
 // x = E[tok] (0 for tok >= V), xg = fp16(x * gain), ssq[t] = sum of x^2 (the
 // deferred norm's one partial per row); the next GEMM's weights streamed
 // through the caches alongside.
@@ -246,6 +266,15 @@ hipError_t prefetch_weights(const void* p, size_t bytes, hipStream_t s) {
   const size_t n16 = bytes / 16;
   const unsigned blocks = (unsigned)std::min<size_t>(1024, (n16 + 255) / 256);
   hipLaunchKernelGGL(prefetch_kernel, dim3(blocks), dim3(256), 0, s, p, bytes);
+  return hipGetLastError();
+}
+
+hipError_t prefetch_list(const PrefetchList& l, hipStream_t s) {
+  size_t tot = 0;
+  for (int r = 0; r < l.n; r++) tot += l.bytes[r];
+  if (tot < 16) return hipSuccess;
+  const unsigned blocks = (unsigned)std::min<size_t>(512, (tot / 16 / 4 + 255) / 256);
+  hipLaunchKernelGGL(prefetch_list_kernel, dim3(blocks), dim3(256), 0, s, l);
   return hipGetLastError();
 }
 

@@ -19,6 +19,8 @@
 #include <string.h>
 #include <time.h>
 
+#include <initializer_list>
+#include <utility>
 #include <vector>
 
 #include "attention.h"
@@ -231,6 +233,22 @@ int backward_body(ane_engine* e, int nseq, bool async) {
   auto by_parity = [&](half_t* a, half_t* b, int l) { return async && (l & 1) ? b : a; };
   auto dcur_h_of = [&](int l) { return by_parity(tb.dcur_h, tb.dcur_h2, l); };
 
+  // Cold GEMM operands streamed into the caches by a prefetch kernel on the
+  // dW stream at each fork: the weight shadow of the dX GEMM that the main
+  // stream starts at the same time (the prefetch runs ahead of that GEMM's
+  // k loop) and the saved activations of the dW GEMMs queued behind it.
+  // Both were last read a step or a forward ago; with them cold, 64 blocks
+  // meet each B panel at once and a 64x64-tile GEMM pays ~10 us (W1|W3 dX
+  // and dW at B16).  A prefetch issued a few kernels earlier does not help:
+  // the data in between evicts it.
+  auto prefetch = [&](hipStream_t s, std::initializer_list<std::pair<const void*, size_t>> regions) -> hipError_t {
+    if (!e->bwd_prefetch) return hipSuccess;
+    PrefetchList pl;
+    for (const auto& r : regions) pl.add(r.first, r.second);
+    return prefetch_list(pl, s);
+  };
+  const size_t TD2 = (size_t)T * D * 2;
+
   int rc = forward_body(e, nseq, 1);
   if (rc) return rc;
 
@@ -282,6 +300,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
     }
   }
   (void)hipEventRecord(e->step_ev[ane_engine::EV_HEAD1], st);
+  HIPCHK(op, prefetch(st, {{e->ls[L - 1].w2_t, (size_t)H * D * 2}}));
 
   // ---- layers, last to first ------------------------------------------------
   // dW stream order per layer: dW2, dW13 (after the SwiGLU-backward GEMM),
@@ -307,6 +326,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
                           llama ? EPI_SWIGLU_BWD : EPI_RELU2_BWD, p));
     }
     if (async) HIPCHK(op, stream_after(e, ds, st));  // dcur_in, dh13 written
+    HIPCHK(op, prefetch(ds, {{s.w13_t, (size_t)KH * D * 2}, {A.xn2, TD2}, {A.gate, (size_t)T * H * 2}}));
     {  // dW2 += dOut gate^T
       EpiParams p;
       p.C = G + o.w2; p.ldc = H; p.accumulate = 1;
@@ -338,6 +358,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
       }
       HIPCHK(op, norm_bwd(a, st));
       if (async) HIPCHK(op, stream_after(e, ds, st));  // dx2_h written
+      HIPCHK(op, prefetch(ds, {{s.wo_t, (size_t)D * D * 2}, {A.att, TD2}}));
       if (llama) {
         phase_begin(e, PH_RMS_DW);
         HIPCHK(op, reduce_partials_add(G + o.g_ffn, tb.dgain_part, nblk, D, st));
@@ -390,6 +411,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
       prof_end(e, 2.5 * 4.0 * 64 * NH * (double)nseq * ((double)S * (S + 1) / 2), 0);
     }
     if (async) HIPCHK(op, stream_after(e, ds, st));  // dqkv written
+    HIPCHK(op, prefetch(ds, {{s.wqkv_t, (size_t)3 * D * D * 2}, {A.xn, TD2}}));
     {  // dWq | dWk | dWv += dqkv xNorm^T
       EpiParams p;
       p.C = G + o.wq; p.ldc = D; p.accumulate = 1;
