@@ -15,6 +15,7 @@
 #include <time.h>
 
 #include <string>
+#include <algorithm>
 #include <vector>
 
 #include "../../include/ane_hip.h"
@@ -213,6 +214,8 @@ static void free_all(ane_engine* e) {
   if (e->stream) (void)hipStreamSynchronize(e->stream);
   for (void* p : e->allocs) (void)hipFree(p);
   e->allocs.clear();
+  if (e->loss_host) (void)hipHostFree(e->loss_host);
+  e->loss_host = nullptr;
   for (ProfEvent& pe : e->prof_events) {
     (void)hipEventDestroy(pe.a);
     (void)hipEventDestroy(pe.b);
@@ -235,6 +238,12 @@ static void free_all(ane_engine* e) {
   e->n_shadow_jobs = e->n_shadow_tiles = 0;
   e->shadow_jobs_t = false;
   drop_fwd_graph(e);
+  for (hipEvent_t& ev : e->refresh_ev)
+    if (ev) {
+      (void)hipEventDestroy(ev);
+      ev = nullptr;
+    }
+  e->refresh_pending = false;
   for (hipEvent_t ev : e->xev) (void)hipEventDestroy(ev);
   e->xev.clear();
   e->xev_next = 0;
@@ -369,6 +378,7 @@ static int open_impl(ane_engine* e) {
   HIPCHK(op, dalloc(e, &e->lse, T));
   HIPCHK(op, dalloc(e, &e->tok_loss, T));
   HIPCHK(op, dalloc(e, &e->loss_seq, (size_t)e->opt.max_batch));
+  HIPCHK(op, hipHostMalloc((void**)&e->loss_host, (size_t)e->opt.max_batch * sizeof(float), hipHostMallocDefault));
   HIPCHK(op, dalloc(e, &e->logits, (size_t)V * S));
   (void)NH;
   HIPCHK(op, hipStreamSynchronize(e->stream));
@@ -392,6 +402,7 @@ extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_e
   if (const char* g = getenv("ANE_TR_DW")) e->tr_dw = atoi(g) != 0;
   if (const char* g = getenv("ANE_DW_ASYNC")) e->dw_async = atoi(g) != 0;
   if (const char* g = getenv("ANE_BWD_PREFETCH")) e->bwd_prefetch = atoi(g) != 0;
+  if (const char* g = getenv("ANE_FUSED_ADAM")) e->fused_adam = atoi(g) != 0;
   if (const char* g = getenv("ANE_PHASE_EVERY")) e->ph_period = atoi(g) > 0 ? atoi(g) : 1;
   e->lr = e->opt.lr;
   int rc = validate_cfg(e, e->cfg);
@@ -424,6 +435,7 @@ extern "C" void ane_destroy(ane_engine* e) {
 extern "C" int ane_sync(ane_engine* e) {
   CLOSED_CHECK("sync");
   HIPCHK("sync", hipStreamSynchronize(e->stream));
+  if (e->dw_stream) HIPCHK("sync", hipStreamSynchronize(e->dw_stream));
   return ANE_OK;
 }
 
@@ -467,14 +479,80 @@ static int build_shadow_jobs(ane_engine* e) {
   }
   HIPCHK(op, hipStreamSynchronize(e->stream));  // no launch still reads the old table
   HIPCHK(op, hipMemcpy(e->shadow_jobs, jobs.data(), jobs.size() * sizeof(ShadowJob), hipMemcpyHostToDevice));
+  e->shadow_jobs_h = jobs;
+  e->upd_sig.clear();  // update jobs point at these shadows
   e->n_shadow_jobs = (int)jobs.size();
   e->n_shadow_tiles = tiles;
   e->shadow_jobs_t = e->embed_t != nullptr;
   return ANE_OK;
 }
 
+int ensure_update_jobs(ane_engine* e, const AdamArgs& a) {
+  const char* op = "flush";
+  std::vector<int64_t> sig;
+  for (int i = 0; i < a.nseg; i++) {
+    sig.push_back(a.seg[i].off);
+    sig.push_back(a.seg[i].len);
+  }
+  if (e->upd_jobs && sig == e->upd_sig) return ANE_OK;
+  // segments in parameter order, each cut at the matrices with a shadow
+  std::vector<int> order(a.nseg);
+  for (int i = 0; i < a.nseg; i++) order[i] = i;
+  std::sort(order.begin(), order.end(), [&](int x, int y) { return a.seg[x].off < a.seg[y].off; });
+  std::vector<const ShadowJob*> sj;
+  for (const ShadowJob& j : e->shadow_jobs_h) sj.push_back(&j);
+  std::sort(sj.begin(), sj.end(), [](const ShadowJob* x, const ShadowJob* y) { return x->src < y->src; });
+  std::vector<UpdateJob> jobs;
+  int blocks = 0;
+  auto emit = [&](int64_t off, int64_t len, const ShadowJob* sh, int seg) {
+    UpdateJob u;
+    u.off = off; u.len = len; u.sh = sh ? sh->dst : nullptr;
+    u.C = sh ? sh->C : 0; u.blk_stride = sh ? sh->blk_stride : 0; u.blk_off = sh ? sh->blk_off : 0;
+    u.seg = seg; u.blk0 = blocks; u.vec = (off % 4 == 0 && len % 4 == 0) ? 1 : 0;
+    blocks += (int)((len + kUpdateChunk - 1) / kUpdateChunk);
+    jobs.push_back(u);
+    return !sh || (u.vec && u.C % 4 == 0);
+  };
+  int64_t covered = 0;
+  for (int si : order) {
+    const AdamSeg& sg = a.seg[si];
+    if (sg.off != covered)
+      return eng_fail(e, ANE_ERR_STATE, "storiesane flush: parameter groups leave [%lld, %lld) uncovered",
+                      (long long)covered, (long long)sg.off);
+    int64_t cur = sg.off;
+    const int64_t end = sg.off + sg.len;
+    for (const ShadowJob* j : sj) {
+      const int64_t jo = j->src - e->P, je = jo + (int64_t)j->R * j->C;
+      if (je <= sg.off || jo >= end) continue;
+      if (jo < sg.off || je > end)
+        return eng_fail(e, ANE_ERR_STATE, "storiesane flush: a shadowed matrix straddles a parameter group");
+      if (cur < jo && !emit(cur, jo - cur, nullptr, si)) return eng_fail(e, ANE_ERR_STATE, "storiesane flush: job");
+      if (!emit(jo, je - jo, j, si))
+        return eng_fail(e, ANE_ERR_STATE, "storiesane flush: shadowed matrix not 16-byte aligned");
+      cur = je;
+    }
+    if (cur < end && !emit(cur, end - cur, nullptr, si)) return eng_fail(e, ANE_ERR_STATE, "storiesane flush: job");
+    covered = end;
+  }
+  if (covered != e->pm.total)
+    return eng_fail(e, ANE_ERR_STATE, "storiesane flush: parameter groups cover %lld of %lld",
+                    (long long)covered, (long long)e->pm.total);
+  if ((int)jobs.size() > e->upd_cap) {
+    HIPCHK(op, dalloc(e, &e->upd_jobs, jobs.size()));
+    e->upd_cap = (int)jobs.size();
+  }
+  HIPCHK(op, hipStreamSynchronize(e->stream));  // no launch still reads the old table
+  HIPCHK(op, hipMemcpy(e->upd_jobs, jobs.data(), jobs.size() * sizeof(UpdateJob), hipMemcpyHostToDevice));
+  e->n_upd_jobs = (int)jobs.size();
+  e->n_upd_blocks = blocks;
+  e->upd_sig = sig;
+  return ANE_OK;
+}
+
 int refresh_shadows(ane_engine* e) {
   const char* op = "refresh weights";
+  // an asynchronous refresh still reading the plain shadows and the table
+  if (e->refresh_pending) HIPCHK(op, hipEventSynchronize(e->refresh_ev[1]));
   if (!e->shadow_jobs || e->shadow_jobs_t != (e->embed_t != nullptr)) {
     int rc = build_shadow_jobs(e);
     if (rc) return rc;
@@ -792,8 +870,8 @@ static int fwd_loss(ane_engine* e, int nseq) {
 
 static int finish_loss(ane_engine* e, int nseq, float* loss_per_seq, float* mean_loss) {
   const char* op = "eval loss";
-  std::vector<float> ls(nseq);
-  HIPCHK(op, hipMemcpyAsync(ls.data(), e->loss_seq, (size_t)nseq * 4, hipMemcpyDeviceToHost, e->stream));
+  const float* ls = e->loss_host;
+  HIPCHK(op, hipMemcpyAsync(e->loss_host, e->loss_seq, (size_t)nseq * 4, hipMemcpyDeviceToHost, e->stream));
   HIPCHK(op, hipStreamSynchronize(e->stream));
   double tot = 0;
   for (int b = 0; b < nseq; b++) {
@@ -825,8 +903,12 @@ int load_windows(ane_engine* e, const uint64_t* positions, int nseq) {
     if (positions[b] + S + 1 > (uint64_t)e->ndata)
       return eng_fail(e, ANE_ERR_ARG, "storiesane eval loss: window %d at %llu exceeds %lld tokens", b,
                       (unsigned long long)positions[b], (long long)e->ndata);
-  HIPCHK(op, hipMemcpyAsync(e->pos_d, positions, (size_t)nseq * 8, hipMemcpyHostToDevice, e->stream));
-  HIPCHK(op, gather_windows(e->tok, e->tgt, e->data, e->pos_d, nseq, e->cfg.seq, e->stream));
+  if (nseq <= kArgWindows) {
+    HIPCHK(op, gather_windows_args(e->tok, e->tgt, e->data, positions, nseq, e->cfg.seq, e->stream));
+  } else {
+    HIPCHK(op, hipMemcpyAsync(e->pos_d, positions, (size_t)nseq * 8, hipMemcpyHostToDevice, e->stream));
+    HIPCHK(op, gather_windows(e->tok, e->tgt, e->data, e->pos_d, nseq, e->cfg.seq, e->stream));
+  }
   return ANE_OK;
 }
 

@@ -131,6 +131,14 @@ struct ane_engine {
   // shadow refresh job table (device), rebuilt when the transposes appear
   ane::ShadowJob* shadow_jobs = nullptr;
   int n_shadow_jobs = 0, n_shadow_tiles = 0;
+  std::vector<ane::ShadowJob> shadow_jobs_h;  // host copy of the table
+  // the flush's fused AdamW + shadow update (ANE_FUSED_ADAM=0: AdamW, then
+  // the fp32 -> fp16 refresh, then a fill of the gradient): job table on the
+  // device, built for the segment list in upd_sig
+  bool fused_adam = true;
+  ane::UpdateJob* upd_jobs = nullptr;
+  int n_upd_jobs = 0, n_upd_blocks = 0, upd_cap = 0;
+  std::vector<int64_t> upd_sig;
   bool shadow_jobs_t = false;
   float* rope_cos = nullptr;
   float* rope_sin = nullptr;
@@ -167,6 +175,12 @@ struct ane_engine {
   bool dw_async = true;
   bool bwd_prefetch = true;  // ANE_BWD_PREFETCH=0: no prefetch of the backward's GEMM operands
   hipStream_t dw_stream = nullptr;
+  // asynchronous weight refresh of an accumulate-mode flush (the transposed
+  // shadows, on the dW stream; startAsyncRefresh, ane/runtime.go:71-83): the
+  // next backward waits for refresh_ev[1] on the GPU, Flush on the host,
+  // returning its duration (waitAsyncRefresh, ane/runtime.go:85-94)
+  hipEvent_t refresh_ev[2] = {};
+  bool refresh_pending = false;
   std::vector<hipEvent_t> xev;  // fork / join events (timing disabled), reused per call
   size_t xev_next = 0;
   int fwd_rr_nparts = 0;
@@ -176,6 +190,7 @@ struct ane_engine {
   float* lse = nullptr;
   float* tok_loss = nullptr;
   float* loss_seq = nullptr;
+  float* loss_host = nullptr;  // pinned copy of loss_seq: the read-back is one queued copy and one wait
   float* logits = nullptr;  // [V, S]
 
   // host-side engine state (ane/engine.go:76-175)
@@ -240,6 +255,8 @@ hipError_t eng_gemm(ane_engine* e, int cls, const ane::half_t* A, int lda, bool 
                     bool bt, int M, int N, int K, int epi, const ane::EpiParams& p, int bm = 0, int bn = 0,
                     bool side = false);
 int refresh_shadows(ane_engine* e);
+// the update job table of adam_fused_update for the segments of a (cached)
+int ensure_update_jobs(ane_engine* e, const ane::AdamArgs& a);
 int forward_body(ane_engine* e, int nseq, int train, bool defer_norm = false);
 void drop_fwd_graph(ane_engine* e);
 template <class T>

@@ -56,6 +56,18 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   return chunk ^ ((row ^ (row >> 3)) & 7);
 }
 
+// Streaming 16-byte accesses (nontemporal: the data is not expected back in
+// the caches soon).  Measured on the flush's update pass: 700 -> 625 us.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ld_nt_f4(const float* p) {
+  const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+  return make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void st_nt_f4(float* p, const float4& x) {
+  const f32x4 v = {x.x, x.y, x.z, x.w};
+  __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+}
+
 __device__ __forceinline__ half8 ld_h8(const half_t* p) {
   return *reinterpret_cast<const half8*>(p);
 }

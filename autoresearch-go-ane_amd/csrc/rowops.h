@@ -49,6 +49,14 @@ hipError_t rmsnorm_f16(half_t* out, const float* x, const float* xsub, const flo
 // tok[b*S + t] = data[pos[b] + t]; tgt[b*S + t] = data[pos[b] + t + 1]   ane/engine.go:403-404
 hipError_t gather_windows(uint16_t* tok, uint16_t* tgt, const uint16_t* data, const uint64_t* pos, int nseq,
                           int S, hipStream_t s);
+// the same with host-side window starts passed as kernel arguments (nseq <=
+// kArgWindows): no copy, so nothing waits on the host before the launch
+constexpr int kArgWindows = 64;
+struct WindowStarts {
+  uint64_t p[kArgWindows];
+};
+hipError_t gather_windows_args(uint16_t* tok, uint16_t* tgt, const uint16_t* data, const uint64_t* pos_host, int nseq,
+                               int S, hipStream_t s);
 
 // Merges the classifier's per-block (max, sumexp) partials into per-token
 // log-sum-exp and the per-sequence mean cross-entropy over valid targets

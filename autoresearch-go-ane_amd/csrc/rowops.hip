@@ -160,6 +160,18 @@ __global__ void gather_kernel(uint16_t* tok, uint16_t* tgt, const uint16_t* data
   tgt[i] = data[p + 1];
 }
 
+// The same with the window starts passed by value (no host-to-device copy
+// before the launch).
+__global__ void gather_arg_kernel(uint16_t* tok, uint16_t* tgt, const uint16_t* data, WindowStarts pos, int nseq,
+                                  int S) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nseq * S) return;
+  const int b = i / S, t = i % S;
+  const uint64_t p = pos.p[b] + (uint64_t)t;
+  tok[i] = data[p];
+  tgt[i] = data[p + 1];
+}
+
 // Per token: merge the partials with a running (max, sum) pair; 4 lanes
 // split the partials of one token and combine with two xor-shuffles.
 __global__ __launch_bounds__(256) void ce_token_kernel(float* lse_out, float* tok_loss, const float2* partial,
@@ -302,6 +314,16 @@ hipError_t gather_windows(uint16_t* tok, uint16_t* tgt, const uint16_t* data, co
                           hipStream_t s) {
   const int n = nseq * S;
   hipLaunchKernelGGL(gather_kernel, dim3((n + 255) / 256), dim3(256), 0, s, tok, tgt, data, pos, nseq, S);
+  return hipGetLastError();
+}
+
+hipError_t gather_windows_args(uint16_t* tok, uint16_t* tgt, const uint16_t* data, const uint64_t* pos_host, int nseq,
+                               int S, hipStream_t s) {
+  if (nseq <= 0 || nseq > kArgWindows) return hipErrorInvalidValue;
+  WindowStarts w;
+  for (int b = 0; b < nseq; b++) w.p[b] = pos_host[b];
+  const int n = nseq * S;
+  hipLaunchKernelGGL(gather_arg_kernel, dim3((n + 255) / 256), dim3(256), 0, s, tok, tgt, data, w, nseq, S);
   return hipGetLastError();
 }
 

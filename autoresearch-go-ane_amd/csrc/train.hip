@@ -111,6 +111,8 @@ int ensure_train(ane_engine* e, const char* op) {
   if (e->dw_async && e->tr_dw) {
     // default priority, like the main stream
     if (!e->dw_stream) HIPCHK(op, hipStreamCreateWithFlags(&e->dw_stream, hipStreamNonBlocking));
+    for (hipEvent_t& ev : e->refresh_ev)
+      if (!ev) HIPCHK(op, hipEventCreate(&ev));
     HIPCHK(op, dalloc(e, &tb.splitk_ws2, tb.splitk_cap));
     HIPCHK(op, dalloc(e, &tb.dcur_h2, T * D));
     HIPCHK(op, dalloc(e, &tb.dh13_2, T * KH));
@@ -251,6 +253,12 @@ int backward_body(ane_engine* e, int nseq, bool async) {
 
   int rc = forward_body(e, nseq, 1);
   if (rc) return rc;
+  // the transposed shadows of an asynchronous refresh (waitAsyncRefresh at
+  // the next step, ane/train_full.go:370-372): waited for on the GPU
+  if (e->refresh_pending) {
+    HIPCHK(op, hipStreamWaitEvent(st, e->refresh_ev[1], 0));
+    e->refresh_pending = false;
+  }
 
   // ---- final head (runFinalHead, ane/train_full.go:480-558) ----------------
   (void)hipEventRecord(e->step_ev[ane_engine::EV_HEAD0], st);
@@ -555,16 +563,40 @@ int flush_pending(ane_engine* e) {
     add_seg(a, pm.resid, 2 * L, lambda_lr, 0.f, O.lambda_beta1, O.lambda_beta2, l1, l2, 0);
   }
   if (a.nseg > kMaxAdamSegs) return eng_fail(e, ANE_ERR_ARG, "storiesane flush: too many parameter groups");
-  (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM0], st);
-  HIPCHK(op, adam_update(a, st));
-  (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM1], st);
-  // the fp16 shadows the next forward reads: the weight refresh
+  // the fp16 shadows the next forward and backward read: the weight refresh
   // (refreshANERuntimeForWeights, ane/runtime.go:25-69)
-  phase_begin(e, PH_REFRESH);
-  int rc = refresh_shadows(e);
-  phase_end(e);
-  if (rc) return rc;
-  HIPCHK(op, fill_f32(tb.G, (size_t)pm.total, 0.f, st));
+  if (e->fused_adam && e->shadow_jobs && e->shadow_jobs_t) {
+    // one pass: AdamW, the gradient zeroed, the plain shadows; then the
+    // refresh proper is the transposed shadows, read from the plain ones
+    int rc = ensure_update_jobs(e, a);
+    if (rc) return rc;
+    (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM0], st);
+    HIPCHK(op, adam_fused_update(a, e->upd_jobs, e->n_upd_jobs, e->n_upd_blocks, st));
+    (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM1], st);
+    if (e->opt.accum_steps > 1 && e->dw_stream && e->refresh_ev[1]) {
+      // accumulate mode: the refresh runs asynchronously (flushPending,
+      // ane/engine.go:674-677), beside the next step's forward, which
+      // reads only the plain shadows
+      HIPCHK(op, stream_after(e, e->dw_stream, st));
+      HIPCHK(op, hipEventRecord(e->refresh_ev[0], e->dw_stream));
+      HIPCHK(op, shadow_transpose(e->shadow_jobs, e->n_shadow_jobs, e->n_shadow_tiles, e->dw_stream));
+      HIPCHK(op, hipEventRecord(e->refresh_ev[1], e->dw_stream));
+      e->refresh_pending = true;
+    } else {
+      phase_begin(e, PH_REFRESH);
+      HIPCHK(op, shadow_transpose(e->shadow_jobs, e->n_shadow_jobs, e->n_shadow_tiles, st));
+      phase_end(e);
+    }
+  } else {
+    (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM0], st);
+    HIPCHK(op, adam_update(a, st));
+    (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM1], st);
+    phase_begin(e, PH_REFRESH);
+    int rc = refresh_shadows(e);
+    phase_end(e);
+    if (rc) return rc;
+    HIPCHK(op, fill_f32(tb.G, (size_t)pm.total, 0.f, st));
+  }
   e->state.pending_steps = 0;
   e->state.cum_batches++;
   e->flushed = true;
@@ -575,12 +607,11 @@ int flush_pending(ane_engine* e) {
 // (forward, backward, weight-gradient GEMMs, update) had finished
 int read_losses(ane_engine* e, int nseq, float* per, double* mean, double* wait_s = nullptr) {
   const char* op = "step";
-  std::vector<float> ls(nseq);
+  const float* ls = e->loss_host;
+  HIPCHK(op, hipMemcpyAsync(e->loss_host, e->loss_seq, (size_t)nseq * 4, hipMemcpyDeviceToHost, e->stream));
   const double t0 = now_s();
   HIPCHK(op, hipStreamSynchronize(e->stream));
   if (wait_s) *wait_s = now_s() - t0;
-  HIPCHK(op, hipMemcpyAsync(ls.data(), e->loss_seq, (size_t)nseq * 4, hipMemcpyDeviceToHost, e->stream));
-  HIPCHK(op, hipStreamSynchronize(e->stream));
   double tot = 0;
   for (int b = 0; b < nseq; b++) {
     tot += ls[b];
@@ -696,7 +727,14 @@ extern "C" int ane_flush(ane_engine* e, int64_t* ns) {
   HIPCHK("flush", hipStreamSynchronize(e->stream));
   double ph[PH_COUNT];
   phase_sum(e, ph);
-  const int64_t refresh_ns = (int64_t)(ph[PH_REFRESH] * 1e6);
+  int64_t refresh_ns = (int64_t)(ph[PH_REFRESH] * 1e6);
+  if (e->refresh_pending) {  // waitAsyncRefresh (ane/engine.go:489)
+    HIPCHK("flush", hipEventSynchronize(e->refresh_ev[1]));
+    float ms = 0.f;
+    HIPCHK("flush", hipEventElapsedTime(&ms, e->refresh_ev[0], e->refresh_ev[1]));
+    refresh_ns = (int64_t)((double)ms * 1e6);
+    e->refresh_pending = false;
+  }
   if (refresh_ns > 0) {
     e->state.cum_train_ms += (double)refresh_ns / 1e6;
     e->state.cum_wall_ms = (now_s() - e->start_s) * 1e3;

@@ -105,7 +105,7 @@ struct AdamSeg {
 constexpr int kMaxAdamSegs = 64;
 struct AdamArgs {
   float* w;
-  const float* g;
+  float* g;  // read by adam_update; read and zeroed by adam_fused_update
   float* m;
   float* v;
   const double* sumsq;  // device: sum of squares of the raw clip-segment grads
@@ -114,5 +114,24 @@ struct AdamArgs {
   AdamSeg seg[kMaxAdamSegs];
 };
 hipError_t adam_update(const AdamArgs& a, hipStream_t s);
+
+// The flush's fused update: the AdamW of adam_update (same arithmetic), the
+// gradient zeroed for the next accumulation, and the fp16 shadow of every
+// updated weight matrix written (rows placed as ShadowJob's blk_stride /
+// blk_off mapping), in one pass.  Jobs are the segments cut where a matrix
+// with a shadow starts or ends; a block updates kUpdateChunk elements of one
+// job (4 per thread and pass when vec: offset and length multiples of 4).
+constexpr int kUpdateChunk = 4096;
+struct UpdateJob {
+  int64_t off, len;
+  half_t* sh;                  // plain fp16 shadow, [rows][C] (null: none)
+  int C, blk_stride, blk_off;  // shadow row of source row r: (r / 32) * blk_stride + blk_off + r % 32
+  int seg;                     // AdamArgs segment: hyperparameters
+  int blk0;                    // first block of the job
+  int vec;
+};
+hipError_t adam_fused_update(const AdamArgs& a, const UpdateJob* jobs_dev, int njobs, int nblocks, hipStream_t s);
+// the transposed shadows (dst_t) of every job, read from the plain fp16 shadows
+hipError_t shadow_transpose(const ShadowJob* jobs_dev, int njobs, int ntiles, hipStream_t s);
 
 }  // namespace ane

@@ -287,15 +287,14 @@ __global__ __launch_bounds__(256) void sumsq_kernel(double* part, const float* g
   __shared__ double sh[256];
   double acc = 0.0, acc2 = 0.0;
   const size_t n4 = n / 4, stride = (size_t)gridDim.x * 256;
-  const float4* g4 = reinterpret_cast<const float4*>(g);
   size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
   for (; i + stride < n4; i += 2 * stride) {
-    const float4 a = g4[i], b = g4[i + stride];
+    const float4 a = ld_nt_f4(g + 4 * i), b = ld_nt_f4(g + 4 * (i + stride));
     acc += (double)a.x * a.x + (double)a.y * a.y + (double)a.z * a.z + (double)a.w * a.w;
     acc2 += (double)b.x * b.x + (double)b.y * b.y + (double)b.z * b.z + (double)b.w * b.w;
   }
   if (i < n4) {
-    const float4 a = g4[i];
+    const float4 a = ld_nt_f4(g + 4 * i);
     acc += (double)a.x * a.x + (double)a.y * a.y + (double)a.z * a.z + (double)a.w * a.w;
   }
   if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
@@ -351,6 +350,76 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
   }
 }
 
+// One block per kUpdateChunk elements of one job (binary search over blk0).
+__global__ __launch_bounds__(256) void adam_fused_kernel(AdamArgs a, const UpdateJob* jobs, int njobs) {
+  int lo = 0, hi = njobs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (jobs[mid].blk0 <= (int)blockIdx.x) lo = mid;
+    else hi = mid - 1;
+  }
+  const UpdateJob jb = jobs[lo];
+  const AdamSeg& sg = a.seg[jb.seg];
+  float cf = 1.f;
+  if (sg.clip && a.clip > 0.f) {
+    const double n2 = *a.sumsq * (double)a.gscale * (double)a.gscale;
+    if (n2 > 0.0) {
+      const float norm = (float)sqrt(n2);
+      if (norm > a.clip) cf = a.clip / norm;
+    }
+  }
+  const float gs = a.gscale;
+  // the per-element update of adam_kernel
+  auto upd = [&](float g, float& m, float& v, float& w) {
+    g = g * gs;
+    g *= cf;
+    m = sg.b1 * m + (1.f - sg.b1) * g;
+    v = sg.b2 * v + (1.f - sg.b2) * g * g;
+    const float mh = m * sg.i1, vh = v * sg.i2;
+    float u = mh / (sqrtf(vh) + a.eps);
+    if (sg.wd != 0.f) u += sg.wd * w;
+    w -= sg.lr * u;
+  };
+  const int64_t base = (int64_t)((int)blockIdx.x - jb.blk0) * kUpdateChunk;
+  if (jb.vec) {
+#pragma unroll
+    for (int u = 0; u < kUpdateChunk / 1024; u++) {
+      const int64_t i = base + (int64_t)(u * 256 + (int)threadIdx.x) * 4;
+      if (i >= jb.len) break;
+      const int64_t k = jb.off + i;
+      const float4 g4 = ld_nt_f4(a.g + k);
+      float4 m4 = ld_nt_f4(a.m + k), v4 = ld_nt_f4(a.v + k), w4 = ld_nt_f4(a.w + k);
+      upd(g4.x, m4.x, v4.x, w4.x);
+      upd(g4.y, m4.y, v4.y, w4.y);
+      upd(g4.z, m4.z, v4.z, w4.z);
+      upd(g4.w, m4.w, v4.w, w4.w);
+      st_nt_f4(a.m + k, m4);
+      st_nt_f4(a.v + k, v4);
+      st_nt_f4(a.w + k, w4);
+      st_nt_f4(a.g + k, make_float4(0.f, 0.f, 0.f, 0.f));
+      if (jb.sh) {
+        const int64_t r = i / jb.C;
+        const int c = (int)(i - r * jb.C);
+        const int64_t sr = (r >> 5) * jb.blk_stride + jb.blk_off + (r & 31);
+        half4 h;
+        h[0] = (half_t)w4.x; h[1] = (half_t)w4.y; h[2] = (half_t)w4.z; h[3] = (half_t)w4.w;
+        *reinterpret_cast<half4*>(jb.sh + sr * jb.C + c) = h;
+      }
+    }
+  } else {
+    const int64_t end = base + kUpdateChunk < jb.len ? base + kUpdateChunk : jb.len;
+    for (int64_t i = base + threadIdx.x; i < end; i += 256) {
+      const int64_t k = jb.off + i;
+      float m = a.m[k], v = a.v[k], w = a.w[k];
+      upd(a.g[k], m, v, w);
+      a.m[k] = m;
+      a.v[k] = v;
+      a.w[k] = w;
+      a.g[k] = 0.f;
+    }
+  }
+}
+
 inline int flat_grid(size_t n, int cap = 4096) {
   size_t g = (n + 255) / 256;
   return (int)(g > (size_t)cap ? cap : (g == 0 ? 1 : g));
@@ -394,25 +463,40 @@ __device__ __forceinline__ int shadow_row(const ShadowJob& jb, int r) {
   return (r >> 5) * jb.blk_stride + jb.blk_off + (r & 31);
 }
 
-// One 64x64 tile of one job per block; jobs are sorted by tile0.
+// One 64x64 tile of one job per block; jobs are sorted by tile0.  FROM_PLAIN:
+// only the transposed shadow, from the plain fp16 shadow rows.
+template <bool FROM_PLAIN>
 __global__ __launch_bounds__(256) void shadow_kernel(const ShadowJob* jobs, int njobs) {
   __shared__ __attribute__((aligned(16))) half_t tile[64 * kTp];
-  int j = 0;
-  for (int k = 1; k < njobs; k++)
-    if (jobs[k].tile0 <= (int)blockIdx.x) j = k;
+  int j = 0, hi = njobs - 1;  // the last job with tile0 <= blockIdx.x
+  while (j < hi) {
+    const int mid = (j + hi + 1) >> 1;
+    if (jobs[mid].tile0 <= (int)blockIdx.x) j = mid;
+    else hi = mid - 1;
+  }
   const ShadowJob jb = jobs[j];
   const int t = (int)blockIdx.x - jb.tile0;
   const int tiles_c = jb.C >> 6;
   const int r0 = (t / tiles_c) * 64, c0 = (t % tiles_c) * 64;
   const int tid = threadIdx.x;
+  if constexpr (FROM_PLAIN) {
+    if (!jb.dst_t) return;  // block-uniform
 #pragma unroll
-  for (int p = 0; p < 4; p++) {
-    const int idx = tid + 256 * p, row = idx >> 4, ch = idx & 15;
-    const float4 v = *reinterpret_cast<const float4*>(jb.src + (size_t)(r0 + row) * jb.C + c0 + ch * 4);
-    half4 h;
-    h[0] = (half_t)v.x; h[1] = (half_t)v.y; h[2] = (half_t)v.z; h[3] = (half_t)v.w;
-    *reinterpret_cast<half4*>(jb.dst + (size_t)shadow_row(jb, r0 + row) * jb.C + c0 + ch * 4) = h;
-    *reinterpret_cast<half4*>(tile + row * kTp + ch * 4) = h;
+    for (int p = 0; p < 2; p++) {  // 16-byte loads: 8 per 64-half row
+      const int idx = tid + 256 * p, row = idx >> 3, ch = idx & 7;
+      const half8 h = ld_h8(jb.dst + (size_t)shadow_row(jb, r0 + row) * jb.C + c0 + ch * 8);
+      *reinterpret_cast<half8*>(tile + row * kTp + ch * 8) = h;
+    }
+  } else {
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const int idx = tid + 256 * p, row = idx >> 4, ch = idx & 15;
+      const float4 v = *reinterpret_cast<const float4*>(jb.src + (size_t)(r0 + row) * jb.C + c0 + ch * 4);
+      half4 h;
+      h[0] = (half_t)v.x; h[1] = (half_t)v.y; h[2] = (half_t)v.z; h[3] = (half_t)v.w;
+      *reinterpret_cast<half4*>(jb.dst + (size_t)shadow_row(jb, r0 + row) * jb.C + c0 + ch * 4) = h;
+      *reinterpret_cast<half4*>(tile + row * kTp + ch * 4) = h;
+    }
   }
   if (!jb.dst_t) return;  // block-uniform
   __syncthreads();
@@ -504,7 +588,19 @@ hipError_t transpose_h(half_t* out, const half_t* in, int R, int C, int ldi, int
 
 hipError_t shadow_refresh(const ShadowJob* jobs_dev, int njobs, int ntiles, hipStream_t s) {
   if (njobs <= 0 || ntiles <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(shadow_kernel, dim3(ntiles), dim3(256), 0, s, jobs_dev, njobs);
+  hipLaunchKernelGGL(shadow_kernel<false>, dim3(ntiles), dim3(256), 0, s, jobs_dev, njobs);
+  return hipGetLastError();
+}
+
+hipError_t shadow_transpose(const ShadowJob* jobs_dev, int njobs, int ntiles, hipStream_t s) {
+  if (njobs <= 0 || ntiles <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(shadow_kernel<true>, dim3(ntiles), dim3(256), 0, s, jobs_dev, njobs);
+  return hipGetLastError();
+}
+
+hipError_t adam_fused_update(const AdamArgs& a, const UpdateJob* jobs_dev, int njobs, int nblocks, hipStream_t s) {
+  if (a.nseg <= 0 || a.nseg > kMaxAdamSegs || njobs <= 0 || nblocks <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(adam_fused_kernel, dim3(nblocks), dim3(256), 0, s, a, jobs_dev, njobs);
   return hipGetLastError();
 }
 
