@@ -42,6 +42,8 @@ enum Epi : int {
 };
 // Partial sums of squares a consumer combines (rr_nparts <= kRrMaxParts).
 constexpr int kRrMaxParts = 16;
+// split-K: most K slices of one GEMM (the reduce keeps one load per slice in flight)
+constexpr int kMaxSplits = 16;
 __host__ __device__ constexpr bool epi_rr(int epi) {
   return epi == EPI_STORE_H_RR || epi == EPI_SWIGLU_RR || epi == EPI_CE_RR;
 }

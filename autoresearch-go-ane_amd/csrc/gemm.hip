@@ -505,8 +505,9 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
     }
   } else if constexpr (EPI == EPI_DLOGITS) {
     // d = (softmax - onehot) * colscale[n], times (1 - tanh^2) under softcap.
-    // C2 (optional): the same values transposed, [N, ldc2]; registers
-    // 4q .. 4q+3 hold 4 consecutive rows, stored as one 8-byte chunk.
+    // C [M, ldc] and C2 (the same values transposed, [N, ldc2]) are each
+    // optional; in C2, registers 4q .. 4q+3 hold 4 consecutive rows, stored
+    // as one 8-byte chunk.
     half_t* C = (half_t*)e.C;
     half_t* C2 = (half_t*)e.C2;
     constexpr float kLog2e = 1.4426950408889634f;
@@ -532,7 +533,7 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
           float d = __builtin_amdgcn_exp2f(__builtin_fmaf(v, kLog2e, -lsel)) - (mo == tsel ? 1.f : 0.f);
           d = mo < vend ? d * cs * dsc : 0.f;
           hv[r] = (half_t)d;
-          C[(size_t)ROW(i, r) * e.ldc + n] = hv[r];
+          if (C) C[(size_t)ROW(i, r) * e.ldc + n] = hv[r];
         }
         if (C2) {
 #pragma unroll
@@ -974,11 +975,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* ws, int
   const size_t i4 = ((size_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (i4 >= MN) return;
   const int m = (int)(i4 / N), n = (int)(i4 % N);
-  float4 v = *reinterpret_cast<const float4*>(ws + i4);
-  for (int s = 1; s < splits; s++) {
-    const float4 w = *reinterpret_cast<const float4*>(ws + (size_t)s * MN + i4);
-    v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
-  }
+  // every slice's load in flight at once (the workspace is not read again),
+  // then the sum in split order
+  float4 w[kMaxSplits];
+#pragma unroll
+  for (int s = 0; s < kMaxSplits; s++)
+    if (s < splits) w[s] = ld_nt_f4(ws + (size_t)s * MN + i4);
+  float4 v = w[0];
+#pragma unroll
+  for (int s = 1; s < kMaxSplits; s++)
+    if (s < splits) {
+      v.x += w[s].x; v.y += w[s].y; v.z += w[s].z; v.w += w[s].w;
+    }
   float o[4] = {v.x * e.scale, v.y * e.scale, v.z * e.scale, v.w * e.scale};
   if constexpr (EPI == EPI_STORE_H) {
     half4 h;
@@ -1267,7 +1275,8 @@ static hipError_t splitk_reduce(const GemmArgs& g, const EpiParams& e, hipStream
 
 hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t s, int bm, int bn, int nw,
                     int ns) {
-  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0 || g.splits < 1) return hipErrorInvalidValue;
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0 || g.splits < 1 || g.splits > kMaxSplits)
+    return hipErrorInvalidValue;
   if (epi == EPI_RESID_NORM &&
       (!e.R || !e.C2 || !e.gain || !e.ssq_part || e.ssq_ld < g.M || g.splits != 1 || g.grp || g.a_t || g.b_t))
     return hipErrorInvalidValue;

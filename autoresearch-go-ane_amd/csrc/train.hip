@@ -265,8 +265,11 @@ int backward_body(ane_engine* e, int nseq, bool async) {
   rc = head_loss(e, nseq, tb.colscale, e->opt.loss_scale * kDlScale);
   if (rc) return rc;
   {
+    // token-major dl_t for the dy GEMM (K = vocab); the vocab-major copy only
+    // for the K-major embedding-gradient GEMM of ANE_TR_DW=0
     EpiParams p;
-    p.C = tb.dl; p.ldc = T; p.C2 = tb.dl_t; p.ldc2 = V; p.targets = e->tgt; p.lse = e->lse; p.colscale = tb.colscale;
+    p.C = e->tr_dw ? nullptr : tb.dl; p.ldc = T; p.C2 = tb.dl_t; p.ldc2 = V;
+    p.targets = e->tgt; p.lse = e->lse; p.colscale = tb.colscale;
     p.softcap = !llama; p.cap = 15.f; p.vocab = V;
     HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, T, D, EPI_DLOGITS, p));
   }
@@ -280,8 +283,8 @@ int backward_body(ane_engine* e, int nseq, bool async) {
     EpiParams p;
     p.C = G + pm.embed; p.ldc = D; p.scale = 1.f / kDlScale; p.accumulate = 1;
     phase_begin(e, PH_EMBED_GRAD, ds);
-    if (e->tr_dw) {  // dl is vocab-major (K-major); xh token-major read through transposing LDS loads
-      HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, e->xh, D, true, V, D, T, EPI_STORE_F, p, 0, 0, async));
+    if (e->tr_dw) {  // dl_t and xh token-major, both read through transposing LDS loads
+      HIPCHK(op, eng_gemm(e, 7, tb.dl_t, V, true, e->xh, D, true, V, D, T, EPI_STORE_F, p, 0, 0, async));
     } else {
       HIPCHK(op, transpose_h(tb.op_b, e->xh, T, D, D, T, st));
       HIPCHK(op, eng_gemm(e, 7, tb.dl, T, false, tb.op_b, T, false, V, D, T, EPI_STORE_F, p));
