@@ -91,6 +91,10 @@ struct TrainBufs {
   float* ve_dx = nullptr;
   ane::half_t* dgp = nullptr;
   float* dgain_part = nullptr;
+  // llama2: per-layer gain-gradient partials [2 L][nblocks][D] (FFN norm
+  // 2 l, attention norm 2 l + 1), so their reductions can run on the dW
+  // stream while the main stream's next norms write other partials
+  float* dgain_parts = nullptr;
   double* dot_part = nullptr;
   double* sumsq = nullptr;
   double* sumsq_part = nullptr;

@@ -132,6 +132,7 @@ int ensure_train(ane_engine* e, const char* op) {
   HIPCHK(op, dalloc(e, &tb.colscale, T));
   const size_t nblk = (size_t)norm_bwd_blocks((int)T);
   HIPCHK(op, dalloc(e, &tb.dgain_part, nblk * D));
+  if (llama) HIPCHK(op, dalloc(e, &tb.dgain_parts, 2 * (size_t)c.layers * nblk * D));
   HIPCHK(op, dalloc(e, &tb.dot_part, (nblk > 256 ? nblk : 256) * 2));
   HIPCHK(op, dalloc(e, &tb.sumsq, 1));
   HIPCHK(op, dalloc(e, &tb.sumsq_part, kSumsqBlocks));
@@ -234,6 +235,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
   // dcur_h(l) is the dY that enters layer l from above
   auto by_parity = [&](half_t* a, half_t* b, int l) { return async && (l & 1) ? b : a; };
   auto dcur_h_of = [&](int l) { return by_parity(tb.dcur_h, tb.dcur_h2, l); };
+  auto gpart = [&](int i) { return tb.dgain_parts + (size_t)i * nblk * D; };
 
   // Cold GEMM operands streamed into the caches by a prefetch kernel on the
   // dW stream at each fork: the weight shadow of the dX GEMM that the main
@@ -318,6 +320,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
   // dWo (after the FFN norm backward), dWqkv (after the attention backward);
   // above_done marks the end of the layer above's dW work
   hipEvent_t above_done = nullptr;
+  int att_gain_layer = -1;
   for (int l = L - 1; l >= 0; l--) {
     const LayerOff& o = pm.L[l];
     const LayerShadow& s = e->ls[l];
@@ -338,6 +341,12 @@ int backward_body(ane_engine* e, int nseq, bool async) {
     }
     if (async) HIPCHK(op, stream_after(e, ds, st));  // dcur_in, dh13 written
     HIPCHK(op, prefetch(ds, {{s.w13_t, (size_t)KH * D * 2}, {A.xn2, TD2}, {A.gate, (size_t)T * H * 2}}));
+    if (att_gain_layer >= 0) {  // the attention-norm gain of the layer above
+      phase_begin(e, PH_RMS_DW, ds);
+      HIPCHK(op, reduce_partials_add(G + pm.L[att_gain_layer].g_att, gpart(2 * att_gain_layer + 1), nblk, D, ds));
+      phase_end(e, ds);
+      att_gain_layer = -1;
+    }
     {  // dW2 += dOut gate^T
       EpiParams p;
       p.C = G + o.w2; p.ldc = H; p.accumulate = 1;
@@ -363,17 +372,17 @@ int backward_body(ane_engine* e, int nseq, bool async) {
       a.dy = tb.dxn; a.x = A.x2; a.T = T; a.D = D; a.addend = tb.dcur; a.alpha_p = rl_p;
       a.out = tb.dx2; a.out_h = dx2_h;
       if (llama) {
-        a.gain = P + o.g_ffn; a.dgain_part = tb.dgain_part;
+        a.gain = P + o.g_ffn; a.dgain_part = gpart(2 * l);
       } else {
         a.lam_x = A.x2; a.lam_x0 = e->x0; a.lam_part = tb.dot_part; a.gx0 = tb.gx0; a.xl_p = xl_p;
       }
       HIPCHK(op, norm_bwd(a, st));
-      if (async) HIPCHK(op, stream_after(e, ds, st));  // dx2_h written
+      if (async) HIPCHK(op, stream_after(e, ds, st));  // dx2_h and the FFN gain partials written
       HIPCHK(op, prefetch(ds, {{s.wo_t, (size_t)D * D * 2}, {A.att, TD2}}));
       if (llama) {
-        phase_begin(e, PH_RMS_DW);
-        HIPCHK(op, reduce_partials_add(G + o.g_ffn, tb.dgain_part, nblk, D, st));
-        phase_end(e);
+        phase_begin(e, PH_RMS_DW, ds);
+        HIPCHK(op, reduce_partials_add(G + o.g_ffn, gpart(2 * l), nblk, D, ds));
+        phase_end(e, ds);
       } else
         HIPCHK(op, reduce_dots_add(G + pm.resid + l, G + pm.x0l + l, tb.dot_part, nblk, 1.f, st));
     }
@@ -450,16 +459,18 @@ int backward_body(ane_engine* e, int nseq, bool async) {
       a.dy = tb.dxn; a.x = A.xin; a.T = T; a.D = D; a.addend = tb.dx2; a.alpha_p = rl_p;
       a.out = tb.dcur; a.out_h = dcur_out;
       if (llama) {
-        a.gain = P + o.g_att; a.dgain_part = tb.dgain_part;
+        a.gain = P + o.g_att; a.dgain_part = gpart(2 * l + 1);
       } else {
         a.lam_x = A.xin; a.lam_x0 = e->x0; a.lam_part = tb.dot_part; a.gx0 = tb.gx0; a.xl_p = xl_p;
         if (o.ve_embed >= 0) a.ve_dx = tb.ve_dx;
         if (l == L / 2) a.addend2 = tb.ginj;  // ane/train_full.go:784-787
       }
       HIPCHK(op, norm_bwd(a, st));
-      if (llama) {
+      if (llama && async && l > 0) {
+        att_gain_layer = l;  // reduced on the dW stream after the next fork
+      } else if (llama) {
         phase_begin(e, PH_RMS_DW);
-        HIPCHK(op, reduce_partials_add(G + o.g_att, tb.dgain_part, nblk, D, st));
+        HIPCHK(op, reduce_partials_add(G + o.g_att, gpart(2 * l + 1), nblk, D, st));
         phase_end(e);
       } else
         HIPCHK(op, reduce_dots_add(G + pm.resid + l, G + pm.x0l + l, tb.dot_part, nblk, 1.f, st));
