@@ -61,16 +61,17 @@ __global__ __launch_bounds__(256) void router_kernel(const float* x, const float
   const int nch = (D + kRChunk - 1) / kRChunk;
   // chunk c covers inputs [c * kRChunk, c * kRChunk + len), len a multiple of 64
   auto chunk_len = [&](int c) { return min(kRChunk, D - c * kRChunk); };
+  // every thread loads all kRStage float4 unconditionally (indices past the
+  // chunk clamped to its last element): conditional writes kept the staging
+  // array in scratch, and each load then waited for its scratch store
   auto fetch = [&](int c, float4 (&v)[kRStage]) {
     const int q4 = chunk_len(c) / 4, nst = (kRouterTok + E) * q4;
 #pragma unroll
     for (int u = 0; u < kRStage; u++) {
-      const int i = tid + 256 * u;
-      if (i < nst) {
-        const int r = i / q4, q = i % q4;
-        const float* src = r < kRouterTok ? x + (size_t)min(t0 + r, T - 1) * D : wr + (size_t)(r - kRouterTok) * D;
-        v[u] = *reinterpret_cast<const float4*>(src + c * kRChunk + q * 4);
-      }
+      const int i = min(tid + 256 * u, nst - 1);
+      const int r = i / q4, q = i % q4;
+      const float* src = r < kRouterTok ? x + (size_t)min(t0 + r, T - 1) * D : wr + (size_t)(r - kRouterTok) * D;
+      v[u] = *reinterpret_cast<const float4*>(src + c * kRChunk + q * 4);
     }
   };
   auto store = [&](int c, int buf, const float4 (&v)[kRStage]) {
@@ -78,11 +79,10 @@ __global__ __launch_bounds__(256) void router_kernel(const float* x, const float
 #pragma unroll
     for (int u = 0; u < kRStage; u++) {
       const int i = tid + 256 * u;
-      if (i < nst) {
-        const int r = i / q4, q = i % q4;
-        float* dst = r < kRouterTok ? &xs[buf][r][q * 4] : &ws[buf][r - kRouterTok][q * 4];
-        *reinterpret_cast<float4*>(dst) = v[u];
-      }
+      const int ic = min(i, nst - 1), r = ic / q4, q = ic % q4;
+      const float4 val = v[u];
+      float* dst = r < kRouterTok ? &xs[buf][r][q * 4] : &ws[buf][r - kRouterTok][q * 4];
+      if (i < nst) *reinterpret_cast<float4*>(dst) = val;
     }
   };
   float4 v[kRStage];
