@@ -23,32 +23,19 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(NormBwdArgs a) {
     const int t = blockIdx.x * kNormBwdRows + wave * (kNormBwdRows / 4) + rr;
     if (t >= a.T) break;
     const size_t ro = (size_t)t * D;
-    float4 dy[kMaxVec], xv[kMaxVec], gv[kMaxVec], adv[kMaxVec];
+    float4 dy[kMaxVec], xv[kMaxVec], gv[kMaxVec];
     float ss = 0.f, dot = 0.f;
-    // every load of the row is issued before any is used: the loads are
-    // unconditional (index clamped into the row, absent operands read from a
-    // row that exists and ignored), the bound applies to the values
-    const float* gsrc = a.gain ? a.gain : a.x + ro;
-    const float* asrc = a.addend ? a.addend + ro : a.dy + ro;
-#pragma unroll
-    for (int k = 0; k < kMaxVec; k++) {
-      const int i = lane + 64 * k, ic = i < nv ? i : nv - 1;
-      dy[k] = reinterpret_cast<const float4*>(a.dy + ro)[ic];
-      xv[k] = reinterpret_cast<const float4*>(a.x + ro)[ic];
-      gv[k] = reinterpret_cast<const float4*>(gsrc)[ic];
-      adv[k] = reinterpret_cast<const float4*>(asrc)[ic];
-    }
 #pragma unroll
     for (int k = 0; k < kMaxVec; k++) {
       const int i = lane + 64 * k;
-      if (!a.gain) gv[k] = make_float4(1.f, 1.f, 1.f, 1.f);
-      if (i >= nv) {
-        dy[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-        xv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (i < nv) {
+        dy[k] = reinterpret_cast<const float4*>(a.dy + ro)[i];
+        xv[k] = reinterpret_cast<const float4*>(a.x + ro)[i];
+        gv[k] = a.gain ? reinterpret_cast<const float4*>(a.gain)[i] : make_float4(1.f, 1.f, 1.f, 1.f);
+        ss += xv[k].x * xv[k].x + xv[k].y * xv[k].y + xv[k].z * xv[k].z + xv[k].w * xv[k].w;
+        dot += dy[k].x * xv[k].x * gv[k].x + dy[k].y * xv[k].y * gv[k].y + dy[k].z * xv[k].z * gv[k].z +
+               dy[k].w * xv[k].w * gv[k].w;
       }
-      ss += xv[k].x * xv[k].x + xv[k].y * xv[k].y + xv[k].z * xv[k].z + xv[k].w * xv[k].w;
-      dot += dy[k].x * xv[k].x * gv[k].x + dy[k].y * xv[k].y * gv[k].y + dy[k].z * xv[k].z * gv[k].z +
-             dy[k].w * xv[k].w * gv[k].w;
     }
     ss = wave_sum(ss);
     dot = wave_sum(dot);
@@ -68,7 +55,7 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(NormBwdArgs a) {
         dg[k].w += dy[k].w * xv[k].w * rrms;
       }
       if (a.addend) {
-        const float4 ad = adv[k];
+        const float4 ad = reinterpret_cast<const float4*>(a.addend + ro)[i];
         const float av[4] = {ad.x, ad.y, ad.z, ad.w};
 #pragma unroll
         for (int u = 0; u < 4; u++) o[u] += alpha * av[u];
