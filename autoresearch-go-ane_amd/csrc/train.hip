@@ -236,6 +236,13 @@ int backward_body(ane_engine* e, int nseq, bool async) {
   auto by_parity = [&](half_t* a, half_t* b, int l) { return async && (l & 1) ? b : a; };
   auto dcur_h_of = [&](int l) { return by_parity(tb.dcur_h, tb.dcur_h2, l); };
   auto gpart = [&](int i) { return tb.dgain_parts + (size_t)i * nblk * D; };
+  // llama2, first backward of an accumulation window: every gradient writer
+  // (the dW GEMMs, the classifier's gEmbed GEMM, the gain reductions)
+  // overwrites its region instead of adding to it, so the flush's update need
+  // not clear the gradient (nanochat's VE tables take atomic adds and keep
+  // the clear)
+  const bool fresh = llama && e->state.pending_steps == 0;
+  const int acc = fresh ? 0 : 1;
 
   // Cold GEMM operands streamed into the caches by a prefetch kernel on the
   // dW stream at each fork: the weight shadow of the dX GEMM that the main
@@ -283,7 +290,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
   }
   {  // classifier part of the embedding gradient (MatMulGradEmbedScale, ane/stories/cpu.go:366-385)
     EpiParams p;
-    p.C = G + pm.embed; p.ldc = D; p.scale = 1.f / kDlScale; p.accumulate = 1;
+    p.C = G + pm.embed; p.ldc = D; p.scale = 1.f / kDlScale; p.accumulate = acc;
     phase_begin(e, PH_EMBED_GRAD, ds);
     if (e->tr_dw) {  // dl_t and xh token-major, both read through transposing LDS loads
       HIPCHK(op, eng_gemm(e, 7, tb.dl_t, V, true, e->xh, D, true, V, D, T, EPI_STORE_F, p, 0, 0, async));
@@ -304,7 +311,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
     HIPCHK(op, norm_bwd(a, st));
     if (llama) {
       phase_begin(e, PH_RMS_DW);
-      HIPCHK(op, reduce_partials_add(G + pm.g_final, tb.dgain_part, nblk, D, st));
+      HIPCHK(op, reduce_partials_add(G + pm.g_final, tb.dgain_part, nblk, D, st, fresh));
       phase_end(e);
     } else {
       HIPCHK(op, backout_bwd(tb.ginj, tb.dot_part, tb.dcur, e->xmid, P + pm.backout_lambda, T, D, st));
@@ -343,20 +350,21 @@ int backward_body(ane_engine* e, int nseq, bool async) {
     HIPCHK(op, prefetch(ds, {{s.w13_t, (size_t)KH * D * 2}, {A.xn2, TD2}, {A.gate, (size_t)T * H * 2}}));
     if (att_gain_layer >= 0) {  // the attention-norm gain of the layer above
       phase_begin(e, PH_RMS_DW, ds);
-      HIPCHK(op, reduce_partials_add(G + pm.L[att_gain_layer].g_att, gpart(2 * att_gain_layer + 1), nblk, D, ds));
+      HIPCHK(op, reduce_partials_add(G + pm.L[att_gain_layer].g_att, gpart(2 * att_gain_layer + 1), nblk, D, ds,
+                                     fresh));
       phase_end(e, ds);
       att_gain_layer = -1;
     }
     {  // dW2 += dOut gate^T
       EpiParams p;
-      p.C = G + o.w2; p.ldc = H; p.accumulate = 1;
+      p.C = G + o.w2; p.ldc = H; p.accumulate = acc;
       phase_begin(e, PH_DW_GEMM, ds);
       HIPCHK(op, dw_gemm(e, 3, dcur_in, D, A.gate, H, T, EPI_STORE_F, p, async));
       phase_end(e, ds);
     }
     {  // dW1 (| dW3) += dh x2Norm^T
       EpiParams p;
-      p.C = G + o.w1; p.ldc = D; p.accumulate = 1;
+      p.C = G + o.w1; p.ldc = D; p.accumulate = acc;
       if (llama) p.C3 = G + o.w3;
       phase_begin(e, PH_DW_GEMM, ds);
       HIPCHK(op, dw_gemm(e, 2, dh13, KH, A.xn2, D, T, llama ? EPI_STORE_W13 : EPI_STORE_F, p, async));
@@ -381,7 +389,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
       HIPCHK(op, prefetch(ds, {{s.wo_t, (size_t)D * D * 2}, {A.att, TD2}}));
       if (llama) {
         phase_begin(e, PH_RMS_DW, ds);
-        HIPCHK(op, reduce_partials_add(G + o.g_ffn, gpart(2 * l), nblk, D, ds));
+        HIPCHK(op, reduce_partials_add(G + o.g_ffn, gpart(2 * l), nblk, D, ds, fresh));
         phase_end(e, ds);
       } else
         HIPCHK(op, reduce_dots_add(G + pm.resid + l, G + pm.x0l + l, tb.dot_part, nblk, 1.f, st));
@@ -389,7 +397,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
     // attention (backwardAttentionCPU, ane/train_full.go:644-675)
     {
       EpiParams p;
-      p.C = G + o.wo; p.ldc = D; p.accumulate = 1;
+      p.C = G + o.wo; p.ldc = D; p.accumulate = acc;
       phase_begin(e, PH_DW_GEMM, ds);
       HIPCHK(op, dw_gemm(e, 1, dx2_h, D, A.att, D, T, EPI_STORE_F, p, async));
       phase_end(e, ds);
@@ -434,7 +442,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
     HIPCHK(op, prefetch(ds, {{s.wqkv_t, (size_t)3 * D * D * 2}, {A.xn, TD2}}));
     {  // dWq | dWk | dWv += dqkv xNorm^T
       EpiParams p;
-      p.C = G + o.wq; p.ldc = D; p.accumulate = 1;
+      p.C = G + o.wq; p.ldc = D; p.accumulate = acc;
       phase_begin(e, PH_DW_GEMM, ds);
       HIPCHK(op, dw_gemm(e, 0, dqkv, 3 * D, A.xn, D, T, EPI_STORE_F, p, async));
       phase_end(e, ds);
@@ -470,7 +478,7 @@ int backward_body(ane_engine* e, int nseq, bool async) {
         att_gain_layer = l;  // reduced on the dW stream after the next fork
       } else if (llama) {
         phase_begin(e, PH_RMS_DW);
-        HIPCHK(op, reduce_partials_add(G + o.g_att, gpart(2 * l + 1), nblk, D, st));
+        HIPCHK(op, reduce_partials_add(G + o.g_att, gpart(2 * l + 1), nblk, D, st, fresh));
         phase_end(e);
       } else
         HIPCHK(op, reduce_dots_add(G + pm.resid + l, G + pm.x0l + l, tb.dot_part, nblk, 1.f, st));
@@ -554,6 +562,7 @@ int flush_pending(ane_engine* e) {
   memset(&a, 0, sizeof a);
   a.w = e->P; a.g = tb.G; a.m = tb.M; a.v = tb.Vv; a.sumsq = tb.sumsq;
   a.gscale = gscale; a.clip = O.grad_clip; a.eps = O.adam_eps;
+  a.zero_g = llama ? 0 : 1;  // llama2's next backward overwrites the gradient (backward_body)
   // applyLayerAdam (ane/train_full.go:1088-1100): matrices with lr + wd; gains
   // and VE gate with the scalar lr, VE table with the embedding lr, no wd
   for (int l = 0; l < L; l++) {
@@ -838,6 +847,10 @@ extern "C" int ane_get_accum_grads(ane_engine* e, float* grads, int64_t n) {
                     (long long)e->pm.total);
   int rc = ensure_train(e, op);
   if (rc) return rc;
+  if (e->state.pending_steps == 0) {  // nothing accumulated (the buffer may hold a finished window's sums)
+    memset(grads, 0, (size_t)n * 4);
+    return ANE_OK;
+  }
   HIPCHK(op, hipMemcpyAsync(grads, e->tr.G, (size_t)n * 4, hipMemcpyDeviceToHost, e->stream));
   HIPCHK(op, hipStreamSynchronize(e->stream));
   return ANE_OK;

@@ -36,7 +36,9 @@ hipError_t norm_bwd(const NormBwdArgs& a, hipStream_t s);
 inline int norm_bwd_blocks(int T) { return (T + kNormBwdRows - 1) / kNormBwdRows; }
 
 // dst[i] += sum over blocks of part[b][i]  (i < n)
-hipError_t reduce_partials_add(float* dst, const float* part, int nblocks, int n, hipStream_t s);
+// (overwrite: dst[i] = the sum, the first gradient of an accumulation window)
+hipError_t reduce_partials_add(float* dst, const float* part, int nblocks, int n, hipStream_t s,
+                               bool overwrite = false);
 // dst[k] += (float)(sign * sum over blocks of part[b][k])  for k < 2 (lambda grads)
 hipError_t reduce_dots_add(float* dst0, float* dst1, const double* part, int nblocks, float sign, hipStream_t s);
 
@@ -105,12 +107,13 @@ struct AdamSeg {
 constexpr int kMaxAdamSegs = 64;
 struct AdamArgs {
   float* w;
-  float* g;  // read by adam_update; read and zeroed by adam_fused_update
+  float* g;  // read by adam_update; read (and zeroed when zero_g) by adam_fused_update
   float* m;
   float* v;
   const double* sumsq;  // device: sum of squares of the raw clip-segment grads
   float gscale, clip, eps;
   int nseg;
+  int zero_g;  // adam_fused_update: clear the gradient (unless the next backward overwrites it)
   AdamSeg seg[kMaxAdamSegs];
 };
 hipError_t adam_update(const AdamArgs& a, hipStream_t s);

@@ -120,7 +120,8 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(NormBwdArgs a) {
 // One block per 64 columns: 16 waves each sum every 16th partial row of
 // the block's columns (independent loads, four in flight per lane), then
 // the 16 wave sums are added in a fixed order.
-__global__ __launch_bounds__(1024) void reduce_partials_kernel(float* dst, const float* part, int nblocks, int n) {
+__global__ __launch_bounds__(1024) void reduce_partials_kernel(float* dst, const float* part, int nblocks, int n,
+                                                              int overwrite) {
   __shared__ float sh[16][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i = blockIdx.x * 64 + lane;
@@ -141,7 +142,7 @@ __global__ __launch_bounds__(1024) void reduce_partials_kernel(float* dst, const
     float s = 0.f;
 #pragma unroll
     for (int w = 0; w < 16; w++) s += sh[w][lane];
-    dst[i] += s;
+    dst[i] = overwrite ? s : dst[i] + s;
   }
 }
 
@@ -396,7 +397,7 @@ __global__ __launch_bounds__(256) void adam_fused_kernel(AdamArgs a, const Updat
       st_nt_f4(a.m + k, m4);
       st_nt_f4(a.v + k, v4);
       st_nt_f4(a.w + k, w4);
-      st_nt_f4(a.g + k, make_float4(0.f, 0.f, 0.f, 0.f));
+      if (a.zero_g) st_nt_f4(a.g + k, make_float4(0.f, 0.f, 0.f, 0.f));
       if (jb.sh) {
         const int64_t r = i / jb.C;
         const int c = (int)(i - r * jb.C);
@@ -415,7 +416,7 @@ __global__ __launch_bounds__(256) void adam_fused_kernel(AdamArgs a, const Updat
       a.m[k] = m;
       a.v[k] = v;
       a.w[k] = w;
-      a.g[k] = 0.f;
+      if (a.zero_g) a.g[k] = 0.f;
     }
   }
 }
@@ -519,8 +520,9 @@ hipError_t norm_bwd(const NormBwdArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t reduce_partials_add(float* dst, const float* part, int nblocks, int n, hipStream_t s) {
-  hipLaunchKernelGGL(reduce_partials_kernel, dim3((n + 63) / 64), dim3(1024), 0, s, dst, part, nblocks, n);
+hipError_t reduce_partials_add(float* dst, const float* part, int nblocks, int n, hipStream_t s, bool overwrite) {
+  hipLaunchKernelGGL(reduce_partials_kernel, dim3((n + 63) / 64), dim3(1024), 0, s, dst, part, nblocks, n,
+                     overwrite ? 1 : 0);
   return hipGetLastError();
 }
 
