@@ -602,19 +602,23 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
 }
 
 // Wide form, one 1024-thread block per (sequence, kv head, split of up to
-// kDecWideChunk keys), scores on MFMA: S^T = K Q^T over 16-key tiles with
-// v_mfma_f32_16x16x32_f16 -- A = 16 keys x 32 dims read straight from the
-// cache rows (lane: key lane % 16, dims 8 (lane / 16) + [0, 8)), B = the G
-// query heads padded to 16 columns.  Tile t goes to wave t % 16, pass t / 16.
-// Every (key, head) score then sits in one lane (C layout: head lane % 16,
-// keys 4 (lane / 16) + [0, 4)), so each probability is formed once, rounded
-// to fp16 into LDS; P.V runs on v_dot2 with 8 lanes per key as in the
-// narrow form, reading the probabilities back.
+// kDecWideChunk keys).  Key tile t (16 keys) belongs to wave t % 16, which
+// does all of that tile's work:
+//   * scores S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims
+//     straight from the cache rows (lane: key lane % 16, dims 8 (lane / 16)
+//     + [0, 8)), B = the G query heads padded to 16 columns;
+//   * the wave's own softmax over its keys (maximum and sum per head);
+//   * O = P V on v_mfma_f32_16x16x16_f16.  The score accumulator already has
+//     the A layout of P (head lane % 16, keys 4 (lane / 16) + [0, 4)), so the
+//     probabilities stay in their lanes; each V tile goes through a per-wave
+//     LDS tile, read back transposed (ds_read_b64_tr_b16) as the B operand.
+// The waves' (maximum, sum, O) meet once in LDS at the end, rescaled to the
+// block maximum.  No block-wide barrier separates the K loads from P V, so
+// each wave works on its rows as they arrive.
 template <int G, bool DIRECT>
 __device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a) {
-  constexpr int NT = 1024, NW = NT / 64, KP = NT / 8, NIT = kDecWideChunk / KP;
-  constexpr int TW = (kDecWideChunk / 16 + NW - 1) / NW;  // K tiles per wave
-  constexpr int NR = NT / (G * 64) < 8 ? NT / (G * 64) : 8;
+  constexpr int NT = 1024, NW = NT / 64;
+  constexpr int TW = (kDecWideChunk / 16 + NW - 1) / NW;  // key tiles per wave
   const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ctx = a.ctr[0] + 1;
@@ -623,10 +627,11 @@ __device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a) {
   if (c0 >= ctx) return;  // uniform over the block, before any barrier
   const int n = min(chunk, ctx - c0);
   __shared__ half_t qs[G][64];
-  __shared__ half_t ps[G][kDecWideChunk];
-  __shared__ __attribute__((aligned(16))) float pv[G][KP][64];
-  __shared__ float red[NR][G * 64];
-  __shared__ float wmax[G][NW], wsum[G][NW];
+  // per-wave V tiles [16 keys][64 dims], two used in turn; 16-byte chunk c
+  // of row r at chunk slot c ^ (r & 7)
+  __shared__ __attribute__((aligned(16))) half_t vt[NW][2][16 * 64];
+  __shared__ float wo[NW][G][64];  // each wave's O (scaled to its own maximum)
+  __shared__ float wm[NW][G], wl[NW][G];
   __shared__ __attribute__((aligned(16))) half_t knew[64], vnew[64];
   const float sl2 = a.scale * kL2E;
   const size_t cache0 = ((size_t)b * a.NKV + kvh) * a.max_ctx;
@@ -634,12 +639,15 @@ __device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a) {
   half_t* Vb = a.vc + (cache0 + c0) * 64;
   const int pos = ctx - 1;
   const bool own = pos - c0 < n;
-  const int kr = lane & 15, kq = lane >> 4;
-  const int kl = tid >> 3, d8 = tid & 7;
+  const int kr = lane & 15, kq = lane >> 4;  // K fragment: key kr, dims 8 kq (+ 32)
+  const int vr = lane >> 2, vc = lane & 3;   // V tile row: key vr, dims 16 vc + [0, 16)
+  // Load order: the QKV partials first (the staging barrier waits for them
+  // alone), then every K row, then every V row.  Unconditional loads (key
+  // index clamped; keys past n unused).
   QkvProj<G, 8> qp;
   qp.issue(a, b, kvh, tid, pos, own);
   __builtin_amdgcn_sched_barrier(0);
-  half8 ka[TW][2];
+  half8 ka[TW][2], va[TW][2];
 #pragma unroll
   for (int u = 0; u < TW; u++) {
     const half_t* row = Kb + (size_t)min((wave + NW * u) * 16 + kr, n - 1) * 64 + kq * 8;
@@ -647,9 +655,12 @@ __device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a) {
     ka[u][1] = ld_h8(row + 32);
   }
   __builtin_amdgcn_sched_barrier(0);
-  half8 kv[NIT];
 #pragma unroll
-  for (int it = 0; it < NIT; it++) kv[it] = ld_h8(Vb + (size_t)min(kl + KP * it, n - 1) * 64 + d8 * 8);
+  for (int u = 0; u < TW; u++) {
+    const half_t* row = Vb + (size_t)min((wave + NW * u) * 16 + vr, n - 1) * 64 + vc * 16;
+    va[u][0] = ld_h8(row);
+    va[u][1] = ld_h8(row + 8);
+  }
   __builtin_amdgcn_sched_barrier(0);
   qp.finish(a, tid, qs, knew, vnew, Kb, Vb, pos - c0);
   __syncthreads();
@@ -657,11 +668,12 @@ __device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a) {
   // too (clamped): those take the new k / v (the row read may be stale, and
   // a NaN there must not reach the sums), by a select at each use.
   const int jrep = own ? pos - c0 : 1 << 30;
-  half8 kn0 = {}, kn1 = {}, vn = {};
+  half8 kn0 = {}, kn1 = {}, vn0 = {}, vn1 = {};
   if (own) {
     kn0 = ld_h8(knew + kq * 8);
     kn1 = ld_h8(knew + 32 + kq * 8);
-    vn = ld_h8(vnew + d8 * 8);
+    vn0 = ld_h8(vnew + vc * 16);
+    vn1 = ld_h8(vnew + vc * 16 + 8);
   }
   half8 qb0, qb1;  // B operand: head kr (zero columns past G), dims as A
   {
@@ -686,92 +698,78 @@ __device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a) {
       m = fmaxf(m, st[u][i]);
     }
   }
-  // per-head maximum: lanes of one head (lane % 16) across the wave, then the waves
+  // the wave's maximum per head (the lanes of head lane % 16); a wave with
+  // no valid key, and the padding columns, have p = exp2(-inf) = 0
   m = fmaxf(m, __shfl_xor(m, 16, 64));
   m = fmaxf(m, xor32_f(m));
-  if (lane < G) wmax[lane][wave] = m;
-  __syncthreads();
-  float mh = kr < G ? -INFINITY : 0.f;  // padding columns: p = exp2(-inf) = 0
-  if (kr < G) {
-#pragma unroll
-    for (int w = 0; w < NW; w++) mh = fmaxf(mh, wmax[kr][w]);
-  }
-  // probabilities rounded to fp16 (they feed fp16 dot products), once per
-  // (key, head); the normaliser sums the same rounded values
+  const float mz = m == -INFINITY ? 0.f : m;
+  // probabilities rounded to fp16 (the P V operand); the sum adds the same
+  // rounded values
+  half4 pa[TW];
   float l = 0.f;
 #pragma unroll
-  for (int u = 0; u < TW; u++) {
-    const int kb = (wave + NW * u) * 16;
+  for (int u = 0; u < TW; u++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int j = kb + 4 * kq + i;
-      const half_t p = (half_t)__builtin_amdgcn_exp2f(st[u][i] - mh);  // 0 for masked scores
-      if (kr < G && j < kDecWideChunk) ps[kr < G ? kr : 0][j] = p;
-      l += (float)p;
+      pa[u][i] = (half_t)__builtin_amdgcn_exp2f(st[u][i] - mz);
+      l += (float)pa[u][i];
     }
-  }
   l += __shfl_xor(l, 16, 64);
   l += xor32_f(l);
-  if (lane < G) wsum[lane][wave] = l;
-  __syncthreads();
-  // P.V over this thread's key pairs (it, it + 1) with v_dot2
-  float acc[G][8];
+  // O[head][dim] += P[head][key] V[key][dim], 16 dims per MFMA: lane
+  // 16 g + j takes V[4 g + e][16 db + j] (e = 0..3), which the transposed
+  // read gives when lane l addresses row l / 4, halves 16 db + 4 (l % 4)
+  floatx4 o[4];
 #pragma unroll
-  for (int h = 0; h < G; h++)
+  for (int db = 0; db < 4; db++) o[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const int rr = lane >> 2, rq = lane & 3;
 #pragma unroll
-    for (int i = 0; i < 8; i++) acc[h][i] = 0.f;
+  for (int u = 0; u < TW; u++) {
+    half_t* t = vt[wave][u & 1];
+    const bool rep = (wave + NW * u) * 16 + vr >= jrep;
+    st_h8(t + vr * 64 + (((2 * vc) ^ (vr & 7)) << 3), rep ? vn0 : va[u][0]);
+    st_h8(t + vr * 64 + (((2 * vc + 1) ^ (vr & 7)) << 3), rep ? vn1 : va[u][1]);
+    // the wave's stores precede its reads (LDS runs one wave's operations
+    // in order); the fence keeps the compiler from reordering them
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
-  for (int it = 0; it < NIT; it += 2) {
-    const bool pair = it + 1 < NIT;
-    const int j0 = kl + KP * it, j1 = j0 + KP;
-    const half8 v0 = j0 >= jrep ? vn : kv[it];
-    const half8 v1 = pair ? (j1 >= jrep ? vn : kv[pair ? it + 1 : it]) : half8{};
-    half2v vp[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      vp[i][0] = v0[i];
-      vp[i][1] = v1[i];
+    for (int db = 0; db < 4; db++) {
+      const int cch = 2 * db + (rq >> 1);
+      const short4v bv = ds_read_tr16(t + rr * 64 + ((cch ^ (rr & 7)) << 3) + 4 * (rq & 1));
+      o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[u], __builtin_bit_cast(half4, bv), o[db], 0, 0, 0);
     }
-#pragma unroll
-    for (int h = 0; h < G; h++) {
-      half2v pp;
-      pp[0] = j0 < n ? ps[h][j0] : (half_t)0.f;
-      pp[1] = pair && j1 < n ? ps[h][pair ? j1 : j0] : (half_t)0.f;
-#pragma unroll
-      for (int i = 0; i < 8; i++) acc[h][i] = __builtin_amdgcn_fdot2(pp, vp[i], acc[h][i], false);
-    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   }
+  // the merge: O rows (heads) 4 (lane / 16) + i, column 16 db + lane % 16;
+  // heads < G sit in lanes 0..15
+  if (lane < 16) {
 #pragma unroll
-  for (int h = 0; h < G; h++) {
-    float4* dst = reinterpret_cast<float4*>(&pv[h][kl][d8 * 8]);
-    dst[0] = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
-    dst[1] = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+    for (int db = 0; db < 4; db++)
+#pragma unroll
+      for (int i = 0; i < G; i++) wo[wave][i][16 * db + lane] = o[db][i];
   }
-  __syncthreads();
-  constexpr int KPR = (KP + NR - 1) / NR;
-  if (tid < NR * G * 64) {
-    const int r = tid / (G * 64), hd = tid % (G * 64), h = hd >> 6, d = hd & 63;
-    float o = 0.f;
-#pragma unroll 8
-    for (int k = r * KPR; k < min(KP, (r + 1) * KPR); k++) o += pv[h][k][d];
-    red[r][hd] = o;
+  if (lane < G) {
+    wm[wave][lane] = m;
+    wl[wave][lane] = l;
   }
   __syncthreads();
   if (tid < G * 64) {
     const int h = tid >> 6, d = tid & 63;
-    float o = 0.f, lt = 0.f, mt = -INFINITY;
+    float mt = -INFINITY;
 #pragma unroll
-    for (int r = 0; r < NR; r++) o += red[r][tid];
+    for (int w = 0; w < NW; w++) mt = fmaxf(mt, wm[w][h]);  // finite: key 0 is valid
+    float ot = 0.f, lt = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; w++) {
-      lt += wsum[h][w];
-      mt = fmaxf(mt, wmax[h][w]);
+      const float f = __builtin_amdgcn_exp2f(wm[w][h] - mt);  // 0 for a wave without keys
+      ot += f * wo[w][h][d];
+      lt += f * wl[w][h];
     }
     if constexpr (DIRECT) {
-      a.att[act_frag_off(b, (kvh * G + h) * 64 + d)] = (half_t)(o / lt);
+      a.att[act_frag_off(b, (kvh * G + h) * 64 + d)] = (half_t)(ot / lt);
     } else {
       float* out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nsplit + sp) * 66;
-      out[d] = o;
+      out[d] = ot;
       if (d == 0) { out[64] = mt; out[65] = lt; }
     }
   }

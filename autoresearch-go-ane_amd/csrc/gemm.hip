@@ -86,7 +86,6 @@ __device__ __forceinline__ void store_tmajor(half_t* tile, const half8 (&v)[8], 
 // publishes the tile).
 // M0 is named as clobbered (these kernels keep nothing else in it; clang
 // warns that it is a reserved register).
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 // lds_addr: the destination's LDS byte address, wave-uniform
@@ -717,14 +716,6 @@ __device__ __forceinline__ void dma16_s(const half_t* sbase, unsigned voff, unsi
 #pragma clang diagnostic pop
 }
 
-// ds_read_b64_tr_b16 (gfx950): lane 16 g + j receives element j % 4 of the 4
-// halves that lane 16 g + 4 e + j / 4 addresses, as its element e.  Two
-// such reads give an MFMA operand from a tile stored with the MFMA row
-// index contiguous ("M-major", [k][m]): see tr_frag.
-typedef short short4v __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ short4v ds_read_tr16(const half_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(lds_ptr_t)p);
-}
 // Chunk swizzle of an M-major LDS tile (rows of CPR 16-byte chunks): the
 // four 16-byte chunks a transposed read takes from one row move with the row
 // (rows r and r + 4 share a position: a two-way bank conflict at most).

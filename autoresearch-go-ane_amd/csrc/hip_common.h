@@ -75,6 +75,16 @@ __device__ __forceinline__ void st_h8(half_t* p, half8 v) {
   *reinterpret_cast<half8*>(p) = v;
 }
 
+// LDS reads that transpose (gfx950 ds_read_b64_tr_b16): lane 16 g + j
+// receives element j % 4 of the 4 halves that lane 16 g + 4 e + j / 4
+// addresses, as its element e.  Such reads give an MFMA operand from a tile
+// stored with the operand's row index contiguous ([k][row]).
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef short short4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ short4v ds_read_tr16(const half_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4v*)(lds_ptr_t)p);
+}
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
 // Streams slice `part` of `nparts` equal slices of [p, p + bytes) through

@@ -589,8 +589,9 @@ int flush_pending(ane_engine* e) {
   // the fp16 shadows the next forward and backward read: the weight refresh
   // (refreshANERuntimeForWeights, ane/runtime.go:25-69)
   if (e->fused_adam && e->shadow_jobs && e->shadow_jobs_t) {
-    // one pass: AdamW, the gradient zeroed, the plain shadows; then the
-    // refresh proper is the transposed shadows, read from the plain ones
+    // one pass: AdamW, the plain shadows and (nanochat) the gradient
+    // cleared; then the refresh proper is the transposed shadows, read from
+    // the plain ones
     int rc = ensure_update_jobs(e, a);
     if (rc) return rc;
     (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM0], st);
