@@ -116,6 +116,33 @@ hipError_t dec_attention(const DecAttnArgs& a, hipStream_t s);
 // W1|W3 pair) over the whole K, blocks ordered by phase; a block waits on the
 // done counter of the phase it reads (no grid barrier).  Requires every block
 // resident at once: dec_tail_blocks_per_cu() x CUs >= the block count.
+// The data-polling form of the chain exchanges its activations through one
+// of two buffer sets (by the parity of the use), in which every dword starts
+// as kTailStale: a consumer polls the data itself until no dword is stale,
+// and each launch resets the other set for the next use.
+constexpr uint32_t kTailStale = 0xFFFFFFFFu;
+struct TailSet {
+  half_t* xg_ffn;   // [64][D] fragments: fp16(x * g_ffn) after Wo
+  half_t* gate;     // [64][H] fragments
+  half_t* xg_next;  // [64][D] fragments: fp16(x * g_next) after W2 (for the next QKV)
+  float* x_mid;     // [64][D] the residual after Wo
+  float* ssq_wo;    // [D/32][64] per column group sum of squares after Wo
+  float* ssq_w2;    // [D/32][64] and after W2
+};
+__host__ __device__ inline size_t tail_set_bytes(int D, int H) {
+  return (size_t)64 * (2 * D + H) * 2 + (size_t)64 * D * 4 + (size_t)2 * (D / 32) * 64 * 4;
+}
+__host__ __device__ inline TailSet tail_set(void* base, int D, int H) {
+  char* p = static_cast<char*>(base);
+  TailSet t;
+  t.xg_ffn = reinterpret_cast<half_t*>(p); p += (size_t)64 * D * 2;
+  t.gate = reinterpret_cast<half_t*>(p); p += (size_t)64 * H * 2;
+  t.xg_next = reinterpret_cast<half_t*>(p); p += (size_t)64 * D * 2;
+  t.x_mid = reinterpret_cast<float*>(p); p += (size_t)64 * D * 4;
+  t.ssq_wo = reinterpret_cast<float*>(p); p += (size_t)(D / 32) * 64 * 4;
+  t.ssq_w2 = reinterpret_cast<float*>(p);
+  return t;
+}
 struct TailArgs {
   const half_t* att;        // [64][D] activation fragments: the attention output
   float* x;                 // [64][D] residual stream (fp32, row-major)
@@ -138,6 +165,11 @@ struct TailArgs {
   unsigned spin_limit;      // polls before a wait times out (kDecTailSpin; 0: every wait fails)
   int D, H, N1, layer, L;
   int b_wo, b_13, b_w2, b_q;  // blocks per phase: D/32, H/32, D/32, N1/32 (0 on the last layer)
+  // data-polling form (poll != 0): the two buffer sets (tail_set_bytes each,
+  // every dword kTailStale at open); xg_ffn, ssq_wo, ssq_w2 and sync above
+  // are then unused, and xg_next receives the last layer's W2 output only
+  int poll = 0;
+  void* sets[2] = {nullptr, nullptr};
 };
 constexpr int kDecTailSync = 64;
 constexpr unsigned kDecTailSpin = 1u << 20;  // polls of ~100 cycles: ~50 ms

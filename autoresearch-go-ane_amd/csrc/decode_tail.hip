@@ -55,8 +55,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
 __device__ __forceinline__ float ld_c1(const float* base, uint32_t elem) {
   return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc(base), elem * 4u, 0, kSc1));
 }
+// A stored dword never equals kTailStale (the data-polling form's "not yet
+// written"): the one NaN pattern that would is replaced by another quiet NaN.
+__device__ __forceinline__ uint32_t not_stale(uint32_t v, uint32_t nan) { return v == kTailStale ? nan : v; }
+__device__ __forceinline__ bool fresh(float v) { return __float_as_uint(v) != kTailStale; }
+__device__ __forceinline__ bool fresh8(half8 v) {
+  const u32x4v u = __builtin_bit_cast(u32x4v, v);
+  return (u[0] != kTailStale) & (u[1] != kTailStale) & (u[2] != kTailStale) & (u[3] != kTailStale);
+}
 __device__ __forceinline__ void st_c1(float* base, uint32_t elem, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), rsrc(base), elem * 4u, 0, kSc1);
+  __builtin_amdgcn_raw_buffer_store_b32(not_stale(__float_as_uint(v), 0x7FC00000u), rsrc(base), elem * 4u, 0, kSc1);
 }
 __device__ __forceinline__ half8 ld_ch8(const half_t* base, uint32_t elem) {
   const u32x4v a = __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), elem * 2u, 0, kSc1);
@@ -102,6 +110,30 @@ __device__ void publish(unsigned* done) {
   drain_stores();
   __syncthreads();
   if (threadIdx.x == 0) __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Data-polling form: a wave re-issues its device-coherent input loads in
+// rounds until none of them returns a stale dword.  give_up() after round r:
+// true after `limit` rounds or when another block has failed (else a short
+// sleep before the next round).  limit 0 fails before the first round.
+__device__ __forceinline__ bool give_up(unsigned r, unsigned limit, const int* err) {
+  if (r + 1 >= limit || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return true;
+  __builtin_amdgcn_s_sleep(1);
+  return false;
+}
+// This wave's outcome into its flag (read after the next barrier by
+// any_failed); a wave whose inputs never arrived also sets the launch's error.
+__device__ __forceinline__ void wave_outcome(bool ok, int* err, int* wfail) {
+  if (__lane_id() == 0) {
+    wfail[threadIdx.x >> 6] = ok ? 0 : 1;
+    if (!ok) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+__device__ __forceinline__ bool any_failed(const int* wfail) {
+  int f = 0;
+#pragma unroll
+  for (int w = 0; w < 16; w++) f |= wfail[w];
+  return f != 0;
 }
 
 // Windows [w0, w0 + nw) of wave `wave` when nwin windows are split over
@@ -155,6 +187,40 @@ struct WaveGemm {
       }
     }
   }
+  // Data-polling form: the activation fragments into px / qx (device-coherent
+  // loads); true when no dword of this lane's is stale.  compute() then
+  // runs the MFMAs on them.
+  half8 px[4 * MAXW], qx[4 * MAXW];
+  __device__ __forceinline__ bool load_x(const half_t* X, Span sp) {
+    // recomputed each round (opaque to loop-invariant hoisting): the load
+    // offsets then hold no register while the round's data is in flight
+    int lane8 = threadIdx.x % 64 * 8;
+    asm volatile("" : "+v"(lane8));
+#pragma unroll
+    for (int s = 0; s < 4 * MAXW; s++) {
+      const int f = (sp.w0 + min(s >> 2, max(sp.nw - 1, 0))) * 4 + (s & 3);
+      px[s] = ld_ch8(X, (uint32_t)(f * 1024 + lane8));
+      qx[s] = ld_ch8(X, (uint32_t)(f * 1024 + 512 + lane8));
+    }
+    bool ok = true;
+#pragma unroll
+    for (int s = 0; s < 4 * MAXW; s++) {
+      ok &= fresh8(px[s]);
+      ok &= fresh8(qx[s]);
+    }
+    return ok;
+  }
+  __device__ __forceinline__ void compute(Span sp) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) { c0[r] = 0.f; c1[r] = 0.f; }
+#pragma unroll
+    for (int s = 0; s < 4 * MAXW; s++) {
+      if ((s >> 2) < sp.nw) {
+        c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(px[s], w[s], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(qx[s], w[s], c1, 0, 0, 0);
+      }
+    }
+  }
   // this wave's partial into red[wave] ([64 rows][32 columns])
   __device__ __forceinline__ void to_lds(float (*red)[64][32]) const {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h = lane >> 5, col = lane & 31;
@@ -182,8 +248,8 @@ __device__ __forceinline__ void st_frag2(half_t* X, int t, int k, float a, float
   half2v h;
   h[0] = (half_t)a;
   h[1] = (half_t)b;
-  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, h), rsrc(X), (uint32_t)act_frag_off(t, k) * 2u,
-                                        0, kSc1);
+  __builtin_amdgcn_raw_buffer_store_b32(not_stale(__builtin_bit_cast(uint32_t, h), 0x7E007E00u), rsrc(X),
+                                        (uint32_t)act_frag_off(t, k) * 2u, 0, kSc1);
 }
 
 // This thread's element pair of a 64 x 32 tile of column group cg: row
@@ -203,8 +269,8 @@ __device__ void resid_epilogue(float2 acc, float2 xv, int cg, float* x, int D, f
   const __amdgpu_buffer_rsrc_t rx = rsrc(x);
   xv.x += acc.x;
   xv.y += acc.y;
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(xv.x), rx, xi * 4u, 0, kSc1);
-  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(xv.y), rx, xi * 4u + 4u, 0, kSc1);
+  __builtin_amdgcn_raw_buffer_store_b32(not_stale(__float_as_uint(xv.x), 0x7FC00000u), rx, xi * 4u, 0, kSc1);
+  __builtin_amdgcn_raw_buffer_store_b32(not_stale(__float_as_uint(xv.y), 0x7FC00000u), rx, xi * 4u + 4u, 0, kSc1);
   float ss = xv.x * xv.x + xv.y * xv.y;
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o, 64);  // the row's 16 threads
@@ -226,39 +292,65 @@ __device__ __forceinline__ float rr_of(const float* ssq, int ncg, int row, int D
 
 constexpr int kTailWaves = 16;
 
-// This thread's x element pair of column group cg (x_index) -> xs[0][tid],
-// xs[1][tid]: device-coherent loads straight into LDS (global_load_lds), so
-// that no register is held while the GEMM's loads are in flight.  They are
-// not in the compiler's wait counts: the caller waits (vmcnt(0)) before
-// reading xs.  Lane l of wave w lands at xs[j][64 w + l].
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
-__device__ __forceinline__ void x_to_lds(const float* x, int cg, int D, float (*xs)[64 * kTailWaves]) {
-  const float* gp = x + x_index(cg, D);
-  const int wave = threadIdx.x >> 6;
+// Device-coherent loads of two floats per thread, base[e0] and base[e1],
+// straight into LDS (buffer_load ... lds), so that no register is held while
+// the GEMM's loads are in flight: lane l of wave w lands at dst[0][64 w + l]
+// and dst[1][64 w + l].  They are not in the compiler's wait counts: the
+// caller issues them before any compiler-tracked load it waits on, and waits
+// (vmcnt(0)) before reading dst.
+__device__ __forceinline__ unsigned lds_rows(float (*dst)[64 * kTailWaves], int j) {
+  return __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)&dst[j][(threadIdx.x >> 6) * 64]);
+}
+__device__ __forceinline__ void two_to_lds(const float* base, uint32_t e0, uint32_t e1, unsigned lds0,
+                                           unsigned lds1) {
+  const __amdgpu_buffer_rsrc_t rs = rsrc(base);
+  asm volatile("" : "+v"(e0), "+v"(e1));  // formed where used (see load_x)
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const unsigned lds = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)&xs[j][wave * 64]);
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off sc1" ::"s"(lds), "v"(gp + j)
-                 : "memory", "m0");
-  }
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen sc1 lds" ::"s"(lds0), "v"(e0 * 4u),
+               "s"(rs)
+               : "memory", "m0");
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen sc1 lds" ::"s"(lds1), "v"(e1 * 4u),
+               "s"(rs)
+               : "memory", "m0");
 #pragma clang diagnostic pop
 }
+// This thread's x element pair of column group cg (x_index) -> xs[0][tid],
+// xs[1][tid].
+__device__ __forceinline__ void x_to_lds(const float* x, int cg, int D, float (*xs)[64 * kTailWaves]) {
+  const uint32_t e = (uint32_t)x_index(cg, D);
+  two_to_lds(x, e, e + 1, lds_rows(xs, 0), lds_rows(xs, 1));
+}
 
+// POLL: the data-polling form (TailArgs::poll): no done counters; each
+// consumer wave re-reads its inputs until none is stale, so a phase costs the
+// producers' stores reaching the shared level and one read round, instead of
+// a store drain, a counter update, a counter read and then the data read.
+template <bool POLL>
 __global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
   __shared__ float red[kTailWaves][64][32];
   __shared__ float ssq_s[32][kDecRows];
   __shared__ float xs[2][64 * kTailWaves];
-  __shared__ int sh;
+  __shared__ int sh, wfail[kTailWaves];
   if (__hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;  // an earlier wait failed
   const int D = a.D, H = a.H, N1 = a.N1, ncg = D / 32, npair = H / 32;
   const int nwd = D / 64, nwh = H / 64;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: window offsets in SGPRs
   const unsigned E = (unsigned)(*a.gstep) * (unsigned)a.L + (unsigned)a.layer + 1u;
   unsigned* done_wo = a.sync;
   unsigned* done_13 = a.sync + 1;
   unsigned* done_w2 = a.sync + 2;
+  TailSet S{};
+  if constexpr (POLL) {
+    S = tail_set(a.sets[E & 1], D, H);
+    // the other set back to stale for the next use: its readers belong to
+    // the previous launch, which has finished
+    const __amdgpu_buffer_rsrc_t ro = rsrc(a.sets[(E & 1) ^ 1]);
+    const u32x4v st = {kTailStale, kTailStale, kTailStale, kTailStale};
+    const uint32_t n16 = (uint32_t)(tail_set_bytes(D, H) / 16);
+    for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n16; k += gridDim.x * blockDim.x)
+      __builtin_amdgcn_raw_buffer_store_b128(st, ro, k * 16u, 0, kSc1);
+  }
   int b = blockIdx.x;
 
   if (b < a.b_wo) {  // ---- Wo: x += Wo att --------------------------------------
@@ -272,8 +364,12 @@ __global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
     g.mma(a.att, sp, false);  // the attention kernel finished before this launch
     g.to_lds(red);
     __syncthreads();
-    resid_epilogue(sum_waves(red, 0, kTailWaves), xv, cg, a.x, D, a.ssq_wo, a.xg_ffn, a.g_ffn);
-    publish(done_wo);
+    if constexpr (POLL) {  // x after Wo goes to x_mid, for this group's W2 block
+      resid_epilogue(sum_waves(red, 0, kTailWaves), xv, cg, S.x_mid, D, S.ssq_wo, S.xg_ffn, a.g_ffn);
+    } else {
+      resid_epilogue(sum_waves(red, 0, kTailWaves), xv, cg, a.x, D, a.ssq_wo, a.xg_ffn, a.g_ffn);
+      publish(done_wo);
+    }
     return;
   }
   b -= a.b_wo;
@@ -283,25 +379,49 @@ __global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
     const Span sp = wave_span<2>(nwd, kTailWaves / 2, wave & 7);
     WaveGemm<2> g;
     g.load_w(a.w13, 2 * pr + half, nwd, sp);
-    if (!wait_count(done_wo, (unsigned)ncg * E, a.spin_limit, a.err, &sh)) return;  // x, its sums of squares, xg_ffn
     // the residual's column-group sums of squares (ncg * 64 <= 2 per thread),
     // in flight with the activations
-    const int t0 = threadIdx.x, t1 = threadIdx.x + 64 * kTailWaves;
-    const float s0 = t0 < ncg * kDecRows ? ld_c1(a.ssq_wo, (uint32_t)t0) : 0.f;
-    const float s1 = t1 < ncg * kDecRows ? ld_c1(a.ssq_wo, (uint32_t)t1) : 0.f;
-    g.mma(a.xg_ffn, sp, true);
-    g.to_lds(red);
-    if (t0 < ncg * kDecRows) ssq_s[t0 / kDecRows][t0 % kDecRows] = s0;
-    if (t1 < ncg * kDecRows) ssq_s[t1 / kDecRows][t1 % kDecRows] = s1;
-    __syncthreads();
+    const int t0 = threadIdx.x, t1 = threadIdx.x + 64 * kTailWaves, nss = ncg * kDecRows;
+    if constexpr (POLL) {
+      // the sums of squares go straight to ssq_s (flat [2][1024]: thread t's
+      // pair at t and t + 1024), then are checked from there
+      float (*ssq_f)[64 * kTailWaves] = reinterpret_cast<float (*)[64 * kTailWaves]>(&ssq_s[0][0]);
+      const unsigned l0 = lds_rows(ssq_f, 0), l1 = lds_rows(ssq_f, 1);
+      bool ok = false;
+      for (unsigned r = 0; a.spin_limit != 0; r++) {
+        asm volatile("" ::: "memory");
+        two_to_lds(S.ssq_wo, (uint32_t)min(t0, nss - 1), (uint32_t)min(t1, nss - 1), l0, l1);
+        bool f = g.load_x(S.xg_ffn, sp);
+        drain_stores();  // the LDS loads above
+        f &= fresh(ssq_f[0][threadIdx.x]);
+        f &= fresh(ssq_f[1][threadIdx.x]);
+        if (__all(f)) { ok = true; break; }
+        if (give_up(r, a.spin_limit, a.err)) break;
+      }
+      wave_outcome(ok, a.err, wfail);
+      g.compute(sp);
+      g.to_lds(red);
+      __syncthreads();
+      if (any_failed(wfail)) return;
+    } else {
+      if (!wait_count(done_wo, (unsigned)ncg * E, a.spin_limit, a.err, &sh)) return;  // x, its sums of squares, xg_ffn
+      const float s0 = t0 < nss ? ld_c1(a.ssq_wo, (uint32_t)t0) : 0.f;
+      const float s1 = t1 < nss ? ld_c1(a.ssq_wo, (uint32_t)t1) : 0.f;
+      g.mma(a.xg_ffn, sp, true);
+      g.to_lds(red);
+      if (t0 < nss) ssq_s[t0 / kDecRows][t0 % kDecRows] = s0;
+      if (t1 < nss) ssq_s[t1 / kDecRows][t1 % kDecRows] = s1;
+      __syncthreads();
+    }
     const float2 h1 = sum_waves(red, 0, kTailWaves / 2), h3 = sum_waves(red, kTailWaves / 2, kTailWaves);
     const int row = threadIdx.x >> 4, c = (threadIdx.x & 15) * 2;
     float ss = 0.f;
     for (int q = 0; q < ncg; q++) ss += ssq_s[q][row];
     const float rr = 1.0f / sqrtf(ss / (float)D + 1e-5f);
     const float u0 = h1.x * rr, u1 = h1.y * rr;
-    st_frag2(a.gate, row, 32 * pr + c, u0 / (1.0f + __expf(-u0)) * (h3.x * rr), u1 / (1.0f + __expf(-u1)) * (h3.y * rr));
-    publish(done_13);
+    st_frag2(POLL ? S.gate : a.gate, row, 32 * pr + c, u0 / (1.0f + __expf(-u0)) * (h3.x * rr),
+             u1 / (1.0f + __expf(-u1)) * (h3.y * rr));
+    if constexpr (!POLL) publish(done_13);
     return;
   }
   b -= a.b_13;
@@ -310,17 +430,45 @@ __global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
     const Span sp = wave_span<2>(nwh, kTailWaves, wave);
     WaveGemm<2> g;
     g.load_w(a.w2, cg, nwh, sp);
-    // done_13 implies done_wo: x (written by the Wo block of this group) is
-    // read device-coherent, in flight with the activations
-    if (!wait_count(done_13, (unsigned)npair * E, a.spin_limit, a.err, &sh)) return;
-    x_to_lds(a.x, cg, D, xs);
-    g.mma(a.gate, sp, true);
-    g.to_lds(red);
-    drain_stores();  // (also the loads: x_to_lds is not in the compiler's count)
-    __syncthreads();
+    if constexpr (POLL) {
+      // x after Wo (x_mid, from this group's Wo block) in the same rounds as
+      // the activations, straight into LDS
+      const uint32_t xm = (uint32_t)x_index(cg, D);
+      const unsigned l0 = lds_rows(xs, 0), l1 = lds_rows(xs, 1);
+      bool ok = false;
+      for (unsigned r = 0; a.spin_limit != 0; r++) {
+        asm volatile("" ::: "memory");
+        two_to_lds(S.x_mid, xm, xm + 1, l0, l1);
+        bool f = g.load_x(S.gate, sp);
+        drain_stores();  // the LDS loads above
+        f &= fresh(xs[0][threadIdx.x]);
+        f &= fresh(xs[1][threadIdx.x]);
+        if (__all(f)) { ok = true; break; }
+        if (give_up(r, a.spin_limit, a.err)) break;
+      }
+      wave_outcome(ok, a.err, wfail);
+      g.compute(sp);
+      g.to_lds(red);
+      __syncthreads();
+      if (any_failed(wfail)) return;
+    } else {
+      // done_13 implies done_wo: x (written by the Wo block of this group) is
+      // read device-coherent, in flight with the activations
+      if (!wait_count(done_13, (unsigned)npair * E, a.spin_limit, a.err, &sh)) return;
+      x_to_lds(a.x, cg, D, xs);
+      g.mma(a.gate, sp, true);
+      g.to_lds(red);
+      drain_stores();  // (also the loads: x_to_lds is not in the compiler's count)
+      __syncthreads();
+    }
     const float2 xv = make_float2(xs[0][threadIdx.x], xs[1][threadIdx.x]);
-    resid_epilogue(sum_waves(red, 0, kTailWaves), xv, cg, a.x, D, a.ssq_w2, a.xg_next, a.g_next);
-    publish(done_w2);
+    if constexpr (POLL) {  // the last layer's output is for the classifier (after this launch)
+      resid_epilogue(sum_waves(red, 0, kTailWaves), xv, cg, a.x, D, S.ssq_w2, a.b_q ? S.xg_next : a.xg_next,
+                     a.g_next);
+    } else {
+      resid_epilogue(sum_waves(red, 0, kTailWaves), xv, cg, a.x, D, a.ssq_w2, a.xg_next, a.g_next);
+      publish(done_w2);
+    }
     return;
   }
   b -= a.b_w2;
@@ -329,18 +477,58 @@ __global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
     const Span sp = wave_span<1>(nwd, kTailWaves, wave);
     WaveGemm<1> g;
     g.load_w(a.wqkv_next, cg, nwd, sp);
-    if (!wait_count(done_w2, (unsigned)ncg * E, a.spin_limit, a.err, &sh)) return;
-    g.mma(a.xg_next, sp, true);
-    g.to_lds(red);
-    __syncthreads();
+    if constexpr (POLL) {
+      bool ok = false;
+      for (unsigned r = 0; a.spin_limit != 0; r++) {
+        asm volatile("" ::: "memory");
+        if (__all(g.load_x(S.xg_next, sp))) { ok = true; break; }
+        if (give_up(r, a.spin_limit, a.err)) break;
+      }
+      wave_outcome(ok, a.err, wfail);
+      g.compute(sp);
+      g.to_lds(red);
+      __syncthreads();
+      if (any_failed(wfail)) return;
+    } else {
+      if (!wait_count(done_w2, (unsigned)ncg * E, a.spin_limit, a.err, &sh)) return;
+      g.mma(a.xg_next, sp, true);
+      g.to_lds(red);
+      __syncthreads();
+    }
     const float2 v = sum_waves(red, 0, kTailWaves);
     const int row = threadIdx.x >> 4, c = cg * 32 + (threadIdx.x & 15) * 2;
     *reinterpret_cast<float2*>(a.p_q + (size_t)row * N1 + c) = v;
     return;
   }
   // ---- 1 / rms of the new residual, for the next consumer ------------------------
-  if (!wait_count(done_w2, (unsigned)ncg * E, a.spin_limit, a.err, &sh)) return;
-  if (threadIdx.x < kDecRows) a.rr_next[threadIdx.x] = rr_of(a.ssq_w2, ncg, threadIdx.x, D);
+  if constexpr (POLL) {
+    if (threadIdx.x >= kDecRows) return;  // one wave: a row per lane
+    const int row = threadIdx.x;
+    float v[32];
+    bool ok = false;
+    for (unsigned r = 0; a.spin_limit != 0; r++) {
+      asm volatile("" ::: "memory");
+      bool f = true;
+#pragma unroll
+      for (int q = 0; q < 32; q++) {
+        v[q] = ld_c1(S.ssq_w2, (uint32_t)(min(q, ncg - 1) * 64 + row));
+        f &= fresh(v[q]);
+      }
+      if (__all(f)) { ok = true; break; }
+      if (give_up(r, a.spin_limit, a.err)) break;
+    }
+    if (!ok) {
+      if (row == 0) __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < 32; q++) ss += q < ncg ? v[q] : 0.f;
+    a.rr_next[row] = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+  } else {
+    if (!wait_count(done_w2, (unsigned)ncg * E, a.spin_limit, a.err, &sh)) return;
+    if (threadIdx.x < kDecRows) a.rr_next[threadIdx.x] = rr_of(a.ssq_w2, ncg, threadIdx.x, D);
+  }
 }
 
 // x [64][D] -> xg = fp16(x * g) fragments and rr = 1 / rms(x); with tok, x is
@@ -384,15 +572,20 @@ hipError_t dec_tail(const TailArgs& a, hipStream_t s) {
   if (a.D % 64 || a.D > 1024 || a.H % 64 || a.H > 2048 || a.N1 % 32) return hipErrorInvalidValue;
   if (a.b_wo != a.D / 32 || a.b_13 != a.H / 32 || a.b_w2 != a.D / 32 || (a.b_q && a.b_q != a.N1 / 32))
     return hipErrorInvalidValue;
+  if (a.poll && (!a.sets[0] || !a.sets[1])) return hipErrorInvalidValue;
   const int blocks = a.b_wo + a.b_13 + a.b_w2 + a.b_q + 1;
-  hipLaunchKernelGGL(tail_kernel, dim3(blocks), dim3(64 * kTailWaves), 0, s, a);
+  if (a.poll) hipLaunchKernelGGL(tail_kernel<true>, dim3(blocks), dim3(64 * kTailWaves), 0, s, a);
+  else hipLaunchKernelGGL(tail_kernel<false>, dim3(blocks), dim3(64 * kTailWaves), 0, s, a);
   return hipGetLastError();
 }
 
+// blocks of the chain kernel resident per CU (both forms)
 int dec_tail_blocks_per_cu() {
-  int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, tail_kernel, 64 * kTailWaves, 0) != hipSuccess) return 0;
-  return n;
+  int n0 = 0, n1 = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n0, tail_kernel<false>, 64 * kTailWaves, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n1, tail_kernel<true>, 64 * kTailWaves, 0) != hipSuccess)
+    return 0;
+  return n0 < n1 ? n0 : n1;
 }
 
 hipError_t dec_row_xg(float* x, half_t* xg, float* rr, const float* embed, const uint16_t* tok, const float* g,

@@ -98,6 +98,9 @@ struct ane_decoder {
   int* err_d = nullptr;
   int b_tail = 0;
   unsigned tail_spin = 0;
+  bool tail_poll = false;      // the data-polling form of the chain (default; ANE_DEC_TAIL=1: done counters)
+  char* tail_sets = nullptr;   // its two buffer sets, tail_set_bytes each
+  size_t tail_set_sz = 0;
   uint16_t *tok_d = nullptr, *hist_d = nullptr, *prefix_d = nullptr;
   int* ctr_d = nullptr;
   int TC = 0;
@@ -267,7 +270,12 @@ int open_impl(ane_decoder* d) {
     DCHK(op, hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, c.device));
     const int per_cu = dec_tail_blocks_per_cu();
     d->use_tail = per_cu > 0 && (long)per_cu * ncu >= d->b_tail;
-    if (const char* f = getenv("ANE_DEC_TAIL")) d->use_tail = d->use_tail && atoi(f) != 0;
+    // ANE_DEC_TAIL: 0 one launch per GEMM; 1 the chain with done counters;
+    // 2 (default) the chain whose consumers poll the data itself
+    int tail_form = 2;
+    if (const char* f = getenv("ANE_DEC_TAIL")) tail_form = atoi(f);
+    d->use_tail = d->use_tail && tail_form != 0;
+    d->tail_poll = tail_form != 1;
     // ANE_DEC_TAIL_SPIN: polls before a dependency wait times out (0: every
     // wait fails at once; for tests of the timeout path)
     d->tail_spin = kDecTailSpin;
@@ -285,6 +293,11 @@ int open_impl(ane_decoder* d) {
       DCHK(op, hipMemset(d->rr_d, 0, (size_t)R * 4));
       DCHK(op, hipMemset(d->sync, 0, (size_t)kDecTailSync * 4));
       DCHK(op, hipMemset(d->err_d, 0, 4));
+      if (d->tail_poll) {
+        d->tail_set_sz = (tail_set_bytes(D, H) + 255) & ~(size_t)255;
+        DCHK(op, dalloc(d, &d->tail_sets, 2 * d->tail_set_sz));
+        DCHK(op, hipMemset(d->tail_sets, 0xff, 2 * d->tail_set_sz));  // every dword kTailStale
+      }
     }
   }
   DCHK(op, hipDeviceSynchronize());
@@ -375,6 +388,9 @@ int enqueue_step_tail(ane_decoder* d, float* logits, uint16_t* hist) {
     t.spin_limit = d->tail_spin;
     t.D = D; t.H = H; t.N1 = N1; t.layer = l; t.L = L;
     t.b_wo = D / 32; t.b_13 = H / 32; t.b_w2 = D / 32; t.b_q = last ? 0 : N1 / 32;
+    t.poll = d->tail_poll ? 1 : 0;
+    t.sets[0] = d->tail_sets;
+    t.sets[1] = d->tail_poll ? d->tail_sets + d->tail_set_sz : nullptr;
     DCHK(op, dec_tail(t, st));
   }
   SkinnyArgs s;
@@ -399,6 +415,7 @@ int check_tail(ane_decoder* d, const char* op) {
   DCHK(op, hipMemset(d->sync, 0, (size_t)kDecTailSync * 4));
   DCHK(op, hipMemset(d->ctr_d + 2, 0, 4));
   DCHK(op, hipMemset(d->err_d, 0, 4));
+  if (d->tail_poll) DCHK(op, hipMemset(d->tail_sets, 0xff, 2 * d->tail_set_sz));  // a failed launch left sets half-used
   DCHK(op, hipDeviceSynchronize());
   return dfail(d, ANE_ERR_HIP, "storiesane decode %s: a dependency wait of the fused layer kernel timed out", op);
 }

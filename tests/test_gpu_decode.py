@@ -1,9 +1,11 @@
 """Greedy KV-cache decoding on the GPU against the CPU decode oracle
 (oracle/refdecode.c, pinned in tests/test_oracle_decode.py).
 
-The per-layer GEMM chain has two implementations -- one fused launch per
-layer (the default where every block of it fits on the GPU at once) and one
-launch per GEMM (ANE_DEC_TAIL=0) -- and the model-level tests run both.
+The per-layer GEMM chain has three implementations -- one fused launch per
+layer whose consumers poll the exchanged data itself (the default where every
+block of it fits on the GPU at once), the same launch with done counters
+(ANE_DEC_TAIL=1), and one launch per GEMM (ANE_DEC_TAIL=0) -- and the
+model-level tests run all three.
 
 Logits are compared at max-abs <= 2e-2 (fp16 weights, activations and KV
 cache; fp32 accumulation), the contract's logit tolerance.  Greedy choices
@@ -138,7 +140,7 @@ def test_long_prefix_multi_chunk_attention(form, plen, max_ctx, monkeypatch):
     assert max(errs) <= TOL
 
 
-@pytest.mark.parametrize("tail", ["1", "0"])
+@pytest.mark.parametrize("tail", ["2", "1", "0"])
 def test_generate_graph_equals_eager_steps_and_oracle_choices(tail, monkeypatch):
     monkeypatch.setenv("ANE_DEC_TAIL", tail)
     cfg = ane.tiny_decode()
@@ -165,7 +167,7 @@ def test_generate_graph_equals_eager_steps_and_oracle_choices(tail, monkeypatch)
     _check_choice(gen, ref_lg[:, 1:])
 
 
-@pytest.mark.parametrize("tail", ["1", "0"])
+@pytest.mark.parametrize("tail", ["2", "1", "0"])
 @pytest.mark.parametrize("form", ["split", "wide"])
 def test_full_size_gqa_model_matches_oracle(form, tail, monkeypatch):
     """The decode benchmark's model (12 layers, dim 768, 12/4 heads,
@@ -220,7 +222,7 @@ def test_decoder_errors():
     assert ei.value.code == _lib.ANE_ERR_CLOSED
 
 
-@pytest.mark.parametrize("tail", ["1", "0"])
+@pytest.mark.parametrize("tail", ["2", "1", "0"])
 @pytest.mark.parametrize("heads,kv_heads", [(4, 2), (6, 2), (3, 1)])
 def test_full_batch_of_64_every_sequence(heads, kv_heads, tail, monkeypatch):
     """64 sequences (every decode row) at dims 256, 384 and 192: the
@@ -256,14 +258,16 @@ def test_full_batch_of_64_every_sequence(heads, kv_heads, tail, monkeypatch):
     _check_choice(gen, g_lg[:, 1:])
 
 
-def test_fused_chain_wait_timeout_is_reported(monkeypatch):
+@pytest.mark.parametrize("tail", ["2", "1"])
+def test_fused_chain_wait_timeout_is_reported(tail, monkeypatch):
     """A dependency wait of the fused layer kernel that times out is an
     error of the call (the host forces it: a poll limit of 0 fails every
-    wait at once, and every block still exits); the decoder's counters are
-    reset, and another decoder of the same process decodes normally."""
+    wait at once, and every block still exits); the decoder's counters (or
+    buffer sets) are reset, and another decoder of the same process decodes
+    normally."""
     cfg = ane.tiny_decode()
     p, prefix = _setup(cfg, 2, 64, 61)
-    monkeypatch.setenv("ANE_DEC_TAIL", "1")
+    monkeypatch.setenv("ANE_DEC_TAIL", tail)
     monkeypatch.setenv("ANE_DEC_TAIL_SPIN", "0")
     dec = ane.Decoder(cfg, p, max_batch=2, max_ctx=128)
     try:
