@@ -128,11 +128,14 @@ struct TailSet {
   float* x_mid;     // [64][D] the residual after Wo
   float* ssq_wo;    // [D/32][64] per column group sum of squares after Wo
   float* ssq_w2;    // [D/32][64] and after W2
+  float* p_q;       // [64][N1] the next layer's q | k | v (read by attention blocks of the same launch)
+  float* rr;        // [64] 1 / rms after W2 (likewise)
 };
-__host__ __device__ inline size_t tail_set_bytes(int D, int H) {
-  return (size_t)64 * (2 * D + H) * 2 + (size_t)64 * D * 4 + (size_t)2 * (D / 32) * 64 * 4;
+__host__ __device__ inline size_t tail_set_bytes(int D, int H, int N1) {
+  return (size_t)64 * (2 * D + H) * 2 + (size_t)64 * D * 4 + (size_t)2 * (D / 32) * 64 * 4 + (size_t)64 * N1 * 4 +
+         64 * 4;
 }
-__host__ __device__ inline TailSet tail_set(void* base, int D, int H) {
+__host__ __device__ inline TailSet tail_set(void* base, int D, int H, int N1) {
   char* p = static_cast<char*>(base);
   TailSet t;
   t.xg_ffn = reinterpret_cast<half_t*>(p); p += (size_t)64 * D * 2;
@@ -140,7 +143,9 @@ __host__ __device__ inline TailSet tail_set(void* base, int D, int H) {
   t.xg_next = reinterpret_cast<half_t*>(p); p += (size_t)64 * D * 2;
   t.x_mid = reinterpret_cast<float*>(p); p += (size_t)64 * D * 4;
   t.ssq_wo = reinterpret_cast<float*>(p); p += (size_t)(D / 32) * 64 * 4;
-  t.ssq_w2 = reinterpret_cast<float*>(p);
+  t.ssq_w2 = reinterpret_cast<float*>(p); p += (size_t)(D / 32) * 64 * 4;
+  t.p_q = reinterpret_cast<float*>(p); p += (size_t)64 * N1 * 4;
+  t.rr = reinterpret_cast<float*>(p);
   return t;
 }
 struct TailArgs {
@@ -170,7 +175,20 @@ struct TailArgs {
   // are then unused, and xg_next receives the last layer's W2 output only
   int poll = 0;
   void* sets[2] = {nullptr, nullptr};
+  // data-polling form only: b_att > 0 adds the next layer's decode attention
+  // (wide form, one split) to the launch as b_att more blocks after the
+  // chain's, one per (sequence, kv head): att_next's qkv_part, qkv_ks and rr
+  // are then the launch's own (the buffer set), and p_q / rr_next above are
+  // unused.  The attention blocks issue their K / V loads at once (the cache
+  // does not depend on the chain) and poll q; every chain block is resident
+  // before any of them (lower block indices), so no chain wait depends on
+  // an attention block.
+  int b_att = 0;
+  DecAttnArgs att_next;
 };
+// Whether the attention of `a` can run inside the chain's launch (the wide
+// form with one split, G <= kGMax).
+bool dec_attention_fusable(const DecAttnArgs& a);
 constexpr int kDecTailSync = 64;
 constexpr unsigned kDecTailSpin = 1u << 20;  // polls of ~100 cycles: ~50 ms
 hipError_t dec_tail(const TailArgs& a, hipStream_t s);

@@ -7,12 +7,11 @@
 #include <algorithm>
 
 #include "decode.h"
+#include "decode_dev.h"
 
 namespace ane {
 
 namespace {
-
-constexpr float kL2E = 1.4426950408889634f;
 
 // ---- classifier GEMM with the argmax epilogue ---------------------------------
 // Block = one column group of 32 vocabulary rows x NWK waves splitting K,
@@ -320,7 +319,6 @@ __global__ __launch_bounds__(256) void finish_swiglu_kernel(const float* part, i
 // lanes with DPP row operations (no LDS traffic); scores of the G heads in
 // LDS; per-head max / sum by one wave each; P.V by v_dot2 over key pairs,
 // each thread's sums reduced across the 32 key lanes through LDS.
-constexpr int kGMax = 4;
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
@@ -345,78 +343,6 @@ __device__ __forceinline__ float grp_sum8(float v) {
   v += __shfl_xor(v, 16, 64);
   return v + xor32_f(v);
 }
-
-// Keys per split for ctx keys over nsplit splits: an even share rounded up
-// to 32 (<= the kernel's chunk, as nsplit covers max_ctx in chunk-key
-// pieces), so no split is left with a short tail while the others run full.
-__device__ __forceinline__ int dec_chunk(int ctx, int nsplit) {
-  return ((ctx + nsplit - 1) / nsplit + 31) & ~31;
-}
-
-// The step's projections from the QKV partials, one column pair per thread:
-// q of the G heads (threads < 32 G) and, in the block whose split holds
-// position pos, the new k (next 32) and v (next 32).  Summed in split order
-// as the finish kernels do, RoPE on q and k.  issue() loads the partials and
-// RoPE factors -- only in the waves holding projection columns, so fewer
-// loads share the CU's memory pipeline with the K / V rows (the q loads
-// still return late under a block's worth of K / V misses: the staging
-// barrier waits for them).  finish() sums, rotates and writes q, the new
-// k / v rows to LDS and the new rows to cache row `row` of the split.
-template <int G, int QS>
-struct QkvProj {
-  float pe[QS], po[QS], cs = 0.f, sn = 0.f, rr = 1.f;
-  int col = -1;
-  bool rot = false;
-  __device__ __forceinline__ void issue(const DecAttnArgs& a, int b, int kvh, int tid, int pos, bool own) {
-    const int D = a.NH * 64, KVD = a.NKV * 64, N1 = D + 2 * KVD;
-    if (tid < G * 32) col = kvh * G * 64 + 2 * tid;
-    else if (own && tid < G * 32 + 32) col = D + kvh * 64 + 2 * (tid - G * 32);
-    else if (own && tid < G * 32 + 64) col = D + KVD + kvh * 64 + 2 * (tid - G * 32 - 32);
-    rot = col >= 0 && col < D + KVD;
-    const int cc = col < 0 ? 0 : col;
-    const float* pp = a.qkv_part + (size_t)b * N1 + cc;
-    if (tid < G * 32 + 64) {
-#pragma unroll
-      for (int s = 0; s < QS; s++) {  // unconditional loads, split index clamped
-        const size_t o = (size_t)min(s, a.qkv_ks - 1) * kDecRows * N1;
-        pe[s] = pp[o];
-        po[s] = pp[o + 1];
-      }
-      const int ri = (cc & 63) >> 1;
-      cs = a.rope_cos[pos * 32 + ri];
-      sn = a.rope_sin[pos * 32 + ri];
-      if (a.rr) rr = a.rr[b];
-    }
-  }
-  __device__ __forceinline__ void finish(const DecAttnArgs& a, int tid, half_t (*qs)[64], half_t* knew, half_t* vnew,
-                                         half_t* Kb, half_t* Vb, int row) const {
-    if (col < 0) return;
-    float e = 0.f, o = 0.f;
-#pragma unroll
-    for (int s = 0; s < QS; s++) {
-      e += s < a.qkv_ks ? pe[s] : 0.f;
-      o += s < a.qkv_ks ? po[s] : 0.f;
-    }
-    e *= rr;  // the partials are of fp16(x * gain): the norm's 1 / rms applied here
-    o *= rr;
-    if (rot) {
-      const float e2 = e * cs - o * sn, o2 = o * cs + e * sn;
-      e = e2;
-      o = o2;
-    }
-    half2v w;
-    w[0] = (half_t)e;
-    w[1] = (half_t)o;
-    if (tid < G * 32) {
-      *reinterpret_cast<half2v*>(&qs[tid >> 5][2 * (tid & 31)]) = w;
-    } else {
-      const bool isk = tid < G * 32 + 32;
-      const int d = 2 * ((tid - G * 32) & 31);
-      *reinterpret_cast<half2v*>((isk ? knew : vnew) + d) = w;
-      *reinterpret_cast<half2v*>((isk ? Kb : Vb) + (size_t)row * 64 + d) = w;  // cache row pos
-    }
-  }
-};
 
 // One block of NT threads per (sequence, kv head, key split): KP = NT / 8
 // keys per pass, NIT passes, so a split holds at most KP * NIT keys.  With
@@ -601,183 +527,6 @@ __device__ __forceinline__ void dec_attn_body(const DecAttnArgs& a) {
   }
 }
 
-// Wide form, one 1024-thread block per (sequence, kv head, split of up to
-// kDecWideChunk keys).  Key tile t (16 keys) belongs to wave t % 16, which
-// does all of that tile's work:
-//   * scores S^T = K Q^T on v_mfma_f32_16x16x32_f16: A = 16 keys x 32 dims
-//     straight from the cache rows (lane: key lane % 16, dims 8 (lane / 16)
-//     + [0, 8)), B = the G query heads padded to 16 columns;
-//   * the wave's own softmax over its keys (maximum and sum per head);
-//   * O = P V on v_mfma_f32_16x16x16_f16.  The score accumulator already has
-//     the A layout of P (head lane % 16, keys 4 (lane / 16) + [0, 4)), so the
-//     probabilities stay in their lanes; each V tile goes through a per-wave
-//     LDS tile, read back transposed (ds_read_b64_tr_b16) as the B operand.
-// The waves' (maximum, sum, O) meet once in LDS at the end, rescaled to the
-// block maximum.  No block-wide barrier separates the K loads from P V, so
-// each wave works on its rows as they arrive.
-template <int G, bool DIRECT>
-__device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a) {
-  constexpr int NT = 1024, NW = NT / 64;
-  constexpr int TW = (kDecWideChunk / 16 + NW - 1) / NW;  // key tiles per wave
-  const int b = blockIdx.x, kvh = blockIdx.y, sp = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ctx = a.ctr[0] + 1;
-  const int chunk = dec_chunk(ctx, a.nsplit);
-  const int c0 = sp * chunk;
-  if (c0 >= ctx) return;  // uniform over the block, before any barrier
-  const int n = min(chunk, ctx - c0);
-  __shared__ half_t qs[G][64];
-  // per-wave V tiles [16 keys][64 dims], two used in turn; 16-byte chunk c
-  // of row r at chunk slot c ^ (r & 7)
-  __shared__ __attribute__((aligned(16))) half_t vt[NW][2][16 * 64];
-  __shared__ float wo[NW][G][64];  // each wave's O (scaled to its own maximum)
-  __shared__ float wm[NW][G], wl[NW][G];
-  __shared__ __attribute__((aligned(16))) half_t knew[64], vnew[64];
-  const float sl2 = a.scale * kL2E;
-  const size_t cache0 = ((size_t)b * a.NKV + kvh) * a.max_ctx;
-  half_t* Kb = a.kc + (cache0 + c0) * 64;
-  half_t* Vb = a.vc + (cache0 + c0) * 64;
-  const int pos = ctx - 1;
-  const bool own = pos - c0 < n;
-  const int kr = lane & 15, kq = lane >> 4;  // K fragment: key kr, dims 8 kq (+ 32)
-  const int vr = lane >> 2, vc = lane & 3;   // V tile row: key vr, dims 16 vc + [0, 16)
-  // q and the new k / v rows first, staged before any K / V load is issued:
-  // a load issued beside the block's K / V misses returns only after most of
-  // them (measured: the staging barrier then completes ~10 us into a 17 us
-  // kernel, and the whole softmax and P V run after the last row arrives).
-  QkvProj<G, 8> qp;
-  qp.issue(a, b, kvh, tid, pos, own);
-  qp.finish(a, tid, qs, knew, vnew, Kb, Vb, pos - c0);
-  __syncthreads();
-  // Then every K row, then every V row.  Unconditional loads (key index
-  // clamped; keys past n unused).
-  half8 ka[TW][2], va[TW][2];
-#pragma unroll
-  for (int u = 0; u < TW; u++) {
-    const half_t* row = Kb + (size_t)min((wave + NW * u) * 16 + kr, n - 1) * 64 + kq * 8;
-    ka[u][0] = ld_h8(row);
-    ka[u][1] = ld_h8(row + 32);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int u = 0; u < TW; u++) {
-    const half_t* row = Vb + (size_t)min((wave + NW * u) * 16 + vr, n - 1) * 64 + vc * 16;
-    va[u][0] = ld_h8(row);
-    va[u][1] = ld_h8(row + 8);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  // Row pos is the last row of the split and every key index past n read it
-  // too (clamped): those take the new k / v (the row read may be stale, or
-  // the new one -- another thread stored it just before -- and a NaN in a
-  // stale row must not reach the sums), by a select at each use.
-  const int jrep = own ? pos - c0 : 1 << 30;
-  half8 kn0 = {}, kn1 = {}, vn0 = {}, vn1 = {};
-  if (own) {
-    kn0 = ld_h8(knew + kq * 8);
-    kn1 = ld_h8(knew + 32 + kq * 8);
-    vn0 = ld_h8(vnew + vc * 16);
-    vn1 = ld_h8(vnew + vc * 16 + 8);
-  }
-  half8 qb0, qb1;  // B operand: head kr (zero columns past G), dims as A
-  {
-    const int h = kr < G ? kr : 0;
-    const half8 z = {};
-    qb0 = kr < G ? ld_h8(&qs[h][kq * 8]) : z;
-    qb1 = kr < G ? ld_h8(&qs[h][32 + kq * 8]) : z;
-  }
-  floatx4 st[TW];
-  float m = -INFINITY;
-#pragma unroll
-  for (int u = 0; u < TW; u++) {
-    const int kb = (wave + NW * u) * 16;
-    const bool rep = kb + kr >= jrep;
-    floatx4 c = {0.f, 0.f, 0.f, 0.f};
-    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(rep ? kn0 : ka[u][0], qb0, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(rep ? kn1 : ka[u][1], qb1, c, 0, 0, 0);
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int j = kb + 4 * kq + i;
-      st[u][i] = j < n && kr < G ? c[i] * sl2 : -INFINITY;
-      m = fmaxf(m, st[u][i]);
-    }
-  }
-  // the wave's maximum per head (the lanes of head lane % 16); a wave with
-  // no valid key, and the padding columns, have p = exp2(-inf) = 0
-  m = fmaxf(m, __shfl_xor(m, 16, 64));
-  m = fmaxf(m, xor32_f(m));
-  const float mz = m == -INFINITY ? 0.f : m;
-  // probabilities rounded to fp16 (the P V operand); the sum adds the same
-  // rounded values
-  half4 pa[TW];
-  float l = 0.f;
-#pragma unroll
-  for (int u = 0; u < TW; u++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      pa[u][i] = (half_t)__builtin_amdgcn_exp2f(st[u][i] - mz);
-      l += (float)pa[u][i];
-    }
-  l += __shfl_xor(l, 16, 64);
-  l += xor32_f(l);
-  // O[head][dim] += P[head][key] V[key][dim], 16 dims per MFMA: lane
-  // 16 g + j takes V[4 g + e][16 db + j] (e = 0..3), which the transposed
-  // read gives when lane l addresses row l / 4, halves 16 db + 4 (l % 4)
-  floatx4 o[4];
-#pragma unroll
-  for (int db = 0; db < 4; db++) o[db] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const int rr = lane >> 2, rq = lane & 3;
-#pragma unroll
-  for (int u = 0; u < TW; u++) {
-    half_t* t = vt[wave][u & 1];
-    const bool rep = (wave + NW * u) * 16 + vr >= jrep;
-    st_h8(t + vr * 64 + (((2 * vc) ^ (vr & 7)) << 3), rep ? vn0 : va[u][0]);
-    st_h8(t + vr * 64 + (((2 * vc + 1) ^ (vr & 7)) << 3), rep ? vn1 : va[u][1]);
-    // the wave's stores precede its reads (LDS runs one wave's operations
-    // in order); the fence keeps the compiler from reordering them
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-    for (int db = 0; db < 4; db++) {
-      const int cch = 2 * db + (rq >> 1);
-      const short4v bv = ds_read_tr16(t + rr * 64 + ((cch ^ (rr & 7)) << 3) + 4 * (rq & 1));
-      o[db] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[u], __builtin_bit_cast(half4, bv), o[db], 0, 0, 0);
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-  }
-  // the merge: O rows (heads) 4 (lane / 16) + i, column 16 db + lane % 16;
-  // heads < G sit in lanes 0..15
-  if (lane < 16) {
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-#pragma unroll
-      for (int i = 0; i < G; i++) wo[wave][i][16 * db + lane] = o[db][i];
-  }
-  if (lane < G) {
-    wm[wave][lane] = m;
-    wl[wave][lane] = l;
-  }
-  __syncthreads();
-  if (tid < G * 64) {
-    const int h = tid >> 6, d = tid & 63;
-    float mt = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < NW; w++) mt = fmaxf(mt, wm[w][h]);  // finite: key 0 is valid
-    float ot = 0.f, lt = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; w++) {
-      const float f = __builtin_amdgcn_exp2f(wm[w][h] - mt);  // 0 for a wave without keys
-      ot += f * wo[w][h][d];
-      lt += f * wl[w][h];
-    }
-    if constexpr (DIRECT) {
-      a.att[act_frag_off(b, (kvh * G + h) * 64 + d)] = (half_t)(ot / lt);
-    } else {
-      float* out = a.part + (((size_t)b * a.NH + kvh * G + h) * a.nsplit + sp) * 66;
-      out[d] = ot;
-      if (d == 0) { out[64] = mt; out[65] = lt; }
-    }
-  }
-}
-
 // Narrow form (batches too small for the wide one): 256 threads, 8 passes
 // of 32 keys = kDecChunk keys per split, QS = 8 or kMaxSplits.
 template <int G>
@@ -793,7 +542,8 @@ __global__ __launch_bounds__(256) void dec_attn_kernel16(DecAttnArgs a) {
 // used when the batch alone gives enough blocks to fill the chip.
 template <int G, bool DIRECT>
 __global__ __launch_bounds__(1024) void dec_attn_wide_kernel(DecAttnArgs a) {
-  dec_attn_wide_body<G, DIRECT>(a);
+  __shared__ WideLds lds;
+  dec_attn_wide_body<G, DIRECT, false>(a, blockIdx.x, blockIdx.y, blockIdx.z, lds);
 }
 
 __global__ __launch_bounds__(64) void dec_combine_kernel(DecAttnArgs a) {
@@ -1104,6 +854,12 @@ hipError_t dec_norm(const float* x, half_t* xn, const float* g, int nb, int D, h
   if (D > 1024) return hipErrorInvalidValue;
   hipLaunchKernelGGL(norm_kernel, dim3(nb), dim3(256), 0, s, x, xn, g, D);
   return hipGetLastError();
+}
+
+bool dec_attention_fusable(const DecAttnArgs& a) {
+  if (a.NKV <= 0 || a.NH % a.NKV || a.NH / a.NKV > kGMax) return false;
+  const int wsplit = (a.max_ctx + kDecWideChunk - 1) / kDecWideChunk;
+  return wsplit == 1 && wsplit <= a.nsplit && (a.form == 1 || (a.form == 0 && a.nb * a.NKV >= kDecWideMinBlocks));
 }
 
 hipError_t dec_attention(const DecAttnArgs& a, hipStream_t s) {

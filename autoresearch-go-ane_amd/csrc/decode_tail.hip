@@ -37,6 +37,7 @@
 #include <math.h>
 
 #include "decode.h"
+#include "decode_dev.h"
 
 namespace ane {
 
@@ -44,38 +45,6 @@ namespace {
 
 __device__ __forceinline__ unsigned ld_relaxed(const unsigned* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// ---- device-coherent accesses of shared data (uniform base + per-lane byte offset)
-constexpr int kSc1 = 16;  // cache policy bit sc1: device scope
-typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
-}
-__device__ __forceinline__ float ld_c1(const float* base, uint32_t elem) {
-  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsrc(base), elem * 4u, 0, kSc1));
-}
-// A stored dword never equals kTailStale (the data-polling form's "not yet
-// written"): the one NaN pattern that would is replaced by another quiet NaN.
-__device__ __forceinline__ uint32_t not_stale(uint32_t v, uint32_t nan) { return v == kTailStale ? nan : v; }
-__device__ __forceinline__ bool fresh(float v) { return __float_as_uint(v) != kTailStale; }
-__device__ __forceinline__ bool fresh8(half8 v) {
-  const u32x4v u = __builtin_bit_cast(u32x4v, v);
-  return (u[0] != kTailStale) & (u[1] != kTailStale) & (u[2] != kTailStale) & (u[3] != kTailStale);
-}
-__device__ __forceinline__ void st_c1(float* base, uint32_t elem, float v) {
-  __builtin_amdgcn_raw_buffer_store_b32(not_stale(__float_as_uint(v), 0x7FC00000u), rsrc(base), elem * 4u, 0, kSc1);
-}
-__device__ __forceinline__ half8 ld_ch8(const half_t* base, uint32_t elem) {
-  const u32x4v a = __builtin_amdgcn_raw_buffer_load_b128(rsrc(base), elem * 2u, 0, kSc1);
-  return __builtin_bit_cast(half8, a);
-}
-// this wave's stores have completed (s_waitcnt vmcnt(0)); the empty asm keeps
-// the compiler from moving memory operations across
-__device__ __forceinline__ void drain_stores() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0x0F70);
-  asm volatile("" ::: "memory");
 }
 
 // Polls *c until it reaches `target` (wave 0; at most `limit` polls of ~100
@@ -112,15 +81,6 @@ __device__ void publish(unsigned* done) {
   if (threadIdx.x == 0) __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Data-polling form: a wave re-issues its device-coherent input loads in
-// rounds until none of them returns a stale dword.  give_up() after round r:
-// true after `limit` rounds or when another block has failed (else a short
-// sleep before the next round).  limit 0 fails before the first round.
-__device__ __forceinline__ bool give_up(unsigned r, unsigned limit, const int* err) {
-  if (r + 1 >= limit || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return true;
-  __builtin_amdgcn_s_sleep(1);
-  return false;
-}
 // This wave's outcome into its flag (read after the next barrier by
 // any_failed); a wave whose inputs never arrived also sets the launch's error.
 __device__ __forceinline__ void wave_outcome(bool ok, int* err, int* wfail) {
@@ -326,12 +286,29 @@ __device__ __forceinline__ void x_to_lds(const float* x, int cg, int D, float (*
 // consumer wave re-reads its inputs until none is stale, so a phase costs the
 // producers' stores reaching the shared level and one read round, instead of
 // a store drain, a counter update, a counter read and then the data read.
-template <bool POLL>
+// The chain's LDS, or (for an attention block of the fused launch) the wide
+// attention's.
+struct ChainLds {
+  float red[kTailWaves][64][32];
+  float ssq_s[32][kDecRows];
+  float xs[2][64 * kTailWaves];
+  int sh, wfail[kTailWaves];
+};
+union TailLds {
+  ChainLds c;
+  WideLds w;
+};
+
+// GA > 0 (data-polling form only): the launch also holds the next layer's
+// attention for G = GA query heads per kv head (TailArgs::b_att).
+template <bool POLL, int GA>
 __global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
-  __shared__ float red[kTailWaves][64][32];
-  __shared__ float ssq_s[32][kDecRows];
-  __shared__ float xs[2][64 * kTailWaves];
-  __shared__ int sh, wfail[kTailWaves];
+  __shared__ TailLds lds;
+  auto& red = lds.c.red;
+  auto& ssq_s = lds.c.ssq_s;
+  auto& xs = lds.c.xs;
+  auto& sh = lds.c.sh;
+  auto& wfail = lds.c.wfail;
   if (__hip_atomic_load(a.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) return;  // an earlier wait failed
   const int D = a.D, H = a.H, N1 = a.N1, ncg = D / 32, npair = H / 32;
   const int nwd = D / 64, nwh = H / 64;
@@ -342,12 +319,12 @@ __global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
   unsigned* done_w2 = a.sync + 2;
   TailSet S{};
   if constexpr (POLL) {
-    S = tail_set(a.sets[E & 1], D, H);
+    S = tail_set(a.sets[E & 1], D, H, N1);
     // the other set back to stale for the next use: its readers belong to
     // the previous launch, which has finished
     const __amdgpu_buffer_rsrc_t ro = rsrc(a.sets[(E & 1) ^ 1]);
     const u32x4v st = {kTailStale, kTailStale, kTailStale, kTailStale};
-    const uint32_t n16 = (uint32_t)(tail_set_bytes(D, H) / 16);
+    const uint32_t n16 = (uint32_t)(tail_set_bytes(D, H, N1) / 16);
     for (uint32_t k = blockIdx.x * blockDim.x + threadIdx.x; k < n16; k += gridDim.x * blockDim.x)
       __builtin_amdgcn_raw_buffer_store_b128(st, ro, k * 16u, 0, kSc1);
   }
@@ -497,8 +474,25 @@ __global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
     }
     const float2 v = sum_waves(red, 0, kTailWaves);
     const int row = threadIdx.x >> 4, c = cg * 32 + (threadIdx.x & 15) * 2;
-    *reinterpret_cast<float2*>(a.p_q + (size_t)row * N1 + c) = v;
+    if (POLL && a.b_att) {  // for the attention blocks of this launch
+      st_c1(S.p_q, (uint32_t)(row * N1 + c), v.x);
+      st_c1(S.p_q, (uint32_t)(row * N1 + c + 1), v.y);
+    } else {
+      *reinterpret_cast<float2*>(a.p_q + (size_t)row * N1 + c) = v;
+    }
     return;
+  }
+  b -= a.b_q;
+  if constexpr (POLL && GA > 0) {  // ---- the next layer's attention -------------------
+    if (b > 0) {
+      const int i = b - 1;
+      DecAttnArgs aa = a.att_next;
+      aa.qkv_part = S.p_q;
+      aa.qkv_ks = 1;
+      aa.rr = S.rr;
+      dec_attn_wide_body<GA, true, true>(aa, i % aa.nb, i / aa.nb, 0, lds.w, a.spin_limit, a.err);
+      return;
+    }
   }
   // ---- 1 / rms of the new residual, for the next consumer ------------------------
   if constexpr (POLL) {
@@ -524,7 +518,9 @@ __global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
     float ss = 0.f;
 #pragma unroll
     for (int q = 0; q < 32; q++) ss += q < ncg ? v[q] : 0.f;
-    a.rr_next[row] = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+    const float r = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+    if (a.b_att) st_c1(S.rr, (uint32_t)row, r);
+    else a.rr_next[row] = r;
   } else {
     if (!wait_count(done_w2, (unsigned)ncg * E, a.spin_limit, a.err, &sh)) return;
     if (threadIdx.x < kDecRows) a.rr_next[threadIdx.x] = rr_of(a.ssq_w2, ncg, threadIdx.x, D);
@@ -573,19 +569,41 @@ hipError_t dec_tail(const TailArgs& a, hipStream_t s) {
   if (a.b_wo != a.D / 32 || a.b_13 != a.H / 32 || a.b_w2 != a.D / 32 || (a.b_q && a.b_q != a.N1 / 32))
     return hipErrorInvalidValue;
   if (a.poll && (!a.sets[0] || !a.sets[1])) return hipErrorInvalidValue;
-  const int blocks = a.b_wo + a.b_13 + a.b_w2 + a.b_q + 1;
-  if (a.poll) hipLaunchKernelGGL(tail_kernel<true>, dim3(blocks), dim3(64 * kTailWaves), 0, s, a);
-  else hipLaunchKernelGGL(tail_kernel<false>, dim3(blocks), dim3(64 * kTailWaves), 0, s, a);
+  int ga = 0;
+  if (a.b_att) {
+    const DecAttnArgs& n = a.att_next;
+    if (!a.poll || !a.b_q || !dec_attention_fusable(n) || a.b_att != n.nb * n.NKV || n.nsplit != 1)
+      return hipErrorInvalidValue;
+    ga = n.NH / n.NKV;
+  }
+  const int blocks = a.b_wo + a.b_13 + a.b_w2 + a.b_q + 1 + a.b_att;
+  const dim3 g(blocks), t(64 * kTailWaves);
+  switch (a.poll ? ga + 1 : 0) {
+    case 0: hipLaunchKernelGGL((tail_kernel<false, 0>), g, t, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((tail_kernel<true, 0>), g, t, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((tail_kernel<true, 1>), g, t, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((tail_kernel<true, 2>), g, t, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((tail_kernel<true, 3>), g, t, 0, s, a); break;
+    default: hipLaunchKernelGGL((tail_kernel<true, 4>), g, t, 0, s, a); break;
+  }
   return hipGetLastError();
 }
 
-// blocks of the chain kernel resident per CU (both forms)
+// blocks of the chain kernel resident per CU (every form)
 int dec_tail_blocks_per_cu() {
-  int n0 = 0, n1 = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n0, tail_kernel<false>, 64 * kTailWaves, 0) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&n1, tail_kernel<true>, 64 * kTailWaves, 0) != hipSuccess)
-    return 0;
-  return n0 < n1 ? n0 : n1;
+  int m = 1 << 30;
+  auto occ = [&](const void* k) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k, 64 * kTailWaves, 0) != hipSuccess) n = 0;
+    m = n < m ? n : m;
+  };
+  occ((const void*)tail_kernel<false, 0>);
+  occ((const void*)tail_kernel<true, 0>);
+  occ((const void*)tail_kernel<true, 1>);
+  occ((const void*)tail_kernel<true, 2>);
+  occ((const void*)tail_kernel<true, 3>);
+  occ((const void*)tail_kernel<true, 4>);
+  return m;
 }
 
 hipError_t dec_row_xg(float* x, half_t* xg, float* rr, const float* embed, const uint16_t* tok, const float* g,

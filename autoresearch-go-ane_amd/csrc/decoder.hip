@@ -81,6 +81,8 @@ struct ane_decoder {
   float *rope_cos = nullptr, *rope_sin = nullptr;
   float* x = nullptr;
   half_t *xn = nullptr, *att = nullptr, *gate = nullptr;
+  half_t* att2 = nullptr;  // the fused chain's odd layers' attention output (the next chain reads the other)
+  bool fuse_att = true;    // the next layer's attention inside each chain launch (ANE_DEC_FUSE_ATT=0: its own launch)
   float* apart = nullptr;
   float* kpart = nullptr;  // split-K partials of the decode-step GEMMs
   size_t kpart_cap = 0;
@@ -276,6 +278,7 @@ int open_impl(ane_decoder* d) {
     if (const char* f = getenv("ANE_DEC_TAIL")) tail_form = atoi(f);
     d->use_tail = d->use_tail && tail_form != 0;
     d->tail_poll = tail_form != 1;
+    if (const char* f = getenv("ANE_DEC_FUSE_ATT")) d->fuse_att = atoi(f) != 0;
     // ANE_DEC_TAIL_SPIN: polls before a dependency wait times out (0: every
     // wait fails at once; for tests of the timeout path)
     d->tail_spin = kDecTailSpin;
@@ -294,9 +297,11 @@ int open_impl(ane_decoder* d) {
       DCHK(op, hipMemset(d->sync, 0, (size_t)kDecTailSync * 4));
       DCHK(op, hipMemset(d->err_d, 0, 4));
       if (d->tail_poll) {
-        d->tail_set_sz = (tail_set_bytes(D, H) + 255) & ~(size_t)255;
+        d->tail_set_sz = (tail_set_bytes(D, H, N1) + 255) & ~(size_t)255;
         DCHK(op, dalloc(d, &d->tail_sets, 2 * d->tail_set_sz));
         DCHK(op, hipMemset(d->tail_sets, 0xff, 2 * d->tail_set_sz));  // every dword kTailStale
+        DCHK(op, dalloc(d, &d->att2, (size_t)R * D));
+        DCHK(op, hipMemset(d->att2, 0, (size_t)R * D * 2));
       }
     }
   }
@@ -364,20 +369,28 @@ int enqueue_step_tail(ane_decoder* d, float* logits, uint16_t* hist) {
   DCHK(op, dec_row_xg(d->x, d->xg_att, d->rr_d, d->P + d->off_embed, d->tok_d, d->P + d->off[0].g_att, nb, D, d->V,
                       st));
   DCHK(op, skinny_partials(d->xg_att, d->fwqkv, d->kpart, d->kpart_cap, N1, D, st));
-  for (int l = 0; l < L; l++) {
-    const DecLayerOff& o = d->off[l];
+  auto attn_args = [&](int l, half_t* out) {
     DecAttnArgs aa;
     aa.qkv_part = d->kpart; aa.qkv_ks = l == 0 ? skinny_splits(N1, D) : 1; aa.rr = d->rr_d;
     aa.rope_cos = d->rope_cos; aa.rope_sin = d->rope_sin;
     aa.kc = d->kc + (size_t)l * d->B * d->NKV * d->C * 64;
     aa.vc = d->vc + (size_t)l * d->B * d->NKV * d->C * 64;
-    aa.ctr = d->ctr_d; aa.part = d->apart; aa.att = d->att; aa.nb = nb;
+    aa.ctr = d->ctr_d; aa.part = d->apart; aa.att = out; aa.nb = nb;
     aa.NH = d->NH; aa.NKV = d->NKV; aa.max_ctx = d->C; aa.nsplit = d->nsplit; aa.scale = 0.125f;
     aa.form = d->attn_form;
-    DCHK(op, dec_attention(aa, st));
+    return aa;
+  };
+  // With the data-polling chain, the next layer's attention (wide form, one
+  // split) runs inside each chain launch; its output alternates between att
+  // and att2 so that a launch never writes what its own Wo blocks read.
+  const bool fuse = d->tail_poll && d->fuse_att && d->att2 && dec_attention_fusable(attn_args(1 < L ? 1 : 0, d->att));
+  auto att_of = [&](int l) { return fuse && (l & 1) ? d->att2 : d->att; };
+  DCHK(op, dec_attention(attn_args(0, att_of(0)), st));
+  for (int l = 0; l < L; l++) {
+    const DecLayerOff& o = d->off[l];
     const bool last = l + 1 == L;
     TailArgs t;
-    t.att = d->att; t.x = d->x;
+    t.att = att_of(l); t.x = d->x;
     t.wo = d->fwo + (size_t)l * D * D; t.w13 = d->fw13 + (size_t)l * 2 * H * D; t.w2 = d->fw2 + (size_t)l * D * H;
     t.wqkv_next = last ? nullptr : d->fwqkv + (size_t)(l + 1) * N1 * D;
     t.g_ffn = d->P + o.g_ffn;
@@ -391,7 +404,13 @@ int enqueue_step_tail(ane_decoder* d, float* logits, uint16_t* hist) {
     t.poll = d->tail_poll ? 1 : 0;
     t.sets[0] = d->tail_sets;
     t.sets[1] = d->tail_poll ? d->tail_sets + d->tail_set_sz : nullptr;
+    if (fuse && !last) {
+      t.att_next = attn_args(l + 1, att_of(l + 1));
+      t.att_next.nsplit = 1;
+      t.b_att = nb * d->NKV;
+    }
     DCHK(op, dec_tail(t, st));
+    if (!fuse && !last) DCHK(op, dec_attention(attn_args(l + 1, d->att), st));
   }
   SkinnyArgs s;
   memset(&s, 0, sizeof s);
