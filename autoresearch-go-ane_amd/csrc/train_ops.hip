@@ -2,6 +2,8 @@
 // Rows are token-major [T, D]; one wave per row, float4 per lane.
 #include "train_ops.h"
 
+#include <cstdlib>
+
 namespace ane {
 
 namespace {
@@ -115,6 +117,81 @@ __global__ __launch_bounds__(256) void norm_bwd_kernel(NormBwdArgs a) {
   if (a.lam_part && threadIdx.x < 2)
     a.lam_part[blockIdx.x * 2 + threadIdx.x] =
         lsh[0][threadIdx.x] + lsh[1][threadIdx.x] + lsh[2][threadIdx.x] + lsh[3][threadIdx.x];
+}
+
+// The gain form without the lambda, value-embedding and second-addend terms
+// (llama2: the final norm, and each layer's two norms with addend = the
+// residual gradient): one wave per row, kNormBwdRows waves per block, and
+// every load of the row -- dy, x, the gain and the addend -- issued before
+// its two reductions, so a row costs one memory round trip (the general
+// kernel above loads the addend after them, two rows per wave in turn).
+// The block's dgain partial sums its rows in row order.
+template <bool ADD>
+__global__ __launch_bounds__(64 * kNormBwdRows) void norm_bwd_gain_kernel(NormBwdArgs a) {
+  __shared__ float gsh[kNormBwdRows][1024];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int D = a.D, nv = D / 4;
+  const int t = blockIdx.x * kNormBwdRows + wave;
+  const size_t ro = (size_t)min(t, a.T - 1) * D;  // a row past T (last block) reads row T - 1, stores nothing
+  float4 dy[kMaxVec], xv[kMaxVec], gv[kMaxVec], ad[kMaxVec];
+#pragma unroll
+  for (int k = 0; k < kMaxVec; k++) {
+    if (64 * k < nv) {  // uniform; lanes past nv read a valid group, their values unused
+      const int i = min(lane + 64 * k, nv - 1);
+      dy[k] = reinterpret_cast<const float4*>(a.dy + ro)[i];
+      xv[k] = reinterpret_cast<const float4*>(a.x + ro)[i];
+      gv[k] = reinterpret_cast<const float4*>(a.gain)[i];
+      if constexpr (ADD) ad[k] = reinterpret_cast<const float4*>(a.addend + ro)[i];
+    }
+  }
+  const float alpha = ADD ? (a.alpha_p ? *a.alpha_p : a.alpha) : 0.f;
+  float ss = 0.f, dot = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxVec; k++) {
+    if (64 * k < nv && lane + 64 * k < nv) {
+      ss += xv[k].x * xv[k].x + xv[k].y * xv[k].y + xv[k].z * xv[k].z + xv[k].w * xv[k].w;
+      dot += dy[k].x * xv[k].x * gv[k].x + dy[k].y * xv[k].y * gv[k].y + dy[k].z * xv[k].z * gv[k].z +
+             dy[k].w * xv[k].w * gv[k].w;
+    }
+  }
+  ss = wave_sum_dpp(ss);
+  dot = wave_sum_dpp(dot);
+  const float rrms = 1.0f / sqrtf(ss / (float)D + 1e-5f);
+  const float c = dot * rrms * rrms / (float)D;
+  const bool row_ok = t < a.T;
+#pragma unroll
+  for (int k = 0; k < kMaxVec; k++) {
+    const int i = lane + 64 * k;
+    if (64 * k >= nv) continue;
+    float o[4] = {(dy[k].x - xv[k].x * c) * rrms * gv[k].x, (dy[k].y - xv[k].y * c) * rrms * gv[k].y,
+                  (dy[k].z - xv[k].z * c) * rrms * gv[k].z, (dy[k].w - xv[k].w * c) * rrms * gv[k].w};
+    if constexpr (ADD) {
+      o[0] += alpha * ad[k].x; o[1] += alpha * ad[k].y; o[2] += alpha * ad[k].z; o[3] += alpha * ad[k].w;
+    }
+    if (i < nv) {
+      const bool live = row_ok;
+      gsh[wave][4 * i] = live ? dy[k].x * xv[k].x * rrms : 0.f;
+      gsh[wave][4 * i + 1] = live ? dy[k].y * xv[k].y * rrms : 0.f;
+      gsh[wave][4 * i + 2] = live ? dy[k].z * xv[k].z * rrms : 0.f;
+      gsh[wave][4 * i + 3] = live ? dy[k].w * xv[k].w * rrms : 0.f;
+      if (row_ok) {
+        reinterpret_cast<float4*>(a.out + ro)[i] = make_float4(o[0], o[1], o[2], o[3]);
+        if (a.out_h) {
+          half4 hv;
+#pragma unroll
+          for (int u = 0; u < 4; u++) hv[u] = (half_t)o[u];
+          reinterpret_cast<half4*>(a.out_h + ro)[i] = hv;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < D; i += 64 * kNormBwdRows) {
+    float g = gsh[0][i];
+#pragma unroll
+    for (int w = 1; w < kNormBwdRows; w++) g += gsh[w][i];
+    a.dgain_part[(size_t)blockIdx.x * D + i] = g;
+  }
 }
 
 // One block per 64 columns: 16 waves each sum every 16th partial row of
@@ -514,9 +591,24 @@ __global__ __launch_bounds__(256) void shadow_kernel(const ShadowJob* jobs, int 
 
 }  // namespace
 
+// ANE_NORM_BWD_FAST=0: every RMSNorm backward through the general kernel
+// (read once per process)
+static bool norm_bwd_fast() {
+  static const bool on = [] {
+    const char* f = getenv("ANE_NORM_BWD_FAST");
+    return !f || atoi(f) != 0;
+  }();
+  return on;
+}
+
 hipError_t norm_bwd(const NormBwdArgs& a, hipStream_t s) {
-  if (a.D % 64 || a.D > 1024) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(norm_bwd_kernel, dim3(norm_bwd_blocks(a.T)), dim3(256), 0, s, a);
+  if (a.D % 64 || a.D > 1024 || a.T <= 0) return hipErrorInvalidValue;
+  const dim3 g(norm_bwd_blocks(a.T));
+  const bool gain_only = a.gain && a.dgain_part && !a.addend2 && !a.ve_dx && !a.lam_x && !a.lam_x0 && !a.lam_part &&
+                         !a.gx0 && norm_bwd_fast();
+  if (gain_only && a.addend) hipLaunchKernelGGL(norm_bwd_gain_kernel<true>, g, dim3(64 * kNormBwdRows), 0, s, a);
+  else if (gain_only) hipLaunchKernelGGL(norm_bwd_gain_kernel<false>, g, dim3(64 * kNormBwdRows), 0, s, a);
+  else hipLaunchKernelGGL(norm_bwd_kernel, g, dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
