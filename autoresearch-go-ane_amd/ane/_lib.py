@@ -110,6 +110,7 @@ SIGNATURES = {
     "ane_debug_attention": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_double, C.c_float, C.c_int, _u16,
                                       _u16, _fp]),
     "ane_debug_transpose2": (C.c_int, [C.c_int, C.c_int, _u16, _u16, C.c_int, C.c_int, _u16, _u16]),
+    "ane_debug_norm_bwd": (C.c_int, [C.c_int, C.c_int, _fp, _fp, _fp, _fp, C.c_float, _fp, _u16, _fp, C.c_int]),
     "ane_debug_classifier": (C.c_int, [C.c_int, C.c_int, C.c_int, _u16, _u16, _u16, C.c_int, C.c_int, C.c_int,
                                        C.c_int, C.c_int, _fp, _fp, _fp, _fp, _fp, _u16, _u16]),
     "ane_debug_last_error": (C.c_char_p, []),

@@ -1325,6 +1325,43 @@ done:
   return rc;
 }
 
+extern "C" int ane_debug_norm_bwd(int T, int D, const float* dy, const float* x, const float* gain,
+                                  const float* addend, float alpha, float* out, uint16_t* out_h, float* dgain_part,
+                                  int general) {
+  int rc = ANE_OK;
+  if (T <= 0 || D <= 0 || D % 64 || D > 1024 || !dy || !x || !gain || !out || !dgain_part)
+    return debug_fail("norm_bwd: T > 0, D a multiple of 64 up to 1024, dy / x / gain / out / dgain_part given",
+                      hipErrorInvalidValue);
+  const size_t n = (size_t)T * D, nb = (size_t)norm_bwd_blocks(T);
+  float *ddy = nullptr, *dx = nullptr, *dg = nullptr, *dad = nullptr, *dout = nullptr, *dpart = nullptr;
+  half_t* douth = nullptr;
+  NormBwdArgs a;
+  DBGCHK(hipMalloc(&ddy, n * 4));
+  DBGCHK(hipMalloc(&dx, n * 4));
+  DBGCHK(hipMalloc(&dg, (size_t)D * 4));
+  DBGCHK(hipMalloc(&dout, n * 4));
+  DBGCHK(hipMalloc(&dpart, nb * D * 4));
+  DBGCHK(hipMemcpy(ddy, dy, n * 4, hipMemcpyHostToDevice));
+  DBGCHK(hipMemcpy(dx, x, n * 4, hipMemcpyHostToDevice));
+  DBGCHK(hipMemcpy(dg, gain, (size_t)D * 4, hipMemcpyHostToDevice));
+  if (addend) {
+    DBGCHK(hipMalloc(&dad, n * 4));
+    DBGCHK(hipMemcpy(dad, addend, n * 4, hipMemcpyHostToDevice));
+  }
+  if (out_h) DBGCHK(hipMalloc(&douth, n * 2));
+  a.dy = ddy; a.x = dx; a.gain = dg; a.dgain_part = dpart; a.addend = dad; a.alpha = alpha;
+  a.out = dout; a.out_h = douth; a.T = T; a.D = D; a.general = general;
+  DBGCHK(norm_bwd(a, nullptr));
+  DBGCHK(hipDeviceSynchronize());
+  DBGCHK(hipMemcpy(out, dout, n * 4, hipMemcpyDeviceToHost));
+  DBGCHK(hipMemcpy(dgain_part, dpart, nb * D * 4, hipMemcpyDeviceToHost));
+  if (out_h) DBGCHK(hipMemcpy(out_h, douth, n * 2, hipMemcpyDeviceToHost));
+done:
+  for (void* p : {(void*)ddy, (void*)dx, (void*)dg, (void*)dad, (void*)dout, (void*)dpart, (void*)douth})
+    if (p) (void)hipFree(p);
+  return rc;
+}
+
 extern "C" int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float scale, int hilo,
                                    const uint16_t* qkv, uint16_t* out, float* lse) {
   int rc = ANE_OK;

@@ -31,6 +31,7 @@ struct NormBwdArgs {
   float* gx0 = nullptr;
   const float* xl_p = nullptr;
   int T = 0, D = 0;
+  int general = 0;                  // host: take the general kernel even for the gain form
 };
 hipError_t norm_bwd(const NormBwdArgs& a, hipStream_t s);
 inline int norm_bwd_blocks(int T) { return (T + kNormBwdRows - 1) / kNormBwdRows; }

@@ -605,7 +605,7 @@ hipError_t norm_bwd(const NormBwdArgs& a, hipStream_t s) {
   if (a.D % 64 || a.D > 1024 || a.T <= 0) return hipErrorInvalidValue;
   const dim3 g(norm_bwd_blocks(a.T));
   const bool gain_only = a.gain && a.dgain_part && !a.addend2 && !a.ve_dx && !a.lam_x && !a.lam_x0 && !a.lam_part &&
-                         !a.gx0 && norm_bwd_fast();
+                         !a.gx0 && !a.general && norm_bwd_fast();
   if (gain_only && a.addend) hipLaunchKernelGGL(norm_bwd_gain_kernel<true>, g, dim3(64 * kNormBwdRows), 0, s, a);
   else if (gain_only) hipLaunchKernelGGL(norm_bwd_gain_kernel<false>, g, dim3(64 * kNormBwdRows), 0, s, a);
   else hipLaunchKernelGGL(norm_bwd_kernel, g, dim3(256), 0, s, a);

@@ -277,6 +277,16 @@ int ane_debug_attention(int nseq, int S, int NH, int qknorm, double theta, float
  * (rows and columns multiples of 64). */
 int ane_debug_transpose2(int Ra, int Ca, const uint16_t *in_a, uint16_t *out_a, int Rb, int Cb,
                          const uint16_t *in_b, uint16_t *out_b);
+/* The training step's RMSNorm backward (stories.RMSNormBackward,
+ * ane/stories/cpu.go:191-210, gain on both terms as there) on host arrays,
+ * gain form: out [T, D] = alpha * addend + RMSNorm-backward(dy; x, gain)
+ * (addend may be NULL), out_h [T, D] its fp16 copy (may be NULL) and
+ * dgain_part [ceil(T / 8), D] each 8-row block's sum of dy * x / rms.
+ * general != 0 forces the general kernel (the one the nanochat terms use);
+ * 0 takes the gain-form kernel the llama2 step runs.  D a multiple of 64,
+ * at most 1024. */
+int ane_debug_norm_bwd(int T, int D, const float *dy, const float *x, const float *gain, const float *addend,
+                       float alpha, float *out, uint16_t *out_h, float *dgain_part, int general);
 /* The classifier epilogues on one forced block tile (bm x bn, nw waves):
  * A [M, K] classifier rows, B [N, K] token rows (fp16), targets [N].
  * Cross-entropy partials (the loss path of runFinalHead /

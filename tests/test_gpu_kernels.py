@@ -242,3 +242,46 @@ def test_transpose_pairs_bit_exact(ra, ca, rb, cb):
     if rb:
         np.testing.assert_array_equal(ob, b.T)
     assert lib.ane_debug_transpose2(100, 64, u16(a), u16(oa), 0, 0, None, None) != 0  # rows not a multiple of 64
+
+
+@pytest.mark.parametrize("T,D,add,half", [(4096, 768, True, True), (4096, 768, False, True), (100, 64, True, False),
+                                          (37, 1024, True, True), (8, 192, False, False)])
+def test_norm_bwd_gain_form(T, D, add, half):
+    """The training step's RMSNorm backward, gain form (stories.RMSNormBackward,
+    ane/stories/cpu.go:191-210, gain on both terms as there): the gain-form
+    kernel the llama2 step runs and the general kernel, each against a
+    float64 restatement, and the fp16 copy as the rounded fp32 output.  Row
+    counts that leave a partial last block (100, 37) and D below one float4
+    per lane (64, 192) included."""
+    lib = _lib.load()
+    rng = np.random.default_rng(T * 7 + D)
+    dy = rng.standard_normal((T, D)).astype(np.float32)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    g = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    ad = rng.standard_normal((T, D)).astype(np.float32) if add else None
+    alpha = 0.75
+    nb = (T + 7) // 8
+    f32 = lambda a: a.ctypes.data_as(C.POINTER(C.c_float)) if a is not None else None
+    x64, dy64, g64 = x.astype(np.float64), dy.astype(np.float64), g.astype(np.float64)
+    rr = 1.0 / np.sqrt((x64 * x64).mean(1, keepdims=True) + 1e-5)
+    c = (dy64 * x64 * g64).sum(1, keepdims=True) * rr * rr / D
+    ref = (dy64 - x64 * c) * rr * g64 + (alpha * ad.astype(np.float64) if add else 0.0)
+    dg = dy64 * x64 * rr
+    dg_ref = np.stack([dg[8 * b:8 * b + 8].sum(0) for b in range(nb)])
+    outs = []
+    for general in (0, 1):
+        out = np.zeros((T, D), np.float32)
+        oh = np.zeros((T, D), np.float16) if half else None
+        part = np.zeros((nb, D), np.float32)
+        rc = lib.ane_debug_norm_bwd(T, D, f32(dy), f32(x), f32(g), f32(ad), alpha, f32(out),
+                                    _u16(oh) if half else None, f32(part), general)
+        assert rc == 0, lib.ane_debug_last_error()
+        scale = np.abs(ref).max()
+        assert np.abs(out - ref).max() <= 2e-6 * scale, (general, np.abs(out - ref).max(), scale)
+        assert np.abs(part - dg_ref).max() <= 2e-6 * np.abs(dg_ref).max() * 8, general
+        if half:
+            np.testing.assert_array_equal(oh, out.astype(np.float16))
+        outs.append(out)
+    # the two kernels: the same function, fp32 rounding apart
+    assert np.abs(outs[0] - outs[1]).max() <= 2e-6 * np.abs(ref).max()
+    assert lib.ane_debug_norm_bwd(T, 96, f32(dy), f32(x), f32(g), None, 1.0, f32(outs[0]), None, f32(part), 0) != 0
