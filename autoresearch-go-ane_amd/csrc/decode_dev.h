@@ -191,9 +191,15 @@ struct WideLds {
 // inside the same launch (the fused chain) and are re-read device-coherent
 // until none is stale (at most spin_limit rounds; a timeout sets *err and
 // the block exits).
+// pf_k / pf_v (POLL only, may be null): after its own K / V loads, the
+// block streams pf_rows cache rows of another (sequence, kv head) through
+// the caches -- one that will start late, on the same XCD, and then finds
+// them in L2 -- while it waits for q.
 template <int G, bool DIRECT, bool POLL>
 __device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a, int b, int kvh, int sp, WideLds& L,
-                                                   unsigned spin_limit = 0, int* err = nullptr) {
+                                                   unsigned spin_limit = 0, int* err = nullptr,
+                                                   const half_t* pf_k = nullptr, const half_t* pf_v = nullptr,
+                                                   int pf_rows = 0) {
   constexpr int NT = 1024, NW = NT / 64;
   constexpr int TW = (kDecWideChunk / 16 + NW - 1) / NW;  // key tiles per wave
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -240,6 +246,19 @@ __device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a, int b, 
     // inside the chain's launch: q is not there yet, the cache is -- every
     // K / V load first, then q polled (its loads wait behind them anyway)
     load_kv();
+    if (pf_k) {  // 16 B per thread per load, 4 in flight; the values are only xor-folded
+      const uint4* pk = reinterpret_cast<const uint4*>(pf_k);
+      const uint4* pv = reinterpret_cast<const uint4*>(pf_v);
+      const int n16 = pf_rows * 8;  // 16-byte chunks per tensor
+      unsigned x = 0;
+      for (int c = tid; c < n16; c += 2 * NT) {
+        const int c1 = min(c + NT, n16 - 1);
+        const uint4 v0 = pk[c], v1 = pk[c1], v2 = pv[c], v3 = pv[c1];
+        x ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w;
+        x ^= v2.x ^ v2.y ^ v2.z ^ v2.w ^ v3.x ^ v3.y ^ v3.z ^ v3.w;
+      }
+      asm volatile("" ::"v"(x));
+    }
     bool ok = false;
     for (unsigned r = 0; spin_limit != 0; r++) {
       asm volatile("" ::: "memory");

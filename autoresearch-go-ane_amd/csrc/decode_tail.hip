@@ -286,6 +286,8 @@ __device__ __forceinline__ void x_to_lds(const float* x, int cg, int D, float (*
 // consumer wave re-reads its inputs until none is stale, so a phase costs the
 // producers' stores reaching the shared level and one read round, instead of
 // a store drain, a counter update, a counter read and then the data read.
+constexpr int kTailLateAtt = 48;  // attention blocks of the fused launch that start after chain blocks exit
+
 // The chain's LDS, or (for an attention block of the fused launch) the wide
 // attention's.
 struct ChainLds {
@@ -490,7 +492,20 @@ __global__ __launch_bounds__(64 * kTailWaves) void tail_kernel(TailArgs a) {
       aa.qkv_part = S.p_q;
       aa.qkv_ks = 1;
       aa.rr = S.rr;
-      dec_attn_wide_body<GA, true, true>(aa, i % aa.nb, i / aa.nb, 0, lds.w, a.spin_limit, a.err);
+      // The last kTailLateAtt blocks start only as chain blocks exit; the
+      // first kTailLateAtt (resident from the start, idle until q) stream
+      // their K / V through L2 beforehand: block i for block i + b_att -
+      // kTailLateAtt, on the same XCD (block indices 8 apart share one).
+      const half_t *pk = nullptr, *pv = nullptr;
+      int rows = 0;
+      if (a.b_att >= 4 * kTailLateAtt && (a.b_att - kTailLateAtt) % 8 == 0 && i < kTailLateAtt) {
+        const int t = i + a.b_att - kTailLateAtt, tb = t % aa.nb, tk = t / aa.nb;
+        const size_t c0 = ((size_t)tb * aa.NKV + tk) * aa.max_ctx;
+        pk = aa.kc + c0 * 64;
+        pv = aa.vc + c0 * 64;
+        rows = min(aa.ctr[0] + 1, aa.max_ctx);
+      }
+      dec_attn_wide_body<GA, true, true>(aa, i % aa.nb, i / aa.nb, 0, lds.w, a.spin_limit, a.err, pk, pv, rows);
       return;
     }
   }
