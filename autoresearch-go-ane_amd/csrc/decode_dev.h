@@ -44,7 +44,6 @@ __device__ __forceinline__ void drain_stores() {
   asm volatile("" ::: "memory");
 }
 
-
 // Data-polling form: a wave re-issues its device-coherent input loads in
 // rounds until none of them returns a stale dword.  give_up() after round r:
 // true after `limit` rounds or when another block has failed (else a short
@@ -61,7 +60,6 @@ __device__ __forceinline__ bool give_up(unsigned r, unsigned limit, const int* e
 __device__ __forceinline__ int dec_chunk(int ctx, int nsplit) {
   return ((ctx + nsplit - 1) / nsplit + 31) & ~31;
 }
-
 
 // The step's projections from the QKV partials, one column pair per thread:
 // q of the G heads (threads < 32 G) and, in the block whose split holds
@@ -159,7 +157,6 @@ struct QkvProj {
     }
   }
 };
-
 
 // Wide form, one 1024-thread block per (sequence, kv head, split of up to
 // kDecWideChunk keys).  Key tile t (16 keys) belongs to wave t % 16, which
@@ -397,7 +394,6 @@ __device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a, int b, 
     }
   }
 }
-
 
 }  // namespace
 }  // namespace ane

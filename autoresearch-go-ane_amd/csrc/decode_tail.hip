@@ -27,6 +27,16 @@
 // epilogue (W1|W3) and in the attention's QKV finish (via rr_next).
 // Every wait is bounded; a timeout sets *err, and later launches exit at once.
 //
+// Two forms of the waits (TailArgs::poll).  With done counters, a producer
+// drains its stores and counts itself done, and a consumer polls the
+// counter, then loads.  In the data-polling form (the default) the data a
+// phase hands on goes through one of two buffer sets whose dwords start as
+// kTailStale, a pattern no store writes; a consumer wave re-reads its inputs
+// until none is stale, and every launch resets the set the previous one
+// used.  That form can also run the next layer's decode attention in the
+// same launch (TailArgs::b_att): those blocks come after the chain's, issue
+// their K / V loads at once and poll q.
+//
 // Memory: the data blocks exchange inside the launch (the residual, the norm
 // sums, the fp16 activation fragments) is stored and loaded device-coherent
 // (cache policy sc1: written through to, and read from, the level shared by
