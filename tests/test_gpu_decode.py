@@ -258,16 +258,20 @@ def test_full_batch_of_64_every_sequence(heads, kv_heads, tail, monkeypatch):
     _check_choice(gen, g_lg[:, 1:])
 
 
-@pytest.mark.parametrize("tail", ["2", "1"])
-def test_fused_chain_wait_timeout_is_reported(tail, monkeypatch):
+@pytest.mark.parametrize("tail,form", [("2", None), ("2", "wide"), ("1", None)])
+def test_fused_chain_wait_timeout_is_reported(tail, form, monkeypatch):
     """A dependency wait of the fused layer kernel that times out is an
     error of the call (the host forces it: a poll limit of 0 fails every
     wait at once, and every block still exits); the decoder's counters (or
     buffer sets) are reset, and another decoder of the same process decodes
-    normally."""
+    normally.  With the wide attention form forced, the polling chain's
+    launches also hold the next layer's attention blocks, whose q wait
+    fails the same way."""
     cfg = ane.tiny_decode()
     p, prefix = _setup(cfg, 2, 64, 61)
     monkeypatch.setenv("ANE_DEC_TAIL", tail)
+    if form:
+        monkeypatch.setenv("ANE_DEC_ATTN", form)
     monkeypatch.setenv("ANE_DEC_TAIL_SPIN", "0")
     dec = ane.Decoder(cfg, p, max_batch=2, max_ctx=128)
     try:
