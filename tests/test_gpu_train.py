@@ -59,6 +59,22 @@ def test_tiny_grads_match_oracle(arch, mode):
     check_grads(cfg, g, g_ref)
 
 
+@pytest.mark.parametrize("seq", [128, 192])
+@pytest.mark.parametrize("arch,mode", [("llama2", "true"), ("nanochat", "compat")])
+def test_tiny_grads_at_other_sequence_lengths(arch, mode, seq):
+    """Sequences of 2 and 3 pairs of 32-query blocks: the attention backward
+    then runs 2 and 3 waves per block (4 at seq 256, 1 at seq 64)."""
+    cfg = ane.tiny(arch, layers=2, grad_mode=mode, seq=seq)
+    p = ane.init_params(cfg, seed=23, std=0.08)
+    tok, tgt = ane.make_tokens(cfg, 2, seed=24)
+    loss_ref, g_ref = oracle.grads(cfg, p, tok, tgt)
+    eng = open_engine(cfg, p, max_batch=2)
+    loss, g = eng.Grads(tok, tgt)
+    eng.Destroy()
+    assert abs(loss - loss_ref) <= 1e-3
+    check_grads(cfg, g, g_ref)
+
+
 @pytest.mark.parametrize("arch,mode", [("llama2", "true"), ("nanochat", "compat")])
 def test_full_size_grads_match_oracle(arch, mode):
     """BASELINE config 3 shape per sequence (stories110M, seq 256)."""
