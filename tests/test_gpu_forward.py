@@ -68,6 +68,24 @@ def test_tiny_model_batched(arch):
     eng.Destroy()
 
 
+@pytest.mark.parametrize("seq", [128, 192])
+@pytest.mark.parametrize("arch", ["llama2", "nanochat"])
+def test_tiny_model_other_sequence_lengths(arch, seq):
+    """Sequences of 2 and 3 pairs of 32-query blocks (2 and 3 attention
+    waves per block)."""
+    cfg = ane.tiny(arch, layers=2, seq=seq)
+    p = ane.init_params(cfg, seed=5, std=0.08)
+    eng = open_engine(cfg, p, max_batch=3)
+    tok, tgt = ane.make_tokens(cfg, 3, seed=6)
+    lo, per_ref, lg_ref = oracle.forward_loss(cfg, p, tok, tgt, want_logits=True)
+    mean, per = eng.EvalLoss(tok, tgt)
+    np.testing.assert_allclose(per, per_ref, atol=LOSS_TOL)
+    for b in (0, 2):
+        lg = eng.EvalLogits(tok[b]).reshape(cfg.vocab, cfg.seq)
+        assert np.abs(lg - lg_ref[b]).max() <= LOGIT_TOL
+    eng.Destroy()
+
+
 @pytest.mark.parametrize("arch", ["llama2", "nanochat"])
 def test_out_of_range_tokens_and_targets(arch):
     """Token >= vocab embeds as a zero row (ane/stories/cpu.go:60-64); target
