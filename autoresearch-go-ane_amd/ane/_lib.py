@@ -130,6 +130,7 @@ SIGNATURES = {
     "ane_decode_generate": (C.c_int, [_eng, C.c_int32, _u16]),
     "ane_decode_position": (C.c_int32, [_eng]),
     "ane_decode_last_ms": (C.c_double, [_eng]),
+    "ane_decode_fused_chain": (C.c_int32, [_eng]),
     "ane_decode_debug_fill_cache": (C.c_int, [_eng, C.c_int]),
     "ane_moe_open": (C.c_int, [C.POINTER(MoeCfg), C.POINTER(C.c_void_p)]),
     "ane_moe_destroy": (None, [_eng]),

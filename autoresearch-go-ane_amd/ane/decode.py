@@ -99,6 +99,13 @@ class Decoder:
         self._live()
         return int(self._lib.ane_decode_position(self._h))
 
+    def FusedChain(self) -> int:
+        """1: steps run the fused per-layer chain; 0: one launch per GEMM;
+        2: one launch per GEMM since a chain wait timed out (the call was
+        redone that way and the decoder stays on it)."""
+        self._live()
+        return int(self._lib.ane_decode_fused_chain(self._h))
+
     def DebugFillCache(self, byte: int = 0xFF):
         """Test-only: every byte of the KV cache set to `byte` (0xFF: NaN)."""
         self._live()

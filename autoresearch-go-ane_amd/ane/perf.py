@@ -101,7 +101,12 @@ class Sampler:
         return t0
 
     def Stop(self, snapshot: Optional[float]) -> Delta:
-        """Ends the window opened by Start(); averages over its samples."""
+        """Ends the window opened by Start(); averages over its samples.
+        The energy covers the whole window: the trapezoids between samples,
+        plus the first sample's power held back to the window's start and the
+        last one's held on to its end (the thread's start-up gap and the time
+        after the last poll)."""
+        t_end = time.perf_counter()
         if self._thread is not None:
             self._stop.set()
             self._thread.join()
@@ -109,11 +114,13 @@ class Sampler:
         if snapshot is None:
             return Delta()
         rows = self._rows
-        dt = time.perf_counter() - snapshot
+        dt = t_end - snapshot
+        rows = [r for r in rows if r[0] <= t_end]
         if not rows:
             return Delta(seconds=dt)
         ws = [r[1] for r in rows]
         energy = sum(0.5 * (rows[i][1] + rows[i - 1][1]) * (rows[i][0] - rows[i - 1][0]) for i in range(1, len(rows)))
+        energy += rows[0][1] * max(0.0, rows[0][0] - snapshot) + rows[-1][1] * max(0.0, t_end - rows[-1][0])
         busy = [r[2] for r in rows if r[2] is not None]
         return Delta(seconds=dt, samples=len(rows), watts_avg=sum(ws) / len(ws), watts_max=max(ws), energy_j=energy,
                      busy_pct=(sum(busy) / len(busy)) if busy else 0.0)

@@ -266,12 +266,13 @@ __device__ __forceinline__ void dec_attn_wide_body(const DecAttnArgs& a, int b, 
       L.fail[wave] = ok ? 0 : 1;
       if (!ok) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    qp.finish(a, tid, qs, knew, vnew, Kb, Vb, pos - c0);
     __syncthreads();
     int f = 0;
 #pragma unroll
     for (int w = 0; w < NW; w++) f |= L.fail[w];
-    if (f) return;  // uniform
+    if (f) return;  // uniform; a block whose q never arrived writes nothing (no cache row)
+    qp.finish(a, tid, qs, knew, vnew, Kb, Vb, pos - c0);
+    __syncthreads();
   } else {
     // q and the new k / v rows first, staged before any K / V load is
     // issued: a load issued beside the block's K / V misses returns only

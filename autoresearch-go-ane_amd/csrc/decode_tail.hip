@@ -66,7 +66,9 @@ __device__ bool wait_count(const unsigned* c, unsigned target, unsigned limit, i
   if (threadIdx.x < 64) {
     int ok = limit != 0;
     unsigned spins = 0;
-    while (ok && ld_relaxed(c) < target) {
+    // wrap-safe: the counters grow by the same amounts as the epoch targets,
+    // modulo 2^32, and a counter trails its target by far less than 2^31
+    while (ok && (int)(ld_relaxed(c) - target) < 0) {
       if (++spins > limit || __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
         ok = 0;
         break;

@@ -104,6 +104,8 @@ struct ane_decoder {
   char* tail_sets = nullptr;   // its two buffer sets, tail_set_bytes each
   size_t tail_set_sz = 0;
   uint16_t *tok_d = nullptr, *hist_d = nullptr, *prefix_d = nullptr;
+  uint16_t* tok_save = nullptr;  // a call's input tokens, kept to redo it after a failed chain wait
+  int chain_latched = 0;         // 1 once a failed chain wait switched the decoder to one launch per GEMM
   int* ctr_d = nullptr;
   int TC = 0;
   float* px = nullptr;
@@ -250,6 +252,7 @@ int open_impl(ane_decoder* d) {
   DCHK(op, dalloc(d, &d->tok_d, (size_t)R));
   DCHK(op, dalloc(d, &d->hist_d, (size_t)C * R));
   DCHK(op, dalloc(d, &d->prefix_d, (size_t)B * C));
+  DCHK(op, dalloc(d, &d->tok_save, (size_t)R));
   DCHK(op, dalloc(d, &d->ctr_d, 3));
   d->TC = std::max(kPrefillTokens, (C + 63) / 64 * 64);
   DCHK(op, dalloc(d, &d->px, (size_t)d->TC * D));
@@ -318,6 +321,7 @@ hipError_t gemm(ane_decoder* d, const half_t* A, const half_t* Bw, int M, int N,
 // One decode step for the active batch; every position/step index is read
 // from ctr_d on the device, so the same launches replay as a graph.
 int enqueue_step_tail(ane_decoder* d, float* logits, uint16_t* hist);
+int generate_run(ane_decoder* d, const char* op, int nsteps, uint16_t* out_tok);
 
 int enqueue_step(ane_decoder* d, float* logits, uint16_t* hist) {
   if (d->use_tail) return enqueue_step_tail(d, logits, hist);
@@ -423,10 +427,13 @@ int enqueue_step_tail(ane_decoder* d, float* logits, uint16_t* hist) {
   return ANE_OK;
 }
 
-// After a synchronised step: a dependency wait of the fused chain that timed
-// out leaves *err set (and every later launch exits at once); report it and
-// clear the chain's state so the decoder can run again.
-int check_tail(ane_decoder* d, const char* op) {
+// After a synchronised call: a dependency wait of the fused chain that timed
+// out leaves *err set (every later launch of the chain exits at once, the
+// other kernels of the step still run on what it left).  Clears the chain's
+// state (epoch counters, buffer sets, error flag) and reports the failure in
+// *failed; the call's outputs and the cache rows it wrote are then invalid.
+int tail_failed(ane_decoder* d, const char* op, bool* failed) {
+  *failed = false;
   if (!d->use_tail) return ANE_OK;
   int err = 0;
   DCHK(op, hipMemcpy(&err, d->err_d, 4, hipMemcpyDeviceToHost));
@@ -436,7 +443,39 @@ int check_tail(ane_decoder* d, const char* op) {
   DCHK(op, hipMemset(d->err_d, 0, 4));
   if (d->tail_poll) DCHK(op, hipMemset(d->tail_sets, 0xff, 2 * d->tail_set_sz));  // a failed launch left sets half-used
   DCHK(op, hipDeviceSynchronize());
-  return dfail(d, ANE_ERR_HIP, "storiesane decode %s: a dependency wait of the fused layer kernel timed out", op);
+  *failed = true;
+  return ANE_OK;
+}
+
+// A failed chain wait means the chain's two assumptions did not hold on this
+// GPU (all of a launch's chain blocks resident at once, and dispatched before
+// its attention blocks: another process on the GPU can break both).  As the
+// reference disables a failing accelerator piece and carries on with its
+// other path (ane/engine.go:887-894, ane/train_full.go:356-368), the decoder
+// switches for good to one launch per GEMM, which has no inter-block waits,
+// and the caller redoes the call from its saved start.
+void latch_per_gemm(ane_decoder* d) {
+  d->use_tail = false;
+  d->chain_latched = 1;
+  if (d->gexec) (void)hipGraphExecDestroy(d->gexec);
+  if (d->graph) (void)hipGraphDestroy(d->graph);
+  d->gexec = nullptr;
+  d->graph = nullptr;
+}
+
+// The start of a step / generate call, kept so that the call can be redone:
+// the input tokens (the device copy the first step reads) and the position.
+int save_start(ane_decoder* d, const char* op) {
+  DCHK(op, hipMemcpyAsync(d->tok_save, d->tok_d, (size_t)d->nseq * 2, hipMemcpyDeviceToDevice, d->stream));
+  return ANE_OK;
+}
+
+// Rewinds to a saved start: the tokens and the device counters of position
+// pos0 (cache rows from pos0 on are rewritten by the redo before any read).
+int restore_start(ane_decoder* d, const char* op, int pos0) {
+  DCHK(op, hipMemcpyAsync(d->tok_d, d->tok_save, (size_t)d->nseq * 2, hipMemcpyDeviceToDevice, d->stream));
+  DCHK(op, dec_set_ctr(d->ctr_d, pos0, 0, d->stream));
+  return ANE_OK;
 }
 
 int copy_out(ane_decoder* d, uint16_t* next_tok, float* logits) {
@@ -445,7 +484,14 @@ int copy_out(ane_decoder* d, uint16_t* next_tok, float* logits) {
   if (logits)
     DCHK(op, hipMemcpyAsync(logits, d->logits_d, (size_t)d->nseq * d->V * 4, hipMemcpyDeviceToHost, d->stream));
   DCHK(op, hipStreamSynchronize(d->stream));
-  return check_tail(d, op);
+  return ANE_OK;
+}
+
+// A failure that the redo cannot repair leaves the cache inconsistent: the
+// active batch is dropped so that Step / Generate refuse until a new Prefill.
+int drop_batch(ane_decoder* d, int rc) {
+  d->nseq = 0;
+  return rc;
 }
 
 }  // namespace
@@ -575,7 +621,7 @@ extern "C" int ane_decode_prefill(ane_decoder* d, const uint16_t* prefix, int32_
   DCHK(op, argmax_reduce(d->tok_d, nullptr, nullptr, d->amax, d->V / 32, nseq, st));
   DCHK(op, dec_set_ctr(d->ctr_d, plen, 0, st));
   d->pos = plen;
-  return copy_out(d, next_tok, logits);
+  return copy_out(d, next_tok, logits);  // prefill launches no chain kernel: nothing to check
 }
 
 extern "C" int ane_decode_step(ane_decoder* d, const uint16_t* in_tok, uint16_t* next_tok, float* logits) {
@@ -585,10 +631,21 @@ extern "C" int ane_decode_step(ane_decoder* d, const uint16_t* in_tok, uint16_t*
   if (d->pos >= d->C) return dfail(d, ANE_ERR_ARG, "storiesane decode step: cache full (max_ctx=%d)", d->C);
   DCHK(op, hipSetDevice(d->cfg.device));
   if (in_tok) DCHK(op, hipMemcpyAsync(d->tok_d, in_tok, (size_t)d->nseq * 2, hipMemcpyHostToDevice, d->stream));
-  int rc = enqueue_step(d, logits ? d->logits_d : nullptr, nullptr);
-  if (rc != ANE_OK) return rc;
-  d->pos++;
-  return copy_out(d, next_tok, logits);
+  const int pos0 = d->pos;
+  int rc = d->use_tail ? save_start(d, op) : ANE_OK;
+  if (rc == ANE_OK) rc = enqueue_step(d, logits ? d->logits_d : nullptr, nullptr);
+  if (rc == ANE_OK) rc = copy_out(d, next_tok, logits);
+  bool failed = false;
+  if (rc == ANE_OK) rc = tail_failed(d, op, &failed);
+  if (rc == ANE_OK && failed) {
+    latch_per_gemm(d);
+    rc = restore_start(d, op, pos0);
+    if (rc == ANE_OK) rc = enqueue_step(d, logits ? d->logits_d : nullptr, nullptr);
+    if (rc == ANE_OK) rc = copy_out(d, next_tok, logits);
+  }
+  if (rc != ANE_OK) return drop_batch(d, rc);
+  d->pos = pos0 + 1;
+  return ANE_OK;
 }
 
 extern "C" int ane_decode_generate(ane_decoder* d, int32_t nsteps, uint16_t* out_tok) {
@@ -599,8 +656,28 @@ extern "C" int ane_decode_generate(ane_decoder* d, int32_t nsteps, uint16_t* out
     return dfail(d, ANE_ERR_ARG, "storiesane decode generate: %d steps from position %d exceed max_ctx=%d", nsteps,
                  d->pos, d->C);
   if (nsteps == 0) return ANE_OK;
-  const hipStream_t st = d->stream;
   DCHK(op, hipSetDevice(d->cfg.device));
+  const int pos0 = d->pos;
+  int rc = d->use_tail ? save_start(d, op) : ANE_OK;
+  if (rc == ANE_OK) rc = generate_run(d, op, nsteps, out_tok);
+  bool failed = false;
+  if (rc == ANE_OK) rc = tail_failed(d, op, &failed);
+  if (rc == ANE_OK && failed) {
+    latch_per_gemm(d);
+    rc = restore_start(d, op, pos0);
+    if (rc == ANE_OK) rc = generate_run(d, op, nsteps, out_tok);
+  }
+  if (rc != ANE_OK) return drop_batch(d, rc);
+  d->pos = pos0 + nsteps;
+  return ANE_OK;
+}
+
+namespace {
+
+// nsteps replays of the step graph (captured on first use, and again after
+// the batch size or the step's form changed), from position d->pos.
+int generate_run(ane_decoder* d, const char* op, int nsteps, uint16_t* out_tok) {
+  const hipStream_t st = d->stream;
   if (!d->gexec || d->graph_nseq != d->nseq) {
     if (d->gexec) (void)hipGraphExecDestroy(d->gexec);
     if (d->graph) (void)hipGraphDestroy(d->graph);
@@ -629,8 +706,14 @@ extern "C" int ane_decode_generate(ane_decoder* d, int32_t nsteps, uint16_t* out
   float ms = 0.f;
   DCHK(op, hipEventElapsedTime(&ms, d->ev0, d->ev1));
   d->last_ms = ms;
-  d->pos += nsteps;
-  return check_tail(d, op);
+  return ANE_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t ane_decode_fused_chain(ane_decoder* d) {
+  if (!d) return -1;
+  return d->chain_latched ? 2 : d->use_tail ? 1 : 0;
 }
 
 extern "C" int32_t ane_decode_position(ane_decoder* d) { return d ? d->pos : -1; }

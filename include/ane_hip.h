@@ -384,6 +384,18 @@ int ane_decode_generate(ane_decoder *d, int32_t nsteps, uint16_t *out_tok);
 int32_t ane_decode_position(ane_decoder *d);
 /* device time of the last ane_decode_generate call (ms, HIP events) */
 double ane_decode_last_ms(ane_decoder *d);
+/* Which form a step runs in (no reference counterpart; the decoder has
+ * none): 1 the fused per-layer chain, 0 one launch per GEMM (chosen at open:
+ * ANE_DEC_TAIL=0, or the chain's blocks do not all fit on the GPU at once),
+ * 2 one launch per GEMM after a chain wait timed out.  The chain's waits
+ * assume all of a launch's chain blocks resident at once and dispatched
+ * before its attention blocks; when one times out (another process on the
+ * GPU can break both) the decoder switches to one launch per GEMM for good
+ * and redoes the call from its start, as the reference disables a failing
+ * accelerator piece and carries on (ane/engine.go:887-894,
+ * ane/train_full.go:356-368).  If the redo itself fails, the active batch is
+ * dropped: Step / Generate then refuse until the next Prefill. */
+int32_t ane_decode_fused_chain(ane_decoder *d);
 /* Test-only (no reference counterpart): fills every byte of the KV cache
  * with `byte` (0xFF: fp16 NaN everywhere), so a test can show that no
  * position is read before it is written. */
