@@ -183,12 +183,16 @@ void phase_sum(ane_engine* e, double ms[PH_COUNT]) {
 }
 
 hipError_t eng_gemm(ane_engine* e, int cls, const half_t* A, int lda, bool at, const half_t* B, int ldb, bool bt,
-                    int M, int N, int K, int epi, const EpiParams& p, int bm, int bn, bool side) {
+                    int M, int N, int K, int epi, const EpiParams& p, int bm, int bn, bool side, bool selfpf) {
   if (side && (!e->dw_stream || !e->tr.splitk_ws2)) return hipErrorInvalidValue;
   hipStream_t s = side ? e->dw_stream : e->stream;
   float* ws = side ? e->tr.splitk_ws2 : e->tr.splitk_ws;
   GemmArgs g;
   g.A = A; g.B = B; g.lda = lda; g.ldb = ldb; g.M = M; g.N = N; g.K = K; g.a_t = at; g.b_t = bt;
+  if (selfpf && !at && !bt && (size_t)N * K * 2 <= (size_t)kPfBlocks * kPfLoads * 256 * 16) {
+    g.pf = B;
+    g.pf_bytes = (size_t)N * K * 2;
+  }
   // training: GEMMs whose output is too small to fill the chip split K
   // (K-major operands, or M-major ones as the weight gradients read them)
   if (!(at && !bt) && ws && bm == 0 && bn == 0) {
@@ -399,6 +403,7 @@ extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_e
   // GEMMs around it instead of launching it
   if (const char* g = getenv("ANE_FUSED_NORM")) e->fused_norm = atoi(g) != 0;
   if (const char* g = getenv("ANE_FUSED_PF")) e->fused_pf = atoi(g) != 0;
+  if (const char* g = getenv("ANE_GEMM_SELFPF")) e->gemm_selfpf = atoi(g) != 0;
   if (const char* g = getenv("ANE_TR_DW")) e->tr_dw = atoi(g) != 0;
   if (const char* g = getenv("ANE_DW_ASYNC")) e->dw_async = atoi(g) != 0;
   if (const char* g = getenv("ANE_BWD_PREFETCH")) e->bwd_prefetch = atoi(g) != 0;
@@ -614,18 +619,19 @@ extern "C" int ane_set_tokens(ane_engine* e, const uint16_t* tokens, int64_t n) 
 // its activations: the residual GEMMs write out-of-place into the next
 // layer's input buffer, so nothing is copied.
 //
-// defer_norm (llama2 eval forward, with ANE_FUSED_NORM=1): no RMSNorm
-// launch.  Each norm's input x comes with xh = fp16(x * gain) and per-row
-// partial sums of x^2 (from the embedding, or from the residual GEMM's
-// epilogue, one partial per column block); the GEMM that consumes xh scales
-// its (linear) output rows by rr = 1 / rms(x) in its epilogue.  The final
-// norm is left to the classifier (e->fwd_rr_nparts > 0).  Off by default:
-// the norm launches also stream the next GEMM's weights through the caches;
-// without any such launch the GEMMs lose more than the norms cost (B32:
-// 2.88 ms per forward against 2.82), and with launches that only stream the
-// weights (ANE_FUSED_PF, default on) the two paths are within the ~3%
-// box-to-box spread (2.78 against 2.82 ms on one box, 2.75 against 2.67 on
-// another).
+// defer_norm (llama2 eval forward; ANE_FUSED_NORM=0 keeps the norm
+// launches): no RMSNorm launch.  Each norm's input x comes with xh =
+// fp16(x * gain) and per-row partial sums of x^2 (from the embedding, or
+// from the residual GEMM's epilogue, one partial per column block); the GEMM
+// that consumes xh scales its (linear) output rows by rr = 1 / rms(x) in its
+// epilogue.  The final norm is left to the classifier (e->fwd_rr_nparts > 0).
+// The norm launches also streamed the next GEMM's weights through the
+// caches; without them each GEMM's blocks would wait on HBM for the same
+// cold weight tile at every k-step, so the QKV, W1|W3 and W2 GEMMs' first
+// blocks stream their own weights with their prologue loads (GemmArgs::pf;
+// Wo's are streamed by attention, the classifier's by a prefetch launch).
+// B32, back to back on one box: 2.770 ms per forward against 2.844 with the
+// norm launches, 2.795 with a prefetch launch before each GEMM instead.
 int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
   const char* op = "forward";
   const ane_model_cfg& c = e->cfg;
@@ -690,7 +696,7 @@ int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
                              (size_t)3 * D * D * sizeof(half_t)));
       prof_end(e, 0, (double)T * D * 6);
     }
-    if (fused && l > 0 && e->fused_pf) {
+    if (fused && l > 0 && e->fused_pf && !e->gemm_selfpf) {
       prof_begin(e, 6);
       HIPCHK(op, prefetch_weights(s.wqkv, (size_t)3 * D * D * sizeof(half_t), st));
       prof_end(e, 0, (double)3 * D * D * 2);
@@ -700,7 +706,7 @@ int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
       p.C = A.qkv; p.ldc = 3 * D;
       if (fused) rr(p, nparts);
       HIPCHK(op, eng_gemm(e, 0, A.xn, D, false, s.wqkv, D, false, T, 3 * D, D, fused ? EPI_STORE_H_RR : EPI_STORE_H,
-                          p));
+                          p, 0, 0, false, fused && e->gemm_selfpf));
     }
     {
       AttnArgs a;
@@ -742,13 +748,14 @@ int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
       p.C = A.gate; p.ldc = H;
       p.C2 = A.h13; p.ldc2 = llama ? 2 * H : H;
       if (fused) {
-        if (e->fused_pf) {
+        if (e->fused_pf && !e->gemm_selfpf) {
           prof_begin(e, 6);
           HIPCHK(op, prefetch_weights(s.w13, ((size_t)2 * H * D + (size_t)D * H) * sizeof(half_t), st));  // W1|W3, W2
           prof_end(e, 0, (double)3 * H * D * 2);
         }
         rr(p, nparts);
-        HIPCHK(op, eng_gemm(e, 2, A.xn2, D, false, s.w13, D, false, T, 2 * H, D, EPI_SWIGLU_RR, p));
+        HIPCHK(op, eng_gemm(e, 2, A.xn2, D, false, s.w13, D, false, T, 2 * H, D, EPI_SWIGLU_RR, p, 0, 0, false,
+                            e->gemm_selfpf));
       } else if (llama) {
         HIPCHK(op, eng_gemm(e, 2, A.xn2, D, false, s.w13, D, false, T, 2 * H, D, EPI_SWIGLU, p));
       } else {
@@ -766,7 +773,8 @@ int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
         // the next norm's inputs: the next layer's attention norm, or the final norm
         p.C2 = A.xn; p.ldc2 = D; p.gain = P + (l + 1 < L ? e->pm.L[l + 1].g_att : e->pm.g_final);
         p.ssq_part = e->ssq_part; p.ssq_ld = T;
-        HIPCHK(op, eng_gemm(e, 3, A.gate, H, false, s.w2, H, false, T, D, H, EPI_RESID_NORM, p, res_bm, res_bn));
+        HIPCHK(op, eng_gemm(e, 3, A.gate, H, false, s.w2, H, false, T, D, H, EPI_RESID_NORM, p, res_bm, res_bn, false,
+                            e->gemm_selfpf));
         nparts = D / res_bn;
       } else {
         HIPCHK(op, eng_gemm(e, 3, A.gate, H, false, s.w2, H, false, T, D, H, EPI_RESID, p));

@@ -163,13 +163,17 @@ struct ane_engine {
   ane::half_t* qkv = nullptr;
   ane::half_t* att = nullptr;
   ane::half_t* gate = nullptr;
-  // deferred RMSNorm of the llama2 eval forward (ANE_FUSED_NORM=1; off by
-  // default: measured slower, see forward_body): per-row partial sums of
+  // deferred RMSNorm of the llama2 eval forward (default; ANE_FUSED_NORM=0
+  // runs the norm launches, see forward_body): per-row partial sums of
   // squares [kRrMaxParts][T] behind xh = fp16(x * gain); fwd_rr_nparts > 0
   // when the last forward left its final norm to the classifier this way
   float* ssq_part = nullptr;
-  bool fused_norm = false;
-  bool fused_pf = true;
+  bool fused_norm = true;
+  bool fused_pf = true;  // the classifier's weights by a prefetch launch (ANE_FUSED_PF)
+  // the deferred-norm forward's QKV, W1|W3 and W2 GEMMs stream their own
+  // weights from their first blocks (GemmArgs::pf; ANE_GEMM_SELFPF=0: a
+  // prefetch launch before each instead)
+  bool gemm_selfpf = true;
   bool tr_dw = true;  // weight gradients read token-major operands directly (ANE_TR_DW=0: transposes)
   // The backward's weight-gradient GEMMs run on a second stream beside the
   // activation-gradient chain (ANE_DW_ASYNC=0: all on one stream).  Events
@@ -254,10 +258,12 @@ int eng_fail(ane_engine* e, int code, const char* fmt, ...);
   } while (0)
 void prof_begin(ane_engine* e, int cls, hipStream_t s = nullptr);
 void prof_end(ane_engine* e, double flops, double bytes, hipStream_t s = nullptr);
-// side = run on the dW stream with its own split-K workspace
+// side = run on the dW stream with its own split-K workspace; selfpf = the
+// first blocks stream the weight operand B through the caches (when it fits
+// GemmArgs::pf's limit)
 hipError_t eng_gemm(ane_engine* e, int cls, const ane::half_t* A, int lda, bool at, const ane::half_t* B, int ldb,
                     bool bt, int M, int N, int K, int epi, const ane::EpiParams& p, int bm = 0, int bn = 0,
-                    bool side = false);
+                    bool side = false, bool selfpf = false);
 int refresh_shadows(ane_engine* e);
 // the update job table of adam_fused_update for the segments of a (cached)
 int ensure_update_jobs(ane_engine* e, const ane::AdamArgs& a);

@@ -73,7 +73,17 @@ struct GemmArgs {
   // and applies the epilogue, so results do not depend on block timing.
   int splits = 1;
   float* ws = nullptr;
+  // Self-prefetch: the launch's first kPfBlocks blocks each stream one slice
+  // of [pf, pf + pf_bytes) (16-byte aligned, at most kPfBlocks * kPfLoads *
+  // 256 * 16 bytes) through the caches with their prologue loads, so that a
+  // cold weight operand is requested whole at the start instead of one
+  // k-tile per k-step.  K-major kernel only.
+  const void* pf = nullptr;
+  size_t pf_bytes = 0;
 };
+// Blocks that share a self-prefetch, and 16-byte loads per thread at most.
+constexpr int kPfBlocks = 256;
+constexpr int kPfLoads = 8;
 
 struct EpiParams {
   void* C = nullptr;

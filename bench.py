@@ -24,6 +24,12 @@ it carries:
   decode          BASELINE configs[3]: GQA KV-cache greedy decode, tokens/s
                   and achieved GB/s against HBM peak;
   moe_ffn         BASELINE configs[4]: top-2 MoE FFN layer, 8192 tokens;
+  reference_benchmarks  the reference's own benchmark surface
+                  (bench_test.go:85-158): Step() per call with its
+                  StepResult fields and tok/s both as the reference computes
+                  it and per window, EvalLogits per 256-token window with the
+                  vocab-major copy-out, EvalLoss val_loss / val_bpb over the
+                  harness's windows;
   cpu_baseline    the reference's CPU path (the C oracle, with the reference's
                   threading: serial linearCF, parallel norms / classifier /
                   CE) timed on a bounded sample of the same workload on this
@@ -130,6 +136,101 @@ def train_bench(ane, arch, steps, batch=16):
                                 / 1e12, 1)}
 
 
+# The reference experiment's engine options (experiment.go:17-38, 43-63).
+REF_EXPERIMENT = dict(AccumSteps=8, LR=3e-4, Seed=42, AdamBeta1=0.8, AdamBeta2=0.95, AdamEps=1e-10, WeightDecay=0.0,
+                      GradClip=1.0, LossScale=256.0, EmbedLRMult=1.0, ScalarLRMult=1.0, LambdaLRMult=0.01,
+                      LambdaBeta1=0.96, LambdaBeta2=0.95)
+
+
+def reference_benchmarks(ane, arch, step_calls=32, logits_calls=20):
+    """The reference's own benchmark surface (bench_test.go:85-158) with the
+    reference experiment's options (AccumSteps 8, ...) on its engine's model
+    (stories110M; `arch` nanochat is what the reference's Engine runs, with
+    MODEL=randinit weights: here N(0, 0.02) from seed 0), over a synthetic
+    token stream (uniform ids from seed 2, long enough for the harness's
+    10,000 validation tokens).  Not the headline: one Step() is one window
+    (batch 1), as in the reference.
+
+      step          BenchmarkStep: 3 warm-up Step() calls, then step_calls
+                    calls; loss / step_ms / ane_ms from the last StepResult,
+                    adam_ms from the last call that ran the update.  tok/s as
+                    the reference computes it, Seq * AccumSteps / StepDuration
+                    (bench_test.go:92,109; it counts AccumSteps windows per
+                    one-window call, so it reads AccumSteps times high), and
+                    per window, Seq / StepDuration, and over the wall clock.
+      eval_logits   BenchmarkEvalLogits: one 256-token window per call,
+                    vocab-major fp32 logits copied out to the host.
+      eval_loss     BenchmarkEvalLoss: val_loss / val_bpb over the harness's
+                    windows (harness.go:46-89), batched in one device call;
+                    and the reference harness's loop as written (one
+                    EvalLogits per window, its vocab-major indexing) with its
+                    own number and time.
+    Board power over each timed loop where the sysfs files exist."""
+    from ane import harness
+    from ane.perf import Sampler
+    cfg = ane.stories110m(arch)
+    params = ane.init_params(cfg, seed=0, std=0.02)
+    stream = np.random.default_rng(2).integers(0, cfg.vocab, 20_000).astype(np.uint16)
+    nwin = len(harness.eval_windows(stream, harness.EVAL_TOKENS, cfg.seq)[1])
+    eng = ane.Open(ane.Options(Config=cfg, Params=params, Tokens=stream, MaxBatch=nwin, **REF_EXPERIMENT))
+    sampler = Sampler()
+
+    def power(d):
+        return d.metrics() if sampler.available else {}
+
+    out = {"arch": arch, "options": "experiment.go:17-38", "data": "synthetic: uniform ids seed 2; N(0,0.02) seed 0"}
+    try:
+        for _ in range(3):
+            eng.Step()
+        eng.Sync()
+        adam_ns = 0
+        snap = sampler.Start()
+        t0 = time.perf_counter()
+        for _ in range(step_calls):
+            r = eng.Step()
+            if r.adam_ns:
+                adam_ns = r.adam_ns
+        wall = time.perf_counter() - t0
+        pw = power(sampler.Stop(snap))
+        acc = REF_EXPERIMENT["AccumSteps"]
+        step_s = r.step_ns * 1e-9
+        out["step"] = {"calls": step_calls, "accum_steps": acc, "loss": round(float(r.loss), 5),
+                       "step_ms": round(r.step_ns / 1e6, 3), "ane_ms": round(r.ane_eval_ns / 1e6, 3),
+                       "adam_ms": round(adam_ns / 1e6, 3),
+                       "tok_s_reference_formula": round(cfg.seq * acc / step_s, 1),
+                       "tok_s_per_window": round(cfg.seq / step_s, 1),
+                       "tok_s_wall": round(cfg.seq * step_calls / wall, 1), "power": pw}
+
+        window = stream[:cfg.seq]
+        eng.EvalLogits(window)
+        snap = sampler.Start()
+        t0 = time.perf_counter()
+        for _ in range(logits_calls):
+            eng.EvalLogits(window)
+        dt = (time.perf_counter() - t0) / logits_calls
+        pw = power(sampler.Stop(snap))
+        out["eval_logits"] = {"calls": logits_calls, "ms_per_call": round(dt * 1e3, 3),
+                              "tok_s": round(cfg.seq / dt, 1), "copy_out_bytes": cfg.vocab * cfg.seq * 4, "power": pw}
+
+        harness.EvalLoss(eng, stream)  # warm-up (graph capture for this batch size)
+        snap = sampler.Start()
+        t0 = time.perf_counter()
+        loss = harness.EvalLoss(eng, stream)
+        dt = time.perf_counter() - t0
+        pw = power(sampler.Stop(snap))
+        t0 = time.perf_counter()
+        ref_loss = harness.ReferenceEvalLoss(eng, stream)
+        dt_ref = time.perf_counter() - t0
+        out["eval_loss"] = {"windows": nwin, "val_loss": round(loss, 6), "val_bpb": round(harness.ValBPB(loss), 6),
+                            "ms": round(dt * 1e3, 3), "power": pw,
+                            "reference_harness_as_written": {"val_loss": round(ref_loss, 6),
+                                                             "val_bpb": round(harness.ValBPB(ref_loss), 6),
+                                                             "ms": round(dt_ref * 1e3, 1)}}
+    finally:
+        eng.Destroy()
+    return out
+
+
 def decode_bytes_per_step(cfg, batch, ctx):
     """Algorithmic HBM bytes of one decode step with `ctx` keys per sequence:
     fp16 weights once, K and V of every cached position, the new K/V rows,
@@ -225,6 +326,10 @@ def main():
                          "profiling those legs alone)")
     ap.add_argument("--no-power", action="store_true", help="skip the board-power pass of the forward")
     ap.add_argument("--decode-steps", type=int, default=128)
+    ap.add_argument("--no-ref-bench", action="store_true",
+                    help="skip the reference's own benchmark surface (Step / EvalLogits / EvalLoss per call)")
+    ap.add_argument("--ref-arch", default="nanochat", choices=["llama2", "nanochat"],
+                    help="model of the reference-benchmark leg (nanochat: the reference Engine's architecture)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -249,6 +354,8 @@ def main():
         out["decode"] = decode_bench(ane, args.decode_steps)
     if not args.no_moe:
         out["moe_ffn"] = moe_bench(ane)
+    if not args.no_ref_bench:
+        out["reference_benchmarks"] = reference_benchmarks(ane, args.ref_arch)
     if not args.no_cpu:
         # every CPU this process may run on (on the GPU pool: the 16-CPU share
         # of one GPU, whatever nproc reports for the whole host)

@@ -25,14 +25,17 @@ exact inputs bench.py measures:
                               stories110M, weights seed 0, 16 x 256 tokens
                               seed 3: per-segment L2 norms of the mean
                               gradient and a few sampled rows of every
-                              segment (token rows for the embeddings)
+                              segment (the token embedding: 16 of the
+                              batch's token rows and 16 other rows; the
+                              value embeddings: token rows)
   bench_decode_b64            the decode model (weights seed 4), 64
                               sequences of 1024 prefix ids seed 4: for 4
                               sampled sequences the oracle's greedy tokens
                               after the prefix and 3 steps and the fp16
                               logits of those 4 positions
 
-Usage:  python tests/golden/make_golden.py [--bench | --all]
+Usage:  python tests/golden/make_golden.py [--bench | --bench-grads | --all]
+        (--bench-grads: only the bench_grads_b16 fixtures, the others kept)
 """
 import json
 import os
@@ -66,10 +69,12 @@ def grad_fingerprint(cfg, g, tokens, seed=90):
     return np.array(norms, np.float64), np.concatenate(rows).astype(np.float32)
 
 
-def bench_fixtures(put):
+def bench_fixtures(put, grads_only=False):
     import time
     oracle.set_threads(os.cpu_count() or 1, parallel_linear=True)
     t0 = time.time()
+    if grads_only:
+        return bench_grads(put)
     cfg = ane.stories110m("llama2")
     p = ane.init_params(cfg, seed=0, std=0.02)
     tok, tgt = ane.make_tokens(cfg, 32, seed=2)
@@ -77,6 +82,12 @@ def bench_fixtures(put):
     put("bench_fwd_b32_llama2_loss_per_seq", per, 2, 1e-3,
         "stories110m('llama2'), init_params(seed 0, std 0.02), make_tokens(batch 32, seed 2): oracle loss per sequence")
     print(f"forward B32: mean {mean:.6f} ({time.time() - t0:.0f} s)", flush=True)
+    bench_grads(put)
+    bench_decode(put)
+
+
+def bench_grads(put):
+    import time
     for arch, mode in (("llama2", "true"), ("nanochat", "compat")):
         t0 = time.time()
         cfg = ane.stories110m(arch, grad_mode=mode)
@@ -92,6 +103,10 @@ def bench_fixtures(put):
             "sampled_rows)")
         put(f"bench_grads_b16_{arch}_{mode}_loss", np.array([loss], np.float32), 3, 1e-3, "mean loss")
         print(f"grads B16 {arch}/{mode}: loss {loss:.6f} ({time.time() - t0:.0f} s)", flush=True)
+
+
+def bench_decode(put):
+    import time
     t0 = time.time()
     dcfg = ane.decode_gqa()
     dp = ane.init_params(dcfg, seed=4, std=0.02)
@@ -107,8 +122,9 @@ def bench_fixtures(put):
 
 
 def main():
-    bench = "--bench" in sys.argv or "--all" in sys.argv
-    small = "--bench" not in sys.argv
+    grads_only = "--bench-grads" in sys.argv
+    bench = "--bench" in sys.argv or "--all" in sys.argv or grads_only
+    small = "--bench" not in sys.argv and not grads_only
     path = os.path.join(HERE, "manifest.json")
     old = json.load(open(path)) if os.path.exists(path) else []
     manifest = []
@@ -121,7 +137,9 @@ def main():
                          "seed": seed, "tolerance": tol, "note": note})
 
     if bench:
-        bench_fixtures(put)
+        bench_fixtures(put, grads_only)
+        if grads_only:  # keep the other benchmark-shape fixtures
+            manifest.extend(m for m in old if m["name"].startswith("bench_") and not m["name"].startswith("bench_grads_"))
     if not small:
         # keep the small fixtures written earlier
         manifest.extend(m for m in old if not m["name"].startswith("bench_"))

@@ -19,27 +19,52 @@ def load(name):
 
 
 BENCH_GRAD_ROWS = 2
+BENCH_EMBED_ROWS = 16
+
+
+def embed_row_split(shape, tokens):
+    """(token rows, other rows) of the token embedding: the rows of the ids
+    that occur in the batch, whose gradient also holds the back-propagated
+    lookup gradient, and the rest, which hold only the classifier part."""
+    tok_rows = np.unique(np.asarray(tokens).reshape(-1).astype(np.int64))
+    tok_rows = tok_rows[tok_rows < shape[0]]
+    return tok_rows, np.setdiff1d(np.arange(shape[0], dtype=np.int64), tok_rows)
 
 
 def sampled_rows(cfg, name, shape, tokens, seed):
     """Row indices of a gradient segment that the benchmark-shape gradient
     fixtures keep: for the value-embedding tables the rows of the first
     tokens of the batch (the only rows their gradient touches); for the
-    token embedding those token rows followed by as many rows drawn from
-    `seed` (its classifier part reaches every row); else rows drawn from
-    `seed`; 1-D segments are kept whole (None)."""
+    token embedding BENCH_EMBED_ROWS rows drawn from `seed` among the
+    batch's token rows, then as many among the other rows (a stratified
+    sample, so that the whole tensor's relative error can be estimated);
+    else rows drawn from `seed`; 1-D segments are kept whole (None)."""
     if len(shape) == 1:
         return None
     r = np.random.default_rng(seed)
-    if name == "embed" or name.endswith("ve_embed"):
+    if name == "embed":
+        tok_rows, other = embed_row_split(shape, tokens)
+        a = np.sort(r.choice(tok_rows, BENCH_EMBED_ROWS, replace=False))
+        b = np.sort(r.choice(other, BENCH_EMBED_ROWS, replace=False))
+        return np.concatenate([a, b]).astype(np.int64)
+    if name.endswith("ve_embed"):
         seen = []
         for t in tokens.reshape(-1):
             if int(t) not in seen:
                 seen.append(int(t))
             if len(seen) == BENCH_GRAD_ROWS:
                 break
-        if name == "embed":
-            others = [int(i) for i in r.permutation(shape[0]) if int(i) not in seen][:BENCH_GRAD_ROWS]
-            seen += sorted(others)
         return np.array(seen, np.int64)
     return np.sort(r.choice(shape[0], BENCH_GRAD_ROWS, replace=False)).astype(np.int64)
+
+
+def stratified_rel_l2(got, want, n_strata, sizes):
+    """Relative L2 error of a whole tensor estimated from equal-sized row
+    samples of its strata (rows concatenated stratum by stratum): each
+    stratum's squared error and squared norm are scaled by its row count
+    over the sampled count."""
+    got = np.asarray(got, np.float64).reshape(n_strata, -1)
+    want = np.asarray(want, np.float64).reshape(n_strata, -1)
+    err = sum(w * np.sum((g - t) ** 2) for g, t, w in zip(got, want, sizes))
+    ref = sum(w * np.sum(t ** 2) for t, w in zip(want, sizes))
+    return float(np.sqrt(err / max(ref, 1e-300)))

@@ -9,7 +9,9 @@ sizes, so it does not run here).
   all 32 per-sequence losses within 1e-3 nats.
 * B16 x 256 gradients, both architectures: the split-K weight
   gradient GEMMs at K = 4096 tokens and the B16 tile rules; per-segment
-  norms and sampled rows at relative L2 <= 1e-2.
+  norms and sampled rows at relative L2 <= 1e-2 (the token embedding: the
+  whole tensor's error, estimated from a stratified sample of its token and
+  other rows).
 * 64 sequences x 1024-token prefix decode in the attention form
   the batch size selects: prefill and three forced steps, the logits of four
   sampled sequences within 2e-2, and the replayed-graph Generate path's
@@ -19,7 +21,7 @@ import numpy as np
 import pytest
 
 import ane
-from golden_io import load, sampled_rows
+from golden_io import BENCH_EMBED_ROWS, embed_row_split, load, sampled_rows, stratified_rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -82,6 +84,7 @@ def test_bench_grads_b16(arch, mode):
             return 0.25
         return 5e-2 if name.split(".")[-1] in SCALARS else tol
 
+
     def rel(a, b):
         return np.linalg.norm(a.astype(np.float64) - b) / max(np.linalg.norm(b), 1e-30)
 
@@ -92,16 +95,20 @@ def test_bench_grads_b16(arch, mode):
         want = ref_rows[off:off + got.size].astype(np.float64)
         off += got.size
         if name == "embed":
-            # rows drawn at random (the classifier part every row has): the
-            # tensor's bound.  The batch's first token rows add one
-            # occurrence's back-propagated activation gradient, a per-token
-            # quantity rather than a sum over tokens: merely rounding the
-            # parameters to fp16 moves the oracle's own value of these rows by
-            # 5.9e-3 (nanochat compat, B16), so they are held to 2e-2.
+            # The whole tensor's relative L2 error, estimated from the
+            # stratified sample: BENCH_EMBED_ROWS of the batch's token rows
+            # (classifier part + the back-propagated lookup gradient) and as
+            # many of the other rows (classifier part only), each stratum
+            # weighted by its row count.  The token rows hold nearly all of
+            # the norm, so this is their error.
+            tok_rows, other = embed_row_split(shape, tok)
+            e_all = stratified_rel_l2(got, want, 2, (len(tok_rows) / BENCH_EMBED_ROWS, len(other) / BENCH_EMBED_ROWS))
             k = got.size // 2
-            e_rnd, e_tok = rel(got[k:], want[k:]), rel(got[:k], want[:k])
-            worst += [(e_rnd, "embed (random rows)"), (e_tok, "embed (token rows)")]
-            assert e_rnd <= tol and e_tok <= 2e-2, (e_rnd, e_tok)
+            e_tok, e_oth = rel(got[:k], want[:k]), rel(got[k:], want[k:])
+            print(f"embed: whole-tensor estimate {e_all:.3e} (token rows {e_tok:.3e}, other rows {e_oth:.3e})")
+            worst += [(e_all, "embed")]
+            assert e_all <= tol, (e_all, e_tok, e_oth)
+            assert e_oth <= tol, e_oth
         else:
             e_rows = rel(got, want)
             worst.append((e_rows, name))

@@ -6,10 +6,9 @@ here runs no norm kernel: the residual GEMM's epilogue leaves fp16(x * g)
 and per-row partial sums of x^2 (one per column block), and the projection
 that consumes them scales its output rows by 1 / rms(x), which the product
 commutes with.  Each epilogue is checked against float64 on every tile the
-dispatcher offers it; the whole forward (EvalLoss with ANE_FUSED_NORM=1; the
-default keeps the norm launches, which also stream the next GEMM's weights
-and measure faster) is checked against the oracle and against the
-norm-launch path.
+dispatcher offers it; the whole forward (EvalLoss, the default; and with
+ANE_FUSED_NORM=0, the norm launches) is checked against the oracle and the
+two paths against each other.
 """
 import ctypes as C
 
