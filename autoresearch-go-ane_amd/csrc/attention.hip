@@ -29,8 +29,13 @@ constexpr int HD = 64;
 // fp16), s = q_hi.k_hi + q_lo.k_hi + q_hi.k_lo, i.e. ~fp32 accuracy.  Used
 // where the scores are large enough for fp16 rounding of q and k to matter
 // (the reference's scale-1 recompute, ane/train_full.go:268-269).
-template <int SMAX, bool HILO>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
+// PERQ: one q block per wave (blocks of 2 x pairs waves: wave w takes the
+// first block of pair slot w % slots if w < slots, else the second), so a
+// pair's two q blocks run on two waves side by side instead of one after
+// the other on one wave; 128 VGPRs, so that two 8-wave blocks share a CU.
+template <int SMAX, bool HILO, bool PERQ>
+__global__ __launch_bounds__(PERQ ? 512 : 256) __attribute__((amdgpu_waves_per_eu(PERQ ? 4 : 1)))
+void attn_fwd_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) half_t Ks[SMAX * HD];
   __shared__ __attribute__((aligned(16))) half_t Ks_lo[HILO ? SMAX * HD : 8];
   constexpr int VST = SMAX + 4;  // V^T row stride (halves): 2-way-free b64 reads
@@ -40,6 +45,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   const size_t pf_part = ((size_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
   const size_t pf_parts = (size_t)gridDim.x * gridDim.y * gridDim.z;
   const int nthr = blockDim.x, tid = threadIdx.x;
+  const int slots = PERQ ? nthr >> 7 : nthr >> 6;  // q-block pairs a block's waves cover
   // Block -> (sequence b, head h, q-block pairs [p0, p0 + np)).  Grid
   // (pair groups, NH, nseq), or with split_from > 0 a 1-D grid: heads below
   // split_from whole, the rest as two half blocks each.
@@ -52,7 +58,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       hl = a.split_from + (u - a.split_from) / 2; p0 = ((u - a.split_from) & 1) * half; np = half;
     }
   } else {
-    hl = blockIdx.z * NH + blockIdx.y; p0 = blockIdx.x * (nthr >> 6); np = nthr >> 6;
+    hl = blockIdx.z * NH + blockIdx.y; p0 = blockIdx.x * slots; np = slots;
   }
   const int h = hl % NH, b = hl / NH;
   const bool first = p0 == 0;  // the block that writes qkvt of its head
@@ -64,7 +70,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   // issued after both and consumed once the staging is done.
   const int nkc = S / 8;
   half8 vpre[8];
-  if (tid < S) {
+  if (!PERQ && tid < S) {  // PERQ: register budget of 128; V is loaded where it is staged
     const int kc = tid % nkc, dc = tid / nkc;
 #pragma unroll
     for (int jj = 0; jj < 8; jj++) vpre[jj] = ld_h8(base + (size_t)(kc * 8 + jj) * D3 + 2 * D + h * HD + dc * 8);
@@ -74,7 +80,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   // Batches of KB chunks per thread: every global load of a batch (the K
   // chunk and its cos / sin as float4) is issued before the first use, so
   // the batch pays one memory latency instead of one per chunk.
-  constexpr int KB = 8;
+  constexpr int KB = PERQ ? 4 : 8;  // PERQ: 512 threads cover S = 256 in one batch of 4
   Prefetch pf{};
   for (int c0 = tid; c0 < S * 8; c0 += KB * nthr) {
     half8 raw[KB];
@@ -89,7 +95,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
         sn4[u] = *reinterpret_cast<const float4*>(a.rope_sin + j * 32 + ch * 4);
       }
     }
-    if (c0 == tid) pf = prefetch_begin(a.pf, a.pf_bytes, pf_part, pf_parts);
+    if (!PERQ && c0 == tid) pf = prefetch_begin(a.pf, a.pf_bytes, pf_part, pf_parts);
 #pragma unroll
     for (int u = 0; u < KB; u++) {
       const int c = c0 + u * nthr;
@@ -129,12 +135,25 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   }
 
   // ---- stage V^T (8 keys x 8 dims per thread), value embeddings added --------
+  // (PERQ: threads past S, which stage no V block, stream the block's slice
+  // of the next GEMM's weights meanwhile)
+  if (PERQ && tid >= S && a.pf && a.pf_bytes >= 16) {
+    const uint4* q = reinterpret_cast<const uint4*>(a.pf);
+    const size_t n16 = a.pf_bytes / 16, per = (n16 + pf_parts - 1) / pf_parts;
+    const size_t i1 = min(n16, (pf_part + 1) * per);
+    uint32_t x = 0;
+    for (size_t i = pf_part * per + (tid - S); i < i1; i += nthr - S) {
+      const uint4 v = q[i];
+      x ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    asm volatile("" ::"v"(x));
+  }
   for (int blk = tid; blk < S; blk += nthr) {
     const int kc = blk % nkc, dc = blk / nkc;
     half8 raw[8];
 #pragma unroll
     for (int jj = 0; jj < 8; jj++)
-      raw[jj] = blk == tid ? vpre[jj] : ld_h8(base + (size_t)(kc * 8 + jj) * D3 + 2 * D + h * HD + dc * 8);
+      raw[jj] = !PERQ && blk == tid ? vpre[jj] : ld_h8(base + (size_t)(kc * 8 + jj) * D3 + 2 * D + h * HD + dc * 8);
     if (a.ve_x) {
       float v[8][8];
 #pragma unroll
@@ -176,18 +195,20 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     }
   }
   __syncthreads();
-  prefetch_end(pf, a.pf, a.pf_bytes, pf_part, pf_parts);
+  if (!PERQ) prefetch_end(pf, a.pf, a.pf_bytes, pf_part, pf_parts);
 
   // ---- per wave: q-block pair ------------------------------------------------
   const int lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;
   const int nqb = S / 32, npairs = nqb / 2;
-  const int pair = p0 + wave;
-  if (wave >= np || pair >= npairs) return;
+  const int slot = PERQ ? wave % slots : wave;
+  const int pair = p0 + slot;
+  if (slot >= np || pair >= npairs) return;
+  const int which0 = PERQ ? wave / slots : 0, which1 = PERQ ? which0 + 1 : 2;
   const int g = lane >> 5, ql = lane & 31;
   const float l2e = 1.4426950408889634f;
   const float sl2 = a.scale * l2e;
 
-  for (int which = 0; which < 2; which++) {
+  for (int which = which0; which < which1; which++) {
     const int qb = which == 0 ? pair : nqb - 1 - pair;
     const int q = qb * 32 + ql;
     // Q fragment (B operand of S^T = K Q^T): dims s*16 + 8g + [0..7]
@@ -356,8 +377,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 hipError_t attention_fwd(const AttnArgs& a, hipStream_t stream) {
   if (a.S <= 0 || a.S % 64 != 0 || a.S > 512 || a.NH <= 0 || a.nseq <= 0) return hipErrorInvalidValue;
   const int npairs = a.S / 64;
-  const int nw = npairs < 4 ? npairs : 4;
+  const int nw = npairs < 4 ? npairs : 4;  // q-block pairs per block
   dim3 grid((npairs + nw - 1) / nw, a.NH, a.nseq);
+  // ANE_ATT_PERQ=0: one wave per pair of q blocks (4-wave blocks)
+  static const bool perq = [] {
+    const char* f = getenv("ANE_ATT_PERQ");
+    return !f || atoi(f) != 0;
+  }();
   // One block of 4 pairs per head leaves 256 < heads < 512 unevenly spread
   // over the 256 CUs (two blocks on some, one on the rest): the heads past
   // 256 run as two half blocks, one beside each whole block.
@@ -370,11 +396,13 @@ hipError_t attention_fwd(const AttnArgs& a, hipStream_t stream) {
   }
   if (a.hilo && a.S > 256) return hipErrorInvalidValue;
   if (a.hilo)
-    hipLaunchKernelGGL((attn_fwd_kernel<256, true>), grid, dim3(64 * nw), 0, stream, k);
+    hipLaunchKernelGGL((attn_fwd_kernel<256, true, false>), grid, dim3(64 * nw), 0, stream, k);
+  else if (a.S <= 256 && perq)
+    hipLaunchKernelGGL((attn_fwd_kernel<256, false, true>), grid, dim3(128 * nw), 0, stream, k);
   else if (a.S <= 256)
-    hipLaunchKernelGGL((attn_fwd_kernel<256, false>), grid, dim3(64 * nw), 0, stream, k);
+    hipLaunchKernelGGL((attn_fwd_kernel<256, false, false>), grid, dim3(64 * nw), 0, stream, k);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<512, false>), grid, dim3(64 * nw), 0, stream, k);
+    hipLaunchKernelGGL((attn_fwd_kernel<512, false, false>), grid, dim3(64 * nw), 0, stream, k);
   return hipGetLastError();
 }
 
