@@ -34,8 +34,14 @@ exact inputs bench.py measures:
                               after the prefix and 3 steps and the fp16
                               logits of those 4 positions
 
-Usage:  python tests/golden/make_golden.py [--bench | --bench-grads | --all]
-        (--bench-grads: only the bench_grads_b16 fixtures, the others kept)
+  bench_grads_b16_nanochat_compat_repeat
+                              nanochat compat, weights seed 0, 16 windows
+                              that each repeat one id (seed 5): the scalar
+                              gradients (the smear lambda's sum over
+                              positions does not cancel on such windows)
+
+Usage:  python tests/golden/make_golden.py [--bench | --bench-grads | --bench-smear | --all]
+        (--bench-grads / --bench-smear: only those fixtures, the others kept)
 """
 import json
 import os
@@ -51,7 +57,7 @@ for p in (os.path.join(ROOT, "autoresearch-go-ane_amd"), os.path.join(ROOT, "ora
 sys.path.insert(0, os.path.dirname(HERE))
 import ane  # noqa: E402
 import oracle  # noqa: E402
-from golden_io import sampled_rows  # noqa: E402
+from golden_io import repeated_windows, sampled_rows  # noqa: E402
 from ane.moe import MoeConfig, init_moe_params, make_moe_input  # noqa: E402
 
 
@@ -69,12 +75,14 @@ def grad_fingerprint(cfg, g, tokens, seed=90):
     return np.array(norms, np.float64), np.concatenate(rows).astype(np.float32)
 
 
-def bench_fixtures(put, grads_only=False):
+def bench_fixtures(put, only=None):
     import time
     oracle.set_threads(os.cpu_count() or 1, parallel_linear=True)
     t0 = time.time()
-    if grads_only:
+    if only == "grads":
         return bench_grads(put)
+    if only == "smear":
+        return bench_smear(put)
     cfg = ane.stories110m("llama2")
     p = ane.init_params(cfg, seed=0, std=0.02)
     tok, tgt = ane.make_tokens(cfg, 32, seed=2)
@@ -83,6 +91,7 @@ def bench_fixtures(put, grads_only=False):
         "stories110m('llama2'), init_params(seed 0, std 0.02), make_tokens(batch 32, seed 2): oracle loss per sequence")
     print(f"forward B32: mean {mean:.6f} ({time.time() - t0:.0f} s)", flush=True)
     bench_grads(put)
+    bench_smear(put)
     bench_decode(put)
 
 
@@ -105,6 +114,30 @@ def bench_grads(put):
         print(f"grads B16 {arch}/{mode}: loss {loss:.6f} ({time.time() - t0:.0f} s)", flush=True)
 
 
+def bench_smear(put):
+    """nanochat compat at B16 on repeated-token windows: the scalar gradients
+    (smear, residual, x0, backout lambdas) and the loss.  On random windows
+    the smear lambda's gradient is a sum of ~3M terms that nearly cancels
+    (rounding only the parameters to fp16 moves it by ~17%); here it moves
+    by 3e-4."""
+    import time
+    t0 = time.time()
+    cfg = ane.stories110m("nanochat", grad_mode="compat")
+    p = ane.init_params(cfg, seed=0, std=0.02)
+    tok, tgt = repeated_windows(cfg, 16, 5)
+    loss, g = oracle.grads(cfg, p, tok, tgt)
+    vals = []
+    for name, off, shape in ane.param_layout(cfg):
+        if name in ("resid_lambdas", "x0_lambdas", "smear_lambda", "backout_lambda"):
+            vals.append(g[off:off + int(np.prod(shape))])
+    put("bench_grads_b16_nanochat_compat_repeat_scalars", np.concatenate(vals).astype(np.float32), 5, 1e-2,
+        "stories110m('nanochat', grad_mode 'compat'), init_params(seed 0), 16 windows each one repeated id "
+        "(rng(5).integers(0, 32000, 16)), targets the same ids: gradients of resid_lambdas, x0_lambdas, "
+        "smear_lambda, backout_lambda in layout order")
+    put("bench_grads_b16_nanochat_compat_repeat_loss", np.array([loss], np.float32), 5, 1e-3, "mean loss")
+    print(f"smear B16 repeated: loss {loss:.6f} ({time.time() - t0:.0f} s)", flush=True)
+
+
 def bench_decode(put):
     import time
     t0 = time.time()
@@ -122,9 +155,9 @@ def bench_decode(put):
 
 
 def main():
-    grads_only = "--bench-grads" in sys.argv
-    bench = "--bench" in sys.argv or "--all" in sys.argv or grads_only
-    small = "--bench" not in sys.argv and not grads_only
+    only = "grads" if "--bench-grads" in sys.argv else "smear" if "--bench-smear" in sys.argv else None
+    bench = "--bench" in sys.argv or "--all" in sys.argv or only is not None
+    small = "--bench" not in sys.argv and only is None
     path = os.path.join(HERE, "manifest.json")
     old = json.load(open(path)) if os.path.exists(path) else []
     manifest = []
@@ -137,9 +170,10 @@ def main():
                          "seed": seed, "tolerance": tol, "note": note})
 
     if bench:
-        bench_fixtures(put, grads_only)
-        if grads_only:  # keep the other benchmark-shape fixtures
-            manifest.extend(m for m in old if m["name"].startswith("bench_") and not m["name"].startswith("bench_grads_"))
+        bench_fixtures(put, only)
+        if only:  # keep the other benchmark-shape fixtures
+            written = {m["name"] for m in manifest}
+            manifest.extend(m for m in old if m["name"].startswith("bench_") and m["name"] not in written)
     if not small:
         # keep the small fixtures written earlier
         manifest.extend(m for m in old if not m["name"].startswith("bench_"))

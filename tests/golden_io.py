@@ -68,3 +68,13 @@ def stratified_rel_l2(got, want, n_strata, sizes):
     err = sum(w * np.sum((g - t) ** 2) for g, t, w in zip(got, want, sizes))
     ref = sum(w * np.sum(t ** 2) for t, w in zip(want, sizes))
     return float(np.sqrt(err / max(ref, 1e-300)))
+
+
+def repeated_windows(cfg, batch, seed):
+    """batch windows that each repeat one token id (ids uniform in
+    [0, vocab) from `seed`), targets the same ids: nanochat's smear-lambda
+    gradient, a sum over positions and channels, then adds up over the
+    positions instead of nearly cancelling as it does on random windows."""
+    ids = np.random.default_rng(seed).integers(0, cfg.vocab, batch)
+    tok = np.repeat(ids[:, None], cfg.seq, 1).astype(np.uint16)
+    return tok, tok.copy()

@@ -152,17 +152,18 @@ def test_params_round_trip_and_profile():
 
 
 def test_graph_replay_matches_eager(monkeypatch):
-    """Eval loss replays a captured graph per batch size.  Every replay must
-    equal the same engine run eagerly (ANE_GRAPHS=0), bit for bit, across
-    changing windows, batch sizes, new parameters, eager work in between
-    (EvalLogits, a training step that allocates its buffers) and profiling."""
+    """With ANE_GRAPHS=1 eval loss replays a captured graph per batch size.
+    Every replay must equal the same engine run eagerly (the default), bit
+    for bit, across changing windows, batch sizes, new parameters, eager work
+    in between (EvalLogits, a training step that allocates its buffers) and
+    profiling."""
     cfg = ane.tiny("llama2", layers=4)
     p = ane.init_params(cfg, seed=11, std=0.08)
     stream = np.random.default_rng(12).integers(0, cfg.vocab, 6000).astype(np.uint16)
+    monkeypatch.setenv("ANE_GRAPHS", "1")
     eng_g = open_engine(cfg, p, max_batch=4, tokens=stream)
-    monkeypatch.setenv("ANE_GRAPHS", "0")
-    eng_e = open_engine(cfg, p, max_batch=4, tokens=stream)
     monkeypatch.delenv("ANE_GRAPHS")
+    eng_e = open_engine(cfg, p, max_batch=4, tokens=stream)
     rng = np.random.default_rng(13)
 
     def check(nseq):
