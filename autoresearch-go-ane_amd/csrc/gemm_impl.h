@@ -825,9 +825,20 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
   // prologue's wait covers them) and combined in LDS after the main loop.
   constexpr bool RR = epi_rr(EPI);
   constexpr int NRR = EPI == EPI_CE_RR ? BN : BM;
-  constexpr int RPER = RR ? (NRR * kRrMaxParts + 64 * NW - 1) / (64 * NW) : 1;
+  // RR_PRO (the 8-wave 256x256 tiles, one block per CU, whose LDS has room
+  // for it): rr is formed in the prologue, thread t < NRR summing row t's
+  // partials (loads in flight with the prologue's, added after its wait, in
+  // part order) into its own LDS slot, which the prologue's barrier
+  // publishes; the epilogue then needs no extra barrier (three extra
+  // barriers and the partials staged through LDS after the main loop cost
+  // the W1|W3 GEMM ~6 us of 55).  Otherwise the partials are loaded here and
+  // combined after the main loop.
+  constexpr bool RR_PRO = RR && NW == 8 && NRR <= 64 * NW;
+  __shared__ float rs_pro[RR_PRO ? NRR : 1];
+  constexpr int RPER = RR && !RR_PRO ? (NRR * kRrMaxParts + 64 * NW - 1) / (64 * NW) : 1;
   float rrv[RPER];
-  if constexpr (RR) {
+  float rrl[RR_PRO ? kRrMaxParts : 1];
+  if constexpr (RR && !RR_PRO) {
     const int r0 = EPI == EPI_CE_RR ? n0 : m0;
 #pragma unroll
     for (int k = 0; k < RPER; k++) {
@@ -913,6 +924,14 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
   // self-prefetch: slice blockIdx.x of kPfBlocks, at most kPfLoads 16-byte
   // loads per thread (the host sizes pf_bytes), in flight with the
   // prologue's loads and waited for with them
+  if constexpr (RR_PRO) {
+    const int r0 = EPI == EPI_CE_RR ? n0 : m0;
+    if (tid < NRR) {
+#pragma unroll
+      for (int p = 0; p < kRrMaxParts; p++)
+        rrl[p] = p < e.rr_nparts ? e.rr_part[(size_t)p * e.rr_ld + r0 + tid] : 0.f;
+    }
+  }
   uint4 pfv[kPfLoads];
   const bool pf_on = !TRA && !TRB && g.pf_bytes >= 16 && blockIdx.x < kPfBlocks;
   if (pf_on) {
@@ -922,7 +941,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
 #pragma unroll
     for (int u = 0; u < kPfLoads; u++) {
       const size_t i = i0 + (size_t)u * (64 * NW) + tid;
-      pfv[u] = q[i < i1 ? i : n16 - 1];  // unconditional: the index is clamped
+      pfv[u] = i < i1 ? q[i] : make_uint4(0, 0, 0, 0);  // lanes past the slice load nothing
     }
   }
   wait_tile();
@@ -931,6 +950,15 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
 #pragma unroll
     for (int u = 0; u < kPfLoads; u++) x ^= pfv[u].x ^ pfv[u].y ^ pfv[u].z ^ pfv[u].w;
     asm volatile("" ::"v"(x));
+  }
+  if constexpr (RR_PRO) {
+    if (tid < NRR) {
+      float sum = 0.f;
+#pragma unroll
+      for (int p = 0; p < kRrMaxParts; p++)
+        if (p < e.rr_nparts) sum += rrl[p];
+      rs_pro[tid] = 1.0f / sqrtf(sum / (float)e.rr_dim + 1e-5f);
+    }
   }
   __syncthreads();
   half8 fa[2][TM], fb[2][TN];
@@ -950,8 +978,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
   }
   // the epilogue of the CE variant reuses LDS as scratch
   if constexpr (EPI == EPI_CE || EPI == EPI_CE_RR) __syncthreads();
-  const float* rr_s = nullptr;
-  if constexpr (RR) {
+  const float* rr_s = RR_PRO ? rs_pro : nullptr;
+  if constexpr (RR && !RR_PRO) {
     // LDS: partials [kRrMaxParts][NRR], then rr [NRR]; rr = 1 / rms over
     // rr_dim columns, the parts added in order
     if constexpr (EPI != EPI_CE_RR) __syncthreads();
