@@ -1275,7 +1275,10 @@ extern "C" int ane_debug_gemm_bench(int a_t, int b_t, int epi, int M, int N, int
     f += N;
     p.ssq_part = f; p.ssq_ld = M;
     f += (size_t)kRrMaxParts * M;
-    p.C2 = f; p.ldc2 = N;
+    if (epi == EPI_RESID_NORM) {  // its fp16 x * gain output (the rr forms have no second output here)
+      p.C2 = f;
+      p.ldc2 = N;
+    }
   }
   if (epi == EPI_CE || epi == EPI_CE_RR) {
     char* x = (char*)dX;
