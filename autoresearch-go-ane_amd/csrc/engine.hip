@@ -183,15 +183,16 @@ void phase_sum(ane_engine* e, double ms[PH_COUNT]) {
 }
 
 hipError_t eng_gemm(ane_engine* e, int cls, const half_t* A, int lda, bool at, const half_t* B, int ldb, bool bt,
-                    int M, int N, int K, int epi, const EpiParams& p, int bm, int bn, bool side, bool selfpf) {
+                    int M, int N, int K, int epi, const EpiParams& p, int bm, int bn, bool side, const void* pf,
+                    size_t pf_bytes) {
   if (side && (!e->dw_stream || !e->tr.splitk_ws2)) return hipErrorInvalidValue;
   hipStream_t s = side ? e->dw_stream : e->stream;
   float* ws = side ? e->tr.splitk_ws2 : e->tr.splitk_ws;
   GemmArgs g;
   g.A = A; g.B = B; g.lda = lda; g.ldb = ldb; g.M = M; g.N = N; g.K = K; g.a_t = at; g.b_t = bt;
-  if (selfpf && !at && !bt && (size_t)N * K * 2 <= (size_t)kPfBlocks * kPfLoads * 256 * 16) {
-    g.pf = B;
-    g.pf_bytes = (size_t)N * K * 2;
+  if (pf && pf_bytes && !at && !bt) {
+    g.pf = pf;
+    g.pf_bytes = pf_bytes;
   }
   // training: GEMMs whose output is too small to fill the chip split K
   // (K-major operands, or M-major ones as the weight gradients read them)
@@ -705,8 +706,9 @@ int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
       EpiParams p;
       p.C = A.qkv; p.ldc = 3 * D;
       if (fused) rr(p, nparts);
+      // its weights were streamed by the previous layer's W2 GEMM (layer 0: by the embedding)
       HIPCHK(op, eng_gemm(e, 0, A.xn, D, false, s.wqkv, D, false, T, 3 * D, D, fused ? EPI_STORE_H_RR : EPI_STORE_H,
-                          p, 0, 0, false, fused && e->gemm_selfpf));
+                          p));
     }
     {
       AttnArgs a;
@@ -754,8 +756,9 @@ int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
           prof_end(e, 0, (double)3 * H * D * 2);
         }
         rr(p, nparts);
+        // streams its own weights and W2's (adjacent shadows)
         HIPCHK(op, eng_gemm(e, 2, A.xn2, D, false, s.w13, D, false, T, 2 * H, D, EPI_SWIGLU_RR, p, 0, 0, false,
-                            e->gemm_selfpf));
+                            e->gemm_selfpf ? s.w13 : nullptr, ((size_t)2 * H * D + (size_t)D * H) * sizeof(half_t)));
       } else if (llama) {
         HIPCHK(op, eng_gemm(e, 2, A.xn2, D, false, s.w13, D, false, T, 2 * H, D, EPI_SWIGLU, p));
       } else {
@@ -773,8 +776,10 @@ int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
         // the next norm's inputs: the next layer's attention norm, or the final norm
         p.C2 = A.xn; p.ldc2 = D; p.gain = P + (l + 1 < L ? e->pm.L[l + 1].g_att : e->pm.g_final);
         p.ssq_part = e->ssq_part; p.ssq_ld = T;
+        // streams the next layer's Wq|Wk|Wv (the classifier's come by a prefetch launch)
+        const void* pf2 = e->gemm_selfpf && l + 1 < L ? (const void*)e->ls[l + 1].wqkv : nullptr;
         HIPCHK(op, eng_gemm(e, 3, A.gate, H, false, s.w2, H, false, T, D, H, EPI_RESID_NORM, p, res_bm, res_bn, false,
-                            e->gemm_selfpf));
+                            pf2, (size_t)3 * D * D * sizeof(half_t)));
         nparts = D / res_bn;
       } else {
         HIPCHK(op, eng_gemm(e, 3, A.gate, H, false, s.w2, H, false, T, D, H, EPI_RESID, p));

@@ -170,9 +170,9 @@ struct ane_engine {
   float* ssq_part = nullptr;
   bool fused_norm = true;
   bool fused_pf = true;  // the classifier's weights by a prefetch launch (ANE_FUSED_PF)
-  // the deferred-norm forward's QKV, W1|W3 and W2 GEMMs stream their own
-  // weights from their first blocks (GemmArgs::pf; ANE_GEMM_SELFPF=0: a
-  // prefetch launch before each instead)
+  // the deferred-norm forward's GEMMs stream weights from their first
+  // blocks (GemmArgs::pf): W1|W3 its own and W2's, W2 the next layer's
+  // Wq|Wk|Wv (ANE_GEMM_SELFPF=0: a prefetch launch before QKV and W1|W3)
   bool gemm_selfpf = true;
   bool tr_dw = true;  // weight gradients read token-major operands directly (ANE_TR_DW=0: transposes)
   // The backward's weight-gradient GEMMs run on a second stream beside the
@@ -260,12 +260,12 @@ int eng_fail(ane_engine* e, int code, const char* fmt, ...);
   } while (0)
 void prof_begin(ane_engine* e, int cls, hipStream_t s = nullptr);
 void prof_end(ane_engine* e, double flops, double bytes, hipStream_t s = nullptr);
-// side = run on the dW stream with its own split-K workspace; selfpf = the
-// first blocks stream the weight operand B through the caches (when it fits
-// GemmArgs::pf's limit)
+// side = run on the dW stream with its own split-K workspace; pf / pf_bytes:
+// bytes the GEMM's first blocks stream through the caches with their
+// prologue loads (GemmArgs::pf; ignored past its limit)
 hipError_t eng_gemm(ane_engine* e, int cls, const ane::half_t* A, int lda, bool at, const ane::half_t* B, int ldb,
                     bool bt, int M, int N, int K, int epi, const ane::EpiParams& p, int bm = 0, int bn = 0,
-                    bool side = false, bool selfpf = false);
+                    bool side = false, const void* pf = nullptr, size_t pf_bytes = 0);
 int refresh_shadows(ane_engine* e);
 // the update job table of adam_fused_update for the segments of a (cached)
 int ensure_update_jobs(ane_engine* e, const ane::AdamArgs& a);

@@ -141,11 +141,7 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
                     int ns) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0 || (g.K % BK) != 0 || g.splits < 1 || g.splits > kMaxSplits)
     return hipErrorInvalidValue;
-  // the self-prefetch covers pf_bytes with kPfBlocks blocks of at least 256
-  // threads, kPfLoads loads each
-  if (g.pf_bytes && (!g.pf || ((uintptr_t)g.pf % 16) != 0 ||
-                     g.pf_bytes > (size_t)kPfBlocks * kPfLoads * 256 * 16))
-    return hipErrorInvalidValue;
+  if (g.pf_bytes && (!g.pf || ((uintptr_t)g.pf % 16) != 0)) return hipErrorInvalidValue;
   if (epi == EPI_RESID_NORM &&
       (!e.R || !e.C2 || !e.gain || !e.ssq_part || e.ssq_ld < g.M || g.splits != 1 || g.grp || g.a_t || g.b_t))
     return hipErrorInvalidValue;
@@ -180,6 +176,11 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
   if (nw == 0) nw = (bm == 256 && bn == 256) ? 8 : 4;
   if (nw != 4 && !(nw == 8 && bm == 256 && bn == 256)) return hipErrorInvalidValue;
   if (ns == 0) ns = 2;
+  // the self-prefetch is a hint: kPfBlocks blocks of 64 nw threads cover at
+  // most kPfLoads 16-byte loads each per thread; a longer region is cut
+  GemmArgs gp = g;
+  gp.pf_bytes = std::min(g.pf_bytes, (size_t)kPfBlocks * kPfLoads * 64 * nw * 16);
+  const GemmArgs& g2 = gp;
   // three LDS stages: both operands K-major, 4 waves, tiles whose 3 stages fit the 160 KB LDS
   if (ns != 2 && !(ns == 3 && nw == 4 && !g.a_t && !g.b_t && (bm + bn) <= 384 && !(bm == 256 && bn == 64) &&
                    !(bm == 128 && bn == 256)))
@@ -187,7 +188,7 @@ hipError_t gemm_run(const GemmArgs& g, int epi, const EpiParams& e, hipStream_t 
   const int lay = (g.a_t ? 2 : 0) | (g.b_t ? 1 : 0);
   if (g.grp && (lay != 0 || ns != 2)) return hipErrorInvalidValue;
 #define CASE(L, AT, BT, E) \
-  if (lay == L && epi == E) return launch<AT, BT, E>(g, e, s, bm, bn, nw, ns);
+  if (lay == L && epi == E) return launch<AT, BT, E>(g2, e, s, bm, bn, nw, ns);
   // forward (activation x weight^T)
   CASE(0, false, false, EPI_STORE_H)
   CASE(0, false, false, EPI_STORE_F)
