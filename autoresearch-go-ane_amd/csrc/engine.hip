@@ -249,6 +249,10 @@ static void free_all(ane_engine* e) {
       ev = nullptr;
     }
   e->refresh_pending = false;
+  for (hipEvent_t ev : e->upd_ev) (void)hipEventDestroy(ev);
+  e->upd_ev.clear();
+  e->upd_pending = false;
+  e->adam_unread = false;
   for (hipEvent_t ev : e->xev) (void)hipEventDestroy(ev);
   e->xev.clear();
   e->xev_next = 0;
@@ -409,6 +413,7 @@ extern "C" int ane_open(const ane_model_cfg* cfg, const ane_options* opts, ane_e
   if (const char* g = getenv("ANE_DW_ASYNC")) e->dw_async = atoi(g) != 0;
   if (const char* g = getenv("ANE_BWD_PREFETCH")) e->bwd_prefetch = atoi(g) != 0;
   if (const char* g = getenv("ANE_FUSED_ADAM")) e->fused_adam = atoi(g) != 0;
+  if (const char* g = getenv("ANE_ASYNC_UPDATE")) e->async_update = atoi(g) != 0;
   if (const char* g = getenv("ANE_PHASE_EVERY")) e->ph_period = atoi(g) > 0 ? atoi(g) : 1;
   e->lr = e->opt.lr;
   int rc = validate_cfg(e, e->cfg);
@@ -440,6 +445,7 @@ extern "C" void ane_destroy(ane_engine* e) {
 
 extern "C" int ane_sync(ane_engine* e) {
   CLOSED_CHECK("sync");
+  HIPCHK("sync", join_update(e));  // an asynchronous update still running
   HIPCHK("sync", hipStreamSynchronize(e->stream));
   if (e->dw_stream) HIPCHK("sync", hipStreamSynchronize(e->dw_stream));
   return ANE_OK;
@@ -499,6 +505,7 @@ int ensure_update_jobs(ane_engine* e, const AdamArgs& a) {
   for (int i = 0; i < a.nseg; i++) {
     sig.push_back(a.seg[i].off);
     sig.push_back(a.seg[i].len);
+    sig.push_back(a.seg[i].chunk);
   }
   if (e->upd_jobs && sig == e->upd_sig) return ANE_OK;
   // segments in parameter order, each cut at the matrices with a shadow
@@ -543,16 +550,51 @@ int ensure_update_jobs(ane_engine* e, const AdamArgs& a) {
   if (covered != e->pm.total)
     return eng_fail(e, ANE_ERR_STATE, "storiesane flush: parameter groups cover %lld of %lld",
                     (long long)covered, (long long)e->pm.total);
-  if ((int)jobs.size() > e->upd_cap) {
-    HIPCHK(op, dalloc(e, &e->upd_jobs, jobs.size()));
-    e->upd_cap = (int)jobs.size();
+  // chunk order (parameter order within a chunk), blocks renumbered to match
+  const int nch = 1 + e->cfg.layers;
+  std::vector<UpdateJob> by;
+  e->upd_j0.assign(nch, 0);
+  e->upd_nj.assign(nch, 0);
+  e->upd_b0.assign(nch, 0);
+  e->upd_nb.assign(nch, 0);
+  int nb = 0;
+  for (int c = 0; c < nch; c++) {
+    e->upd_j0[c] = (int)by.size();
+    e->upd_b0[c] = nb;
+    for (UpdateJob u : jobs) {
+      if (a.seg[u.seg].chunk != c) continue;
+      u.blk0 = nb;
+      nb += (int)((u.len + kUpdateChunk - 1) / kUpdateChunk);
+      by.push_back(u);
+    }
+    e->upd_nj[c] = (int)by.size() - e->upd_j0[c];
+    e->upd_nb[c] = nb - e->upd_b0[c];
   }
-  HIPCHK(op, hipStreamSynchronize(e->stream));  // no launch still reads the old table
-  HIPCHK(op, hipMemcpy(e->upd_jobs, jobs.data(), jobs.size() * sizeof(UpdateJob), hipMemcpyHostToDevice));
-  e->n_upd_jobs = (int)jobs.size();
-  e->n_upd_blocks = blocks;
+  if (by.size() != jobs.size() || nb != blocks)
+    return eng_fail(e, ANE_ERR_STATE, "storiesane flush: a parameter group has no update chunk");
+  if ((int)by.size() > e->upd_cap) {
+    HIPCHK(op, dalloc(e, &e->upd_jobs, by.size()));
+    e->upd_cap = (int)by.size();
+  }
+  // no launch still reads the old table (an asynchronous update reads it on the dW stream)
+  HIPCHK(op, hipStreamSynchronize(e->stream));
+  if (e->dw_stream) HIPCHK(op, hipStreamSynchronize(e->dw_stream));
+  HIPCHK(op, hipMemcpy(e->upd_jobs, by.data(), by.size() * sizeof(UpdateJob), hipMemcpyHostToDevice));
+  e->n_upd_jobs = (int)by.size();
+  e->n_upd_blocks = nb;
   e->upd_sig = sig;
   return ANE_OK;
+}
+
+hipError_t join_update(ane_engine* e) {
+  if (!e->upd_pending) return hipSuccess;
+  e->upd_pending = false;
+  return hipStreamWaitEvent(e->stream, e->upd_ev.back(), 0);
+}
+
+hipError_t wait_update(ane_engine* e, int chunk) {
+  if (!e->upd_pending) return hipSuccess;
+  return hipStreamWaitEvent(e->stream, e->upd_ev[chunk], 0);
 }
 
 int refresh_shadows(ane_engine* e) {
@@ -569,6 +611,7 @@ int refresh_shadows(ane_engine* e) {
 
 extern "C" int ane_set_params(ane_engine* e, const float* params, int64_t n) {
   CLOSED_CHECK("set params");
+  HIPCHK("set params", join_update(e));  // an asynchronous update still running
   if (!params || n != e->pm.total)
     return eng_fail(e, ANE_ERR_ARG, "storiesane set params: len=%lld want=%lld", (long long)n,
                     (long long)e->pm.total);
@@ -581,6 +624,7 @@ extern "C" int ane_set_params(ane_engine* e, const float* params, int64_t n) {
 
 extern "C" int ane_get_params(ane_engine* e, float* params, int64_t n) {
   CLOSED_CHECK("get params");
+  HIPCHK("get params", join_update(e));  // an asynchronous update still running
   if (!params || n != e->pm.total)
     return eng_fail(e, ANE_ERR_ARG, "storiesane get params: len=%lld want=%lld", (long long)n,
                     (long long)e->pm.total);
@@ -658,6 +702,10 @@ int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
   int nparts = 1;
 
   float* x_first = train ? tb.L[0].xin : e->x;
+  // a training forward behind an asynchronous update: each part starts once
+  // the update chunk of the weights it reads is done (every other caller
+  // has waited for the whole update at its entry point)
+  if (train) HIPCHK(op, wait_update(e, 0));
   if (llama && fused) {
     prof_begin(e, 7);
     HIPCHK(op, embed_xg(x_first, e->xh, e->ssq_part, P + e->pm.embed, e->tok, P + e->pm.L[0].g_att, T, D, V, st,
@@ -688,6 +736,7 @@ int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
       A.xin = e->x; A.x2 = e->x; A.xn = e->xh; A.xn2 = e->xh; A.qkv = e->qkv; A.att = e->att; A.gate = e->gate;
     }
     float* xout = train ? (l + 1 < L ? tb.L[l + 1].xin : tb.xlast) : e->x;
+    if (train) HIPCHK(op, wait_update(e, 1 + l));
     if (!fused) {
       prof_begin(e, 6);
       // each memory-bound kernel also streams the next GEMM's weights through
@@ -786,6 +835,7 @@ int forward_body(ane_engine* e, int nseq, int train, bool defer_norm) {
       }
     }
   }
+  if (train) e->upd_pending = false;  // the main stream now follows every chunk
   if (fused) {  // xh = fp16(x * g_final); the classifier applies 1 / rms
     if (e->fused_pf) {
       prof_begin(e, 6);
@@ -898,6 +948,7 @@ static int finish_loss(ane_engine* e, int nseq, float* loss_per_seq, float* mean
 extern "C" int ane_eval_loss(ane_engine* e, const uint16_t* tokens, const uint16_t* targets, int32_t nseq,
                              float* loss_per_seq, float* mean_loss) {
   CLOSED_CHECK("eval loss");
+  HIPCHK("eval loss", join_update(e));  // an asynchronous update still running
   if (nseq <= 0 || nseq > e->opt.max_batch || !tokens || !targets)
     return eng_fail(e, ANE_ERR_ARG, "storiesane eval loss: nseq=%d must be in [1, %d]", nseq, e->opt.max_batch);
   const size_t T = (size_t)nseq * e->cfg.seq;
@@ -928,6 +979,7 @@ int load_windows(ane_engine* e, const uint64_t* positions, int nseq) {
 extern "C" int ane_eval_loss_windows(ane_engine* e, const uint64_t* positions, int32_t nseq, float* loss_per_seq,
                                      float* mean_loss) {
   CLOSED_CHECK("eval loss");
+  HIPCHK("eval loss", join_update(e));  // an asynchronous update still running
   if (nseq <= 0 || nseq > e->opt.max_batch || !positions)
     return eng_fail(e, ANE_ERR_ARG, "storiesane eval loss: nseq=%d must be in [1, %d]", nseq, e->opt.max_batch);
   int rc = load_windows(e, positions, nseq);
@@ -938,6 +990,7 @@ extern "C" int ane_eval_loss_windows(ane_engine* e, const uint64_t* positions, i
 
 extern "C" int ane_eval_logits(ane_engine* e, const uint16_t* tokens, int64_t ntok, float* logits) {
   CLOSED_CHECK("eval logits");
+  HIPCHK("eval logits", join_update(e));  // an asynchronous update still running
   if (ntok != e->cfg.seq || !tokens)
     return eng_fail(e, ANE_ERR_ARG, "storiesane eval logits: token len=%lld want=%d", (long long)ntok, e->cfg.seq);
   if (!logits) return eng_fail(e, ANE_ERR_ARG, "storiesane eval logits: null output");

@@ -143,6 +143,26 @@ struct ane_engine {
   ane::UpdateJob* upd_jobs = nullptr;
   int n_upd_jobs = 0, n_upd_blocks = 0, upd_cap = 0;
   std::vector<int64_t> upd_sig;
+  // The table is ordered by update chunk: chunk 0 = the model-level groups
+  // (embedding, final gain; nanochat's smear and residual scalars), chunk
+  // 1 + l = layer l's groups; chunk c is jobs [upd_j0[c], upd_j0[c] + upd_nj[c])
+  // and blocks [upd_b0[c], upd_b0[c] + upd_nb[c]).
+  std::vector<int> upd_j0, upd_nj, upd_b0, upd_nb;
+  // Asynchronous update (accumulate-mode flushes with the dW stream;
+  // ANE_ASYNC_UPDATE=0: in line on the main stream): the gradient norm and
+  // the chunks run on the dW stream behind the backward, upd_ev[c] marking
+  // chunk c done, while the call returns once the losses are in.  The next
+  // training forward waits on the GPU for chunk 0 before the embedding and
+  // for chunk 1 + l before layer l; every other entry point that launches
+  // work waits for the whole update first (join_update).
+  bool async_update = true;
+  std::vector<hipEvent_t> upd_ev;
+  bool upd_pending = false;
+  // StepResult.AdamDuration of an asynchronous update: the step_ev pair is
+  // read once complete (adam_unread until then); adam_ns_last keeps the
+  // latest completed update's duration
+  bool adam_unread = false;
+  int64_t adam_ns_last = 0;
   bool shadow_jobs_t = false;
   float* rope_cos = nullptr;
   float* rope_sin = nullptr;
@@ -267,8 +287,13 @@ hipError_t eng_gemm(ane_engine* e, int cls, const ane::half_t* A, int lda, bool 
                     bool bt, int M, int N, int K, int epi, const ane::EpiParams& p, int bm = 0, int bn = 0,
                     bool side = false, const void* pf = nullptr, size_t pf_bytes = 0);
 int refresh_shadows(ane_engine* e);
-// the update job table of adam_fused_update for the segments of a (cached)
+// the update job table of adam_fused_update for the segments of a (cached),
+// in chunk order (AdamSeg::chunk)
 int ensure_update_jobs(ane_engine* e, const ane::AdamArgs& a);
+// An asynchronous update still pending: the main stream waits for all of it
+// (join_update) or for chunk c (wait_update); both are no-ops otherwise.
+hipError_t join_update(ane_engine* e);
+hipError_t wait_update(ane_engine* e, int chunk);
 int forward_body(ane_engine* e, int nseq, int train, bool defer_norm = false);
 void drop_fwd_graph(ane_engine* e);
 template <class T>

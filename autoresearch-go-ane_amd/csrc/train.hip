@@ -113,6 +113,12 @@ int ensure_train(ane_engine* e, const char* op) {
     if (!e->dw_stream) HIPCHK(op, hipStreamCreateWithFlags(&e->dw_stream, hipStreamNonBlocking));
     for (hipEvent_t& ev : e->refresh_ev)
       if (!ev) HIPCHK(op, hipEventCreate(&ev));
+    // update chunk events: ordering between the two streams only
+    while ((int)e->upd_ev.size() < 1 + c.layers) {
+      hipEvent_t x = nullptr;
+      HIPCHK(op, hipEventCreateWithFlags(&x, hipEventDisableTiming | hipEventDisableSystemFence));
+      e->upd_ev.push_back(x);
+    }
     HIPCHK(op, dalloc(e, &tb.splitk_ws2, tb.splitk_cap));
     HIPCHK(op, dalloc(e, &tb.dcur_h2, T * D));
     HIPCHK(op, dalloc(e, &tb.dh13_2, T * KH));
@@ -529,10 +535,20 @@ void bias_inv(int t, float b1, float b2, float* i1, float* i2) {
 }
 
 void add_seg(AdamArgs& a, int64_t off, int64_t len, float lr, float wd, float b1, float b2, float i1, float i2,
-             int clip) {
+             int clip, int chunk) {
   AdamSeg& s = a.seg[a.nseg++];
   s.off = off; s.len = len; s.lr = lr; s.wd = wd; s.b1 = b1; s.b2 = b2; s.i1 = i1; s.i2 = i2; s.clip = clip;
-  s.pad = 0;
+  s.chunk = chunk;
+}
+
+// The duration of the last asynchronous update into adam_ns_last once its
+// end event has completed (no wait).
+void read_adam_ns(ane_engine* e) {
+  if (!e->adam_unread || hipEventQuery(e->step_ev[ane_engine::EV_ADAM1]) != hipSuccess) return;
+  float ms = 0.f;
+  if (hipEventElapsedTime(&ms, e->step_ev[ane_engine::EV_ADAM0], e->step_ev[ane_engine::EV_ADAM1]) == hipSuccess)
+    e->adam_ns_last = (int64_t)((double)ms * 1e6);
+  e->adam_unread = false;
 }
 
 // flushPending (ane/engine.go:646-682)
@@ -546,10 +562,21 @@ int flush_pending(ane_engine* e) {
   TrainBufs& tb = e->tr;
   const ane_options& O = e->opt;
   hipStream_t st = e->stream;
+  // accumulate mode with the dW stream: the update runs there behind the
+  // backward, in chunks the next training forward waits for one at a time
+  const bool async_upd = e->async_update && e->fused_adam && e->shadow_jobs && e->shadow_jobs_t &&
+                         O.accum_steps > 1 && e->dw_stream && e->refresh_ev[1] &&
+                         (int)e->upd_ev.size() == 1 + (int)L;
+  hipStream_t us = async_upd ? e->dw_stream : st;
+  // the previous asynchronous update's duration, before its events are reused
+  if (e->adam_unread) HIPCHK(op, hipEventSynchronize(e->step_ev[ane_engine::EV_ADAM1]));
+  read_adam_ns(e);
+  HIPCHK(op, join_update(e));
+  if (async_upd) HIPCHK(op, stream_after(e, us, st));
 
   float gscale = (float)(1.0 / (double)e->state.pending_steps);
   gscale /= O.loss_scale;
-  HIPCHK(op, sumsq(tb.sumsq, tb.sumsq_part, tb.G, (size_t)(pm.embed + V * D), st));
+  HIPCHK(op, sumsq(tb.sumsq, tb.sumsq_part, tb.G, (size_t)(pm.embed + V * D), us));
   e->state.adam_t++;
   const int t = (int)e->state.adam_t;
   float i1, i2, l1, l2;
@@ -567,23 +594,24 @@ int flush_pending(ane_engine* e) {
   // and VE gate with the scalar lr, VE table with the embedding lr, no wd
   for (int l = 0; l < L; l++) {
     const LayerOff& o = pm.L[l];
-    add_seg(a, o.wq, o.w2 + D * H - o.wq, lr, wd, b1, b2, i1, i2, 1);
+    const int ch = 1 + l;
+    add_seg(a, o.wq, o.w2 + D * H - o.wq, lr, wd, b1, b2, i1, i2, 1, ch);
     if (llama) {
-      add_seg(a, o.w3, H * D, lr, wd, b1, b2, i1, i2, 1);
-      add_seg(a, o.g_att, 2 * D, scalar_lr, 0.f, b1, b2, i1, i2, 1);
+      add_seg(a, o.w3, H * D, lr, wd, b1, b2, i1, i2, 1, ch);
+      add_seg(a, o.g_att, 2 * D, scalar_lr, 0.f, b1, b2, i1, i2, 1, ch);
     } else if (o.ve_embed >= 0) {
-      add_seg(a, o.ve_embed, V * D, embed_lr, 0.f, b1, b2, i1, i2, 1);
-      add_seg(a, o.ve_gate, NH * 12, scalar_lr, 0.f, b1, b2, i1, i2, 1);
+      add_seg(a, o.ve_embed, V * D, embed_lr, 0.f, b1, b2, i1, i2, 1, ch);
+      add_seg(a, o.ve_gate, NH * 12, scalar_lr, 0.f, b1, b2, i1, i2, 1, ch);
     }
   }
   // model-level groups (ane/engine.go:659-673)
-  add_seg(a, pm.embed, V * D, embed_lr, 0.f, b1, b2, i1, i2, 1);
+  add_seg(a, pm.embed, V * D, embed_lr, 0.f, b1, b2, i1, i2, 1, 0);
   if (llama) {
-    add_seg(a, pm.g_final, D, scalar_lr, 0.f, b1, b2, i1, i2, 0);
+    add_seg(a, pm.g_final, D, scalar_lr, 0.f, b1, b2, i1, i2, 0, 0);
   } else {
-    add_seg(a, pm.smear_gate, D * D, lr, wd, b1, b2, i1, i2, 0);
-    add_seg(a, pm.smear_lambda, 2, scalar_lr, 0.f, b1, b2, i1, i2, 0);
-    add_seg(a, pm.resid, 2 * L, lambda_lr, 0.f, O.lambda_beta1, O.lambda_beta2, l1, l2, 0);
+    add_seg(a, pm.smear_gate, D * D, lr, wd, b1, b2, i1, i2, 0, 0);
+    add_seg(a, pm.smear_lambda, 2, scalar_lr, 0.f, b1, b2, i1, i2, 0, 0);
+    add_seg(a, pm.resid, 2 * L, lambda_lr, 0.f, O.lambda_beta1, O.lambda_beta2, l1, l2, 0, 0);
   }
   if (a.nseg > kMaxAdamSegs) return eng_fail(e, ANE_ERR_ARG, "storiesane flush: too many parameter groups");
   // the fp16 shadows the next forward and backward read: the weight refresh
@@ -594,14 +622,23 @@ int flush_pending(ane_engine* e) {
     // the plain ones
     int rc = ensure_update_jobs(e, a);
     if (rc) return rc;
-    (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM0], st);
-    HIPCHK(op, adam_fused_update(a, e->upd_jobs, e->n_upd_jobs, e->n_upd_blocks, st));
-    (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM1], st);
+    (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM0], us);
+    if (async_upd) {
+      for (int c = 0; c <= (int)L; c++) {
+        HIPCHK(op, adam_fused_update(a, e->upd_jobs + e->upd_j0[c], e->upd_nj[c], e->upd_nb[c], e->upd_b0[c], us));
+        HIPCHK(op, hipEventRecord(e->upd_ev[c], us));
+      }
+      e->upd_pending = true;
+      e->adam_unread = true;
+    } else {
+      HIPCHK(op, adam_fused_update(a, e->upd_jobs, e->n_upd_jobs, e->n_upd_blocks, 0, us));
+    }
+    (void)hipEventRecord(e->step_ev[ane_engine::EV_ADAM1], us);
     if (e->opt.accum_steps > 1 && e->dw_stream && e->refresh_ev[1]) {
       // accumulate mode: the refresh runs asynchronously (flushPending,
       // ane/engine.go:674-677), beside the next step's forward, which
       // reads only the plain shadows
-      HIPCHK(op, stream_after(e, e->dw_stream, st));
+      if (!async_upd) HIPCHK(op, stream_after(e, e->dw_stream, st));
       HIPCHK(op, hipEventRecord(e->refresh_ev[0], e->dw_stream));
       HIPCHK(op, shadow_transpose(e->shadow_jobs, e->n_shadow_jobs, e->n_shadow_tiles, e->dw_stream));
       HIPCHK(op, hipEventRecord(e->refresh_ev[1], e->dw_stream));
@@ -715,7 +752,13 @@ int train_windows(ane_engine* e, int nseq, ane_step_result* res) {
     res->dw_gemm_ns = e->ph_last_ns[PH_DW_GEMM] * nseq;
     res->dw_wait_ns = (int64_t)(wait_s * 1e9);
     if (e->flushed) {
-      res->adam_ns = ev_ns(ane_engine::EV_ADAM0, ane_engine::EV_ADAM1);
+      // an asynchronous update is still running: the latest completed one's
+      if (e->adam_unread) {
+        read_adam_ns(e);
+        res->adam_ns = e->adam_ns_last;
+      } else {
+        res->adam_ns = ev_ns(ane_engine::EV_ADAM0, ane_engine::EV_ADAM1);
+      }
       res->weight_refresh_ns = (int64_t)(ph[PH_REFRESH] * 1e6);
     }
     res->compile_ns = res->startup_compile_ns + res->weight_refresh_ns;
@@ -745,9 +788,11 @@ extern "C" int ane_train_batch(ane_engine* e, int32_t nseq, ane_step_result* res
 // reference's waitAsyncRefresh) and adds it to CumTrainMS / CumWallMS.
 extern "C" int ane_flush(ane_engine* e, int64_t* ns) {
   CLOSED_CHECK("flush");
+  HIPCHK("flush", join_update(e));  // an asynchronous update still running
   phase_reset(e);
   int rc = flush_pending(e);
   if (rc) return rc;
+  HIPCHK("flush", join_update(e));
   HIPCHK("flush", hipStreamSynchronize(e->stream));
   double ph[PH_COUNT];
   phase_sum(e, ph);
@@ -770,6 +815,7 @@ extern "C" int ane_flush(ane_engine* e, int64_t* ns) {
 extern "C" int ane_grads(ane_engine* e, const uint16_t* tokens, const uint16_t* targets, int32_t nseq, float* grads,
                          float* mean_loss) {
   CLOSED_CHECK("grads");
+  HIPCHK("grads", join_update(e));  // an asynchronous update still running
   const char* op = "grads";
   if (nseq <= 0 || nseq > e->opt.max_batch || !tokens || !targets || !grads)
     return eng_fail(e, ANE_ERR_ARG, "storiesane grads: nseq=%d must be in [1, %d]", nseq, e->opt.max_batch);
@@ -799,6 +845,7 @@ extern "C" int ane_grads(ane_engine* e, const uint16_t* tokens, const uint16_t* 
 
 extern "C" int ane_set_grads(ane_engine* e, const float* grads, int64_t n, uint32_t pending) {
   CLOSED_CHECK("set grads");
+  HIPCHK("set grads", join_update(e));  // an asynchronous update still running
   const char* op = "set grads";
   if (!grads || n != e->pm.total)
     return eng_fail(e, ANE_ERR_ARG, "storiesane set grads: len=%lld want=%lld", (long long)n, (long long)e->pm.total);
@@ -812,6 +859,7 @@ extern "C" int ane_set_grads(ane_engine* e, const float* grads, int64_t n, uint3
 
 extern "C" int ane_get_opt_state(ane_engine* e, float* m, float* v, int64_t n) {
   CLOSED_CHECK("optimizer state");
+  HIPCHK("optimizer state", join_update(e));  // an asynchronous update still running
   const char* op = "optimizer state";
   if (n != e->pm.total)
     return eng_fail(e, ANE_ERR_ARG, "storiesane optimizer state: len=%lld want=%lld", (long long)n,
@@ -826,6 +874,7 @@ extern "C" int ane_get_opt_state(ane_engine* e, float* m, float* v, int64_t n) {
 
 extern "C" int ane_set_opt_state(ane_engine* e, const float* m, const float* v, int64_t n) {
   CLOSED_CHECK("set optimizer state");
+  HIPCHK("set optimizer state", join_update(e));  // an asynchronous update still running
   const char* op = "set optimizer state";
   if (n != e->pm.total)
     return eng_fail(e, ANE_ERR_ARG, "storiesane set optimizer state: len=%lld want=%lld", (long long)n,
@@ -842,6 +891,7 @@ extern "C" int ane_set_opt_state(ane_engine* e, const float* m, const float* v, 
 
 extern "C" int ane_get_accum_grads(ane_engine* e, float* grads, int64_t n) {
   CLOSED_CHECK("accumulated grads");
+  HIPCHK("accumulated grads", join_update(e));  // an asynchronous update still running
   const char* op = "accumulated grads";
   if (!grads || n != e->pm.total)
     return eng_fail(e, ANE_ERR_ARG, "storiesane accumulated grads: len=%lld want=%lld", (long long)n,

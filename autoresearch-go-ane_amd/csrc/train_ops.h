@@ -103,7 +103,7 @@ struct AdamSeg {
   int64_t off, len;
   float lr, wd, b1, b2, i1, i2;
   int clip;
-  int pad;
+  int chunk;  // update chunk the host launches it in (scheduling only; the kernels ignore it)
 };
 constexpr int kMaxAdamSegs = 64;
 struct AdamArgs {
@@ -131,10 +131,13 @@ struct UpdateJob {
   half_t* sh;                  // plain fp16 shadow, [rows][C] (null: none)
   int C, blk_stride, blk_off;  // shadow row of source row r: (r / 32) * blk_stride + blk_off + r % 32
   int seg;                     // AdamArgs segment: hyperparameters
-  int blk0;                    // first block of the job
+  int blk0;                    // first block of the job (counted over the whole table)
   int vec;
 };
-hipError_t adam_fused_update(const AdamArgs& a, const UpdateJob* jobs_dev, int njobs, int nblocks, hipStream_t s);
+// One launch covers jobs_dev[0, njobs), whose blocks are [blk_base, blk_base + nblocks)
+// of the table: the whole table, or the jobs of one chunk (kept together).
+hipError_t adam_fused_update(const AdamArgs& a, const UpdateJob* jobs_dev, int njobs, int nblocks, int blk_base,
+                             hipStream_t s);
 // the transposed shadows (dst_t) of every job, read from the plain fp16 shadows
 hipError_t shadow_transpose(const ShadowJob* jobs_dev, int njobs, int ntiles, hipStream_t s);
 

@@ -428,12 +428,14 @@ __global__ __launch_bounds__(256) void adam_kernel(AdamArgs a) {
   }
 }
 
-// One block per kUpdateChunk elements of one job (binary search over blk0).
-__global__ __launch_bounds__(256) void adam_fused_kernel(AdamArgs a, const UpdateJob* jobs, int njobs) {
+// One block per kUpdateChunk elements of one job (binary search over blk0);
+// block blockIdx.x is block blk_base + blockIdx.x of the table.
+__global__ __launch_bounds__(256) void adam_fused_kernel(AdamArgs a, const UpdateJob* jobs, int njobs, int blk_base) {
+  const int blk = blk_base + (int)blockIdx.x;
   int lo = 0, hi = njobs - 1;
   while (lo < hi) {
     const int mid = (lo + hi + 1) >> 1;
-    if (jobs[mid].blk0 <= (int)blockIdx.x) lo = mid;
+    if (jobs[mid].blk0 <= blk) lo = mid;
     else hi = mid - 1;
   }
   const UpdateJob jb = jobs[lo];
@@ -458,7 +460,7 @@ __global__ __launch_bounds__(256) void adam_fused_kernel(AdamArgs a, const Updat
     if (sg.wd != 0.f) u += sg.wd * w;
     w -= sg.lr * u;
   };
-  const int64_t base = (int64_t)((int)blockIdx.x - jb.blk0) * kUpdateChunk;
+  const int64_t base = (int64_t)(blk - jb.blk0) * kUpdateChunk;
   if (jb.vec) {
 #pragma unroll
     for (int u = 0; u < kUpdateChunk / 1024; u++) {
@@ -692,9 +694,10 @@ hipError_t shadow_transpose(const ShadowJob* jobs_dev, int njobs, int ntiles, hi
   return hipGetLastError();
 }
 
-hipError_t adam_fused_update(const AdamArgs& a, const UpdateJob* jobs_dev, int njobs, int nblocks, hipStream_t s) {
-  if (a.nseg <= 0 || a.nseg > kMaxAdamSegs || njobs <= 0 || nblocks <= 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(adam_fused_kernel, dim3(nblocks), dim3(256), 0, s, a, jobs_dev, njobs);
+hipError_t adam_fused_update(const AdamArgs& a, const UpdateJob* jobs_dev, int njobs, int nblocks, int blk_base,
+                             hipStream_t s) {
+  if (a.nseg <= 0 || a.nseg > kMaxAdamSegs || njobs <= 0 || nblocks <= 0 || blk_base < 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(adam_fused_kernel, dim3(nblocks), dim3(256), 0, s, a, jobs_dev, njobs, blk_base);
   return hipGetLastError();
 }
 

@@ -311,11 +311,63 @@ def test_training_error_behaviour():
     eng.Destroy()
 
 
-@pytest.mark.parametrize("arch", ["llama2", "nanochat"])
-def test_step_result_phase_timers_and_flush_duration(arch):
+@pytest.mark.parametrize("arch,nseq,accum,calls", [("llama2", 8, 16, 2), ("llama2", 8, 8, 3), ("llama2", 2, 1, 3),
+                                                    ("nanochat", 2, 2, 3)])
+def test_async_update_matches_update_in_line(arch, nseq, accum, calls, monkeypatch):
+    """The update of an accumulate-mode flush on the dW stream, in per-layer
+    chunks the next forward waits for (ANE_ASYNC_UPDATE=1, the default),
+    gives what the update in line on the main stream gives: the same losses
+    call after call and the same weights and optimizer state (bit for bit
+    where no atomically summed gradient feeds them).  Reading the weights
+    waits for an update still running."""
+    cfg = ane.stories110m(arch) if nseq == 8 else ane.tiny(arch, layers=2)
+    p = ane.init_params(cfg, seed=81, std=0.05)
+    stream = np.random.default_rng(82).integers(0, cfg.vocab, 64 * (cfg.seq + 1)).astype(np.uint16)
+    out = {}
+    for flag in ("0", "1"):
+        monkeypatch.setenv("ANE_ASYNC_UPDATE", flag)
+        eng = open_engine(cfg, p, max_batch=nseq, tokens=stream, AccumSteps=accum, LR=1e-3, GradClip=1.0)
+        try:
+            losses = [eng.TrainBatch(nseq).loss for _ in range(calls)]
+            w = eng.Params()
+            m, v = eng.OptState()
+            out[flag] = (losses, w, m, v, eng.State().adam_t)
+        finally:
+            eng.Destroy()
+    pending, updates = 0, 0
+    for _ in range(calls):  # TrainBatch flushes once pending >= AccumSteps
+        pending += nseq
+        if pending >= accum:
+            pending, updates = 0, updates + 1
+    assert out["0"][4] == out["1"][4] == updates
+    # the atomically summed gradient segments (embedding rows of repeated
+    # tokens, nanochat's value embeddings) round differently per run, and so
+    # do the updates and losses that follow from them, by a few ulps
+    # (the next forward rounds its activations to fp16, which turns such
+    # differences into whole-ulp ones in a few activations; two runs of the
+    # in-line update differ by ~4e-6 in every weight tensor after 3
+    # updates, and by ~2e-4 in the moments, which follow the gradients.  A
+    # forward reading a layer before its update would move that layer's
+    # weights and gradients by ~lr / |w| ~ 2e-2.)
+    np.testing.assert_allclose(out["0"][0], out["1"][0], rtol=1e-6)
+    for what, a, b, tol in zip(("w", "m", "v"), out["0"][1:4], out["1"][1:4], (1e-4, 2e-3, 2e-3)):
+        for name, off, shape in ane.param_layout(cfg):
+            n = int(np.prod(shape))
+            x, y = a[off:off + n].astype(np.float64), b[off:off + n].astype(np.float64)
+            if updates == 1 and name.split(".")[-1] not in ATOMIC_SEGMENTS:
+                assert np.array_equal(x, y), (what, name)
+            else:
+                assert np.linalg.norm(x - y) <= tol * max(np.linalg.norm(x), 1e-12), (what, name)
+
+
+@pytest.mark.parametrize("arch,async_update", [("llama2", "1"), ("llama2", "0"), ("nanochat", "1")])
+def test_step_result_phase_timers_and_flush_duration(arch, async_update, monkeypatch):
     """StepResult's phase durations (ane/engine.go:416-441) and Flush's
     return value (the weight-refresh time, added to CumTrainMS,
-    ane/engine.go:484-496)."""
+    ane/engine.go:484-496).  With the update asynchronous (the default) a
+    flushing call reports the latest update that has completed: the one
+    before its own."""
+    monkeypatch.setenv("ANE_ASYNC_UPDATE", async_update)
     cfg = ane.tiny(arch, layers=2)
     p = ane.init_params(cfg, seed=61, std=0.05)
     stream = np.random.default_rng(62).integers(0, cfg.vocab, 4000).astype(np.uint16)
@@ -334,15 +386,20 @@ def test_step_result_phase_timers_and_flush_duration(arch):
         # ane/engine.go:674-682); Flush waits for it and returns its duration
         r2 = eng.TrainBatch(2)
         assert r2.startup_compile_ns == 0
-        assert r2.adam_ns > 0 and r2.weight_refresh_ns == 0 and r2.compile_ns == 0
+        assert (r2.adam_ns > 0 or async_update == "1") and r2.weight_refresh_ns == 0 and r2.compile_ns == 0
         assert eng.State().pending_steps == 0
         assert eng.Flush() > 0           # nothing pending: the outstanding refresh
         assert eng.Flush() == 0          # nothing pending, nothing outstanding
+        eng.TrainBatch(2)                # 2 pending
+        r4 = eng.TrainBatch(2)           # 4 pending: the second update
+        assert r4.adam_ns > 0            # (asynchronous: the first one's, complete since the Flush)
+        assert eng.State().adam_t == 2
+        eng.Flush()
         eng.Step()                       # one pending window
         before = eng.State().cum_train_ms
         ns = eng.Flush()
         st = eng.State()
-        assert ns > 0 and st.pending_steps == 0 and st.adam_t == 2
+        assert ns > 0 and st.pending_steps == 0 and st.adam_t == 3
         assert abs((st.cum_train_ms - before) - ns / 1e6) < 1e-6
     finally:
         eng.Destroy()
