@@ -77,8 +77,10 @@ void gemm_pick_tile(int M, int N, int K, int epi, int* pbm, int* pbn) {
 void gemm_pick_split(int M, int N, int K, int epi, size_t ws_cap, int* pbm, int* pbn, int* psplits) {
   // Rules from a sweep of the training shapes on MI355X (B16 x 256, so
   // K = tokens = 4096 for the weight gradients):
-  //  (a) very long K (dy = dlogits Embed, K = vocab): 256x256 tiles split
-  //      until >= 160 blocks (4 splits: 838 TFLOP/s vs 537 for 64x64);
+  //  (a) very long K (dy = dlogits Embed, K = vocab): 256x256 tiles, split
+  //      so that the last round of blocks over the 256 CUs is the fullest
+  //      (fewest splits on a tie): 48 tiles at B16 take 5 splits, 240
+  //      blocks (204 us vs 229 for 4 splits, 192 blocks; 233 for 10);
   //  (b) long K and room for >= 256 blocks of 256x256: one pass of the big
   //      tile (classifier weight gradient: 953 vs 832 for 128x128);
   //  (c) long K with fewer than 512 blocks of the default tile (dW of
@@ -96,12 +98,20 @@ void gemm_pick_split(int M, int N, int K, int epi, size_t ws_cap, int* pbm, int*
   const bool big = M % 256 == 0 && N % 256 == 0;
   const long t256 = big ? (long)(M / 256) * (N / 256) : 0;
   if (big && K >= 16384) {
-    for (int sp : {1, 2, 3, 4, 5, 6, 8}) {
+    int best = 0;
+    double best_fill = 0.0;
+    for (int sp : {1, 2, 3, 4, 5, 6, 8, 10}) {
       if (!fits(sp)) continue;
-      if (t256 * sp >= 160) {
-        *pbm = 256; *pbn = 256; *psplits = sp;
-        return;
+      const long b = t256 * sp;
+      const double fill = (double)b / (double)(((b + 255) / 256) * 256);
+      if (fill > best_fill + 1e-9) {
+        best_fill = fill;
+        best = sp;
       }
+    }
+    if (best) {
+      *pbm = 256; *pbn = 256; *psplits = best;
+      return;
     }
   }
   if (big && K >= 2048 && t256 >= 256) {

@@ -177,11 +177,12 @@ __device__ __forceinline__ void block_tile(int nbm, int nbn, int bid, int& bm, i
 // of C; bm is the block's row-tile index (classifier partials); lds is
 // free scratch once the main loop is done (classifier reduction).
 // rr_s (rr variants): LDS, 1 / rms of the block's rows (EPI_CE_RR: columns),
-// indexed from m0 (n0).
+// indexed from m0 (n0).  tg_pre (cross-entropy, optional): the target id of
+// each of the lane's TN columns, loaded ahead.
 template <int BN, int WTM, int WTN, int TM, int TN, int EPI>
 __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs& g, const EpiParams& e, int m0,
                                          int n0, int bm, int wm, int wn, int lane, half_t* lds,
-                                         const float* rr_s = nullptr) {
+                                         const float* rr_s = nullptr, const int* tg_pre = nullptr) {
   const int rbase = m0 + wm * WTM + 4 * (lane >> 5);
   const int cbase = n0 + wn * WTN + (lane & 31);
 #define ROW(i, r) (rbase + (i) * 32 + 8 * ((r) >> 2) + ((r) & 3))
@@ -465,7 +466,7 @@ __device__ __forceinline__ void epilogue(floatx16 (&acc)[TM][TN], const GemmArgs
       const int n = n0 + nl;
       // the target's row relative to this lane's first row: a match is one
       // compare against a constant per register
-      const int tsel = e.targets[n] - ROW(0, 0);
+      const int tsel = (tg_pre ? tg_pre[j] : (int)e.targets[n]) - ROW(0, 0);
       const bool hit = tsel >= 0 && tsel < 32 * TM && (tsel & 4) == 0;
       const float rr_col = EPI == EPI_CE_RR ? rr_s[nl] : 1.f;
       float mx = -INFINITY, tv = 0.f;
@@ -743,8 +744,15 @@ __device__ __forceinline__ half8 tr_frag(const half_t* tile, int r0, int s, int 
   return __builtin_bit_cast(half8, lohi);
 }
 
-template <int BM, int BN, int EPI, int NW, bool TRA = false, bool TRB = false>
+// PERSIST: a grid of fewer blocks than tiles, block b taking tiles b, b +
+// gridDim.x, ... (K-major, one split, no groups): each next tile's first two
+// k-tiles (and its rr partials) are requested before the current tile's
+// epilogue runs, which then overlaps their latency instead of a block
+// launch plus a prologue following it.  The epilogue's LDS scratch (the
+// cross-entropy merge) and 1/rms rows are separate from the stages.
+template <int BM, int BN, int EPI, int NW, bool TRA = false, bool TRB = false, bool PERSIST = false>
 __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams e) {
+  static_assert(!PERSIST || (!TRA && !TRB), "persistent form: K-major operands only");
   constexpr int WN = NW / 2;
   constexpr int WTM = BM / 2, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
   constexpr int STAGE = (BM + BN) * BK;  // halves
@@ -769,7 +777,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
   int bm, bn;
   block_tile(g.M / BM, g.N / BN, bid, bm, bn);
   int m0 = bm * BM;
-  const int n0 = bn * BN;
+  int n0 = bn * BN;
   const half_t* Bp = g.B;
   if (g.grp) {  // grouped: row tile bm of the valid tiles, B of its group
     if (bm >= g.grp[0]) return;  // whole block, before any LDS traffic
@@ -802,6 +810,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
   if constexpr (TRB) vob[0] = tr_voff(BN, g.ldb);
   const half_t* abase = TRA ? g.A + koff * g.lda + m0 : g.A + (size_t)m0 * g.lda + koff;
   const half_t* bbase = TRB ? Bp + koff * g.ldb + n0 : Bp + (size_t)n0 * g.ldb + koff;
+  int tile = bid;  // PERSIST: the tile in hand
   auto dma_a = [&](int q, int kt, int st) {
     const int gi = wave_s + NW * q;
     if constexpr (TRA)
@@ -834,10 +843,26 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
   // the W1|W3 GEMM ~6 us of 55).  Otherwise the partials are loaded here and
   // combined after the main loop.
   constexpr bool RR_PRO = RR && NW == 8 && NRR <= 64 * NW;
-  __shared__ float rs_pro[RR_PRO ? NRR : 1];
+  static_assert(!PERSIST || !RR || RR_PRO, "persistent form: rr formed in the prologue only");
+  static_assert(!PERSIST || EPI != EPI_RESID_NORM, "persistent form: no epilogue that stages through the LDS stages");
+  // PERSIST: two rr buffers (the tile in hand's, the next one's) and the
+  // cross-entropy merge scratch of its own
+  __shared__ float rs_pro[RR_PRO ? (PERSIST ? 2 : 1) * NRR : 1];
+  constexpr bool CE_SCRATCH = PERSIST && (EPI == EPI_CE || EPI == EPI_CE_RR);
+  __shared__ __attribute__((aligned(16))) float2 ce_red[CE_SCRATCH ? 2 * BN : 1];
+  int rbuf = 0;
+  // PERSIST: the rr partials come in by the same LDS DMA as the operands
+  // (one 1 KB row segment per partial), so no registers hold them across
+  // the epilogue that runs while they are in flight
+  constexpr bool RR_STAGE = PERSIST && RR_PRO;
+  static_assert(!RR_STAGE || NRR == 256, "rr staging: one 16-byte load per lane per partial");
+  __shared__ __attribute__((aligned(16))) float rr_stage[RR_STAGE ? kRrMaxParts * NRR : 1];
   constexpr int RPER = RR && !RR_PRO ? (NRR * kRrMaxParts + 64 * NW - 1) / (64 * NW) : 1;
   float rrv[RPER];
-  float rrl[RR_PRO ? kRrMaxParts : 1];
+  float rrl[RR_PRO && !RR_STAGE ? kRrMaxParts : 1];
+  // PERSIST, cross-entropy: the target ids of the tile being set up (loaded
+  // with its prologue) and of the tile in hand
+  int tg_next[CE_SCRATCH ? TN : 1], tg_cur[CE_SCRATCH ? TN : 1];
   if constexpr (RR && !RR_PRO) {
     const int r0 = EPI == EPI_CE_RR ? n0 : m0;
 #pragma unroll
@@ -911,29 +936,46 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
   using I2 = std::integral_constant<int, 2>;
 
   // prologue: tiles 0 and 1 in flight, wait for both
+  auto prologue_loads = [&]() {
 #pragma unroll
-  for (int q = 0; q < LA; q++) dma_a(q, 0, 0);
+    for (int q = 0; q < LA; q++) dma_a(q, 0, 0);
 #pragma unroll
-  for (int q = 0; q < LB; q++) dma_b(q, 0, 0);
-  if (nk > 1) {
+    for (int q = 0; q < LB; q++) dma_b(q, 0, 0);
+    if (nk > 1) {
 #pragma unroll
-    for (int q = 0; q < LA; q++) dma_a(q, 1, 1);
+      for (int q = 0; q < LA; q++) dma_a(q, 1, 1);
 #pragma unroll
-    for (int q = 0; q < LB; q++) dma_b(q, 1, 1);
-  }
+      for (int q = 0; q < LB; q++) dma_b(q, 1, 1);
+    }
+    if constexpr (RR_STAGE) {
+      const int r0 = EPI == EPI_CE_RR ? n0 : m0;
+      const unsigned rr0 = (unsigned)(size_t)(lds_ptr_t)rr_stage;
+#pragma unroll
+      for (int q = 0; q < kRrMaxParts / NW; q++) {
+        const int p = wave_s + NW * q;
+        if (p < e.rr_nparts)
+          dma16_at(reinterpret_cast<const half_t*>(e.rr_part + (size_t)p * e.rr_ld + r0 + lane * 4),
+                   rr0 + (unsigned)(p * NRR * 4));
+      }
+    } else if constexpr (RR_PRO) {
+      const int r0 = EPI == EPI_CE_RR ? n0 : m0;
+      if (tid < NRR) {
+#pragma unroll
+        for (int p = 0; p < kRrMaxParts; p++)
+          rrl[p] = p < e.rr_nparts ? e.rr_part[(size_t)p * e.rr_ld + r0 + tid] : 0.f;
+      }
+    }
+    if constexpr (CE_SCRATCH) {
+#pragma unroll
+      for (int j = 0; j < TN; j++) tg_next[j] = e.targets[n0 + wn * WTN + j * 32 + (lane & 31)];
+    }
+  };
+  prologue_loads();
   // self-prefetch: slice blockIdx.x of kPfBlocks, at most kPfLoads 16-byte
   // loads per thread (the host sizes pf_bytes), in flight with the
   // prologue's loads and waited for with them
-  if constexpr (RR_PRO) {
-    const int r0 = EPI == EPI_CE_RR ? n0 : m0;
-    if (tid < NRR) {
-#pragma unroll
-      for (int p = 0; p < kRrMaxParts; p++)
-        rrl[p] = p < e.rr_nparts ? e.rr_part[(size_t)p * e.rr_ld + r0 + tid] : 0.f;
-    }
-  }
   uint4 pfv[kPfLoads];
-  const bool pf_on = !TRA && !TRB && g.pf_bytes >= 16 && blockIdx.x < kPfBlocks;
+  bool pf_on = !TRA && !TRB && g.pf_bytes >= 16 && blockIdx.x < kPfBlocks;
   if (pf_on) {
     const uint4* q = reinterpret_cast<const uint4*>(g.pf);
     const size_t n16 = g.pf_bytes / 16, per = (n16 + kPfBlocks - 1) / kPfBlocks;
@@ -944,70 +986,118 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
       pfv[u] = i < i1 ? q[i] : make_uint4(0, 0, 0, 0);  // lanes past the slice load nothing
     }
   }
-  wait_tile();
-  if (pf_on) {
-    uint32_t x = 0;
+  for (;;) {  // one pass, or (PERSIST) one per tile of the block
+    wait_tile();
+    if (pf_on) {
+      uint32_t x = 0;
 #pragma unroll
-    for (int u = 0; u < kPfLoads; u++) x ^= pfv[u].x ^ pfv[u].y ^ pfv[u].z ^ pfv[u].w;
-    asm volatile("" ::"v"(x));
-  }
-  if constexpr (RR_PRO) {
-    if (tid < NRR) {
-      float sum = 0.f;
-#pragma unroll
-      for (int p = 0; p < kRrMaxParts; p++)
-        if (p < e.rr_nparts) sum += rrl[p];
-      rs_pro[tid] = 1.0f / sqrtf(sum / (float)e.rr_dim + 1e-5f);
+      for (int u = 0; u < kPfLoads; u++) x ^= pfv[u].x ^ pfv[u].y ^ pfv[u].z ^ pfv[u].w;
+      asm volatile("" ::"v"(x));
+      pf_on = false;
     }
-  }
-  __syncthreads();
-  half8 fa[2][TM], fb[2][TN];
+    if constexpr (RR_STAGE) {
+      barrier_keep_loads();  // every wave's partial rows are in
+      if (tid < NRR) {
+        float sum = 0.f;
 #pragma unroll
-  for (int q = 0; q < NRD; q++) read_frag(fa[0], fb[0], lds, 0, q);
-  __builtin_amdgcn_sched_barrier(0);
+        for (int p = 0; p < kRrMaxParts; p++)
+          if (p < e.rr_nparts) sum += rr_stage[p * NRR + tid];
+        rs_pro[rbuf * NRR + tid] = 1.0f / sqrtf(sum / (float)e.rr_dim + 1e-5f);
+      }
+    } else if constexpr (RR_PRO) {
+      if (tid < NRR) {
+        float sum = 0.f;
+#pragma unroll
+        for (int p = 0; p < kRrMaxParts; p++)
+          if (p < e.rr_nparts) sum += rrl[p];
+        rs_pro[rbuf * NRR + tid] = 1.0f / sqrtf(sum / (float)e.rr_dim + 1e-5f);
+      }
+    }
+    if constexpr (CE_SCRATCH) {
+#pragma unroll
+      for (int j = 0; j < TN; j++) tg_cur[j] = tg_next[j];
+    }
+    __syncthreads();
+    half8 fa[2][TM], fb[2][TN];
+#pragma unroll
+    for (int q = 0; q < NRD; q++) read_frag(fa[0], fb[0], lds, 0, q);
+    __builtin_amdgcn_sched_barrier(0);
 
-  for (int kt = 0; kt < nk; kt++) {
-    const half_t* cur = lds + (kt & 1) * STAGE;
-    const half_t* nxt = lds + ((kt + 1) & 1) * STAGE;
-    substep(F{}, I2{}, fa[0], fb[0], fa[1], fb[1], cur, 1, kt >= 1 && kt + 1 < nk, kt + 1, (kt + 1) & 1);
-    substep(F{}, I0{}, fa[1], fb[1], fa[0], fb[0], cur, 2, false, 0, 0);
-    substep(T{}, I0{}, fa[0], fb[0], fa[1], fb[1], cur, 3, false, 0, 0);
-    wait_tile();           // this wave's loads of tile kt+1
-    barrier_keep_loads();  // everyone's, and every read of stage kt is done
-    substep(F{}, I1{}, fa[1], fb[1], fa[0], fb[0], nxt, 0, kt + 2 < nk, kt + 2, kt & 1);
-  }
-  // the epilogue of the CE variant reuses LDS as scratch
-  if constexpr (EPI == EPI_CE || EPI == EPI_CE_RR) __syncthreads();
-  const float* rr_s = RR_PRO ? rs_pro : nullptr;
-  if constexpr (RR && !RR_PRO) {
-    // LDS: partials [kRrMaxParts][NRR], then rr [NRR]; rr = 1 / rms over
-    // rr_dim columns, the parts added in order
-    if constexpr (EPI != EPI_CE_RR) __syncthreads();
-    float* pl = reinterpret_cast<float*>(lds);
-    float* rs = pl + kRrMaxParts * NRR;
+    for (int kt = 0; kt < nk; kt++) {
+      const half_t* cur = lds + (kt & 1) * STAGE;
+      const half_t* nxt = lds + ((kt + 1) & 1) * STAGE;
+      substep(F{}, I2{}, fa[0], fb[0], fa[1], fb[1], cur, 1, kt >= 1 && kt + 1 < nk, kt + 1, (kt + 1) & 1);
+      substep(F{}, I0{}, fa[1], fb[1], fa[0], fb[0], cur, 2, false, 0, 0);
+      substep(T{}, I0{}, fa[0], fb[0], fa[1], fb[1], cur, 3, false, 0, 0);
+      wait_tile();           // this wave's loads of tile kt+1
+      barrier_keep_loads();  // everyone's, and every read of stage kt is done
+      substep(F{}, I1{}, fa[1], fb[1], fa[0], fb[0], nxt, 0, kt + 2 < nk, kt + 2, kt & 1);
+    }
+    if constexpr (PERSIST) {
+      // the next tile's first k-tiles (and rr partials, target ids) go out
+      // before this tile's epilogue, once every wave is past its last read
+      // of the stages
+      const int bm_c = bm, m0_c = m0, n0_c = n0;
+      const float* rr_c = RR_PRO ? rs_pro + rbuf * NRR : nullptr;
+      const int next = tile + (int)gridDim.x;
+      const bool more = next < ntiles;
+      if (more) {
+        __syncthreads();
+        tile = next;
+        block_tile(g.M / BM, g.N / BN, tile, bm, bn);
+        m0 = bm * BM;
+        n0 = bn * BN;
+        abase = g.A + (size_t)m0 * g.lda;
+        bbase = g.B + (size_t)n0 * g.ldb;
+        prologue_loads();
+      }
+      epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, e, m0_c, n0_c, bm_c, wm, wn, lane,
+                                          CE_SCRATCH ? reinterpret_cast<half_t*>(ce_red) : lds, rr_c,
+                                          CE_SCRATCH ? tg_cur : nullptr);
+      if (!more) return;
 #pragma unroll
-    for (int k = 0; k < RPER; k++) {
-      const int idx = tid + k * 64 * NW;
-      if (idx < kRrMaxParts * NRR) pl[idx] = rrv[k];
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+      rbuf ^= 1;
+      continue;
     }
-    __syncthreads();
-    for (int row = tid; row < NRR; row += 64 * NW) {
-      float sum = 0.f;
-      for (int p = 0; p < e.rr_nparts; p++) sum += pl[p * NRR + row];
-      rs[row] = 1.0f / sqrtf(sum / (float)e.rr_dim + 1e-5f);
+    // the epilogue of the CE variant reuses LDS as scratch
+    if constexpr (EPI == EPI_CE || EPI == EPI_CE_RR) __syncthreads();
+    const float* rr_s = RR_PRO ? rs_pro : nullptr;
+    if constexpr (RR && !RR_PRO) {
+      // LDS: partials [kRrMaxParts][NRR], then rr [NRR]; rr = 1 / rms over
+      // rr_dim columns, the parts added in order
+      if constexpr (EPI != EPI_CE_RR) __syncthreads();
+      float* pl = reinterpret_cast<float*>(lds);
+      float* rs = pl + kRrMaxParts * NRR;
+#pragma unroll
+      for (int k = 0; k < RPER; k++) {
+        const int idx = tid + k * 64 * NW;
+        if (idx < kRrMaxParts * NRR) pl[idx] = rrv[k];
+      }
+      __syncthreads();
+      for (int row = tid; row < NRR; row += 64 * NW) {
+        float sum = 0.f;
+        for (int p = 0; p < e.rr_nparts; p++) sum += pl[p * NRR + row];
+        rs[row] = 1.0f / sqrtf(sum / (float)e.rr_dim + 1e-5f);
+      }
+      __syncthreads();
+      rr_s = rs;
     }
-    __syncthreads();
-    rr_s = rs;
+    if constexpr (EPI == EPI_STORE_F) {
+      if (g.splits > 1) {  // this split's slice of the workspace (C = ws, ldc = N)
+        EpiParams es = e;
+        es.C = (float*)e.C + (size_t)ks * g.M * g.N;
+        epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, es, m0, n0, bm, wm, wn, lane, lds);
+        return;
+      }
+    }
+    epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, e, m0, n0, bm, wm, wn, lane, lds, rr_s);
+    return;
   }
-  if constexpr (EPI == EPI_STORE_F) {
-    if (g.splits > 1) {  // this split's slice of the workspace (C = ws, ldc = N)
-      EpiParams es = e;
-      es.C = (float*)e.C + (size_t)ks * g.M * g.N;
-      epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, es, m0, n0, bm, wm, wn, lane, lds);
-      return;
-    }
-  }
-  epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, e, m0, n0, bm, wm, wn, lane, lds, rr_s);
 }
 
 // Sum of the split-K workspace slices in split order, then the epilogue:
@@ -1073,6 +1163,23 @@ hipError_t launch_tile(const GemmArgs& g, const EpiParams& e, hipStream_t s) {
 #define LAUNCH_HOT(BM_, BN_, NW_) \
   hipLaunchKernelGGL((gemm_ho_kernel<BM_, BN_, EPI, NW_, AT, BT>), grid, dim3(64 * NW_), 0, s, g, e)
 
+// Blocks of a persistent launch (opt-in, ANE_GEMM_PERSIST=1, read at each
+// launch): the CU count, a multiple of the 8 XCDs the tile order assumes;
+// 0 = one block per tile.  Measured on the B32 forward (W1|W3: 512 tiles,
+// classifier: 4000) no faster than one block per tile (2.642 against 2.641
+// ms per step), so not the default.
+inline int persist_blocks() {
+  static const int cus = [] {
+    int dev = 0, cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cu, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                  hipSuccess)
+      return 0;
+    return cu / 8 * 8;
+  }();
+  const char* f = getenv("ANE_GEMM_PERSIST");
+  return f && atoi(f) != 0 ? cus : 0;
+}
+
 template <bool AT, bool BT, int EPI>
 hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, int bn, int nw, int ns) {
   const int key = bm * 1000 + bn;
@@ -1103,7 +1210,19 @@ hipError_t launch(const GemmArgs& g, const EpiParams& e, hipStream_t s, int bm, 
   constexpr bool HO_ONLY = epi_rr(EPI) || EPI == EPI_RESID_NORM;
   if constexpr (!AT && !BT && EPI != EPI_RESID_NORM) {
     if (nw == 8 && ns == 2) {  // caller checked the tile
-      const dim3 grid((g.M / 256) * (g.N / 256) * g.splits);
+      const int ntiles = (g.M / 256) * (g.N / 256);
+      if constexpr (EPI == EPI_CE || EPI == EPI_CE_RR || EPI == EPI_SWIGLU || EPI == EPI_SWIGLU_RR ||
+                    EPI == EPI_STORE_H || EPI == EPI_STORE_H_RR) {
+        // more tiles than CUs: one block per CU (the tile's LDS allows no
+        // more), each walking its tiles (ANE_GEMM_PERSIST=1)
+        const int ncu = persist_blocks();
+        if (g.splits == 1 && !g.grp && ncu > 0 && ntiles > ncu) {
+          hipLaunchKernelGGL((gemm_ho_kernel<256, 256, EPI, 8, false, false, true>), dim3(ncu), dim3(512), 0, s, g,
+                             e);
+          return hipGetLastError();
+        }
+      }
+      const dim3 grid(ntiles * g.splits);
       LAUNCH_HO(256, 256, 8);
       return hipGetLastError();
     }
