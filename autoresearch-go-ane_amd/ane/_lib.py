@@ -114,6 +114,7 @@ SIGNATURES = {
     "ane_debug_classifier": (C.c_int, [C.c_int, C.c_int, C.c_int, _u16, _u16, _u16, C.c_int, C.c_int, C.c_int,
                                        C.c_int, C.c_int, _fp, _fp, _fp, _fp, _fp, _u16, _u16]),
     "ane_debug_last_error": (C.c_char_p, []),
+    "ane_kernel_abi": (C.c_int, [C.c_char_p, C.POINTER(C.c_int64), C.POINTER(C.c_int64), C.c_int]),
     "ane_debug_gemm_bench": (C.c_int, [C.c_int] * 12 + [_u16, _u16, _fp]),
     "ane_head_loss": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                 C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p]),

@@ -34,8 +34,7 @@ constexpr int HD = 64;
 // pair's two q blocks run on two waves side by side instead of one after
 // the other on one wave; 128 VGPRs, so that two 8-wave blocks share a CU.
 template <int SMAX, bool HILO, bool PERQ>
-__global__ __launch_bounds__(PERQ ? 512 : 256) __attribute__((amdgpu_waves_per_eu(PERQ ? 4 : 1)))
-void attn_fwd_kernel(AttnArgs a) {
+__device__ __forceinline__ void attn_fwd_body(const AttnArgs& a) {
   __shared__ __attribute__((aligned(16))) half_t Ks[SMAX * HD];
   __shared__ __attribute__((aligned(16))) half_t Ks_lo[HILO ? SMAX * HD : 8];
   constexpr int VST = SMAX + 4;  // V^T row stride (halves): 2-way-free b64 reads
@@ -372,7 +371,19 @@ void attn_fwd_kernel(AttnArgs a) {
   }
 }
 
+template <int SMAX, bool HILO, bool PERQ>
+__global__ __launch_bounds__(PERQ ? 512 : 256) __attribute__((amdgpu_waves_per_eu(PERQ ? 4 : 1)))
+void attn_fwd_kernel(AttnArgs a) {
+  attn_fwd_body<SMAX, HILO, PERQ>(a);
+}
+
 }  // namespace
+
+// The per-q-block kernel (S <= 256, no split operands) under a C name for
+// a host that loads the code object itself (ane_kernels.h): 512 threads.
+extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void ane_k_attn_fwd(AttnArgs a) {
+  attn_fwd_body<256, false, true>(a);
+}
 
 hipError_t attention_fwd(const AttnArgs& a, hipStream_t stream) {
   if (a.S <= 0 || a.S % 64 != 0 || a.S > 512 || a.NH <= 0 || a.nseq <= 0) return hipErrorInvalidValue;

@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "../../include/ane_hip.h"
+#include "../../include/ane_kernels.h"
 #include "attention.h"
 #include "engine_internal.h"
 #include "gemm.h"
@@ -1054,6 +1055,45 @@ static int debug_fail(const char* what, hipError_t h) {
   } while (0)
 
 extern "C" const char* ane_debug_last_error(void) { return g_debug_err.c_str(); }
+
+// The argument structs of the code objects' kernels as compiled here (the C
+// mirrors of ane_kernels.h are checked against them where the kernels are).
+extern "C" int ane_kernel_abi(const char* name, int64_t* size, int64_t* offsets, int max) {
+  if (!name || !size) return -1;
+  std::vector<int64_t> off;
+#define ANE_FIELD(T, f) off.push_back((int64_t)offsetof(T, f))
+  if (!strcmp(name, "AneGemmArgs")) {
+    *size = (int64_t)sizeof(GemmArgs);
+    ANE_FIELD(GemmArgs, A); ANE_FIELD(GemmArgs, B); ANE_FIELD(GemmArgs, lda); ANE_FIELD(GemmArgs, ldb);
+    ANE_FIELD(GemmArgs, M); ANE_FIELD(GemmArgs, N); ANE_FIELD(GemmArgs, K); ANE_FIELD(GemmArgs, a_t);
+    ANE_FIELD(GemmArgs, b_t); ANE_FIELD(GemmArgs, grp); ANE_FIELD(GemmArgs, b_group_stride);
+    ANE_FIELD(GemmArgs, splits); ANE_FIELD(GemmArgs, ws); ANE_FIELD(GemmArgs, pf); ANE_FIELD(GemmArgs, pf_bytes);
+  } else if (!strcmp(name, "AneEpiParams")) {
+    *size = (int64_t)sizeof(EpiParams);
+    ANE_FIELD(EpiParams, C); ANE_FIELD(EpiParams, ldc); ANE_FIELD(EpiParams, C2); ANE_FIELD(EpiParams, ldc2);
+    ANE_FIELD(EpiParams, R); ANE_FIELD(EpiParams, X0); ANE_FIELD(EpiParams, alpha); ANE_FIELD(EpiParams, beta);
+    ANE_FIELD(EpiParams, scale); ANE_FIELD(EpiParams, alpha_ptr); ANE_FIELD(EpiParams, beta_ptr);
+    ANE_FIELD(EpiParams, accumulate); ANE_FIELD(EpiParams, seq); ANE_FIELD(EpiParams, targets);
+    ANE_FIELD(EpiParams, partial); ANE_FIELD(EpiParams, tgt_logit); ANE_FIELD(EpiParams, lse);
+    ANE_FIELD(EpiParams, colscale); ANE_FIELD(EpiParams, softcap); ANE_FIELD(EpiParams, cap);
+    ANE_FIELD(EpiParams, vocab); ANE_FIELD(EpiParams, C3); ANE_FIELD(EpiParams, rowscale); ANE_FIELD(EpiParams, gain);
+    ANE_FIELD(EpiParams, ssq_part); ANE_FIELD(EpiParams, ssq_ld); ANE_FIELD(EpiParams, rr_part);
+    ANE_FIELD(EpiParams, rr_ld); ANE_FIELD(EpiParams, rr_nparts); ANE_FIELD(EpiParams, rr_dim);
+  } else if (!strcmp(name, "AneAttnArgs")) {
+    *size = (int64_t)sizeof(AttnArgs);
+    ANE_FIELD(AttnArgs, qkv); ANE_FIELD(AttnArgs, out); ANE_FIELD(AttnArgs, lse); ANE_FIELD(AttnArgs, rope_cos);
+    ANE_FIELD(AttnArgs, rope_sin); ANE_FIELD(AttnArgs, nseq); ANE_FIELD(AttnArgs, S); ANE_FIELD(AttnArgs, NH);
+    ANE_FIELD(AttnArgs, qknorm); ANE_FIELD(AttnArgs, scale); ANE_FIELD(AttnArgs, ve_x); ANE_FIELD(AttnArgs, ve_gate);
+    ANE_FIELD(AttnArgs, ve_embed); ANE_FIELD(AttnArgs, tokens); ANE_FIELD(AttnArgs, vocab); ANE_FIELD(AttnArgs, qkvt);
+    ANE_FIELD(AttnArgs, qkvt_lo); ANE_FIELD(AttnArgs, hilo); ANE_FIELD(AttnArgs, pf); ANE_FIELD(AttnArgs, pf_bytes);
+    ANE_FIELD(AttnArgs, split_from);
+  } else {
+    return -1;
+  }
+#undef ANE_FIELD
+  for (int i = 0; i < (int)off.size() && i < max && offsets; i++) offsets[i] = off[i];
+  return (int)off.size();
+}
 
 extern "C" int ane_debug_gemm(int a_t, int b_t, int epi, int M, int N, int K, const uint16_t* A, const uint16_t* B,
                               void* C, int bm, int bn, int nw, int ns, int splits) {

@@ -750,8 +750,10 @@ __device__ __forceinline__ half8 tr_frag(const half_t* tile, int r0, int s, int 
 // epilogue runs, which then overlaps their latency instead of a block
 // launch plus a prologue following it.  The epilogue's LDS scratch (the
 // cross-entropy merge) and 1/rms rows are separate from the stages.
+// The kernel body is a device function so that the code object's extern "C"
+// entry points (module_gemm.hip) share it with the templated kernel.
 template <int BM, int BN, int EPI, int NW, bool TRA = false, bool TRB = false, bool PERSIST = false>
-__global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams e) {
+__device__ __forceinline__ void gemm_ho_body(const GemmArgs& g, const EpiParams& e) {
   static_assert(!PERSIST || (!TRA && !TRB), "persistent form: K-major operands only");
   constexpr int WN = NW / 2;
   constexpr int WTM = BM / 2, WTN = BN / WN, TM = WTM / 32, TN = WTN / 32;
@@ -1098,6 +1100,11 @@ __global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams 
     epilogue<BN, WTM, WTN, TM, TN, EPI>(acc, g, e, m0, n0, bm, wm, wn, lane, lds, rr_s);
     return;
   }
+}
+
+template <int BM, int BN, int EPI, int NW, bool TRA = false, bool TRB = false, bool PERSIST = false>
+__global__ __launch_bounds__(64 * NW) void gemm_ho_kernel(GemmArgs g, EpiParams e) {
+  gemm_ho_body<BM, BN, EPI, NW, TRA, TRB, PERSIST>(g, e);
 }
 
 // Sum of the split-K workspace slices in split order, then the epilogue:

@@ -21,10 +21,6 @@ __global__ __launch_bounds__(256) void embed_kernel(float* x, const float* E, co
   for (int i = lane; i < D; i += 64) xr[i] = tk < V ? er[i] : 0.f;
 }
 
-__global__ __launch_bounds__(256) void prefetch_kernel(const void* pf, size_t pf_bytes) {
-  prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
-}
-
 // Each thread keeps four 16-byte loads in flight per region pass.
 __global__ __launch_bounds__(256) void prefetch_list_kernel(PrefetchList l) {
   uint32_t x = 0;
@@ -43,29 +39,6 @@ __global__ __launch_bounds__(256) void prefetch_list_kernel(PrefetchList l) {
     }
   }
   asm volatile("" ::"v"(x));
-}
-
-// x = E[tok] (0 for tok >= V), xg = fp16(x * gain), ssq[t] = sum of x^2 (the
-// deferred norm's one partial per row); the next GEMM's weights streamed
-// through the caches alongside.
-__global__ __launch_bounds__(256) void embed_xg_kernel(float* x, half_t* xg, float* ssq, const float* E,
-                                                       const uint16_t* tok, const float* gain, int T, int D, int V,
-                                                       const void* pf, size_t pf_bytes) {
-  prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
-  const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (t >= T) return;
-  const int tk = tok[t];
-  const float* er = E + (size_t)tk * D;
-  float ss = 0.f;
-  for (int i = lane; i < D; i += 64) {
-    const float v = tk < V ? er[i] : 0.f;
-    const size_t idx = (size_t)t * D + i;
-    x[idx] = v;
-    xg[idx] = (half_t)(v * gain[i]);
-    ss += v * v;
-  }
-  ss = wave_sum(ss);
-  if (lane == 0) ssq[t] = ss;
 }
 
 __global__ __launch_bounds__(256) void embed_norm_kernel(float* xpre, float* x0, half_t* xh, const float* E,
@@ -172,9 +145,64 @@ __global__ void gather_arg_kernel(uint16_t* tok, uint16_t* tgt, const uint16_t* 
   tgt[i] = data[p + 1];
 }
 
+__global__ void f32_to_f16_kernel(half_t* dst, const float* src, size_t n) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) dst[i] = (half_t)src[i];
+}
+
+__global__ void interleave_w13_kernel(half_t* dst, const float* w1, const float* w3, int H, int D) {
+  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t n = (size_t)2 * H * D, stride = (size_t)gridDim.x * blockDim.x;
+  for (; i < n; i += stride) {
+    const int f = (int)(i / D), c = (int)(i % D);
+    const int blk = f >> 5;
+    const int row = (blk >> 1) * 32 + (f & 31);
+    const float* src = (blk & 1) ? w3 : w1;
+    dst[i] = (half_t)src[(size_t)row * D + c];
+  }
+}
+
+inline int rows_grid(int T) { return (T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK; }
+inline int flat_grid(size_t n) {
+  size_t g = (n + 255) / 256;
+  return (int)(g > 65536 ? 65536 : (g == 0 ? 1 : g));
+}
+
+}  // namespace
+
+// Kernels a host loads from the code object itself (ane_kernels.h): C
+// names, launched below by the library as well.
+extern "C" __global__ __launch_bounds__(256) void ane_k_prefetch(const void* pf, size_t pf_bytes) {
+  prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
+}
+
+// x = E[tok] (0 for tok >= V), xg = fp16(x * gain), ssq[t] = sum of x^2 (the
+// deferred norm's one partial per row); the next GEMM's weights streamed
+// through the caches alongside.
+extern "C" __global__ __launch_bounds__(256) void ane_k_embed_xg(float* x, half_t* xg, float* ssq, const float* E,
+                                                            const uint16_t* tok, const float* gain, int T, int D, int V,
+                                                       const void* pf, size_t pf_bytes) {
+  prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
+  const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= T) return;
+  const int tk = tok[t];
+  const float* er = E + (size_t)tk * D;
+  float ss = 0.f;
+  for (int i = lane; i < D; i += 64) {
+    const float v = tk < V ? er[i] : 0.f;
+    const size_t idx = (size_t)t * D + i;
+    x[idx] = v;
+    xg[idx] = (half_t)(v * gain[i]);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) ssq[t] = ss;
+}
+
 // Per token: merge the partials with a running (max, sum) pair; 4 lanes
 // split the partials of one token and combine with two xor-shuffles.
-__global__ __launch_bounds__(256) void ce_token_kernel(float* lse_out, float* tok_loss, const float2* partial,
+extern "C" __global__ __launch_bounds__(256) void ane_k_ce_token(float* lse_out, float* tok_loss, const float2* partial,
                                                        int np, const float* tgt_logit, const uint16_t* tgt, int V,
                                                        int T) {
   const int n = blockIdx.x * 64 + (threadIdx.x >> 2), q = threadIdx.x & 3;
@@ -207,7 +235,7 @@ __global__ __launch_bounds__(256) void ce_token_kernel(float* lse_out, float* to
   }
 }
 
-__global__ __launch_bounds__(256) void ce_reduce_kernel(float* loss_seq, float* colscale, float dscale,
+extern "C" __global__ __launch_bounds__(256) void ane_k_ce_reduce(float* loss_seq, float* colscale, float dscale,
                                                         const float* tok_loss, const uint16_t* tgt, int V, int S) {
   const int b = blockIdx.x;
   __shared__ float red_l[256];
@@ -242,31 +270,6 @@ __global__ __launch_bounds__(256) void ce_reduce_kernel(float* loss_seq, float* 
   }
 }
 
-__global__ void f32_to_f16_kernel(half_t* dst, const float* src, size_t n) {
-  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (; i < n; i += stride) dst[i] = (half_t)src[i];
-}
-
-__global__ void interleave_w13_kernel(half_t* dst, const float* w1, const float* w3, int H, int D) {
-  size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const size_t n = (size_t)2 * H * D, stride = (size_t)gridDim.x * blockDim.x;
-  for (; i < n; i += stride) {
-    const int f = (int)(i / D), c = (int)(i % D);
-    const int blk = f >> 5;
-    const int row = (blk >> 1) * 32 + (f & 31);
-    const float* src = (blk & 1) ? w3 : w1;
-    dst[i] = (half_t)src[(size_t)row * D + c];
-  }
-}
-
-inline int rows_grid(int T) { return (T + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK; }
-inline int flat_grid(size_t n) {
-  size_t g = (n + 255) / 256;
-  return (int)(g > 65536 ? 65536 : (g == 0 ? 1 : g));
-}
-
-}  // namespace
 
 hipError_t embed_lookup(float* x, const float* E, const uint16_t* tok, int T, int D, int V, hipStream_t s) {
   hipLaunchKernelGGL(embed_kernel, dim3(rows_grid(T)), dim3(256), 0, s, x, E, tok, T, D, V);
@@ -277,7 +280,7 @@ hipError_t prefetch_weights(const void* p, size_t bytes, hipStream_t s) {
   if (!p || bytes < 16) return hipSuccess;
   const size_t n16 = bytes / 16;
   const unsigned blocks = (unsigned)std::min<size_t>(1024, (n16 + 255) / 256);
-  hipLaunchKernelGGL(prefetch_kernel, dim3(blocks), dim3(256), 0, s, p, bytes);
+  hipLaunchKernelGGL(ane_k_prefetch, dim3(blocks), dim3(256), 0, s, p, bytes);
   return hipGetLastError();
 }
 
@@ -292,7 +295,7 @@ hipError_t prefetch_list(const PrefetchList& l, hipStream_t s) {
 
 hipError_t embed_xg(float* x, half_t* xg, float* ssq, const float* E, const uint16_t* tok, const float* gain, int T,
                     int D, int V, hipStream_t s, const void* pf, size_t pf_bytes) {
-  hipLaunchKernelGGL(embed_xg_kernel, dim3(rows_grid(T)), dim3(256), 0, s, x, xg, ssq, E, tok, gain, T, D, V, pf,
+  hipLaunchKernelGGL(ane_k_embed_xg, dim3(rows_grid(T)), dim3(256), 0, s, x, xg, ssq, E, tok, gain, T, D, V, pf,
                      pf_bytes);
   return hipGetLastError();
 }
@@ -331,9 +334,9 @@ hipError_t ce_reduce(float* loss_seq, float* lse, float* tok_loss, float* colsca
                      const float2* partial, int np, const float* tgt_logit, const uint16_t* tgt, int V, int nseq, int S,
                      hipStream_t s) {
   const int T = nseq * S;
-  hipLaunchKernelGGL(ce_token_kernel, dim3((T + 63) / 64), dim3(256), 0, s, lse, tok_loss, partial, np, tgt_logit,
+  hipLaunchKernelGGL(ane_k_ce_token, dim3((T + 63) / 64), dim3(256), 0, s, lse, tok_loss, partial, np, tgt_logit,
                      tgt, V, T);
-  hipLaunchKernelGGL(ce_reduce_kernel, dim3(nseq), dim3(256), 0, s, loss_seq, colscale, dscale, tok_loss, tgt, V, S);
+  hipLaunchKernelGGL(ane_k_ce_reduce, dim3(nseq), dim3(256), 0, s, loss_seq, colscale, dscale, tok_loss, tgt, V, S);
   return hipGetLastError();
 }
 

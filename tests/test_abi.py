@@ -64,3 +64,27 @@ def test_open_requires_weights():
         assert str(e) == "storiesane open: model path is empty"
     else:
         raise AssertionError("Open without weights must fail")
+
+
+def test_code_object_arg_structs_match_the_kernels():
+    """The ctypes mirrors of include/ane_kernels.h's argument structs (what a
+    host that launches the code objects itself passes) against the layout
+    the kernels were compiled with."""
+    from ane import hsaco
+    hsaco.check_abi()
+
+
+def test_code_objects_hold_the_kernel_table():
+    """Every kernel include/ane_kernels.h names is a global kernel of one of
+    the built code objects (gfx950 ELF)."""
+    from ane import hsaco
+    src = open(os.path.join(ROOT, "include", "ane_kernels.h")).read()
+    names = sorted(n for n in set(re.findall(r"\b(ane_k_\w+)", src)) if not n.endswith("_"))
+    assert len(names) >= 9
+    blobs = []
+    for fname in hsaco.MODULES.values():
+        data = open(os.path.join(hsaco.HERE, fname), "rb").read()
+        assert data[:4] == b"\x7fELF", fname
+        blobs.append(data)
+    for n in names:
+        assert any((n + ".kd").encode() in b for b in blobs), n
