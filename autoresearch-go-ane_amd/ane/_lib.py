@@ -63,6 +63,20 @@ class MoeCfg(C.Structure):
                 ("max_tokens", C.c_int32), ("device", C.c_int32)]
 
 
+class LayerWeights(C.Structure):
+    """ane_layer_weights (include/ane_objects.h)."""
+    _fields_ = [(n, C.POINTER(C.c_float)) for n in ("wq", "wk", "wv", "wo", "w1", "w2")]
+
+
+LAYER_TAPS = ("x_norm", "q", "k", "v", "att_out", "x2", "x2_norm", "h1", "gate")
+
+
+class LayerCache(C.Structure):
+    """ane_layer_cache (include/ane_objects.h)."""
+    _fields_ = [(n, C.POINTER(C.c_float)) for n in LAYER_TAPS] + [("att_taps_ready", C.c_int32),
+                                                                  ("ffn_taps_ready", C.c_int32)]
+
+
 class ProfEntry(C.Structure):
     _fields_ = [("launches", C.c_int64), ("ms", C.c_double), ("flops", C.c_double), ("bytes", C.c_double)]
 
@@ -142,6 +156,32 @@ SIGNATURES = {
     "ane_moe_run": (C.c_int, [_eng]),
     "ane_moe_read_output": (C.c_int, [_eng, _fp, C.POINTER(C.c_int32), _fp]),
     "ane_moe_last_ms": (C.c_double, [_eng]),
+    # the per-object seam (include/ane_objects.h)
+    "ane_seam_last_error": (C.c_char_p, []),
+    "ane_layer_forward_open": (C.c_int, [C.c_int32] * 4 + [C.POINTER(LayerWeights), C.POINTER(C.c_void_p)]),
+    "ane_layer_forward_run": (C.c_int, [_eng, _fp, _fp]),
+    "ane_layer_forward_run_taps": (C.c_int, [_eng, _fp, _fp, C.POINTER(LayerCache)]),
+    "ane_layer_forward_refresh": (C.c_int, [_eng, C.POINTER(LayerWeights)]),
+    "ane_layer_forward_close": (None, [_eng]),
+    "ane_layer_forward_destroy": (None, [_eng]),
+    "ane_layer_backward_open": (C.c_int, [C.c_int32] * 4 + [C.POINTER(LayerWeights), C.POINTER(C.c_void_p)]),
+    "ane_layer_backward_run_attention": (C.c_int, [_eng] + [_fp] * 8),
+    "ane_layer_backward_run_ffn": (C.c_int, [_eng] + [_fp] * 4),
+    "ane_layer_backward_refresh": (C.c_int, [_eng, C.POINTER(LayerWeights)]),
+    "ane_layer_backward_close": (None, [_eng]),
+    "ane_layer_backward_destroy": (None, [_eng]),
+    "ane_offload_open": (C.c_int, [C.c_int32] * 3 + [_fp, C.c_int32, C.POINTER(C.c_void_p)]),
+    "ane_offload_has": (C.c_int, [_eng, C.c_int32]),
+    "ane_offload_disable": (None, [_eng, C.c_int32]),
+    "ane_offload_run_rms_forward": (C.c_int, [_eng, _fp, _fp]),
+    "ane_offload_run_classifier_forward": (C.c_int, [_eng, _fp, _fp]),
+    "ane_offload_run_classifier_softmax": (C.c_int, [_eng, _fp, _fp]),
+    "ane_offload_run_softmax": (C.c_int, [_eng, _fp]),
+    "ane_offload_run_classifier_backward": (C.c_int, [_eng, _fp, _fp]),
+    "ane_offload_run_rms_backward": (C.c_int, [_eng, _fp, _fp, _fp]),
+    "ane_offload_refresh": (C.c_int, [_eng, _fp]),
+    "ane_offload_close": (None, [_eng]),
+    "ane_offload_destroy": (None, [_eng]),
 }
 
 _lib = None

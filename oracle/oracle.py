@@ -36,6 +36,17 @@ class OrcMoeCfg(C.Structure):
     _fields_ = [("dim", C.c_int32), ("hidden", C.c_int32), ("experts", C.c_int32)]
 
 
+class OrcSeamLayer(C.Structure):
+    _fields_ = [(n, C.POINTER(C.c_float)) for n in ("wq", "wk", "wv", "wo", "w1", "w2")]
+
+
+SEAM_TAPS = ("x_norm", "q", "k", "v", "att_out", "x2", "x2_norm", "h1", "gate")
+
+
+class OrcSeamTaps(C.Structure):
+    _fields_ = [(n, C.POINTER(C.c_float)) for n in SEAM_TAPS]
+
+
 class OrcAdam(C.Structure):
     _fields_ = [(n, C.c_float) for n in (
         "lr", "beta1", "beta2", "eps", "weight_decay", "grad_clip", "embed_lr_mult",
@@ -95,6 +106,18 @@ def lib():
         L.orc_moe_route.argtypes = [C.POINTER(OrcMoeCfg), fp, fp, C.c_int, i32, fp]
         L.orc_moe_forward.restype = None
         L.orc_moe_forward.argtypes = [C.POINTER(OrcMoeCfg), fp, fp, C.c_int, C.c_int, fp, i32, fp]
+        L.orc_linear_bwd_dx_cf.argtypes = [fp, fp, fp, C.c_int, C.c_int, C.c_int]
+        L.orc_rmsnorm_noweight_bwd_cf.argtypes = [fp, fp, fp, C.c_int, C.c_int]
+        L.orc_causal_attention_bwd_cf.argtypes = [fp, fp, fp, fp, fp, fp, fp, C.c_int, C.c_int, C.c_int, C.c_float]
+        L.orc_matmul_vocab_seq.argtypes = [fp, fp, fp, C.c_int, C.c_int, C.c_int]
+        L.orc_matmul_embedT.argtypes = [fp, fp, fp, C.c_int, C.c_int, C.c_int]
+        L.orc_softmax_row.argtypes = [fp, fp, C.c_int]
+        L.orc_seam_layer_forward.argtypes = [C.POINTER(OrcSeamLayer), C.c_int, C.c_int, C.c_int, C.c_int, fp, fp,
+                                             C.POINTER(OrcSeamTaps)]
+        L.orc_seam_attention_backward.argtypes = [C.POINTER(OrcSeamLayer), C.c_int, C.c_int, C.c_int, fp, fp, fp,
+                                                  fp, fp, fp, fp, fp]
+        L.orc_seam_ffn_backward.argtypes = [C.POINTER(OrcSeamLayer), C.c_int, C.c_int, C.c_int, fp, fp, fp, fp]
+        L.orc_seam_softmax_vocab.argtypes = [fp, C.c_int, C.c_int]
         ncpu = os.cpu_count() or 1
         L.orc_set_threads(min(ncpu, 64))
         L.orc_set_parallel_linear(1)
@@ -289,3 +312,80 @@ def moe_forward(params, x, hidden, experts, threads=None):
 def drand48_stream(seed, n):
     st = C.c_uint64(lib().orc_drand48_seed(int(seed)))
     return np.array([lib().orc_drand48_next(C.byref(st)) for _ in range(n)])
+
+
+# --- the per-object accelerator seam (refseam.c) --------------------------
+def _seam_layer(w):
+    """w: dict of fp32 arrays wq, wk, wv, wo [D, D], w1 [H, D], w2 [D, H]."""
+    keep = {n: np.ascontiguousarray(w[n], dtype=np.float32) for n in ("wq", "wk", "wv", "wo", "w1", "w2")}
+    return OrcSeamLayer(*[_f(keep[n]) for n in ("wq", "wk", "wv", "wo", "w1", "w2")]), keep
+
+
+def seam_layer_forward(w, heads, x):
+    """The layer forward the accelerator programs compute; x [D, seq].
+    Returns (out, taps) with the runWithTaps taps as a dict."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    dim, seq = x.shape
+    hidden = w["w1"].shape[0]
+    lw, keep = _seam_layer(w)
+    out = np.zeros_like(x)
+    taps = {n: np.zeros((hidden if n in ("h1", "gate") else dim, seq), np.float32) for n in SEAM_TAPS}
+    t = OrcSeamTaps(*[_f(taps[n]) for n in SEAM_TAPS])
+    lib().orc_seam_layer_forward(C.byref(lw), dim, hidden, heads, seq, _f(x), _f(out), C.byref(t))
+    return out, taps
+
+
+def seam_attention_backward(w, heads, q, k, v, dx2):
+    """Returns (dx_norm, dq, dk, dv), each [D, seq]."""
+    q, k, v, dx2 = (np.ascontiguousarray(a, dtype=np.float32) for a in (q, k, v, dx2))
+    dim, seq = q.shape
+    lw, keep = _seam_layer(w)
+    outs = [np.zeros_like(q) for _ in range(4)]
+    lib().orc_seam_attention_backward(C.byref(lw), dim, heads, seq, _f(q), _f(k), _f(v), _f(dx2),
+                                      *[_f(o) for o in outs])
+    return tuple(outs)
+
+
+def seam_ffn_backward(w, dffn, h1):
+    """Returns (dx_norm [D, seq], dh1 [H, seq])."""
+    dffn = np.ascontiguousarray(dffn, dtype=np.float32)
+    h1 = np.ascontiguousarray(h1, dtype=np.float32)
+    dim, seq = dffn.shape
+    hidden = h1.shape[0]
+    lw, keep = _seam_layer(w)
+    dx = np.zeros_like(dffn)
+    dh1 = np.zeros_like(h1)
+    lib().orc_seam_ffn_backward(C.byref(lw), dim, hidden, seq, _f(dffn), _f(h1), _f(dx), _f(dh1))
+    return dx, dh1
+
+
+def seam_softmax_vocab(logits):
+    p = np.ascontiguousarray(logits, dtype=np.float32).copy()
+    lib().orc_seam_softmax_vocab(_f(p), p.shape[0], p.shape[1])
+    return p
+
+
+def rmsnorm_noweight_bwd_cf(dy, x):
+    dy = np.ascontiguousarray(dy, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    dx = np.zeros_like(x)
+    lib().orc_rmsnorm_noweight_bwd_cf(_f(dx), _f(dy), _f(x), x.shape[0], x.shape[1])
+    return dx
+
+
+def matmul_vocab_seq(embed, x):
+    """logits [V, seq] = Embed [V, D] x [D, seq]."""
+    embed = np.ascontiguousarray(embed, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros((embed.shape[0], x.shape[1]), np.float32)
+    lib().orc_matmul_vocab_seq(_f(out), _f(embed), _f(x), embed.shape[0], embed.shape[1], x.shape[1])
+    return out
+
+
+def matmul_embed_t(embed, dlogits):
+    """dy [D, seq] = Embed^T dlogits."""
+    embed = np.ascontiguousarray(embed, dtype=np.float32)
+    dlogits = np.ascontiguousarray(dlogits, dtype=np.float32)
+    out = np.zeros((embed.shape[1], dlogits.shape[1]), np.float32)
+    lib().orc_matmul_embedT(_f(out), _f(embed), _f(dlogits), embed.shape[0], embed.shape[1], dlogits.shape[1])
+    return out

@@ -1149,3 +1149,24 @@ double orc_drand48_next(uint64_t *st) {
   *st = (0x5DEECE66DULL * *st + 0xBULL) & ((1ULL << 48) - 1);
   return (double)*st / (double)(1ULL << 48);
 }
+
+/* Single ops the seam oracle (refseam.c) composes, at the reference's
+ * channel-first signatures. */
+void orc_linear_bwd_dx_cf(float *dx, const float *w, const float *dy, int out_ch, int in_ch, int seq) {
+  linear_bwd_dx(dx, w, dy, out_ch, in_ch, seq);
+}
+void orc_rmsnorm_noweight_bwd_cf(float *dx, const float *dy, const float *x, int dim, int seq) {
+  rmsnorm_noweight_bwd(dx, dy, x, dim, seq);
+}
+void orc_causal_attention_bwd_cf(float *dq, float *dk, float *dv, const float *dout, const float *q,
+                                 const float *k, const float *v, int heads, int head_dim, int seq,
+                                 float scale) {
+  causal_attention_bwd(dq, dk, dv, dout, q, k, v, heads, head_dim, seq, scale);
+}
+void orc_matmul_vocab_seq(float *logits, const float *embed, const float *x, int vocab, int dim, int seq) {
+  matmul_vocab_seq(logits, embed, x, vocab, dim, seq);
+}
+void orc_matmul_embedT(float *dx, const float *embed, const float *dlogits, int vocab, int dim, int seq) {
+  matmul_embedT_scale(dx, embed, dlogits, vocab, dim, seq, 1.f);
+}
+void orc_softmax_row(float *out, const float *in, int n) { softmax_row(out, in, n); }

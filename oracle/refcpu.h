@@ -90,9 +90,39 @@ void orc_apply_rope_cf(float *x, int heads, int head_dim, int seq, const float *
                        const float *sin_t);
 void orc_qknorm_cf(float *q, float *k, int dim, int heads, int seq);
 float orc_cross_entropy(float *dlogits, const float *logits, const uint16_t *targets, int v, int s);
+void orc_linear_bwd_dx_cf(float *dx, const float *w, const float *dy, int out_ch, int in_ch, int seq);
+void orc_rmsnorm_noweight_bwd_cf(float *dx, const float *dy, const float *x, int dim, int seq);
+/* scale: of the scores in the recomputed probabilities and in ds */
+void orc_causal_attention_bwd_cf(float *dq, float *dk, float *dv, const float *dout, const float *q,
+                                 const float *k, const float *v, int heads, int head_dim, int seq,
+                                 float scale);
+void orc_matmul_vocab_seq(float *logits, const float *embed, const float *x, int vocab, int dim, int seq);
+void orc_matmul_embedT(float *dx, const float *embed, const float *dlogits, int vocab, int dim, int seq);
+void orc_softmax_row(float *out, const float *in, int n);
 void orc_softcap(float *x, size_t n);
 uint64_t orc_drand48_seed(int64_t seed);
 double orc_drand48_next(uint64_t *state);
+
+/* --- the per-object accelerator seam (refseam.c) ------------------------
+ * What the reference's Neural Engine programs compute for layerForward,
+ * layerBackward and offload (not the CPU path's layer: no QK-norm,
+ * residual lambdas or value embeddings; plain residuals). */
+typedef struct {
+  const float *wq, *wk, *wv, *wo, *w1, *w2;
+} orc_seam_layer;
+/* runWithTaps' layerCache taps; NULL fields are not written */
+typedef struct {
+  float *x_norm, *q, *k, *v, *att_out, *x2, *x2_norm, *h1, *gate;
+} orc_seam_taps;
+void orc_seam_layer_forward(const orc_seam_layer *w, int dim, int hidden, int heads, int seq, const float *x,
+                            float *out, orc_seam_taps *taps);
+void orc_seam_attention_backward(const orc_seam_layer *w, int dim, int heads, int seq, const float *q,
+                                 const float *k, const float *v, const float *dx2, float *dx_norm, float *dq,
+                                 float *dk, float *dv);
+void orc_seam_ffn_backward(const orc_seam_layer *w, int dim, int hidden, int seq, const float *dffn,
+                           const float *h1, float *dx_norm, float *dh1);
+/* in place: softmax over the vocabulary of each position of [vocab, seq] */
+void orc_seam_softmax_vocab(float *probs, int vocab, int seq);
 
 /* --- greedy KV-cache decoding (refdecode.c) ----------------------------
  * Llama2-style model with grouped-query attention: kv_heads key/value
