@@ -181,7 +181,8 @@ def attn_ref(qkv, nseq, S, NH, qknorm, theta, scale=0.125):
 
 @pytest.mark.parametrize("S,NH,nseq,qknorm", [(256, 12, 2, True), (256, 4, 3, False), (64, 2, 1, True),
                                              (128, 3, 2, False), (512, 2, 1, True),
-                                             (256, 12, 25, False)])  # 300 heads: 44 of them as half blocks
+                                             (256, 12, 25, False),  # 300 heads: 1.5 heads per block on 88 blocks
+                                             (256, 12, 32, True), (256, 12, 32, False)])  # 384: every block 1.5
 def test_attention_matches_f64(S, NH, nseq, qknorm):
     lib = _lib.load()
     r = np.random.default_rng(S + NH + nseq)
