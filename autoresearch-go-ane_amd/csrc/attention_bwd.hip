@@ -23,6 +23,8 @@
 // reference's 1.2^2 coefficient or the exact 1.2) and, for the exact
 // gradient, the transposed RoPE rotation (the reference applies none,
 // ane/train_full.go:646-665), each on the 64 dims a lane pair holds.
+#include <stdlib.h>
+
 #include "attention.h"
 
 namespace ane {
@@ -160,8 +162,12 @@ __device__ __forceinline__ void store_row(half_t* dst, const float (&dv)[2][16],
 
 // HILO: the scores are recomputed from split fp16 operands (hi + lo,
 // ~fp32 accuracy), matching a forward that used them (AttnArgs.hilo).
-template <int SMAX, bool HILO>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
+// PERQ: one q block (dQ pass) or key block (dK/dV pass) per wave, 8 waves
+// per block, so two waves share each SIMD instead of one wave walking a
+// pair of blocks in turn (wave w takes the first block of pair w % (waves / 2)
+// if w < waves / 2, else the second).
+template <int SMAX, bool HILO, bool PERQ>
+__global__ __launch_bounds__(PERQ ? 512 : 256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   constexpr int ST = SMAX + 4;
   __shared__ __attribute__((aligned(16))) half_t Ks[SMAX * HD];
   __shared__ __attribute__((aligned(16))) half_t Ks_lo[HILO ? SMAX * HD : 8];
@@ -179,12 +185,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
 
   const int lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;
   const int nqb = S / 32, npairs = nqb / 2;
-  const int pair = blockIdx.x * nw + wave;
+  const int slots = PERQ ? nw / 2 : nw, slot = PERQ ? wave % slots : wave;
+  const int pair = blockIdx.x * slots + slot;
   if (pair >= npairs) return;
   const int g = lane >> 5, ql = lane & 31;
   const float sp = a.scale_p * kL2E;
+  const int which0 = PERQ ? wave / slots : 0, which1 = PERQ ? which0 + 1 : 2;
 
-  for (int which = 0; which < 2; which++) {
+  for (int which = which0; which < which1; which++) {
     const int qb = which == 0 ? pair : nqb - 1 - pair;
     const int q = qb * 32 + ql;
     const size_t t = tok0 + q;
@@ -249,8 +257,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   }
 }
 
-template <int SMAX, bool HILO>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
+template <int SMAX, bool HILO, bool PERQ>
+__global__ __launch_bounds__(PERQ ? 512 : 256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
   constexpr int ST = SMAX + 4;
   __shared__ __attribute__((aligned(16))) half_t Qs[SMAX * HD];
   __shared__ __attribute__((aligned(16))) half_t Qt[HD * ST];
@@ -274,12 +282,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
 
   const int lane = tid & 63, wave = tid >> 6, nw = nthr >> 6;
   const int nkb = S / 32, npairs = nkb / 2;
-  const int pair = blockIdx.x * nw + wave;
+  const int slots = PERQ ? nw / 2 : nw, slot = PERQ ? wave % slots : wave;
+  const int pair = blockIdx.x * slots + slot;
   if (pair >= npairs) return;
   const int g = lane >> 5, kl = lane & 31;
   const float sp = a.scale_p * kL2E;
+  const int which0 = PERQ ? wave / slots : 0, which1 = PERQ ? which0 + 1 : 2;
 
-  for (int which = 0; which < 2; which++) {
+  for (int which = which0; which < which1; which++) {
     const int kb = which == 0 ? pair : nkb - 1 - pair;
     const int key = kb * 32 + kl;
     const size_t t = tok0 + key;
@@ -362,13 +372,21 @@ hipError_t attention_bwd(const AttnBwdArgs& a, hipStream_t stream) {
   const int npairs = a.S / 64;
   const int nw = npairs < 4 ? npairs : 4;
   dim3 grid((npairs + nw - 1) / nw, a.NH, a.nseq);
+  // ANE_ATT_BWD_PERQ=0: one wave per pair of blocks (4-wave blocks)
+  static const bool perq = [] {
+    const char* f = getenv("ANE_ATT_BWD_PERQ");
+    return !f || atoi(f) != 0;
+  }();
   if (a.hilo) {
     if (!a.qkvt_lo) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<256, true>), grid, dim3(64 * nw), 0, stream, a);
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<256, true>), grid, dim3(64 * nw), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<256, true, false>), grid, dim3(64 * nw), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<256, true, false>), grid, dim3(64 * nw), 0, stream, a);
+  } else if (perq) {
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<256, false, true>), grid, dim3(128 * nw), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<256, false, true>), grid, dim3(128 * nw), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<256, false>), grid, dim3(64 * nw), 0, stream, a);
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<256, false>), grid, dim3(64 * nw), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<256, false, false>), grid, dim3(64 * nw), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<256, false, false>), grid, dim3(64 * nw), 0, stream, a);
   }
   return hipGetLastError();
 }
