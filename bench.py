@@ -291,6 +291,54 @@ def moe_bench(ane, iters=10, tokens=8192):
             "tflops_alg": round(tf, 1), "mfma_frac": round(tf / PEAK_FP16_TFLOPS, 4), "iters": iters}
 
 
+def seam_bench(iters=20):
+    """The per-object seam (include/ane_objects.h) at the reference's stories
+    shapes (dim 768, hidden 2048, 12 heads, seq 256, vocab 32000): wall time
+    per call of each object method the reference's Engine calls, host
+    copies of the channel-first slices included (as the reference's objects
+    copy through IOSurfaces).  Median over `iters` calls after 3 untimed."""
+    from ane import objects
+    D, H, NH, S, V = 768, 2048, 12, 256, 32000
+    rng = np.random.default_rng(7)
+    w = {n: (rng.standard_normal(sh) / np.sqrt(sh[1])).astype(np.float32)
+         for n, sh in (("wq", (D, D)), ("wk", (D, D)), ("wv", (D, D)), ("wo", (D, D)), ("w1", (H, D)),
+                       ("w2", (D, H)))}
+    f32 = lambda *sh: rng.standard_normal(sh).astype(np.float32).ravel()
+    x, dx2, dffn = f32(D, S), f32(D, S), f32(D, S)
+    out, dxn, dq, dk, dv = (np.zeros(D * S, np.float32) for _ in range(5))
+    dh1 = np.zeros(H * S, np.float32)
+    logits = np.zeros(V * S, np.float32)
+    embed = (rng.standard_normal((V, D)) * 0.02).astype(np.float32)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        t = []
+        for _ in range(iters):
+            t0 = time.perf_counter()
+            fn()
+            t.append(time.perf_counter() - t0)
+        return round(float(np.median(t)) * 1e3, 3)
+
+    lf = objects.compile_stories_layer_forward(w, S, heads=NH)
+    cache = objects.LayerCache(D, H, S)
+    lb = objects.compile_stories_layer_backward(w, S, heads=NH)
+    off = objects.new_offload(embed, S)
+    res = {"shape": f"dim {D}, hidden {H}, heads {NH}, seq {S}, vocab {V}", "iters": iters}
+    res["layer_forward_run_ms"] = timed(lambda: lf.run(out, x))
+    res["layer_forward_run_with_taps_ms"] = timed(lambda: lf.run_with_taps(out, x, cache))
+    res["layer_backward_run_attention_ms"] = timed(
+        lambda: lb.run_attention(dxn, dq, dk, dv, cache.q, cache.k, cache.v, dx2))
+    res["layer_backward_run_ffn_ms"] = timed(lambda: lb.run_ffn(dxn, dh1, dffn, cache.h1))
+    res["offload_classifier_forward_ms"] = timed(lambda: off.run_classifier_forward(logits, cache.x2_norm))
+    res["offload_softmax_ms"] = timed(lambda: off.run_softmax(logits))
+    res["offload_classifier_backward_ms"] = timed(lambda: off.run_classifier_backward(dxn, logits))
+    res["offload_rms_forward_ms"] = timed(lambda: off.run_rms_forward(out, x))
+    for o in (lf, lb, off):
+        o.close()
+    return res
+
+
 def copy_calibration(mb):
     """A plain device-to-device copy of `mb` MiB (HIP's blit kernel), the
     reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings into
@@ -325,6 +373,7 @@ def main():
                     help="skip the forward+loss leg (the headline line then carries only the other legs; for "
                          "profiling those legs alone)")
     ap.add_argument("--no-power", action="store_true", help="skip the board-power pass of the forward")
+    ap.add_argument("--no-seam", action="store_true", help="skip the per-object seam leg (per-call object methods)")
     ap.add_argument("--decode-steps", type=int, default=128)
     ap.add_argument("--no-ref-bench", action="store_true",
                     help="skip the reference's own benchmark surface (Step / EvalLogits / EvalLoss per call)")
@@ -356,6 +405,8 @@ def main():
         out["moe_ffn"] = moe_bench(ane)
     if not args.no_ref_bench:
         out["reference_benchmarks"] = reference_benchmarks(ane, args.ref_arch)
+    if not args.no_seam:
+        out["seam"] = seam_bench()
     if not args.no_cpu:
         # every CPU this process may run on (on the GPU pool: the 16-CPU share
         # of one GPU, whatever nproc reports for the whole host)
