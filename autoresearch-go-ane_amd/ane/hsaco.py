@@ -232,7 +232,11 @@ def eval_loss(cfg: Config, params: np.ndarray, tokens: np.ndarray, targets: np.n
                   u64(0))
         nparts = 1
         heads = nseq * NH
-        split = 256 if 256 < heads < 512 else 0
+        # the library's dispatch: 1.5 heads per block for 256 < heads <= 384
+        # (unless ANE_ATT_15=0), else whole heads with the heads past 256 as
+        # two half blocks each
+        by15 = S == 256 and 256 < heads <= 384 and os.environ.get("ANE_ATT_15", "1") != "0"
+        split = 256 if 256 < heads < 512 and not by15 else 0
         for l, lw in enumerate(layers):
             g = _gemm(T, 3 * D, D, xh, D, lw["wqkv"], D)
             e = AneEpiParams(C=qkv, ldc=3 * D, scale=1.0, alpha=1.0, cap=15.0, rr_part=ssq, rr_ld=T, rr_nparts=nparts,
@@ -240,8 +244,11 @@ def eval_loss(cfg: Config, params: np.ndarray, tokens: np.ndarray, targets: np.n
             co.launch("gemm", "ane_k_gemm_qkv_rr", ((T // 128) * (3 * D // 192),), 256, g, e)
             a = AneAttnArgs(qkv=qkv, out=att, rope_cos=rope_cos, rope_sin=rope_sin, nseq=nseq, S=S, NH=NH, qknorm=0,
                             scale=0.125, split_from=split)
-            grid = (256 + 2 * (heads - 256),) if split else (1, NH, nseq)
-            co.launch("attention", "ane_k_attn_fwd", grid, 512, a)
+            if by15:
+                co.launch("attention", "ane_k_attn_fwd15", (256,), 768, a)
+            else:
+                grid = (256 + 2 * (heads - 256),) if split else (1, NH, nseq)
+                co.launch("attention", "ane_k_attn_fwd", grid, 512, a)
             g = _gemm(T, D, D, att, D, lw["wo"], D)
             e = AneEpiParams(C=x, ldc=D, R=x, C2=xh, ldc2=D, gain=lw["g_ffn"], ssq_part=ssq, ssq_ld=T, scale=1.0,
                              alpha=1.0, cap=15.0)

@@ -115,7 +115,11 @@ __device__ __forceinline__ void v_block_store(const AttnArgs& a, half8 (&raw)[8]
 
 // One wave: the 32 queries of q block qb of one (sequence, head) against
 // keys 0 .. 32 qb + 31 staged in LDS (Ks rows, V^T rows of stride SMAX + 4).
-template <int SMAX, bool HILO>
+// RSUM: the probabilities' row sum is taken by the matrix core, as a third
+// P.V product against a constant tile whose row 0 is ones (two MFMAs per
+// key block, 20 VGPRs), instead of 16 adds per key block; it then sums the
+// fp16 probabilities P.V multiplies.
+template <int SMAX, bool HILO, bool RSUM = false>
 __device__ __forceinline__ void q_block(const AttnArgs& a, const half_t* base, size_t tok0, int h, int qb,
                                         const half_t* Ks, const half_t* Ks_lo, const half_t* Vt) {
   constexpr int VST = SMAX + 4;
@@ -178,9 +182,12 @@ __device__ __forceinline__ void q_block(const AttnArgs& a, const half_t* base, s
     for (int s = 0; s < 4; s++) st_h8(a.qkvt_lo + (tok0 + q) * 2 * D + h * HD + s * 16 + g * 8, qlo[s]);
   }
 
-  floatx16 o0, o1;
+  floatx16 o0, o1, o2;
 #pragma unroll
-  for (int r = 0; r < 16; r++) { o0[r] = 0.f; o1[r] = 0.f; }
+  for (int r = 0; r < 16; r++) { o0[r] = 0.f; o1[r] = 0.f; o2[r] = 0.f; }
+  half8 ones_row;  // A operand [32 rows][16 k]: row 0 ones, the rest zero
+#pragma unroll
+  for (int u = 0; u < 8; u++) ones_row[u] = (half_t)(ql == 0 ? 1.f : 0.f);
   // m: the reference maximum (scaled, log2 units) of the exponentials in
   // lsum and o.  It is raised only when a block's maximum exceeds it by
   // more than kRescale (or on the first block), so o is rescaled rarely;
@@ -243,7 +250,11 @@ __device__ __forceinline__ void q_block(const AttnArgs& a, const half_t* base, s
     if (__any(mloc > m + kRescale)) {
       const float mnew = fmaxf(m, mloc);
       const float alpha = __builtin_amdgcn_exp2f(m - mnew);
-      lsum *= alpha;
+      if constexpr (RSUM) {
+        o2[0] *= alpha;  // the only nonzero element: row 0 of the sum tile
+      } else {
+        lsum *= alpha;
+      }
 #pragma unroll
       for (int r = 0; r < 16; r++) { o0[r] *= alpha; o1[r] *= alpha; }
       m = mnew;
@@ -253,9 +264,9 @@ __device__ __forceinline__ void q_block(const AttnArgs& a, const half_t* base, s
     for (int r = 0; r < 16; r++) {
       const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[r], sl2, -m));
       sacc[r] = p;
-      ps += p;
+      if constexpr (!RSUM) ps += p;
     }
-    lsum += ps;
+    if constexpr (!RSUM) lsum += ps;
 #pragma unroll
     for (int jh = 0; jh < 2; jh++) {
       half8 pf;
@@ -263,12 +274,19 @@ __device__ __forceinline__ void q_block(const AttnArgs& a, const half_t* base, s
       for (int u = 0; u < 8; u++) pf[u] = (half_t)sacc[8 * jh + u];
       o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v0[jh], pf, o0, 0, 0, 0);
       o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(v1[jh], pf, o1, 0, 0, 0);
+      if constexpr (RSUM) o2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ones_row, pf, o2, 0, 0, 0);
     }
   };
   load_k(0);
   for (int kb = 0; kb < qb; kb++) block(std::false_type{}, kb);
   block(std::true_type{}, qb);
-  lsum += xor32_f(lsum);
+  if constexpr (RSUM) {
+    // row 0 of the sum tile sits in o2[0] of lanes 0..31 (the query's lane of the lower half)
+    const float other = xor32_f(o2[0]);
+    lsum = g == 0 ? o2[0] : other;
+  } else {
+    lsum += xor32_f(lsum);
+  }
   const float inv = 1.0f / lsum;
   half_t* orow = a.out + (tok0 + q) * D + h * HD;
 #pragma unroll
@@ -423,8 +441,7 @@ __device__ constexpr int8_t kTask15[3][12] = {
     {7, 6, 13, 5, 11, 12, 4, 10, 0, 1, 2, 3}};  // half with q-block pairs 2, 3
 constexpr int kWaves15 = 12;
 
-__global__ __launch_bounds__(64 * kWaves15) __attribute__((amdgpu_waves_per_eu(3)))
-void attn_fwd15_kernel(AttnArgs a) {
+__device__ __forceinline__ void attn_fwd15_body(const AttnArgs& a) {
   constexpr int SMAX = 256, VST = SMAX + 4, NT = 64 * kWaves15;
   __shared__ __attribute__((aligned(16))) half_t Ks[2][SMAX * HD];
   __shared__ __attribute__((aligned(16))) half_t Vt[2][HD * VST];
@@ -496,7 +513,7 @@ void attn_fwd15_kernel(AttnArgs a) {
   const int t = kTask15[has_b ? 1 + (p0b != 0) : 0][tid >> 6];
   if (t < 0) return;
   const int hd = t >> 3;
-  q_block<SMAX, false>(a, base[hd], tok[hd], hh[hd], t & 7, Ks[hd], nullptr, Vt[hd]);
+  q_block<SMAX, false, true>(a, base[hd], tok[hd], hh[hd], t & 7, Ks[hd], nullptr, Vt[hd]);
 }
 
 }  // namespace
@@ -505,6 +522,13 @@ void attn_fwd15_kernel(AttnArgs a) {
 // a host that loads the code object itself (ane_kernels.h): 512 threads.
 extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void ane_k_attn_fwd(AttnArgs a) {
   attn_fwd_body<256, false, true>(a);
+}
+
+// 1.5 heads per block (above): 768 threads, grid 256; the library launches it
+// under this name too.
+extern "C" __global__ __launch_bounds__(64 * kWaves15) __attribute__((amdgpu_waves_per_eu(3)))
+void ane_k_attn_fwd15(AttnArgs a) {
+  attn_fwd15_body(a);
 }
 
 hipError_t attention_fwd(const AttnArgs& a, hipStream_t stream) {
@@ -535,7 +559,7 @@ hipError_t attention_fwd(const AttnArgs& a, hipStream_t stream) {
   }();
   if (!a.hilo && perq && by15 && a.S == 256 && heads > 256 && heads <= 384) {
     k.split_from = 0;
-    hipLaunchKernelGGL(attn_fwd15_kernel, dim3(256), dim3(64 * kWaves15), 0, stream, k);
+    hipLaunchKernelGGL(ane_k_attn_fwd15, dim3(256), dim3(64 * kWaves15), 0, stream, k);
     return hipGetLastError();
   }
   if (a.hilo)

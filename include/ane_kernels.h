@@ -18,7 +18,7 @@
  *
  * Code objects (one per compilation unit):
  *   ane_gemm.hsaco       ane_k_gemm_*      (args: AneGemmArgs, AneEpiParams)
- *   ane_attention.hsaco  ane_k_attn_fwd    (args: AneAttnArgs)
+ *   ane_attention.hsaco  ane_k_attn_fwd, ane_k_attn_fwd15 (args: AneAttnArgs)
  *   ane_rowops.hsaco     ane_k_embed_xg, ane_k_prefetch, ane_k_ce_token,
  *                        ane_k_ce_reduce   (scalar / pointer args)
  */
@@ -118,6 +118,10 @@ typedef struct AneAttnArgs {
  *                        (S = 256), or 1-D 256 + 2 (nseq NH - 256) blocks with
  *                        split_from = 256 when 256 < nseq NH < 512 (the heads
  *                        past 256 as two half blocks)
+ *  ane_k_attn_fwd15      768 threads, grid 256 (one block per CU), split_from =
+ *                        0, S = 256, 256 < nseq NH <= 384: block c stages head c
+ *                        and, for c < 2 (nseq NH - 256), half c % 2 of head
+ *                        256 + c / 2 (the library's choice for those head counts)
  *  ane_k_embed_xg(x, xg, ssq, E, tok, gain, T, D, V, pf, pf_bytes)
  *                        256 threads, grid ceil(T / 4): x = E[tok] (0 when tok
  *                        >= V), xg = fp16(x * gain), ssq[t] = sum x^2
