@@ -162,8 +162,8 @@ __global__ __launch_bounds__(256) void vocab_softmax_stats_kernel(float2* __rest
   }
 }
 
-__global__ __launch_bounds__(256) void vocab_softmax_apply_kernel(float* __restrict__ out,
-                                                                  const float* __restrict__ x,
+// (out may be x: each element is read and then written by the same thread)
+__global__ __launch_bounds__(256) void vocab_softmax_apply_kernel(float* out, const float* x,
                                                                   const float2* __restrict__ part, int nch, int V,
                                                                   int T) {
   const int lx = threadIdx.x & 63, g = threadIdx.x >> 6, t = blockIdx.x * 64 + lx;
@@ -183,6 +183,18 @@ __global__ __launch_bounds__(256) void vocab_softmax_apply_kernel(float* __restr
 }
 
 // ---- shared object state ----------------------------------------------------
+
+// Restores the calling thread's current device when a seam call returns
+// (each object switches to the device it was opened on).
+struct DeviceRestore {
+  int prev = -1;
+  DeviceRestore() {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+  }
+  ~DeviceRestore() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
 
 struct SeamBase {
   int device = -1;
@@ -459,14 +471,17 @@ extern "C" int ane_layer_forward_open(int32_t dim, int32_t hidden, int32_t heads
 }
 
 extern "C" int ane_layer_forward_run(ane_layer_fwd* lf, float* out, const float* x) {
+  DeviceRestore restore;
   return layer_forward_call(lf, out, x, nullptr);
 }
 
 extern "C" int ane_layer_forward_run_taps(ane_layer_fwd* lf, float* out, const float* x, ane_layer_cache* cache) {
+  DeviceRestore restore;
   return layer_forward_call(lf, out, x, cache);
 }
 
 extern "C" int ane_layer_forward_refresh(ane_layer_fwd* lf, const ane_layer_weights* w) {
+  DeviceRestore restore;
   const char* op = "refresh layer forward";
   if (!lf) return seam_fail(ANE_ERR_ARG, "%s: layer is nil", op);
   if (lf->closed) return seam_fail(ANE_ERR_CLOSED, "%s: layer is closed", op);
@@ -478,6 +493,7 @@ extern "C" int ane_layer_forward_refresh(ane_layer_fwd* lf, const ane_layer_weig
 }
 
 extern "C" void ane_layer_forward_close(ane_layer_fwd* lf) {
+  DeviceRestore restore;
   if (lf && !lf->closed) lf->release();
 }
 
@@ -560,6 +576,7 @@ extern "C" int ane_layer_backward_open(int32_t dim, int32_t hidden, int32_t head
 // backward kernels read.
 extern "C" int ane_layer_backward_run_attention(ane_layer_bwd* lb, float* dx_norm, float* dq, float* dk, float* dv,
                                                 const float* q, const float* k, const float* v, const float* dx2) {
+  DeviceRestore restore;
   const char* op = "run layer backward attention";
   int rc = backward_enter(op, lb);
   if (rc) return rc;
@@ -615,6 +632,7 @@ extern "C" int ane_layer_backward_run_attention(ane_layer_bwd* lb, float* dx_nor
 // ane/mil_stories.go:351-381).
 extern "C" int ane_layer_backward_run_ffn(ane_layer_bwd* lb, float* dx_norm, float* dh1, const float* dffn,
                                           const float* h1) {
+  DeviceRestore restore;
   const char* op = "run layer backward ffn";
   int rc = backward_enter(op, lb);
   if (rc) return rc;
@@ -642,6 +660,7 @@ extern "C" int ane_layer_backward_run_ffn(ane_layer_bwd* lb, float* dx_norm, flo
 }
 
 extern "C" int ane_layer_backward_refresh(ane_layer_bwd* lb, const ane_layer_weights* w) {
+  DeviceRestore restore;
   const char* op = "refresh layer backward";
   int rc = backward_enter(op, lb);
   if (rc) return rc;
@@ -651,6 +670,7 @@ extern "C" int ane_layer_backward_refresh(ane_layer_bwd* lb, const ane_layer_wei
 }
 
 extern "C" void ane_layer_backward_close(ane_layer_bwd* lb) {
+  DeviceRestore restore;
   if (lb && !lb->closed) lb->release();
 }
 
@@ -782,6 +802,7 @@ extern "C" void ane_offload_disable(ane_offload* o, int32_t piece) {
 }
 
 extern "C" int ane_offload_run_rms_forward(ane_offload* o, float* out, const float* x) {
+  DeviceRestore restore;
   const char* op = "run rms forward";
   int rc = offload_enter(op, o, ANE_OFF_RMS_FORWARD);
   if (rc) return rc;
@@ -797,6 +818,7 @@ extern "C" int ane_offload_run_rms_forward(ane_offload* o, float* out, const flo
 }
 
 extern "C" int ane_offload_run_classifier_forward(ane_offload* o, float* logits, const float* x_norm) {
+  DeviceRestore restore;
   const char* op = "run classifier forward";
   int rc = offload_enter(op, o, ANE_OFF_CLASSIFIER_FORWARD);
   if (rc) return rc;
@@ -808,6 +830,7 @@ extern "C" int ane_offload_run_classifier_forward(ane_offload* o, float* logits,
 }
 
 extern "C" int ane_offload_run_classifier_softmax(ane_offload* o, float* probs, const float* x_norm) {
+  DeviceRestore restore;
   const char* op = "run classifier softmax";
   int rc = offload_enter(op, o, ANE_OFF_CLASSIFIER_FORWARD);
   if (rc) return rc;
@@ -821,6 +844,7 @@ extern "C" int ane_offload_run_classifier_softmax(ane_offload* o, float* probs, 
 }
 
 extern "C" int ane_offload_run_softmax(ane_offload* o, float* probs) {
+  DeviceRestore restore;
   const char* op = "run softmax";
   int rc = offload_enter(op, o, ANE_OFF_SOFTMAX);
   if (rc) return rc;
@@ -834,6 +858,7 @@ extern "C" int ane_offload_run_softmax(ane_offload* o, float* probs) {
 }
 
 extern "C" int ane_offload_run_classifier_backward(ane_offload* o, float* dy, const float* dlogits) {
+  DeviceRestore restore;
   const char* op = "run classifier backward";
   int rc = offload_enter(op, o, ANE_OFF_CLASSIFIER_BACKWARD);
   if (rc) return rc;
@@ -857,6 +882,7 @@ extern "C" int ane_offload_run_classifier_backward(ane_offload* o, float* dy, co
 }
 
 extern "C" int ane_offload_run_rms_backward(ane_offload* o, float* dx, const float* dy, const float* x) {
+  DeviceRestore restore;
   const char* op = "run rms backward";
   int rc = offload_enter(op, o, ANE_OFF_RMS_BACKWARD);
   if (rc) return rc;
@@ -873,6 +899,7 @@ extern "C" int ane_offload_run_rms_backward(ane_offload* o, float* dx, const flo
 }
 
 extern "C" int ane_offload_refresh(ane_offload* o, const float* embed) {
+  DeviceRestore restore;
   const char* op = "refresh offload weights";
   if (!o) return seam_fail(ANE_ERR_ARG, "%s: offload is nil", op);
   if (o->closed) return seam_fail(ANE_ERR_CLOSED, "%s: offload is closed", op);
@@ -884,6 +911,7 @@ extern "C" int ane_offload_refresh(ane_offload* o, const float* embed) {
 }
 
 extern "C" void ane_offload_close(ane_offload* o) {
+  DeviceRestore restore;
   if (o && !o->closed) {
     o->release();
     o->pieces = 0;
