@@ -268,7 +268,7 @@ def eval_loss(cfg: Config, params: np.ndarray, tokens: np.ndarray, targets: np.n
         e = AneEpiParams(targets=tgt, partial=partial, tgt_logit=tgt_logit, softcap=0, cap=15.0, vocab=V, scale=1.0,
                          alpha=1.0, rr_part=ssq, rr_ld=T, rr_nparts=nparts, rr_dim=D)
         co.launch("gemm", "ane_k_gemm_ce_rr", ((V // 256) * (T // 256),), 512, g, e)
-        co.launch("rowops", "ane_k_ce_token", ((T + 63) // 64,), 256, ip(lse), ip(tok_loss), ip(partial),
+        co.launch("rowops", "ane_k_ce_token", ((T + 31) // 32,), 256, ip(lse), ip(tok_loss), ip(partial),
                   i32(npart), ip(tgt_logit), ip(tgt), i32(V), i32(T))
         co.launch("rowops", "ane_k_ce_reduce", (nseq,), 256, ip(loss_seq), ip(None), C.c_float(0.0), ip(tok_loss),
                   ip(tgt), i32(V), i32(S))

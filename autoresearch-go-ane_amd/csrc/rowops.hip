@@ -180,43 +180,101 @@ extern "C" __global__ __launch_bounds__(256) void ane_k_prefetch(const void* pf,
 // x = E[tok] (0 for tok >= V), xg = fp16(x * gain), ssq[t] = sum of x^2 (the
 // deferred norm's one partial per row); the next GEMM's weights streamed
 // through the caches alongside.
+// D <= 1024 (the engine's widths): each lane's float4 groups i = lane + 64 k
+// of the row and of the gains are requested before anything is stored (the
+// stores could alias later loads, so a load / store loop waits one memory
+// round trip per element group); then this block's share of the next
+// GEMM's weights, consumed after the stores.  Wider rows take the loop.
 extern "C" __global__ __launch_bounds__(256) void ane_k_embed_xg(float* x, half_t* xg, float* ssq, const float* E,
                                                             const uint16_t* tok, const float* gain, int T, int D, int V,
                                                        const void* pf, size_t pf_bytes) {
-  prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
   const int t = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (t >= T) return;
-  const int tk = tok[t];
-  const float* er = E + (size_t)tk * D;
-  float ss = 0.f;
-  for (int i = lane; i < D; i += 64) {
-    const float v = tk < V ? er[i] : 0.f;
-    const size_t idx = (size_t)t * D + i;
-    x[idx] = v;
-    xg[idx] = (half_t)(v * gain[i]);
-    ss += v * v;
+  if (D > 1024) {
+    prefetch_slice(pf, pf_bytes, blockIdx.x, gridDim.x);
+    if (t >= T) return;
+    const int tk = tok[t];
+    const float* er = E + (size_t)tk * D;
+    float ss = 0.f;
+    for (int i = lane; i < D; i += 64) {
+      const float v = tk < V ? er[i] : 0.f;
+      const size_t idx = (size_t)t * D + i;
+      x[idx] = v;
+      xg[idx] = (half_t)(v * gain[i]);
+      ss += v * v;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) ssq[t] = ss;
+    return;
   }
-  ss = wave_sum(ss);
-  if (lane == 0) ssq[t] = ss;
+  const int nv = D / 4;
+  const bool row_ok = t < T;
+  const int tk = row_ok ? tok[t] : V;
+  const bool hit = tk < V;
+  const float4* er = reinterpret_cast<const float4*>(E + (size_t)(hit ? tk : 0) * D);
+  const float4* g4 = reinterpret_cast<const float4*>(gain);
+  float4 v[4], gg[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int i = lane + 64 * k;
+    if (i < nv) {
+      v[k] = hit ? er[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      gg[k] = g4[i];
+    }
+  }
+  const Prefetch pfd = prefetch_begin(pf, pf_bytes, blockIdx.x, gridDim.x);
+  float ss = 0.f;
+  if (row_ok) {
+    float4* xr = reinterpret_cast<float4*>(x + (size_t)t * D);
+    half4* hr = reinterpret_cast<half4*>(xg + (size_t)t * D);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int i = lane + 64 * k;
+      if (i < nv) {
+        const float4 a = v[k], g = gg[k];
+        xr[i] = a;
+        half4 h;
+        h[0] = (half_t)(a.x * g.x);
+        h[1] = (half_t)(a.y * g.y);
+        h[2] = (half_t)(a.z * g.z);
+        h[3] = (half_t)(a.w * g.w);
+        hr[i] = h;
+        ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+      }
+    }
+  }
+  ss = wave_sum_dpp(ss);
+  if (row_ok && lane == 0) ssq[t] = ss;
+  prefetch_end(pfd, pf, pf_bytes, blockIdx.x, gridDim.x);
 }
 
-// Per token: merge the partials with a running (max, sum) pair; 4 lanes
-// split the partials of one token and combine with two xor-shuffles.
+// Per token: merge the partials with a running (max, sum) pair; kCeLanes
+// lanes split the partials of one token (lane q takes q, q + kCeLanes, ...)
+// and combine with xor-shuffles.
+constexpr int kCeLanes = 8;
 extern "C" __global__ __launch_bounds__(256) void ane_k_ce_token(float* lse_out, float* tok_loss, const float2* partial,
                                                        int np, const float* tgt_logit, const uint16_t* tgt, int V,
                                                        int T) {
-  const int n = blockIdx.x * 64 + (threadIdx.x >> 2), q = threadIdx.x & 3;
+  const int n = blockIdx.x * (256 / kCeLanes) + threadIdx.x / kCeLanes, q = threadIdx.x % kCeLanes;
   float mx = -INFINITY, sum = 0.f;
+  auto merge = [&](float2 v) {
+    const float m2 = fmaxf(mx, v.x);
+    sum = sum * __expf(mx - m2) + v.y * __expf(v.x - m2);
+    mx = m2;
+  };
   if (n < T) {
-    for (int p = q; p < np; p += 4) {
-      const float2 v = partial[(size_t)p * T + n];
-      const float m2 = fmaxf(mx, v.x);
-      sum = sum * __expf(mx - m2) + v.y * __expf(v.x - m2);
-      mx = m2;
+    // four of the thread's partials requested at a time, merged in order
+    int p = q;
+    for (; p + 3 * kCeLanes < np; p += 4 * kCeLanes) {
+      float2 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) v[u] = partial[(size_t)(p + kCeLanes * u) * T + n];
+#pragma unroll
+      for (int u = 0; u < 4; u++) merge(v[u]);
     }
+    for (; p < np; p += kCeLanes) merge(partial[(size_t)p * T + n]);
   }
 #pragma unroll
-  for (int o = 1; o < 4; o <<= 1) {
+  for (int o = 1; o < kCeLanes; o <<= 1) {
     const float om = __shfl_xor(mx, o, 64), os = __shfl_xor(sum, o, 64);
     const float m2 = fmaxf(mx, om);
     sum = (mx == -INFINITY ? 0.f : sum * __expf(mx - m2)) + (om == -INFINITY ? 0.f : os * __expf(om - m2));
@@ -334,8 +392,8 @@ hipError_t ce_reduce(float* loss_seq, float* lse, float* tok_loss, float* colsca
                      const float2* partial, int np, const float* tgt_logit, const uint16_t* tgt, int V, int nseq, int S,
                      hipStream_t s) {
   const int T = nseq * S;
-  hipLaunchKernelGGL(ane_k_ce_token, dim3((T + 63) / 64), dim3(256), 0, s, lse, tok_loss, partial, np, tgt_logit,
-                     tgt, V, T);
+  hipLaunchKernelGGL(ane_k_ce_token, dim3((T + 256 / kCeLanes - 1) / (256 / kCeLanes)), dim3(256), 0, s, lse, tok_loss,
+                     partial, np, tgt_logit, tgt, V, T);
   hipLaunchKernelGGL(ane_k_ce_reduce, dim3(nseq), dim3(256), 0, s, loss_seq, colscale, dscale, tok_loss, tgt, V, S);
   return hipGetLastError();
 }

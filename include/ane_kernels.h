@@ -127,7 +127,7 @@ typedef struct AneAttnArgs {
  *                        >= V), xg = fp16(x * gain), ssq[t] = sum x^2
  *  ane_k_prefetch(p, bytes)   256 threads, any grid: streams [p, p + bytes)
  *  ane_k_ce_token(lse, tok_loss, partial, np, tgt_logit, tgt, V, T)
- *                        256 threads, grid ceil(T / 64): merges the np block-row
+ *                        256 threads, grid ceil(T / 32): merges the np block-row
  *                        partials per token; tok_loss = -max(log p, log 1e-10)
  *  ane_k_ce_reduce(loss_seq, colscale, dscale, tok_loss, tgt, V, S)
  *                        256 threads, grid nseq: mean loss per sequence over
