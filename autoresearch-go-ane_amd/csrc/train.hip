@@ -576,7 +576,9 @@ int flush_pending(ane_engine* e) {
 
   float gscale = (float)(1.0 / (double)e->state.pending_steps);
   gscale /= O.loss_scale;
-  HIPCHK(op, sumsq(tb.sumsq, tb.sumsq_part, tb.G, (size_t)(pm.embed + V * D), us));
+  // the norm only feeds the clip: clipLayerGradients returns before it
+  // without one (ane/train_full.go:168)
+  if (O.grad_clip > 0.f) HIPCHK(op, sumsq(tb.sumsq, tb.sumsq_part, tb.G, (size_t)(pm.embed + V * D), us));
   e->state.adam_t++;
   const int t = (int)e->state.adam_t;
   float i1, i2, l1, l2;
