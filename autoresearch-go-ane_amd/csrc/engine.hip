@@ -936,7 +936,7 @@ static int finish_loss(ane_engine* e, int nseq, float* loss_per_seq, float* mean
   const char* op = "eval loss";
   const float* ls = e->loss_host;
   HIPCHK(op, hipMemcpyAsync(e->loss_host, e->loss_seq, (size_t)nseq * 4, hipMemcpyDeviceToHost, e->stream));
-  HIPCHK(op, hipStreamSynchronize(e->stream));
+  HIPCHK(op, stream_wait(e->stream));
   double tot = 0;
   for (int b = 0; b < nseq; b++) {
     tot += ls[b];
@@ -1005,7 +1005,7 @@ extern "C" int ane_eval_logits(ane_engine* e, const uint16_t* tokens, int64_t nt
   p.C = e->logits; p.ldc = S; p.softcap = c.arch == ANE_ARCH_NANOCHAT; p.cap = 15.f;
   HIPCHK(op, eng_gemm(e, 4, e->embed_h, D, false, e->xh, D, false, V, S, D, EPI_LOGITS, p));
   HIPCHK(op, hipMemcpyAsync(logits, e->logits, (size_t)V * S * 4, hipMemcpyDeviceToHost, e->stream));
-  HIPCHK(op, hipStreamSynchronize(e->stream));
+  HIPCHK(op, stream_wait(e->stream));
   return ANE_OK;
 }
 

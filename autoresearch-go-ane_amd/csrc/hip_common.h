@@ -9,6 +9,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 namespace ane {
 
@@ -164,6 +165,22 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += __shfl_xor(v, 16, 64);
   v += xor32_f(v);
   return v;
+}
+
+// Host: wait for everything queued on stream s by polling it, for calls
+// that return results to their caller.  hipStreamSynchronize may block the
+// thread until an interrupt wakes it, tens of microseconds after the GPU has
+// finished; polling returns within a few.  ANE_SPIN_WAIT=0 blocks instead.
+inline hipError_t stream_wait(hipStream_t s) {
+  static const bool spin = [] {
+    const char* f = getenv("ANE_SPIN_WAIT");
+    return !f || atoi(f) != 0;
+  }();
+  if (!spin) return hipStreamSynchronize(s);
+  hipError_t r;
+  while ((r = hipStreamQuery(s)) == hipErrorNotReady) {
+  }
+  return r;
 }
 
 }  // namespace ane

@@ -283,7 +283,7 @@ hipError_t stage_layer(SeamBase* b, LayerShadows* s, const ane_layer_weights* w,
   if ((h = stage_f16(b, s->wo, w->wo, DD, s->staging)) != hipSuccess) return h;
   if ((h = stage_f16(b, s->w1, w->w1, (size_t)H * D, s->staging)) != hipSuccess) return h;
   if ((h = stage_f16(b, s->w2, w->w2, (size_t)D * H, s->staging)) != hipSuccess) return h;
-  return hipStreamSynchronize(b->st);  // the caller may free its host copies
+  return stream_wait(b->st);  // the caller may free its host copies
 }
 
 // RoPE tables [S, 32] of the layer programs (theta 100000,
@@ -301,7 +301,7 @@ hipError_t upload_rope(SeamBase* b, float** cs_d, float** sn_d, int S, bool iden
   if ((h = b->alloc(sn_d, sn.size())) != hipSuccess) return h;
   if ((h = b->up(*cs_d, cs.data(), cs.size() * 4)) != hipSuccess) return h;
   if ((h = b->up(*sn_d, sn.data(), sn.size() * 4)) != hipSuccess) return h;
-  return hipStreamSynchronize(b->st);
+  return stream_wait(b->st);
 }
 
 GemmArgs gemm_args(const half_t* A, int lda, bool at, const half_t* B, int ldb, bool bt, int M, int N, int K) {
@@ -420,7 +420,7 @@ int layer_forward_call(ane_layer_fwd* f, float* out, const float* x, ane_layer_c
       SEAMCHK(op, tap(cache->gate, HS, f->cf2));
     }
   }
-  SEAMCHK(op, hipStreamSynchronize(st));
+  SEAMCHK(op, stream_wait(st));
   if (cache) {
     cache->att_taps_ready = 1;
     cache->ffn_taps_ready = 1;
@@ -623,7 +623,7 @@ extern "C" int ane_layer_backward_run_attention(ane_layer_bwd* lb, float* dx_nor
   }
   SEAMCHK(op, (xpose<float, float>(lb->cf, lb->dxn, S, D, D, S, st)));
   SEAMCHK(op, lb->down(dx_norm, lb->cf, DS * 4));
-  SEAMCHK(op, hipStreamSynchronize(st));
+  SEAMCHK(op, stream_wait(st));
   return ANE_OK;
 }
 
@@ -655,7 +655,7 @@ extern "C" int ane_layer_backward_run_ffn(ane_layer_bwd* lb, float* dx_norm, flo
   SEAMCHK(op, lb->down(dh1, lb->cf, (size_t)H * S * 4));
   SEAMCHK(op, (xpose<float, float>(lb->cf, lb->dxn, S, D, D, S, st)));
   SEAMCHK(op, lb->down(dx_norm, lb->cf, (size_t)D * S * 4));
-  SEAMCHK(op, hipStreamSynchronize(st));
+  SEAMCHK(op, stream_wait(st));
   return ANE_OK;
 }
 
@@ -716,7 +716,7 @@ hipError_t stage_embed(ane_offload* o, const float* embed) {
   hipError_t h = o->up(o->staging, embed, n * 4);
   if (h != hipSuccess) return h;
   if ((h = f32_to_f16(o->embed, o->staging, n, o->st)) != hipSuccess) return h;
-  return hipStreamSynchronize(o->st);
+  return stream_wait(o->st);
 }
 
 // logits [V, S] (device) = Embed x_norm, x_norm channel-first [D, S] from the host
@@ -813,7 +813,7 @@ extern "C" int ane_offload_run_rms_forward(ane_offload* o, float* out, const flo
                      o->S);
   SEAMCHK(op, hipGetLastError());
   SEAMCHK(op, o->down(out, o->out, DS * 4));
-  SEAMCHK(op, hipStreamSynchronize(o->st));
+  SEAMCHK(op, stream_wait(o->st));
   return ANE_OK;
 }
 
@@ -825,7 +825,7 @@ extern "C" int ane_offload_run_classifier_forward(ane_offload* o, float* logits,
   if (!logits || !x_norm) return seam_fail(ANE_ERR_ARG, "%s: null buffer", op);
   SEAMCHK(op, classifier_device(o, x_norm));
   SEAMCHK(op, o->down(logits, o->logits, (size_t)o->V * o->S * 4));
-  SEAMCHK(op, hipStreamSynchronize(o->st));
+  SEAMCHK(op, stream_wait(o->st));
   return ANE_OK;
 }
 
@@ -839,7 +839,7 @@ extern "C" int ane_offload_run_classifier_softmax(ane_offload* o, float* probs, 
   SEAMCHK(op, classifier_device(o, x_norm));
   SEAMCHK(op, softmax_device(o));
   SEAMCHK(op, o->down(probs, o->logits, (size_t)o->V * o->S * 4));
-  SEAMCHK(op, hipStreamSynchronize(o->st));
+  SEAMCHK(op, stream_wait(o->st));
   return ANE_OK;
 }
 
@@ -853,7 +853,7 @@ extern "C" int ane_offload_run_softmax(ane_offload* o, float* probs) {
   SEAMCHK(op, o->up(o->logits, probs, VS * 4));
   SEAMCHK(op, softmax_device(o));
   SEAMCHK(op, o->down(probs, o->logits, VS * 4));
-  SEAMCHK(op, hipStreamSynchronize(o->st));
+  SEAMCHK(op, stream_wait(o->st));
   return ANE_OK;
 }
 
@@ -877,7 +877,7 @@ extern "C" int ane_offload_run_classifier_backward(ane_offload* o, float* dy, co
   p.C = o->dycf; p.ldc = o->S;
   SEAMCHK(op, gemm_run(g, EPI_STORE_F, p, o->st, o->bwd_bm, o->bwd_bn));
   SEAMCHK(op, o->down(dy, o->dycf, (size_t)o->D * o->S * 4));
-  SEAMCHK(op, hipStreamSynchronize(o->st));
+  SEAMCHK(op, stream_wait(o->st));
   return ANE_OK;
 }
 
@@ -894,7 +894,7 @@ extern "C" int ane_offload_run_rms_backward(ane_offload* o, float* dx, const flo
                      o->xcf, o->D, o->S);
   SEAMCHK(op, hipGetLastError());
   SEAMCHK(op, o->down(dx, o->out, DS * 4));
-  SEAMCHK(op, hipStreamSynchronize(o->st));
+  SEAMCHK(op, stream_wait(o->st));
   return ANE_OK;
 }
 

@@ -673,7 +673,7 @@ int read_losses(ane_engine* e, int nseq, float* per, double* mean, double* wait_
   const float* ls = e->loss_host;
   HIPCHK(op, hipMemcpyAsync(e->loss_host, e->loss_seq, (size_t)nseq * 4, hipMemcpyDeviceToHost, e->stream));
   const double t0 = now_s();
-  HIPCHK(op, hipStreamSynchronize(e->stream));
+  HIPCHK(op, stream_wait(e->stream));
   if (wait_s) *wait_s = now_s() - t0;
   double tot = 0;
   for (int b = 0; b < nseq; b++) {
