@@ -329,8 +329,8 @@ int backward_body(ane_engine* e, int nseq, bool async) {
   HIPCHK(op, prefetch(st, {{e->ls[L - 1].w2_t, (size_t)H * D * 2}}));
 
   // ---- layers, last to first ------------------------------------------------
-  // dW stream order per layer: dW2, dW13 (after the SwiGLU-backward GEMM),
-  // dWo (after the FFN norm backward), dWqkv (after the attention backward);
+  // dW stream order per layer: dW2 (after the SwiGLU-backward GEMM), dWo and
+  // dW13 (after the FFN norm backward), dWqkv (after the attention backward);
   // above_done marks the end of the layer above's dW work
   hipEvent_t above_done = nullptr;
   int att_gain_layer = -1;
@@ -361,21 +361,24 @@ int backward_body(ane_engine* e, int nseq, bool async) {
       phase_end(e, ds);
       att_gain_layer = -1;
     }
-    {  // dW2 += dOut gate^T
+    auto dw2 = [&]() -> int {  // dW2 += dOut gate^T
       EpiParams p;
       p.C = G + o.w2; p.ldc = H; p.accumulate = acc;
       phase_begin(e, PH_DW_GEMM, ds);
       HIPCHK(op, dw_gemm(e, 3, dcur_in, D, A.gate, H, T, EPI_STORE_F, p, async));
       phase_end(e, ds);
-    }
-    {  // dW1 (| dW3) += dh x2Norm^T
+      return ANE_OK;
+    };
+    auto dw13 = [&]() -> int {  // dW1 (| dW3) += dh x2Norm^T
       EpiParams p;
       p.C = G + o.w1; p.ldc = D; p.accumulate = acc;
       if (llama) p.C3 = G + o.w3;
       phase_begin(e, PH_DW_GEMM, ds);
       HIPCHK(op, dw_gemm(e, 2, dh13, KH, A.xn2, D, T, llama ? EPI_STORE_W13 : EPI_STORE_F, p, async));
       phase_end(e, ds);
-    }
+      return ANE_OK;
+    };
+    if ((rc = dw2())) return rc;
     {
       EpiParams p;
       p.C = tb.dxn; p.ldc = D;
@@ -408,6 +411,10 @@ int backward_body(ane_engine* e, int nseq, bool async) {
       HIPCHK(op, dw_gemm(e, 1, dx2_h, D, A.att, D, T, EPI_STORE_F, p, async));
       phase_end(e, ds);
     }
+    // dW1|3 behind dWo: beside the Wo dX GEMM and the attention backward
+    // rather than the W1|W3 dX GEMM (6.55-6.58 against 6.60-6.63 ms per B16
+    // step with it at the first fork)
+    if ((rc = dw13())) return rc;
     {
       EpiParams p;
       p.C = tb.datt; p.ldc = D;
