@@ -9,7 +9,7 @@
 //                  rounded) -> top-2 (ties to the lower expert) and the
 //                  softmax over the two chosen logits
 //   2. permute     stable counting sort over blocks of 256 tokens (count,
-//                  scan, scatter): rows of each expert in token order, each
+//                  scatter): rows of each expert in token order, each
 //                  expert's group padded to a multiple of 128 rows; tile
 //                  table (first row, expert) for the grouped GEMMs
 //   3. gather      xg[row] = fp16(x[token of row]) (zero for padding rows)
@@ -131,15 +131,15 @@ __global__ __launch_bounds__(256) void router_kernel(const float* x, const float
   }
 }
 
-// Permutation as a stable counting sort in three launches (blocks of 256
+// Permutation as a stable counting sort in two launches (blocks of 256
 // tokens; the rows of each expert come out in token order):
 //   perm_count: per block and expert, the tokens that chose the expert
 //               (wave ballots), counts[e][block];
-//   perm_scan:  one block: exclusive scan of counts[e][.] over blocks, each
-//               expert's group padded to whole 128-row tiles, tile table,
-//               padding rows;
-//   perm_scatter: row = group base + block base + rank inside the block
-//               (ballot prefix counts), perm / rw / rowpos.
+//   perm_scatter: every block sums the counts into the experts' totals and
+//               its own offsets; row = group base (groups padded to whole
+//               128-row tiles) + block base + rank inside the block (ballot
+//               prefix counts), perm / rw / rowpos; block 0 writes the tile
+//               table and the padding rows.
 constexpr int kPermTok = 256;
 __device__ __forceinline__ bool chose(const int32_t* idx, int t, int T, int e) {
   return t < T && (idx[2 * t] == e || idx[2 * t + 1] == e);
@@ -163,84 +163,31 @@ __global__ __launch_bounds__(kPermTok) void perm_count_kernel(const int32_t* idx
   }
 }
 
-// counts[e][b] -> exclusive block offsets (in place); grp[e] = group start,
-// grp[E + e] = rows of expert e; tiles[0] = number of 128-row tiles, then
-// (first row, expert) per tile
-__global__ __launch_bounds__(256) void perm_scan_kernel(int* counts, int nblk, int E, int* grp, int* tiles,
-                                                        int* perm, float* rw) {
-  __shared__ int part[kMaxExperts][256];
-  __shared__ int tot[kMaxExperts], start[kMaxExperts + 1], tstart[kMaxExperts + 1];
-  const int tid = threadIdx.x;
-  const int per = (nblk + 255) / 256;
-  const int b0 = min(nblk, tid * per), b1 = min(nblk, b0 + per);
-  int sum[kMaxExperts];
-#pragma unroll
-  for (int e = 0; e < kMaxExperts; e++) {
-    sum[e] = 0;
-    if (e < E)
-      for (int b = b0; b < b1; b++) sum[e] += counts[(size_t)e * nblk + b];
-    part[e][tid] = sum[e];
-  }
-  __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {  // inclusive scan of the thread sums, every expert at once
-    int v[kMaxExperts];
-#pragma unroll
-    for (int e = 0; e < kMaxExperts; e++) v[e] = (e < E && tid >= off) ? part[e][tid - off] : 0;
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < kMaxExperts; e++)
-      if (e < E) part[e][tid] += v[e];
-    __syncthreads();
-  }
-#pragma unroll
-  for (int e = 0; e < kMaxExperts; e++) {
-    if (e >= E) continue;
-    int* c = counts + (size_t)e * nblk;
-    int run = part[e][tid] - sum[e];  // exclusive
-    for (int b = b0; b < b1; b++) {
-      const int n = c[b];
-      c[b] = run;
-      run += n;
-    }
-  }
-  if (tid < E) tot[tid] = part[tid][255];
-  __syncthreads();
-  if (tid == 0) {
-    int p = 0, nt = 0;
-    for (int e = 0; e < E; e++) {
-      start[e] = p;
-      tstart[e] = nt;
-      const int ntl = (tot[e] + kGroupRows - 1) / kGroupRows;
-      nt += ntl;
-      p += ntl * kGroupRows;
-      grp[e] = start[e];
-      grp[E + e] = tot[e];
-    }
-    start[E] = p;
-    tstart[E] = nt;
-    tiles[0] = nt;
-  }
-  __syncthreads();
-  for (int j = tid; j < tstart[E]; j += 256) {
-    int e = 0;
-    while (j >= tstart[e + 1]) e++;
-    tiles[1 + 2 * j] = start[e] + (j - tstart[e]) * kGroupRows;
-    tiles[2 + 2 * j] = e;
-  }
-  for (int e = 0; e < E; e++)  // padding rows of every group
-    for (int r = start[e] + tot[e] + tid; r < start[e + 1]; r += 256) {
-      perm[r] = -1;
-      rw[r] = 0.f;
-    }
-}
-
+// Scatter, with the prefix sums folded in: every block adds up the per-block
+// expert counts (E x nblk integers, by LDS atomics, exact in any order) into
+// the experts' totals and its own exclusive offsets, lays the groups out
+// (each padded to whole 128-row GEMM tiles) from the totals, and places its
+// tokens; block 0 also writes the tile table (tiles[0] = number of tiles,
+// then (first row, expert) per tile) and clears the groups' padding rows,
+// which no token reaches.
 __global__ __launch_bounds__(kPermTok) void perm_scatter_kernel(const int32_t* idx, const float* wts, int T, int E,
-                                                                const int* offs, int nblk, const int* grp, int* perm,
+                                                                const int* counts, int nblk, int* tiles, int* perm,
                                                                 float* rw, int* rowpos) {
   __shared__ int wc[kPermTok / 64][kMaxExperts];
+  __shared__ int tot[kMaxExperts], off[kMaxExperts], start[kMaxExperts + 1], tstart[kMaxExperts + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid < kMaxExperts) {
+    tot[tid] = 0;
+    off[tid] = 0;
+  }
   const int t = blockIdx.x * kPermTok + tid;
   const int a = t < T ? idx[2 * t] : -1, b = t < T ? idx[2 * t + 1] : -1;
+  __syncthreads();
+  for (int i = tid; i < E * nblk; i += kPermTok) {
+    const int e = i / nblk, v = counts[i];
+    atomicAdd(&tot[e], v);
+    if (i - e * nblk < (int)blockIdx.x) atomicAdd(&off[e], v);
+  }
   const unsigned long long below = (1ull << lane) - 1ull;
   int ra = 0, rb = 0;  // rank of this token among the wave's tokens of expert a / b
   for (int e = 0; e < E; e++) {
@@ -251,11 +198,38 @@ __global__ __launch_bounds__(kPermTok) void perm_scatter_kernel(const int32_t* i
     if (b == e) rb = r;
   }
   __syncthreads();
+  if (tid == 0) {
+    int p = 0, nt = 0;
+    for (int e = 0; e < E; e++) {
+      start[e] = p;
+      tstart[e] = nt;
+      const int ntl = (tot[e] + kGroupRows - 1) / kGroupRows;
+      nt += ntl;
+      p += ntl * kGroupRows;
+    }
+    start[E] = p;
+    tstart[E] = nt;
+  }
+  __syncthreads();
+  if (blockIdx.x == 0) {
+    if (tid == 0) tiles[0] = tstart[E];
+    for (int j = tid; j < tstart[E]; j += kPermTok) {
+      int e = 0;
+      while (j >= tstart[e + 1]) e++;
+      tiles[1 + 2 * j] = start[e] + (j - tstart[e]) * kGroupRows;
+      tiles[2 + 2 * j] = e;
+    }
+    for (int e = 0; e < E; e++)
+      for (int r = start[e] + tot[e] + tid; r < start[e + 1]; r += kPermTok) {
+        perm[r] = -1;
+        rw[r] = 0.f;
+      }
+  }
   if (t >= T) return;
 #pragma unroll
   for (int k = 0; k < 2; k++) {
     const int e = k == 0 ? a : b;
-    int pos = grp[e] + offs[(size_t)e * nblk + blockIdx.x] + (k == 0 ? ra : rb);
+    int pos = start[e] + off[e] + (k == 0 ? ra : rb);
     for (int w = 0; w < wave; w++) pos += wc[w][e];
     perm[pos] = t;
     rw[pos] = wts[2 * t + k];
@@ -306,7 +280,7 @@ struct ane_moe {
   float *x = nullptr, *wts = nullptr, *rw = nullptr, *yw = nullptr, *out = nullptr;
   int32_t* idx = nullptr;
   int *perm = nullptr, *rowpos = nullptr, *tiles = nullptr;
-  int *counts = nullptr, *grp = nullptr;  // permutation: per-block counts / offsets, group starts and sizes
+  int* counts = nullptr;  // permutation: per-block expert counts
   half_t *xg = nullptr, *g = nullptr;
 };
 
@@ -402,7 +376,6 @@ extern "C" int ane_moe_open(const ane_moe_cfg* cfg, ane_moe** out) {
     OPEN_CHK(malloc_(m, &m->rw, RC));
     OPEN_CHK(malloc_(m, &m->tiles, 1 + 2 * (RC / kGroupRows)));
     OPEN_CHK(malloc_(m, &m->counts, E * ((TM + kPermTok - 1) / kPermTok)));
-    OPEN_CHK(malloc_(m, &m->grp, 2 * E));
     OPEN_CHK(malloc_(m, &m->xg, RC * D));
     OPEN_CHK(malloc_(m, &m->g, RC * H));
     OPEN_CHK(malloc_(m, &m->yw, RC * D));
@@ -468,11 +441,8 @@ extern "C" int ane_moe_run(ane_moe* m) {
   const int nblk = (T + kPermTok - 1) / kPermTok;
   hipLaunchKernelGGL(perm_count_kernel, dim3(nblk), dim3(kPermTok), 0, st, m->idx, T, E, m->counts, nblk);
   MCHK(op, hipGetLastError());
-  hipLaunchKernelGGL(perm_scan_kernel, dim3(1), dim3(256), 0, st, m->counts, nblk, E, m->grp, m->tiles, m->perm,
-                     m->rw);
-  MCHK(op, hipGetLastError());
   hipLaunchKernelGGL(perm_scatter_kernel, dim3(nblk), dim3(kPermTok), 0, st, m->idx, m->wts, T, E, m->counts, nblk,
-                     m->grp, m->perm, m->rw, m->rowpos);
+                     m->tiles, m->perm, m->rw, m->rowpos);
   MCHK(op, hipGetLastError());
   hipLaunchKernelGGL(gather_kernel, dim3(m->RC), dim3(256), 0, st, m->xg, m->x, m->perm, m->tiles, D);
   MCHK(op, hipGetLastError());
