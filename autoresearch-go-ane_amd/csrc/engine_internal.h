@@ -189,7 +189,11 @@ struct ane_engine {
   // when the last forward left its final norm to the classifier this way
   float* ssq_part = nullptr;
   bool fused_norm = true;
-  bool fused_pf = true;  // the classifier's weights by a prefetch launch (ANE_FUSED_PF)
+  // the classifier's weights by a prefetch launch before it (ANE_FUSED_PF=1;
+  // off: 2.643-2.653 against 2.650-2.657 ms per B32 forward, seven
+  // alternating pairs, since the self-prefetching GEMMs and the 1.5-head
+  // attention)
+  bool fused_pf = false;
   // the deferred-norm forward's GEMMs stream weights from their first
   // blocks (GemmArgs::pf): W1|W3 its own and W2's, W2 the next layer's
   // Wq|Wk|Wv (ANE_GEMM_SELFPF=0: a prefetch launch before QKV and W1|W3)
