@@ -170,3 +170,51 @@ def test_refresh_close_and_disable():
         off.run_classifier_forward(lg, xn.ravel())
     off.close()
     assert not off.has_rms_forward()
+
+
+@pytest.mark.parametrize("seq", [64, 512])
+def test_layer_forward_edge_sequence_lengths(seq):
+    """The shortest sequence the objects take and the longest a forward
+    object takes (ane/layer_darwin.go compiles per sequence length), at a
+    small width: every tap against the seam oracle."""
+    print(f"seam layer forward edge seq={seq}", flush=True)
+    dim, hidden, heads = 256, 512, 4
+    rng = np.random.default_rng(50 + seq)
+    w = layer_weights(rng, dim, hidden)
+    x = rng.standard_normal((dim, seq)).astype(np.float32)
+    ref_out, ref_taps = oracle.seam_layer_forward(w, heads, x)
+    lf = objects.compile_stories_layer_forward(w, seq, heads=heads)
+    out = np.full(dim * seq, np.nan, np.float32)
+    cache = objects.LayerCache(dim, hidden, seq)
+    lf.run_with_taps(out, x.ravel(), cache)
+    check("out", out, ref_out, 5e-3)
+    for n in ("x_norm", "q", "k", "v", "att_out", "x2", "x2_norm", "h1", "gate"):
+        check(n, getattr(cache, n), ref_taps[n], 5e-3)
+    lf.close()
+
+
+@pytest.mark.parametrize("seq", [64, 256])
+def test_layer_backward_edge_sequence_lengths(seq):
+    """The backward object at the shortest and the longest sequence it
+    takes, at a small width, against the seam oracle."""
+    print(f"seam layer backward edge seq={seq}", flush=True)
+    dim, hidden, heads = 256, 512, 4
+    rng = np.random.default_rng(60 + seq)
+    w = layer_weights(rng, dim, hidden)
+    x = rng.standard_normal((dim, seq)).astype(np.float32)
+    _, taps = oracle.seam_layer_forward(w, heads, x)
+    dx2 = rng.standard_normal((dim, seq)).astype(np.float32)
+    dffn = rng.standard_normal((dim, seq)).astype(np.float32)
+    lb = objects.compile_stories_layer_backward(w, seq, heads=heads)
+    outs = [np.full(dim * seq, np.nan, np.float32) for _ in range(4)]
+    lb.run_attention(*outs, taps["q"].ravel(), taps["k"].ravel(), taps["v"].ravel(), dx2.ravel())
+    ref = oracle.seam_attention_backward(w, heads, taps["q"], taps["k"], taps["v"], dx2)
+    for n, got, r in zip(("dx_norm", "dq", "dk", "dv"), outs, ref):
+        check(n, got, r, 1e-2)
+    dxn = np.full(dim * seq, np.nan, np.float32)
+    dh1 = np.full(hidden * seq, np.nan, np.float32)
+    lb.run_ffn(dxn, dh1, dffn.ravel(), taps["h1"].ravel())
+    ref_dx, ref_dh1 = oracle.seam_ffn_backward(w, dffn, taps["h1"])
+    check("ffn dx_norm", dxn, ref_dx, 1e-2)
+    check("dh1", dh1, ref_dh1, 1e-2)
+    lb.close()
