@@ -44,11 +44,12 @@ def test_small_layer_matches_oracle():
     np.testing.assert_array_equal(out, out2)  # deterministic
 
 
-@pytest.mark.parametrize("experts,tokens", [(2, 513), (4, 1000), (16, 777), (16, 4096)])
+@pytest.mark.parametrize("experts,tokens", [(2, 513), (4, 1000), (16, 777), (16, 4096), (8, 1), (8, 256)])
 def test_expert_counts_and_ragged_token_counts(experts, tokens):
     """Every supported expert count, token counts that leave a partial
-    256-token permutation block, and (16 x 4096) several full blocks and
-    tile groups per expert."""
+    256-token permutation block, (16 x 4096) several full blocks and tile
+    groups per expert, and one token or exactly one block (a single
+    permutation block forms every group's offsets and the tile table)."""
     cfg = MoeConfig(dim=128, hidden=192, experts=experts)
     p = init_moe_params(cfg, seed=31 + experts, std=0.05)
     x = make_moe_input(cfg, tokens, seed=32 + tokens)
