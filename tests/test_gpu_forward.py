@@ -122,6 +122,26 @@ def test_windows_equal_explicit_batch():
     eng.Destroy()
 
 
+@pytest.mark.parametrize("arch", ["nanochat", "llama2"])
+def test_more_windows_than_kernel_arguments_hold(arch):
+    """72 windows: past the 64 window starts a launch carries as arguments,
+    the starts go to the device first and a separate gather reads them; the
+    losses equal the explicit batch bit for bit (both architectures, the
+    llama2 one through the deferred-norm forward)."""
+    cfg = ane.tiny(arch)
+    p = ane.init_params(cfg, seed=9, std=0.08)
+    stream = np.random.default_rng(10).integers(0, cfg.vocab, 20000).astype(np.uint16)
+    n = 72
+    eng = open_engine(cfg, p, max_batch=n, tokens=stream)
+    pos = np.random.default_rng(11).integers(0, 20000 - cfg.seq - 1, n).astype(np.uint64)
+    m1, per1 = eng.EvalLossWindows(pos)
+    tok = np.stack([stream[int(q):int(q) + cfg.seq] for q in pos])
+    tgt = np.stack([stream[int(q) + 1:int(q) + 1 + cfg.seq] for q in pos])
+    m2, per2 = eng.EvalLoss(tok, tgt)
+    np.testing.assert_array_equal(per1, per2)
+    eng.Destroy()
+
+
 def test_error_behaviour():
     cfg = ane.tiny("llama2")
     p = ane.init_params(cfg, seed=9)
